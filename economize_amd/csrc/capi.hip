@@ -1,0 +1,288 @@
+// extern "C" entry points of libeconomize_amd.so (declared in include/economize_amd.h): argument validation, launch
+// plans and error reporting around the kernels.
+
+#include <cstdlib>
+#include <cstring>
+#include <string>
+
+#include "../../include/economize_amd.h"
+#include "common.hpp"
+#include "kv_quant.hpp"
+#include "paged_attention.hpp"
+
+namespace eco {
+
+namespace {
+thread_local std::string g_error;
+}
+
+void set_error(const std::string& message) { g_error = message; }
+
+int fail(const std::string& message) {
+    set_error(message);
+    return 1;
+}
+
+int check_launch(const char* what) {
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) {
+        set_error(std::string(what) + ": " + hipGetErrorString(err));
+        return 2;
+    }
+    return 0;
+}
+
+namespace {
+
+int device_cus() {
+    static int cached[64] = {0};
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 256;
+    if (cached[device] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+            cus = 256;
+        cached[device] = cus;
+    }
+    return cached[device];
+}
+
+struct PagedPlan {
+    int split_pages;
+    int max_splits;
+};
+
+// Splits sized so that the batch's KV heads and splits give about four workgroups per CU over the longest row; a
+// split holds whole tiles of 4 pages per wave (ECO_SPLIT_PAGES overrides the split length for tuning).
+PagedPlan paged_plan(int batch, int kv_heads, int max_virt) {
+    PagedPlan plan;
+    max_virt = max_virt < 1 ? 1 : max_virt;
+    static const int forced = [] {
+        const char* env = std::getenv("ECO_SPLIT_PAGES");
+        return env ? std::atoi(env) : 0;
+    }();
+    if (forced > 0) {
+        plan.split_pages = forced;
+    } else {
+        const int pairs = batch * kv_heads;
+        const int target = 4 * device_cus();
+        int splits = (target + pairs - 1) / pairs;
+        const int tiles = (max_virt + 3) / 4;
+        splits = splits < 1 ? 1 : (splits > tiles ? tiles : splits);
+        int pages = (max_virt + splits - 1) / splits;
+        plan.split_pages = (pages + 15) / 16 * 16;  // whole tiles for each of up to four waves
+    }
+    plan.max_splits = (max_virt + plan.split_pages - 1) / plan.split_pages;
+    return plan;
+}
+
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+struct Workspace {
+    size_t o_bytes, ml_bytes;
+    size_t total() const { return o_bytes + 2 * ml_bytes; }
+};
+
+Workspace paged_workspace(int batch, int kv_heads, int rows, int head_dim, int max_splits) {
+    const size_t parts = static_cast<size_t>(batch) * kv_heads * max_splits * rows;
+    return Workspace{align256(parts * head_dim * sizeof(float)), align256(parts * sizeof(float))};
+}
+
+int max_virtual_pages(int max_seq_len, int n_sel) { return (max_seq_len + 15) / 16 + (n_sel > 0 ? n_sel : 0); }
+
+int run_paged_decode(bool merge, const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
+                     const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
+                     const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                     const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h, int32_t n_sel, const int32_t* done,
+                     const float* sinks, void* out, int64_t so_b, int64_t so_q, int64_t so_h, int32_t batch,
+                     int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                     int32_t max_seq_len, float scale, float softcap, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+    if (!q || !k_cache || !v_cache || !block_table || !seq_lens || !out)
+        return fail("paged decode: null q, cache, block table, seq_lens or out pointer");
+    if (batch <= 0 || queries <= 0 || q_heads <= 0 || kv_heads <= 0 || num_pages <= 0 || bt_cols <= 0)
+        return fail("paged decode: batch, queries, heads, pages and block-table columns must be positive");
+    if (bt_stride < bt_cols) return fail("paged decode: block-table stride is smaller than its column count");
+    if (q_heads % kv_heads) return fail("paged decode: query heads are not a multiple of the KV heads");
+    if (page_size != 16) return fail("paged decode: pages must hold 16 tokens");
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return fail("paged decode: head dim must be 64, 128 or 256");
+    if (kv_format != BF16 && kv_format != FP8_E4M3 && kv_format != FP8_E5M2)
+        return fail("paged decode: KV format must be bf16, fp8 e4m3 or fp8 e5m2");
+    const int groups = q_heads / kv_heads;
+    const int rows = groups * queries;
+    if (rows > 64) return fail("paged decode: at most 64 query rows per KV head (query heads per KV head x queries)");
+    if ((reinterpret_cast<uintptr_t>(q) & 15) || (sq_b & 7) || (sq_q & 7) || (sq_h & 7))
+        return fail("paged decode: the query must be 16-byte aligned with strides that are multiples of 8");
+    if (page_list && (!done || n_sel < 0)) return fail("paged decode: a page list needs done[] and n_sel >= 0");
+    if (max_seq_len <= 0) return fail("paged decode: max_seq_len must be positive");
+    if (!(scale == scale)) return fail("paged decode: scale is NaN");
+
+    const int max_virt = max_virtual_pages(max_seq_len, page_list ? n_sel : 0);
+    const PagedPlan plan = paged_plan(batch, kv_heads, max_virt);
+    const Workspace ws = paged_workspace(batch, kv_heads, rows, head_dim, plan.max_splits);
+    if (!workspace || workspace_bytes < ws.total())
+        return fail("paged decode: workspace too small (" + std::to_string(workspace_bytes) + " < " +
+                    std::to_string(ws.total()) + " bytes)");
+
+    const int es = kv_format == BF16 ? 2 : 1;
+    PagedParams p;
+    std::memset(&p, 0, sizeof(p));
+    p.q = static_cast<const uint16_t*>(q);
+    p.sq_b = sq_b;
+    p.sq_q = sq_q;
+    p.sq_h = sq_h;
+    p.k_cache = static_cast<const uint8_t*>(k_cache);
+    p.v_cache = static_cast<const uint8_t*>(v_cache);
+    p.kc_head = static_cast<int64_t>(head_dim) * 16 * es;
+    p.kc_page = p.kc_head * kv_heads;
+    p.vc_head = p.kc_head;
+    p.vc_page = p.kc_page;
+    p.block_table = block_table;
+    p.bt_stride = bt_stride;
+    p.bt_cols = bt_cols;
+    p.num_pages = num_pages;
+    p.seq_lens = seq_lens;
+    p.page_list = page_list;
+    p.pl_b = pl_b;
+    p.pl_h = pl_h;
+    p.n_sel = page_list ? n_sel : 0;
+    p.done = done;
+    p.k_scale = k_scale;
+    p.v_scale = v_scale;
+    p.sinks = sinks;
+    char* base = static_cast<char*>(workspace);
+    p.part_o = reinterpret_cast<float*>(base);
+    p.part_m = reinterpret_cast<float*>(base + ws.o_bytes);
+    p.part_l = reinterpret_cast<float*>(base + ws.o_bytes + ws.ml_bytes);
+    p.out = static_cast<uint16_t*>(out);
+    p.so_b = so_b;
+    p.so_q = so_q;
+    p.so_h = so_h;
+    p.batch = batch;
+    p.queries = queries;
+    p.q_heads = q_heads;
+    p.kv_heads = kv_heads;
+    p.groups = groups;
+    p.rows = rows;
+    p.head_dim = head_dim;
+    p.kv_format = kv_format;
+    p.split_pages = plan.split_pages;
+    p.max_splits = plan.max_splits;
+    p.scale = scale;
+    p.softcap = softcap > 0.0f ? softcap : 0.0f;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (int rc = paged_split(p, s)) return rc;
+    if (merge) return paged_merge(p, s);
+    return 0;
+}
+
+}  // namespace
+
+}  // namespace eco
+
+using namespace eco;
+
+extern "C" {
+
+const char* eco_last_error(void) { return g_error.c_str(); }
+
+int eco_abi_version(void) { return 1; }
+
+int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
+                     int64_t sv_t, int64_t sv_h, const int32_t* slot_mapping, int32_t tokens, void* k_cache,
+                     void* v_cache, int32_t num_pages, int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                     int32_t cache_format, const float* k_scale, const float* v_scale, void* stream) {
+    if (tokens < 0) return fail("paged append: negative token count");
+    if (tokens == 0) return 0;
+    if (!k_new || !v_new || !slot_mapping || !k_cache || !v_cache)
+        return fail("paged append: null input, slot mapping or cache pointer");
+    if (in_format != BF16 && in_format != FP16 && in_format != FP32)
+        return fail("paged append: inputs must be bf16, fp16 or fp32");
+    if (cache_format != BF16 && cache_format != FP8_E4M3 && cache_format != FP8_E5M2)
+        return fail("paged append: cache format must be bf16, fp8 e4m3 or fp8 e5m2");
+    if (page_size != 16) return fail("paged append: pages must hold 16 tokens");
+    if (head_dim <= 0 || head_dim % 16 || kv_heads <= 0 || num_pages <= 0)
+        return fail("paged append: head dim must be a positive multiple of 16, heads and pages positive");
+    if (cache_format == BF16 && (k_scale || v_scale)) return fail("paged append: a bf16 cache takes no scales");
+    const int es = cache_format == BF16 ? 2 : 1;
+    AppendParams p;
+    p.k_new = k_new;
+    p.v_new = v_new;
+    p.in_format = in_format;
+    p.sk_t = sk_t;
+    p.sk_h = sk_h;
+    p.sv_t = sv_t;
+    p.sv_h = sv_h;
+    p.slots = slot_mapping;
+    p.tokens = tokens;
+    p.k_cache = static_cast<uint8_t*>(k_cache);
+    p.v_cache = static_cast<uint8_t*>(v_cache);
+    p.kc_head = static_cast<int64_t>(head_dim) * 16 * es;
+    p.kc_page = p.kc_head * kv_heads;
+    p.vc_head = p.kc_head;
+    p.vc_page = p.kc_page;
+    p.kv_heads = kv_heads;
+    p.head_dim = head_dim;
+    p.num_pages = num_pages;
+    p.cache_format = cache_format;
+    p.k_scale = k_scale;
+    p.v_scale = v_scale;
+    return paged_append(p, static_cast<hipStream_t>(stream));
+}
+
+int eco_kv_head_absmax(const void* x, int32_t in_format, int32_t a, int32_t h, int32_t s, int32_t d, int64_t sa,
+                       int64_t sh, int64_t ss, int64_t sd, uint32_t* absmax_bits, void* stream) {
+    if (!x || !absmax_bits) return fail("head absmax: null pointer");
+    if (in_format != BF16 && in_format != FP16 && in_format != FP32)
+        return fail("head absmax: input must be bf16, fp16 or fp32");
+    if (a < 0 || h <= 0 || s < 0 || d <= 0) return fail("head absmax: bad shape");
+    if (a == 0 || s == 0) return 0;
+    AbsmaxParams p{x, in_format, a, h, s, d, sa, sh, ss, sd, absmax_bits};
+    return head_absmax(p, static_cast<hipStream_t>(stream));
+}
+
+int eco_fp8_scales_from_absmax(const uint32_t* absmax_bits, int32_t heads, int32_t format, float* scales,
+                               void* stream) {
+    if (!absmax_bits || !scales || heads <= 0) return fail("fp8 scales: null pointer or no heads");
+    if (format != FP8_E4M3 && format != FP8_E5M2) return fail("fp8 scales: format must be fp8 e4m3 or e5m2");
+    return scales_from_absmax(absmax_bits, heads, format, scales, static_cast<hipStream_t>(stream));
+}
+
+size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
+                                       int32_t head_dim, int32_t max_seq_len, int32_t n_sel) {
+    if (batch <= 0 || queries <= 0 || kv_heads <= 0 || q_heads <= 0 || head_dim <= 0) return 0;
+    const PagedPlan plan = paged_plan(batch, kv_heads, max_virtual_pages(max_seq_len, n_sel));
+    const int rows = (q_heads / kv_heads) * queries;
+    return paged_workspace(batch, kv_heads, rows, head_dim, plan.max_splits).total();
+}
+
+int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
+                     const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
+                     const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                     const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h, int32_t n_sel, const int32_t* done,
+                     const float* sinks, void* out, int64_t so_b, int64_t so_q, int64_t so_h, int32_t batch,
+                     int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                     int32_t max_seq_len, float scale, float softcap, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+    return run_paged_decode(true, q, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
+                            block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel, done, sinks, out, so_b,
+                            so_q, so_h, batch, queries, q_heads, kv_heads, head_dim, page_size, max_seq_len, scale,
+                            softcap, workspace, workspace_bytes, stream);
+}
+
+int eco_paged_decode_split_only(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
+                                const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
+                                const float* v_scale, const int32_t* block_table, int64_t bt_stride,
+                                int32_t bt_cols, const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h,
+                                int32_t n_sel, const int32_t* done, const float* sinks, void* out, int64_t so_b,
+                                int64_t so_q, int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads,
+                                int32_t kv_heads, int32_t head_dim, int32_t page_size, int32_t max_seq_len,
+                                float scale, float softcap, void* workspace, size_t workspace_bytes, void* stream) {
+    return run_paged_decode(false, q, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
+                            block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel, done, sinks, out, so_b,
+                            so_q, so_h, batch, queries, q_heads, kv_heads, head_dim, page_size, max_seq_len, scale,
+                            softcap, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,47 @@
+// Shared definitions of the economize_amd HIP kernels (gfx950 / CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "fp8_codec.hpp"
+
+namespace eco {
+
+// Element formats of the C-ABI (economize_amd.h).
+enum Format : int { BF16 = 0, FP8_E4M3 = 1, FP8_E5M2 = 2, FP16 = 3, FP32 = 4 };
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---- errors -------------------------------------------------------------------------------------------------
+void set_error(const std::string& message);
+int fail(const std::string& message);  // set_error + return 1
+int check_launch(const char* what);    // 0, or 2 with the HIP error of the last launch recorded
+
+template <int FMT>
+ECO_HD constexpr float fp8_max() {
+    return FMT == FP8_E4M3 ? 448.0f : 57344.0f;
+}
+
+__device__ inline float group_max(float x) {  // max over the four lanes l, l^16, l^32, l^48
+    x = fmaxf(x, __shfl_xor(x, 16));
+    return fmaxf(x, __shfl_xor(x, 32));
+}
+
+__device__ inline float group_sum(float x) {  // sum over the four lanes l, l^16, l^32, l^48
+    x += __shfl_xor(x, 16);
+    return x + __shfl_xor(x, 32);
+}
+
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+}  // namespace eco

@@ -1,0 +1,142 @@
+// FP8 / bf16 quantize-and-append into the paged KV cache, and per-head absmax scales (gfx950).
+//
+// Append follows the reference's fp8 encode (techniques/kv_quant/fp8.py:81-86, FP8Cache.transform_update
+// fp8.py:161-176): x.float() / scale with IEEE division, clamp to the format's finite maximum, cast with
+// round-to-nearest-even (f32_to_fp8 in common.hpp), written at the token's slot (vLLM-style slot mapping: slot =
+// page * 16 + position; a negative slot is padding and writes nothing, like the trash slot of
+// modules/kv_cache.py:13-27). The per-head scale is the reference's static_scales rule (fp8.py:130-133) over each
+// KV head's absolute maximum.
+//
+// Layout of the caches: see paged_attention.hip. One workgroup per new token; a thread encodes 8 consecutive
+// channels of one head, so the key write is one 8-byte (fp8) or 16-byte (bf16) store into the token's 16-byte run,
+// and the value write scatters the 8 channels into their channel rows.
+
+#include "common.hpp"
+#include "kv_quant.hpp"
+
+namespace eco {
+
+namespace {
+
+constexpr int PAGE = 16;
+
+__device__ inline float load_elem(const void* base, int64_t offset, int format) {
+    if (format == BF16) return bf16_to_f32(static_cast<const uint16_t*>(base)[offset]);
+    if (format == FP16) return static_cast<float>(static_cast<const _Float16*>(base)[offset]);
+    return static_cast<const float*>(base)[offset];
+}
+
+template <int FMT>
+__device__ inline uint8_t encode(float x, float scale, bool scaled) {
+    float w = scaled ? __fdiv_rn(x, scale) : x;
+    w = fminf(fmaxf(w, -fp8_max<FMT>()), fp8_max<FMT>());  // clamp; NaN stays NaN (fminf/fmaxf would drop it)
+    if (x != x) w = x;
+    return f32_to_fp8<FMT>(w);
+}
+
+template <int FMT>
+__global__ __launch_bounds__(256) void paged_append_kernel(AppendParams p) {
+    constexpr int ES = FMT == BF16 ? 2 : 1;
+    constexpr int E = 16 / ES;  // channels per 16-byte run of the key layout
+    const int t = blockIdx.x;
+    const int slot = p.slots[t];
+    if (slot < 0 || slot / PAGE >= p.num_pages) return;
+    const int page = slot / PAGE;
+    const int pos = slot % PAGE;
+    const int runs = p.head_dim / 8;
+    for (int item = threadIdx.x; item < p.kv_heads * runs; item += blockDim.x) {
+        const int h = item / runs;
+        const int d0 = (item % runs) * 8;
+        const float ks = p.k_scale ? p.k_scale[h] : 1.0f;
+        const float vs = p.v_scale ? p.v_scale[h] : 1.0f;
+        float k[8], v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            k[i] = load_elem(p.k_new, t * p.sk_t + h * p.sk_h + d0 + i, p.in_format);
+            v[i] = load_elem(p.v_new, t * p.sv_t + h * p.sv_h + d0 + i, p.in_format);
+        }
+        uint8_t* kp = p.k_cache + static_cast<int64_t>(page) * p.kc_page + h * p.kc_head;
+        uint8_t* vp = p.v_cache + static_cast<int64_t>(page) * p.vc_page + h * p.vc_head;
+        const int64_t k_off = ((d0 / E) * PAGE + pos) * 16 + (d0 % E) * ES;
+        if constexpr (FMT == BF16) {
+            uint4 w;
+            w.x = f32_to_bf16(k[0]) | (static_cast<uint32_t>(f32_to_bf16(k[1])) << 16);
+            w.y = f32_to_bf16(k[2]) | (static_cast<uint32_t>(f32_to_bf16(k[3])) << 16);
+            w.z = f32_to_bf16(k[4]) | (static_cast<uint32_t>(f32_to_bf16(k[5])) << 16);
+            w.w = f32_to_bf16(k[6]) | (static_cast<uint32_t>(f32_to_bf16(k[7])) << 16);
+            *reinterpret_cast<uint4*>(kp + k_off) = w;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                *reinterpret_cast<uint16_t*>(vp + ((d0 + i) * PAGE + pos) * 2) = f32_to_bf16(v[i]);
+        } else {
+            const bool scaled = p.k_scale != nullptr;
+            uint32_t lo = 0, hi = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                lo |= static_cast<uint32_t>(encode<FMT>(k[i], ks, scaled)) << (8 * i);
+                hi |= static_cast<uint32_t>(encode<FMT>(k[i + 4], ks, scaled)) << (8 * i);
+            }
+            *reinterpret_cast<uint2*>(kp + k_off) = make_uint2(lo, hi);
+            const bool vscaled = p.v_scale != nullptr;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) vp[(d0 + i) * PAGE + pos] = encode<FMT>(v[i], vs, vscaled);
+        }
+    }
+}
+
+// absmax[h] = max |x[a, h, s, d]| as float bits (non-negative floats order like their bit patterns).
+__global__ __launch_bounds__(256) void head_absmax_kernel(AbsmaxParams p) {
+    const int h = blockIdx.y;
+    const int64_t total = static_cast<int64_t>(p.a) * p.s * p.d;
+    float m = 0.0f;
+    for (int64_t idx = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; idx < total;
+         idx += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t a = idx / (static_cast<int64_t>(p.s) * p.d);
+        const int64_t s = (idx / p.d) % p.s;
+        const int64_t d = idx % p.d;
+        const float x = load_elem(p.x, a * p.sa + h * p.sh + s * p.ss + d * p.sd, p.in_format);
+        m = fmaxf(m, fabsf(x));
+    }
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((threadIdx.x & 63) == 0) atomicMax(p.absmax_bits + h, f32_bits(m));
+}
+
+// static_scales (fp8.py:130-133): absmax / format max with IEEE division, 1 where that is not positive.
+__global__ void scales_from_absmax_kernel(const uint32_t* absmax_bits, int heads, float format_max, float* scales) {
+    const int h = blockIdx.x * blockDim.x + threadIdx.x;
+    if (h < heads) {
+        const float s = __fdiv_rn(bits_f32(absmax_bits[h]), format_max);
+        scales[h] = s > 0.0f ? s : 1.0f;
+    }
+}
+
+}  // namespace
+
+int paged_append(const AppendParams& p, hipStream_t stream) {
+    if (p.tokens == 0) return 0;
+    dim3 grid(p.tokens);
+    switch (p.cache_format) {
+        case BF16: hipLaunchKernelGGL(paged_append_kernel<BF16>, grid, dim3(256), 0, stream, p); break;
+        case FP8_E4M3: hipLaunchKernelGGL(paged_append_kernel<FP8_E4M3>, grid, dim3(256), 0, stream, p); break;
+        case FP8_E5M2: hipLaunchKernelGGL(paged_append_kernel<FP8_E5M2>, grid, dim3(256), 0, stream, p); break;
+        default: return fail("paged append: cache format must be bf16, fp8 e4m3 or fp8 e5m2");
+    }
+    return check_launch("paged_append_kernel");
+}
+
+int head_absmax(const AbsmaxParams& p, hipStream_t stream) {
+    const int64_t total = static_cast<int64_t>(p.a) * p.s * p.d;
+    int blocks = static_cast<int>((total + 256 * 16 - 1) / (256 * 16));
+    blocks = blocks < 1 ? 1 : (blocks > 1024 ? 1024 : blocks);
+    hipLaunchKernelGGL(head_absmax_kernel, dim3(blocks, p.h), dim3(256), 0, stream, p);
+    return check_launch("head_absmax_kernel");
+}
+
+int scales_from_absmax(const uint32_t* absmax_bits, int heads, int format, float* scales, hipStream_t stream) {
+    const float fmax = format == FP8_E4M3 ? 448.0f : 57344.0f;
+    hipLaunchKernelGGL(scales_from_absmax_kernel, dim3((heads + 63) / 64), dim3(64), 0, stream, absmax_bits, heads,
+                       fmax, scales);
+    return check_launch("scales_from_absmax_kernel");
+}
+
+}  // namespace eco

@@ -1,0 +1,96 @@
+/* economize_amd: C ABI of the compressed-KV decode-attention kernels for AMD MI355X (gfx950).
+ *
+ * Every entry point takes plain device pointers, sizes and strides, launches asynchronously on the given HIP
+ * stream (hipStream_t passed as void*; NULL = the null stream) and returns 0, or nonzero with a message that
+ * eco_last_error() returns (validation errors are raised before any launch, as the reference raises ConfigError
+ * before launching, attention/decode.py:287-300). Nothing allocates device memory: scratch space is a caller-owned
+ * workspace whose size the matching *_workspace_size function returns.
+ *
+ * Element formats: ECO_BF16, ECO_FP8_E4M3 (OCP e4m3fn), ECO_FP8_E5M2, ECO_FP16, ECO_FP32.
+ *
+ * Paged KV cache (16-token pages, vLLM's paged-attention layout), per layer:
+ *   keys   [num_pages, Hkv, D / X, 16, X]  X = 16 / element bytes
+ *   values [num_pages, Hkv, D, 16]
+ * Row b's token t lives in page block_table[b * bt_stride + t / 16] at position t % 16 (t / 16 < bt_cols).
+ * Kernels skip table entries outside [0, num_pages) and logical pages outside [0, bt_cols), so a malformed table
+ * reads nothing out of bounds (it gives wrong results instead).
+ */
+#ifndef ECONOMIZE_AMD_H
+#define ECONOMIZE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ECO_BF16 = 0, ECO_FP8_E4M3 = 1, ECO_FP8_E5M2 = 2, ECO_FP16 = 3, ECO_FP32 = 4 };
+
+/* The message of the last failed call on this thread ("" if none). */
+const char* eco_last_error(void);
+
+/* Version of this ABI (bumped on incompatible changes). */
+int eco_abi_version(void);
+
+/* FP8 / bf16 quantize-and-append into the paged cache.
+ * Replaces the reference's FP8Cache.transform_update + fp8_encode + write_slots
+ * (techniques/kv_quant/fp8.py:81-86, 161-176; modules/kv_cache.py:30-41): k_new / v_new [tokens, Hkv, D] (channel
+ * stride 1, element strides sk_t, sk_h, sv_t, sv_h, format in_format = bf16, fp16 or fp32) are divided by the
+ * per-head scale (k_scale / v_scale [Hkv] fp32, or NULL for none), clamped to the format's maximum, rounded to
+ * nearest even and stored at slot_mapping[t] (slot = page * 16 + position; negative = skip). A bf16 cache stores the
+ * values rounded to bf16. */
+int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
+                     int64_t sv_t, int64_t sv_h, const int32_t* slot_mapping, int32_t tokens, void* k_cache,
+                     void* v_cache, int32_t num_pages, int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                     int32_t cache_format, const float* k_scale, const float* v_scale, void* stream);
+
+/* Per-head absolute maximum of x [A, H, S, D] (element strides sa, sh, ss, sd; format bf16, fp16 or fp32),
+ * max-accumulated into absmax_bits[H] as float bit patterns (zero them before the first call). With
+ * eco_fp8_scales_from_absmax it is the reference's calibrate_kv_absmax + static_scales
+ * (techniques/kv_quant/fp8.py:100-133) per KV head. */
+int eco_kv_head_absmax(const void* x, int32_t in_format, int32_t a, int32_t h, int32_t s, int32_t d, int64_t sa,
+                       int64_t sh, int64_t ss, int64_t sd, uint32_t* absmax_bits, void* stream);
+
+/* scales[h] = absmax[h] / format max (IEEE division), 1 where that is not positive (fp8.py:130-133). */
+int eco_fp8_scales_from_absmax(const uint32_t* absmax_bits, int32_t heads, int32_t format, float* scales,
+                               void* stream);
+
+/* Workspace bytes eco_paged_decode needs for this shape (n_sel = Quest's selected pages, 0 without). */
+size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
+                                       int32_t head_dim, int32_t max_seq_len, int32_t n_sel);
+
+/* Split-K decode attention over the paged cache: out[b, qi, h, :] (bf16, element strides so_*) for query q[b, qi,
+ * h, :] (bf16, element strides sq_*, channel stride 1), query head h reading KV head h / (q_heads / kv_heads).
+ * Row b holds seq_lens[b] tokens, its queries the last `queries` of them, query qi seeing tokens
+ * < seq_lens[b] - queries + qi + 1. Scores are q . k * scale (k, v decoded times k_scale / v_scale [Hkv], NULL =
+ * 1), an optional softcap > 0 applies softcap * tanh(s / softcap), optional sinks [Hq] join the softmax's
+ * denominator. A row that sees no key gives 0.
+ * Replaces decode_attention (attention/decode.py:252-324) for a paged cache, and with page_list != NULL
+ * quest_decode_attention (attention/quest.py:239-344): the keys read are the pages page_list[b, kvh, 0..n_sel)
+ * (strides pl_b, pl_h; logical page indices, -1 = none) and then every token from page done[b] on. */
+int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
+                     const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
+                     const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                     const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h, int32_t n_sel, const int32_t* done,
+                     const float* sinks, void* out, int64_t so_b, int64_t so_q, int64_t so_h, int32_t batch,
+                     int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                     int32_t max_seq_len, float scale, float softcap, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* The split phase of eco_paged_decode alone (same arguments; writes only the workspace): a profiling entry that
+ * times the KV-streaming kernel without the merge. */
+int eco_paged_decode_split_only(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
+                                const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
+                                const float* v_scale, const int32_t* block_table, int64_t bt_stride,
+                                int32_t bt_cols, const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h,
+                                int32_t n_sel, const int32_t* done, const float* sinks, void* out, int64_t so_b,
+                                int64_t so_q, int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads,
+                                int32_t kv_heads, int32_t head_dim, int32_t page_size, int32_t max_seq_len,
+                                float scale, float softcap, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ECONOMIZE_AMD_H */

@@ -1,0 +1,156 @@
+"""Parity of the paged fp8 / bf16 kernels with the oracle on the GPU.
+
+* append: fp8 codes bit-exact against the oracle's ``fp8_encode`` (techniques/kv_quant/fp8.py:81-86) at every slot;
+  per-head scales bit-exact against ``static_scales`` (fp8.py:130-133).
+* decode: within atol 2e-3 / rtol 1e-2 of the fp32 definition (attention/decode.py:66-103) over the gathered,
+  decoded cache, for GQA shapes, ragged and empty rows, verification queries (causal), soft caps and sinks.
+* every finite fp8 byte decodes exactly (the reference's test_fp8_bytes_decode_exactly,
+  tests/unit/test_attention_kernel.py:146-158): one visible key returns its value row.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8 as ofp8
+from oracle import paged as opaged
+from oracle.numerics import f32_to_bf16_bits
+from paged_cases import FMT_NAME, make_case, oracle_output, to_numpy_f32
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def _decode(case, **kwargs):
+    from economize_amd.paged import paged_decode_attention
+
+    cache = case.device_cache()
+    table = torch.from_numpy(case.table).cuda()
+    lens = torch.tensor(case.lens, dtype=torch.int32).cuda()
+    out = paged_decode_attention(case.q.cuda(), cache, table, lens, max(max(case.lens), 1), **kwargs)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+CASES = [
+    # batch, queries, q heads, kv heads, head dim, lengths, dtype
+    (1, 1, 8, 2, 64, [512], torch.float8_e4m3fn),  # the CPU-runnable plumbing shape
+    (6, 1, 32, 8, 128, [1, 15, 16, 17, 100, 1000], torch.float8_e4m3fn),
+    (3, 1, 32, 8, 128, [300, 64, 1025], torch.bfloat16),
+    (2, 1, 16, 4, 128, [700, 33], torch.float8_e5m2),
+    (2, 4, 16, 2, 128, [260, 71], torch.float8_e4m3fn),  # verification: 32 rows per KV head, causal
+    (2, 8, 64, 8, 128, [200, 129], torch.float8_e4m3fn),  # 64 rows per KV head
+    (2, 2, 8, 8, 256, [90, 300], torch.bfloat16),
+    (3, 1, 4, 4, 64, [0, 5, 40], torch.float8_e4m3fn),  # an empty row gives zeros
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"b{c[0]}q{c[1]}h{c[2]}k{c[3]}d{c[4]}-{str(c[6])[6:]}" for c in CASES])
+def test_decode_matches_the_oracle(case) -> None:
+    batch, queries, hq, hkv, d, lens, dtype = case
+    c = make_case(batch, queries, hq, hkv, d, lens, dtype, seed=sum(lens) + d)
+    got = _decode(c)
+    want = oracle_output(c)
+    np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
+    for b, n in enumerate(lens):
+        if n == 0:
+            assert (got[b] == 0).all()
+
+
+def test_softcap_and_sinks() -> None:
+    c = make_case(2, 2, 16, 4, 128, [333, 50], torch.float8_e4m3fn, seed=7)
+    sinks = np.random.default_rng(0).standard_normal(16).astype(np.float32)
+    got = _decode(c, softcap=5.0, sinks=torch.from_numpy(sinks).cuda(), scale=0.3)
+    want = oracle_output(c, scale=0.3, softcap=5.0, sinks=sinks)
+    np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("dtype", [torch.float8_e4m3fn, torch.float8_e5m2])
+def test_every_fp8_byte_decodes_exactly(dtype) -> None:
+    from economize_amd.paged import PagedKVCache, paged_decode_attention
+
+    raw = np.arange(256, dtype=np.uint8)
+    table = ofp8.decode_table(FMT_NAME[dtype])
+    raw = np.where(np.isfinite(table), raw, 0).astype(np.uint8)
+    d = 256
+    cache = PagedKVCache.empty(1, 1, d, dtype, "cuda")
+    v = np.zeros((1, 1, 16, d), np.uint8)
+    v[0, 0, 0] = raw
+    kc, vc = opaged.scatter_kv(np.zeros((1, 1, 16, d), np.uint8), v, [16], np.zeros((1, 1), np.int32), 1, 16, 1)
+    cache.keys.copy_(torch.from_numpy(kc).view(dtype))
+    cache.values.copy_(torch.from_numpy(vc).view(dtype))
+    q = torch.zeros(1, 1, 2, d, dtype=torch.bfloat16, device="cuda")
+    out = paged_decode_attention(q, cache, torch.zeros(1, 1, dtype=torch.int32, device="cuda"),
+                                 torch.ones(1, dtype=torch.int32, device="cuda"), 1)
+    want = table[raw]
+    got = out[0, 0].float().cpu().numpy()
+    assert np.array_equal(got[0], want) and np.array_equal(got[1], want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float8_e4m3fn, torch.float8_e5m2, torch.bfloat16])
+def test_append_writes_the_oracle_codes(dtype) -> None:
+    from economize_amd.paged import PagedKVCache, head_scales, paged_append
+
+    gen = torch.Generator().manual_seed(3)
+    lens = [37, 16, 70]
+    hkv, d = 4, 128
+    k = (torch.randn(3, hkv, 70, d, generator=gen) * 3).to(torch.bfloat16)
+    v = torch.randn(3, hkv, 70, d, generator=gen).to(torch.bfloat16)
+    k[0, 1, 5, 7] = 1e4  # an outlier sets head 1's key scale
+    table, pages = opaged.shuffled_block_table(lens, 16, seed=4)
+    kf, vf = to_numpy_f32(k), to_numpy_f32(v)
+    mask = np.zeros((3, 1, 70, 1), bool)
+    for b, n in enumerate(lens):
+        mask[b, :, :n] = True
+    scaled = dtype != torch.bfloat16
+    if scaled:
+        fmt = FMT_NAME[dtype]
+        ks_np = ofp8.head_scales(np.where(mask, kf, 0), fmt)
+        vs_np = ofp8.head_scales(np.where(mask, vf, 0), fmt)
+        ks = head_scales(torch.where(torch.from_numpy(mask), k, 0).cuda(), dtype)
+        vs = head_scales(torch.where(torch.from_numpy(mask), v, 0).cuda(), dtype)
+        assert np.array_equal(ks.cpu().numpy(), ks_np) and np.array_equal(vs.cpu().numpy(), vs_np)
+        want_k = ofp8.fp8_encode(kf, fmt, ks_np.reshape(1, -1, 1, 1))
+        want_v = ofp8.fp8_encode(vf, fmt, vs_np.reshape(1, -1, 1, 1))
+        element = 1
+    else:
+        ks = vs = None
+        want_k, want_v = f32_to_bf16_bits(kf), f32_to_bf16_bits(vf)
+        element = 2
+    cache = PagedKVCache.empty(pages, hkv, d, dtype, "cuda", ks, vs)
+    for b, n in enumerate(lens):
+        # appended in two passes: a prompt, then the rest one token at a time in a batch with a padding slot
+        cut = n // 2
+        slots = torch.from_numpy(opaged.slot_mapping(table, b, 0, cut, 16)).cuda()
+        paged_append(cache, k[b, :, :cut].transpose(0, 1).cuda(), v[b, :, :cut].transpose(0, 1).cuda(), slots)
+        for t in range(cut, n):
+            slot = opaged.slot_mapping(table, b, t, 1, 16)
+            slots = torch.tensor([slot[0], -1], dtype=torch.int32).cuda()
+            kk = k[b, :, t: t + 1].transpose(0, 1).repeat(2, 1, 1).cuda()
+            vv = v[b, :, t: t + 1].transpose(0, 1).repeat(2, 1, 1).cuda()
+            paged_append(cache, kk, vv, slots)
+    torch.cuda.synchronize()
+    raw = torch.int16 if element == 2 else torch.uint8
+    got_k = cache.keys.view(raw).cpu().numpy()
+    got_v = cache.values.view(raw).cpu().numpy()
+    if element == 2:
+        got_k, got_v = got_k.view(np.uint16), got_v.view(np.uint16)
+    want_kc, want_vc = opaged.scatter_kv(want_k, want_v, lens, table, pages, 16, element)
+    assert np.array_equal(got_k, want_kc) and np.array_equal(got_v, want_vc)
+
+
+def test_bad_arguments_raise_before_launch() -> None:
+    from economize_amd.errors import ConfigError
+    from economize_amd.paged import PagedKVCache, paged_decode_attention
+
+    cache = PagedKVCache.empty(2, 2, 128, torch.float8_e4m3fn, "cuda")
+    q = torch.zeros(1, 1, 3, 128, dtype=torch.bfloat16, device="cuda")  # 3 query heads over 2 KV heads
+    table = torch.zeros(1, 2, dtype=torch.int32, device="cuda")
+    lens = torch.ones(1, dtype=torch.int32, device="cuda")
+    with pytest.raises(ConfigError):
+        paged_decode_attention(q, cache, table, lens, 1)
+    with pytest.raises(ConfigError):
+        paged_decode_attention(torch.zeros(1, 1, 4, 128, device="cuda"), cache, table, lens, 1)  # fp32 query
