@@ -1,0 +1,254 @@
+"""Benchmark of the fp8 paged decode-attention path on one MI355X.
+
+Workload (one "step" = one decode-attention call over the whole batch): Llama-3-8B decode shape, batch 32, one
+query per row, 32 query heads over 8 KV heads of 128 channels, K/V in fp8 e4m3 with per-head absmax scales, in
+16-token pages assigned from a shuffled page pool. Inputs are resident in HBM before the timed region: q, K and V are
+drawn N(0, 1) in bf16 from a seeded generator and quantize-appended into the cache by the fp8 append kernel.
+
+* ``value``: KV-read GB/s at L = 4096 for every row = sum_b L_b * 2 * Hkv * D bytes / seconds per call (split and
+  merge kernels together, HIP events on the launch stream around ``--steps`` calls after ``--warmup`` calls).
+* ``roofline``: the split (KV-streaming) kernel alone: algorithmic bytes per launch (KV + q + block table + scales)
+  over its average launch time, against 8 TB/s.
+* ``ragged``: the same with lengths drawn uniformly from [1024, 8192] (mean 4608).
+* ``cpu_baseline``: the numpy oracle (the fp32 definition over gathered, decoded pages) on a bounded sample of rows
+  of the L = 4096 workload, one thread, extrapolated to the whole batch.
+
+``--gpus`` must be 1: the path runs on one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BATCH, Q_HEADS, KV_HEADS, HEAD_DIM, PAGE = 32, 32, 8, 128, 16
+TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_fp8_b32_l4096_traffic.txt"
+
+
+def build_workload(lens: list[int], seed: int):
+    """q [B, 1, Hq, D] bf16, a fp8 e4m3 paged cache holding every row's lens[b] tokens, block table, lengths."""
+    import numpy as np
+    import torch
+
+    from economize_amd.paged import PagedKVCache, head_scales, paged_append
+
+    device = torch.device("cuda:0")
+    gen = torch.Generator(device=device).manual_seed(seed)
+    smax = max(lens)
+    q = torch.randn(BATCH, 1, Q_HEADS, HEAD_DIM, generator=gen, device=device).to(torch.bfloat16)
+    need = [-(-n // PAGE) for n in lens]
+    total = sum(need) + 3
+    order = np.random.default_rng(seed + 1).permutation(total)
+    table = np.full((BATCH, max(need)), -1, dtype=np.int32)
+    at = 0
+    for b, n in enumerate(need):
+        table[b, :n] = order[at: at + n]
+        at += n
+    block_table = torch.from_numpy(table).to(device)
+    seq_lens = torch.tensor(lens, dtype=torch.int32, device=device)
+    k = torch.randn(BATCH, KV_HEADS, smax, HEAD_DIM, generator=gen, device=device).to(torch.bfloat16)
+    v = torch.randn(BATCH, KV_HEADS, smax, HEAD_DIM, generator=gen, device=device).to(torch.bfloat16)
+    valid = (torch.arange(smax, device=device)[None, :] < seq_lens[:, None])[:, None, :, None]
+    k = torch.where(valid, k, 0)
+    v = torch.where(valid, v, 0)
+    cache = PagedKVCache.empty(total, KV_HEADS, HEAD_DIM, torch.float8_e4m3fn, device,
+                               head_scales(k), head_scales(v))
+    for b, n in enumerate(lens):
+        t = torch.arange(n, device=device)
+        slots = (block_table[b, t // PAGE] * PAGE + t % PAGE).to(torch.int32)
+        paged_append(cache, k[b, :, :n].transpose(0, 1), v[b, :, :n].transpose(0, 1), slots)
+    torch.cuda.synchronize()
+    del k, v
+    return q, cache, block_table, seq_lens
+
+
+def time_calls(fn, steps: int, warmup: int) -> float:
+    """Average seconds per call of ``fn`` over ``steps`` calls after ``warmup`` calls (HIP events on the current
+    stream, which is the stream the kernels launch on)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / 1e3 / steps
+
+
+def kv_bytes(lens: list[int]) -> int:
+    return sum(lens) * 2 * KV_HEADS * HEAD_DIM  # one byte per fp8 element, K and V
+
+
+def split_kernel_bytes(lens: list[int]) -> int:
+    """Algorithmic bytes the split kernel must read: K/V, the query, the block table entries and the scales."""
+    pages = sum(-(-n // PAGE) for n in lens)
+    return kv_bytes(lens) + BATCH * Q_HEADS * HEAD_DIM * 2 + pages * 4 + 2 * KV_HEADS * 4
+
+
+def measure(lens: list[int], steps: int, warmup: int, seed: int) -> dict:
+    import torch
+
+    from economize_amd.paged import paged_decode_attention, workspace_size
+
+    q, cache, table, seq_lens = build_workload(lens, seed)
+    smax = max(lens)
+    out = torch.empty_like(q)
+    ws = torch.empty(workspace_size(BATCH, 1, Q_HEADS, KV_HEADS, HEAD_DIM, smax), dtype=torch.uint8,
+                     device=q.device)
+
+    def call() -> None:
+        paged_decode_attention(q, cache, table, seq_lens, smax, out=out, workspace=ws)
+
+    def split_only() -> None:
+        paged_decode_attention(q, cache, table, seq_lens, smax, out=out, workspace=ws, split_only=True)
+
+    seconds = time_calls(call, steps, warmup)
+    split_seconds = time_calls(split_only, steps, warmup)
+    return {
+        "seconds": seconds,
+        "split_seconds": split_seconds,
+        "kv_bytes": kv_bytes(lens),
+        "split_bytes": split_kernel_bytes(lens),
+        "workload": (q, cache, table, seq_lens, out),
+    }
+
+
+def cpu_baseline(workload, lens: list[int], budget_s: float = 12.0) -> dict:
+    """The numpy oracle on a bounded sample of rows (one BLAS thread), extrapolated to the batch."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+
+    from oracle import fp8 as ofp8
+    from oracle.attention import reference_attention
+
+    q, cache, table, seq_lens, _ = workload
+    scale = 1.0 / math.sqrt(HEAD_DIM)
+    q_np = q.float().cpu().numpy()
+    table_np = table.cpu().numpy()
+    ks = cache.k_scale.cpu().numpy().reshape(1, -1, 1, 1)
+    vs = cache.v_scale.cpu().numpy().reshape(1, -1, 1, 1)
+    done_rows = 0
+    elapsed = 0.0
+    with threadpool_limits(1):
+        for b in range(BATCH):
+            pages = table_np[b, : -(-lens[b] // PAGE)]
+            kc = cache.keys[torch.from_numpy(pages).long().to(cache.keys.device)].view(torch.uint8).cpu().numpy()
+            vc = cache.values[torch.from_numpy(pages).long().to(cache.keys.device)].view(torch.uint8).cpu().numpy()
+            t0 = time.perf_counter()
+            # gather: keys [P, H, D/16, 16, 16] -> [H, P*16, D]; values [P, H, D, 16] -> [H, P*16, D]
+            k = kc.transpose(1, 0, 3, 2, 4).reshape(KV_HEADS, -1, HEAD_DIM)[:, : lens[b]]
+            v = vc.transpose(1, 0, 3, 2).reshape(KV_HEADS, -1, HEAD_DIM)[:, : lens[b]]
+            kd = ofp8.fp8_decode(k[None], "e4m3", ks, "f32")
+            vd = ofp8.fp8_decode(v[None], "e4m3", vs, "f32")
+            reference_attention(q_np[b: b + 1].transpose(0, 2, 1, 3), kd, vd, None, scale)
+            elapsed += time.perf_counter() - t0
+            done_rows += 1
+            if elapsed > budget_s:
+                break
+    per_call = elapsed / done_rows * BATCH
+    return {
+        "value": kv_bytes(lens) / per_call / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "us_per_call": per_call * 1e6,
+        "sample": f"{done_rows} of {BATCH} rows of the L=4096 batch (numpy oracle: page gather, fp8 decode, fp32 "
+                  f"attention), {elapsed:.1f} s, extrapolated to {BATCH} rows",
+    }
+
+
+def traffic_per_launch() -> float | None:
+    """HBM bytes per split-kernel launch from the committed rocprofv3 counter summary, if present."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("hbm_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def main() -> None:
+    parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--seed", type=int, default=0)
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the decode-attention path shards by (batch row, KV head) with no "
+              f"collective, so --gpus {args.gpus} is not run; use --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    fixed = [4096] * BATCH
+    head = measure(fixed, args.steps, args.warmup, args.seed)
+    ragged_lens = np.random.default_rng(args.seed + 100).integers(1024, 8193, BATCH).tolist()
+    ragged = measure(ragged_lens, args.steps, args.warmup, args.seed + 1)
+    cpu = None if args.no_cpu else cpu_baseline(head["workload"], fixed)
+
+    value = head["kv_bytes"] / head["seconds"] / 1e9
+    achieved = head["split_bytes"] / head["split_seconds"] / 1e9
+    traffic = traffic_per_launch()
+    line = {
+        "metric": "KV-read GB/s (% HBM peak) + µs per decode-attn call, Llama-3-8B B=32 L=4096",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["seconds"] * 1e3, 5),
+        "us_per_call": round(head["seconds"] * 1e6, 2),
+        "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8_e4m3",
+        "data": "synthetic",
+        "config": {
+            "workload": "fp8 e4m3 paged decode attention (per-head scales), Llama-3-8B decode shape",
+            "batch": BATCH, "q_len": 1, "q_heads": Q_HEADS, "kv_heads": KV_HEADS, "head_dim": HEAD_DIM,
+            "seq_len": 4096, "page_size": PAGE, "kv_bytes_per_call": head["kv_bytes"],
+            "compute": "bf16 x bf16 MFMA for q.k, fp16 x fp16 MFMA for p.v, fp32 accumulation",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "paged_split_kernel",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": head["split_bytes"],
+            "us_per_launch": round(head["split_seconds"] * 1e6, 2),
+        },
+        "ragged": {
+            "lens": "uniform [1024, 8192], seed 100",
+            "sum_len": int(sum(ragged_lens)),
+            "us_per_call": round(ragged["seconds"] * 1e6, 2),
+            "kv_gb_s": round(ragged["kv_bytes"] / ragged["seconds"] / 1e9, 1),
+            "hbm_frac": round(ragged["kv_bytes"] / ragged["seconds"] / 1e9 / HBM_PEAK_GBS, 4),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
