@@ -101,13 +101,12 @@ def split_kernel_bytes(lens: list[int]) -> int:
 def measure(lens: list[int], steps: int, warmup: int, seed: int) -> dict:
     import torch
 
-    from economize_amd.paged import paged_decode_attention, workspace_size
+    from economize_amd.paged import new_workspace, paged_decode_attention, workspace_size
 
     q, cache, table, seq_lens = build_workload(lens, seed)
     smax = max(lens)
     out = torch.empty_like(q)
-    ws = torch.empty(workspace_size(BATCH, 1, Q_HEADS, KV_HEADS, HEAD_DIM, smax), dtype=torch.uint8,
-                     device=q.device)
+    ws = new_workspace(workspace_size(BATCH, 1, Q_HEADS, KV_HEADS, HEAD_DIM, smax), q.device)
 
     def call() -> None:
         paged_decode_attention(q, cache, table, seq_lens, smax, out=out, workspace=ws)

@@ -78,14 +78,17 @@ PagedPlan paged_plan(int batch, int kv_heads, int max_virt) {
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
+// Workspace: split counters [B * Hkv] int32 (must be zero before the first call; every call leaves them zero),
+// then the partial accumulators [B, Hkv, splits, rows, D] and the partial maxima and sums [B, Hkv, splits, rows].
 struct Workspace {
-    size_t o_bytes, ml_bytes;
-    size_t total() const { return o_bytes + 2 * ml_bytes; }
+    size_t counter_bytes, o_bytes, ml_bytes;
+    size_t total() const { return counter_bytes + o_bytes + 2 * ml_bytes; }
 };
 
 Workspace paged_workspace(int batch, int kv_heads, int rows, int head_dim, int max_splits) {
     const size_t parts = static_cast<size_t>(batch) * kv_heads * max_splits * rows;
-    return Workspace{align256(parts * head_dim * sizeof(float)), align256(parts * sizeof(float))};
+    return Workspace{align256(static_cast<size_t>(batch) * kv_heads * sizeof(int32_t)),
+                     align256(parts * head_dim * sizeof(float)), align256(parts * sizeof(float))};
 }
 
 int max_virtual_pages(int max_seq_len, int n_sel) { return (max_seq_len + 15) / 16 + (n_sel > 0 ? n_sel : 0); }
@@ -152,9 +155,10 @@ int run_paged_decode(bool merge, const void* q, int64_t sq_b, int64_t sq_q, int6
     p.v_scale = v_scale;
     p.sinks = sinks;
     char* base = static_cast<char*>(workspace);
-    p.part_o = reinterpret_cast<float*>(base);
-    p.part_m = reinterpret_cast<float*>(base + ws.o_bytes);
-    p.part_l = reinterpret_cast<float*>(base + ws.o_bytes + ws.ml_bytes);
+    p.counters = reinterpret_cast<int32_t*>(base);
+    p.part_o = reinterpret_cast<float*>(base + ws.counter_bytes);
+    p.part_m = reinterpret_cast<float*>(base + ws.counter_bytes + ws.o_bytes);
+    p.part_l = reinterpret_cast<float*>(base + ws.counter_bytes + ws.o_bytes + ws.ml_bytes);
     p.out = static_cast<uint16_t*>(out);
     p.so_b = so_b;
     p.so_q = so_q;
@@ -169,12 +173,10 @@ int run_paged_decode(bool merge, const void* q, int64_t sq_b, int64_t sq_q, int6
     p.kv_format = kv_format;
     p.split_pages = plan.split_pages;
     p.max_splits = plan.max_splits;
+    p.fused = merge ? 1 : 0;
     p.scale = scale;
     p.softcap = softcap > 0.0f ? softcap : 0.0f;
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    if (int rc = paged_split(p, s)) return rc;
-    if (merge) return paged_merge(p, s);
-    return 0;
+    return paged_split(p, static_cast<hipStream_t>(stream));
 }
 
 }  // namespace

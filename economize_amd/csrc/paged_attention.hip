@@ -27,8 +27,9 @@
 // moves short rows by ~2^-9 of |v|). A bf16 cache multiplies its bf16 values by P split into two bf16 terms
 // (P = P_hi + P_lo, 16 significant bits), two MFMAs per block.
 //
-// The waves of a workgroup merge their (max, sum, acc) in LDS and write one partial per split; a second kernel
-// merges the splits by log-sum-exp (attention/_decode_kernels.py:183-226) and writes bf16.
+// The waves of a workgroup merge their (max, sum, acc) in LDS. A row with one split writes its bf16 output directly;
+// otherwise each split writes a partial and the last split of the row to finish (a per-(b, kvh) counter in the
+// workspace) merges them by log-sum-exp (attention/_decode_kernels.py:183-226), so one launch does the whole call.
 
 #include "common.hpp"
 #include "paged_attention.hpp"
@@ -121,6 +122,61 @@ __device__ inline int virtual_pages(const PagedParams& p, int b, int* done_out) 
     return p.n_sel + max(0, pages - done);
 }
 
+// Splits that hold pages of a row with n_virt virtual pages (rows longer than the launch's max_seq_len are cut at
+// the planned splits: their later pages are not read).
+__device__ inline int row_splits(const PagedParams& p, int n_virt) {
+    return n_virt <= 0 ? 0 : min((n_virt + p.split_pages - 1) / p.split_pages, p.max_splits);
+}
+
+// out[b, qi, h, d] of query row r from its merged (acc, max, sum) in log2 units, with the sink logit of head h in
+// the denominator (attention/_decode_kernels.py:216-226): zeros for a row that sees nothing.
+__device__ inline void store_output(const PagedParams& p, int b, int kvh, int r, int d, float o, float m, float l) {
+    const int gq = r / p.queries;
+    const int qi = r % p.queries;
+    const int h = kvh * p.groups + gq;
+    if (p.sinks) {
+        const float sink = p.sinks[h] * kLog2e;
+        const float m_new = fmaxf(m, sink);
+        const float a = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - m_new);
+        o *= a;
+        l = l * a + __builtin_amdgcn_exp2f(sink - m_new);
+    }
+    const float out = l > 0.0f ? o / fmaxf(l, 1e-30f) : 0.0f;
+    p.out[b * p.so_b + qi * p.so_q + h * p.so_h + d] = f32_to_bf16(out);
+}
+
+// Device-coherent (agent-scope) store and load of partials: they bypass the caches that are not coherent across the
+// chip's XCDs (gfx950 lowers them to global_store / global_load with sc1), so no L2 writeback or invalidation is
+// needed to hand a partial from one workgroup to another.
+__device__ inline void coherent_store(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+__device__ inline float coherent_load(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Log-sum-exp merge of a row's split partials, in split order (attention/_decode_kernels.py:183-215).
+template <int D>
+__device__ inline void merge_splits(const PagedParams& p, int b, int kvh, int n_splits, int tid, int threads) {
+    const int64_t part = (static_cast<int64_t>(b) * p.kv_heads + kvh) * p.max_splits * p.rows;
+    for (int idx = tid; idx < p.rows * D; idx += threads) {
+        const int r = idx / D;
+        const int d = idx % D;
+        float m = -INFINITY;
+        for (int s = 0; s < n_splits; ++s) m = fmaxf(m, coherent_load(p.part_m + part + s * p.rows + r));
+        float o = 0.0f, l = 0.0f;
+        if (m != -INFINITY) {
+            for (int s = 0; s < n_splits; ++s) {
+                const float ms = coherent_load(p.part_m + part + s * p.rows + r);
+                if (ms == -INFINITY) continue;
+                const float c = __builtin_amdgcn_exp2f(ms - m);
+                o += coherent_load(p.part_o + (part + s * p.rows + r) * D + d) * c;
+                l += coherent_load(p.part_l + part + s * p.rows + r) * c;
+            }
+        }
+        store_output(p, b, kvh, r, d, o, m, l);
+    }
+}
+
 template <int D, int FMT, int NB, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void paged_split_kernel(PagedParams p) {
     constexpr int ES = FMT == BF16 ? 2 : 1;  // bytes per element
@@ -142,7 +198,13 @@ __global__ __launch_bounds__(64 * WAVES) void paged_split_kernel(PagedParams p) 
     int done = 0;
     const int n_virt = virtual_pages(p, b, &done);
     const int v_begin = split * p.split_pages;
-    if (v_begin >= n_virt) return;  // uniform over the workgroup: this split of the row is empty
+    if (v_begin >= n_virt) {  // uniform over the workgroup: this split of the row is empty
+        if (p.fused && split == 0) {  // a row with no key: zeros (sinks included, decode.py:17)
+            for (int idx = threadIdx.x; idx < p.rows * D; idx += 64 * WAVES)
+                store_output(p, b, kvh, idx / D, idx % D, 0.0f, -INFINITY, 0.0f);
+        }
+        return;
+    }
     const int v_end = min(v_begin + p.split_pages, n_virt);
     const int len = p.seq_lens[b];
 
@@ -340,12 +402,13 @@ __global__ __launch_bounds__(64 * WAVES) void paged_split_kernel(PagedParams p) 
         }
     }
 
-    // ---- merge the waves in LDS and write the split's partial ----
+    // ---- merge the waves in LDS ----
     // acc fragment of lane (n, g): channel 16 nd + 4 g + i of column nb * 16 + n.
     constexpr int SLOTS = ND * NB * 4;
     __shared__ float lds_acc[WAVES][SLOTS][64];
     __shared__ float lds_m[WAVES][16 * NB];
     __shared__ float lds_l[WAVES][16 * NB];
+    __shared__ int lds_last;
 #pragma unroll
     for (int nd = 0; nd < ND; ++nd)
 #pragma unroll
@@ -361,17 +424,19 @@ __global__ __launch_bounds__(64 * WAVES) void paged_split_kernel(PagedParams p) 
     }
     __syncthreads();
 
-    const int64_t part = (static_cast<int64_t>(b * p.kv_heads + kvh) * p.max_splits + split) * p.rows;
+    // A row with one split writes its output here; otherwise every split writes a partial (max, sum, acc) and the
+    // last split of the row to finish merges them (a device-scope counter per (b, kvh), reset by that split).
+    const int n_splits = row_splits(p, n_virt);
+    const int64_t bh = static_cast<int64_t>(b) * p.kv_heads + kvh;
+    const int64_t part = (bh * p.max_splits + split) * p.rows;
+    const bool direct = p.fused && n_splits == 1;
     for (int idx = threadIdx.x; idx < p.rows * D; idx += 64 * WAVES) {
         const int r = idx / D;
         const int d = idx % D;
         const int nb = r >> 4;
         const int col = r & 15;
-        const int nd = d >> 4;
-        const int gi = (d & 15) >> 2;
-        const int i = d & 3;
-        const int slot = (nd * NB + nb) * 4 + i;
-        const int src_lane = gi * 16 + col;
+        const int slot = ((d >> 4) * NB + nb) * 4 + (d & 3);
+        const int src_lane = ((d & 15) >> 2) * 16 + col;
         float m = -INFINITY;
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) m = fmaxf(m, lds_m[w][r]);
@@ -386,50 +451,30 @@ __global__ __launch_bounds__(64 * WAVES) void paged_split_kernel(PagedParams p) 
                 l += lds_l[w][r] * c;
             }
         }
-        p.part_o[(part + r) * D + d] = o * vs;
-        if (d == 0) {
-            p.part_m[part + r] = m;
-            p.part_l[part + r] = l;
-        }
-    }
-}
-
-template <int D>
-__global__ __launch_bounds__(256) void paged_merge_kernel(PagedParams p) {
-    const int kvh = blockIdx.x;
-    const int b = blockIdx.y;
-    int done = 0;
-    const int n_virt = virtual_pages(p, b, &done);
-    // rows longer than the launch's max_seq_len are cut at the planned splits (their later pages are not read)
-    const int n_splits = min((n_virt + p.split_pages - 1) / p.split_pages, p.max_splits);
-    const int64_t part = static_cast<int64_t>(b * p.kv_heads + kvh) * p.max_splits * p.rows;
-    for (int idx = threadIdx.x; idx < p.rows * D; idx += blockDim.x) {
-        const int r = idx / D;
-        const int d = idx % D;
-        float m = -INFINITY;
-        for (int s = 0; s < n_splits; ++s) m = fmaxf(m, p.part_m[part + s * p.rows + r]);
-        const int gq = r / p.queries;
-        const int qi = r % p.queries;
-        const int h = kvh * p.groups + gq;
-        float sink = -INFINITY;
-        if (p.sinks) {
-            sink = p.sinks[h] * kLog2e;
-            m = fmaxf(m, sink);
-        }
-        float o = 0.0f, l = 0.0f;
-        if (m != -INFINITY) {
-            for (int s = 0; s < n_splits; ++s) {
-                const float ms = p.part_m[part + s * p.rows + r];
-                if (ms == -INFINITY) continue;
-                const float c = __builtin_amdgcn_exp2f(ms - m);
-                o += p.part_o[(part + s * p.rows + r) * D + d] * c;
-                l += p.part_l[part + s * p.rows + r] * c;
+        o *= vs;
+        if (direct) {
+            store_output(p, b, kvh, r, d, o, m, l);
+        } else {
+            coherent_store(p.part_o + (part + r) * D + d, o);
+            if (d == 0) {
+                coherent_store(p.part_m + part + r, m);
+                coherent_store(p.part_l + part + r, l);
             }
-            if (p.sinks) l += __builtin_amdgcn_exp2f(sink - m);
         }
-        const float out = l > 0.0f ? o / fmaxf(l, 1e-30f) : 0.0f;
-        p.out[b * p.so_b + qi * p.so_q + h * p.so_h + d] = f32_to_bf16(out);
     }
+    if (!p.fused || direct) return;
+    // The partial was written with device-coherent stores: every wave waits until its stores completed (vmcnt 0),
+    // the barrier joins the waves, then one thread counts the split. The last split reads the partials back with
+    // device-coherent loads.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        lds_last = __hip_atomic_fetch_add(p.counters + bh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   n_splits - 1;
+    __syncthreads();
+    if (!lds_last) return;
+    merge_splits<D>(p, b, kvh, n_splits, threadIdx.x, 64 * WAVES);
+    if (threadIdx.x == 0) __hip_atomic_store(p.counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- host side ----------------------------------------------------------------------------------------------
@@ -474,17 +519,6 @@ int paged_split(const PagedParams& p, hipStream_t stream) {
         case 256: return dispatch_fmt<256>(p, stream);
         default: return fail("paged decode attention supports head dims 64, 128 and 256");
     }
-}
-
-int paged_merge(const PagedParams& p, hipStream_t stream) {
-    dim3 grid(p.kv_heads, p.batch);
-    switch (p.head_dim) {
-        case 64: hipLaunchKernelGGL(paged_merge_kernel<64>, grid, dim3(256), 0, stream, p); break;
-        case 128: hipLaunchKernelGGL(paged_merge_kernel<128>, grid, dim3(256), 0, stream, p); break;
-        case 256: hipLaunchKernelGGL(paged_merge_kernel<256>, grid, dim3(256), 0, stream, p); break;
-        default: return fail("paged decode attention supports head dims 64, 128 and 256");
-    }
-    return check_launch("paged_merge_kernel");
 }
 
 }  // namespace eco

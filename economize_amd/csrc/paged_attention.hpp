@@ -26,6 +26,7 @@ struct PagedParams {
     const float* k_scale;  // optional [Hkv]
     const float* v_scale;
     const float* sinks;  // optional [Hq] logits
+    int32_t* counters;  // [B * Hkv], zero between calls (the merging split resets its counter)
     float* part_o;
     float* part_m;
     float* part_l;
@@ -33,10 +34,10 @@ struct PagedParams {
     int64_t so_b, so_q, so_h;
     int batch, queries, q_heads, kv_heads, groups, rows, head_dim, kv_format;
     int split_pages, max_splits;
+    int fused;  // 1: merge in the last split of each row; 0: write partials only (profiling)
     float scale, softcap;
 };
 
 int paged_split(const PagedParams& p, hipStream_t stream);
-int paged_merge(const PagedParams& p, hipStream_t stream);
 
 }  // namespace eco

@@ -22,7 +22,9 @@ import torch
 from . import _lib
 from .errors import ConfigError
 
-__all__ = ["PAGE", "PagedKVCache", "head_scales", "paged_append", "paged_decode_attention", "workspace_size"]
+__all__ = [
+    "PAGE", "PagedKVCache", "head_scales", "new_workspace", "paged_append", "paged_decode_attention", "workspace_size",
+]
 
 #: Tokens per page.
 PAGE = 16
@@ -135,6 +137,25 @@ def workspace_size(batch: int, queries: int, q_heads: int, kv_heads: int, head_d
                                                           n_sel))
 
 
+def new_workspace(nbytes: int, device: torch.device | str) -> torch.Tensor:
+    """A workspace for :func:`paged_decode_attention`: zeroed, since the split counters at its start must be zero
+    before the first call (every call leaves them zero). One workspace serves one stream at a time."""
+    return torch.zeros(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+_workspaces: dict[tuple[torch.device, int], torch.Tensor] = {}
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    """The cached workspace of ``device`` (grown on demand) used when the caller passes none."""
+    stream = torch.cuda.current_stream(device).cuda_stream
+    key = (device, stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = _workspaces[key] = new_workspace(max(nbytes, 2 * (ws.numel() if ws is not None else 0)), device)
+    return ws
+
+
 def paged_decode_attention(
     query: torch.Tensor,
     cache: PagedKVCache,
@@ -159,7 +180,8 @@ def paged_decode_attention(
 
     With ``page_list`` (int32 ``[B, Hkv, n_sel]``, logical pages, ``-1`` = none) and ``done`` (int32 ``[B]``) the
     keys read are the listed pages and every token from page ``done[b]`` on (Quest's gathered attention).
-    ``split_only`` launches only the KV-streaming phase (profiling; ``out`` is not written).
+    ``workspace`` (from :func:`new_workspace`, at least :func:`workspace_size` bytes) defaults to a cached one per
+    device and stream. ``split_only`` launches only the KV-streaming phase (profiling; ``out`` is not written).
     """
     cache.check()
     device = _lib.require_gpu(query, cache.keys, block_table, seq_lens)
@@ -193,7 +215,7 @@ def paged_decode_attention(
         raise ConfigError("out must be bf16 like the query, with a contiguous channel axis")
     need = workspace_size(batch, queries, q_heads, cache.kv_heads, head_dim, max_seq_len, n_sel)
     if workspace is None:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+        workspace = _workspace(need, device)
     scale = 1.0 / math.sqrt(head_dim) if scale is None else float(scale)
     _lib.call(
         "eco_paged_decode_split_only" if split_only else "eco_paged_decode",

@@ -60,6 +60,24 @@ def test_decode_matches_the_oracle(case) -> None:
             assert (got[b] == 0).all()
 
 
+def test_repeated_calls_reset_the_split_counters() -> None:
+    """The merging split resets its row's counter: calls on one workspace keep agreeing with the oracle, for rows
+    with one split, several splits and none."""
+    from economize_amd.paged import new_workspace, paged_decode_attention, workspace_size
+
+    c = make_case(4, 1, 32, 8, 128, [4000, 20, 0, 2500], torch.float8_e4m3fn, seed=11)
+    cache = c.device_cache()
+    table = torch.from_numpy(c.table).cuda()
+    lens = torch.tensor(c.lens, dtype=torch.int32).cuda()
+    ws = new_workspace(workspace_size(4, 1, 32, 8, 128, 4000), "cuda")
+    want = oracle_output(c)
+    for _ in range(3):
+        out = paged_decode_attention(c.q.cuda(), cache, table, lens, 4000, workspace=ws)
+        np.testing.assert_allclose(out.float().cpu().numpy(), want, atol=ATOL, rtol=RTOL)
+    counters = ws[: 4 * 8 * 4].view(torch.int32)
+    assert int(counters.abs().sum()) == 0
+
+
 def test_softcap_and_sinks() -> None:
     c = make_case(2, 2, 16, 4, 128, [333, 50], torch.float8_e4m3fn, seed=7)
     sinks = np.random.default_rng(0).standard_normal(16).astype(np.float32)
