@@ -7,8 +7,8 @@ drawn N(0, 1) in bf16 from a seeded generator and quantize-appended into the cac
 
 * ``value``: KV-read GB/s at L = 4096 for every row = sum_b L_b * 2 * Hkv * D bytes / seconds per call (split and
   merge kernels together, HIP events on the launch stream around ``--steps`` calls after ``--warmup`` calls).
-* ``roofline``: the split (KV-streaming) kernel alone: algorithmic bytes per launch (KV + q + block table + scales)
-  over its average launch time, against 8 TB/s.
+* ``roofline``: the call is one kernel launch (``paged_attention_kernel``): algorithmic bytes per launch (KV + q +
+  out + block table + lengths + scales) over its average launch time, against 8 TB/s.
 * ``ragged``: the same with lengths drawn uniformly from [1024, 8192] (mean 4608).
 * ``cpu_baseline``: the numpy oracle (the fp32 definition over gathered, decoded pages) on a bounded sample of rows
   of the L = 4096 workload, one thread, extrapolated to the whole batch.
@@ -92,10 +92,11 @@ def kv_bytes(lens: list[int]) -> int:
     return sum(lens) * 2 * KV_HEADS * HEAD_DIM  # one byte per fp8 element, K and V
 
 
-def split_kernel_bytes(lens: list[int]) -> int:
-    """Algorithmic bytes the split kernel must read: K/V, the query, the block table entries and the scales."""
+def call_bytes(lens: list[int]) -> int:
+    """Algorithmic bytes of one call: K/V, the query and the output (bf16), the block table entries, the lengths and
+    the scales."""
     pages = sum(-(-n // PAGE) for n in lens)
-    return kv_bytes(lens) + BATCH * Q_HEADS * HEAD_DIM * 2 + pages * 4 + 2 * KV_HEADS * 4
+    return kv_bytes(lens) + 2 * BATCH * Q_HEADS * HEAD_DIM * 2 + pages * 4 + BATCH * 4 + 2 * KV_HEADS * 4
 
 
 def measure(lens: list[int], steps: int, warmup: int, seed: int) -> dict:
@@ -106,21 +107,16 @@ def measure(lens: list[int], steps: int, warmup: int, seed: int) -> dict:
     q, cache, table, seq_lens = build_workload(lens, seed)
     smax = max(lens)
     out = torch.empty_like(q)
-    ws = new_workspace(workspace_size(BATCH, 1, Q_HEADS, KV_HEADS, HEAD_DIM, smax), q.device)
+    ws = new_workspace(workspace_size(BATCH, 1, Q_HEADS, KV_HEADS, HEAD_DIM, smax, 0, cache.dtype), q.device)
 
     def call() -> None:
         paged_decode_attention(q, cache, table, seq_lens, smax, out=out, workspace=ws)
 
-    def split_only() -> None:
-        paged_decode_attention(q, cache, table, seq_lens, smax, out=out, workspace=ws, split_only=True)
-
     seconds = time_calls(call, steps, warmup)
-    split_seconds = time_calls(split_only, steps, warmup)
     return {
         "seconds": seconds,
-        "split_seconds": split_seconds,
         "kv_bytes": kv_bytes(lens),
-        "split_bytes": split_kernel_bytes(lens),
+        "call_bytes": call_bytes(lens),
         "workload": (q, cache, table, seq_lens, out),
     }
 
@@ -203,7 +199,7 @@ def main() -> None:
     cpu = None if args.no_cpu else cpu_baseline(head["workload"], fixed)
 
     value = head["kv_bytes"] / head["seconds"] / 1e9
-    achieved = head["split_bytes"] / head["split_seconds"] / 1e9
+    achieved = head["call_bytes"] / head["seconds"] / 1e9
     traffic = traffic_per_launch()
     line = {
         "metric": "KV-read GB/s (% HBM peak) + µs per decode-attn call, Llama-3-8B B=32 L=4096",
@@ -228,14 +224,14 @@ def main() -> None:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "paged_split_kernel",
+            "kernel": "paged_attention_kernel",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "algorithmic_bytes_per_launch": head["split_bytes"],
-            "us_per_launch": round(head["split_seconds"] * 1e6, 2),
+            "algorithmic_bytes_per_launch": head["call_bytes"],
+            "us_per_launch": round(head["seconds"] * 1e6, 2),
         },
         "ragged": {
             "lens": "uniform [1024, 8192], seed 100",

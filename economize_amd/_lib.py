@@ -37,9 +37,8 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
     "eco_paged_append": (c_int32, [_P, _P, _I, _L, _L, _L, _L, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "eco_kv_head_absmax": (c_int32, [_P, _I, _I, _I, _I, _I, _L, _L, _L, _L, _P, _P]),
     "eco_fp8_scales_from_absmax": (c_int32, [_P, _I, _I, _P, _P]),
-    "eco_paged_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I]),
+    "eco_paged_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I, _I]),
     "eco_paged_decode": (c_int32, _PAGED_DECODE),
-    "eco_paged_decode_split_only": (c_int32, _PAGED_DECODE),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -47,53 +47,38 @@ int device_cus() {
     return cached[device];
 }
 
-struct PagedPlan {
-    int split_pages;
-    int max_splits;
-};
-
-// Splits sized so that the batch's KV heads and splits give about four workgroups per CU over the longest row; a
-// split holds whole tiles of 4 pages per wave (ECO_SPLIT_PAGES overrides the split length for tuning).
-PagedPlan paged_plan(int batch, int kv_heads, int max_virt) {
-    PagedPlan plan;
-    max_virt = max_virt < 1 ? 1 : max_virt;
-    static const int forced = [] {
-        const char* env = std::getenv("ECO_SPLIT_PAGES");
-        return env ? std::atoi(env) : 0;
-    }();
-    if (forced > 0) {
-        plan.split_pages = forced;
-    } else {
-        const int pairs = batch * kv_heads;
-        const int target = 4 * device_cus();
-        int splits = (target + pairs - 1) / pairs;
-        const int tiles = (max_virt + 3) / 4;
-        splits = splits < 1 ? 1 : (splits > tiles ? tiles : splits);
-        int pages = (max_virt + splits - 1) / splits;
-        plan.split_pages = (pages + 15) / 16 * 16;  // whole tiles for each of up to four waves
-    }
-    plan.max_splits = (max_virt + plan.split_pages - 1) / plan.split_pages;
-    return plan;
-}
-
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-// Workspace: split counters [B * Hkv] int32 (must be zero before the first call; every call leaves them zero),
-// then the partial accumulators [B, Hkv, splits, rows, D] and the partial maxima and sums [B, Hkv, splits, rows].
-struct Workspace {
-    size_t counter_bytes, o_bytes, ml_bytes;
-    size_t total() const { return counter_bytes + o_bytes + 2 * ml_bytes; }
-};
-
-Workspace paged_workspace(int batch, int kv_heads, int rows, int head_dim, int max_splits) {
-    const size_t parts = static_cast<size_t>(batch) * kv_heads * max_splits * rows;
-    return Workspace{align256(static_cast<size_t>(batch) * kv_heads * sizeof(int32_t)),
-                     align256(parts * head_dim * sizeof(float)), align256(parts * sizeof(float))};
+// Single-wave workgroups of a launch: every CU's resident waves of the kernel instance, but at least four tiles
+// (256 tokens) per wave over the longest possible tile sequence, which bounds the partials a row can be cut into
+// (ECO_PAGED_GRID overrides the count for tuning).
+int paged_grid(int batch, int kv_heads, int rows, int head_dim, int format, int max_seq_len, int n_sel) {
+    static const int forced = [] {
+        const char* env = std::getenv("ECO_PAGED_GRID");
+        return env ? std::atoi(env) : 0;
+    }();
+    const int64_t tiles = static_cast<int64_t>(batch) * kv_heads * (((max_seq_len + 15) / 16 + n_sel + 3) / 4);
+    int per_cu = 1;
+    if (paged_resident_waves(head_dim, format, rows, &per_cu)) return 0;
+    int64_t grid = forced > 0 ? forced : static_cast<int64_t>(device_cus()) * per_cu;
+    const int64_t cap = (tiles + 3) / 4;
+    grid = grid < cap ? grid : cap;
+    return static_cast<int>(grid < 1 ? 1 : grid);
 }
 
-int max_virtual_pages(int max_seq_len, int n_sel) { return (max_seq_len + 15) / 16 + (n_sel > 0 ? n_sel : 0); }
+// Workspace: row counters [B * Hkv] int32 (zero before the first call; every call leaves them zero), then two
+// partial slots per wave, each [rows, D + 2] floats (maxima, sums, accumulators).
+struct Workspace {
+    size_t counter_bytes, part_bytes;
+    size_t total() const { return counter_bytes + part_bytes; }
+};
 
-int run_paged_decode(bool merge, const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
+Workspace paged_workspace(int batch, int kv_heads, int rows, int head_dim, int grid) {
+    return Workspace{align256(static_cast<size_t>(batch) * kv_heads * sizeof(int32_t)),
+                     align256(static_cast<size_t>(2) * grid * rows * (head_dim + 2) * sizeof(float))};
+}
+
+int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
                      const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
                      const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
                      const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h, int32_t n_sel, const int32_t* done,
@@ -121,9 +106,9 @@ int run_paged_decode(bool merge, const void* q, int64_t sq_b, int64_t sq_q, int6
     if (max_seq_len <= 0) return fail("paged decode: max_seq_len must be positive");
     if (!(scale == scale)) return fail("paged decode: scale is NaN");
 
-    const int max_virt = max_virtual_pages(max_seq_len, page_list ? n_sel : 0);
-    const PagedPlan plan = paged_plan(batch, kv_heads, max_virt);
-    const Workspace ws = paged_workspace(batch, kv_heads, rows, head_dim, plan.max_splits);
+    const int grid = paged_grid(batch, kv_heads, rows, head_dim, kv_format, max_seq_len, page_list ? n_sel : 0);
+    if (grid <= 0) return 1;
+    const Workspace ws = paged_workspace(batch, kv_heads, rows, head_dim, grid);
     if (!workspace || workspace_bytes < ws.total())
         return fail("paged decode: workspace too small (" + std::to_string(workspace_bytes) + " < " +
                     std::to_string(ws.total()) + " bytes)");
@@ -156,9 +141,7 @@ int run_paged_decode(bool merge, const void* q, int64_t sq_b, int64_t sq_q, int6
     p.sinks = sinks;
     char* base = static_cast<char*>(workspace);
     p.counters = reinterpret_cast<int32_t*>(base);
-    p.part_o = reinterpret_cast<float*>(base + ws.counter_bytes);
-    p.part_m = reinterpret_cast<float*>(base + ws.counter_bytes + ws.o_bytes);
-    p.part_l = reinterpret_cast<float*>(base + ws.counter_bytes + ws.o_bytes + ws.ml_bytes);
+    p.part = reinterpret_cast<float*>(base + ws.counter_bytes);
     p.out = static_cast<uint16_t*>(out);
     p.so_b = so_b;
     p.so_q = so_q;
@@ -171,12 +154,10 @@ int run_paged_decode(bool merge, const void* q, int64_t sq_b, int64_t sq_q, int6
     p.rows = rows;
     p.head_dim = head_dim;
     p.kv_format = kv_format;
-    p.split_pages = plan.split_pages;
-    p.max_splits = plan.max_splits;
-    p.fused = merge ? 1 : 0;
+    p.grid = grid;
     p.scale = scale;
     p.softcap = softcap > 0.0f ? softcap : 0.0f;
-    return paged_split(p, static_cast<hipStream_t>(stream));
+    return paged_attention(p, static_cast<hipStream_t>(stream));
 }
 
 }  // namespace
@@ -252,11 +233,12 @@ int eco_fp8_scales_from_absmax(const uint32_t* absmax_bits, int32_t heads, int32
 }
 
 size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
-                                       int32_t head_dim, int32_t max_seq_len, int32_t n_sel) {
-    if (batch <= 0 || queries <= 0 || kv_heads <= 0 || q_heads <= 0 || head_dim <= 0) return 0;
-    const PagedPlan plan = paged_plan(batch, kv_heads, max_virtual_pages(max_seq_len, n_sel));
+                                       int32_t head_dim, int32_t max_seq_len, int32_t n_sel, int32_t kv_format) {
+    if (batch <= 0 || queries <= 0 || kv_heads <= 0 || q_heads <= 0 || head_dim <= 0 || max_seq_len <= 0) return 0;
     const int rows = (q_heads / kv_heads) * queries;
-    return paged_workspace(batch, kv_heads, rows, head_dim, plan.max_splits).total();
+    const int grid = paged_grid(batch, kv_heads, rows, head_dim, kv_format, max_seq_len, n_sel > 0 ? n_sel : 0);
+    if (grid <= 0) return 0;
+    return paged_workspace(batch, kv_heads, rows, head_dim, grid).total();
 }
 
 int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
@@ -267,21 +249,7 @@ int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
                      int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
                      int32_t max_seq_len, float scale, float softcap, void* workspace, size_t workspace_bytes,
                      void* stream) {
-    return run_paged_decode(true, q, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
-                            block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel, done, sinks, out, so_b,
-                            so_q, so_h, batch, queries, q_heads, kv_heads, head_dim, page_size, max_seq_len, scale,
-                            softcap, workspace, workspace_bytes, stream);
-}
-
-int eco_paged_decode_split_only(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
-                                const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
-                                const float* v_scale, const int32_t* block_table, int64_t bt_stride,
-                                int32_t bt_cols, const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h,
-                                int32_t n_sel, const int32_t* done, const float* sinks, void* out, int64_t so_b,
-                                int64_t so_q, int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads,
-                                int32_t kv_heads, int32_t head_dim, int32_t page_size, int32_t max_seq_len,
-                                float scale, float softcap, void* workspace, size_t workspace_bytes, void* stream) {
-    return run_paged_decode(false, q, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
+    return run_paged_decode(q, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
                             block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel, done, sinks, out, so_b,
                             so_q, so_h, batch, queries, q_heads, kv_heads, head_dim, page_size, max_seq_len, scale,
                             softcap, workspace, workspace_bytes, stream);

@@ -1,8 +1,9 @@
-// Split-K decode attention over a paged fp8 / bf16 KV cache on CDNA4 matrix cores (gfx950).
+// Decode attention over a paged fp8 / bf16 KV cache on CDNA4 matrix cores (gfx950), one launch per call.
 //
 // What it computes is the reference's decode attention (attention/decode.py:66-103 as the definition,
-// attention/_decode_kernels.py:110-226 for the split-K structure, log2-unit online softmax and the split merge):
-// for every batch row b, KV head kvh and query row r = g * Q + qi of its group (query head h = kvh * G + g),
+// attention/_decode_kernels.py:110-226 for the log2-unit online softmax and the log-sum-exp merge of partial
+// results): for every batch row b, KV head kvh and query row r = g * Q + qi of its group (query head
+// h = kvh * G + g),
 //   out[b, qi, h] = sum_t softmax_t(q . k_t * scale) v_t   over the row's visible tokens,
 // with K/V decoded exactly from fp8 and multiplied by per-head scales. A page list turns it into Quest's gathered
 // attention (attention/_quest_kernels.py:13-97): the virtual key axis is the selected pages, then the dense tail.
@@ -11,7 +12,15 @@
 //   keys   [pages, Hkv, D / X, 16, X]  (X = 16 bytes of channels: 16 fp8 or 8 bf16)
 //   values [pages, Hkv, D, 16]         (a channel's 16 tokens contiguous)
 //
-// Work decomposition. A workgroup handles one (split, kvh, b); its waves take tiles of 4 pages (64 tokens) in turn.
+// Work decomposition (stream-K over waves). The work is the sequence of tiles (4 virtual pages = 64 tokens) of
+// every (b, kvh) row, rows in (b, kvh) order. Each single-wave workgroup w of the G launched takes the contiguous
+// range [W w / G, W (w + 1) / G) of the W tiles, so every wave streams the same number of bytes whatever the row
+// lengths are. A row that lies inside one wave's range is finished by that wave and written directly; a row cut by
+// range boundaries is left as partial (max, sum, acc) results in the workspace (at most two per wave: its first and
+// its last row) and the last of its waves to finish (a per-row counter) merges them. Tile loads are double-buffered
+// where the registers allow: the next tile's K/V (and at a row change its query) are in flight while the current
+// tile is computed.
+//
 // Per tile a wave computes S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (M = 16 tokens, N = 16 query rows, K = 32
 // channels) and O^T += V^T P^T (M = 16 channels, N = 16 query rows, K = 32 tokens):
 //   * lane (n = l % 16, g = l / 16) holds A-row n and B-column n; the C/D fragment gives lane (n, g) rows 4g..4g+3.
@@ -23,13 +32,11 @@
 //     MFMA's K dimension is mirrored in the query operand (a dot product does not depend on the order).
 // fp8 bytes are converted exactly (v_cvt_scalef32_pk_{bf16,f16}_{fp8,bf8}, scale 1): keys to bf16 for S (the
 // query is bf16, so every product is exact in the fp32 accumulator, as in the reference's tl.dot), values to fp16 for
-// O with the softmax weights P in fp16 (11 significant bits against the reference's bf16 rounding of P, which alone
-// moves short rows by ~2^-9 of |v|). A bf16 cache multiplies its bf16 values by P split into two bf16 terms
-// (P = P_hi + P_lo, 16 significant bits), two MFMAs per block.
-//
-// The waves of a workgroup merge their (max, sum, acc) in LDS. A row with one split writes its bf16 output directly;
-// otherwise each split writes a partial and the last split of the row to finish (a per-(b, kvh) counter in the
-// workspace) merges them by log-sum-exp (attention/_decode_kernels.py:183-226), so one launch does the whole call.
+// O with the softmax weights P in fp16 (11 significant bits against the reference's bf16 rounding of P). A bf16
+// cache multiplies its bf16 values by P split into two bf16 terms (P = P_hi + P_lo), two MFMAs per block.
+
+#include <cstdlib>
+#include <type_traits>
 
 #include "common.hpp"
 #include "paged_attention.hpp"
@@ -39,6 +46,7 @@ namespace eco {
 namespace {
 
 constexpr int PAGE = 16;
+constexpr int TILE = 4;  // pages per tile
 
 template <int FMT, bool HIGH>
 __device__ inline uint32_t fp8x2_to_bf16x2(uint32_t word) {
@@ -100,32 +108,152 @@ __device__ constexpr int k_channel(int j, int g) {
     return E * (4 * (j / per_run) + g) + 8 * (j % per_run);
 }
 
-// Logical page of virtual page v of row b (see paged_attention.hpp), -1 when it holds nothing.
-__device__ inline int logical_page(const PagedParams& p, int b, int kvh, int v, int v_end, int done) {
-    if (v >= v_end) return -1;
-    int page = v;
-    if (p.page_list != nullptr) page = v < p.n_sel ? p.page_list[b * p.pl_b + kvh * p.pl_h + v] : done + (v - p.n_sel);
-    return page >= 0 && page < p.bt_cols ? page : -1;
+// Device-coherent (agent-scope) store and load of partials: they bypass the caches that are not coherent across the
+// chip's XCDs (gfx950 lowers them to global_store / global_load with sc1), so no L2 writeback or invalidation is
+// needed to hand a partial from one workgroup to another.
+__device__ inline void coherent_store(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-}  // namespace
+__device__ inline float coherent_load(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-__device__ inline int virtual_pages(const PagedParams& p, int b, int* done_out) {
-    const int len = p.seq_lens[b];
-    const int pages = (len + PAGE - 1) / PAGE;
-    if (p.page_list == nullptr) {
-        *done_out = 0;
-        return pages;
+__device__ inline int64_t wave_sum(int64_t x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+    return x;
+}
+
+__device__ inline float wave_sum_f(float x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+    return x;
+}
+
+__device__ inline float wave_max(float x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+    return x;
+}
+
+__device__ inline int64_t wave_inclusive_sum(int64_t x, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int64_t y = __shfl_up(x, off);
+        if (lane >= off) x += y;
     }
-    const int done = p.done[b];
-    *done_out = done;
-    return p.n_sel + max(0, pages - done);
+    return x;
 }
 
-// Splits that hold pages of a row with n_virt virtual pages (rows longer than the launch's max_seq_len are cut at
-// the planned splits: their later pages are not read).
-__device__ inline int row_splits(const PagedParams& p, int n_virt) {
-    return n_virt <= 0 ? 0 : min((n_virt + p.split_pages - 1) / p.split_pages, p.max_splits);
+__device__ inline int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ inline int64_t uniform64(int64_t x) {
+    const uint64_t u = static_cast<uint64_t>(x);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Geometry of batch row b: tokens (cut at the block table's reach), where a page list's dense tail starts, and
+// its virtual pages and tiles (the same for every KV head).
+struct Row {
+    int len, done, n_virt, tiles;
+};
+
+__device__ inline Row row_of(const PagedParams& p, int b) {
+    Row r;
+    r.len = min(max(p.seq_lens[b], 0), p.bt_cols * PAGE);  // the same in every lane when b is
+    const int pages = (r.len + PAGE - 1) / PAGE;
+    if (p.page_list != nullptr) {
+        r.done = min(max(p.done[b], 0), pages);
+        r.n_virt = p.n_sel + pages - r.done;
+    } else {
+        r.done = 0;
+        r.n_virt = pages;
+    }
+    r.tiles = (r.n_virt + TILE - 1) / TILE;
+    return r;
+}
+
+// Logical page of virtual page v of a row, -1 when it holds nothing (past the row, an unselected list entry, or a
+// listed page that is not committed).
+__device__ inline int logical_page(const PagedParams& p, const Row& row, int b, int kvh, int v) {
+    if (v >= row.n_virt) return -1;
+    if (p.page_list == nullptr) return v;
+    if (v < p.n_sel) {
+        const int page = p.page_list[b * p.pl_b + kvh * p.pl_h + v];
+        return page >= 0 && page < row.done ? page : -1;
+    }
+    return row.done + (v - p.n_sel);
+}
+
+// Position in the tile sequence: row (b, kvh), its tile t, and the sequence offset of the row's first tile.
+struct Cursor {
+    int b, kvh, t;
+    Row row;
+    int64_t row_start;
+};
+
+__device__ inline int64_t total_tiles(const PagedParams& p, int lane) {
+    int64_t total = 0;
+    for (int b0 = 0; b0 < p.batch; b0 += 64) {
+        const int b = b0 + lane;
+        total += wave_sum(b < p.batch ? row_of(p, b).tiles : 0);
+    }
+    return total * p.kv_heads;
+}
+
+// The cursor of sequence offset x < total_tiles.
+__device__ inline Cursor locate(const PagedParams& p, int64_t x, int lane) {
+    Cursor c{};
+    int64_t base = 0;
+    for (int b0 = 0; b0 < p.batch; b0 += 64) {
+        const int b = b0 + lane;
+        const int tiles = b < p.batch ? row_of(p, b).tiles : 0;
+        const int64_t incl = wave_inclusive_sum(static_cast<int64_t>(tiles) * p.kv_heads, lane);
+        const int64_t chunk = __shfl(incl, 63);
+        if (x < base + chunk) {
+            const int src = __builtin_ctzll(__ballot(base + incl > x));
+            c.b = uniform(b0 + src);
+            c.row = row_of(p, c.b);
+            c.row.len = uniform(c.row.len);
+            c.row.done = uniform(c.row.done);
+            c.row.n_virt = uniform(c.row.n_virt);
+            c.row.tiles = uniform(c.row.tiles);
+            const int64_t start_b =
+                uniform64(base + __shfl(incl, src) - static_cast<int64_t>(c.row.tiles) * p.kv_heads);
+            const int64_t off = x - start_b;
+            c.kvh = uniform(static_cast<int>(off / c.row.tiles));
+            c.t = uniform(static_cast<int>(off % c.row.tiles));
+            c.row_start = uniform64(start_b + static_cast<int64_t>(c.kvh) * c.row.tiles);
+            return c;
+        }
+        base += chunk;
+    }
+    return c;
+}
+
+// The next tile (called only when one exists).
+__device__ inline void advance(const PagedParams& p, Cursor& c) {
+    if (++c.t < c.row.tiles) return;
+    c.row_start += c.row.tiles;
+    c.t = 0;
+    if (++c.kvh < p.kv_heads) return;
+    c.kvh = 0;
+    do {
+        ++c.b;
+        c.row = row_of(p, c.b);
+        c.row.len = uniform(c.row.len);
+        c.row.done = uniform(c.row.done);
+        c.row.n_virt = uniform(c.row.n_virt);
+        c.row.tiles = uniform(c.row.tiles);
+    } while (c.row.tiles == 0 && c.b + 1 < p.batch);
+}
+
+// The wave whose range holds sequence offset x.
+__device__ inline int wave_of(int64_t x, int64_t total, int grid) {
+    return static_cast<int>(((x + 1) * grid - 1) / total);
 }
 
 // out[b, qi, h, d] of query row r from its merged (acc, max, sum) in log2 units, with the sink logit of head h in
@@ -145,142 +273,190 @@ __device__ inline void store_output(const PagedParams& p, int b, int kvh, int r,
     p.out[b * p.so_b + qi * p.so_q + h * p.so_h + d] = f32_to_bf16(out);
 }
 
-// Device-coherent (agent-scope) store and load of partials: they bypass the caches that are not coherent across the
-// chip's XCDs (gfx950 lowers them to global_store / global_load with sc1), so no L2 writeback or invalidation is
-// needed to hand a partial from one workgroup to another.
-__device__ inline void coherent_store(float* p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+template <int D, int FMT>
+struct Tile {
+    static constexpr int ES = FMT == BF16 ? 2 : 1;  // bytes per element
+    static constexpr int NU = D * ES / 64;          // 16-byte K loads per lane per S MFMA block
+    static constexpr int ND = D / 16;               // value blocks of 16 channels
+    static constexpr int NV = ES;                   // 16-byte V loads per lane per value block
+    uint4 k[4][NU];
+    uint4 v[ND][NV];
+    int lv;  // logical page of the lane group's tile page (-1: none)
+};
 
-__device__ inline float coherent_load(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Log-sum-exp merge of a row's split partials, in split order (attention/_decode_kernels.py:183-215).
-template <int D>
-__device__ inline void merge_splits(const PagedParams& p, int b, int kvh, int n_splits, int tid, int threads) {
-    const int64_t part = (static_cast<int64_t>(b) * p.kv_heads + kvh) * p.max_splits * p.rows;
-    for (int idx = tid; idx < p.rows * D; idx += threads) {
-        const int r = idx / D;
-        const int d = idx % D;
-        float m = -INFINITY;
-        for (int s = 0; s < n_splits; ++s) m = fmaxf(m, coherent_load(p.part_m + part + s * p.rows + r));
-        float o = 0.0f, l = 0.0f;
-        if (m != -INFINITY) {
-            for (int s = 0; s < n_splits; ++s) {
-                const float ms = coherent_load(p.part_m + part + s * p.rows + r);
-                if (ms == -INFINITY) continue;
-                const float c = __builtin_amdgcn_exp2f(ms - m);
-                o += coherent_load(p.part_o + (part + s * p.rows + r) * D + d) * c;
-                l += coherent_load(p.part_l + part + s * p.rows + r) * c;
-            }
-        }
-        store_output(p, b, kvh, r, d, o, m, l);
+// Issues the loads of the tile under cursor c (lane (n, g): K rows of tile page n / 4, V channel n of page g).
+template <int D, int FMT>
+__device__ inline void issue_tile(const PagedParams& p, const Cursor& c, int n, int g, Tile<D, FMT>& tile) {
+    using T = Tile<D, FMT>;
+    const int32_t* table = p.block_table + c.b * p.bt_stride;
+    const int lk = logical_page(p, c.row, c.b, c.kvh, TILE * c.t + (n >> 2));
+    const int lv = logical_page(p, c.row, c.b, c.kvh, TILE * c.t + g);
+    int pk = lk >= 0 ? table[lk] : -1;
+    int pv = lv >= 0 ? table[lv] : -1;
+    pk = pk < p.num_pages ? pk : -1;  // a table entry outside the cache reads nothing
+    pv = pv < p.num_pages ? pv : -1;
+    tile.lv = pv >= 0 ? lv : -1;
+    if (pk >= 0) {
+        const uint8_t* kp = p.k_cache + c.kvh * p.kc_head + static_cast<int64_t>(pk) * p.kc_page;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int u = 0; u < T::NU; ++u) tile.k[v][u] = load16(kp + ((4 * u + g) * PAGE + 4 * v + (n & 3)) * 16);
+    } else {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+#pragma unroll
+            for (int u = 0; u < T::NU; ++u) tile.k[v][u] = make_uint4(0, 0, 0, 0);
+    }
+    if (pv >= 0) {
+        const uint8_t* vp = p.v_cache + c.kvh * p.vc_head + static_cast<int64_t>(pv) * p.vc_page;
+#pragma unroll
+        for (int nd = 0; nd < T::ND; ++nd)
+#pragma unroll
+            for (int w = 0; w < T::NV; ++w) tile.v[nd][w] = load16(vp + (16 * nd + n) * PAGE * T::ES + 16 * w);
+    } else {
+#pragma unroll
+        for (int nd = 0; nd < T::ND; ++nd)
+#pragma unroll
+            for (int w = 0; w < T::NV; ++w) tile.v[nd][w] = make_uint4(0, 0, 0, 0);
     }
 }
 
-template <int D, int FMT, int NB, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void paged_split_kernel(PagedParams p) {
-    constexpr int ES = FMT == BF16 ? 2 : 1;  // bytes per element
-    constexpr int E = 16 / ES;               // channels per 16-byte run
-    constexpr int NU = D * ES / 64;          // 16-byte K loads per lane per S MFMA block
-    constexpr int KS = D / 32;               // k-steps of an S MFMA block
-    constexpr int ND = D / 16;               // value blocks of 16 channels
-    constexpr int NV = ES;                   // 16-byte V loads per lane per value block
-    constexpr int KPR = E / 8;               // k-steps per run
+// The merge of a row's partials by the last of its waves to finish: per query row, the maximum and the weighted sum
+// over the partials (lanes over partials), then the weighted accumulators (lanes over channels). Returns without
+// merging when other partials of the row are still outstanding.
+template <int D>
+__device__ inline void merge_row(const PagedParams& p, const Cursor& c, int prev, int64_t total, int grid,
+                                       int lane) {
+    const int64_t row_end = c.row_start + c.row.tiles;
+    const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
+    int32_t* counter = p.counters + c.b * p.kv_heads + c.kvh;
+        // the waves holding part of the row (a wave's range is empty only when there are fewer tiles than waves)
+        const int w_first = wave_of(c.row_start, total, grid);
+        const int w_last = wave_of(row_end - 1, total, grid);
+        auto holds = [&](int k) { return total * k / grid < total * (k + 1) / grid; };
+        auto slot_of = [&](int k) {
+            return p.part + (2 * static_cast<int64_t>(k) + (total * k / grid < c.row_start ? 1 : 0)) * stride;
+        };
+        int parts = 0;
+        for (int k = w_first + lane; k <= w_last; k += 64) parts += holds(k) ? 1 : 0;
+        parts = static_cast<int>(wave_sum(parts));
+        if (prev != parts - 1) return;
+        // lane-owned runs of 8 channels of one query row; the partials are folded in batches of 4 with an online
+        // log-sum-exp, the batch's loads all in flight together
+        for (int base = 0; base < p.rows * D; base += 64 * 8) {
+            const int e = base + lane * 8;
+            const bool active = e < p.rows * D;
+            const int r = active ? e / D : 0;
+            const int d = active ? e % D : 0;
+            float m_run = -INFINITY, l_run = 0.0f, o_run[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o_run[i] = 0.0f;
+            for (int k0 = w_first; k0 <= w_last; k0 += 4) {
+                float mk[4], lk[4], ok[4][8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int k = k0 + j;
+                    const bool use = active && k <= w_last && holds(k);
+                    const float* sk = slot_of(use ? k : w_first);
+                    mk[j] = use ? coherent_load(sk + r) : -INFINITY;
+                    lk[j] = use ? coherent_load(sk + p.rows + r) : 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) ok[j][i] = use ? coherent_load(sk + 2 * p.rows + r * D + d + i) : 0.0f;
+                }
+                float m_new = m_run;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) m_new = fmaxf(m_new, mk[j]);
+                if (m_new == -INFINITY) continue;
+                const float a = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+                l_run *= a;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o_run[i] *= a;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (mk[j] == -INFINITY) continue;
+                    const float cw = __builtin_amdgcn_exp2f(mk[j] - m_new);
+                    l_run += lk[j] * cw;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o_run[i] += ok[j][i] * cw;
+                }
+                m_run = m_new;
+            }
+            if (active)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) store_output(p, c.b, c.kvh, r, d + i, o_run[i], m_run, l_run);
+        }
+        if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+}  // namespace
+
+template <int D, int FMT, int NB, bool PREFETCH>
+__global__ __launch_bounds__(64) void paged_attention_kernel(PagedParams p) {
+    using T = Tile<D, FMT>;
+    constexpr int ES = T::ES;
+    constexpr int E = 16 / ES;  // channels per 16-byte run
+    constexpr int KS = D / 32;  // k-steps of an S MFMA block
+    constexpr int ND = T::ND;
+    constexpr int KPR = E / 8;  // k-steps per run
+
+    const int lane = threadIdx.x;
     const int n = lane & 15;
     const int g = lane >> 4;
-    const int split = blockIdx.x;
-    const int kvh = blockIdx.y;
-    const int b = blockIdx.z;
+    const int w = blockIdx.x;
+    const int grid = gridDim.x;
 
-    int done = 0;
-    const int n_virt = virtual_pages(p, b, &done);
-    const int v_begin = split * p.split_pages;
-    if (v_begin >= n_virt) {  // uniform over the workgroup: this split of the row is empty
-        if (p.fused && split == 0) {  // a row with no key: zeros (sinks included, decode.py:17)
-            for (int idx = threadIdx.x; idx < p.rows * D; idx += 64 * WAVES)
-                store_output(p, b, kvh, idx / D, idx % D, 0.0f, -INFINITY, 0.0f);
-        }
-        return;
+    const int64_t total = uniform64(total_tiles(p, lane));
+    // rows of batch entries without a key: zeros (sinks included, decode.py:17)
+    for (int b = w; b < p.batch; b += grid) {
+        if (row_of(p, b).tiles == 0)
+            for (int idx = lane; idx < p.kv_heads * p.rows * D; idx += 64)
+                store_output(p, b, idx / (p.rows * D), (idx / D) % p.rows, idx % D, 0.0f, -INFINITY, 0.0f);
     }
-    const int v_end = min(v_begin + p.split_pages, n_virt);
-    const int len = p.seq_lens[b];
+    const int64_t lo = total * w / grid;
+    const int64_t hi = total * (w + 1) / grid;
+    if (lo >= hi) return;
 
-    // ---- query operand (B of the S MFMAs): column n = query row nb * 16 + n ----
+    // ---- row state: query operand, visibility limits, scales, online-softmax accumulators ----
     bf16x8 qop[NB][KS];
-    float limit[NB];  // tokens at positions < limit are visible to the column
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-        const int r = nb * 16 + n;
-        const bool valid = r < p.rows;
-        const int gq = valid ? r / p.queries : 0;
-        const int qi = valid ? r % p.queries : 0;
-        const int h = kvh * p.groups + gq;
-        const uint16_t* base = p.q + b * p.sq_b + qi * p.sq_q + h * p.sq_h;
-        limit[nb] = valid ? static_cast<float>(len - p.queries + qi + 1) : 0.0f;
-#pragma unroll
-        for (int j = 0; j < KS; ++j) {
-            uint4 raw = valid ? *reinterpret_cast<const uint4*>(base + k_channel<E>(j, g)) : make_uint4(0, 0, 0, 0);
-            qop[nb][j] = __builtin_bit_cast(bf16x8, raw);
-        }
-    }
-    const float ks = p.k_scale ? p.k_scale[kvh] : 1.0f;
-    const float vs = p.v_scale ? p.v_scale[kvh] : 1.0f;
-    const float score_scale = p.softcap > 0.0f ? p.scale * ks : p.scale * ks * kLog2e;
-
-    const uint8_t* kbase = p.k_cache + kvh * p.kc_head;
-    const uint8_t* vbase = p.v_cache + kvh * p.vc_head;
-    const int32_t* table = p.block_table + b * p.bt_stride;
-
+    float limit[NB];
+    float score_scale = 0.0f, vs = 1.0f;
     float m_i[NB], l_i[NB];
     f32x4 acc[ND][NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-        m_i[nb] = -INFINITY;
-        l_i[nb] = 0.0f;
-#pragma unroll
-        for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    }
 
-    for (int t0 = v_begin + 4 * wave; t0 < v_end; t0 += 4 * WAVES) {
-        // pages: the K rows of lane (n, g) come from tile page n / 4, its V channel from tile page g
-        const int lk = logical_page(p, b, kvh, t0 + (n >> 2), v_end, done);
-        const int lv = logical_page(p, b, kvh, t0 + g, v_end, done);
-        int pk = lk >= 0 ? table[lk] : -1;
-        int pv = lv >= 0 ? table[lv] : -1;
-        pk = pk < p.num_pages ? pk : -1;  // a table entry outside the cache reads nothing
-        pv = pv < p.num_pages ? pv : -1;
-
-        uint4 kraw[4][NU];
-        uint4 vraw[ND][NV];
-        if (pk >= 0) {
-            const uint8_t* kp = kbase + static_cast<int64_t>(pk) * p.kc_page;
+    auto load_q = [&](const Cursor& c, bf16x8 (&q)[NB][KS]) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v)
+        for (int nb = 0; nb < NB; ++nb) {
+            const int r = nb * 16 + n;
+            const bool valid = r < p.rows;
+            const int gq = valid ? r / p.queries : 0;
+            const int qi = valid ? r % p.queries : 0;
+            const uint16_t* base = p.q + c.b * p.sq_b + qi * p.sq_q + (c.kvh * p.groups + gq) * p.sq_h;
 #pragma unroll
-                for (int u = 0; u < NU; ++u) kraw[v][u] = load16(kp + ((4 * u + g) * PAGE + 4 * v + (n & 3)) * 16);
-        } else {
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-#pragma unroll
-                for (int u = 0; u < NU; ++u) kraw[v][u] = make_uint4(0, 0, 0, 0);
+            for (int j = 0; j < KS; ++j) {
+                const uint4 raw =
+                    valid ? *reinterpret_cast<const uint4*>(base + k_channel<E>(j, g)) : make_uint4(0, 0, 0, 0);
+                q[nb][j] = __builtin_bit_cast(bf16x8, raw);
+            }
         }
-        if (pv >= 0) {
-            const uint8_t* vp = vbase + static_cast<int64_t>(pv) * p.vc_page;
+    };
+    auto begin_row = [&](const Cursor& c) {
 #pragma unroll
-            for (int nd = 0; nd < ND; ++nd)
+        for (int nb = 0; nb < NB; ++nb) {
+            const int r = nb * 16 + n;
+            limit[nb] = r < p.rows ? static_cast<float>(c.row.len - p.queries + r % p.queries + 1) : 0.0f;
+            m_i[nb] = -INFINITY;
+            l_i[nb] = 0.0f;
 #pragma unroll
-                for (int w = 0; w < NV; ++w) vraw[nd][w] = load16(vp + (16 * nd + n) * PAGE * ES + 16 * w);
-        } else {
-#pragma unroll
-            for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-                for (int w = 0; w < NV; ++w) vraw[nd][w] = make_uint4(0, 0, 0, 0);
+            for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
+        const float ks = p.k_scale ? p.k_scale[c.kvh] : 1.0f;
+        vs = p.v_scale ? p.v_scale[c.kvh] : 1.0f;
+        score_scale = p.softcap > 0.0f ? p.scale * ks : p.scale * ks * kLog2e;
+    };
 
-        // ---- S^T = K Q^T: s[v][nb][i] = score of column n against token 4v + i of tile page g ----
+    // ---- one tile of the online softmax ----
+    auto compute = [&](const T& tile) {
         f32x4 s[4][NB];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -288,7 +464,7 @@ __global__ __launch_bounds__(64 * WAVES) void paged_split_kernel(PagedParams p) 
             for (int nb = 0; nb < NB; ++nb) s[v][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < KS; ++j) {
-                const uint4 run = kraw[v][j / KPR];
+                const uint4 run = tile.k[v][j / KPR];
                 bf16x8 a;
                 if constexpr (FMT == BF16) {
                     a = __builtin_bit_cast(bf16x8, run);
@@ -301,12 +477,10 @@ __global__ __launch_bounds__(64 * WAVES) void paged_split_kernel(PagedParams p) 
                     s[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qop[nb][j], s[v][nb], 0, 0, 0);
             }
         }
-
-        // ---- online softmax per column, P^T operands ----
         // P operands: fp16 for fp8 caches, bf16 hi + lo for bf16 caches
         f16x8 pop_h[NB][2];
         bf16x8 pop_hi[NB][2], pop_lo[NB][2];
-        const int first = lv * PAGE;  // position of token 0 of tile page g (lv < 0: nothing)
+        const int first = tile.lv * PAGE;  // position of token 0 of tile page g
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             float tile_max = -INFINITY;
@@ -314,8 +488,7 @@ __global__ __launch_bounds__(64 * WAVES) void paged_split_kernel(PagedParams p) 
             for (int v = 0; v < 4; ++v)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const int pos = first + 4 * v + i;
-                    const bool ok = lv >= 0 && static_cast<float>(pos) < limit[nb];
+                    const bool ok = tile.lv >= 0 && static_cast<float>(first + 4 * v + i) < limit[nb];
                     float x = s[v][nb][i] * score_scale;
                     if (p.softcap > 0.0f) {
                         const float t = x / p.softcap;
@@ -332,13 +505,13 @@ __global__ __launch_bounds__(64 * WAVES) void paged_split_kernel(PagedParams p) 
             const float m_safe = m_new == -INFINITY ? 0.0f : m_new;
             const float alpha = __builtin_amdgcn_exp2f(m_i[nb] - m_safe);
             float sum = 0.0f;
-            float pv_[4][4];
+            float pw[4][4];
 #pragma unroll
             for (int v = 0; v < 4; ++v)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    pv_[v][i] = __builtin_amdgcn_exp2f(s[v][nb][i] - m_safe);
-                    sum += pv_[v][i];
+                    pw[v][i] = __builtin_amdgcn_exp2f(s[v][nb][i] - m_safe);
+                    sum += pw[v][i];
                 }
             sum = group_sum(sum);
             l_i[nb] = l_i[nb] * alpha + sum;
@@ -347,52 +520,51 @@ __global__ __launch_bounds__(64 * WAVES) void paged_split_kernel(PagedParams p) 
             for (int nd = 0; nd < ND; ++nd) acc[nd][nb] *= alpha;
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const float* a = pv_[2 * u];
-                const float* c = pv_[2 * u + 1];
+                const float* a = pw[2 * u];
+                const float* c = pw[2 * u + 1];
                 if constexpr (FMT == BF16) {
-                    float lo[8];
-                    uint4 w;
-                    w.x = pack_bf16x2(a[0], a[1]);
-                    w.y = pack_bf16x2(a[2], a[3]);
-                    w.z = pack_bf16x2(c[0], c[1]);
-                    w.w = pack_bf16x2(c[2], c[3]);
-                    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+                    uint4 hi4;
+                    hi4.x = pack_bf16x2(a[0], a[1]);
+                    hi4.y = pack_bf16x2(a[2], a[3]);
+                    hi4.z = pack_bf16x2(c[0], c[1]);
+                    hi4.w = pack_bf16x2(c[2], c[3]);
+                    const uint32_t words[4] = {hi4.x, hi4.y, hi4.z, hi4.w};
                     const float vals[8] = {a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
+                    float lo8[8];
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
-                        lo[e] = vals[e] - bits_f32((e & 1 ? words[e >> 1] & 0xFFFF0000u : words[e >> 1] << 16));
-                    uint4 z;
-                    z.x = pack_bf16x2(lo[0], lo[1]);
-                    z.y = pack_bf16x2(lo[2], lo[3]);
-                    z.z = pack_bf16x2(lo[4], lo[5]);
-                    z.w = pack_bf16x2(lo[6], lo[7]);
-                    pop_hi[nb][u] = __builtin_bit_cast(bf16x8, w);
-                    pop_lo[nb][u] = __builtin_bit_cast(bf16x8, z);
+                        lo8[e] = vals[e] - bits_f32(e & 1 ? words[e >> 1] & 0xFFFF0000u : words[e >> 1] << 16);
+                    uint4 lo4;
+                    lo4.x = pack_bf16x2(lo8[0], lo8[1]);
+                    lo4.y = pack_bf16x2(lo8[2], lo8[3]);
+                    lo4.z = pack_bf16x2(lo8[4], lo8[5]);
+                    lo4.w = pack_bf16x2(lo8[6], lo8[7]);
+                    pop_hi[nb][u] = __builtin_bit_cast(bf16x8, hi4);
+                    pop_lo[nb][u] = __builtin_bit_cast(bf16x8, lo4);
                 } else {
-                    uint4 w;
-                    w.x = pack_f16x2(a[0], a[1]);
-                    w.y = pack_f16x2(a[2], a[3]);
-                    w.z = pack_f16x2(c[0], c[1]);
-                    w.w = pack_f16x2(c[2], c[3]);
-                    pop_h[nb][u] = __builtin_bit_cast(f16x8, w);
+                    uint4 w4;
+                    w4.x = pack_f16x2(a[0], a[1]);
+                    w4.y = pack_f16x2(a[2], a[3]);
+                    w4.z = pack_f16x2(c[0], c[1]);
+                    w4.w = pack_f16x2(c[2], c[3]);
+                    pop_h[nb][u] = __builtin_bit_cast(f16x8, w4);
                 }
             }
         }
-
-        // ---- O^T += V^T P^T: lane (n, g) supplies channel 16 nd + n of tile page g ----
+        // O^T += V^T P^T: lane (n, g) supplies channel 16 nd + n of tile page g
 #pragma unroll
         for (int nd = 0; nd < ND; ++nd) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 if constexpr (FMT == BF16) {
-                    const bf16x8 a = __builtin_bit_cast(bf16x8, vraw[nd][u]);
+                    const bf16x8 a = __builtin_bit_cast(bf16x8, tile.v[nd][u]);
 #pragma unroll
                     for (int nb = 0; nb < NB; ++nb) {
                         acc[nd][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pop_hi[nb][u], acc[nd][nb], 0, 0, 0);
                         acc[nd][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pop_lo[nb][u], acc[nd][nb], 0, 0, 0);
                     }
                 } else {
-                    const uint4 run = vraw[nd][0];
+                    const uint4 run = tile.v[nd][0];
                     const f16x8 a = fp8x8_to_f16x8<FMT>(u ? run.z : run.x, u ? run.w : run.y);
 #pragma unroll
                     for (int nb = 0; nb < NB; ++nb)
@@ -400,125 +572,203 @@ __global__ __launch_bounds__(64 * WAVES) void paged_split_kernel(PagedParams p) 
                 }
             }
         }
-    }
+    };
 
-    // ---- merge the waves in LDS ----
-    // acc fragment of lane (n, g): channel 16 nd + 4 g + i of column nb * 16 + n.
-    constexpr int SLOTS = ND * NB * 4;
-    __shared__ float lds_acc[WAVES][SLOTS][64];
-    __shared__ float lds_m[WAVES][16 * NB];
-    __shared__ float lds_l[WAVES][16 * NB];
-    __shared__ int lds_last;
+    // ---- end of a row segment: direct output, or a partial and (for the last wave of the row) the merge ----
+    auto finish = [&](const Cursor& c, int64_t seg_begin, int64_t seg_end, bool first_segment) {
+        const int64_t row_end = c.row_start + c.row.tiles;
+        if (seg_begin == c.row_start && seg_end == row_end) {
 #pragma unroll
-    for (int nd = 0; nd < ND; ++nd)
+            for (int nb = 0; nb < NB; ++nb) {
+                const int r = nb * 16 + n;
+                if (r >= p.rows) continue;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
+                for (int nd = 0; nd < ND; ++nd)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) lds_acc[wave][(nd * NB + nb) * 4 + i][lane] = acc[nd][nb][i];
-    if (g == 0) {
+                    for (int i = 0; i < 4; ++i)
+                        store_output(p, c.b, c.kvh, r, 16 * nd + 4 * g + i, acc[nd][nb][i] * vs, m_i[nb], l_i[nb]);
+            }
+            return;
+        }
+        const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
+        float* slot = p.part + (2 * static_cast<int64_t>(w) + (first_segment ? 0 : 1)) * stride;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            lds_m[wave][nb * 16 + n] = m_i[nb];
-            lds_l[wave][nb * 16 + n] = l_i[nb];
+            const int r = nb * 16 + n;
+            if (r >= p.rows) continue;
+            if (g == 0) {
+                coherent_store(slot + r, m_i[nb]);
+                coherent_store(slot + p.rows + r, l_i[nb]);
+            }
+#pragma unroll
+            for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    coherent_store(slot + 2 * p.rows + r * D + 16 * nd + 4 * g + i, acc[nd][nb][i] * vs);
         }
-    }
-    __syncthreads();
+        // the partial's stores complete before the row's counter counts it; the last wave reads them back with
+        // device-coherent loads
+        __builtin_amdgcn_s_waitcnt(0);
+        int prev = 0;
+        if (lane == 0)
+            prev = __hip_atomic_fetch_add(p.counters + c.b * p.kv_heads + c.kvh, 1, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+        merge_row<D>(p, c, __shfl(prev, 0), total, grid, lane);
+    };
 
-    // A row with one split writes its output here; otherwise every split writes a partial (max, sum, acc) and the
-    // last split of the row to finish merges them (a device-scope counter per (b, kvh), reset by that split).
-    const int n_splits = row_splits(p, n_virt);
-    const int64_t bh = static_cast<int64_t>(b) * p.kv_heads + kvh;
-    const int64_t part = (bh * p.max_splits + split) * p.rows;
-    const bool direct = p.fused && n_splits == 1;
-    for (int idx = threadIdx.x; idx < p.rows * D; idx += 64 * WAVES) {
-        const int r = idx / D;
-        const int d = idx % D;
-        const int nb = r >> 4;
-        const int col = r & 15;
-        const int slot = ((d >> 4) * NB + nb) * 4 + (d & 3);
-        const int src_lane = ((d & 15) >> 2) * 16 + col;
-        float m = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < WAVES; ++w) m = fmaxf(m, lds_m[w][r]);
-        float o = 0.0f, l = 0.0f;
-        if (m != -INFINITY) {
-#pragma unroll
-            for (int w = 0; w < WAVES; ++w) {
-                const float mw = lds_m[w][r];
-                if (mw == -INFINITY) continue;
-                const float c = __builtin_amdgcn_exp2f(mw - m);
-                o += lds_acc[w][slot][src_lane] * c;
-                l += lds_l[w][r] * c;
+    Cursor cur = locate(p, lo, lane);
+    int64_t pos = lo;
+    int64_t seg_begin = lo;
+    bool first_segment = true;
+    load_q(cur, qop);
+    begin_row(cur);
+
+    if constexpr (PREFETCH) {
+        T bufs[2];
+        bf16x8 qnext[NB][KS];
+        issue_tile<D, FMT>(p, cur, n, g, bufs[0]);
+        // Each step computes the tile in one buffer while the next tile's loads fill the other; the loop is unrolled
+        // by two so that both buffers stay in registers.
+        auto step = [&](T& now, T& next) -> bool {
+            const bool more = pos + 1 < hi;
+            Cursor ahead = cur;
+            bool new_row = false;
+            if (more) {
+                advance(p, ahead);
+                issue_tile<D, FMT>(p, ahead, n, g, next);
+                new_row = ahead.t == 0;
+                if (new_row) load_q(ahead, qnext);
             }
+            compute(now);
+            if (cur.t + 1 == cur.row.tiles || !more) {
+                finish(cur, seg_begin, pos + 1, first_segment);
+                first_segment = false;
+                seg_begin = pos + 1;
+            }
+            if (new_row) {
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int j = 0; j < KS; ++j) qop[nb][j] = qnext[nb][j];
+                begin_row(ahead);
+            }
+            cur = ahead;
+            ++pos;
+            return more;
+        };
+        while (step(bufs[0], bufs[1]) && step(bufs[1], bufs[0])) {
         }
-        o *= vs;
-        if (direct) {
-            store_output(p, b, kvh, r, d, o, m, l);
-        } else {
-            coherent_store(p.part_o + (part + r) * D + d, o);
-            if (d == 0) {
-                coherent_store(p.part_m + part + r, m);
-                coherent_store(p.part_l + part + r, l);
+    } else {
+        T tile;
+        while (true) {
+            issue_tile<D, FMT>(p, cur, n, g, tile);
+            compute(tile);
+            const bool more = pos + 1 < hi;
+            if (cur.t + 1 == cur.row.tiles || !more) {
+                finish(cur, seg_begin, pos + 1, first_segment);
+                first_segment = false;
+                seg_begin = pos + 1;
             }
+            if (!more) break;
+            Cursor ahead = cur;
+            advance(p, ahead);
+            if (ahead.t == 0) {
+                load_q(ahead, qop);
+                begin_row(ahead);
+            }
+            cur = ahead;
+            ++pos;
         }
     }
-    if (!p.fused || direct) return;
-    // The partial was written with device-coherent stores: every wave waits until its stores completed (vmcnt 0),
-    // the barrier joins the waves, then one thread counts the split. The last split reads the partials back with
-    // device-coherent loads.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0)
-        lds_last = __hip_atomic_fetch_add(p.counters + bh, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                   n_splits - 1;
-    __syncthreads();
-    if (!lds_last) return;
-    merge_splits<D>(p, b, kvh, n_splits, threadIdx.x, 64 * WAVES);
-    if (threadIdx.x == 0) __hip_atomic_store(p.counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- host side ----------------------------------------------------------------------------------------------
 
 namespace {
 
+// Register-double-buffered tiles where two of them fit beside the accumulators.
 template <int D, int FMT, int NB>
-int launch_split(const PagedParams& p, hipStream_t stream) {
-    // the wave merge keeps WAVES * D * NB * 64 bytes in LDS: at most 64 KiB
-    constexpr int FIT = 1024 / (D * NB);
-    constexpr int WAVES = FIT >= 4 ? 4 : (FIT >= 1 ? FIT : 1);
-    dim3 grid(p.max_splits, p.kv_heads, p.batch);
-    hipLaunchKernelGGL((paged_split_kernel<D, FMT, NB, WAVES>), grid, dim3(64 * WAVES), 0, stream, p);
-    return check_launch("paged_split_kernel");
+constexpr bool prefetch_fits() {
+    return FMT != BF16 && D <= 128 && NB <= 2;
 }
 
-template <int D, int FMT>
-int dispatch_nb(const PagedParams& p, hipStream_t stream) {
-    const int nb = (p.rows + 15) / 16;
-    if (nb == 1) return launch_split<D, FMT, 1>(p, stream);
-    if (nb == 2) return launch_split<D, FMT, 2>(p, stream);
-    if (nb <= 4) return launch_split<D, FMT, 4>(p, stream);
-    return fail("paged decode attention takes at most 64 query rows per KV head (query heads per KV head x queries)");
+bool prefetch_enabled() {
+    static const bool on = [] {
+        const char* env = std::getenv("ECO_PAGED_PREFETCH");
+        return env == nullptr || env[0] != '0';
+    }();
+    return on;
 }
 
-template <int D>
-int dispatch_fmt(const PagedParams& p, hipStream_t stream) {
-    switch (p.kv_format) {
-        case BF16: return dispatch_nb<D, BF16>(p, stream);
-        case FP8_E4M3: return dispatch_nb<D, FP8_E4M3>(p, stream);
-        case FP8_E5M2: return dispatch_nb<D, FP8_E5M2>(p, stream);
-        default: return fail("paged decode attention: KV format must be bf16, fp8 e4m3 or fp8 e5m2");
+template <int D, int FMT, int NB>
+auto kernel_of() {
+    if constexpr (prefetch_fits<D, FMT, NB>())
+        if (prefetch_enabled()) return paged_attention_kernel<D, FMT, NB, true>;
+    return paged_attention_kernel<D, FMT, NB, false>;
+}
+
+// Calls f.template run<D, FMT, NB>() for the instance of (head dim, format, 16-row column blocks).
+template <typename F>
+int dispatch(int head_dim, int format, int rows, const F& f) {
+    const int nb = (rows + 15) / 16;
+    auto by_nb = [&](auto d_tag, auto fmt_tag) -> int {
+        constexpr int D = decltype(d_tag)::value;
+        constexpr int FMT = decltype(fmt_tag)::value;
+        if (nb == 1) return f.template run<D, FMT, 1>();
+        if (nb == 2) return f.template run<D, FMT, 2>();
+        if (nb <= 4) return f.template run<D, FMT, 4>();
+        return fail("paged decode attention takes at most 64 query rows per KV head (query heads per KV head x "
+                    "queries)");
+    };
+    auto by_fmt = [&](auto d_tag) -> int {
+        switch (format) {
+            case BF16: return by_nb(d_tag, std::integral_constant<int, BF16>{});
+            case FP8_E4M3: return by_nb(d_tag, std::integral_constant<int, FP8_E4M3>{});
+            case FP8_E5M2: return by_nb(d_tag, std::integral_constant<int, FP8_E5M2>{});
+            default: return fail("paged decode attention: KV format must be bf16, fp8 e4m3 or fp8 e5m2");
+        }
+    };
+    switch (head_dim) {
+        case 64: return by_fmt(std::integral_constant<int, 64>{});
+        case 128: return by_fmt(std::integral_constant<int, 128>{});
+        case 256: return by_fmt(std::integral_constant<int, 256>{});
+        default: return fail("paged decode attention supports head dims 64, 128 and 256");
     }
 }
+
+struct Launch {
+    hipStream_t stream;
+    const PagedParams* p;
+    template <int D, int FMT, int NB>
+    int run() const {
+        const auto kernel = kernel_of<D, FMT, NB>();
+        hipLaunchKernelGGL(kernel, dim3(p->grid), dim3(64), 0, stream, *p);
+        return check_launch("paged_attention_kernel");
+    }
+};
+
+struct Occupancy {
+    int* per_cu;
+    template <int D, int FMT, int NB>
+    int run() const {
+        int blocks = 0;
+        const auto kernel = kernel_of<D, FMT, NB>();
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, 64, 0) != hipSuccess ||
+            blocks <= 0)
+            blocks = 1;
+        *per_cu = blocks;
+        return 0;
+    }
+};
 
 }  // namespace
 
-int paged_split(const PagedParams& p, hipStream_t stream) {
-    switch (p.head_dim) {
-        case 64: return dispatch_fmt<64>(p, stream);
-        case 128: return dispatch_fmt<128>(p, stream);
-        case 256: return dispatch_fmt<256>(p, stream);
-        default: return fail("paged decode attention supports head dims 64, 128 and 256");
-    }
+int paged_resident_waves(int head_dim, int format, int rows, int* per_cu) {
+    return dispatch(head_dim, format, rows, Occupancy{per_cu});
+}
+
+int paged_attention(const PagedParams& p, hipStream_t stream) {
+    return dispatch(p.head_dim, p.kv_format, p.rows, Launch{stream, &p});
 }
 
 }  // namespace eco

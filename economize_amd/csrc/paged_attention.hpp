@@ -1,4 +1,4 @@
-// Parameters of the paged decode-attention kernels (paged_attention.hip).
+// Parameters of the paged decode-attention kernel (paged_attention.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -8,7 +8,6 @@ namespace eco {
 
 // Virtual pages of row b: without a page list, its ceil(len / 16) pages; with one (Quest), the n_sel listed pages
 // (logical page indices, -1 for none) followed by the dense tail, logical pages done[b] .. ceil(len / 16) - 1.
-// Split s of a row covers virtual pages [s * split_pages, (s + 1) * split_pages).
 struct PagedParams {
     const uint16_t* q;  // bf16 [B, Q, Hq, D], channel stride 1
     int64_t sq_b, sq_q, sq_h;
@@ -26,18 +25,17 @@ struct PagedParams {
     const float* k_scale;  // optional [Hkv]
     const float* v_scale;
     const float* sinks;  // optional [Hq] logits
-    int32_t* counters;  // [B * Hkv], zero between calls (the merging split resets its counter)
-    float* part_o;
-    float* part_m;
-    float* part_l;
+    int32_t* counters;  // [B * Hkv], zero between calls (the merging wave resets its row's counter)
+    float* part;        // [2 * grid, rows, D + 2]: per slot the maxima, sums and accumulators of a row segment
     uint16_t* out;  // bf16 [B, Q, Hq, D], channel stride 1
     int64_t so_b, so_q, so_h;
     int batch, queries, q_heads, kv_heads, groups, rows, head_dim, kv_format;
-    int split_pages, max_splits;
-    int fused;  // 1: merge in the last split of each row; 0: write partials only (profiling)
+    int grid;  // single-wave workgroups launched
     float scale, softcap;
 };
 
-int paged_split(const PagedParams& p, hipStream_t stream);
+// Resident single-wave workgroups per CU of the kernel instance for this shape.
+int paged_resident_waves(int head_dim, int format, int rows, int* per_cu);
+int paged_attention(const PagedParams& p, hipStream_t stream);
 
 }  // namespace eco

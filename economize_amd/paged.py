@@ -131,10 +131,10 @@ def head_scales(x: torch.Tensor, dtype: torch.dtype = torch.float8_e4m3fn) -> to
 
 
 def workspace_size(batch: int, queries: int, q_heads: int, kv_heads: int, head_dim: int, max_seq_len: int,
-                   n_sel: int = 0) -> int:
-    """Bytes of scratch :func:`paged_decode_attention` needs for this shape."""
+                   n_sel: int = 0, dtype: torch.dtype = torch.float8_e4m3fn) -> int:
+    """Bytes of scratch :func:`paged_decode_attention` needs for this shape and cache dtype."""
     return int(_lib.lib().eco_paged_decode_workspace_size(batch, queries, q_heads, kv_heads, head_dim, max_seq_len,
-                                                          n_sel))
+                                                          n_sel, _lib.fmt(dtype)))
 
 
 def new_workspace(nbytes: int, device: torch.device | str) -> torch.Tensor:
@@ -169,7 +169,6 @@ def paged_decode_attention(
     page_list: torch.Tensor | None = None,
     done: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
-    split_only: bool = False,
 ) -> torch.Tensor:
     """Attention of ``query`` ``[B, Q, Hq, D]`` (bf16, channel-contiguous) over the paged cache, ``[B, Q, Hq, D]``
     bf16 out.
@@ -181,7 +180,7 @@ def paged_decode_attention(
     With ``page_list`` (int32 ``[B, Hkv, n_sel]``, logical pages, ``-1`` = none) and ``done`` (int32 ``[B]``) the
     keys read are the listed pages and every token from page ``done[b]`` on (Quest's gathered attention).
     ``workspace`` (from :func:`new_workspace`, at least :func:`workspace_size` bytes) defaults to a cached one per
-    device and stream. ``split_only`` launches only the KV-streaming phase (profiling; ``out`` is not written).
+    device and stream.
     """
     cache.check()
     device = _lib.require_gpu(query, cache.keys, block_table, seq_lens)
@@ -213,12 +212,14 @@ def paged_decode_attention(
         out = torch.empty(batch, queries, q_heads, head_dim, dtype=torch.bfloat16, device=device)
     elif out.shape != query.shape or out.dtype != torch.bfloat16 or out.stride(-1) != 1:
         raise ConfigError("out must be bf16 like the query, with a contiguous channel axis")
-    need = workspace_size(batch, queries, q_heads, cache.kv_heads, head_dim, max_seq_len, n_sel)
+    if max_seq_len <= 0:
+        raise ConfigError("max_seq_len must be positive")
+    need = workspace_size(batch, queries, q_heads, cache.kv_heads, head_dim, max_seq_len, n_sel, cache.dtype)
     if workspace is None:
         workspace = _workspace(need, device)
     scale = 1.0 / math.sqrt(head_dim) if scale is None else float(scale)
     _lib.call(
-        "eco_paged_decode_split_only" if split_only else "eco_paged_decode",
+        "eco_paged_decode",
         query.data_ptr(), query.stride(0), query.stride(1), query.stride(2),
         cache.keys.data_ptr(), cache.values.data_ptr(), _lib.fmt(cache.dtype), cache.num_pages,
         _lib.ptr(cache.k_scale), _lib.ptr(cache.v_scale),

@@ -56,9 +56,11 @@ int eco_kv_head_absmax(const void* x, int32_t in_format, int32_t a, int32_t h, i
 int eco_fp8_scales_from_absmax(const uint32_t* absmax_bits, int32_t heads, int32_t format, float* scales,
                                void* stream);
 
-/* Workspace bytes eco_paged_decode needs for this shape (n_sel = Quest's selected pages, 0 without). */
+/* Workspace bytes eco_paged_decode needs for this shape (n_sel = Quest's selected pages, 0 without). The workspace
+ * starts with per-row counters that must be zero before its first use; every call leaves them zero. One workspace
+ * serves one stream at a time. */
 size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
-                                       int32_t head_dim, int32_t max_seq_len, int32_t n_sel);
+                                       int32_t head_dim, int32_t max_seq_len, int32_t n_sel, int32_t kv_format);
 
 /* Split-K decode attention over the paged cache: out[b, qi, h, :] (bf16, element strides so_*) for query q[b, qi,
  * h, :] (bf16, element strides sq_*, channel stride 1), query head h reading KV head h / (q_heads / kv_heads).
@@ -68,7 +70,9 @@ size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q
  * denominator. A row that sees no key gives 0.
  * Replaces decode_attention (attention/decode.py:252-324) for a paged cache, and with page_list != NULL
  * quest_decode_attention (attention/quest.py:239-344): the keys read are the pages page_list[b, kvh, 0..n_sel)
- * (strides pl_b, pl_h; logical page indices, -1 = none) and then every token from page done[b] on. */
+ * (strides pl_b, pl_h; logical page indices below done[b], others read nothing) and then every token from page
+ * done[b] on. One launch: the work is cut into equal contiguous ranges of 64-token tiles, one per wave, so ragged
+ * rows need no host-side plan; max_seq_len (>= every seq_lens[b]) only bounds the launch. */
 int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
                      const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
                      const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
@@ -77,17 +81,6 @@ int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
                      int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
                      int32_t max_seq_len, float scale, float softcap, void* workspace, size_t workspace_bytes,
                      void* stream);
-
-/* The split phase of eco_paged_decode alone (same arguments; writes only the workspace): a profiling entry that
- * times the KV-streaming kernel without the merge. */
-int eco_paged_decode_split_only(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
-                                const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
-                                const float* v_scale, const int32_t* block_table, int64_t bt_stride,
-                                int32_t bt_cols, const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h,
-                                int32_t n_sel, const int32_t* done, const float* sinks, void* out, int64_t so_b,
-                                int64_t so_q, int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads,
-                                int32_t kv_heads, int32_t head_dim, int32_t page_size, int32_t max_seq_len,
-                                float scale, float softcap, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

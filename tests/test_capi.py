@@ -51,7 +51,7 @@ def test_validation_errors_are_reported_without_a_device() -> None:
     lib = _lib.lib()
     rc = lib.eco_paged_append(None, None, 0, 0, 0, 0, 0, None, 3, None, None, 1, 1, 64, 16, 1, None, None, None)
     assert rc == 1 and b"null" in lib.eco_last_error()
-    assert lib.eco_paged_decode_workspace_size(32, 1, 32, 8, 128, 4096, 0) > 0
+    assert lib.eco_paged_decode_workspace_size(32, 1, 32, 8, 128, 4096, 0, 1) > 0
 
 
 @pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")

@@ -45,6 +45,9 @@ CASES = [
     (2, 8, 64, 8, 128, [200, 129], torch.float8_e4m3fn),  # 64 rows per KV head
     (2, 2, 8, 8, 256, [90, 300], torch.bfloat16),
     (3, 1, 4, 4, 64, [0, 5, 40], torch.float8_e4m3fn),  # an empty row gives zeros
+    (1, 1, 32, 8, 128, [32768], torch.float8_e4m3fn),  # rows cut into many waves' ranges
+    (40, 1, 8, 1, 128, [3 + 97 * i for i in range(40)], torch.float8_e4m3fn),  # many short rows per wave
+    (5, 2, 8, 2, 64, [300, 0, 0, 17, 1], torch.bfloat16),  # empty rows between others
 ]
 
 
@@ -76,6 +79,28 @@ def test_repeated_calls_reset_the_split_counters() -> None:
         np.testing.assert_allclose(out.float().cpu().numpy(), want, atol=ATOL, rtol=RTOL)
     counters = ws[: 4 * 8 * 4].view(torch.int32)
     assert int(counters.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
+def test_page_list_attends_the_selected_pages_and_the_tail(dtype) -> None:
+    """Quest's gathered attention (attention/quest.py:239-344) through the page list: the oracle's selection
+    (quest.py:73-108) over the decoded keys, then attention over the selected pages and the dense tail
+    (quest.py:207-219)."""
+    from oracle import quest as oquest
+
+    lens = [2000, 700, 64, 1100]
+    c = make_case(4, 1, 16, 4, 128, lens, dtype, seed=21)
+    kd, vd = c.decoded()
+    done = np.array([(n - 1) // 16 for n in lens])
+    max_done = int(done.max())
+    pages = 9
+    kmin, kmax = oquest.page_bounds(kd, 0, max_done, 16)
+    q = to_numpy_f32(c.q).transpose(0, 2, 1, 3)
+    index = oquest.select_pages(q, kmin, kmax, done, max_done, pages)
+    got = _decode(c, page_list=torch.from_numpy(index).cuda(), done=torch.from_numpy(done.astype(np.int32)).cuda())
+    visible = (np.arange(kd.shape[2])[None, :] < np.array(lens)[:, None])[:, None, None, :]  # each row's tokens
+    want = oquest.quest_reference(q, kd, vd, visible, 1 / np.sqrt(128), index, done, 16)
+    np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
 
 
 def test_softcap_and_sinks() -> None:
