@@ -183,6 +183,7 @@ def main() -> None:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--fixed-only", action="store_true", help="skip the ragged-length run (for profiling)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the decode-attention path shards by (batch row, KV head) with no "
@@ -195,7 +196,7 @@ def main() -> None:
     fixed = [4096] * BATCH
     head = measure(fixed, args.steps, args.warmup, args.seed)
     ragged_lens = np.random.default_rng(args.seed + 100).integers(1024, 8193, BATCH).tolist()
-    ragged = measure(ragged_lens, args.steps, args.warmup, args.seed + 1)
+    ragged = None if args.fixed_only else measure(ragged_lens, args.steps, args.warmup, args.seed + 1)
     cpu = None if args.no_cpu else cpu_baseline(head["workload"], fixed)
 
     value = head["kv_bytes"] / head["seconds"] / 1e9
@@ -233,7 +234,7 @@ def main() -> None:
             "algorithmic_bytes_per_launch": head["call_bytes"],
             "us_per_launch": round(head["seconds"] * 1e6, 2),
         },
-        "ragged": {
+        "ragged": None if ragged is None else {
             "lens": "uniform [1024, 8192], seed 100",
             "sum_len": int(sum(ragged_lens)),
             "us_per_call": round(ragged["seconds"] * 1e6, 2),

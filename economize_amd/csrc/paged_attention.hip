@@ -148,6 +148,13 @@ __device__ inline int64_t wave_inclusive_sum(int64_t x, int lane) {
 
 __device__ inline int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// ptr[index] for a wave-uniform index through the scalar cache (a scalar load waits on its own counter, not on the
+// vector loads in flight). Only for data no kernel of the call writes.
+template <typename T>
+__device__ inline T scalar_load(const T* ptr, int index) {
+    return ((const __attribute__((address_space(4))) T*)ptr)[uniform(index)];
+}
+
 __device__ inline int64_t uniform64(int64_t x) {
     const uint64_t u = static_cast<uint64_t>(x);
     const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
@@ -156,17 +163,20 @@ __device__ inline int64_t uniform64(int64_t x) {
 }
 
 // Geometry of batch row b: tokens (cut at the block table's reach), where a page list's dense tail starts, and
-// its virtual pages and tiles (the same for every KV head).
+// its virtual pages and tiles (the same for every KV head). UNIFORM: b is the same in every lane (scalar loads).
 struct Row {
     int len, done, n_virt, tiles;
 };
 
+template <bool UNIFORM = false>
 __device__ inline Row row_of(const PagedParams& p, int b) {
     Row r;
-    r.len = min(max(p.seq_lens[b], 0), p.bt_cols * PAGE);  // the same in every lane when b is
+    const int len = UNIFORM ? scalar_load(p.seq_lens, b) : p.seq_lens[b];
+    r.len = min(max(len, 0), p.bt_cols * PAGE);
     const int pages = (r.len + PAGE - 1) / PAGE;
     if (p.page_list != nullptr) {
-        r.done = min(max(p.done[b], 0), pages);
+        const int done = UNIFORM ? scalar_load(p.done, b) : p.done[b];
+        r.done = min(max(done, 0), pages);
         r.n_virt = p.n_sel + pages - r.done;
     } else {
         r.done = 0;
@@ -242,8 +252,8 @@ __device__ inline void advance(const PagedParams& p, Cursor& c) {
     if (++c.kvh < p.kv_heads) return;
     c.kvh = 0;
     do {
-        ++c.b;
-        c.row = row_of(p, c.b);
+        c.b = uniform(c.b + 1);
+        c.row = row_of<true>(p, c.b);
         c.row.len = uniform(c.row.len);
         c.row.done = uniform(c.row.done);
         c.row.n_virt = uniform(c.row.n_virt);
@@ -273,53 +283,110 @@ __device__ inline void store_output(const PagedParams& p, int b, int kvh, int r,
     p.out[b * p.so_b + qi * p.so_q + h * p.so_h + d] = f32_to_bf16(out);
 }
 
-template <int D, int FMT>
+template <int D, int FMT, int NB>
 struct Tile {
     static constexpr int ES = FMT == BF16 ? 2 : 1;  // bytes per element
     static constexpr int NU = D * ES / 64;          // 16-byte K loads per lane per S MFMA block
     static constexpr int ND = D / 16;               // value blocks of 16 channels
     static constexpr int NV = ES;                   // 16-byte V loads per lane per value block
+    static constexpr int KS = D / 32;               // k-steps of an S MFMA block
     uint4 k[4][NU];
     uint4 v[ND][NV];
-    int lv;  // logical page of the lane group's tile page (-1: none)
+    bf16x8 q[NB][KS];  // the query operand of the tile's row (an L2 hit after the row's first tile)
+    int lv;    // logical page of the lane group's tile page (-1: none)
+    int vcnt;  // tokens of that page inside the row (0 to 16); the V bytes of the others are cleared before use
 };
 
+// Page ids of 64 consecutive virtual pages of one (b, kvh) row, one per lane: lane i holds the logical page and the
+// cache page of virtual page base + i (-1 when it holds nothing). A tile's K/V addresses then come from a lane
+// shuffle instead of a block-table load issued right before the K/V loads (whose latency the loads would wait out,
+// and, since loads retire in order, with them every load in flight). The window is reloaded once per 16 tiles.
+struct PageWindow {
+    int b = -1, kvh = -1, base = 0;
+    int logical = -1, physical = -1;
+};
+
+__device__ __forceinline__ void ensure_window(const PagedParams& p, const Cursor& c, int lane, PageWindow& win) {
+    const int first = TILE * c.t;
+    if (c.b == win.b && c.kvh == win.kvh && first >= win.base && first + TILE <= win.base + 64) return;
+    win.b = c.b;
+    win.kvh = c.kvh;
+    win.base = first;
+    const int lp = logical_page(p, c.row, c.b, c.kvh, first + lane);
+    int pp = lp >= 0 ? p.block_table[c.b * p.bt_stride + lp] : -1;
+    pp = pp < p.num_pages ? pp : -1;  // a table entry outside the cache reads nothing
+    win.logical = pp >= 0 ? lp : -1;
+    win.physical = pp;
+    // wait here for the table load (vmcnt(0)), so that the common path, which reloads nothing, does not wait at
+    // the branch's join for every load in flight
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
 // Issues the loads of the tile under cursor c (lane (n, g): K rows of tile page n / 4, V channel n of page g).
-template <int D, int FMT>
-__device__ inline void issue_tile(const PagedParams& p, const Cursor& c, int n, int g, Tile<D, FMT>& tile) {
-    using T = Tile<D, FMT>;
-    const int32_t* table = p.block_table + c.b * p.bt_stride;
-    const int lk = logical_page(p, c.row, c.b, c.kvh, TILE * c.t + (n >> 2));
-    const int lv = logical_page(p, c.row, c.b, c.kvh, TILE * c.t + g);
-    int pk = lk >= 0 ? table[lk] : -1;
-    int pv = lv >= 0 ? table[lv] : -1;
-    pk = pk < p.num_pages ? pk : -1;  // a table entry outside the cache reads nothing
-    pv = pv < p.num_pages ? pv : -1;
-    tile.lv = pv >= 0 ? lv : -1;
-    if (pk >= 0) {
-        const uint8_t* kp = p.k_cache + c.kvh * p.kc_head + static_cast<int64_t>(pk) * p.kc_page;
+template <int D, int FMT, int NB>
+__device__ __forceinline__ void issue_tile(const PagedParams& p, const Cursor& c, int n, int g, int lane, PageWindow& win,
+                                  Tile<D, FMT, NB>& tile) {
+    using T = Tile<D, FMT, NB>;
+    ensure_window(p, c, lane, win);
+    const int at = TILE * c.t - win.base;
+    const int pk = __shfl(win.physical, at + (n >> 2));
+    const int pv = __shfl(win.physical, at + g);
+    tile.lv = __shfl(win.logical, at + g);
+    tile.vcnt = tile.lv >= 0 ? min(max(c.row.len - tile.lv * PAGE, 0), PAGE) : 0;
+    // Every lane issues the same loads whatever its pages are (a page that holds nothing reads page 0, and its
+    // scores and values are masked when the tile is computed): with the same number of loads on every path, the
+    // wait before a tile's use leaves the younger tiles' loads in flight.
+    const uint8_t* kp = p.k_cache + c.kvh * p.kc_head + static_cast<int64_t>(pk >= 0 ? pk : 0) * p.kc_page;
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
+    for (int v = 0; v < 4; ++v)
 #pragma unroll
-            for (int u = 0; u < T::NU; ++u) tile.k[v][u] = load16(kp + ((4 * u + g) * PAGE + 4 * v + (n & 3)) * 16);
-    } else {
+        for (int u = 0; u < T::NU; ++u) tile.k[v][u] = load16(kp + ((4 * u + g) * PAGE + 4 * v + (n & 3)) * 16);
+    const uint8_t* vp = p.v_cache + c.kvh * p.vc_head + static_cast<int64_t>(pv >= 0 ? pv : 0) * p.vc_page;
 #pragma unroll
-        for (int v = 0; v < 4; ++v)
+    for (int nd = 0; nd < T::ND; ++nd)
 #pragma unroll
-            for (int u = 0; u < T::NU; ++u) tile.k[v][u] = make_uint4(0, 0, 0, 0);
+        for (int w = 0; w < T::NV; ++w) tile.v[nd][w] = load16(vp + (16 * nd + n) * PAGE * T::ES + 16 * w);
+    // the query operand: lane (n, g) holds query row nb * 16 + n, channels of k-step j as the K runs order them (a lane
+    // of a row past the group reads row 0: its MFMA column is computed and never stored)
+    constexpr int E = 16 / T::ES;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int r = nb * 16 + n;
+        const bool valid = r < p.rows;
+        const int gq = valid ? r / p.queries : 0;
+        const int qi = valid ? r % p.queries : 0;
+        const uint16_t* base = p.q + c.b * p.sq_b + qi * p.sq_q + (c.kvh * p.groups + gq) * p.sq_h;
+#pragma unroll
+        for (int j = 0; j < T::KS; ++j)
+            tile.q[nb][j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base + k_channel<E>(j, g)));
     }
-    if (pv >= 0) {
-        const uint8_t* vp = p.v_cache + c.kvh * p.vc_head + static_cast<int64_t>(pv) * p.vc_page;
+}
+
+// Clears the V bytes of the tokens a tile page does not hold (past the row's end, or the whole page when it holds
+// nothing): cache slots that were never written may hold NaN codes, and a zero softmax weight times NaN is NaN.
+// V run w of a lane holds 16 bytes of channel data for tokens 16 w / ES .. of its page (ES bytes per token).
+template <int D, int FMT, int NB>
+__device__ inline void clear_unheld_values(Tile<D, FMT, NB>& tile) {
+    using T = Tile<D, FMT, NB>;
+    constexpr int TPD = 4 / T::ES;  // tokens per dword
+    uint32_t mask[T::NV][4];
 #pragma unroll
-        for (int nd = 0; nd < T::ND; ++nd)
+    for (int w = 0; w < T::NV; ++w)
 #pragma unroll
-            for (int w = 0; w < T::NV; ++w) tile.v[nd][w] = load16(vp + (16 * nd + n) * PAGE * T::ES + 16 * w);
-    } else {
+        for (int i = 0; i < 4; ++i) {
+            const int first = (4 * w + i) * TPD;  // first token of this dword
+            const int held = min(max(tile.vcnt - first, 0), TPD);
+            mask[w][i] = held == TPD ? 0xFFFFFFFFu : (1u << (8 * T::ES * held)) - 1u;
+        }
 #pragma unroll
-        for (int nd = 0; nd < T::ND; ++nd)
+    for (int nd = 0; nd < T::ND; ++nd)
 #pragma unroll
-            for (int w = 0; w < T::NV; ++w) tile.v[nd][w] = make_uint4(0, 0, 0, 0);
-    }
+        for (int w = 0; w < T::NV; ++w) {
+            tile.v[nd][w].x &= mask[w][0];
+            tile.v[nd][w].y &= mask[w][1];
+            tile.v[nd][w].z &= mask[w][2];
+            tile.v[nd][w].w &= mask[w][3];
+        }
 }
 
 // The merge of a row's partials by the last of its waves to finish: per query row, the maximum and the weighted sum
@@ -334,8 +401,8 @@ __device__ inline void merge_row(const PagedParams& p, const Cursor& c, int prev
         // the waves holding part of the row (a wave's range is empty only when there are fewer tiles than waves)
         const int w_first = wave_of(c.row_start, total, grid);
         const int w_last = wave_of(row_end - 1, total, grid);
-        auto holds = [&](int k) { return total * k / grid < total * (k + 1) / grid; };
-        auto slot_of = [&](int k) {
+        auto holds = [&](int k) __attribute__((always_inline)) { return total * k / grid < total * (k + 1) / grid; };
+        auto slot_of = [&](int k) __attribute__((always_inline)) {
             return p.part + (2 * static_cast<int64_t>(k) + (total * k / grid < c.row_start ? 1 : 0)) * stride;
         };
         int parts = 0;
@@ -391,9 +458,9 @@ __device__ inline void merge_row(const PagedParams& p, const Cursor& c, int prev
 
 }  // namespace
 
-template <int D, int FMT, int NB, bool PREFETCH>
+template <int D, int FMT, int NB, int NBUF>
 __global__ __launch_bounds__(64) void paged_attention_kernel(PagedParams p) {
-    using T = Tile<D, FMT>;
+    using T = Tile<D, FMT, NB>;
     constexpr int ES = T::ES;
     constexpr int E = 16 / ES;  // channels per 16-byte run
     constexpr int KS = D / 32;  // k-steps of an S MFMA block
@@ -418,29 +485,13 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(PagedParams p) {
     if (lo >= hi) return;
 
     // ---- row state: query operand, visibility limits, scales, online-softmax accumulators ----
-    bf16x8 qop[NB][KS];
     float limit[NB];
+    int all_see = 0;  // tokens below this are visible to every query row of the row
     float score_scale = 0.0f, vs = 1.0f;
     float m_i[NB], l_i[NB];
     f32x4 acc[ND][NB];
 
-    auto load_q = [&](const Cursor& c, bf16x8 (&q)[NB][KS]) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const int r = nb * 16 + n;
-            const bool valid = r < p.rows;
-            const int gq = valid ? r / p.queries : 0;
-            const int qi = valid ? r % p.queries : 0;
-            const uint16_t* base = p.q + c.b * p.sq_b + qi * p.sq_q + (c.kvh * p.groups + gq) * p.sq_h;
-#pragma unroll
-            for (int j = 0; j < KS; ++j) {
-                const uint4 raw =
-                    valid ? *reinterpret_cast<const uint4*>(base + k_channel<E>(j, g)) : make_uint4(0, 0, 0, 0);
-                q[nb][j] = __builtin_bit_cast(bf16x8, raw);
-            }
-        }
-    };
-    auto begin_row = [&](const Cursor& c) {
+    auto begin_row = [&](const Cursor& c) __attribute__((always_inline)) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             const int r = nb * 16 + n;
@@ -450,13 +501,15 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(PagedParams p) {
 #pragma unroll
             for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
-        const float ks = p.k_scale ? p.k_scale[c.kvh] : 1.0f;
-        vs = p.v_scale ? p.v_scale[c.kvh] : 1.0f;
+        all_see = c.row.len - p.queries + 1;
+        const float ks = p.k_scale ? scalar_load(p.k_scale, c.kvh) : 1.0f;
+        vs = p.v_scale ? scalar_load(p.v_scale, c.kvh) : 1.0f;
         score_scale = p.softcap > 0.0f ? p.scale * ks : p.scale * ks * kLog2e;
     };
 
     // ---- one tile of the online softmax ----
-    auto compute = [&](const T& tile) {
+    auto compute = [&](T& tile) __attribute__((always_inline)) {
+        if (__ballot(tile.vcnt < PAGE) != 0) clear_unheld_values<D, FMT, NB>(tile);
         f32x4 s[4][NB];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -474,50 +527,77 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(PagedParams p) {
                 }
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
-                    s[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qop[nb][j], s[v][nb], 0, 0, 0);
+                    s[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, tile.q[nb][j], s[v][nb], 0, 0, 0);
             }
         }
         // P operands: fp16 for fp8 caches, bf16 hi + lo for bf16 caches
         f16x8 pop_h[NB][2];
         bf16x8 pop_hi[NB][2], pop_lo[NB][2];
         const int first = tile.lv * PAGE;  // position of token 0 of tile page g
+        // Scores in log2 units (times the scale, through the soft cap if one is set). Only a tile that holds a
+        // row's end, an empty page or a token some causal query row must not see is masked.
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s[v][nb][i] *= score_scale;
+        if (p.softcap > 0.0f) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float t = s[v][nb][i] / p.softcap;
+                        const float e = __expf(-2.0f * fabsf(t));
+                        const float th = (1.0f - e) / (1.0f + e);
+                        s[v][nb][i] = p.softcap * (t < 0.0f ? -th : th) * kLog2e;
+                    }
+        }
+        if (__ballot(tile.lv < 0 || first + PAGE > all_see) != 0) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const bool ok = tile.lv >= 0 && static_cast<float>(first + 4 * v + i) < limit[nb];
+                        s[v][nb][i] = ok ? s[v][nb][i] : -INFINITY;
+                    }
+        }
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             float tile_max = -INFINITY;
 #pragma unroll
             for (int v = 0; v < 4; ++v)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const bool ok = tile.lv >= 0 && static_cast<float>(first + 4 * v + i) < limit[nb];
-                    float x = s[v][nb][i] * score_scale;
-                    if (p.softcap > 0.0f) {
-                        const float t = x / p.softcap;
-                        const float e = __expf(-2.0f * fabsf(t));
-                        const float th = (1.0f - e) / (1.0f + e);
-                        x = p.softcap * (t < 0.0f ? -th : th) * kLog2e;
-                    }
-                    x = ok ? x : -INFINITY;
-                    s[v][nb][i] = x;
-                    tile_max = fmaxf(tile_max, x);
-                }
+                tile_max = fmaxf(fmaxf(tile_max, fmaxf(s[v][nb][0], s[v][nb][1])), fmaxf(s[v][nb][2], s[v][nb][3]));
             tile_max = group_max(tile_max);
-            const float m_new = fmaxf(m_i[nb], tile_max);
-            const float m_safe = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m_i[nb] - m_safe);
+            // Lazy rescaling: the reference maximum m_i moves only when a score exceeds it by more than 2^8, so that
+            // the accumulators are rescaled a few times per row instead of at every tile (the weights stay below
+            // 2^8, far inside fp16's range; the quotient acc / l does not depend on the reference). The bf16 instance
+            // at D = 256 rescales at every tile: on gfx950 its lazy form (and a form with the scale folded into the
+            // exponent) gave wrong results although the same source is correct in every other instance.
+            constexpr float lazy = FMT == BF16 && D > 128 ? 0.0f : 8.0f;
+            if (lazy == 0.0f || __ballot(tile_max > m_i[nb] + lazy) != 0) {
+                const float m_new = fmaxf(m_i[nb], tile_max);
+                const float alpha = m_i[nb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_i[nb] - m_new);
+                l_i[nb] *= alpha;
+#pragma unroll
+                for (int nd = 0; nd < ND; ++nd) acc[nd][nb] *= alpha;
+                m_i[nb] = m_new;
+            }
+            const float neg_m = m_i[nb] == -INFINITY ? 0.0f : -m_i[nb];
             float sum = 0.0f;
             float pw[4][4];
 #pragma unroll
             for (int v = 0; v < 4; ++v)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    pw[v][i] = __builtin_amdgcn_exp2f(s[v][nb][i] - m_safe);
+                    pw[v][i] = __builtin_amdgcn_exp2f(s[v][nb][i] + neg_m);
                     sum += pw[v][i];
                 }
-            sum = group_sum(sum);
-            l_i[nb] = l_i[nb] * alpha + sum;
-            m_i[nb] = m_new;
-#pragma unroll
-            for (int nd = 0; nd < ND; ++nd) acc[nd][nb] *= alpha;
+            l_i[nb] += group_sum(sum);
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const float* a = pw[2 * u];
@@ -575,7 +655,7 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(PagedParams p) {
     };
 
     // ---- end of a row segment: direct output, or a partial and (for the last wave of the row) the merge ----
-    auto finish = [&](const Cursor& c, int64_t seg_begin, int64_t seg_end, bool first_segment) {
+    auto finish = [&](const Cursor& c, int64_t seg_begin, int64_t seg_end, bool first_segment) __attribute__((always_inline)) {
         const int64_t row_end = c.row_start + c.row.tiles;
         if (seg_begin == c.row_start && seg_end == row_end) {
 #pragma unroll
@@ -616,68 +696,60 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(PagedParams p) {
         merge_row<D>(p, c, __shfl(prev, 0), total, grid, lane);
     };
 
+    // ---- the tile pipeline: NBUF register buffers, tile pos + NBUF - 1 issued while tile pos is computed ----
     Cursor cur = locate(p, lo, lane);
-    int64_t pos = lo;
+    PageWindow win;
     int64_t seg_begin = lo;
     bool first_segment = true;
-    load_q(cur, qop);
     begin_row(cur);
 
-    if constexpr (PREFETCH) {
-        T bufs[2];
-        bf16x8 qnext[NB][KS];
-        issue_tile<D, FMT>(p, cur, n, g, bufs[0]);
-        // Each step computes the tile in one buffer while the next tile's loads fill the other; the loop is unrolled
-        // by two so that both buffers stay in registers.
-        auto step = [&](T& now, T& next) -> bool {
-            const bool more = pos + 1 < hi;
-            Cursor ahead = cur;
-            bool new_row = false;
-            if (more) {
-                advance(p, ahead);
-                issue_tile<D, FMT>(p, ahead, n, g, next);
-                new_row = ahead.t == 0;
-                if (new_row) load_q(ahead, qnext);
-            }
-            compute(now);
-            if (cur.t + 1 == cur.row.tiles || !more) {
-                finish(cur, seg_begin, pos + 1, first_segment);
-                first_segment = false;
-                seg_begin = pos + 1;
-            }
-            if (new_row) {
+    T bufs[NBUF];
+    Cursor cs[NBUF];  // the cursor of the tile each buffer holds
+    Cursor icur = cur;  // the next tile to issue, at sequence offset ipos
+    int64_t ipos = lo;
+
+    // Every step issues one tile, past the end of the range a repeat of the range's last tile (read from L2 and never
+    // computed): with the same number of loads issued on every path through the loop, the wait before a tile's use
+    // counts the younger tiles' loads and leaves them in flight.
+    auto issue_next = [&](T& buf, Cursor& slot) __attribute__((always_inline)) {
+        issue_tile<D, FMT, NB>(p, icur, n, g, lane, win, buf);
+        slot = icur;
+        if (ipos < hi) {
+            if (ipos + 1 < hi) advance(p, icur);
+            ++ipos;
+        }
+    };
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-                    for (int j = 0; j < KS; ++j) qop[nb][j] = qnext[nb][j];
-                begin_row(ahead);
-            }
-            cur = ahead;
-            ++pos;
-            return more;
-        };
-        while (step(bufs[0], bufs[1]) && step(bufs[1], bufs[0])) {
+    for (int s = 0; s + 1 < NBUF; ++s) issue_next(bufs[s], cs[s]);
+
+    int64_t pos = lo;
+    // computes the tile held in buffer I (the loop is unrolled by NBUF so that every buffer index is a constant)
+    auto step = [&](auto tag) __attribute__((always_inline)) -> bool {
+        constexpr int I = decltype(tag)::value;
+        constexpr int J = (I + NBUF - 1) % NBUF;
+        issue_next(bufs[J], cs[J]);
+        cur = cs[I];
+        if (cur.t == 0 && pos != lo) begin_row(cur);
+        compute(bufs[I]);
+        const bool more = pos + 1 < hi;
+        if (cur.t + 1 == cur.row.tiles || !more) {
+            finish(cur, seg_begin, pos + 1, first_segment);
+            first_segment = false;
+            seg_begin = pos + 1;
+        }
+        ++pos;
+        return more;
+    };
+    if constexpr (NBUF == 1) {
+        while (step(std::integral_constant<int, 0>{})) {
+        }
+    } else if constexpr (NBUF == 2) {
+        while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{})) {
         }
     } else {
-        T tile;
-        while (true) {
-            issue_tile<D, FMT>(p, cur, n, g, tile);
-            compute(tile);
-            const bool more = pos + 1 < hi;
-            if (cur.t + 1 == cur.row.tiles || !more) {
-                finish(cur, seg_begin, pos + 1, first_segment);
-                first_segment = false;
-                seg_begin = pos + 1;
-            }
-            if (!more) break;
-            Cursor ahead = cur;
-            advance(p, ahead);
-            if (ahead.t == 0) {
-                load_q(ahead, qop);
-                begin_row(ahead);
-            }
-            cur = ahead;
-            ++pos;
+        static_assert(NBUF == 3, "1 to 3 tile buffers");
+        while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{}) &&
+               step(std::integral_constant<int, 2>{})) {
         }
     }
 }
@@ -686,32 +758,40 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(PagedParams p) {
 
 namespace {
 
-// Register-double-buffered tiles where two of them fit beside the accumulators.
+// Tile buffers of an instance: as many as fit in the registers beside the accumulators (a tile of fp8 K/V at
+// D = 128 is 64 VGPRs per lane). ECO_PAGED_STAGES (1 to 3) lowers the count for tuning.
 template <int D, int FMT, int NB>
-constexpr bool prefetch_fits() {
-    return FMT != BF16 && D <= 128 && NB <= 2;
+constexpr int max_stages() {
+    if (FMT != BF16 && D <= 128 && NB == 1) return 3;
+    if (FMT != BF16 && D <= 128 && NB == 2) return 2;
+    return 1;
 }
 
-bool prefetch_enabled() {
-    static const bool on = [] {
-        const char* env = std::getenv("ECO_PAGED_PREFETCH");
-        return env == nullptr || env[0] != '0';
+int stages_cap() {
+    static const int cap = [] {
+        const char* env = std::getenv("ECO_PAGED_STAGES");
+        const int v = env ? std::atoi(env) : 3;
+        return v < 1 ? 1 : (v > 3 ? 3 : v);
     }();
-    return on;
+    return cap;
 }
 
 template <int D, int FMT, int NB>
 auto kernel_of() {
-    if constexpr (prefetch_fits<D, FMT, NB>())
-        if (prefetch_enabled()) return paged_attention_kernel<D, FMT, NB, true>;
-    return paged_attention_kernel<D, FMT, NB, false>;
+    constexpr int M = max_stages<D, FMT, NB>();
+    const int s = stages_cap() < M ? stages_cap() : M;
+    if constexpr (M >= 3)
+        if (s == 3) return paged_attention_kernel<D, FMT, NB, 3>;
+    if constexpr (M >= 2)
+        if (s >= 2) return paged_attention_kernel<D, FMT, NB, 2>;
+    return paged_attention_kernel<D, FMT, NB, 1>;
 }
 
 // Calls f.template run<D, FMT, NB>() for the instance of (head dim, format, 16-row column blocks).
 template <typename F>
 int dispatch(int head_dim, int format, int rows, const F& f) {
     const int nb = (rows + 15) / 16;
-    auto by_nb = [&](auto d_tag, auto fmt_tag) -> int {
+    auto by_nb = [&](auto d_tag, auto fmt_tag) __attribute__((always_inline)) -> int {
         constexpr int D = decltype(d_tag)::value;
         constexpr int FMT = decltype(fmt_tag)::value;
         if (nb == 1) return f.template run<D, FMT, 1>();
@@ -720,7 +800,7 @@ int dispatch(int head_dim, int format, int rows, const F& f) {
         return fail("paged decode attention takes at most 64 query rows per KV head (query heads per KV head x "
                     "queries)");
     };
-    auto by_fmt = [&](auto d_tag) -> int {
+    auto by_fmt = [&](auto d_tag) __attribute__((always_inline)) -> int {
         switch (format) {
             case BF16: return by_nb(d_tag, std::integral_constant<int, BF16>{});
             case FP8_E4M3: return by_nb(d_tag, std::integral_constant<int, FP8_E4M3>{});

@@ -49,11 +49,19 @@ class PagedCase:
         vs = self.v_scale.reshape(1, -1, 1, 1)
         return ofp8.fp8_decode(self.k_codes, fmt, ks, out), ofp8.fp8_decode(self.v_codes, fmt, vs, out)
 
-    def device_cache(self, device: str = "cuda"):
+    def device_cache(self, device: str = "cuda", poison: bool = False):
+        """The paged cache on ``device``. With ``poison`` every slot the rows do not hold (the tail of each row's
+        last page and every unused page) holds NaN codes instead of zeros, as never-written cache memory may."""
         from economize_amd.paged import PagedKVCache
 
         element = 2 if self.dtype == torch.bfloat16 else 1
         kc, vc = opaged.scatter_kv(self.k_codes, self.v_codes, self.lens, self.table, self.pages, 16, element)
+        if poison:
+            held_k, held_v = opaged.scatter_kv(np.ones_like(self.k_codes), np.ones_like(self.v_codes), self.lens,
+                                               self.table, self.pages, 16, element)
+            nan = np.array(0xFFFF if element == 2 else 0xFF, dtype=kc.dtype)
+            kc = np.where(held_k != 0, kc, nan)
+            vc = np.where(held_v != 0, vc, nan)
         raw = torch.int16 if element == 2 else torch.uint8
         keys = torch.from_numpy(kc.view(np.int16) if element == 2 else kc).to(raw).view(self.dtype).to(device)
         values = torch.from_numpy(vc.view(np.int16) if element == 2 else vc).to(raw).view(self.dtype).to(device)

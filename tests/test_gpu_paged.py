@@ -44,6 +44,8 @@ CASES = [
     (2, 4, 16, 2, 128, [260, 71], torch.float8_e4m3fn),  # verification: 32 rows per KV head, causal
     (2, 8, 64, 8, 128, [200, 129], torch.float8_e4m3fn),  # 64 rows per KV head
     (2, 2, 8, 8, 256, [90, 300], torch.bfloat16),
+    (2, 1, 8, 2, 256, [2000, 3333], torch.bfloat16),  # long rows at D = 256
+    (2, 1, 8, 2, 256, [2000, 3333], torch.float8_e4m3fn),
     (3, 1, 4, 4, 64, [0, 5, 40], torch.float8_e4m3fn),  # an empty row gives zeros
     (1, 1, 32, 8, 128, [32768], torch.float8_e4m3fn),  # rows cut into many waves' ranges
     (40, 1, 8, 1, 128, [3 + 97 * i for i in range(40)], torch.float8_e4m3fn),  # many short rows per wave
@@ -61,6 +63,22 @@ def test_decode_matches_the_oracle(case) -> None:
     for b, n in enumerate(lens):
         if n == 0:
             assert (got[b] == 0).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float8_e4m3fn, torch.float8_e5m2, torch.bfloat16])
+def test_slots_past_each_row_may_hold_nan_codes(dtype) -> None:
+    """Cache memory a row does not hold (the rest of its last page, unused pages) is never read into the result,
+    whatever it holds: the reference's kernels load K/V with a mask (attention/_decode_kernels.py:161-171)."""
+    from economize_amd.paged import paged_decode_attention
+
+    lens = [1, 17, 250, 1000, 31]
+    c = make_case(5, 1, 16, 4, 128, lens, dtype, seed=5)
+    cache = c.device_cache(poison=True)
+    table = torch.from_numpy(c.table).cuda()
+    seq = torch.tensor(lens, dtype=torch.int32).cuda()
+    out = paged_decode_attention(c.q.cuda(), cache, table, seq, max(lens)).float().cpu().numpy()
+    assert np.isfinite(out).all()
+    np.testing.assert_allclose(out, oracle_output(c), atol=ATOL, rtol=RTOL)
 
 
 def test_repeated_calls_reset_the_split_counters() -> None:
