@@ -184,6 +184,9 @@ def main() -> None:
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--fixed-only", action="store_true", help="skip the ragged-length run (for profiling)")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="only run a plain device copy of 256 MiB, 20 times (the reference kernel for scaling the "
+                             "FETCH_SIZE / WRITE_SIZE counters of rocprofv3)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the decode-attention path shards by (batch row, KV head) with no "
@@ -192,6 +195,15 @@ def main() -> None:
 
     import numpy as np
     import torch
+
+    if args.copy_calibration:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_per_launch": src.numel(), "launches": 20}), flush=True)
+        return
 
     fixed = [4096] * BATCH
     head = measure(fixed, args.steps, args.warmup, args.seed)

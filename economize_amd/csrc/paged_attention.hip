@@ -758,8 +758,10 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(PagedParams p) {
 
 namespace {
 
-// Tile buffers of an instance: as many as fit in the registers beside the accumulators (a tile of fp8 K/V at
-// D = 128 is 64 VGPRs per lane). ECO_PAGED_STAGES (1 to 3) lowers the count for tuning.
+// Tile buffers of an instance: two where they fit in the registers beside the accumulators (a tile of fp8 K/V at
+// D = 128 is 64 VGPRs per lane, plus 16 of query operand). Three fit for one column block, but measured slower at
+// the Llama-3-8B decode shape (55.0 against 53.6 us; ragged lengths 77.1 against 71.8 us). ECO_PAGED_STAGES (1 to 3)
+// selects the count for tuning.
 template <int D, int FMT, int NB>
 constexpr int max_stages() {
     if (FMT != BF16 && D <= 128 && NB == 1) return 3;
@@ -770,7 +772,7 @@ constexpr int max_stages() {
 int stages_cap() {
     static const int cap = [] {
         const char* env = std::getenv("ECO_PAGED_STAGES");
-        const int v = env ? std::atoi(env) : 3;
+        const int v = env ? std::atoi(env) : 2;
         return v < 1 ? 1 : (v > 3 ? 3 : v);
     }();
     return cap;
