@@ -29,16 +29,20 @@ _FORMATS = {
 
 # argument types of every exported function (kept in the order of include/economize_amd.h)
 _P, _I, _L, _F, _S = c_void_p, c_int32, c_int64, c_float, c_size_t
-_PAGED_DECODE = [_P, _L, _L, _L, _P, _P, _I, _I, _P, _P, _P, _L, _I, _P, _P, _L, _L, _I, _P, _P, _P, _L, _L, _L,
-                 _I, _I, _I, _I, _I, _I, _I, _F, _F, _P, _S, _P]
+_PAGED_DECODE = [_P, _L, _L, _L, _P, _P, _I, _I, _P, _P, _P, _L, _I, _P, _P, _L, _L, _I, _I, _P, _P, _P, _L, _L,
+                 _L, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P, _S, _P]
 SIGNATURES: dict[str, tuple[type | None, list]] = {
     "eco_last_error": (ctypes.c_char_p, []),
     "eco_abi_version": (c_int32, []),
     "eco_paged_append": (c_int32, [_P, _P, _I, _L, _L, _L, _L, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P]),
     "eco_kv_head_absmax": (c_int32, [_P, _I, _I, _I, _I, _I, _L, _L, _L, _L, _P, _P]),
     "eco_fp8_scales_from_absmax": (c_int32, [_P, _I, _I, _P, _P]),
-    "eco_paged_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I, _I]),
+    "eco_paged_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I, _I, _I]),
     "eco_paged_decode": (c_int32, _PAGED_DECODE),
+    "eco_quest_page_bounds": (c_int32, [_P, _I, _I, _P, _L, _I, _I, _I, _I, _P, _P, _L, _L, _L, _I, _I, _I, _I, _P]),
+    "eco_quest_select_workspace_size": (c_size_t, [_I, _I, _I]),
+    "eco_quest_select": (c_int32, [_P, _L, _L, _L, _P, _P, _L, _L, _L, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _S,
+                                   _P]),
 }
 
 _lib: ctypes.CDLL | None = None

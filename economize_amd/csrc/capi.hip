@@ -9,6 +9,7 @@
 #include "common.hpp"
 #include "kv_quant.hpp"
 #include "paged_attention.hpp"
+#include "quest.hpp"
 
 namespace eco {
 
@@ -81,11 +82,11 @@ Workspace paged_workspace(int batch, int kv_heads, int rows, int head_dim, int g
 int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
                      const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
                      const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
-                     const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h, int32_t n_sel, const int32_t* done,
-                     const float* sinks, void* out, int64_t so_b, int64_t so_q, int64_t so_h, int32_t batch,
-                     int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
-                     int32_t max_seq_len, float scale, float softcap, void* workspace, size_t workspace_bytes,
-                     void* stream) {
+                     const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h, int32_t n_sel,
+                     int32_t list_page_size, const int32_t* done, const float* sinks, void* out, int64_t so_b,
+                     int64_t so_q, int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
+                     int32_t head_dim, int32_t page_size, int32_t max_seq_len, float scale, float softcap,
+                     void* workspace, size_t workspace_bytes, void* stream) {
     if (!q || !k_cache || !v_cache || !block_table || !seq_lens || !out)
         return fail("paged decode: null q, cache, block table, seq_lens or out pointer");
     if (batch <= 0 || queries <= 0 || q_heads <= 0 || kv_heads <= 0 || num_pages <= 0 || bt_cols <= 0)
@@ -103,10 +104,15 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
     if ((reinterpret_cast<uintptr_t>(q) & 15) || (sq_b & 7) || (sq_q & 7) || (sq_h & 7))
         return fail("paged decode: the query must be 16-byte aligned with strides that are multiples of 8");
     if (page_list && (!done || n_sel < 0)) return fail("paged decode: a page list needs done[] and n_sel >= 0");
+    if (list_page_size == 0) list_page_size = 16;
+    if (list_page_size < 16 || list_page_size % 16)
+        return fail("paged decode: listed pages must hold a positive multiple of 16 tokens");
+    const int span = list_page_size / 16;
     if (max_seq_len <= 0) return fail("paged decode: max_seq_len must be positive");
     if (!(scale == scale)) return fail("paged decode: scale is NaN");
 
-    const int grid = paged_grid(batch, kv_heads, rows, head_dim, kv_format, max_seq_len, page_list ? n_sel : 0);
+    const int grid =
+        paged_grid(batch, kv_heads, rows, head_dim, kv_format, max_seq_len, page_list ? n_sel * span : 0);
     if (grid <= 0) return 1;
     const Workspace ws = paged_workspace(batch, kv_heads, rows, head_dim, grid);
     if (!workspace || workspace_bytes < ws.total())
@@ -135,6 +141,7 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
     p.pl_b = pl_b;
     p.pl_h = pl_h;
     p.n_sel = page_list ? n_sel : 0;
+    p.span = span;
     p.done = done;
     p.k_scale = k_scale;
     p.v_scale = v_scale;
@@ -170,7 +177,7 @@ extern "C" {
 
 const char* eco_last_error(void) { return g_error.c_str(); }
 
-int eco_abi_version(void) { return 1; }
+int eco_abi_version(void) { return 2; }
 
 int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
                      int64_t sv_t, int64_t sv_h, const int32_t* slot_mapping, int32_t tokens, void* k_cache,
@@ -233,10 +240,13 @@ int eco_fp8_scales_from_absmax(const uint32_t* absmax_bits, int32_t heads, int32
 }
 
 size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
-                                       int32_t head_dim, int32_t max_seq_len, int32_t n_sel, int32_t kv_format) {
+                                       int32_t head_dim, int32_t max_seq_len, int32_t n_sel, int32_t list_page_size,
+                                       int32_t kv_format) {
     if (batch <= 0 || queries <= 0 || kv_heads <= 0 || q_heads <= 0 || head_dim <= 0 || max_seq_len <= 0) return 0;
     const int rows = (q_heads / kv_heads) * queries;
-    const int grid = paged_grid(batch, kv_heads, rows, head_dim, kv_format, max_seq_len, n_sel > 0 ? n_sel : 0);
+    const int span = list_page_size >= 16 ? list_page_size / 16 : 1;
+    const int grid =
+        paged_grid(batch, kv_heads, rows, head_dim, kv_format, max_seq_len, n_sel > 0 ? n_sel * span : 0);
     if (grid <= 0) return 0;
     return paged_workspace(batch, kv_heads, rows, head_dim, grid).total();
 }
@@ -244,15 +254,101 @@ size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q
 int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
                      const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
                      const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
-                     const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h, int32_t n_sel, const int32_t* done,
-                     const float* sinks, void* out, int64_t so_b, int64_t so_q, int64_t so_h, int32_t batch,
-                     int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
-                     int32_t max_seq_len, float scale, float softcap, void* workspace, size_t workspace_bytes,
-                     void* stream) {
+                     const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h, int32_t n_sel,
+                     int32_t list_page_size, const int32_t* done, const float* sinks, void* out, int64_t so_b,
+                     int64_t so_q, int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
+                     int32_t head_dim, int32_t page_size, int32_t max_seq_len, float scale, float softcap,
+                     void* workspace, size_t workspace_bytes, void* stream) {
     return run_paged_decode(q, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
-                            block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel, done, sinks, out, so_b,
-                            so_q, so_h, batch, queries, q_heads, kv_heads, head_dim, page_size, max_seq_len, scale,
-                            softcap, workspace, workspace_bytes, stream);
+                            block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel, list_page_size,
+                            done, sinks, out, so_b, so_q, so_h, batch, queries, q_heads, kv_heads, head_dim, page_size,
+                            max_seq_len, scale, softcap, workspace, workspace_bytes, stream);
+}
+
+int eco_quest_page_bounds(const void* k_cache, int32_t kv_format, int32_t num_pages, const int32_t* block_table,
+                          int64_t bt_stride, int32_t bt_cols, int32_t first, int32_t last, int32_t quest_page_size,
+                          void* kmin, void* kmax, int64_t sb_b, int64_t sb_h, int64_t sb_p, int32_t batch,
+                          int32_t kv_heads, int32_t head_dim, int32_t page_size, void* stream) {
+    if (!k_cache || !block_table || !kmin || !kmax) return fail("quest page bounds: null cache, table or bounds");
+    if (batch <= 0 || kv_heads <= 0 || num_pages <= 0 || bt_cols <= 0 || bt_stride < bt_cols)
+        return fail("quest page bounds: batch, heads, pages and block-table columns must be positive");
+    if (page_size != 16) return fail("quest page bounds: cache pages must hold 16 tokens");
+    if (quest_page_size < 16 || quest_page_size % 16 || (quest_page_size & (quest_page_size - 1)))
+        return fail("quest page bounds: quest pages must hold a power of two of at least 16 tokens");
+    if (kv_format != BF16 && kv_format != FP8_E4M3 && kv_format != FP8_E5M2)
+        return fail("quest page bounds: KV format must be bf16, fp8 e4m3 or fp8 e5m2");
+    const int es = kv_format == BF16 ? 2 : 1;
+    if (head_dim <= 0 || (head_dim * es) % 64) return fail("quest page bounds: head dim must fill whole runs");
+    if (first < 0 || last < first) return fail("quest page bounds: need 0 <= first <= last");
+    BoundsParams p;
+    p.k_cache = static_cast<const uint8_t*>(k_cache);
+    p.kc_head = static_cast<int64_t>(head_dim) * 16 * es;
+    p.kc_page = p.kc_head * kv_heads;
+    p.kv_format = kv_format;
+    p.num_pages = num_pages;
+    p.block_table = block_table;
+    p.bt_stride = bt_stride;
+    p.bt_cols = bt_cols;
+    p.first = first;
+    p.last = last;
+    p.span = quest_page_size / 16;
+    p.kmin = static_cast<uint16_t*>(kmin);
+    p.kmax = static_cast<uint16_t*>(kmax);
+    p.sb_b = sb_b;
+    p.sb_h = sb_h;
+    p.sb_p = sb_p;
+    p.batch = batch;
+    p.kv_heads = kv_heads;
+    p.head_dim = head_dim;
+    return quest_bounds(p, static_cast<hipStream_t>(stream));
+}
+
+size_t eco_quest_select_workspace_size(int32_t batch, int32_t kv_heads, int32_t max_done) {
+    if (batch <= 0 || kv_heads <= 0 || max_done < 0) return 0;
+    return align256(static_cast<size_t>(batch) * kv_heads * (max_done > 0 ? max_done : 1) * sizeof(float));
+}
+
+int eco_quest_select(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* kmin, const void* kmax,
+                     int64_t sb_b, int64_t sb_h, int64_t sb_p, const int32_t* done, int32_t max_done, int32_t pages,
+                     int32_t* out, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
+                     int32_t head_dim, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!q || !done || !out) return fail("quest select: null query, done or output");
+    if (batch <= 0 || queries <= 0 || q_heads <= 0 || kv_heads <= 0 || pages < 0 || max_done < 0)
+        return fail("quest select: batch, queries and heads must be positive, pages and max_done non-negative");
+    if (q_heads % kv_heads) return fail("quest select: query heads are not a multiple of the KV heads");
+    if (head_dim <= 0 || head_dim % 8 || head_dim > 512) return fail("quest select: head dim must be a multiple of 8 up to 512");
+    if (max_done > 0 && (!kmin || !kmax)) return fail("quest select: null page bounds");
+    if ((reinterpret_cast<uintptr_t>(kmin) & 15) || (reinterpret_cast<uintptr_t>(kmax) & 15) || (sb_b & 7) ||
+        (sb_h & 7) || (sb_p & 7))
+        return fail("quest select: page bounds must be 16-byte aligned with strides that are multiples of 8");
+    if (pages == 0) return 0;
+    const size_t need = eco_quest_select_workspace_size(batch, kv_heads, max_done);
+    if (max_done > 0 && (!workspace || workspace_bytes < need))
+        return fail("quest select: workspace too small (" + std::to_string(workspace_bytes) + " < " +
+                    std::to_string(need) + " bytes)");
+    SelectParams p;
+    p.q = static_cast<const uint16_t*>(q);
+    p.sq_b = sq_b;
+    p.sq_q = sq_q;
+    p.sq_h = sq_h;
+    p.kmin = static_cast<const uint16_t*>(kmin);
+    p.kmax = static_cast<const uint16_t*>(kmax);
+    p.sb_b = sb_b;
+    p.sb_h = sb_h;
+    p.sb_p = sb_p;
+    p.done = done;
+    p.max_done = max_done;
+    p.pages = pages;
+    p.out = out;
+    p.scores = static_cast<float*>(workspace);
+    p.batch = batch;
+    p.queries = queries;
+    p.q_heads = q_heads;
+    p.kv_heads = kv_heads;
+    p.groups = q_heads / kv_heads;
+    p.head_dim = head_dim;
+    p.chunk = 64;
+    return quest_select(p, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

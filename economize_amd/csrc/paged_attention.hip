@@ -176,8 +176,8 @@ __device__ inline Row row_of(const PagedParams& p, int b) {
     const int pages = (r.len + PAGE - 1) / PAGE;
     if (p.page_list != nullptr) {
         const int done = UNIFORM ? scalar_load(p.done, b) : p.done[b];
-        r.done = min(max(done, 0), pages);
-        r.n_virt = p.n_sel + pages - r.done;
+        r.done = min(max(done, 0) * p.span, pages);
+        r.n_virt = p.n_sel * p.span + pages - r.done;
     } else {
         r.done = 0;
         r.n_virt = pages;
@@ -191,11 +191,13 @@ __device__ inline Row row_of(const PagedParams& p, int b) {
 __device__ inline int logical_page(const PagedParams& p, const Row& row, int b, int kvh, int v) {
     if (v >= row.n_virt) return -1;
     if (p.page_list == nullptr) return v;
-    if (v < p.n_sel) {
-        const int page = p.page_list[b * p.pl_b + kvh * p.pl_h + v];
-        return page >= 0 && page < row.done ? page : -1;
+    const int listed = p.n_sel * p.span;
+    if (v < listed) {
+        const int entry = p.page_list[b * p.pl_b + kvh * p.pl_h + v / p.span];
+        const int page = entry * p.span + v % p.span;
+        return entry >= 0 && page < row.done ? page : -1;
     }
-    return row.done + (v - p.n_sel);
+    return row.done + (v - listed);
 }
 
 // Position in the tile sequence: row (b, kvh), its tile t, and the sequence offset of the row's first tile.

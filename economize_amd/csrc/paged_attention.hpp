@@ -6,8 +6,9 @@
 
 namespace eco {
 
-// Virtual pages of row b: without a page list, its ceil(len / 16) pages; with one (Quest), the n_sel listed pages
-// (logical page indices, -1 for none) followed by the dense tail, logical pages done[b] .. ceil(len / 16) - 1.
+// Virtual pages of row b: without a page list, its ceil(len / 16) pages; with one (Quest), the span cache pages of
+// each of the n_sel listed pages (listed page e covers logical cache pages e * span .. e * span + span - 1; -1 for
+// none), followed by the dense tail, logical cache pages done[b] * span .. ceil(len / 16) - 1.
 struct PagedParams {
     const uint16_t* q;  // bf16 [B, Q, Hq, D], channel stride 1
     int64_t sq_b, sq_q, sq_h;
@@ -18,10 +19,10 @@ struct PagedParams {
     int64_t bt_stride;
     int bt_cols, num_pages;
     const int32_t* seq_lens;  // tokens of every row (the queries' own included)
-    const int32_t* page_list;  // optional [B, Hkv, n_sel]
+    const int32_t* page_list;  // optional [B, Hkv, n_sel] listed pages of span cache pages each
     int64_t pl_b, pl_h;
-    int n_sel;
-    const int32_t* done;  // [B] first page of the dense tail (with a page list)
+    int n_sel, span;
+    const int32_t* done;  // [B] first listed-size page of the dense tail (with a page list)
     const float* k_scale;  // optional [Hkv]
     const float* v_scale;
     const float* sinks;  // optional [Hq] logits

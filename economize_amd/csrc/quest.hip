@@ -1,0 +1,275 @@
+// Quest page bounds and query-aware page selection (gfx950).
+//
+// Page bounds follow page_bounds (attention/quest.py:54-65): the channel-wise smallest and largest key of every page,
+// fp8 keys decoded exactly (bf16 holds every fp8 value), written as bf16. They are computed from the stored cache
+// elements; a per-head fp8 scale is positive and multiplies every score of a (row, KV head) alike, so it does not
+// change which pages are selected and is not applied.
+//
+// Selection follows select_pages (attention/quest.py:73-108):
+//   score[b, h, p] = sum_d qsum_d (lo_pd + hi_pd) / 2 + sum_d qabs_d (hi_pd - lo_pd) / 2
+// with qsum / qabs the fp32 sums of q / |q| over the KV head's query rows (rows r = g * Q + qi added in order),
+// pages at or past done[b] excluded, the top min(pages, max_done) pages, increasing, then -1. The reference leaves
+// two things open that are fixed here (and in the oracle): the fp32 order of the two dot products (products rounded
+// to fp32, sequential sums over runs of 8 channels, then a halving tree over the runs, run j plus run j + n / 2, n
+// the run count padded to a power of two) and ties (equal scores are taken lowest page first).
+//
+// Kernels: quest_bounds_kernel (one wave per row, Quest page and KV head), quest_score_kernel (a chunk of pages of
+// one (row, KV head) per workgroup: the bounds are the bytes a selection reads, so the scoring is spread over the
+// whole chip), quest_topk_kernel (one workgroup per (row, KV head): a radix select over order-preserving integer keys
+// of the scores, ties to the lower index, then a compaction in page order).
+
+#include "common.hpp"
+#include "quest.hpp"
+
+namespace eco {
+
+namespace {
+
+constexpr int PAGE = 16;
+
+template <int FMT>
+__device__ inline float decode_elem(const uint8_t* p, int i) {
+    if constexpr (FMT == BF16) {
+        return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+    } else {
+        // exact fp8 value, through the hardware converter (scale 1)
+        const uint32_t word = p[i];
+        if constexpr (FMT == FP8_E4M3)
+            return __builtin_amdgcn_cvt_scalef32_f32_fp8(word, 1.0f, 0);
+        else
+            return __builtin_amdgcn_cvt_scalef32_f32_bf8(word, 1.0f, 0);
+    }
+}
+
+// One wave per (row b, Quest page p, KV head): lane l holds token l % 16 of the runs l / 16, l / 16 + 4, ... of
+// every cache page of the Quest page; the 16 lanes of a run then reduce over the tokens.
+template <int FMT>
+__global__ __launch_bounds__(64) void quest_bounds_kernel(BoundsParams p) {
+    constexpr int ES = FMT == BF16 ? 2 : 1;
+    constexpr int X = 16 / ES;  // channels per 16-byte run
+    const int pages = p.last - p.first;
+    const int b = blockIdx.x / pages;
+    const int qp = p.first + blockIdx.x % pages;
+    const int kvh = blockIdx.y;
+    const int lane = threadIdx.x;
+    const int runs = p.head_dim / X;
+    const int token = lane & 15;
+    // every cache page of the Quest page must be held (a missing one leaves the bounds untouched)
+    for (int s = 0; s < p.span; ++s) {
+        const int lp = qp * p.span + s;
+        if (lp >= p.bt_cols) return;
+        const int phys = p.block_table[b * p.bt_stride + lp];
+        if (phys < 0 || phys >= p.num_pages) return;
+    }
+    for (int r0 = 0; r0 < runs; r0 += 4) {
+        const int run = r0 + (lane >> 4);
+        float lo[X], hi[X];
+#pragma unroll
+        for (int i = 0; i < X; ++i) {
+            lo[i] = INFINITY;
+            hi[i] = -INFINITY;
+        }
+        if (run < runs) {
+            for (int s = 0; s < p.span; ++s) {
+                const int phys = p.block_table[b * p.bt_stride + qp * p.span + s];
+                const uint8_t* src = p.k_cache + static_cast<int64_t>(phys) * p.kc_page + kvh * p.kc_head +
+                                     (run * PAGE + token) * 16;
+                uint8_t raw[16];
+                *reinterpret_cast<uint4*>(raw) = *reinterpret_cast<const uint4*>(src);
+#pragma unroll
+                for (int i = 0; i < X; ++i) {
+                    const float v = decode_elem<FMT>(raw, i);
+                    lo[i] = fminf(lo[i], v);
+                    hi[i] = fmaxf(hi[i], v);
+                }
+            }
+        }
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1)
+#pragma unroll
+            for (int i = 0; i < X; ++i) {
+                lo[i] = fminf(lo[i], __shfl_xor(lo[i], off));
+                hi[i] = fmaxf(hi[i], __shfl_xor(hi[i], off));
+            }
+        if (run < runs && token == 0) {
+            const int64_t at = b * p.sb_b + kvh * p.sb_h + qp * p.sb_p + run * X;
+#pragma unroll
+            for (int i = 0; i < X; ++i) {
+                p.kmin[at + i] = f32_to_bf16(lo[i]);
+                p.kmax[at + i] = f32_to_bf16(hi[i]);
+            }
+        }
+    }
+}
+
+// Scores of pages [chunk * blockIdx.x, +chunk) of row (b, kvh) = blockIdx.y: L lanes per page (L = the run count
+// padded to a power of two), lane j holding channels 8 j .. 8 j + 7.
+__global__ __launch_bounds__(256) void quest_score_kernel(SelectParams p) {
+    __shared__ float qsum[512], qabs[512];
+    const int row = blockIdx.y;
+    const int b = row / p.kv_heads;
+    const int kvh = row % p.kv_heads;
+    const int rows = p.groups * p.queries;
+    for (int d = threadIdx.x; d < p.head_dim; d += blockDim.x) {
+        float s = 0.0f, a = 0.0f;
+        for (int r = 0; r < rows; ++r) {
+            const int g = r / p.queries, qi = r % p.queries;
+            const float x = bf16_to_f32(p.q[b * p.sq_b + qi * p.sq_q + (kvh * p.groups + g) * p.sq_h + d]);
+            s = r == 0 ? x : s + x;
+            a = r == 0 ? fabsf(x) : a + fabsf(x);
+        }
+        qsum[d] = s;
+        qabs[d] = a;
+    }
+    __syncthreads();
+    const int runs = p.head_dim / 8;
+    int L = 1;
+    while (L < runs) L <<= 1;
+    const int per_pass = blockDim.x / L;
+    const int j = threadIdx.x % L;
+    const int done = min(max(p.done[b], 0), p.max_done);
+    float* out = p.scores + static_cast<int64_t>(row) * p.max_done;
+    const int p0 = blockIdx.x * p.chunk;
+    const int p1 = min(p0 + p.chunk, p.max_done);
+    for (int base = p0; base < p1; base += per_pass) {
+        const int page = base + static_cast<int>(threadIdx.x) / L;
+        float s1 = 0.0f, s2 = 0.0f;
+        if (page < p1 && j < runs) {
+            const int64_t at = b * p.sb_b + kvh * p.sb_h + static_cast<int64_t>(page) * p.sb_p + 8 * j;
+            const uint4 lw = *reinterpret_cast<const uint4*>(p.kmin + at);
+            const uint4 hw = *reinterpret_cast<const uint4*>(p.kmax + at);
+            const uint32_t lo_w[4] = {lw.x, lw.y, lw.z, lw.w};
+            const uint32_t hi_w[4] = {hw.x, hw.y, hw.z, hw.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float lo = bf16_to_f32(static_cast<uint16_t>(lo_w[i >> 1] >> (16 * (i & 1))));
+                const float hi = bf16_to_f32(static_cast<uint16_t>(hi_w[i >> 1] >> (16 * (i & 1))));
+                const float mid = (lo + hi) * 0.5f;
+                const float half = (hi - lo) * 0.5f;
+                const float t1 = qsum[8 * j + i] * mid;
+                const float t2 = qabs[8 * j + i] * half;
+                s1 = i == 0 ? t1 : s1 + t1;
+                s2 = i == 0 ? t2 : s2 + t2;
+            }
+        }
+        for (int off = L / 2; off > 0; off >>= 1) {
+            s1 += __shfl_xor(s1, off);
+            s2 += __shfl_xor(s2, off);
+        }
+        if (page < p1 && j == 0) out[page] = page < done ? s1 + s2 : -INFINITY;
+    }
+}
+
+// Order-preserving integer key of a score (a larger score has a larger key; -0 counts as +0).
+__device__ inline uint32_t score_key(float x) {
+    const uint32_t u = f32_bits(x == 0.0f ? 0.0f : x);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Inclusive scan of one value per thread over a 256-thread workgroup; *total receives the sum.
+__device__ inline int block_scan(int x, int* lds4, int* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off);
+        if (lane >= off) x += y;
+    }
+    if (lane == 63) lds4[wave] = x;
+    __syncthreads();
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += lds4[w];
+    *total = lds4[0] + lds4[1] + lds4[2] + lds4[3];
+    __syncthreads();
+    return x + before;
+}
+
+// One workgroup of 256 threads per (row, KV head): the top `count` of the row's committed pages by score, written in
+// increasing page order, then -1.
+__global__ __launch_bounds__(256) void quest_topk_kernel(SelectParams p) {
+    __shared__ int hist[256];
+    __shared__ int lds4[4];
+    __shared__ uint32_t shared_prefix;
+    __shared__ int shared_rem;
+    const int row = blockIdx.x;
+    const int b = row / p.kv_heads;
+    const int t = threadIdx.x;
+    const int n = min(max(p.done[b], 0), p.max_done);
+    const int count = min(p.pages, p.max_done);
+    int32_t* out = p.out + static_cast<int64_t>(row) * p.pages;
+    const float* scores = p.scores + static_cast<int64_t>(row) * p.max_done;
+    const int per = (n + 255) / 256;
+    const int i0 = min(t * per, n), i1 = min(i0 + per, n);
+    int total = 0;
+    if (n <= count) {  // every committed page
+        for (int i = t; i < p.pages; i += 256) out[i] = i < n ? i : -1;
+        return;
+    }
+    // radix select of the count-th largest key, most significant byte first
+    uint32_t prefix = 0, known = 0;
+    int rem = count;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        hist[t] = 0;
+        __syncthreads();
+        for (int i = i0; i < i1; ++i) {
+            const uint32_t key = score_key(scores[i]);
+            if (((key ^ prefix) & known) == 0) atomicAdd(&hist[(key >> shift) & 255], 1);
+        }
+        __syncthreads();
+        const int c = hist[255 - t];  // thread t counts digit 255 - t: the scan runs from the largest digit down
+        const int incl = block_scan(c, lds4, &total);
+        if (incl >= rem && incl - c < rem) {
+            shared_prefix = prefix | (static_cast<uint32_t>(255 - t) << shift);
+            shared_rem = rem - (incl - c);
+        }
+        __syncthreads();
+        prefix = shared_prefix;
+        rem = shared_rem;
+        known |= 0xFFu << shift;
+        __syncthreads();
+    }
+    // keys above the threshold, and the first `rem` keys equal to it in page order
+    int eq = 0;
+    for (int i = i0; i < i1; ++i) eq += score_key(scores[i]) == prefix ? 1 : 0;
+    int eq_before = block_scan(eq, lds4, &total) - eq;
+    int sel = 0;
+    for (int i = i0, e = eq_before; i < i1; ++i) {
+        const uint32_t key = score_key(scores[i]);
+        if (key > prefix) ++sel;
+        else if (key == prefix) sel += e++ < rem ? 1 : 0;
+    }
+    int pos = block_scan(sel, lds4, &total) - sel;
+    for (int i = i0, e = eq_before; i < i1; ++i) {
+        const uint32_t key = score_key(scores[i]);
+        bool take = key > prefix;
+        if (key == prefix) take = e++ < rem;
+        if (take) out[pos++] = i;
+    }
+    for (int i = count + t; i < p.pages; i += 256) out[i] = -1;
+}
+
+}  // namespace
+
+int quest_bounds(const BoundsParams& p, hipStream_t stream) {
+    if (p.last <= p.first) return 0;
+    dim3 grid(static_cast<unsigned>(p.batch) * (p.last - p.first), p.kv_heads);
+    switch (p.kv_format) {
+        case BF16: hipLaunchKernelGGL(quest_bounds_kernel<BF16>, grid, dim3(64), 0, stream, p); break;
+        case FP8_E4M3: hipLaunchKernelGGL(quest_bounds_kernel<FP8_E4M3>, grid, dim3(64), 0, stream, p); break;
+        case FP8_E5M2: hipLaunchKernelGGL(quest_bounds_kernel<FP8_E5M2>, grid, dim3(64), 0, stream, p); break;
+        default: return fail("quest page bounds: KV format must be bf16, fp8 e4m3 or fp8 e5m2");
+    }
+    return check_launch("quest_bounds_kernel");
+}
+
+int quest_select(const SelectParams& p, hipStream_t stream) {
+    const int rows = p.batch * p.kv_heads;
+    if (p.max_done > 0) {
+        dim3 grid((p.max_done + p.chunk - 1) / p.chunk, rows);
+        hipLaunchKernelGGL(quest_score_kernel, grid, dim3(256), 0, stream, p);
+        if (int rc = check_launch("quest_score_kernel")) return rc;
+    }
+    hipLaunchKernelGGL(quest_topk_kernel, dim3(rows), dim3(256), 0, stream, p);
+    return check_launch("quest_topk_kernel");
+}
+
+}  // namespace eco

@@ -1,0 +1,41 @@
+// Parameters of the Quest kernels (quest.hip): page bounds over the paged key cache, page scores, top-k selection.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace eco {
+
+struct BoundsParams {
+    const uint8_t* k_cache;  // [pages, Hkv, D / X, 16, X]
+    int64_t kc_page, kc_head;  // byte strides
+    int kv_format, num_pages;
+    const int32_t* block_table;  // [B, bt_cols], row stride bt_stride
+    int64_t bt_stride;
+    int bt_cols;
+    int first, last;  // Quest pages [first, last) of every row
+    int span;         // cache pages (16 tokens) per Quest page
+    uint16_t* kmin;   // bf16 [B, Hkv, P, D], element strides
+    uint16_t* kmax;
+    int64_t sb_b, sb_h, sb_p;
+    int batch, kv_heads, head_dim;
+};
+
+struct SelectParams {
+    const uint16_t* q;  // bf16 [B, Q, Hq, D], channel stride 1
+    int64_t sq_b, sq_q, sq_h;
+    const uint16_t* kmin;  // bf16 [B, Hkv, P, D], channel stride 1
+    const uint16_t* kmax;
+    int64_t sb_b, sb_h, sb_p;
+    const int32_t* done;  // [B] committed Quest pages of every row
+    int max_done, pages;
+    int32_t* out;     // [B, Hkv, pages]
+    float* scores;    // workspace [B, Hkv, max_done]
+    int batch, queries, q_heads, kv_heads, groups, head_dim;
+    int chunk;        // pages scored per workgroup
+};
+
+int quest_bounds(const BoundsParams& p, hipStream_t stream);
+int quest_select(const SelectParams& p, hipStream_t stream);
+
+}  // namespace eco

@@ -131,10 +131,11 @@ def head_scales(x: torch.Tensor, dtype: torch.dtype = torch.float8_e4m3fn) -> to
 
 
 def workspace_size(batch: int, queries: int, q_heads: int, kv_heads: int, head_dim: int, max_seq_len: int,
-                   n_sel: int = 0, dtype: torch.dtype = torch.float8_e4m3fn) -> int:
-    """Bytes of scratch :func:`paged_decode_attention` needs for this shape and cache dtype."""
+                   n_sel: int = 0, dtype: torch.dtype = torch.float8_e4m3fn, list_page_size: int = PAGE) -> int:
+    """Bytes of scratch :func:`paged_decode_attention` needs for this shape and cache dtype (``n_sel`` listed pages
+    of ``list_page_size`` tokens)."""
     return int(_lib.lib().eco_paged_decode_workspace_size(batch, queries, q_heads, kv_heads, head_dim, max_seq_len,
-                                                          n_sel, _lib.fmt(dtype)))
+                                                          n_sel, list_page_size, _lib.fmt(dtype)))
 
 
 def new_workspace(nbytes: int, device: torch.device | str) -> torch.Tensor:
@@ -169,6 +170,7 @@ def paged_decode_attention(
     page_list: torch.Tensor | None = None,
     done: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
+    list_page_size: int = PAGE,
 ) -> torch.Tensor:
     """Attention of ``query`` ``[B, Q, Hq, D]`` (bf16, channel-contiguous) over the paged cache, ``[B, Q, Hq, D]``
     bf16 out.
@@ -177,8 +179,9 @@ def paged_decode_attention(
     sizes the launch), its ``Q`` queries the last of them: query ``qi`` sees tokens ``< seq_lens[b] - Q + qi + 1``.
     ``block_table`` is int32 ``[B, pages per row]``. ``scale`` defaults to ``1 / sqrt(D)``.
 
-    With ``page_list`` (int32 ``[B, Hkv, n_sel]``, logical pages, ``-1`` = none) and ``done`` (int32 ``[B]``) the
-    keys read are the listed pages and every token from page ``done[b]`` on (Quest's gathered attention).
+    With ``page_list`` (int32 ``[B, Hkv, n_sel]``, pages of ``list_page_size`` tokens, ``-1`` = none) and ``done``
+    (int32 ``[B]``, in the same pages) the keys read are the listed pages below ``done[b]`` and every token from page
+    ``done[b]`` on (Quest's gathered attention).
     ``workspace`` (from :func:`new_workspace`, at least :func:`workspace_size` bytes) defaults to a cached one per
     device and stream.
     """
@@ -214,7 +217,10 @@ def paged_decode_attention(
         raise ConfigError("out must be bf16 like the query, with a contiguous channel axis")
     if max_seq_len <= 0:
         raise ConfigError("max_seq_len must be positive")
-    need = workspace_size(batch, queries, q_heads, cache.kv_heads, head_dim, max_seq_len, n_sel, cache.dtype)
+    if list_page_size < PAGE or list_page_size % PAGE:
+        raise ConfigError(f"listed pages must hold a positive multiple of {PAGE} tokens, not {list_page_size}")
+    need = workspace_size(batch, queries, q_heads, cache.kv_heads, head_dim, max_seq_len, n_sel, cache.dtype,
+                          list_page_size)
     if workspace is None:
         workspace = _workspace(need, device)
     scale = 1.0 / math.sqrt(head_dim) if scale is None else float(scale)
@@ -225,7 +231,8 @@ def paged_decode_attention(
         _lib.ptr(cache.k_scale), _lib.ptr(cache.v_scale),
         block_table.data_ptr(), block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(),
         _lib.ptr(page_list), page_list.stride(0) if page_list is not None else 0,
-        page_list.stride(1) if page_list is not None else 0, n_sel, _lib.ptr(done), _lib.ptr(sinks),
+        page_list.stride(1) if page_list is not None else 0, n_sel, int(list_page_size), _lib.ptr(done),
+        _lib.ptr(sinks),
         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
         batch, queries, q_heads, cache.kv_heads, head_dim, PAGE, int(max_seq_len), scale, float(softcap or 0.0),
         workspace.data_ptr(), workspace.numel(), _lib.stream_of(device),

@@ -56,11 +56,12 @@ int eco_kv_head_absmax(const void* x, int32_t in_format, int32_t a, int32_t h, i
 int eco_fp8_scales_from_absmax(const uint32_t* absmax_bits, int32_t heads, int32_t format, float* scales,
                                void* stream);
 
-/* Workspace bytes eco_paged_decode needs for this shape (n_sel = Quest's selected pages, 0 without). The workspace
- * starts with per-row counters that must be zero before its first use; every call leaves them zero. One workspace
- * serves one stream at a time. */
+/* Workspace bytes eco_paged_decode needs for this shape (n_sel = Quest's selected pages of list_page_size tokens,
+ * 0 without). The workspace starts with per-row counters that must be zero before its first use; every call leaves
+ * them zero. One workspace serves one stream at a time. */
 size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
-                                       int32_t head_dim, int32_t max_seq_len, int32_t n_sel, int32_t kv_format);
+                                       int32_t head_dim, int32_t max_seq_len, int32_t n_sel, int32_t list_page_size,
+                                       int32_t kv_format);
 
 /* Split-K decode attention over the paged cache: out[b, qi, h, :] (bf16, element strides so_*) for query q[b, qi,
  * h, :] (bf16, element strides sq_*, channel stride 1), query head h reading KV head h / (q_heads / kv_heads).
@@ -70,17 +71,42 @@ size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q
  * denominator. A row that sees no key gives 0.
  * Replaces decode_attention (attention/decode.py:252-324) for a paged cache, and with page_list != NULL
  * quest_decode_attention (attention/quest.py:239-344): the keys read are the pages page_list[b, kvh, 0..n_sel)
- * (strides pl_b, pl_h; logical page indices below done[b], others read nothing) and then every token from page
- * done[b] on. One launch: the work is cut into equal contiguous ranges of 64-token tiles, one per wave, so ragged
- * rows need no host-side plan; max_seq_len (>= every seq_lens[b]) only bounds the launch. */
+ * (strides pl_b, pl_h; page indices of list_page_size tokens each, 0 = 16; pages below done[b] are read, others
+ * read nothing) and then every token from page done[b] on (done in listed pages too). One launch: the work is cut
+ * into equal contiguous ranges of 64-token tiles, one per wave, so ragged rows need no host-side plan; max_seq_len
+ * (>= every seq_lens[b]) only bounds the launch. */
 int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
                      const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
                      const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
-                     const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h, int32_t n_sel, const int32_t* done,
-                     const float* sinks, void* out, int64_t so_b, int64_t so_q, int64_t so_h, int32_t batch,
-                     int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
-                     int32_t max_seq_len, float scale, float softcap, void* workspace, size_t workspace_bytes,
-                     void* stream);
+                     const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h, int32_t n_sel,
+                     int32_t list_page_size, const int32_t* done, const float* sinks, void* out, int64_t so_b,
+                     int64_t so_q, int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
+                     int32_t head_dim, int32_t page_size, int32_t max_seq_len, float scale, float softcap,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Quest page bounds: kmin / kmax (bf16 [B, Hkv, P, D], element strides sb_b, sb_h, sb_p, channel stride 1) of the
+ * Quest pages [first, last) of every row (quest_page_size tokens each, a power of two >= 16), the channel-wise
+ * smallest and largest stored key read through the block table (fp8 decoded exactly; per-head scales not applied:
+ * they scale every score of a (row, KV head) alike). A Quest page with a cache page outside the table or the cache
+ * is left untouched. Replaces page_bounds (attention/quest.py:54-65) as QuestCache._layer_bounds calls it
+ * (techniques/quest/technique.py:229-259). */
+int eco_quest_page_bounds(const void* k_cache, int32_t kv_format, int32_t num_pages, const int32_t* block_table,
+                          int64_t bt_stride, int32_t bt_cols, int32_t first, int32_t last, int32_t quest_page_size,
+                          void* kmin, void* kmax, int64_t sb_b, int64_t sb_h, int64_t sb_p, int32_t batch,
+                          int32_t kv_heads, int32_t head_dim, int32_t page_size, void* stream);
+
+/* Workspace bytes of eco_quest_select (the page scores, fp32 [B, Hkv, max_done]). */
+size_t eco_quest_select_workspace_size(int32_t batch, int32_t kv_heads, int32_t max_done);
+
+/* Quest page selection: out[b, kvh, 0..pages) (int32, contiguous) = the pages of row b with the largest scores
+ * sum_d qsum_d (lo + hi) / 2 + qabs_d (hi - lo) / 2 among its committed pages [0, done[b]) (pages >= max_done never),
+ * min(pages, max_done) of them in increasing order, then -1; ties go to the lower page. qsum / qabs are the sums of
+ * q / |q| (q [B, Q, Hq, D] bf16, element strides sq_*, channel stride 1) over the KV head's query rows; lo / hi are
+ * the page bounds (bf16, 16-byte aligned, strides multiples of 8). Replaces select_pages (attention/quest.py:73-108). */
+int eco_quest_select(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* kmin, const void* kmax,
+                     int64_t sb_b, int64_t sb_h, int64_t sb_p, const int32_t* done, int32_t max_done, int32_t pages,
+                     int32_t* out, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
+                     int32_t head_dim, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -42,7 +42,26 @@ def test_library_exports_every_declared_function() -> None:
     from economize_amd import _lib
 
     assert sorted(_lib.SIGNATURES) == declared  # the binding declares every entry point
-    assert _lib.lib().eco_abi_version() == 1
+    assert _lib.lib().eco_abi_version() == 2
+
+
+def _parameter_counts() -> dict[str, int]:
+    counts = {}
+    for header in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        for name, params in re.findall(r"\b(eco_\w+)\s*\(([^)]*)\)\s*;", text):
+            params = params.strip()
+            counts[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return counts
+
+
+def test_binding_argument_counts_match_the_header() -> None:
+    from economize_amd import _lib
+
+    counts = _parameter_counts()
+    assert set(counts) == set(_lib.SIGNATURES)
+    for name, (_, argtypes) in _lib.SIGNATURES.items():
+        assert len(argtypes) == counts[name], name
 
 
 def test_validation_errors_are_reported_without_a_device() -> None:
@@ -51,7 +70,7 @@ def test_validation_errors_are_reported_without_a_device() -> None:
     lib = _lib.lib()
     rc = lib.eco_paged_append(None, None, 0, 0, 0, 0, 0, None, 3, None, None, 1, 1, 64, 16, 1, None, None, None)
     assert rc == 1 and b"null" in lib.eco_last_error()
-    assert lib.eco_paged_decode_workspace_size(32, 1, 32, 8, 128, 4096, 0, 1) > 0
+    assert lib.eco_paged_decode_workspace_size(32, 1, 32, 8, 128, 4096, 0, 16, 1) > 0
 
 
 @pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
