@@ -41,6 +41,14 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
     "eco_paged_decode": (c_int32, _PAGED_DECODE),
     "eco_quest_page_bounds": (c_int32, [_P, _I, _I, _P, _L, _I, _I, _I, _I, _P, _P, _L, _L, _L, _I, _I, _I, _I, _P]),
     "eco_quest_select_workspace_size": (c_size_t, [_I, _I, _I]),
+    "eco_kivi_block_bytes": (c_size_t, [_I, _I, _I]),
+    "eco_kivi_schedule": (c_int32, [_P, _I, _I, _P, _P, _P, _I, _P]),
+    "eco_kivi_quantize": (c_int32, [_I, _P, _I, _L, _L, _L, _L, _I, _I, _P, _P, _P, _I, _P, _L, _I, _I, _I, _I, _I, _I,
+                                    _I, _P, _P]),
+    "eco_kivi_ring_write": (c_int32, [_P, _P, _I, _L, _L, _L, _L, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P]),
+    "eco_kivi_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I]),
+    "eco_kivi_decode": (c_int32, [_P, _L, _L, _L, _P, _I, _P, _P, _I, _P, _P, _P, _L, _I, _P, _P, _P, _L, _L, _L, _I, _I,
+                                  _I, _I, _I, _I, _I, _I, _F, _F, _P, _S, _P]),
     "eco_quest_select": (c_int32, [_P, _L, _L, _L, _P, _P, _L, _L, _L, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _S,
                                    _P]),
 }

@@ -7,6 +7,7 @@
 
 #include "../../include/economize_amd.h"
 #include "common.hpp"
+#include "kivi.hpp"
 #include "kv_quant.hpp"
 #include "paged_attention.hpp"
 #include "quest.hpp"
@@ -77,6 +78,28 @@ struct Workspace {
 Workspace paged_workspace(int batch, int kv_heads, int rows, int head_dim, int grid) {
     return Workspace{align256(static_cast<size_t>(batch) * kv_heads * sizeof(int32_t)),
                      align256(static_cast<size_t>(2) * grid * rows * (head_dim + 2) * sizeof(float))};
+}
+
+// The KIVI decode launch: as paged_grid, over 32-token tiles.
+int kivi_grid(int batch, int kv_heads, int rows, int head_dim, int bits, int max_seq_len) {
+    static const int forced = [] {
+        const char* env = std::getenv("ECO_KIVI_GRID");
+        return env ? std::atoi(env) : 0;
+    }();
+    const int64_t tiles = static_cast<int64_t>(batch) * kv_heads * ((max_seq_len + 31) / 32);
+    int per_cu = 1;
+    if (kivi_resident_waves(head_dim, bits, rows, &per_cu)) return 0;
+    int64_t grid = forced > 0 ? forced : static_cast<int64_t>(device_cus()) * per_cu;
+    const int64_t cap = (tiles + 3) / 4;
+    grid = grid < cap ? grid : cap;
+    return static_cast<int>(grid < 1 ? 1 : grid);
+}
+
+int check_kivi_shape(int head_dim, int bits, int group) {
+    if (group != 32) return fail("kivi: the paged cache takes groups of 32 (key tokens and value channels)");
+    if (bits != 2 && bits != 4) return fail("kivi: codes must have 2 or 4 bits");
+    if (head_dim != 64 && head_dim != 128) return fail("kivi: head dim must be 64 or 128");
+    return 0;
 }
 
 int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
@@ -263,6 +286,158 @@ int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
                             block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel, list_page_size,
                             done, sinks, out, so_b, so_q, so_h, batch, queries, q_heads, kv_heads, head_dim, page_size,
                             max_seq_len, scale, softcap, workspace, workspace_bytes, stream);
+}
+
+size_t eco_kivi_block_bytes(int32_t head_dim, int32_t bits, int32_t group) {
+    if (check_kivi_shape(head_dim, bits, group)) return 0;
+    return static_cast<size_t>(KiviLayout{head_dim, bits}.size());
+}
+
+int eco_kivi_schedule(const int32_t* committed, int32_t residual, int32_t group, int32_t* keys_quantized,
+                      int32_t* values_quantized, int32_t* ranges, int32_t batch, void* stream) {
+    if (!committed || !keys_quantized || !values_quantized || !ranges) return fail("kivi schedule: null pointer");
+    if (batch <= 0) return fail("kivi schedule: batch must be positive");
+    if (group != 32 || residual <= 0 || residual % 32)
+        return fail("kivi schedule: the residual length must be a positive multiple of the group (32)");
+    return kivi_schedule(committed, residual, keys_quantized, values_quantized, ranges, batch,
+                         static_cast<hipStream_t>(stream));
+}
+
+int eco_kivi_quantize(int32_t kind, const void* src, int32_t src_format, int64_t ss_b, int64_t ss_h, int64_t ss_t,
+                      int64_t ss_d, int32_t src_start, int32_t src_ring, const int32_t* from, const int32_t* to,
+                      void* blocks, int32_t num_pages, const int32_t* block_table, int64_t bt_stride,
+                      int32_t bt_cols, int32_t batch, int32_t kv_heads, int32_t head_dim, int32_t bits,
+                      int32_t group, int32_t max_tokens, uint32_t* overflow, void* stream) {
+    if (kind != 0 && kind != 1) return fail("kivi quantize: kind must be 0 (keys) or 1 (values)");
+    if (!src || !from || !to || !blocks || !block_table) return fail("kivi quantize: null pointer");
+    if (src_format != BF16 && src_format != FP16 && src_format != FP32)
+        return fail("kivi quantize: the source must be bf16, fp16 or fp32");
+    if (batch <= 0 || kv_heads <= 0 || num_pages <= 0 || bt_cols <= 0 || bt_stride < bt_cols)
+        return fail("kivi quantize: batch, heads, pages and block-table columns must be positive");
+    if (int rc = check_kivi_shape(head_dim, bits, group)) return rc;
+    if (src_ring < 0) return fail("kivi quantize: negative ring");
+    if (max_tokens <= 0) return 0;
+    const KiviLayout L{head_dim, bits};
+    KiviQuantParams p;
+    p.src = src;
+    p.src_format = src_format;
+    p.ss_b = ss_b;
+    p.ss_h = ss_h;
+    p.ss_t = ss_t;
+    p.ss_d = ss_d;
+    p.src_start = src_start;
+    p.src_ring = src_ring;
+    p.from = from;
+    p.to = to;
+    p.blocks = static_cast<uint8_t*>(blocks);
+    p.blk_head = L.size();
+    p.blk_page = static_cast<int64_t>(L.size()) * kv_heads;
+    p.block_table = block_table;
+    p.bt_stride = bt_stride;
+    p.bt_cols = bt_cols;
+    p.num_pages = num_pages;
+    p.batch = batch;
+    p.kv_heads = kv_heads;
+    p.head_dim = head_dim;
+    p.bits = bits;
+    p.overflow = overflow;
+    return kivi_quantize(p, kind, max_tokens, static_cast<hipStream_t>(stream));
+}
+
+int eco_kivi_ring_write(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
+                        int64_t sv_t, int64_t sv_h, const int32_t* rows, const int32_t* positions, int32_t tokens,
+                        void* k_ring, void* v_ring, int32_t batch, int32_t kv_heads, int32_t head_dim, int32_t ring,
+                        void* stream) {
+    if (tokens < 0) return fail("kivi ring write: negative token count");
+    if (tokens == 0) return 0;
+    if (!k_new || !v_new || !rows || !positions || !k_ring || !v_ring) return fail("kivi ring write: null pointer");
+    if (in_format != BF16 && in_format != FP16 && in_format != FP32)
+        return fail("kivi ring write: inputs must be bf16, fp16 or fp32");
+    if (batch <= 0 || kv_heads <= 0 || head_dim <= 0 || ring <= 0) return fail("kivi ring write: bad shape");
+    KiviRingParams p{k_new, v_new, in_format, sk_t, sk_h, sv_t, sv_h, rows, positions, tokens,
+                     static_cast<uint16_t*>(k_ring), static_cast<uint16_t*>(v_ring), batch, kv_heads, head_dim, ring};
+    return kivi_ring_write(p, static_cast<hipStream_t>(stream));
+}
+
+size_t eco_kivi_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
+                                      int32_t head_dim, int32_t max_seq_len, int32_t bits) {
+    if (batch <= 0 || queries <= 0 || kv_heads <= 0 || q_heads <= 0 || max_seq_len <= 0) return 0;
+    if (check_kivi_shape(head_dim, bits, 32)) return 0;
+    const int rows = (q_heads / kv_heads) * queries;
+    const int grid = kivi_grid(batch, kv_heads, rows, head_dim, bits, max_seq_len);
+    if (grid <= 0) return 0;
+    return paged_workspace(batch, kv_heads, rows, head_dim, grid).total();
+}
+
+int eco_kivi_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* blocks, int32_t num_pages,
+                    const void* k_ring, const void* v_ring, int32_t ring, const int32_t* keys_quantized,
+                    const int32_t* values_quantized, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                    const int32_t* seq_lens, const float* sinks, void* out, int64_t so_b, int64_t so_q, int64_t so_h,
+                    int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                    int32_t bits, int32_t group, int32_t max_seq_len, float scale, float softcap, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+    if (!q || !blocks || !k_ring || !v_ring || !keys_quantized || !values_quantized || !block_table || !seq_lens ||
+        !out)
+        return fail("kivi decode: null query, cache, ring, counts, table, lengths or output");
+    if (batch <= 0 || queries <= 0 || q_heads <= 0 || kv_heads <= 0 || num_pages <= 0 || bt_cols <= 0 ||
+        bt_stride < bt_cols)
+        return fail("kivi decode: batch, queries, heads, pages and block-table columns must be positive");
+    if (q_heads % kv_heads) return fail("kivi decode: query heads are not a multiple of the KV heads");
+    if (int rc = check_kivi_shape(head_dim, bits, group)) return rc;
+    if (ring <= 0 || ring % 32) return fail("kivi decode: the ring must hold a positive multiple of 32 slots");
+    const int groups = q_heads / kv_heads;
+    const int rows = groups * queries;
+    if (rows > 64) return fail("kivi decode: at most 64 query rows per KV head (query heads per KV head x queries)");
+    if ((reinterpret_cast<uintptr_t>(q) & 15) || (sq_b & 7) || (sq_q & 7) || (sq_h & 7))
+        return fail("kivi decode: the query must be 16-byte aligned with strides that are multiples of 8");
+    if (max_seq_len <= 0) return fail("kivi decode: max_seq_len must be positive");
+    if (!(scale == scale)) return fail("kivi decode: scale is NaN");
+    const int grid = kivi_grid(batch, kv_heads, rows, head_dim, bits, max_seq_len);
+    if (grid <= 0) return 1;
+    const Workspace ws = paged_workspace(batch, kv_heads, rows, head_dim, grid);
+    if (!workspace || workspace_bytes < ws.total())
+        return fail("kivi decode: workspace too small (" + std::to_string(workspace_bytes) + " < " +
+                    std::to_string(ws.total()) + " bytes)");
+    const KiviLayout L{head_dim, bits};
+    KiviParams p;
+    std::memset(&p, 0, sizeof(p));
+    p.q = static_cast<const uint16_t*>(q);
+    p.sq_b = sq_b;
+    p.sq_q = sq_q;
+    p.sq_h = sq_h;
+    p.blocks = static_cast<const uint8_t*>(blocks);
+    p.blk_head = L.size();
+    p.blk_page = static_cast<int64_t>(L.size()) * kv_heads;
+    p.k_ring = static_cast<const uint16_t*>(k_ring);
+    p.v_ring = static_cast<const uint16_t*>(v_ring);
+    p.ring = ring;
+    p.keys_quantized = keys_quantized;
+    p.values_quantized = values_quantized;
+    p.block_table = block_table;
+    p.bt_stride = bt_stride;
+    p.bt_cols = bt_cols;
+    p.num_pages = num_pages;
+    p.seq_lens = seq_lens;
+    p.sinks = sinks;
+    char* base = static_cast<char*>(workspace);
+    p.counters = reinterpret_cast<int32_t*>(base);
+    p.part = reinterpret_cast<float*>(base + ws.counter_bytes);
+    p.out = static_cast<uint16_t*>(out);
+    p.so_b = so_b;
+    p.so_q = so_q;
+    p.so_h = so_h;
+    p.batch = batch;
+    p.queries = queries;
+    p.q_heads = q_heads;
+    p.kv_heads = kv_heads;
+    p.groups = groups;
+    p.rows = rows;
+    p.head_dim = head_dim;
+    p.bits = bits;
+    p.grid = grid;
+    p.scale = scale;
+    p.softcap = softcap > 0.0f ? softcap : 0.0f;
+    return kivi_attention(p, static_cast<hipStream_t>(stream));
 }
 
 int eco_quest_page_bounds(const void* k_cache, int32_t kv_format, int32_t num_pages, const int32_t* block_table,

@@ -1,0 +1,811 @@
+// KIVI (Liu et al., ICML 2024) on gfx950: the quantization schedule, the full-precision residual ring,
+// quantize-and-append into 32-token pages, and decode attention that feeds the codes to the matrix cores.
+//
+// Quantization follows the reference's quantize (techniques/kv_quant/kivi.py:121-140): fp32 min and max along the
+// group; scale = fp16r((high - low) / levels) and low = fp16r(low), fp16r rounding to nearest even where fp16 holds
+// the value; codes = round_half_even((x - low) / safe) clamped to [0, levels], safe = scale or 1 where the scale is 0.
+// Both divisions are IEEE divisions (__fdiv_rn), the CPU semantics of torch's tensor / int and tensor / tensor (GPU
+// torch multiplies by a reciprocal instead; the parity oracle is the CPU definition). Keys are quantized per channel
+// over a 32-token group (one page), values per token over 32-channel groups. The schedule is the reference's
+// (kivi.py:230-243): with c committed tokens, keys below (c / R) * R and values below max(0, c - R) are quantized.
+//
+// Page block (one per (page, KV head), offsets in KiviLayout): key codes token-major, each token's channels packed
+// in 32-bit words; value codes as words (u * 16 + n) * (D / 16) + nd, channel 16 nd + n, tokens u * 32 / bits ..;
+// key scales and zero points [D]; value scales and zero points [D / 32][32]. A word holds 32 / bits elements,
+// element e in byte e % 4 at bit (e / 4) * bits.
+//
+// Attention. The reference dequantizes code * scale + zero in fp32 and attends over the values rounded to the model
+// dtype (attention/kivi.py:56-76, attention/_kivi_kernels.py:14-15). Keys are dequantized that way (the softmax is
+// sensitive to the rounding of the keys, most of all in outlier channels) and multiplied by q with bf16 MFMAs. For
+// the values the dequantization is folded into the matrix-core operands by linearity:
+//   sum_t p_t v_td = sum_t (p_t s_tg) c_td + sum_t p_t z_tg     (value scale and zero of token t, group g of d)
+// so the MFMA A operand is the codes themselves: a code c < 16 zero-extended to a byte is the e4m3 pattern of
+// c * 2^-9, and v_cvt_scalef32_pk_f16_fp8 with scale 2^9 turns it into the exact fp16 value c (the same conversion
+// to fp32 feeds the key dequantization). The B operand p * s is rounded to fp16 (11 significant bits; the reference
+// rounds p to bf16, 8 bits), and the zero term is an MFMA too: z (one row per value group) times p. Tokens not yet
+// quantized are read from the bf16 ring (bf16 MFMAs, p split into two bf16 terms).
+//
+// Work decomposition, pipeline and merge: the stream-K scheme of paged_attention.hip (stream_k.hpp), with tiles of
+// one 32-token page. The query of the current row lives in LDS, so that row changes do not put loads of varying
+// count in the tile pipeline.
+
+#include <type_traits>
+
+#include "common.hpp"
+#include "kivi.hpp"
+#include "stream_k.hpp"
+
+namespace eco {
+
+namespace {
+
+constexpr int KPAGE = KiviParams::kPage;  // 32 tokens
+
+__device__ inline float load_elem(const void* base, int64_t offset, int format) {
+    if (format == BF16) return bf16_to_f32(static_cast<const uint16_t*>(base)[offset]);
+    if (format == FP16) return static_cast<float>(static_cast<const _Float16*>(base)[offset]);
+    return static_cast<const float*>(base)[offset];
+}
+
+// fp16r of the reference: x rounded to fp16 where |x| <= 65504, else x.
+__device__ inline float fp16_rounded(float x) {
+    return fabsf(x) <= 65504.0f ? static_cast<float>(static_cast<_Float16>(x)) : x;
+}
+
+__device__ inline uint16_t f16_bits(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+}
+
+// ---- schedule --------------------------------------------------------------------------------------------------
+
+// ranges [4][B]: keys [from, to), values [from, to) to quantize now; the counts advance to their new values.
+__global__ void kivi_schedule_kernel(const int32_t* committed, int residual, int32_t* kq, int32_t* vq,
+                                     int32_t* ranges, int batch) {
+    const int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= batch) return;
+    const int c = max(committed[b], 0);
+    const int k_to = max(kq[b], (c / residual) * residual);
+    const int v_to = max(vq[b], c - residual);
+    ranges[b] = kq[b];
+    ranges[batch + b] = k_to;
+    ranges[2 * batch + b] = vq[b];
+    ranges[3 * batch + b] = v_to;
+    kq[b] = k_to;
+    vq[b] = v_to;
+}
+
+// ---- residual ring ------------------------------------------------------------------------------------------
+
+// One workgroup per new token: keys to slot t % W of [B, Hkv, W, D], values to [B, Hkv, D, W], rounded to bf16.
+__global__ __launch_bounds__(256) void kivi_ring_kernel(KiviRingParams p) {
+    const int t = blockIdx.x;
+    const int pos = p.positions[t];
+    const int b = p.rows[t];
+    if (pos < 0 || b < 0 || b >= p.batch) return;
+    const int slot = pos % p.ring;
+    for (int i = threadIdx.x; i < p.kv_heads * p.head_dim; i += blockDim.x) {
+        const int h = i / p.head_dim, d = i % p.head_dim;
+        const float k = load_elem(p.k_new, t * p.sk_t + h * p.sk_h + d, p.in_format);
+        const float v = load_elem(p.v_new, t * p.sv_t + h * p.sv_h + d, p.in_format);
+        const int64_t row = static_cast<int64_t>(b) * p.kv_heads + h;
+        p.k_ring[(row * p.ring + slot) * p.head_dim + d] = f32_to_bf16(k);
+        p.v_ring[(row * p.head_dim + d) * p.ring + slot] = f32_to_bf16(v);
+    }
+}
+
+// ---- quantize-and-append ----------------------------------------------------------------------------------------
+
+__device__ inline float src_elem(const KiviQuantParams& p, int b, int h, int t, int d) {
+    const int slot = p.src_ring > 0 ? t % p.src_ring : t - p.src_start;
+    return load_elem(p.src, b * p.ss_b + h * p.ss_h + static_cast<int64_t>(slot) * p.ss_t + d * p.ss_d,
+                     p.src_format);
+}
+
+__device__ inline uint8_t* page_block(const KiviQuantParams& p, int b, int h, int page) {
+    if (page >= p.bt_cols) return nullptr;
+    const int phys = p.block_table[b * p.bt_stride + page];
+    if (phys < 0 || phys >= p.num_pages) return nullptr;
+    return p.blocks + static_cast<int64_t>(phys) * p.blk_page + h * p.blk_head;
+}
+
+// (code, scale, low) arithmetic of one group: low / high in fp32, scale = fp16r((high - low) / levels).
+struct Quant {
+    float scale, low, safe;
+};
+
+__device__ inline Quant make_quant(float lo, float hi, int levels, uint32_t* overflow) {
+    Quant q;
+    q.scale = fp16_rounded(__fdiv_rn(hi - lo, static_cast<float>(levels)));
+    q.low = fp16_rounded(lo);
+    q.safe = q.scale > 0.0f ? q.scale : 1.0f;
+    if (overflow && (fabsf(q.scale) > 65504.0f || fabsf(q.low) > 65504.0f)) atomicOr(overflow, 1u);
+    return q;
+}
+
+__device__ inline uint32_t code_of(float x, const Quant& q, int levels) {
+    const float c = rintf(__fdiv_rn(x - q.low, q.safe));
+    return static_cast<uint32_t>(fminf(fmaxf(c, 0.0f), static_cast<float>(levels)));
+}
+
+// Keys: one workgroup per (row, KV head) and 32-token group in [from, to) (multiples of 32).
+__global__ __launch_bounds__(256) void kivi_quant_keys_kernel(KiviQuantParams p) {
+    __shared__ float s_low[256], s_safe[256];
+    const int row = blockIdx.x;
+    const int b = row / p.kv_heads, h = row % p.kv_heads;
+    const int page = p.from[b] / KPAGE + static_cast<int>(blockIdx.y);
+    const int t0 = page * KPAGE;
+    if (t0 + KPAGE > p.to[b]) return;
+    uint8_t* blk = page_block(p, b, h, page);
+    if (!blk) return;
+    const KiviLayout L{p.head_dim, p.bits};
+    const int levels = (1 << p.bits) - 1;
+    for (int d = threadIdx.x; d < p.head_dim; d += blockDim.x) {
+        float lo = INFINITY, hi = -INFINITY;
+        for (int t = 0; t < KPAGE; ++t) {
+            const float x = src_elem(p, b, h, t0 + t, d);
+            lo = fminf(lo, x);
+            hi = fmaxf(hi, x);
+        }
+        const Quant q = make_quant(lo, hi, levels, p.overflow);
+        s_low[d] = q.low;
+        s_safe[d] = q.safe;
+        reinterpret_cast<uint16_t*>(blk + L.k_scale())[d] = f16_bits(q.scale);
+        reinterpret_cast<uint16_t*>(blk + L.k_zero())[d] = f16_bits(q.low);
+    }
+    __syncthreads();
+    const int per_word = 32 / p.bits;
+    const int words = p.head_dim / per_word;  // per token
+    for (int item = threadIdx.x; item < KPAGE * words; item += blockDim.x) {
+        const int t = item / words, w = item % words;
+        uint32_t word = 0;
+        for (int e = 0; e < per_word; ++e) {
+            const int d = w * per_word + e;
+            const Quant q{0.0f, s_low[d], s_safe[d]};
+            word |= code_of(src_elem(p, b, h, t0 + t, d), q, levels) << (8 * (e & 3) + (e >> 2) * p.bits);
+        }
+        reinterpret_cast<uint32_t*>(blk + L.k_codes() + t * (p.head_dim * p.bits / 8))[w] = word;
+    }
+}
+
+// Values: one workgroup per (row, KV head) and page overlapping [from, to); the page's other tokens keep their codes.
+__global__ __launch_bounds__(256) void kivi_quant_values_kernel(KiviQuantParams p) {
+    __shared__ float s_low[KPAGE][8], s_safe[KPAGE][8];
+    const int row = blockIdx.x;
+    const int b = row / p.kv_heads, h = row % p.kv_heads;
+    const int page = p.from[b] / KPAGE + static_cast<int>(blockIdx.y);
+    const int t0 = page * KPAGE;
+    const int lo_t = max(p.from[b], t0), hi_t = min(p.to[b], t0 + KPAGE);
+    if (lo_t >= hi_t) return;
+    uint8_t* blk = page_block(p, b, h, page);
+    if (!blk) return;
+    const KiviLayout L{p.head_dim, p.bits};
+    const int levels = (1 << p.bits) - 1;
+    const int groups = p.head_dim / 32;
+    for (int item = threadIdx.x; item < (hi_t - lo_t) * groups; item += blockDim.x) {
+        const int t = lo_t + item / groups, grp = item % groups;
+        float lo = INFINITY, hi = -INFINITY;
+        for (int d = 32 * grp; d < 32 * grp + 32; ++d) {
+            const float x = src_elem(p, b, h, t, d);
+            lo = fminf(lo, x);
+            hi = fmaxf(hi, x);
+        }
+        const Quant q = make_quant(lo, hi, levels, p.overflow);
+        s_low[t - t0][grp] = q.low;
+        s_safe[t - t0][grp] = q.safe;
+        reinterpret_cast<uint16_t*>(blk + L.v_scale())[grp * KPAGE + (t - t0)] = f16_bits(q.scale);
+        reinterpret_cast<uint16_t*>(blk + L.v_zero())[grp * KPAGE + (t - t0)] = f16_bits(q.low);
+    }
+    __syncthreads();
+    const int per_word = 32 / p.bits;  // tokens per word
+    const int nd_count = p.head_dim / 16;
+    uint32_t* words = reinterpret_cast<uint32_t*>(blk + L.v_codes());
+    for (int item = threadIdx.x; item < p.bits * 16 * nd_count; item += blockDim.x) {
+        const int u = item / (16 * nd_count);
+        const int n = (item / nd_count) % 16;
+        const int nd = item % nd_count;
+        const int d = 16 * nd + n;
+        const int w0 = t0 + u * per_word;  // first token of the word
+        if (w0 + per_word <= lo_t || w0 >= hi_t) continue;
+        uint32_t word = words[item];
+        for (int e = 0; e < per_word; ++e) {
+            const int t = w0 + e;
+            if (t < lo_t || t >= hi_t) continue;
+            const int shift = 8 * (e & 3) + (e >> 2) * p.bits;
+            const Quant q{0.0f, s_low[t - t0][d / 32], s_safe[t - t0][d / 32]};
+            word = (word & ~(static_cast<uint32_t>(levels) << shift)) | (code_of(src_elem(p, b, h, t, d), q, levels) << shift);
+        }
+        words[item] = word;
+    }
+}
+
+// ---- attention ----------------------------------------------------------------------------------------------
+
+// Eight codes of a word, as exact fp16 values, in element order: for 4-bit codes the word's 8 elements, for 2-bit
+// codes elements 8 h .. 8 h + 7 of its 16.
+template <int BITS>
+__device__ inline f16x8 codes_to_f16(uint32_t word, int h) {
+    uint32_t lo, hi;
+    if constexpr (BITS == 4) {
+        lo = word & 0x0F0F0F0Fu;
+        hi = (word >> 4) & 0x0F0F0F0Fu;
+    } else {
+        lo = (word >> (4 * h)) & 0x03030303u;
+        hi = (word >> (4 * h + 2)) & 0x03030303u;
+    }
+    uint4 r;
+    r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, false));
+    r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, true));
+    r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, false));
+    r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, true));
+    return __builtin_bit_cast(f16x8, r);
+}
+
+// The same eight codes as fp32 values.
+template <int BITS>
+__device__ inline void codes_to_f32(uint32_t word, int h, float (&out)[8]) {
+    uint32_t lo, hi;
+    if constexpr (BITS == 4) {
+        lo = word & 0x0F0F0F0Fu;
+        hi = (word >> 4) & 0x0F0F0F0Fu;
+    } else {
+        lo = (word >> (4 * h)) & 0x03030303u;
+        hi = (word >> (4 * h + 2)) & 0x03030303u;
+    }
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, 512.0f, false);
+    const f32x2 b = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, 512.0f, true);
+    const f32x2 c = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 512.0f, false);
+    const f32x2 d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 512.0f, true);
+    out[0] = a.x;
+    out[1] = a.y;
+    out[2] = b.x;
+    out[3] = b.y;
+    out[4] = c.x;
+    out[5] = c.y;
+    out[6] = d.x;
+    out[7] = d.y;
+}
+
+__device__ inline uint32_t pack_f16x2(float a, float b) {
+    f16x2 v = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ inline uint32_t pack_bf16x2(float a, float b) {
+    return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+
+// Zeroes the fp16 / bf16 halves of x whose bit in keep (8 bits, element e = bit e) is clear.
+__device__ inline uint4 keep_halves(uint4 x, uint32_t keep) {
+    auto m = [&](int e) { return ((keep >> e) & 1u ? 0x0000FFFFu : 0u) | ((keep >> (e + 1)) & 1u ? 0xFFFF0000u : 0u); };
+    x.x &= m(0);
+    x.y &= m(2);
+    x.z &= m(4);
+    x.w &= m(6);
+    return x;
+}
+
+template <int D, int BITS>
+struct KTile {
+    static constexpr int KW = D * BITS / 128;  // words of a lane's key slice (D / 4 channels)
+    static constexpr int ND = D / 16;          // value blocks of 16 channels
+    static constexpr int KS = D / 32;          // k-steps of an S MFMA (8 channels each per lane)
+    static constexpr int VG = D / 32;          // value groups
+    uint32_t kc[2][KW];
+    uint32_t vc[ND];
+    uint4 ks[KS], kz[KS];
+    uint4 vs[VG];
+    uint4 vz;
+    int page;  // physical page (the same in every lane), -1 for none
+};
+
+template <int N>
+__device__ inline void load_words(const uint32_t* src, uint32_t (&dst)[N]) {
+    if constexpr (N % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < N; i += 4) {
+            const uint4 w = reinterpret_cast<const uint4*>(src)[i / 4];
+            dst[i] = w.x;
+            dst[i + 1] = w.y;
+            dst[i + 2] = w.z;
+            dst[i + 3] = w.w;
+        }
+    } else if constexpr (N == 2) {
+        const uint2 w = *reinterpret_cast<const uint2*>(src);
+        dst[0] = w.x;
+        dst[1] = w.y;
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) dst[i] = src[i];
+    }
+}
+
+// Issues the page loads of the tile under cursor c (the same loads in every lane and for every tile: a tile without
+// a page reads page 0 and masks it).
+template <int D, int BITS>
+__device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c, int n, int g, int lane,
+                                           PageWindow& win, KTile<D, BITS>& tile) {
+    using T = KTile<D, BITS>;
+    constexpr KiviLayout L{D, BITS};
+    ensure_window(p, c, lane, win);
+    const int phys = __builtin_amdgcn_readlane(win.physical, c.t - win.base);
+    tile.page = phys;
+    const uint8_t* blk = p.blocks + static_cast<int64_t>(phys >= 0 ? phys : 0) * p.blk_page + c.kvh * p.blk_head;
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+        const int token = 8 * (n >> 2) + 4 * v + (n & 3);
+        load_words(reinterpret_cast<const uint32_t*>(blk + L.k_codes() + token * (D * BITS / 8)) + g * T::KW,
+                   tile.kc[v]);
+    }
+    constexpr int TPW = 32 / BITS;  // tokens per value word
+    const int u = 8 * g / TPW;
+    load_words(reinterpret_cast<const uint32_t*>(blk + L.v_codes()) + (u * 16 + n) * T::ND, tile.vc);
+#pragma unroll
+    for (int j = 0; j < T::KS; ++j) {
+        tile.ks[j] = *reinterpret_cast<const uint4*>(blk + L.k_scale() + (g * (D / 4) + 8 * j) * 2);
+        tile.kz[j] = *reinterpret_cast<const uint4*>(blk + L.k_zero() + (g * (D / 4) + 8 * j) * 2);
+    }
+#pragma unroll
+    for (int grp = 0; grp < T::VG; ++grp)
+        tile.vs[grp] = *reinterpret_cast<const uint4*>(blk + L.v_scale() + (grp * 32 + 8 * g) * 2);
+    tile.vz = *reinterpret_cast<const uint4*>(blk + L.v_zero() + ((n % T::VG) * 32 + 8 * g) * 2);
+}
+
+}  // namespace
+
+template <int D, int BITS, int NB, int NBUF>
+__global__ __launch_bounds__(64) void kivi_attention_kernel(KiviParams p) {
+    using T = KTile<D, BITS>;
+    constexpr int KS = T::KS, ND = T::ND, VG = T::VG;
+    constexpr int R = NB * 16;  // query rows of the MFMA columns
+    __shared__ uint4 q_bf[R][D / 8];
+
+    const int lane = threadIdx.x;
+    const int n = lane & 15;
+    const int g = lane >> 4;
+    const int w = blockIdx.x;
+    const int grid = gridDim.x;
+
+    const int64_t total = uniform64(total_tiles(p, lane));
+    for (int b = w; b < p.batch; b += grid) {  // rows without a key: zeros
+        if (row_of(p, b).tiles == 0)
+            for (int idx = lane; idx < p.kv_heads * p.rows * D; idx += 64)
+                store_output(p, b, idx / (p.rows * D), (idx / D) % p.rows, idx % D, 0.0f, -INFINITY, 0.0f);
+    }
+    const int64_t lo = total * w / grid;
+    const int64_t hi = total * (w + 1) / grid;
+    if (lo >= hi) return;
+
+    // ---- row state ----
+    float limit[NB];
+    int all_see = 0, kq = 0, vq = 0, row_len = 0;
+    float m_i[NB], l_i[NB];
+    f32x4 acc[ND][NB], gam[NB];
+
+    auto begin_row = [&](const Cursor& c) __attribute__((always_inline)) {
+        // the row's query rows into LDS (rows past the group are zero); the loads wait here, once per row, outside the
+        // tile pipeline
+        for (int i = lane; i < R * (D / 8); i += 64) {
+            const int r = i / (D / 8), k = i % (D / 8);
+            uint4 x = make_uint4(0, 0, 0, 0);
+            if (r < p.rows) {
+                const int gq = r / p.queries, qi = r % p.queries;
+                x = *reinterpret_cast<const uint4*>(p.q + c.b * p.sq_b + qi * p.sq_q +
+                                                    (c.kvh * p.groups + gq) * p.sq_h + 8 * k);
+            }
+            q_bf[r][k] = x;
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        kq = scalar_load(p.keys_quantized, c.b);
+        vq = scalar_load(p.values_quantized, c.b);
+        row_len = c.row.len;
+        all_see = c.row.len - p.queries + 1;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const int r = nb * 16 + n;
+            limit[nb] = r < p.rows ? static_cast<float>(c.row.len - p.queries + r % p.queries + 1) : 0.0f;
+            m_i[nb] = -INFINITY;
+            l_i[nb] = 0.0f;
+            gam[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    };
+    const float score_scale = p.softcap > 0.0f ? p.scale : p.scale * kLog2e;
+
+    // ---- one tile (32 tokens) of the online softmax ----
+    auto compute = [&](const T& tile, const Cursor& c) __attribute__((always_inline)) {
+        const int t0 = KPAGE * c.t;
+        const bool valid = tile.page >= 0;
+        f32x4 s[2][NB];
+        // keys from codes, dequantized as the reference does (code * scale + zero in fp32, two roundings, then bf16;
+        // attention/kivi.py:56-76), so that the scores see the reference's key values exactly
+#pragma unroll
+        for (int v = 0; v < 2; ++v)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) s[v][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (t0 < kq) {
+#pragma unroll
+            for (int j = 0; j < KS; ++j) {
+                const f16x8 sh = __builtin_bit_cast(f16x8, tile.ks[j]);
+                const f16x8 zh = __builtin_bit_cast(f16x8, tile.kz[j]);
+                float sf[8], zf[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    sf[e] = static_cast<float>(sh[e]);
+                    zf[e] = static_cast<float>(zh[e]);
+                }
+#pragma unroll
+                for (int v = 0; v < 2; ++v) {
+                    float c8[8];
+                    codes_to_f32<BITS>(BITS == 4 ? tile.kc[v][j] : tile.kc[v][j / 2], j % 2, c8);
+                    bf16x8 kv;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) kv[e] = static_cast<__bf16>(c8[e] * sf[e] + zf[e]);
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb)
+                        s[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            kv, __builtin_bit_cast(bf16x8, q_bf[nb * 16 + n][g * (D / 32) + j]), s[v][nb], 0, 0, 0);
+                }
+            }
+        }
+        // keys from the ring (tokens at or past kq)
+        if (t0 + KPAGE > kq) {
+            uint4 kr[2][KS];
+#pragma unroll
+            for (int v = 0; v < 2; ++v) {
+                const int token = t0 + 8 * (n >> 2) + 4 * v + (n & 3);
+                const uint16_t* src = p.k_ring + (static_cast<int64_t>(c.b) * p.kv_heads + c.kvh) * p.ring * D +
+                                      static_cast<int64_t>(token % p.ring) * D + g * (D / 4);
+#pragma unroll
+                for (int j = 0; j < KS; ++j) kr[v][j] = *reinterpret_cast<const uint4*>(src + 8 * j);
+            }
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the ring loads of this rare branch
+            f32x4 sd[2][NB];
+#pragma unroll
+            for (int v = 0; v < 2; ++v)
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    sd[v][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                    for (int j = 0; j < KS; ++j)
+                        sd[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8, kr[v][j]),
+                            __builtin_bit_cast(bf16x8, q_bf[nb * 16 + n][g * (D / 32) + j]), sd[v][nb], 0, 0, 0);
+                }
+#pragma unroll
+            for (int v = 0; v < 2; ++v)
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int token = t0 + 8 * g + 4 * v + i;
+                        if (t0 >= kq || token >= kq) s[v][nb][i] = sd[v][nb][i];
+                    }
+        }
+        // scores in log2 units; masking where the tile holds a row's end, a causal limit or a missing page
+#pragma unroll
+        for (int v = 0; v < 2; ++v)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s[v][nb][i] *= score_scale;
+        if (p.softcap > 0.0f) {
+#pragma unroll
+            for (int v = 0; v < 2; ++v)
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float t = s[v][nb][i] / p.softcap;
+                        const float e = __expf(-2.0f * fabsf(t));
+                        const float th = (1.0f - e) / (1.0f + e);
+                        s[v][nb][i] = p.softcap * (t < 0.0f ? -th : th) * kLog2e;
+                    }
+        }
+        if (t0 + KPAGE > all_see || (!valid && t0 < kq)) {
+#pragma unroll
+            for (int v = 0; v < 2; ++v)
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int token = t0 + 8 * g + 4 * v + i;
+                        const bool ok = static_cast<float>(token) < limit[nb] && (valid || token >= kq);
+                        s[v][nb][i] = ok ? s[v][nb][i] : -INFINITY;
+                    }
+        }
+        // online softmax with lazy rescaling (the reference maximum moves when a score exceeds it by 2^8)
+        float pw[NB][8];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            float tile_max = -INFINITY;
+#pragma unroll
+            for (int v = 0; v < 2; ++v)
+                tile_max = fmaxf(fmaxf(tile_max, fmaxf(s[v][nb][0], s[v][nb][1])), fmaxf(s[v][nb][2], s[v][nb][3]));
+            tile_max = group_max(tile_max);
+            if (__ballot(tile_max > m_i[nb] + 8.0f) != 0) {
+                const float m_new = fmaxf(m_i[nb], tile_max);
+                const float alpha = m_i[nb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_i[nb] - m_new);
+                l_i[nb] *= alpha;
+                gam[nb] *= alpha;
+#pragma unroll
+                for (int nd = 0; nd < ND; ++nd) acc[nd][nb] *= alpha;
+                m_i[nb] = m_new;
+            }
+            const float neg_m = m_i[nb] == -INFINITY ? 0.0f : -m_i[nb];
+            float sum = 0.0f;
+#pragma unroll
+            for (int v = 0; v < 2; ++v)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    pw[nb][4 * v + i] = __builtin_amdgcn_exp2f(s[v][nb][i] + neg_m);
+                    sum += pw[nb][4 * v + i];
+                }
+            l_i[nb] += group_sum(sum);
+        }
+        // values: element e of the lane's operands is token t0 + 8 g + e
+        const int tok0 = t0 + 8 * g;
+        if (t0 < vq) {  // from codes: O += codes . (p * s) + z . p
+            uint32_t keep = 0xFFu;
+            if (t0 + KPAGE > vq || !valid)
+                keep = valid ? (vq - tok0 >= 8 ? 0xFFu : (vq > tok0 ? (1u << (vq - tok0)) - 1u : 0u)) : 0u;
+            f16x8 pp[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                uint4 w4;
+                w4.x = pack_f16x2(pw[nb][0], pw[nb][1]);
+                w4.y = pack_f16x2(pw[nb][2], pw[nb][3]);
+                w4.z = pack_f16x2(pw[nb][4], pw[nb][5]);
+                w4.w = pack_f16x2(pw[nb][6], pw[nb][7]);
+                pp[nb] = __builtin_bit_cast(f16x8, keep_halves(w4, keep));
+            }
+#pragma unroll
+            for (int grp = 0; grp < VG; ++grp) {
+                f16x8 ps[NB];
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    ps[nb] = __builtin_bit_cast(
+                        f16x8, keep_halves(__builtin_bit_cast(uint4, pp[nb] * __builtin_bit_cast(f16x8, tile.vs[grp])),
+                                           keep));
+#pragma unroll
+                for (int nd = 2 * grp; nd < 2 * grp + 2; ++nd) {
+                    const f16x8 a = BITS == 4 ? codes_to_f16<BITS>(tile.vc[nd], 0)
+                                              : codes_to_f16<BITS>(tile.vc[nd], g & 1);
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb)
+                        acc[nd][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ps[nb], acc[nd][nb], 0, 0, 0);
+                }
+            }
+            const f16x8 z = __builtin_bit_cast(f16x8, keep_halves(tile.vz, keep));
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) gam[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(z, pp[nb], gam[nb], 0, 0, 0);
+        }
+        if (t0 + KPAGE > vq) {  // from the ring (tokens at or past vq, below the row's end)
+            const int from = max(vq - tok0, 0), to = min(row_len - tok0, 8);
+            const uint32_t keep = to > from ? ((to >= 8 ? 0xFFu : (1u << to) - 1u) & ~((1u << from) - 1u)) : 0u;
+            uint4 vr[ND];
+            const int slot = tok0 % p.ring;
+#pragma unroll
+            for (int nd = 0; nd < ND; ++nd)
+                vr[nd] = *reinterpret_cast<const uint4*>(
+                    p.v_ring + ((static_cast<int64_t>(c.b) * p.kv_heads + c.kvh) * D + 16 * nd + n) * p.ring + slot);
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the ring loads of this rare branch
+            bf16x8 phi[NB], plo[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                float pv[8], lo8[8];
+                uint32_t hw[4], lw[4];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) pv[e] = (keep >> e) & 1u ? pw[nb][e] : 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) hw[e] = pack_bf16x2(pv[2 * e], pv[2 * e + 1]);
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    lo8[e] = pv[e] - bits_f32(e & 1 ? hw[e >> 1] & 0xFFFF0000u : hw[e >> 1] << 16);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) lw[e] = pack_bf16x2(lo8[2 * e], lo8[2 * e + 1]);
+                phi[nb] = __builtin_bit_cast(bf16x8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+                plo[nb] = __builtin_bit_cast(bf16x8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+            }
+#pragma unroll
+            for (int nd = 0; nd < ND; ++nd) {
+                const bf16x8 a = __builtin_bit_cast(bf16x8, keep_halves(vr[nd], keep));
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) {
+                    acc[nd][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, phi[nb], acc[nd][nb], 0, 0, 0);
+                    acc[nd][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, plo[nb], acc[nd][nb], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // ---- end of a row segment: direct output, or a partial and (for the last wave of the row) the merge ----
+    auto finish = [&](const Cursor& c, int64_t seg_begin, int64_t seg_end, bool first_segment) __attribute__((always_inline)) {
+        // the value zero-point term of channel 16 nd + 4 g + i: row (group (16 nd) / 32) of the gamma tile, held by
+        // lane group 0, column n
+        float o[ND][NB][4];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int nd = 0; nd < ND; ++nd) {
+                const float z = __shfl(gam[nb][(nd / 2) & 3], n);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[nd][nb][i] = acc[nd][nb][i] + z;
+            }
+        const int64_t row_end = c.row_start + c.row.tiles;
+        if (seg_begin == c.row_start && seg_end == row_end) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const int r = nb * 16 + n;
+                if (r >= p.rows) continue;
+#pragma unroll
+                for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        store_output(p, c.b, c.kvh, r, 16 * nd + 4 * g + i, o[nd][nb][i], m_i[nb], l_i[nb]);
+            }
+            return;
+        }
+        const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
+        float* slot = p.part + (2 * static_cast<int64_t>(w) + (first_segment ? 0 : 1)) * stride;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            const int r = nb * 16 + n;
+            if (r >= p.rows) continue;
+            if (g == 0) {
+                coherent_store(slot + r, m_i[nb]);
+                coherent_store(slot + p.rows + r, l_i[nb]);
+            }
+#pragma unroll
+            for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    coherent_store(slot + 2 * p.rows + r * D + 16 * nd + 4 * g + i, o[nd][nb][i]);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        int prev = 0;
+        if (lane == 0)
+            prev = __hip_atomic_fetch_add(p.counters + c.b * p.kv_heads + c.kvh, 1, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+        merge_row<D>(p, c, __shfl(prev, 0), total, grid, lane);
+    };
+
+    // ---- the tile pipeline (as in paged_attention.hip) ----
+    Cursor cur = locate(p, lo, lane);
+    PageWindow win;
+    int64_t seg_begin = lo;
+    bool first_segment = true;
+    begin_row(cur);
+
+    T bufs[NBUF];
+    Cursor cs[NBUF];
+    Cursor icur = cur;
+    int64_t ipos = lo;
+    auto issue_next = [&](T& buf, Cursor& slot) __attribute__((always_inline)) {
+        issue_tile<D, BITS>(p, icur, n, g, lane, win, buf);
+        slot = icur;
+        if (ipos < hi) {
+            if (ipos + 1 < hi) advance(p, icur);
+            ++ipos;
+        }
+    };
+#pragma unroll
+    for (int s = 0; s + 1 < NBUF; ++s) issue_next(bufs[s], cs[s]);
+
+    int64_t pos = lo;
+    auto step = [&](auto tag) __attribute__((always_inline)) -> bool {
+        constexpr int I = decltype(tag)::value;
+        constexpr int J = (I + NBUF - 1) % NBUF;
+        issue_next(bufs[J], cs[J]);
+        cur = cs[I];
+        if (cur.t == 0 && pos != lo) begin_row(cur);
+        compute(bufs[I], cur);
+        const bool more = pos + 1 < hi;
+        if (cur.t + 1 == cur.row.tiles || !more) {
+            finish(cur, seg_begin, pos + 1, first_segment);
+            first_segment = false;
+            seg_begin = pos + 1;
+        }
+        ++pos;
+        return more;
+    };
+    if constexpr (NBUF == 1) {
+        while (step(std::integral_constant<int, 0>{})) {
+        }
+    } else {
+        static_assert(NBUF == 2, "one or two tile buffers");
+        while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{})) {
+        }
+    }
+}
+
+// ---- host side ----------------------------------------------------------------------------------------------
+
+namespace {
+
+template <int D, int BITS, int NB>
+auto kivi_kernel_of() {
+    if constexpr (NB == 1) return kivi_attention_kernel<D, BITS, NB, 2>;
+    return kivi_attention_kernel<D, BITS, NB, 1>;
+}
+
+template <typename F>
+int kivi_dispatch(int head_dim, int bits, int rows, const F& f) {
+    const int nb = (rows + 15) / 16;
+    auto by_nb = [&](auto d_tag, auto b_tag) -> int {
+        constexpr int D = decltype(d_tag)::value;
+        constexpr int BITS = decltype(b_tag)::value;
+        if (nb == 1) return f.template run<D, BITS, 1>();
+        if (nb == 2) return f.template run<D, BITS, 2>();
+        if (nb <= 4) return f.template run<D, BITS, 4>();
+        return fail("kivi decode attention takes at most 64 query rows per KV head");
+    };
+    auto by_bits = [&](auto d_tag) -> int {
+        if (bits == 2) return by_nb(d_tag, std::integral_constant<int, 2>{});
+        if (bits == 4) return by_nb(d_tag, std::integral_constant<int, 4>{});
+        return fail("kivi decode attention supports 2- and 4-bit codes");
+    };
+    if (head_dim == 64) return by_bits(std::integral_constant<int, 64>{});
+    if (head_dim == 128) return by_bits(std::integral_constant<int, 128>{});
+    return fail("kivi decode attention supports head dims 64 and 128");
+}
+
+struct KiviLaunch {
+    hipStream_t stream;
+    const KiviParams* p;
+    template <int D, int BITS, int NB>
+    int run() const {
+        const auto kernel = kivi_kernel_of<D, BITS, NB>();
+        hipLaunchKernelGGL(kernel, dim3(p->grid), dim3(64), 0, stream, *p);
+        return check_launch("kivi_attention_kernel");
+    }
+};
+
+struct KiviOccupancy {
+    int* per_cu;
+    template <int D, int BITS, int NB>
+    int run() const {
+        int blocks = 0;
+        const auto kernel = kivi_kernel_of<D, BITS, NB>();
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, 64, 0) != hipSuccess || blocks <= 0)
+            blocks = 1;
+        *per_cu = blocks;
+        return 0;
+    }
+};
+
+}  // namespace
+
+int kivi_schedule(const int32_t* committed, int residual, int32_t* keys_quantized, int32_t* values_quantized,
+                  int32_t* ranges, int batch, hipStream_t stream) {
+    hipLaunchKernelGGL(kivi_schedule_kernel, dim3((batch + 255) / 256), dim3(256), 0, stream, committed, residual,
+                       keys_quantized, values_quantized, ranges, batch);
+    return check_launch("kivi_schedule_kernel");
+}
+
+int kivi_ring_write(const KiviRingParams& p, hipStream_t stream) {
+    if (p.tokens == 0) return 0;
+    hipLaunchKernelGGL(kivi_ring_kernel, dim3(p.tokens), dim3(256), 0, stream, p);
+    return check_launch("kivi_ring_kernel");
+}
+
+int kivi_quantize(const KiviQuantParams& p, int kind, int max_tokens, hipStream_t stream) {
+    const int pages = (max_tokens + KPAGE - 1) / KPAGE + 1;  // a range need not start at a page boundary
+    dim3 grid(p.batch * p.kv_heads, pages);
+    if (kind == 0)
+        hipLaunchKernelGGL(kivi_quant_keys_kernel, grid, dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(kivi_quant_values_kernel, grid, dim3(256), 0, stream, p);
+    return check_launch(kind == 0 ? "kivi_quant_keys_kernel" : "kivi_quant_values_kernel");
+}
+
+int kivi_resident_waves(int head_dim, int bits, int rows, int* per_cu) {
+    return kivi_dispatch(head_dim, bits, rows, KiviOccupancy{per_cu});
+}
+
+int kivi_attention(const KiviParams& p, hipStream_t stream) {
+    return kivi_dispatch(p.head_dim, p.bits, p.rows, KiviLaunch{stream, &p});
+}
+
+}  // namespace eco

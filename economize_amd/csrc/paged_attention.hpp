@@ -10,6 +10,9 @@ namespace eco {
 // each of the n_sel listed pages (listed page e covers logical cache pages e * span .. e * span + span - 1; -1 for
 // none), followed by the dense tail, logical cache pages done[b] * span .. ceil(len / 16) - 1.
 struct PagedParams {
+    static constexpr int kPage = 16;   // tokens per cache page
+    static constexpr int kTile = 4;    // cache pages per tile
+    static constexpr bool kPageList = true;
     const uint16_t* q;  // bf16 [B, Q, Hq, D], channel stride 1
     int64_t sq_b, sq_q, sq_h;
     const uint8_t* k_cache;  // [pages, Hkv, D / X, 16, X]

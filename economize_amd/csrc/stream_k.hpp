@@ -1,0 +1,298 @@
+// The stream-K machinery shared by the decode-attention kernels (paged_attention.hip, kivi.hip): the geometry of a
+// row's tiles, the cursor over the sequence of every (row, KV head)'s tiles, the per-lane window of page ids, the
+// output store with attention sinks, and the merge of the partials of a row cut between waves.
+//
+// A params type P provides: kPage (tokens per cache page), kTile (cache pages per tile), kPageList (whether it takes a
+// Quest page list); the fields batch, kv_heads, rows, queries, groups, seq_lens, bt_cols, block_table, bt_stride,
+// num_pages, sinks, out, so_b, so_q, so_h, counters, part; and, with kPageList, page_list, pl_b, pl_h, n_sel, span,
+// done.
+#pragma once
+
+#include "common.hpp"
+
+namespace eco {
+namespace {
+
+// Device-coherent (agent-scope) store and load of partials: they bypass the caches that are not coherent across the
+// chip's XCDs (gfx950 lowers them to global_store / global_load with sc1), so no L2 writeback or invalidation is
+// needed to hand a partial from one workgroup to another.
+__device__ inline void coherent_store(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline float coherent_load(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline int64_t wave_sum(int64_t x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+    return x;
+}
+
+__device__ inline float wave_sum_f(float x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+    return x;
+}
+
+__device__ inline float wave_max(float x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+    return x;
+}
+
+__device__ inline int64_t wave_inclusive_sum(int64_t x, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int64_t y = __shfl_up(x, off);
+        if (lane >= off) x += y;
+    }
+    return x;
+}
+
+__device__ inline int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// ptr[index] for a wave-uniform index through the scalar cache (a scalar load waits on its own counter, not on the
+// vector loads in flight). Only for data no kernel of the call writes.
+template <typename T>
+__device__ inline T scalar_load(const T* ptr, int index) {
+    return ((const __attribute__((address_space(4))) T*)ptr)[uniform(index)];
+}
+
+__device__ inline int64_t uniform64(int64_t x) {
+    const uint64_t u = static_cast<uint64_t>(x);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Geometry of batch row b: tokens (cut at the block table's reach), where a page list's dense tail starts, and
+// its virtual pages and tiles (the same for every KV head). UNIFORM: b is the same in every lane (scalar loads).
+struct Row {
+    int len, done, n_virt, tiles;
+};
+
+template <bool UNIFORM = false, typename P>
+__device__ inline Row row_of(const P& p, int b) {
+    Row r;
+    const int len = UNIFORM ? scalar_load(p.seq_lens, b) : p.seq_lens[b];
+    r.len = min(max(len, 0), p.bt_cols * P::kPage);
+    const int pages = (r.len + P::kPage - 1) / P::kPage;
+    r.done = 0;
+    r.n_virt = pages;
+    if constexpr (P::kPageList) {
+        if (p.page_list != nullptr) {
+            const int done = UNIFORM ? scalar_load(p.done, b) : p.done[b];
+            r.done = min(max(done, 0) * p.span, pages);
+            r.n_virt = p.n_sel * p.span + pages - r.done;
+        }
+    }
+    r.tiles = (r.n_virt + P::kTile - 1) / P::kTile;
+    return r;
+}
+
+// Logical page of virtual page v of a row, -1 when it holds nothing (past the row, an unselected list entry, or a
+// listed page that is not committed).
+template <typename P>
+__device__ inline int logical_page(const P& p, const Row& row, int b, int kvh, int v) {
+    if (v >= row.n_virt) return -1;
+    if constexpr (P::kPageList) {
+        if (p.page_list == nullptr) return v;
+        const int listed = p.n_sel * p.span;
+        if (v < listed) {
+            const int entry = p.page_list[b * p.pl_b + kvh * p.pl_h + v / p.span];
+            const int page = entry * p.span + v % p.span;
+            return entry >= 0 && page < row.done ? page : -1;
+        }
+        return row.done + (v - listed);
+    } else {
+        return v;
+    }
+}
+
+// Position in the tile sequence: row (b, kvh), its tile t, and the sequence offset of the row's first tile.
+struct Cursor {
+    int b, kvh, t;
+    Row row;
+    int64_t row_start;
+};
+
+template <typename P>
+__device__ inline int64_t total_tiles(const P& p, int lane) {
+    int64_t total = 0;
+    for (int b0 = 0; b0 < p.batch; b0 += 64) {
+        const int b = b0 + lane;
+        total += wave_sum(b < p.batch ? row_of(p, b).tiles : 0);
+    }
+    return total * p.kv_heads;
+}
+
+// The cursor of sequence offset x < total_tiles.
+template <typename P>
+__device__ inline Cursor locate(const P& p, int64_t x, int lane) {
+    Cursor c{};
+    int64_t base = 0;
+    for (int b0 = 0; b0 < p.batch; b0 += 64) {
+        const int b = b0 + lane;
+        const int tiles = b < p.batch ? row_of(p, b).tiles : 0;
+        const int64_t incl = wave_inclusive_sum(static_cast<int64_t>(tiles) * p.kv_heads, lane);
+        const int64_t chunk = __shfl(incl, 63);
+        if (x < base + chunk) {
+            const int src = __builtin_ctzll(__ballot(base + incl > x));
+            c.b = uniform(b0 + src);
+            c.row = row_of(p, c.b);
+            c.row.len = uniform(c.row.len);
+            c.row.done = uniform(c.row.done);
+            c.row.n_virt = uniform(c.row.n_virt);
+            c.row.tiles = uniform(c.row.tiles);
+            const int64_t start_b =
+                uniform64(base + __shfl(incl, src) - static_cast<int64_t>(c.row.tiles) * p.kv_heads);
+            const int64_t off = x - start_b;
+            c.kvh = uniform(static_cast<int>(off / c.row.tiles));
+            c.t = uniform(static_cast<int>(off % c.row.tiles));
+            c.row_start = uniform64(start_b + static_cast<int64_t>(c.kvh) * c.row.tiles);
+            return c;
+        }
+        base += chunk;
+    }
+    return c;
+}
+
+// The next tile (called only when one exists).
+template <typename P>
+__device__ inline void advance(const P& p, Cursor& c) {
+    if (++c.t < c.row.tiles) return;
+    c.row_start += c.row.tiles;
+    c.t = 0;
+    if (++c.kvh < p.kv_heads) return;
+    c.kvh = 0;
+    do {
+        c.b = uniform(c.b + 1);
+        c.row = row_of<true>(p, c.b);
+        c.row.len = uniform(c.row.len);
+        c.row.done = uniform(c.row.done);
+        c.row.n_virt = uniform(c.row.n_virt);
+        c.row.tiles = uniform(c.row.tiles);
+    } while (c.row.tiles == 0 && c.b + 1 < p.batch);
+}
+
+// The wave whose range holds sequence offset x.
+__device__ inline int wave_of(int64_t x, int64_t total, int grid) {
+    return static_cast<int>(((x + 1) * grid - 1) / total);
+}
+
+// out[b, qi, h, d] of query row r from its merged (acc, max, sum) in log2 units, with the sink logit of head h in
+// the denominator (attention/_decode_kernels.py:216-226): zeros for a row that sees nothing.
+template <typename P>
+__device__ inline void store_output(const P& p, int b, int kvh, int r, int d, float o, float m, float l) {
+    const int gq = r / p.queries;
+    const int qi = r % p.queries;
+    const int h = kvh * p.groups + gq;
+    if (p.sinks) {
+        const float sink = p.sinks[h] * kLog2e;
+        const float m_new = fmaxf(m, sink);
+        const float a = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - m_new);
+        o *= a;
+        l = l * a + __builtin_amdgcn_exp2f(sink - m_new);
+    }
+    const float out = l > 0.0f ? o / fmaxf(l, 1e-30f) : 0.0f;
+    p.out[b * p.so_b + qi * p.so_q + h * p.so_h + d] = f32_to_bf16(out);
+}
+
+// Page ids of 64 consecutive virtual pages of one (b, kvh) row, one per lane: lane i holds the logical page and the
+// cache page of virtual page base + i (-1 when it holds nothing). A tile's K/V addresses then come from a lane
+// shuffle instead of a block-table load issued right before the K/V loads (whose latency the loads would wait out,
+// and, since loads retire in order, with them every load in flight). The window is reloaded once per 16 tiles.
+struct PageWindow {
+    int b = -1, kvh = -1, base = 0;
+    int logical = -1, physical = -1;
+};
+
+template <typename P>
+__device__ __forceinline__ void ensure_window(const P& p, const Cursor& c, int lane, PageWindow& win) {
+    const int first = P::kTile * c.t;
+    if (c.b == win.b && c.kvh == win.kvh && first >= win.base && first + P::kTile <= win.base + 64) return;
+    win.b = c.b;
+    win.kvh = c.kvh;
+    win.base = first;
+    const int lp = logical_page(p, c.row, c.b, c.kvh, first + lane);
+    int pp = lp >= 0 ? p.block_table[c.b * p.bt_stride + lp] : -1;
+    pp = pp < p.num_pages ? pp : -1;  // a table entry outside the cache reads nothing
+    win.logical = pp >= 0 ? lp : -1;
+    win.physical = pp;
+    // wait here for the table load (vmcnt(0)), so that the common path, which reloads nothing, does not wait at
+    // the branch's join for every load in flight
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+}
+
+// The merge of a row's partials by the last of its waves to finish: per query row, the maximum and the weighted sum
+// over the partials (lanes over partials), then the weighted accumulators (lanes over channels). Returns without
+// merging when other partials of the row are still outstanding.
+template <int D, typename P>
+__device__ inline void merge_row(const P& p, const Cursor& c, int prev, int64_t total, int grid,
+                                       int lane) {
+    const int64_t row_end = c.row_start + c.row.tiles;
+    const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
+    int32_t* counter = p.counters + c.b * p.kv_heads + c.kvh;
+        // the waves holding part of the row (a wave's range is empty only when there are fewer tiles than waves)
+        const int w_first = wave_of(c.row_start, total, grid);
+        const int w_last = wave_of(row_end - 1, total, grid);
+        auto holds = [&](int k) __attribute__((always_inline)) { return total * k / grid < total * (k + 1) / grid; };
+        auto slot_of = [&](int k) __attribute__((always_inline)) {
+            return p.part + (2 * static_cast<int64_t>(k) + (total * k / grid < c.row_start ? 1 : 0)) * stride;
+        };
+        int parts = 0;
+        for (int k = w_first + lane; k <= w_last; k += 64) parts += holds(k) ? 1 : 0;
+        parts = static_cast<int>(wave_sum(parts));
+        if (prev != parts - 1) return;
+        // lane-owned runs of 8 channels of one query row; the partials are folded in batches of 4 with an online
+        // log-sum-exp, the batch's loads all in flight together
+        for (int base = 0; base < p.rows * D; base += 64 * 8) {
+            const int e = base + lane * 8;
+            const bool active = e < p.rows * D;
+            const int r = active ? e / D : 0;
+            const int d = active ? e % D : 0;
+            float m_run = -INFINITY, l_run = 0.0f, o_run[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o_run[i] = 0.0f;
+            for (int k0 = w_first; k0 <= w_last; k0 += 4) {
+                float mk[4], lk[4], ok[4][8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int k = k0 + j;
+                    const bool use = active && k <= w_last && holds(k);
+                    const float* sk = slot_of(use ? k : w_first);
+                    mk[j] = use ? coherent_load(sk + r) : -INFINITY;
+                    lk[j] = use ? coherent_load(sk + p.rows + r) : 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) ok[j][i] = use ? coherent_load(sk + 2 * p.rows + r * D + d + i) : 0.0f;
+                }
+                float m_new = m_run;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) m_new = fmaxf(m_new, mk[j]);
+                if (m_new == -INFINITY) continue;
+                const float a = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+                l_run *= a;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o_run[i] *= a;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (mk[j] == -INFINITY) continue;
+                    const float cw = __builtin_amdgcn_exp2f(mk[j] - m_new);
+                    l_run += lk[j] * cw;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o_run[i] += ok[j][i] * cw;
+                }
+                m_run = m_new;
+            }
+            if (active)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) store_output(p, c.b, c.kvh, r, d + i, o_run[i], m_run, l_run);
+        }
+        if (lane == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+
+}  // namespace
+}  // namespace eco

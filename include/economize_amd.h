@@ -108,6 +108,60 @@ int eco_quest_select(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
                      int32_t* out, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
                      int32_t head_dim, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- KIVI (2- and 4-bit KV codes) --------------------------------------------------------------------------
+ * Paged KIVI cache, per layer: blocks [num_pages, Hkv, eco_kivi_block_bytes] (one block per 32-token page and KV
+ * head: key codes, value codes, key scales and zero points per channel of the page's 32-token key group, value scales
+ * and zero points per token and 32-channel group; fp16), and the full-precision residual of every row in two bf16
+ * rings of W slots (token t at slot t % W): keys [B, Hkv, W, D], values [B, Hkv, D, W]. Keys below
+ * keys_quantized[b] and values below values_quantized[b] (int32 [B] on the device) are read from the pages, the
+ * others from the rings. Row b's token t lives in page block_table[b * bt_stride + t / 32]. */
+
+/* Bytes of one (page, KV head) block (0 for an unsupported shape: head dim 64 or 128, 2 or 4 bits, group 32). */
+size_t eco_kivi_block_bytes(int32_t head_dim, int32_t bits, int32_t group);
+
+/* The reference's KIVI schedule (techniques/kv_quant/kivi.py:230-243) on the device: with committed[b] tokens, keys
+ * below (c / residual) * residual and values below max(0, c - residual) are quantized. Writes ranges int32 [4, B]
+ * (keys from, keys to, values from, values to: what to quantize now) and advances keys_quantized / values_quantized. */
+int eco_kivi_schedule(const int32_t* committed, int32_t residual, int32_t group, int32_t* keys_quantized,
+                      int32_t* values_quantized, int32_t* ranges, int32_t batch, void* stream);
+
+/* KIVI quantize-and-append: quantizes tokens [from[b], to[b]) of every row into its pages, keys (kind 0, per channel
+ * over 32-token groups; from and to multiples of 32) or values (kind 1, per token over 32-channel groups). The source
+ * element (b, h, t, d) is at src + b * ss_b + h * ss_h + slot * ss_t + d * ss_d (elements of src_format), slot =
+ * t - src_start, or t % src_ring with a ring. max_tokens bounds to - from over the rows (it sizes the launch). A scale
+ * or zero point beyond fp16 sets *overflow (optional). Replaces quantize / pack_codes as FusedKIVICache._quantize_block
+ * and the paged _quantize_kernel call them (techniques/kv_quant/kivi.py:121-140, attention/kivi.py:38-45,
+ * techniques/kv_kivi_fused/fused.py:152-175, backends/vllm/kivi/kernels.py:94-207). */
+int eco_kivi_quantize(int32_t kind, const void* src, int32_t src_format, int64_t ss_b, int64_t ss_h, int64_t ss_t,
+                      int64_t ss_d, int32_t src_start, int32_t src_ring, const int32_t* from, const int32_t* to,
+                      void* blocks, int32_t num_pages, const int32_t* block_table, int64_t bt_stride,
+                      int32_t bt_cols, int32_t batch, int32_t kv_heads, int32_t head_dim, int32_t bits,
+                      int32_t group, int32_t max_tokens, uint32_t* overflow, void* stream);
+
+/* Writes new tokens k_new / v_new [T, Hkv, D] (element strides, channel stride 1) into the rings at slot
+ * positions[t] % ring of row rows[t] (negative positions skip), rounded to bf16 (the reference's ring writes,
+ * kv_quant/packed.py:258-277). */
+int eco_kivi_ring_write(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
+                        int64_t sv_t, int64_t sv_h, const int32_t* rows, const int32_t* positions, int32_t tokens,
+                        void* k_ring, void* v_ring, int32_t batch, int32_t kv_heads, int32_t head_dim, int32_t ring,
+                        void* stream);
+
+/* Workspace bytes eco_kivi_decode needs (zero before its first use; every call leaves its counters zero). */
+size_t eco_kivi_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
+                                      int32_t head_dim, int32_t max_seq_len, int32_t bits);
+
+/* Decode attention over the paged KIVI cache and the rings: as eco_paged_decode (query [B, Q, Hq, D] bf16, out
+ * [B, Q, Hq, D] bf16, causal over the last Q of seq_lens[b] tokens, soft cap, sinks), with keys below
+ * keys_quantized[b] and values below values_quantized[b] read as codes. Replaces kivi_decode_attention
+ * (attention/kivi.py:199-309) and paged_kivi_attention (backends/vllm/kivi/kernels.py:354-415). */
+int eco_kivi_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* blocks, int32_t num_pages,
+                    const void* k_ring, const void* v_ring, int32_t ring, const int32_t* keys_quantized,
+                    const int32_t* values_quantized, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                    const int32_t* seq_lens, const float* sinks, void* out, int64_t so_b, int64_t so_q, int64_t so_h,
+                    int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                    int32_t bits, int32_t group, int32_t max_seq_len, float scale, float softcap, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,204 @@
+"""Parity of the KIVI kernels with the oracle on the GPU.
+
+* quantize-and-append: the page blocks (codes, fp16 scales and zero points) bit-exact against the oracle's
+  restatement of the reference's ``quantize`` (techniques/kv_quant/kivi.py:121-140) laid out in the paged format
+  (oracle/kivi_paged.py), for prompts and for the decode-time schedule (kivi.py:230-243) run step by step;
+* decode attention within atol 2e-3 / rtol 1e-2 of the fp32 definition (attention/decode.py:66-103) over the values
+  the reference's ``dequantize`` gives (attention/kivi.py:56-76) and the bf16 residual, for 2- and 4-bit codes,
+  outlier key channels, GQA, causal verification queries (64 rows per KV head), soft cap and sinks, and caches whose
+  unused slots hold NaN.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import kivi_paged as okp
+from oracle import paged as opaged
+from oracle.attention import reference_attention
+from oracle.numerics import bf16_bits_to_f32
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2
+R, HEADROOM = 128, 256
+W = R + HEADROOM
+
+
+@dataclass
+class KiviCase:
+    q: torch.Tensor  # [B, Q, Hq, D] bf16 (CPU)
+    k: torch.Tensor  # [B, Hkv, S, D] bf16 (CPU)
+    v: torch.Tensor
+    lens: list[int]
+    queries: int
+    bits: int
+    table: np.ndarray
+    pages: int
+    kq: np.ndarray
+    vq: np.ndarray
+
+
+def make_case(batch, queries, q_heads, kv_heads, head_dim, lens, bits, seed) -> KiviCase:
+    gen = torch.Generator().manual_seed(seed)
+    smax = max(lens)
+    q = torch.randn(batch, queries, q_heads, head_dim, generator=gen).to(torch.bfloat16)
+    k = torch.randn(batch, kv_heads, smax, head_dim, generator=gen)
+    v = torch.randn(batch, kv_heads, smax, head_dim, generator=gen)
+    outliers = torch.randperm(head_dim, generator=gen)[:4 * head_dim // 128 or 1]
+    k[..., outliers] *= 10.0  # outlier key channels, as in KIVI's analysis
+    table, pages = opaged.shuffled_block_table(lens, okp.PAGE, seed=seed + 1)
+    committed = np.array([n - queries for n in lens])
+    kq = (committed // R) * R
+    vq = np.maximum(committed - R, 0)
+    return KiviCase(q, k.to(torch.bfloat16), v.to(torch.bfloat16), list(lens), queries, bits, table, pages,
+                    kq.astype(np.int32), vq.astype(np.int32))
+
+
+def oracle_blocks(c: KiviCase, head_dim: int) -> np.ndarray:
+    kv_heads = c.k.shape[1]
+    size = okp.block_layout(head_dim, c.bits, 32)["size"]
+    blocks = np.zeros((c.pages, kv_heads, size), np.uint8)
+    kf, vf = c.k.float().numpy(), c.v.float().numpy()
+    for b in range(len(c.lens)):
+        okp.write_keys(blocks, kf, b, 0, int(c.kq[b]), c.table, c.bits, 32)
+        okp.write_values(blocks, vf, b, 0, int(c.vq[b]), c.table, c.bits, 32)
+    return blocks
+
+
+def device_cache(c: KiviCase, poison: bool = False):
+    """The GPU cache after a prompt of every row's tokens: codes below kq / vq, the last W tokens in the rings."""
+    from economize_amd.kivi import PagedKIVICache, kivi_append, kivi_quantize
+
+    batch, kv_heads, smax, head_dim = c.k.shape
+    cache = PagedKIVICache.empty(c.pages, batch, kv_heads, head_dim, c.bits, "cuda", residual=R, headroom=HEADROOM)
+    if poison:  # never-written memory: NaN scales, zero points and ring entries
+        cache.blocks.fill_(0xFF)
+        cache.k_ring.fill_(float("nan"))
+        cache.v_ring.fill_(float("nan"))
+    table = torch.from_numpy(c.table).cuda()
+    zeros = torch.zeros(batch, dtype=torch.int32, device="cuda")
+    kivi_quantize(cache, table, c.k.cuda(), "k", zeros, torch.from_numpy(c.kq).cuda(), int(c.kq.max()))
+    kivi_quantize(cache, table, c.v.cuda(), "v", zeros, torch.from_numpy(c.vq).cuda(), int(c.vq.max()))
+    rows, pos = [], []
+    for b, n in enumerate(c.lens):
+        for t in range(max(0, n - W), n):
+            rows.append(b)
+            pos.append(t)
+    rows_t = torch.tensor(rows, dtype=torch.int32)
+    pos_t = torch.tensor(pos, dtype=torch.int32)
+    kk = c.k[rows_t.long(), :, pos_t.long()]  # [T, Hkv, D]
+    vv = c.v[rows_t.long(), :, pos_t.long()]
+    kivi_append(cache, kk.cuda(), vv.cuda(), rows_t.cuda(), pos_t.cuda())
+    cache.keys_quantized.copy_(torch.from_numpy(c.kq))
+    cache.values_quantized.copy_(torch.from_numpy(c.vq))
+    return cache, table
+
+
+def oracle_output(c: KiviCase, scale=None, softcap=None, sinks=None) -> np.ndarray:
+    batch, kv_heads, smax, head_dim = c.k.shape
+    blocks = oracle_blocks(c, head_dim)
+    kf, vf = c.k.float().numpy(), c.v.float().numpy()
+    k_ring = np.zeros((batch, kv_heads, W, head_dim), np.float32)
+    v_ring = np.zeros((batch, kv_heads, head_dim, W), np.float32)
+    for b, n in enumerate(c.lens):
+        for t in range(max(0, n - W), n):
+            k_ring[b, :, t % W] = kf[b, :, t]
+            v_ring[b, :, :, t % W] = vf[b, :, t]
+    keys, values = okp.dense_view(blocks, c.table, k_ring, v_ring, c.lens, c.kq, c.vq, c.bits, 32)
+    q = c.q.float().numpy().transpose(0, 2, 1, 3)
+    mask = np.zeros((batch, 1, c.queries, smax), bool)
+    for b, n in enumerate(c.lens):
+        for qi in range(c.queries):
+            mask[b, 0, qi, : n - c.queries + qi + 1] = True
+    scale = 1 / np.sqrt(head_dim) if scale is None else scale
+    return reference_attention(q, keys, values, mask, scale, softcap=softcap, sinks=sinks)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_prompt_quantization_matches_the_oracle(bits, head_dim) -> None:
+    c = make_case(3, 1, 8, 2, head_dim, [700, 300, 1025], bits, seed=bits + head_dim)
+    cache, _ = device_cache(c)
+    torch.cuda.synchronize()
+    got = cache.blocks.cpu().numpy()
+    want = oracle_blocks(c, head_dim)
+    assert np.array_equal(got, want)
+    assert int(cache.overflow.item()) == 0
+
+
+def test_decode_time_schedule_matches_one_shot_quantization() -> None:
+    """Tokens appended one at a time with the schedule run after every step (kivi_commit) leave the same pages and
+    counts as quantizing the final prefixes at once."""
+    from economize_amd.kivi import PagedKIVICache, kivi_append, kivi_commit
+
+    bits, head_dim, kv_heads = 4, 128, 2
+    lens = [200, 131]
+    c = make_case(2, 1, 8, kv_heads, head_dim, lens, bits, seed=5)
+    cache = PagedKIVICache.empty(c.pages, 2, kv_heads, head_dim, bits, "cuda", residual=R, headroom=HEADROOM)
+    table = torch.from_numpy(c.table).cuda()
+    for t in range(max(lens)):
+        rows = [b for b, n in enumerate(lens) if t < n]
+        kk = c.k[rows, :, t]
+        vv = c.v[rows, :, t]
+        kivi_append(cache, kk.cuda(), vv.cuda(), torch.tensor(rows, dtype=torch.int32).cuda(),
+                    torch.full((len(rows),), t, dtype=torch.int32).cuda())
+        committed = torch.tensor([min(t + 1, n) for n in lens], dtype=torch.int32).cuda()
+        kivi_commit(cache, table, committed, 1)
+    torch.cuda.synchronize()
+    c.kq = np.array([(n // R) * R for n in lens], np.int32)
+    c.vq = np.array([max(n - R, 0) for n in lens], np.int32)
+    assert np.array_equal(cache.keys_quantized.cpu().numpy(), c.kq)
+    assert np.array_equal(cache.values_quantized.cpu().numpy(), c.vq)
+    assert np.array_equal(cache.blocks.cpu().numpy(), oracle_blocks(c, head_dim))
+
+
+CASES = [
+    # batch, queries, q heads, kv heads, head dim, lengths, bits
+    (3, 1, 32, 8, 128, [1000, 333, 2050], 2),
+    (3, 1, 32, 8, 128, [1000, 333, 2050], 4),
+    (2, 1, 8, 2, 64, [700, 129], 2),
+    (2, 1, 16, 4, 64, [90, 520], 4),
+    (2, 8, 64, 8, 128, [1500, 1100], 4),  # verification: 8 draft tokens x GQA 8 = 64 rows per KV head
+    (4, 2, 16, 2, 128, [40, 1, 160, 385], 2),  # rows shorter than the residual: no codes at all
+    (1, 1, 32, 8, 128, [8192], 2),  # one long row cut into many waves' ranges
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"b{c[0]}q{c[1]}h{c[2]}k{c[3]}d{c[4]}-int{c[6]}" for c in CASES])
+def test_decode_matches_the_oracle(case) -> None:
+    from economize_amd.kivi import kivi_decode_attention
+
+    batch, queries, hq, hkv, d, lens, bits = case
+    c = make_case(batch, queries, hq, hkv, d, lens, bits, seed=sum(lens) + bits)
+    cache, table = device_cache(c)
+    seq = torch.tensor(lens, dtype=torch.int32).cuda()
+    got = kivi_decode_attention(c.q.cuda(), cache, table, seq, max(lens)).float().cpu().numpy()
+    np.testing.assert_allclose(got, oracle_output(c), atol=ATOL, rtol=RTOL)
+
+
+def test_unused_slots_may_hold_nan() -> None:
+    from economize_amd.kivi import kivi_decode_attention
+
+    c = make_case(3, 1, 16, 4, 128, [1000, 77, 450], 4, seed=17)
+    cache, table = device_cache(c, poison=True)
+    seq = torch.tensor(c.lens, dtype=torch.int32).cuda()
+    got = kivi_decode_attention(c.q.cuda(), cache, table, seq, max(c.lens)).float().cpu().numpy()
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, oracle_output(c), atol=ATOL, rtol=RTOL)
+
+
+def test_softcap_and_sinks() -> None:
+    from economize_amd.kivi import kivi_decode_attention
+
+    c = make_case(2, 2, 16, 4, 128, [600, 333], 2, seed=23)
+    cache, table = device_cache(c)
+    sinks = np.random.default_rng(1).standard_normal(16).astype(np.float32)
+    seq = torch.tensor(c.lens, dtype=torch.int32).cuda()
+    got = kivi_decode_attention(c.q.cuda(), cache, table, seq, max(c.lens), scale=0.2, softcap=4.0,
+                                sinks=torch.from_numpy(sinks).cuda()).float().cpu().numpy()
+    np.testing.assert_allclose(got, oracle_output(c, scale=0.2, softcap=4.0, sinks=sinks), atol=ATOL, rtol=RTOL)
