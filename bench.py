@@ -166,6 +166,159 @@ def cpu_baseline(workload, lens: list[int], budget_s: float = 12.0) -> dict:
     }
 
 
+# ---- the other paths: KIVI decode, Quest selection + gathered attention, KIVI verification (MFMA) -------------------
+
+
+def _shuffled_table(batch: int, pages_per_row: list[int], seed: int, device):
+    import numpy as np
+    import torch
+
+    total = sum(pages_per_row) + 3
+    order = np.random.default_rng(seed).permutation(total)
+    table = np.full((batch, max(pages_per_row)), -1, dtype=np.int32)
+    at = 0
+    for b, n in enumerate(pages_per_row):
+        table[b, :n] = order[at: at + n]
+        at += n
+    return torch.from_numpy(table).to(device), total
+
+
+def kivi_workload(batch, queries, q_heads, kv_heads, lens, bits, seed, residual=128, headroom=256):
+    """A KIVI cache holding every row's lens[b] tokens (committed: lens[b] - queries), filled by the GPU kernels:
+    K/V/q N(0, 1) in bf16 with 4 of 128 key channels scaled by 10, 32-token pages in a shuffled pool."""
+    import torch
+
+    from economize_amd.kivi import PagedKIVICache, kivi_append, kivi_quantize
+
+    device = torch.device("cuda:0")
+    gen = torch.Generator(device=device).manual_seed(seed)
+    smax = max(lens)
+    q = torch.randn(batch, queries, q_heads, HEAD_DIM, generator=gen, device=device).to(torch.bfloat16)
+    k = torch.randn(batch, kv_heads, smax, HEAD_DIM, generator=gen, device=device)
+    k[..., torch.randperm(HEAD_DIM, generator=gen, device=device)[:4]] *= 10.0
+    k = k.to(torch.bfloat16)
+    v = torch.randn(batch, kv_heads, smax, HEAD_DIM, generator=gen, device=device).to(torch.bfloat16)
+    table, pages = _shuffled_table(batch, [-(-n // 32) for n in lens], seed + 1, device)
+    cache = PagedKIVICache.empty(pages, batch, kv_heads, HEAD_DIM, bits, device, residual=residual,
+                                 headroom=headroom)
+    committed = torch.tensor([n - queries for n in lens], dtype=torch.int32, device=device)
+    kq = (committed // residual) * residual
+    vq = torch.clamp(committed - residual, min=0)
+    zeros = torch.zeros(batch, dtype=torch.int32, device=device)
+    kivi_quantize(cache, table, k, "k", zeros, kq.to(torch.int32), smax)
+    kivi_quantize(cache, table, v, "v", zeros, vq.to(torch.int32), smax)
+    ring = cache.ring
+    rows = torch.cat([torch.full((min(n, ring),), b, dtype=torch.int32) for b, n in enumerate(lens)]).to(device)
+    pos = torch.cat([torch.arange(max(0, n - ring), n, dtype=torch.int32) for n in lens]).to(device)
+    kivi_append(cache, k[rows.long(), :, pos.long()], v[rows.long(), :, pos.long()], rows, pos)
+    cache.keys_quantized.copy_(kq)
+    cache.values_quantized.copy_(vq)
+    torch.cuda.synchronize()
+    del k, v
+    return q, cache, table, torch.tensor(lens, dtype=torch.int32, device=device), kq.tolist(), vq.tolist()
+
+
+def kivi_call_bytes(lens, kq, vq, bits, batch, queries, q_heads, kv_heads) -> int:
+    """Algorithmic bytes of a KIVI call: per (row, KV head) the codes and fp16 scales / zero points of the quantized
+    keys and values (D * bits / 8 + 4 D / 32 bytes per token each) and the bf16 ring entries of the rest (the
+    reference's kivi_bytes, techniques/kv_quant/kivi.py:163-175), plus q, out, table entries and counts."""
+    d = HEAD_DIM
+    per_q = d * bits // 8 + 4 * d // 32
+    kv = sum(kv_heads * (k * per_q + v * per_q + (2 * n - k - v) * d * 2) for n, k, v in zip(lens, kq, vq))
+    return kv + 2 * batch * queries * q_heads * d * 2 + sum(-(-n // 32) for n in lens) * 4 + 3 * batch * 4
+
+
+def measure_kivi(bits: int, steps: int, warmup: int, seed: int, batch=16, queries=1, q_heads=32, kv_heads=8,
+                 lens=None) -> dict:
+    import torch
+
+    from economize_amd.kivi import kivi_decode_attention
+
+    lens = lens or [8192] * batch
+    q, cache, table, seq, kq, vq = kivi_workload(batch, queries, q_heads, kv_heads, lens, bits, seed)
+    out = torch.empty_like(q)
+    smax = max(lens)
+    seconds = time_calls(lambda: kivi_decode_attention(q, cache, table, seq, smax, out=out), steps, warmup)
+    nbytes = kivi_call_bytes(lens, kq, vq, bits, batch, queries, q_heads, kv_heads)
+    flops = sum(2 * 2 * kv_heads * (q_heads // kv_heads) * queries * n * HEAD_DIM for n in lens)
+    del cache
+    return {"us_per_call": round(seconds * 1e6, 2), "algorithmic_bytes": nbytes,
+            "gb_s": round(nbytes / seconds / 1e9, 1), "hbm_frac": round(nbytes / seconds / 1e9 / HBM_PEAK_GBS, 4),
+            "tflop_s": round(flops / seconds / 1e12, 2)}
+
+
+def measure_quest(steps: int, warmup: int, seed: int, batch=8, q_heads=32, kv_heads=8, length=32768, budget=1024,
+                  planted=32) -> dict:
+    """Quest decode: bf16 K/V in 16-token pages; per (row, KV head) `planted` pages whose keys are the group's first
+    query plus 0.1 N(0, 1); bounds of the committed pages built once (the cache maintains them); a call is the
+    selection (scores + top-k) plus the attention over the selected pages and the dense tail."""
+    import torch
+
+    from economize_amd.paged import PagedKVCache, paged_append
+    from economize_amd.quest import QuestPages, page_bounds
+
+    device = torch.device("cuda:0")
+    gen = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn(batch, 1, q_heads, HEAD_DIM, generator=gen, device=device).to(torch.bfloat16)
+    pages_per_row = length // PAGE
+    table, total = _shuffled_table(batch, [pages_per_row] * batch, seed + 1, device)
+    cache = PagedKVCache.empty(total, kv_heads, HEAD_DIM, torch.bfloat16, device)
+    groups = q_heads // kv_heads
+    for b in range(batch):
+        k = torch.randn(length, kv_heads, HEAD_DIM, generator=gen, device=device)
+        v = torch.randn(length, kv_heads, HEAD_DIM, generator=gen, device=device)
+        for h in range(kv_heads):
+            chosen = torch.randperm(pages_per_row - 1, generator=gen, device=device)[:planted]
+            idx = (chosen[:, None] * PAGE + torch.arange(PAGE, device=device)[None, :]).reshape(-1)
+            k[idx, h] = q[b, 0, h * groups].float() + 0.1 * torch.randn(idx.numel(), HEAD_DIM, generator=gen,
+                                                                           device=device)
+        t = torch.arange(length, device=device)
+        slots = (table[b, t // PAGE] * PAGE + t % PAGE).to(torch.int32)
+        paged_append(cache, k.to(torch.bfloat16), v.to(torch.bfloat16), slots)
+    done = (length - 1) // PAGE
+    kmin, kmax = page_bounds(cache, table, 0, done, PAGE)
+    pages = budget // PAGE - 1
+    qp = QuestPages(kmin, kmax, torch.full((batch,), done, dtype=torch.int32, device=device), done, done, PAGE, pages)
+    seq = torch.full((batch,), length, dtype=torch.int32, device=device)
+    query = q.transpose(1, 2)
+    out = torch.empty_like(q)
+    from economize_amd.quest import quest_decode_attention
+
+    seconds = time_calls(lambda: quest_decode_attention(query, cache, table, seq, length, qp, out=out), steps, warmup)
+    d = HEAD_DIM
+    tail = length - done * PAGE
+    nbytes = (batch * kv_heads * (2 * d * 2 * done + (pages * PAGE + tail) * 2 * d * 2 + done * 4 * 2)
+              + 2 * batch * q_heads * d * 2 + batch * kv_heads * pages * 4 * 2)
+    torch.cuda.synchronize()
+    del cache, kmin, kmax
+    return {"us_per_call": round(seconds * 1e6, 2), "algorithmic_bytes": nbytes,
+            "gb_s": round(nbytes / seconds / 1e9, 1), "hbm_frac": round(nbytes / seconds / 1e9 / HBM_PEAK_GBS, 4),
+            "dense_bytes_avoided": batch * kv_heads * length * 2 * d * 2}
+
+
+def measure_paths(steps: int, warmup: int, seed: int) -> dict:
+    import numpy as np
+    import torch
+
+    paths = {
+        "kivi_int2_decode": {"workload": "KIVI int2 decode, B=16 Hq=32 Hkv=8 D=128 L=8192, G=32 R=128",
+                             **measure_kivi(2, steps, warmup, seed)},
+        "kivi_int4_decode": {"workload": "KIVI int4 decode, B=16 Hq=32 Hkv=8 D=128 L=8192, G=32 R=128",
+                             **measure_kivi(4, steps, warmup, seed)},
+    }
+    torch.cuda.empty_cache()
+    paths["quest_decode"] = {"workload": "Quest decode, B=8 Hq=32 Hkv=8 D=128 L=32768 bf16, 63 pages + tail",
+                             **measure_quest(steps, warmup, seed)}
+    torch.cuda.empty_cache()
+    lens = np.random.default_rng(seed + 200).integers(1024, 4097, 64).tolist()
+    paths["kivi_int4_verify"] = {
+        "workload": "KIVI int4 speculative verification, B=64 Q=8 Hq=64 Hkv=8 D=128 L~U[1024,4096], causal draft",
+        "sum_len": int(sum(lens)),
+        **measure_kivi(4, steps, warmup, seed, batch=64, queries=8, q_heads=64, kv_heads=8, lens=lens)}
+    torch.cuda.empty_cache()
+    return paths
+
+
 def traffic_per_launch() -> float | None:
     """HBM bytes per split-kernel launch from the committed rocprofv3 counter summary, if present."""
     if not TRAFFIC_FILE.exists():
@@ -184,6 +337,7 @@ def main() -> None:
     parser.add_argument("--seed", type=int, default=0)
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--fixed-only", action="store_true", help="skip the ragged-length run (for profiling)")
+    parser.add_argument("--no-paths", action="store_true", help="skip the KIVI and Quest measurements")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run a plain device copy of 256 MiB, 20 times (the reference kernel for scaling the "
                              "FETCH_SIZE / WRITE_SIZE counters of rocprofv3)")
@@ -210,6 +364,9 @@ def main() -> None:
     ragged_lens = np.random.default_rng(args.seed + 100).integers(1024, 8193, BATCH).tolist()
     ragged = None if args.fixed_only else measure(ragged_lens, args.steps, args.warmup, args.seed + 1)
     cpu = None if args.no_cpu else cpu_baseline(head["workload"], fixed)
+    del head["workload"]
+    torch.cuda.empty_cache()
+    paths = None if (args.no_paths or args.fixed_only) else measure_paths(args.steps, args.warmup, args.seed)
 
     value = head["kv_bytes"] / head["seconds"] / 1e9
     achieved = head["call_bytes"] / head["seconds"] / 1e9
@@ -254,6 +411,7 @@ def main() -> None:
             "hbm_frac": round(ragged["kv_bytes"] / ragged["seconds"] / 1e9 / HBM_PEAK_GBS, 4),
         },
         "cpu_baseline": cpu,
+        "paths": paths,
     }
     print(json.dumps(line), flush=True)
 
