@@ -54,12 +54,16 @@ size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 // Single-wave workgroups of a launch: every CU's resident waves of the kernel instance, but at least four tiles
 // (256 tokens) per wave over the longest possible tile sequence, which bounds the partials a row can be cut into
 // (ECO_PAGED_GRID overrides the count for tuning).
-int paged_grid(int batch, int kv_heads, int rows, int head_dim, int format, int max_seq_len, int n_sel) {
+int paged_grid(int batch, int kv_heads, int rows, int head_dim, int format, int max_seq_len, int listed, int span) {
     static const int forced = [] {
         const char* env = std::getenv("ECO_PAGED_GRID");
         return env ? std::atoi(env) : 0;
     }();
-    const int64_t tiles = static_cast<int64_t>(batch) * kv_heads * (((max_seq_len + 15) / 16 + n_sel + 3) / 4);
+    // cache pages a row reads: every page, or with a page list the listed pages and a tail of about one list page
+    // (rows whose tail is longer only get more tiles per wave)
+    const int64_t dense = (max_seq_len + 15) / 16;
+    const int64_t row_pages = listed > 0 ? std::min<int64_t>(dense, listed + span + 1) : dense;
+    const int64_t tiles = static_cast<int64_t>(batch) * kv_heads * ((row_pages + 3) / 4);
     int per_cu = 1;
     if (paged_resident_waves(head_dim, format, rows, &per_cu)) return 0;
     int64_t grid = forced > 0 ? forced : static_cast<int64_t>(device_cus()) * per_cu;
@@ -135,7 +139,7 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
     if (!(scale == scale)) return fail("paged decode: scale is NaN");
 
     const int grid =
-        paged_grid(batch, kv_heads, rows, head_dim, kv_format, max_seq_len, page_list ? n_sel * span : 0);
+        paged_grid(batch, kv_heads, rows, head_dim, kv_format, max_seq_len, page_list ? n_sel * span : 0, span);
     if (grid <= 0) return 1;
     const Workspace ws = paged_workspace(batch, kv_heads, rows, head_dim, grid);
     if (!workspace || workspace_bytes < ws.total())
@@ -269,7 +273,7 @@ size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q
     const int rows = (q_heads / kv_heads) * queries;
     const int span = list_page_size >= 16 ? list_page_size / 16 : 1;
     const int grid =
-        paged_grid(batch, kv_heads, rows, head_dim, kv_format, max_seq_len, n_sel > 0 ? n_sel * span : 0);
+        paged_grid(batch, kv_heads, rows, head_dim, kv_format, max_seq_len, n_sel > 0 ? n_sel * span : 0, span);
     if (grid <= 0) return 0;
     return paged_workspace(batch, kv_heads, rows, head_dim, grid).total();
 }
@@ -522,7 +526,7 @@ int eco_quest_select(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
     p.kv_heads = kv_heads;
     p.groups = q_heads / kv_heads;
     p.head_dim = head_dim;
-    p.chunk = 64;
+    p.chunk = quest_score_chunk(head_dim);
     return quest_select(p, static_cast<hipStream_t>(stream));
 }
 

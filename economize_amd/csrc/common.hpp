@@ -42,6 +42,16 @@ __device__ inline float group_sum(float x) {  // sum over the four lanes l, l^16
     return x + __shfl_xor(x, 32);
 }
 
+// cap * tanh(x / cap) in log2 units (times log2 e), with inv_cap = 1 / cap: tanh(|t|) = (1 - e) / (1 + e), e =
+// exp(-2 |t|), through the hardware exp2 and reciprocal (each within a few ulp; the reference's soft cap is the same
+// expression in fp32).
+__device__ inline float soft_cap_log2(float x, float cap, float inv_cap) {
+    const float t = x * inv_cap;
+    const float e = __builtin_amdgcn_exp2f(-2.0f * kLog2e * fabsf(t));
+    const float th = (1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e);
+    return cap * kLog2e * (t < 0.0f ? -th : th);
+}
+
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
 }  // namespace eco

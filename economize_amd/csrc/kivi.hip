@@ -491,17 +491,13 @@ __global__ __launch_bounds__(64) void kivi_attention_kernel(KiviParams p) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) s[v][nb][i] *= score_scale;
         if (p.softcap > 0.0f) {
+            const float inv_cap = 1.0f / p.softcap;
 #pragma unroll
             for (int v = 0; v < 2; ++v)
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const float t = s[v][nb][i] / p.softcap;
-                        const float e = __expf(-2.0f * fabsf(t));
-                        const float th = (1.0f - e) / (1.0f + e);
-                        s[v][nb][i] = p.softcap * (t < 0.0f ? -th : th) * kLog2e;
-                    }
+                    for (int i = 0; i < 4; ++i) s[v][nb][i] = soft_cap_log2(s[v][nb][i], p.softcap, inv_cap);
         }
         if (t0 + KPAGE > all_see || (!valid && t0 < kq)) {
 #pragma unroll

@@ -192,8 +192,20 @@ __device__ inline void clear_unheld_values(Tile<D, FMT, NB>& tile) {
 
 }  // namespace
 
+// Two waves per SIMD for the single-buffer instances whose state fits 256 VGPRs: the compiler then keeps the
+// accumulators in VGPRs (no copies between the accumulation registers and the VGPRs at every tile), and the second
+// wave's loads and arithmetic fill the first one's waits. These instances also clear the accumulators through a
+// row's first rescale and take the soft cap through the hardware reciprocal (see begin_row and compute); the others
+// keep the explicit clear and the IEEE divisions.
 template <int D, int FMT, int NB, int NBUF>
-__global__ __launch_bounds__(64) void paged_attention_kernel(PagedParams p) {
+constexpr int waves_per_simd() {
+    return NBUF == 1 && D <= 128 && (NB == 1 || (NB == 2 && FMT != BF16)) ? 2 : 1;
+}
+
+template <int D, int FMT, int NB, int NBUF>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(waves_per_simd<D, FMT, NB, NBUF>()))) void
+paged_attention_kernel(PagedParams p) {
+    constexpr bool kTwoWaves = waves_per_simd<D, FMT, NB, NBUF>() == 2;
     using T = Tile<D, FMT, NB>;
     constexpr int ES = T::ES;
     constexpr int E = 16 / ES;  // channels per 16-byte run
@@ -232,8 +244,12 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(PagedParams p) {
             limit[nb] = r < p.rows ? static_cast<float>(c.row.len - p.queries + r % p.queries + 1) : 0.0f;
             m_i[nb] = -INFINITY;
             l_i[nb] = 0.0f;
+            // two-wave instances: the accumulators are cleared by the row's first rescale (m_i = -inf marks a row
+            // with no weight yet), so that a row change does not give them a second register version to merge at
+            // every tile
+            if constexpr (!kTwoWaves)
 #pragma unroll
-            for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
         all_see = c.row.len - p.queries + 1;
         const float ks = p.k_scale ? scalar_load(p.k_scale, c.kvh) : 1.0f;
@@ -277,16 +293,21 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(PagedParams p) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) s[v][nb][i] *= score_scale;
         if (p.softcap > 0.0f) {
+            const float inv_cap = 1.0f / p.softcap;
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const float t = s[v][nb][i] / p.softcap;
-                        const float e = __expf(-2.0f * fabsf(t));
-                        const float th = (1.0f - e) / (1.0f + e);
-                        s[v][nb][i] = p.softcap * (t < 0.0f ? -th : th) * kLog2e;
+                        if constexpr (kTwoWaves) {
+                            s[v][nb][i] = soft_cap_log2(s[v][nb][i], p.softcap, inv_cap);
+                        } else {
+                            const float t = s[v][nb][i] / p.softcap;
+                            const float e = __expf(-2.0f * fabsf(t));
+                            const float th = (1.0f - e) / (1.0f + e);
+                            s[v][nb][i] = p.softcap * (t < 0.0f ? -th : th) * kLog2e;
+                        }
                     }
         }
         if (__ballot(tile.lv < 0 || first + PAGE > all_see) != 0) {
@@ -313,7 +334,19 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(PagedParams p) {
             // at D = 256 rescales at every tile: on gfx950 its lazy form (and a form with the scale folded into the
             // exponent) gave wrong results although the same source is correct in every other instance.
             constexpr float lazy = FMT == BF16 && D > 128 ? 0.0f : 8.0f;
-            if (lazy == 0.0f || __ballot(tile_max > m_i[nb] + lazy) != 0) {
+            if constexpr (kTwoWaves) {
+                if (lazy == 0.0f || __ballot(tile_max > m_i[nb] + lazy || m_i[nb] == -INFINITY) != 0) {
+                    const bool fresh = m_i[nb] == -INFINITY;
+                    const float m_new = fmaxf(m_i[nb], tile_max);
+                    const float alpha = fresh ? 0.0f : __builtin_amdgcn_exp2f(m_i[nb] - m_new);
+                    l_i[nb] *= alpha;
+#pragma unroll
+                    for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[nd][nb][i] = fresh ? 0.0f : acc[nd][nb][i] * alpha;
+                    m_i[nb] = m_new;
+                }
+            } else if (lazy == 0.0f || __ballot(tile_max > m_i[nb] + lazy) != 0) {
                 const float m_new = fmaxf(m_i[nb], tile_max);
                 const float alpha = m_i[nb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_i[nb] - m_new);
                 l_i[nb] *= alpha;
@@ -435,6 +468,11 @@ __global__ __launch_bounds__(64) void paged_attention_kernel(PagedParams p) {
     PageWindow win;
     int64_t seg_begin = lo;
     bool first_segment = true;
+    if constexpr (kTwoWaves)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     begin_row(cur);
 
     T bufs[NBUF];

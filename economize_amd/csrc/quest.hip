@@ -26,6 +26,8 @@ namespace eco {
 namespace {
 
 constexpr int PAGE = 16;
+constexpr int SCORE_PASSES = 4;  // pages per scoring thread
+constexpr int TOPK_LDS_KEYS = 15360;  // rows of at most this many committed pages select from keys held in LDS (60 KiB)
 
 template <int FMT>
 __device__ inline float decode_elem(const uint8_t* p, int i) {
@@ -103,13 +105,33 @@ __global__ __launch_bounds__(64) void quest_bounds_kernel(BoundsParams p) {
 }
 
 // Scores of pages [chunk * blockIdx.x, +chunk) of row (b, kvh) = blockIdx.y: L lanes per page (L = the run count
-// padded to a power of two), lane j holding channels 8 j .. 8 j + 7.
+// padded to a power of two), lane j holding channels 8 j .. 8 j + 7; a workgroup covers SCORE_PASSES * 256 / L
+// pages, and every thread issues the bound loads of all its pages before it sums the query rows.
 __global__ __launch_bounds__(256) void quest_score_kernel(SelectParams p) {
     __shared__ float qsum[512], qabs[512];
     const int row = blockIdx.y;
     const int b = row / p.kv_heads;
     const int kvh = row % p.kv_heads;
     const int rows = p.groups * p.queries;
+    const int runs = p.head_dim / 8;
+    int L = 1;
+    while (L < runs) L <<= 1;
+    const int per_pass = blockDim.x / L;
+    const int j = threadIdx.x % L;
+    const int done = min(max(p.done[b], 0), p.max_done);
+    const int p0 = blockIdx.x * p.chunk;
+    const int p1 = min(p0 + p.chunk, p.max_done);
+    uint4 lw[SCORE_PASSES], hw[SCORE_PASSES];
+#pragma unroll
+    for (int k = 0; k < SCORE_PASSES; ++k) {
+        const int page = p0 + k * per_pass + static_cast<int>(threadIdx.x) / L;
+        lw[k] = hw[k] = make_uint4(0, 0, 0, 0);
+        if (page < p1 && j < runs) {
+            const int64_t at = b * p.sb_b + kvh * p.sb_h + static_cast<int64_t>(page) * p.sb_p + 8 * j;
+            lw[k] = *reinterpret_cast<const uint4*>(p.kmin + at);
+            hw[k] = *reinterpret_cast<const uint4*>(p.kmax + at);
+        }
+    }
     for (int d = threadIdx.x; d < p.head_dim; d += blockDim.x) {
         float s = 0.0f, a = 0.0f;
         for (int r = 0; r < rows; ++r) {
@@ -122,24 +144,14 @@ __global__ __launch_bounds__(256) void quest_score_kernel(SelectParams p) {
         qabs[d] = a;
     }
     __syncthreads();
-    const int runs = p.head_dim / 8;
-    int L = 1;
-    while (L < runs) L <<= 1;
-    const int per_pass = blockDim.x / L;
-    const int j = threadIdx.x % L;
-    const int done = min(max(p.done[b], 0), p.max_done);
     float* out = p.scores + static_cast<int64_t>(row) * p.max_done;
-    const int p0 = blockIdx.x * p.chunk;
-    const int p1 = min(p0 + p.chunk, p.max_done);
-    for (int base = p0; base < p1; base += per_pass) {
-        const int page = base + static_cast<int>(threadIdx.x) / L;
+#pragma unroll
+    for (int k = 0; k < SCORE_PASSES; ++k) {
+        const int page = p0 + k * per_pass + static_cast<int>(threadIdx.x) / L;
         float s1 = 0.0f, s2 = 0.0f;
-        if (page < p1 && j < runs) {
-            const int64_t at = b * p.sb_b + kvh * p.sb_h + static_cast<int64_t>(page) * p.sb_p + 8 * j;
-            const uint4 lw = *reinterpret_cast<const uint4*>(p.kmin + at);
-            const uint4 hw = *reinterpret_cast<const uint4*>(p.kmax + at);
-            const uint32_t lo_w[4] = {lw.x, lw.y, lw.z, lw.w};
-            const uint32_t hi_w[4] = {hw.x, hw.y, hw.z, hw.w};
+        if (j < runs) {
+            const uint32_t lo_w[4] = {lw[k].x, lw[k].y, lw[k].z, lw[k].w};
+            const uint32_t hi_w[4] = {hw[k].x, hw[k].y, hw[k].z, hw[k].w};
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const float lo = bf16_to_f32(static_cast<uint16_t>(lo_w[i >> 1] >> (16 * (i & 1))));
@@ -184,8 +196,11 @@ __device__ inline int block_scan(int x, int* lds4, int* total) {
 }
 
 // One workgroup of 256 threads per (row, KV head): the top `count` of the row's committed pages by score, written in
-// increasing page order, then -1.
+// increasing page order, then -1. With IN_LDS the row's keys are read from global memory once, into LDS; otherwise
+// (rows of more than TOPK_LDS_KEYS pages) every pass reads them from global memory again.
+template <bool IN_LDS>
 __global__ __launch_bounds__(256) void quest_topk_kernel(SelectParams p) {
+    extern __shared__ uint32_t lds_keys[];
     __shared__ int hist[256];
     __shared__ int lds4[4];
     __shared__ uint32_t shared_prefix;
@@ -197,21 +212,30 @@ __global__ __launch_bounds__(256) void quest_topk_kernel(SelectParams p) {
     const int count = min(p.pages, p.max_done);
     int32_t* out = p.out + static_cast<int64_t>(row) * p.pages;
     const float* scores = p.scores + static_cast<int64_t>(row) * p.max_done;
-    const int per = (n + 255) / 256;
-    const int i0 = min(t * per, n), i1 = min(i0 + per, n);
     int total = 0;
     if (n <= count) {  // every committed page
         for (int i = t; i < p.pages; i += 256) out[i] = i < n ? i : -1;
         return;
     }
-    // radix select of the count-th largest key, most significant byte first
+    if constexpr (IN_LDS) {
+#pragma unroll 8
+        for (int i = t; i < n; i += 256) lds_keys[i] = score_key(scores[i]);
+        __syncthreads();
+    }
+    auto key_at = [&](int i) __attribute__((always_inline)) -> uint32_t {
+        if constexpr (IN_LDS)
+            return lds_keys[i];
+        else
+            return score_key(scores[i]);
+    };
+    // radix select of the count-th largest key, most significant byte first (the histogram visits keys in any order)
     uint32_t prefix = 0, known = 0;
     int rem = count;
     for (int shift = 24; shift >= 0; shift -= 8) {
         hist[t] = 0;
         __syncthreads();
-        for (int i = i0; i < i1; ++i) {
-            const uint32_t key = score_key(scores[i]);
+        for (int i = t; i < n; i += 256) {
+            const uint32_t key = key_at(i);
             if (((key ^ prefix) & known) == 0) atomicAdd(&hist[(key >> shift) & 255], 1);
         }
         __syncthreads();
@@ -227,19 +251,21 @@ __global__ __launch_bounds__(256) void quest_topk_kernel(SelectParams p) {
         known |= 0xFFu << shift;
         __syncthreads();
     }
-    // keys above the threshold, and the first `rem` keys equal to it in page order
+    // keys above the threshold, and the first `rem` keys equal to it in page order: thread t takes a contiguous range
+    const int per = (n + 255) / 256;
+    const int i0 = min(t * per, n), i1 = min(i0 + per, n);
     int eq = 0;
-    for (int i = i0; i < i1; ++i) eq += score_key(scores[i]) == prefix ? 1 : 0;
+    for (int i = i0; i < i1; ++i) eq += key_at(i) == prefix ? 1 : 0;
     int eq_before = block_scan(eq, lds4, &total) - eq;
     int sel = 0;
     for (int i = i0, e = eq_before; i < i1; ++i) {
-        const uint32_t key = score_key(scores[i]);
+        const uint32_t key = key_at(i);
         if (key > prefix) ++sel;
         else if (key == prefix) sel += e++ < rem ? 1 : 0;
     }
     int pos = block_scan(sel, lds4, &total) - sel;
     for (int i = i0, e = eq_before; i < i1; ++i) {
-        const uint32_t key = score_key(scores[i]);
+        const uint32_t key = key_at(i);
         bool take = key > prefix;
         if (key == prefix) take = e++ < rem;
         if (take) out[pos++] = i;
@@ -248,6 +274,12 @@ __global__ __launch_bounds__(256) void quest_topk_kernel(SelectParams p) {
 }
 
 }  // namespace
+
+int quest_score_chunk(int head_dim) {
+    int L = 1;
+    while (L < head_dim / 8) L <<= 1;
+    return SCORE_PASSES * 256 / L;
+}
 
 int quest_bounds(const BoundsParams& p, hipStream_t stream) {
     if (p.last <= p.first) return 0;
@@ -264,11 +296,17 @@ int quest_bounds(const BoundsParams& p, hipStream_t stream) {
 int quest_select(const SelectParams& p, hipStream_t stream) {
     const int rows = p.batch * p.kv_heads;
     if (p.max_done > 0) {
+        if (p.chunk != quest_score_chunk(p.head_dim)) return fail("quest select: score chunk does not match the head dim");
         dim3 grid((p.max_done + p.chunk - 1) / p.chunk, rows);
         hipLaunchKernelGGL(quest_score_kernel, grid, dim3(256), 0, stream, p);
         if (int rc = check_launch("quest_score_kernel")) return rc;
     }
-    hipLaunchKernelGGL(quest_topk_kernel, dim3(rows), dim3(256), 0, stream, p);
+    if (p.max_done <= TOPK_LDS_KEYS) {
+        const size_t lds = static_cast<size_t>(p.max_done > 0 ? p.max_done : 1) * sizeof(uint32_t);
+        hipLaunchKernelGGL(quest_topk_kernel<true>, dim3(rows), dim3(256), lds, stream, p);
+    } else {
+        hipLaunchKernelGGL(quest_topk_kernel<false>, dim3(rows), dim3(256), 0, stream, p);
+    }
     return check_launch("quest_topk_kernel");
 }
 

@@ -37,5 +37,6 @@ struct SelectParams {
 
 int quest_bounds(const BoundsParams& p, hipStream_t stream);
 int quest_select(const SelectParams& p, hipStream_t stream);
+int quest_score_chunk(int head_dim);  // pages scored per workgroup
 
 }  // namespace eco
