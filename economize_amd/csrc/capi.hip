@@ -51,8 +51,8 @@ int device_cus() {
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-// Single-wave workgroups of a launch: every CU's resident waves of the kernel instance, but at least four tiles
-// (256 tokens) per wave over the longest possible tile sequence, which bounds the partials a row can be cut into
+// Workgroups of a launch: every CU's resident workgroups of the kernel instance, but at least four tiles (256 tokens)
+// per wave over the longest possible tile sequence, which bounds the partials a row can be cut into
 // (ECO_PAGED_GRID overrides the count for tuning).
 int paged_grid(int batch, int kv_heads, int rows, int head_dim, int format, int max_seq_len, int listed, int span) {
     static const int forced = [] {
@@ -64,10 +64,10 @@ int paged_grid(int batch, int kv_heads, int rows, int head_dim, int format, int 
     const int64_t dense = (max_seq_len + 15) / 16;
     const int64_t row_pages = listed > 0 ? std::min<int64_t>(dense, listed + span + 1) : dense;
     const int64_t tiles = static_cast<int64_t>(batch) * kv_heads * ((row_pages + 3) / 4);
-    int per_cu = 1;
-    if (paged_resident_waves(head_dim, format, rows, &per_cu)) return 0;
+    int per_cu = 1, waves = 1;
+    if (paged_resident_groups(head_dim, format, rows, &per_cu, &waves)) return 0;
     int64_t grid = forced > 0 ? forced : static_cast<int64_t>(device_cus()) * per_cu;
-    const int64_t cap = (tiles + 3) / 4;
+    const int64_t cap = (tiles + 4 * waves - 1) / (4 * waves);  // at least four tiles per wave
     grid = grid < cap ? grid : cap;
     return static_cast<int>(grid < 1 ? 1 : grid);
 }

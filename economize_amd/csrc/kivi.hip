@@ -366,9 +366,13 @@ __global__ __launch_bounds__(64) void kivi_attention_kernel(KiviParams p) {
     const int w = blockIdx.x;
     const int grid = gridDim.x;
 
-    const int64_t total = uniform64(total_tiles(p, lane));
+    // row geometry: one load of the lengths for batches of at most 64 rows
+    const bool small = p.batch <= 64;
+    RowTable rt{};
+    if (small) rt = row_table(p, lane);
+    const int64_t total = small ? uniform64(__shfl(rt.incl, 63)) : uniform64(total_tiles(p, lane));
     for (int b = w; b < p.batch; b += grid) {  // rows without a key: zeros
-        if (row_of(p, b).tiles == 0)
+        if ((small ? __builtin_amdgcn_readlane(rt.row.tiles, b) : row_of(p, b).tiles) == 0)
             for (int idx = lane; idx < p.kv_heads * p.rows * D; idx += 64)
                 store_output(p, b, idx / (p.rows * D), (idx / D) % p.rows, idx % D, 0.0f, -INFINITY, 0.0f);
     }
@@ -668,7 +672,7 @@ __global__ __launch_bounds__(64) void kivi_attention_kernel(KiviParams p) {
     };
 
     // ---- the tile pipeline (as in paged_attention.hip) ----
-    Cursor cur = locate(p, lo, lane);
+    Cursor cur = small ? locate_in(p, rt, lo) : locate(p, lo, lane);
     PageWindow win;
     int64_t seg_begin = lo;
     bool first_segment = true;
@@ -682,7 +686,7 @@ __global__ __launch_bounds__(64) void kivi_attention_kernel(KiviParams p) {
         issue_tile<D, BITS>(p, icur, n, g, lane, win, buf);
         slot = icur;
         if (ipos < hi) {
-            if (ipos + 1 < hi) advance(p, icur);
+            if (ipos + 1 < hi) advance(p, icur, small ? &rt : nullptr);
             ++ipos;
         }
     };

@@ -109,7 +109,9 @@ __device__ constexpr int k_channel(int j, int g) {
     return E * (4 * (j / per_run) + g) + 8 * (j % per_run);
 }
 
-template <int D, int FMT, int NB>
+// A tile's K/V registers, and (unless RQ) the query operand of its row. With RQ the kernel keeps the query operand
+// once per row instead (loaded with the row's first tile), which frees NB * D / 8 VGPRs per tile buffer.
+template <int D, int FMT, int NB, bool RQ = false>
 struct Tile {
     static constexpr int ES = FMT == BF16 ? 2 : 1;  // bytes per element
     static constexpr int NU = D * ES / 64;          // 16-byte K loads per lane per S MFMA block
@@ -118,12 +120,32 @@ struct Tile {
     static constexpr int KS = D / 32;               // k-steps of an S MFMA block
     uint4 k[4][NU];
     uint4 v[ND][NV];
-    bf16x8 q[NB][KS];  // the query operand of the tile's row (an L2 hit after the row's first tile)
+    bf16x8 q[RQ ? 1 : NB][RQ ? 1 : KS];  // the query operand of the tile's row (an L2 hit after the row's first tile)
     int lv;    // logical page of the lane group's tile page (-1: none)
     int vcnt;  // tokens of that page inside the row (0 to 16); the V bytes of the others are cleared before use
 };
 
-// Issues the loads of the tile under cursor c (lane (n, g): K rows of tile page n / 4, V channel n of page g).
+// The query operand of row c: lane (n, g) holds query row nb * 16 + n, channels of k-step j as the K runs order them
+// (a lane of a row past the group reads row 0: its MFMA column is computed and never stored).
+template <int D, int FMT, int NB>
+__device__ __forceinline__ void load_query(const PagedParams& p, const Cursor& c, int n, int g,
+                                           bf16x8 (&q)[NB][D / 32]) {
+    constexpr int E = FMT == BF16 ? 8 : 16;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int r = nb * 16 + n;
+        const bool valid = r < p.rows;
+        const int gq = valid ? r / p.queries : 0;
+        const int qi = valid ? r % p.queries : 0;
+        const uint16_t* base = p.q + c.b * p.sq_b + qi * p.sq_q + (c.kvh * p.groups + gq) * p.sq_h;
+#pragma unroll
+        for (int j = 0; j < D / 32; ++j)
+            q[nb][j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(base + k_channel<E>(j, g)));
+    }
+}
+
+// Issues the loads of the tile under cursor c (lane (n, g): K rows of tile page n / 4, V channel n of page g), and
+// the query operand of its row into the tile.
 template <int D, int FMT, int NB>
 __device__ __forceinline__ void issue_tile(const PagedParams& p, const Cursor& c, int n, int g, int lane, PageWindow& win,
                                   Tile<D, FMT, NB>& tile) {
@@ -163,12 +185,39 @@ __device__ __forceinline__ void issue_tile(const PagedParams& p, const Cursor& c
     }
 }
 
+// As issue_tile for a tile without a query operand: the row's query operand goes to q_next, only when load_q is set
+// (the first tile of a row, or of the wave's range), and those loads come first, so that waiting for them does not
+// wait for the tile's K/V.
+template <int D, int FMT, int NB>
+__device__ __forceinline__ void issue_tile_rq(const PagedParams& p, const Cursor& c, int n, int g, int lane,
+                                              PageWindow& win, Tile<D, FMT, NB, true>& tile,
+                                              bf16x8 (&q_next)[NB][D / 32], bool load_q) {
+    using T = Tile<D, FMT, NB, true>;
+    if (load_q) load_query<D, FMT, NB>(p, c, n, g, q_next);
+    ensure_window(p, c, lane, win);
+    const int at = TILE * c.t - win.base;
+    const int pk = __shfl(win.physical, at + (n >> 2));
+    const int pv = __shfl(win.physical, at + g);
+    tile.lv = __shfl(win.logical, at + g);
+    tile.vcnt = tile.lv >= 0 ? min(max(c.row.len - tile.lv * PAGE, 0), PAGE) : 0;
+    const uint8_t* kp = p.k_cache + c.kvh * p.kc_head + static_cast<int64_t>(pk >= 0 ? pk : 0) * p.kc_page;
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int u = 0; u < T::NU; ++u) tile.k[v][u] = load16(kp + ((4 * u + g) * PAGE + 4 * v + (n & 3)) * 16);
+    const uint8_t* vp = p.v_cache + c.kvh * p.vc_head + static_cast<int64_t>(pv >= 0 ? pv : 0) * p.vc_page;
+#pragma unroll
+    for (int nd = 0; nd < T::ND; ++nd)
+#pragma unroll
+        for (int w = 0; w < T::NV; ++w) tile.v[nd][w] = load16(vp + (16 * nd + n) * PAGE * T::ES + 16 * w);
+}
+
 // Clears the V bytes of the tokens a tile page does not hold (past the row's end, or the whole page when it holds
 // nothing): cache slots that were never written may hold NaN codes, and a zero softmax weight times NaN is NaN.
 // V run w of a lane holds 16 bytes of channel data for tokens 16 w / ES .. of its page (ES bytes per token).
-template <int D, int FMT, int NB>
-__device__ inline void clear_unheld_values(Tile<D, FMT, NB>& tile) {
-    using T = Tile<D, FMT, NB>;
+template <int D, int FMT, int NB, bool RQ>
+__device__ inline void clear_unheld_values(Tile<D, FMT, NB, RQ>& tile) {
+    using T = Tile<D, FMT, NB, RQ>;
     constexpr int TPD = 4 / T::ES;  // tokens per dword
     uint32_t mask[T::NV][4];
 #pragma unroll
@@ -202,33 +251,63 @@ constexpr int waves_per_simd() {
     return NBUF == 1 && D <= 128 && (NB == 1 || (NB == 2 && FMT != BF16)) ? 2 : 1;
 }
 
+// Waves of a workgroup. Four for one column block at D <= 128: the workgroup's tile range is split in four
+// contiguous quarters, and the pieces of a row that lies inside the workgroup's range are merged through LDS after
+// one barrier; only rows cut at a workgroup boundary go through the counter and the workspace partials.
+template <int D, int NB, int NBUF>
+constexpr int wg_waves() {
+    return NB == 1 && D <= 128 && NBUF <= 2 ? 4 : 1;
+}
+
 template <int D, int FMT, int NB, int NBUF>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(waves_per_simd<D, FMT, NB, NBUF>()))) void
+__global__ __launch_bounds__((64 * wg_waves<D, NB, NBUF>()))
+    __attribute__((amdgpu_waves_per_eu(waves_per_simd<D, FMT, NB, NBUF>()))) void
 paged_attention_kernel(PagedParams p) {
     constexpr bool kTwoWaves = waves_per_simd<D, FMT, NB, NBUF>() == 2;
-    using T = Tile<D, FMT, NB>;
+    constexpr int WAVES = wg_waves<D, NB, NBUF>();
+    // two buffers: the query operand is kept once per row (q_row), loaded into q_next with the row's first tile
+    constexpr bool kRowQ = NBUF == 2;
+    using T = Tile<D, FMT, NB, kRowQ>;
     constexpr int ES = T::ES;
     constexpr int E = 16 / ES;  // channels per 16-byte run
     constexpr int KS = D / 32;  // k-steps of an S MFMA block
     constexpr int ND = T::ND;
     constexpr int KPR = E / 8;  // k-steps per run
 
-    const int lane = threadIdx.x;
+    const int lane = WAVES > 1 ? static_cast<int>(threadIdx.x) & 63 : static_cast<int>(threadIdx.x);
+    const int wave = WAVES > 1 ? uniform(static_cast<int>(threadIdx.x) >> 6) : 0;
     const int n = lane & 15;
     const int g = lane >> 4;
-    const int w = blockIdx.x;
+    const int w = blockIdx.x;  // workgroup
     const int grid = gridDim.x;
 
-    const int64_t total = uniform64(total_tiles(p, lane));
+    // row geometry: one load of the lengths for batches of at most 64 rows
+    const bool small = p.batch <= 64;
+    RowTable rt{};
+    if (small) rt = row_table(p, lane);
+    const int64_t total = small ? uniform64(__shfl(rt.incl, 63)) : uniform64(total_tiles(p, lane));
     // rows of batch entries without a key: zeros (sinks included, decode.py:17)
-    for (int b = w; b < p.batch; b += grid) {
-        if (row_of(p, b).tiles == 0)
+    for (int b = w * WAVES + wave; b < p.batch; b += grid * WAVES) {
+        if ((small ? __builtin_amdgcn_readlane(rt.row.tiles, b) : row_of(p, b).tiles) == 0)
             for (int idx = lane; idx < p.kv_heads * p.rows * D; idx += 64)
                 store_output(p, b, idx / (p.rows * D), (idx / D) % p.rows, idx % D, 0.0f, -INFINITY, 0.0f);
     }
-    const int64_t lo = total * w / grid;
-    const int64_t hi = total * (w + 1) / grid;
-    if (lo >= hi) return;
+    const int64_t wlo = total * w / grid;  // the workgroup's tile range
+    const int64_t whi = total * (w + 1) / grid;
+    const int64_t lo = wlo + (whi - wlo) * wave / WAVES;  // this wave's quarter of it
+    const int64_t hi = wlo + (whi - wlo) * (wave + 1) / WAVES;
+    // Row pieces of the workgroup's waves (two per wave: its first and its last row segment, when they are not
+    // whole rows): maxima, sums and accumulators of at most 16 query rows, and the row they belong to.
+    constexpr int PIECE = WAVES > 1 ? 16 * (D + 2) : 1;
+    __shared__ float piece_data[WAVES > 1 ? 2 * WAVES : 1][PIECE];
+    __shared__ int64_t piece_row[WAVES > 1 ? 2 * WAVES : 1];  // row_start of the piece's row, -1 for none
+    __shared__ int piece_b[WAVES > 1 ? 2 * WAVES : 1], piece_kvh[WAVES > 1 ? 2 * WAVES : 1],
+        piece_tiles[WAVES > 1 ? 2 * WAVES : 1];
+    if constexpr (WAVES > 1) {
+        if (lane < 2) piece_row[2 * wave + lane] = -1;
+    } else {
+        if (lo >= hi) return;
+    }
 
     // ---- row state: query operand, visibility limits, scales, online-softmax accumulators ----
     float limit[NB];
@@ -258,8 +337,9 @@ paged_attention_kernel(PagedParams p) {
     };
 
     // ---- one tile of the online softmax ----
+    bf16x8 q_row[kRowQ ? NB : 1][kRowQ ? KS : 1], q_next[kRowQ ? NB : 1][kRowQ ? KS : 1];
     auto compute = [&](T& tile) __attribute__((always_inline)) {
-        if (__ballot(tile.vcnt < PAGE) != 0) clear_unheld_values<D, FMT, NB>(tile);
+        if (__ballot(tile.vcnt < PAGE) != 0) clear_unheld_values<D, FMT, NB, kRowQ>(tile);
         f32x4 s[4][NB];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
@@ -277,7 +357,14 @@ paged_attention_kernel(PagedParams p) {
                 }
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
-                    s[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, tile.q[nb][j], s[v][nb], 0, 0, 0);
+                {
+                    bf16x8 qo;
+                    if constexpr (kRowQ)
+                        qo = q_row[nb][j];
+                    else
+                        qo = tile.q[nb][j];
+                    s[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qo, s[v][nb], 0, 0, 0);
+                }
             }
         }
         // P operands: fp16 for fp8 caches, bf16 hi + lo for bf16 caches
@@ -437,6 +524,28 @@ paged_attention_kernel(PagedParams p) {
             }
             return;
         }
+        if constexpr (WAVES > 1) {
+            const int k = 2 * wave + (first_segment ? 0 : 1);
+            float* piece = piece_data[k];
+            const int r = n;
+            if (r < p.rows) {
+                if (g == 0) {
+                    piece[r] = m_i[0];
+                    piece[p.rows + r] = l_i[0];
+                }
+#pragma unroll
+                for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) piece[2 * p.rows + r * D + 16 * nd + 4 * g + i] = acc[nd][0][i] * vs;
+            }
+            if (lane == 0) {
+                piece_row[k] = c.row_start;
+                piece_b[k] = c.b;
+                piece_kvh[k] = c.kvh;
+                piece_tiles[k] = c.row.tiles;
+            }
+            return;
+        }
         const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
         float* slot = p.part + (2 * static_cast<int64_t>(w) + (first_segment ? 0 : 1)) * stride;
 #pragma unroll
@@ -463,66 +572,163 @@ paged_attention_kernel(PagedParams p) {
         merge_row<D>(p, c, __shfl(prev, 0), total, grid, lane);
     };
 
+    // ---- the workgroup's row pieces, merged by its first wave once every wave has finished its range ----
+    auto merge_pieces = [&]() __attribute__((always_inline)) {
+        if constexpr (WAVES > 1) {
+            __syncthreads();
+            if (wave != 0) return;
+            const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
+            int k = 0;
+            while (k < 2 * WAVES) {
+                const int64_t row = piece_row[k];
+                if (row < 0) {
+                    ++k;
+                    continue;
+                }
+                // the pieces of one row are consecutive among the valid ones (rows follow the tile order)
+                uint32_t members = 0;
+                int k2 = k;
+                while (k2 < 2 * WAVES && (piece_row[k2] == row || piece_row[k2] < 0)) {
+                    if (piece_row[k2] == row) members |= 1u << k2;
+                    ++k2;
+                }
+                Cursor c{};
+                c.b = piece_b[k];
+                c.kvh = piece_kvh[k];
+                c.row.tiles = piece_tiles[k];
+                c.row_start = row;
+                k = k2;
+                const bool inside = row >= wlo && row + c.row.tiles <= whi;
+                float* slot = p.part + (2 * static_cast<int64_t>(w) + (wlo < row ? 1 : 0)) * stride;
+                for (int base = 0; base < p.rows * D; base += 64 * 8) {
+                    const int e = base + lane * 8;
+                    const bool active = e < p.rows * D;
+                    const int r = active ? e / D : 0;
+                    const int d = active ? e % D : 0;
+                    float m = -INFINITY;
+                    for (int j = 0; j < 2 * WAVES; ++j)
+                        if ((members >> j) & 1u) m = fmaxf(m, piece_data[j][r]);
+                    float l = 0.0f, o[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) o[i] = 0.0f;
+                    for (int j = 0; j < 2 * WAVES; ++j) {
+                        if (!((members >> j) & 1u)) continue;
+                        const float mj = piece_data[j][r];
+                        if (mj == -INFINITY) continue;
+                        const float cw = __builtin_amdgcn_exp2f(mj - m);
+                        l += piece_data[j][p.rows + r] * cw;
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) o[i] += piece_data[j][2 * p.rows + r * D + d + i] * cw;
+                    }
+                    if (!active) continue;
+                    if (inside) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) store_output(p, c.b, c.kvh, r, d + i, o[i], m, l);
+                    } else {
+                        if (d == 0) {
+                            coherent_store(slot + r, m);
+                            coherent_store(slot + p.rows + r, l);
+                        }
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) coherent_store(slot + 2 * p.rows + r * D + d + i, o[i]);
+                    }
+                }
+                if (!inside) {
+                    // the row is cut at a workgroup boundary: the workgroup's partial joins the others' in the
+                    // workspace, and the last workgroup to finish merges them
+                    __builtin_amdgcn_s_waitcnt(0);
+                    int prev = 0;
+                    if (lane == 0)
+                        prev = __hip_atomic_fetch_add(p.counters + c.b * p.kv_heads + c.kvh, 1, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                    merge_row<D>(p, c, __shfl(prev, 0), total, grid, lane);
+                }
+            }
+        }
+    };
+
     // ---- the tile pipeline: NBUF register buffers, tile pos + NBUF - 1 issued while tile pos is computed ----
-    Cursor cur = locate(p, lo, lane);
-    PageWindow win;
-    int64_t seg_begin = lo;
-    bool first_segment = true;
-    if constexpr (kTwoWaves)
+    auto pipeline = [&]() __attribute__((always_inline)) {
+        Cursor cur = small ? locate_in(p, rt, lo) : locate(p, lo, lane);
+        PageWindow win;
+        int64_t seg_begin = lo;
+        bool first_segment = true;
+        if constexpr (kTwoWaves)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
+            for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-            for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    begin_row(cur);
+                for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        begin_row(cur);
 
-    T bufs[NBUF];
-    Cursor cs[NBUF];  // the cursor of the tile each buffer holds
-    Cursor icur = cur;  // the next tile to issue, at sequence offset ipos
-    int64_t ipos = lo;
+        T bufs[NBUF];
+        Cursor cs[NBUF];  // the cursor of the tile each buffer holds
+        Cursor icur = cur;  // the next tile to issue, at sequence offset ipos
+        int64_t ipos = lo;
 
-    // Every step issues one tile, past the end of the range a repeat of the range's last tile (read from L2 and never
-    // computed): with the same number of loads issued on every path through the loop, the wait before a tile's use
-    // counts the younger tiles' loads and leaves them in flight.
-    auto issue_next = [&](T& buf, Cursor& slot) __attribute__((always_inline)) {
-        issue_tile<D, FMT, NB>(p, icur, n, g, lane, win, buf);
-        slot = icur;
-        if (ipos < hi) {
-            if (ipos + 1 < hi) advance(p, icur);
-            ++ipos;
+        // Every step issues one tile, past the end of the range a repeat of the range's last tile (read from L2 and never
+        // computed): with the same number of loads issued on every path through the loop, the wait before a tile's use
+        // counts the younger tiles' loads and leaves them in flight.
+        auto issue_next = [&](T& buf, Cursor& slot) __attribute__((always_inline)) {
+            if constexpr (kRowQ)
+                issue_tile_rq<D, FMT, NB>(p, icur, n, g, lane, win, buf, q_next, icur.t == 0 || ipos == lo);
+            else
+                issue_tile<D, FMT, NB>(p, icur, n, g, lane, win, buf);
+            slot = icur;
+            if (ipos < hi) {
+                if (ipos + 1 < hi) advance(p, icur, small ? &rt : nullptr);
+                ++ipos;
+            }
+        };
+#pragma unroll
+        for (int s = 0; s + 1 < NBUF; ++s) issue_next(bufs[s], cs[s]);
+
+        int64_t pos = lo;
+        // computes the tile held in buffer I (the loop is unrolled by NBUF so that every buffer index is a constant)
+        auto step = [&](auto tag) __attribute__((always_inline)) -> bool {
+            constexpr int I = decltype(tag)::value;
+            constexpr int J = (I + NBUF - 1) % NBUF;
+            if constexpr (kRowQ) {
+                // the row's query operand moves to q_row before the next issue may reload q_next
+                cur = cs[I];
+                if (cur.t == 0 || pos == lo)
+#pragma unroll
+                    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                        for (int j = 0; j < KS; ++j) q_row[nb][j] = q_next[nb][j];
+                issue_next(bufs[J], cs[J]);
+            } else {
+                issue_next(bufs[J], cs[J]);
+                cur = cs[I];
+            }
+            if (cur.t == 0 && pos != lo) begin_row(cur);
+            compute(bufs[I]);
+            const bool more = pos + 1 < hi;
+            if (cur.t + 1 == cur.row.tiles || !more) {
+                finish(cur, seg_begin, pos + 1, first_segment);
+                first_segment = false;
+                seg_begin = pos + 1;
+            }
+            ++pos;
+            return more;
+        };
+        if constexpr (NBUF == 1) {
+            while (step(std::integral_constant<int, 0>{})) {
+            }
+        } else if constexpr (NBUF == 2) {
+            while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{})) {
+            }
+        } else {
+            static_assert(NBUF == 3, "1 to 3 tile buffers");
+            while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{}) &&
+                   step(std::integral_constant<int, 2>{})) {
+            }
         }
     };
-#pragma unroll
-    for (int s = 0; s + 1 < NBUF; ++s) issue_next(bufs[s], cs[s]);
-
-    int64_t pos = lo;
-    // computes the tile held in buffer I (the loop is unrolled by NBUF so that every buffer index is a constant)
-    auto step = [&](auto tag) __attribute__((always_inline)) -> bool {
-        constexpr int I = decltype(tag)::value;
-        constexpr int J = (I + NBUF - 1) % NBUF;
-        issue_next(bufs[J], cs[J]);
-        cur = cs[I];
-        if (cur.t == 0 && pos != lo) begin_row(cur);
-        compute(bufs[I]);
-        const bool more = pos + 1 < hi;
-        if (cur.t + 1 == cur.row.tiles || !more) {
-            finish(cur, seg_begin, pos + 1, first_segment);
-            first_segment = false;
-            seg_begin = pos + 1;
-        }
-        ++pos;
-        return more;
-    };
-    if constexpr (NBUF == 1) {
-        while (step(std::integral_constant<int, 0>{})) {
-        }
-    } else if constexpr (NBUF == 2) {
-        while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{})) {
-        }
+    if constexpr (WAVES == 1) {
+        pipeline();
     } else {
-        static_assert(NBUF == 3, "1 to 3 tile buffers");
-        while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{}) &&
-               step(std::integral_constant<int, 2>{})) {
-        }
+        if (lo < hi) pipeline();
+        merge_pieces();
     }
 }
 
@@ -550,15 +756,22 @@ int stages_cap() {
     return cap;
 }
 
+// The kernel instance for the tile-buffer count, and its waves per workgroup.
+using KernelFn = decltype(&paged_attention_kernel<64, BF16, 1, 1>);
+struct Instance {
+    KernelFn kernel;
+    int waves;
+};
+
 template <int D, int FMT, int NB>
-auto kernel_of() {
+Instance kernel_of() {
     constexpr int M = max_stages<D, FMT, NB>();
     const int s = stages_cap() < M ? stages_cap() : M;
     if constexpr (M >= 3)
-        if (s == 3) return paged_attention_kernel<D, FMT, NB, 3>;
+        if (s == 3) return {paged_attention_kernel<D, FMT, NB, 3>, wg_waves<D, NB, 3>()};
     if constexpr (M >= 2)
-        if (s >= 2) return paged_attention_kernel<D, FMT, NB, 2>;
-    return paged_attention_kernel<D, FMT, NB, 1>;
+        if (s >= 2) return {paged_attention_kernel<D, FMT, NB, 2>, wg_waves<D, NB, 2>()};
+    return {paged_attention_kernel<D, FMT, NB, 1>, wg_waves<D, NB, 1>()};
 }
 
 // Calls f.template run<D, FMT, NB>() for the instance of (head dim, format, 16-row column blocks).
@@ -595,30 +808,32 @@ struct Launch {
     const PagedParams* p;
     template <int D, int FMT, int NB>
     int run() const {
-        const auto kernel = kernel_of<D, FMT, NB>();
-        hipLaunchKernelGGL(kernel, dim3(p->grid), dim3(64), 0, stream, *p);
+        const Instance in = kernel_of<D, FMT, NB>();
+        hipLaunchKernelGGL(in.kernel, dim3(p->grid), dim3(64 * in.waves), 0, stream, *p);
         return check_launch("paged_attention_kernel");
     }
 };
 
 struct Occupancy {
     int* per_cu;
+    int* waves;
     template <int D, int FMT, int NB>
     int run() const {
         int blocks = 0;
-        const auto kernel = kernel_of<D, FMT, NB>();
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, 64, 0) != hipSuccess ||
+        const Instance in = kernel_of<D, FMT, NB>();
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, in.kernel, 64 * in.waves, 0) != hipSuccess ||
             blocks <= 0)
             blocks = 1;
         *per_cu = blocks;
+        *waves = in.waves;
         return 0;
     }
 };
 
 }  // namespace
 
-int paged_resident_waves(int head_dim, int format, int rows, int* per_cu) {
-    return dispatch(head_dim, format, rows, Occupancy{per_cu});
+int paged_resident_groups(int head_dim, int format, int rows, int* per_cu, int* waves) {
+    return dispatch(head_dim, format, rows, Occupancy{per_cu, waves});
 }
 
 int paged_attention(const PagedParams& p, hipStream_t stream) {

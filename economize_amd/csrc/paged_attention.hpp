@@ -30,16 +30,16 @@ struct PagedParams {
     const float* v_scale;
     const float* sinks;  // optional [Hq] logits
     int32_t* counters;  // [B * Hkv], zero between calls (the merging wave resets its row's counter)
-    float* part;        // [2 * grid, rows, D + 2]: per slot the maxima, sums and accumulators of a row segment
+    float* part;        // [2 * grid, rows, D + 2]: per workgroup two slots of a row segment's maxima, sums, accumulators
     uint16_t* out;  // bf16 [B, Q, Hq, D], channel stride 1
     int64_t so_b, so_q, so_h;
     int batch, queries, q_heads, kv_heads, groups, rows, head_dim, kv_format;
-    int grid;  // single-wave workgroups launched
+    int grid;  // workgroups launched
     float scale, softcap;
 };
 
-// Resident single-wave workgroups per CU of the kernel instance for this shape.
-int paged_resident_waves(int head_dim, int format, int rows, int* per_cu);
+// Resident workgroups per CU of the kernel instance for this shape, and its waves per workgroup.
+int paged_resident_groups(int head_dim, int format, int rows, int* per_cu, int* waves);
 int paged_attention(const PagedParams& p, hipStream_t stream);
 
 }  // namespace eco

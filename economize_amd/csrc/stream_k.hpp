@@ -159,9 +159,49 @@ __device__ inline Cursor locate(const P& p, int64_t x, int lane) {
     return c;
 }
 
-// The next tile (called only when one exists).
+// Batches of at most 64 rows: lane b holds row b's geometry and the inclusive sum of the tile counts (times the KV
+// heads) up to it, from one load of the lengths; the total, the cursor of an offset and the next row then come from
+// lane reads instead of loads.
+struct RowTable {
+    Row row;
+    int64_t incl;
+};
+
 template <typename P>
-__device__ inline void advance(const P& p, Cursor& c) {
+__device__ inline RowTable row_table(const P& p, int lane) {
+    RowTable t;
+    t.row = lane < p.batch ? row_of(p, lane) : Row{0, 0, 0, 0};
+    t.incl = wave_inclusive_sum(static_cast<int64_t>(t.row.tiles) * p.kv_heads, lane);
+    return t;
+}
+
+__device__ inline Row row_at(const RowTable& t, int b) {
+    Row r;
+    r.len = __builtin_amdgcn_readlane(t.row.len, b);
+    r.done = __builtin_amdgcn_readlane(t.row.done, b);
+    r.n_virt = __builtin_amdgcn_readlane(t.row.n_virt, b);
+    r.tiles = __builtin_amdgcn_readlane(t.row.tiles, b);
+    return r;
+}
+
+// The cursor of sequence offset x < total, from the row table.
+template <typename P>
+__device__ inline Cursor locate_in(const P& p, const RowTable& t, int64_t x) {
+    Cursor c{};
+    const int b = uniform(__builtin_ctzll(__ballot(t.incl > x)));
+    c.b = b;
+    c.row = row_at(t, b);
+    const int64_t start_b = uniform64(__shfl(t.incl, b)) - static_cast<int64_t>(c.row.tiles) * p.kv_heads;
+    const int64_t off = x - start_b;
+    c.kvh = uniform(static_cast<int>(off / c.row.tiles));
+    c.t = uniform(static_cast<int>(off % c.row.tiles));
+    c.row_start = uniform64(start_b + static_cast<int64_t>(c.kvh) * c.row.tiles);
+    return c;
+}
+
+// The next tile (called only when one exists); rows come from the table when one is given.
+template <typename P>
+__device__ inline void advance(const P& p, Cursor& c, const RowTable* table = nullptr) {
     if (++c.t < c.row.tiles) return;
     c.row_start += c.row.tiles;
     c.t = 0;
@@ -169,11 +209,15 @@ __device__ inline void advance(const P& p, Cursor& c) {
     c.kvh = 0;
     do {
         c.b = uniform(c.b + 1);
-        c.row = row_of<true>(p, c.b);
-        c.row.len = uniform(c.row.len);
-        c.row.done = uniform(c.row.done);
-        c.row.n_virt = uniform(c.row.n_virt);
-        c.row.tiles = uniform(c.row.tiles);
+        if (table) {
+            c.row = row_at(*table, c.b);
+        } else {
+            c.row = row_of<true>(p, c.b);
+            c.row.len = uniform(c.row.len);
+            c.row.done = uniform(c.row.done);
+            c.row.n_virt = uniform(c.row.n_virt);
+            c.row.tiles = uniform(c.row.tiles);
+        }
     } while (c.row.tiles == 0 && c.b + 1 < p.batch);
 }
 

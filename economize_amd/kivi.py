@@ -22,6 +22,7 @@ import torch
 
 from . import _lib
 from .errors import ConfigError
+from .paged import cached_workspace, counter_bytes
 
 __all__ = ["KIVI_PAGE", "PagedKIVICache", "kivi_append", "kivi_commit", "kivi_decode_attention", "kivi_quantize"]
 
@@ -188,9 +189,6 @@ def kivi_commit(cache: PagedKIVICache, block_table: torch.Tensor, committed: tor
     return ranges
 
 
-_workspaces: dict[tuple[torch.device, int], torch.Tensor] = {}
-
-
 def kivi_decode_attention(query: torch.Tensor, cache: PagedKIVICache, block_table: torch.Tensor,
                           seq_lens: torch.Tensor, max_seq_len: int, scale: float | None = None,
                           softcap: float | None = None, sinks: torch.Tensor | None = None,
@@ -222,10 +220,7 @@ def kivi_decode_attention(query: torch.Tensor, cache: PagedKIVICache, block_tabl
     need = int(_lib.lib().eco_kivi_decode_workspace_size(batch, queries, q_heads, cache.kv_heads, head_dim,
                                                          int(max_seq_len), cache.bits))
     if workspace is None:
-        key = (device, torch.cuda.current_stream(device).cuda_stream)
-        workspace = _workspaces.get(key)
-        if workspace is None or workspace.numel() < need:
-            workspace = _workspaces[key] = torch.zeros(max(need, 1), dtype=torch.uint8, device=device)
+        workspace = cached_workspace(need, counter_bytes(batch, cache.kv_heads), device)
     scale = 1.0 / math.sqrt(head_dim) if scale is None else float(scale)
     _lib.call(
         "eco_kivi_decode", query.data_ptr(), query.stride(0), query.stride(1), query.stride(2),

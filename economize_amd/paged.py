@@ -139,22 +139,46 @@ def workspace_size(batch: int, queries: int, q_heads: int, kv_heads: int, head_d
 
 
 def new_workspace(nbytes: int, device: torch.device | str) -> torch.Tensor:
-    """A workspace for :func:`paged_decode_attention`: zeroed, since the split counters at its start must be zero
-    before the first call (every call leaves them zero). One workspace serves one stream at a time."""
+    """A workspace for :func:`paged_decode_attention`: zeroed, since the row counters at its start must be zero when a
+    call starts. A call leaves its counters zero but may write anything after them: a workspace passed to calls with
+    more rows times KV heads than the previous call needs the bytes between cleared first (:class:`CachedWorkspace`
+    does this for the workspace used when none is passed). One workspace serves one stream at a time."""
     return torch.zeros(max(int(nbytes), 1), dtype=torch.uint8, device=device)
 
 
-_workspaces: dict[tuple[torch.device, int], torch.Tensor] = {}
+def counter_bytes(batch: int, kv_heads: int) -> int:
+    """Bytes of the row counters at the start of a decode workspace (int32 per row and KV head, 256-byte aligned).
+    They must be zero when a call starts; a call leaves them zero and may write anything after them."""
+    return (4 * batch * kv_heads + 255) // 256 * 256
 
 
-def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
-    """The cached workspace of ``device`` (grown on demand) used when the caller passes none."""
-    stream = torch.cuda.current_stream(device).cuda_stream
-    key = (device, stream)
-    ws = _workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = _workspaces[key] = new_workspace(max(nbytes, 2 * (ws.numel() if ws is not None else 0)), device)
-    return ws
+class CachedWorkspace:
+    """A workspace reused across calls of any shape on one stream, grown on demand. It tracks the prefix known to be
+    zero: a call leaves its counters zero and may dirty everything after them, so a later call with more counters
+    first clears the bytes between."""
+
+    def __init__(self) -> None:
+        self.buffer: torch.Tensor | None = None
+        self.zero_prefix = 0
+
+    def take(self, nbytes: int, counters: int, device: torch.device) -> torch.Tensor:
+        if self.buffer is None or self.buffer.numel() < nbytes:
+            size = max(nbytes, 2 * (self.buffer.numel() if self.buffer is not None else 0))
+            self.buffer = new_workspace(size, device)
+            self.zero_prefix = self.buffer.numel()
+        if counters > self.zero_prefix:
+            self.buffer[self.zero_prefix:counters].zero_()
+        self.zero_prefix = counters
+        return self.buffer
+
+
+_workspaces: dict[tuple[torch.device, int], CachedWorkspace] = {}
+
+
+def cached_workspace(nbytes: int, counters: int, device: torch.device) -> torch.Tensor:
+    """The workspace of ``device``'s current stream used when the caller passes none (see :class:`CachedWorkspace`)."""
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    return _workspaces.setdefault(key, CachedWorkspace()).take(nbytes, counters, device)
 
 
 def paged_decode_attention(
@@ -222,7 +246,7 @@ def paged_decode_attention(
     need = workspace_size(batch, queries, q_heads, cache.kv_heads, head_dim, max_seq_len, n_sel, cache.dtype,
                           list_page_size)
     if workspace is None:
-        workspace = _workspace(need, device)
+        workspace = cached_workspace(need, counter_bytes(batch, cache.kv_heads), device)
     scale = 1.0 / math.sqrt(head_dim) if scale is None else float(scale)
     _lib.call(
         "eco_paged_decode",

@@ -57,8 +57,10 @@ int eco_fp8_scales_from_absmax(const uint32_t* absmax_bits, int32_t heads, int32
                                void* stream);
 
 /* Workspace bytes eco_paged_decode needs for this shape (n_sel = Quest's selected pages of list_page_size tokens,
- * 0 without). The workspace starts with per-row counters that must be zero before its first use; every call leaves
- * them zero. One workspace serves one stream at a time. */
+ * 0 without). The workspace starts with per-row counters, int32 per batch row and KV head, padded to 256 bytes,
+ * which must be zero when a call starts; every call leaves them zero and may write anything after them, so a call
+ * with more rows times KV heads than the previous one on the same workspace needs the bytes between cleared first.
+ * One workspace serves one stream at a time. */
 size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
                                        int32_t head_dim, int32_t max_seq_len, int32_t n_sel, int32_t list_page_size,
                                        int32_t kv_format);
@@ -146,7 +148,7 @@ int eco_kivi_ring_write(const void* k_new, const void* v_new, int32_t in_format,
                         void* k_ring, void* v_ring, int32_t batch, int32_t kv_heads, int32_t head_dim, int32_t ring,
                         void* stream);
 
-/* Workspace bytes eco_kivi_decode needs (zero before its first use; every call leaves its counters zero). */
+/* Workspace bytes eco_kivi_decode needs; the same layout and counter rule as eco_paged_decode's workspace. */
 size_t eco_kivi_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
                                       int32_t head_dim, int32_t max_seq_len, int32_t bits);
 

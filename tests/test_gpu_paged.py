@@ -50,6 +50,7 @@ CASES = [
     (1, 1, 32, 8, 128, [32768], torch.float8_e4m3fn),  # rows cut into many waves' ranges
     (40, 1, 8, 1, 128, [3 + 97 * i for i in range(40)], torch.float8_e4m3fn),  # many short rows per wave
     (5, 2, 8, 2, 64, [300, 0, 0, 17, 1], torch.bfloat16),  # empty rows between others
+    (70, 1, 8, 2, 64, [(37 * i) % 700 for i in range(70)], torch.float8_e4m3fn),  # more than 64 batch rows
 ]
 
 

@@ -140,3 +140,21 @@ def test_forward_refuses_what_the_paged_kernels_do_not_take() -> None:
         PagedKV(object(), table, torch.tensor([5], dtype=torch.int32), 5)
     fp8 = PagedKV(PagedKVCache.empty(2, 1, 64, torch.float8_e5m2, "cpu"), table, kv.seq_lens, 5)
     assert fp8.format == "fp8"
+
+
+def test_cached_workspace_clears_counters_a_previous_call_may_have_dirtied() -> None:
+    """A call leaves its counters zero and may write partials after them; a later call with more counters gets the
+    bytes in between cleared (a stale partial byte read as a counter miscounts a row's pieces)."""
+    from economize_amd.paged import CachedWorkspace, counter_bytes
+
+    assert counter_bytes(1, 1) == 256 and counter_bytes(70, 2) == 768 and counter_bytes(64, 1) == 256
+    ws = CachedWorkspace()
+    buf = ws.take(4096, counter_bytes(8, 8), "cpu")  # 256 counter bytes
+    assert ws.zero_prefix == 256 and int(buf.sum()) == 0
+    buf[256:].fill_(7)  # the call's partials
+    again = ws.take(4096, counter_bytes(8, 8), "cpu")
+    assert again is buf and int(buf[256:300].sum()) > 0  # same counters: nothing to clear
+    ws.take(4096, counter_bytes(70, 2), "cpu")  # 768 counter bytes
+    assert int(buf[:768].sum()) == 0 and int(buf[768:].min()) == 7
+    grown = ws.take(8192, counter_bytes(70, 2), "cpu")
+    assert grown.numel() == 8192 and int(grown.sum()) == 0
