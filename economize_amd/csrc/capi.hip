@@ -69,6 +69,9 @@ int paged_grid(int batch, int kv_heads, int rows, int head_dim, int format, int 
     int64_t grid = forced > 0 ? forced : static_cast<int64_t>(device_cus()) * per_cu;
     const int64_t cap = (tiles + 4 * waves - 1) / (4 * waves);  // at least four tiles per wave
     grid = grid < cap ? grid : cap;
+    // short rows (Quest's selected pages): one workgroup per row, so that every row is merged inside its workgroup
+    const int64_t rows_total = static_cast<int64_t>(batch) * kv_heads;
+    if (forced <= 0 && (row_pages + 3) / 4 <= 8 * waves && rows_total < grid) grid = rows_total;
     return static_cast<int>(grid < 1 ? 1 : grid);
 }
 
@@ -484,7 +487,8 @@ int eco_quest_page_bounds(const void* k_cache, int32_t kv_format, int32_t num_pa
 
 size_t eco_quest_select_workspace_size(int32_t batch, int32_t kv_heads, int32_t max_done) {
     if (batch <= 0 || kv_heads <= 0 || max_done < 0) return 0;
-    return align256(static_cast<size_t>(batch) * kv_heads * (max_done > 0 ? max_done : 1) * sizeof(float));
+    const size_t stride = (static_cast<size_t>(max_done > 0 ? max_done : 1) + 3) / 4 * 4;  // 16-byte aligned rows
+    return align256(static_cast<size_t>(batch) * kv_heads * stride * sizeof(float));
 }
 
 int eco_quest_select(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* kmin, const void* kmax,

@@ -27,6 +27,9 @@ namespace {
 
 constexpr int PAGE = 16;
 constexpr int SCORE_PASSES = 4;  // pages per scoring thread
+
+// Scores of a (row, KV head) in the workspace: max_done floats, rows 16-byte aligned.
+__host__ __device__ inline int64_t score_stride(int max_done) { return (max_done + 3) & ~3; }
 constexpr int TOPK_LDS_KEYS = 15360;  // rows of at most this many committed pages select from keys held in LDS (60 KiB)
 
 template <int FMT>
@@ -134,17 +137,27 @@ __global__ __launch_bounds__(256) void quest_score_kernel(SelectParams p) {
     }
     for (int d = threadIdx.x; d < p.head_dim; d += blockDim.x) {
         float s = 0.0f, a = 0.0f;
-        for (int r = 0; r < rows; ++r) {
-            const int g = r / p.queries, qi = r % p.queries;
-            const float x = bf16_to_f32(p.q[b * p.sq_b + qi * p.sq_q + (kvh * p.groups + g) * p.sq_h + d]);
-            s = r == 0 ? x : s + x;
-            a = r == 0 ? fabsf(x) : a + fabsf(x);
+        // rows added in order; the loads of 8 rows are in flight together
+        for (int r0 = 0; r0 < rows; r0 += 8) {
+            float x[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int r = r0 + u < rows ? r0 + u : r0;
+                const int g = r / p.queries, qi = r % p.queries;
+                x[u] = bf16_to_f32(p.q[b * p.sq_b + qi * p.sq_q + (kvh * p.groups + g) * p.sq_h + d]);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (r0 + u >= rows) break;
+                s = r0 + u == 0 ? x[u] : s + x[u];
+                a = r0 + u == 0 ? fabsf(x[u]) : a + fabsf(x[u]);
+            }
         }
         qsum[d] = s;
         qabs[d] = a;
     }
     __syncthreads();
-    float* out = p.scores + static_cast<int64_t>(row) * p.max_done;
+    float* out = p.scores + static_cast<int64_t>(row) * score_stride(p.max_done);
 #pragma unroll
     for (int k = 0; k < SCORE_PASSES; ++k) {
         const int page = p0 + k * per_pass + static_cast<int>(threadIdx.x) / L;
@@ -208,10 +221,11 @@ __global__ __launch_bounds__(256) void quest_topk_kernel(SelectParams p) {
     const int row = blockIdx.x;
     const int b = row / p.kv_heads;
     const int t = threadIdx.x;
+    const int lane = t & 63;
     const int n = min(max(p.done[b], 0), p.max_done);
     const int count = min(p.pages, p.max_done);
     int32_t* out = p.out + static_cast<int64_t>(row) * p.pages;
-    const float* scores = p.scores + static_cast<int64_t>(row) * p.max_done;
+    const float* scores = p.scores + static_cast<int64_t>(row) * score_stride(p.max_done);
     int total = 0;
     if (n <= count) {  // every committed page
         for (int i = t; i < p.pages; i += 256) out[i] = i < n ? i : -1;
@@ -234,9 +248,19 @@ __global__ __launch_bounds__(256) void quest_topk_kernel(SelectParams p) {
     for (int shift = 24; shift >= 0; shift -= 8) {
         hist[t] = 0;
         __syncthreads();
-        for (int i = t; i < n; i += 256) {
-            const uint32_t key = key_at(i);
-            if (((key ^ prefix) & known) == 0) atomicAdd(&hist[(key >> shift) & 255], 1);
+        for (int i0 = t - lane; i0 < n; i0 += 256) {
+            // the wave's keys of this round: lanes whose digit equals the first matching lane's add as one
+            const int i = i0 + lane;
+            const uint32_t key = i < n ? key_at(i) : 0u;
+            const bool match = i < n && ((key ^ prefix) & known) == 0;
+            const int digit = static_cast<int>((key >> shift) & 255u);
+            const uint64_t matching = __ballot(match);
+            if (matching == 0) continue;
+            const int leader = __builtin_ctzll(matching);
+            const int lead_digit = __shfl(digit, leader);
+            const uint64_t same = __ballot(match && digit == lead_digit);
+            if (lane == leader) atomicAdd(&hist[lead_digit], static_cast<int>(__popcll(same)));
+            if (match && digit != lead_digit) atomicAdd(&hist[digit], 1);
         }
         __syncthreads();
         const int c = hist[255 - t];  // thread t counts digit 255 - t: the scan runs from the largest digit down
