@@ -94,10 +94,10 @@ int kivi_grid(int batch, int kv_heads, int rows, int head_dim, int bits, int max
         return env ? std::atoi(env) : 0;
     }();
     const int64_t tiles = static_cast<int64_t>(batch) * kv_heads * ((max_seq_len + 31) / 32);
-    int per_cu = 1;
-    if (kivi_resident_waves(head_dim, bits, rows, &per_cu)) return 0;
+    int per_cu = 1, waves = 1;
+    if (kivi_resident_groups(head_dim, bits, rows, &per_cu, &waves)) return 0;
     int64_t grid = forced > 0 ? forced : static_cast<int64_t>(device_cus()) * per_cu;
-    const int64_t cap = (tiles + 3) / 4;
+    const int64_t cap = (tiles + 4 * waves - 1) / (4 * waves);  // at least four tiles per wave
     grid = grid < cap ? grid : cap;
     return static_cast<int>(grid < 1 ? 1 : grid);
 }

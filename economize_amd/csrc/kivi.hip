@@ -353,17 +353,27 @@ __device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c,
 
 }  // namespace
 
+// Waves of a workgroup: four for one column block (pieces of rows inside the workgroup merge through LDS, as in
+// paged_attention.hip), else one.
+template <int D, int NB>
+constexpr int kivi_wg_waves() {
+    return NB == 1 && D <= 128 ? 4 : 1;
+}
+
 template <int D, int BITS, int NB, int NBUF>
-__global__ __launch_bounds__(64) void kivi_attention_kernel(KiviParams p) {
+__global__ __launch_bounds__((64 * kivi_wg_waves<D, NB>())) void kivi_attention_kernel(KiviParams p) {
     using T = KTile<D, BITS>;
     constexpr int KS = T::KS, ND = T::ND, VG = T::VG;
     constexpr int R = NB * 16;  // query rows of the MFMA columns
-    __shared__ uint4 q_bf[R][D / 8];
+    constexpr int WAVES = kivi_wg_waves<D, NB>();
+    __shared__ uint4 q_lds[WAVES][R][D / 8];  // each wave's current query rows
 
-    const int lane = threadIdx.x;
+    const int lane = WAVES > 1 ? static_cast<int>(threadIdx.x) & 63 : static_cast<int>(threadIdx.x);
+    const int wave = WAVES > 1 ? uniform(static_cast<int>(threadIdx.x) >> 6) : 0;
+    auto& q_bf = q_lds[wave];
     const int n = lane & 15;
     const int g = lane >> 4;
-    const int w = blockIdx.x;
+    const int w = blockIdx.x;  // workgroup
     const int grid = gridDim.x;
 
     // row geometry: one load of the lengths for batches of at most 64 rows
@@ -371,14 +381,21 @@ __global__ __launch_bounds__(64) void kivi_attention_kernel(KiviParams p) {
     RowTable rt{};
     if (small) rt = row_table(p, lane);
     const int64_t total = small ? uniform64(__shfl(rt.incl, 63)) : uniform64(total_tiles(p, lane));
-    for (int b = w; b < p.batch; b += grid) {  // rows without a key: zeros
+    for (int b = w * WAVES + wave; b < p.batch; b += grid * WAVES) {  // rows without a key: zeros
         if ((small ? __builtin_amdgcn_readlane(rt.row.tiles, b) : row_of(p, b).tiles) == 0)
             for (int idx = lane; idx < p.kv_heads * p.rows * D; idx += 64)
                 store_output(p, b, idx / (p.rows * D), (idx / D) % p.rows, idx % D, 0.0f, -INFINITY, 0.0f);
     }
-    const int64_t lo = total * w / grid;
-    const int64_t hi = total * (w + 1) / grid;
-    if (lo >= hi) return;
+    const int64_t wlo = total * w / grid;  // the workgroup's tile range
+    const int64_t whi = total * (w + 1) / grid;
+    const int64_t lo = wlo + (whi - wlo) * wave / WAVES;  // this wave's part of it
+    const int64_t hi = wlo + (whi - wlo) * (wave + 1) / WAVES;
+    __shared__ typename std::conditional<(WAVES > 1), Pieces<D, WAVES>, char>::type pieces;
+    if constexpr (WAVES > 1) {
+        clear_pieces(pieces, wave, lane);
+    } else {
+        if (lo >= hi) return;
+    }
 
     // ---- row state ----
     float limit[NB];
@@ -408,11 +425,10 @@ __global__ __launch_bounds__(64) void kivi_attention_kernel(KiviParams p) {
         for (int nb = 0; nb < NB; ++nb) {
             const int r = nb * 16 + n;
             limit[nb] = r < p.rows ? static_cast<float>(c.row.len - p.queries + r % p.queries + 1) : 0.0f;
+            // the accumulators are cleared by the row's first rescale (m_i = -inf marks a row with no weight yet),
+            // so that a row change does not give them a second register version to merge at every tile
             m_i[nb] = -INFINITY;
             l_i[nb] = 0.0f;
-            gam[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
     };
     const float score_scale = p.softcap > 0.0f ? p.scale : p.scale * kLog2e;
@@ -444,8 +460,10 @@ __global__ __launch_bounds__(64) void kivi_attention_kernel(KiviParams p) {
                     float c8[8];
                     codes_to_f32<BITS>(BITS == 4 ? tile.kc[v][j] : tile.kc[v][j / 2], j % 2, c8);
                     bf16x8 kv;
+                    // code * scale is exact in fp32 (a code of at most 4 bits times an fp16), so one fused
+                    // multiply-add rounds exactly as the reference's product then sum
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) kv[e] = static_cast<__bf16>(c8[e] * sf[e] + zf[e]);
+                    for (int e = 0; e < 8; ++e) kv[e] = static_cast<__bf16>(__builtin_fmaf(c8[e], sf[e], zf[e]));
 #pragma unroll
                     for (int nb = 0; nb < NB; ++nb)
                         s[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
@@ -524,13 +542,17 @@ __global__ __launch_bounds__(64) void kivi_attention_kernel(KiviParams p) {
             for (int v = 0; v < 2; ++v)
                 tile_max = fmaxf(fmaxf(tile_max, fmaxf(s[v][nb][0], s[v][nb][1])), fmaxf(s[v][nb][2], s[v][nb][3]));
             tile_max = group_max(tile_max);
-            if (__ballot(tile_max > m_i[nb] + 8.0f) != 0) {
+            if (__ballot(tile_max > m_i[nb] + 8.0f || m_i[nb] == -INFINITY) != 0) {
+                const bool fresh = m_i[nb] == -INFINITY;
                 const float m_new = fmaxf(m_i[nb], tile_max);
-                const float alpha = m_i[nb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_i[nb] - m_new);
+                const float alpha = fresh ? 0.0f : __builtin_amdgcn_exp2f(m_i[nb] - m_new);
                 l_i[nb] *= alpha;
-                gam[nb] *= alpha;
 #pragma unroll
-                for (int nd = 0; nd < ND; ++nd) acc[nd][nb] *= alpha;
+                for (int i = 0; i < 4; ++i) gam[nb][i] = fresh ? 0.0f : gam[nb][i] * alpha;
+#pragma unroll
+                for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[nd][nb][i] = fresh ? 0.0f : acc[nd][nb][i] * alpha;
                 m_i[nb] = m_new;
             }
             const float neg_m = m_i[nb] == -INFINITY ? 0.0f : -m_i[nb];
@@ -647,6 +669,11 @@ __global__ __launch_bounds__(64) void kivi_attention_kernel(KiviParams p) {
             }
             return;
         }
+        if constexpr (WAVES > 1) {
+            write_piece(pieces, 2 * wave + (first_segment ? 0 : 1), c, p.rows, n, g, lane, m_i[0], l_i[0],
+                        [&](int nd, int i) __attribute__((always_inline)) { return o[nd][0][i]; });
+            return;
+        }
         const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
         float* slot = p.part + (2 * static_cast<int64_t>(w) + (first_segment ? 0 : 1)) * stride;
 #pragma unroll
@@ -672,51 +699,65 @@ __global__ __launch_bounds__(64) void kivi_attention_kernel(KiviParams p) {
     };
 
     // ---- the tile pipeline (as in paged_attention.hip) ----
-    Cursor cur = small ? locate_in(p, rt, lo) : locate(p, lo, lane);
-    PageWindow win;
-    int64_t seg_begin = lo;
-    bool first_segment = true;
-    begin_row(cur);
-
-    T bufs[NBUF];
-    Cursor cs[NBUF];
-    Cursor icur = cur;
-    int64_t ipos = lo;
-    auto issue_next = [&](T& buf, Cursor& slot) __attribute__((always_inline)) {
-        issue_tile<D, BITS>(p, icur, n, g, lane, win, buf);
-        slot = icur;
-        if (ipos < hi) {
-            if (ipos + 1 < hi) advance(p, icur, small ? &rt : nullptr);
-            ++ipos;
-        }
-    };
+    auto pipeline = [&]() __attribute__((always_inline)) {
+        Cursor cur = small ? locate_in(p, rt, lo) : locate(p, lo, lane);
+        PageWindow win;
+        int64_t seg_begin = lo;
+        bool first_segment = true;
 #pragma unroll
-    for (int s = 0; s + 1 < NBUF; ++s) issue_next(bufs[s], cs[s]);
+        for (int nb = 0; nb < NB; ++nb) {
+            gam[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        begin_row(cur);
 
-    int64_t pos = lo;
-    auto step = [&](auto tag) __attribute__((always_inline)) -> bool {
-        constexpr int I = decltype(tag)::value;
-        constexpr int J = (I + NBUF - 1) % NBUF;
-        issue_next(bufs[J], cs[J]);
-        cur = cs[I];
-        if (cur.t == 0 && pos != lo) begin_row(cur);
-        compute(bufs[I], cur);
-        const bool more = pos + 1 < hi;
-        if (cur.t + 1 == cur.row.tiles || !more) {
-            finish(cur, seg_begin, pos + 1, first_segment);
-            first_segment = false;
-            seg_begin = pos + 1;
+        T bufs[NBUF];
+        Cursor cs[NBUF];
+        Cursor icur = cur;
+        int64_t ipos = lo;
+        auto issue_next = [&](T& buf, Cursor& slot) __attribute__((always_inline)) {
+            issue_tile<D, BITS>(p, icur, n, g, lane, win, buf);
+            slot = icur;
+            if (ipos < hi) {
+                if (ipos + 1 < hi) advance(p, icur, small ? &rt : nullptr);
+                ++ipos;
+            }
+        };
+#pragma unroll
+        for (int s = 0; s + 1 < NBUF; ++s) issue_next(bufs[s], cs[s]);
+
+        int64_t pos = lo;
+        auto step = [&](auto tag) __attribute__((always_inline)) -> bool {
+            constexpr int I = decltype(tag)::value;
+            constexpr int J = (I + NBUF - 1) % NBUF;
+            issue_next(bufs[J], cs[J]);
+            cur = cs[I];
+            if (cur.t == 0 && pos != lo) begin_row(cur);
+            compute(bufs[I], cur);
+            const bool more = pos + 1 < hi;
+            if (cur.t + 1 == cur.row.tiles || !more) {
+                finish(cur, seg_begin, pos + 1, first_segment);
+                first_segment = false;
+                seg_begin = pos + 1;
+            }
+            ++pos;
+            return more;
+        };
+        if constexpr (NBUF == 1) {
+            while (step(std::integral_constant<int, 0>{})) {
+            }
+        } else {
+            static_assert(NBUF == 2, "one or two tile buffers");
+            while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{})) {
+            }
         }
-        ++pos;
-        return more;
     };
-    if constexpr (NBUF == 1) {
-        while (step(std::integral_constant<int, 0>{})) {
-        }
+    if constexpr (WAVES == 1) {
+        pipeline();
     } else {
-        static_assert(NBUF == 2, "one or two tile buffers");
-        while (step(std::integral_constant<int, 0>{}) && step(std::integral_constant<int, 1>{})) {
-        }
+        if (lo < hi) pipeline();
+        merge_pieces<D, WAVES>(p, pieces, wave, lane, wlo, whi, total, grid, w);
     }
 }
 
@@ -728,6 +769,11 @@ template <int D, int BITS, int NB>
 auto kivi_kernel_of() {
     if constexpr (NB == 1) return kivi_attention_kernel<D, BITS, NB, 2>;
     return kivi_attention_kernel<D, BITS, NB, 1>;
+}
+
+template <int D, int NB>
+constexpr int kivi_block_threads() {
+    return 64 * kivi_wg_waves<D, NB>();
 }
 
 template <typename F>
@@ -757,20 +803,24 @@ struct KiviLaunch {
     template <int D, int BITS, int NB>
     int run() const {
         const auto kernel = kivi_kernel_of<D, BITS, NB>();
-        hipLaunchKernelGGL(kernel, dim3(p->grid), dim3(64), 0, stream, *p);
+        hipLaunchKernelGGL(kernel, dim3(p->grid), dim3(kivi_block_threads<D, NB>()), 0, stream, *p);
         return check_launch("kivi_attention_kernel");
     }
 };
 
 struct KiviOccupancy {
     int* per_cu;
+    int* waves;
     template <int D, int BITS, int NB>
     int run() const {
         int blocks = 0;
         const auto kernel = kivi_kernel_of<D, BITS, NB>();
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, 64, 0) != hipSuccess || blocks <= 0)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, kivi_block_threads<D, NB>(), 0) !=
+                hipSuccess ||
+            blocks <= 0)
             blocks = 1;
         *per_cu = blocks;
+        *waves = kivi_wg_waves<D, NB>();
         return 0;
     }
 };
@@ -800,8 +850,8 @@ int kivi_quantize(const KiviQuantParams& p, int kind, int max_tokens, hipStream_
     return check_launch(kind == 0 ? "kivi_quant_keys_kernel" : "kivi_quant_values_kernel");
 }
 
-int kivi_resident_waves(int head_dim, int bits, int rows, int* per_cu) {
-    return kivi_dispatch(head_dim, bits, rows, KiviOccupancy{per_cu});
+int kivi_resident_groups(int head_dim, int bits, int rows, int* per_cu, int* waves) {
+    return kivi_dispatch(head_dim, bits, rows, KiviOccupancy{per_cu, waves});
 }
 
 int kivi_attention(const KiviParams& p, hipStream_t stream) {

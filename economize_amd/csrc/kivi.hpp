@@ -82,7 +82,7 @@ int kivi_schedule(const int32_t* committed, int residual, int32_t* keys_quantize
                   int32_t* ranges, int batch, hipStream_t stream);
 int kivi_ring_write(const KiviRingParams& p, hipStream_t stream);
 int kivi_quantize(const KiviQuantParams& p, int kind, int max_tokens, hipStream_t stream);
-int kivi_resident_waves(int head_dim, int bits, int rows, int* per_cu);
+int kivi_resident_groups(int head_dim, int bits, int rows, int* per_cu, int* waves);  // workgroups per CU, waves per workgroup
 int kivi_attention(const KiviParams& p, hipStream_t stream);
 
 }  // namespace eco

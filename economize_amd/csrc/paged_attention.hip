@@ -296,15 +296,10 @@ paged_attention_kernel(PagedParams p) {
     const int64_t whi = total * (w + 1) / grid;
     const int64_t lo = wlo + (whi - wlo) * wave / WAVES;  // this wave's quarter of it
     const int64_t hi = wlo + (whi - wlo) * (wave + 1) / WAVES;
-    // Row pieces of the workgroup's waves (two per wave: its first and its last row segment, when they are not
-    // whole rows): maxima, sums and accumulators of at most 16 query rows, and the row they belong to.
-    constexpr int PIECE = WAVES > 1 ? 16 * (D + 2) : 1;
-    __shared__ float piece_data[WAVES > 1 ? 2 * WAVES : 1][PIECE];
-    __shared__ int64_t piece_row[WAVES > 1 ? 2 * WAVES : 1];  // row_start of the piece's row, -1 for none
-    __shared__ int piece_b[WAVES > 1 ? 2 * WAVES : 1], piece_kvh[WAVES > 1 ? 2 * WAVES : 1],
-        piece_tiles[WAVES > 1 ? 2 * WAVES : 1];
+    // row pieces of the workgroup's waves (stream_k.hpp)
+    __shared__ typename std::conditional<(WAVES > 1), Pieces<D, WAVES>, char>::type pieces;
     if constexpr (WAVES > 1) {
-        if (lane < 2) piece_row[2 * wave + lane] = -1;
+        clear_pieces(pieces, wave, lane);
     } else {
         if (lo >= hi) return;
     }
@@ -525,25 +520,8 @@ paged_attention_kernel(PagedParams p) {
             return;
         }
         if constexpr (WAVES > 1) {
-            const int k = 2 * wave + (first_segment ? 0 : 1);
-            float* piece = piece_data[k];
-            const int r = n;
-            if (r < p.rows) {
-                if (g == 0) {
-                    piece[r] = m_i[0];
-                    piece[p.rows + r] = l_i[0];
-                }
-#pragma unroll
-                for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) piece[2 * p.rows + r * D + 16 * nd + 4 * g + i] = acc[nd][0][i] * vs;
-            }
-            if (lane == 0) {
-                piece_row[k] = c.row_start;
-                piece_b[k] = c.b;
-                piece_kvh[k] = c.kvh;
-                piece_tiles[k] = c.row.tiles;
-            }
+            write_piece(pieces, 2 * wave + (first_segment ? 0 : 1), c, p.rows, n, g, lane, m_i[0], l_i[0],
+                        [&](int nd, int i) __attribute__((always_inline)) { return acc[nd][0][i] * vs; });
             return;
         }
         const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
@@ -570,81 +548,6 @@ paged_attention_kernel(PagedParams p) {
             prev = __hip_atomic_fetch_add(p.counters + c.b * p.kv_heads + c.kvh, 1, __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT);
         merge_row<D>(p, c, __shfl(prev, 0), total, grid, lane);
-    };
-
-    // ---- the workgroup's row pieces, merged by its first wave once every wave has finished its range ----
-    auto merge_pieces = [&]() __attribute__((always_inline)) {
-        if constexpr (WAVES > 1) {
-            __syncthreads();
-            if (wave != 0) return;
-            const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
-            int k = 0;
-            while (k < 2 * WAVES) {
-                const int64_t row = piece_row[k];
-                if (row < 0) {
-                    ++k;
-                    continue;
-                }
-                // the pieces of one row are consecutive among the valid ones (rows follow the tile order)
-                uint32_t members = 0;
-                int k2 = k;
-                while (k2 < 2 * WAVES && (piece_row[k2] == row || piece_row[k2] < 0)) {
-                    if (piece_row[k2] == row) members |= 1u << k2;
-                    ++k2;
-                }
-                Cursor c{};
-                c.b = piece_b[k];
-                c.kvh = piece_kvh[k];
-                c.row.tiles = piece_tiles[k];
-                c.row_start = row;
-                k = k2;
-                const bool inside = row >= wlo && row + c.row.tiles <= whi;
-                float* slot = p.part + (2 * static_cast<int64_t>(w) + (wlo < row ? 1 : 0)) * stride;
-                for (int base = 0; base < p.rows * D; base += 64 * 8) {
-                    const int e = base + lane * 8;
-                    const bool active = e < p.rows * D;
-                    const int r = active ? e / D : 0;
-                    const int d = active ? e % D : 0;
-                    float m = -INFINITY;
-                    for (int j = 0; j < 2 * WAVES; ++j)
-                        if ((members >> j) & 1u) m = fmaxf(m, piece_data[j][r]);
-                    float l = 0.0f, o[8];
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) o[i] = 0.0f;
-                    for (int j = 0; j < 2 * WAVES; ++j) {
-                        if (!((members >> j) & 1u)) continue;
-                        const float mj = piece_data[j][r];
-                        if (mj == -INFINITY) continue;
-                        const float cw = __builtin_amdgcn_exp2f(mj - m);
-                        l += piece_data[j][p.rows + r] * cw;
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) o[i] += piece_data[j][2 * p.rows + r * D + d + i] * cw;
-                    }
-                    if (!active) continue;
-                    if (inside) {
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) store_output(p, c.b, c.kvh, r, d + i, o[i], m, l);
-                    } else {
-                        if (d == 0) {
-                            coherent_store(slot + r, m);
-                            coherent_store(slot + p.rows + r, l);
-                        }
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) coherent_store(slot + 2 * p.rows + r * D + d + i, o[i]);
-                    }
-                }
-                if (!inside) {
-                    // the row is cut at a workgroup boundary: the workgroup's partial joins the others' in the
-                    // workspace, and the last workgroup to finish merges them
-                    __builtin_amdgcn_s_waitcnt(0);
-                    int prev = 0;
-                    if (lane == 0)
-                        prev = __hip_atomic_fetch_add(p.counters + c.b * p.kv_heads + c.kvh, 1, __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT);
-                    merge_row<D>(p, c, __shfl(prev, 0), total, grid, lane);
-                }
-            }
-        }
     };
 
     // ---- the tile pipeline: NBUF register buffers, tile pos + NBUF - 1 issued while tile pos is computed ----
@@ -728,7 +631,7 @@ paged_attention_kernel(PagedParams p) {
         pipeline();
     } else {
         if (lo < hi) pipeline();
-        merge_pieces();
+        merge_pieces<D, WAVES>(p, pieces, wave, lane, wlo, whi, total, grid, w);
     }
 }
 

@@ -338,5 +338,121 @@ __device__ inline void merge_row(const P& p, const Cursor& c, int prev, int64_t 
 }
 
 
+// ---- the pieces of rows inside one multi-wave workgroup ----------------------------------------------------------
+// Each wave of a workgroup takes a contiguous part of the workgroup's tile range; its first and last row segments
+// that are not whole rows are left in LDS as pieces (maxima, sums and output values of at most 16 query rows). After
+// a barrier the first wave merges the pieces of every row: a row inside the workgroup's range is written out, a row
+// cut at a range boundary becomes the workgroup's partial in the workspace (slot 0 when the row started before the
+// workgroup, else slot 1) and joins the counter merge of merge_row.
+template <int D, int WAVES>
+struct Pieces {
+    float data[2 * WAVES][16 * (D + 2)];
+    int64_t row[2 * WAVES];  // row_start of the piece's row, -1 for none
+    int b[2 * WAVES], kvh[2 * WAVES], tiles[2 * WAVES];
+};
+
+template <int D, int WAVES>
+__device__ inline void clear_pieces(Pieces<D, WAVES>& pc, int wave, int lane) {
+    if (lane < 2) pc.row[2 * wave + lane] = -1;
+}
+
+// Stores the segment of row c as piece k: lane (n, g) holds query row n's output channels 16 nd + 4 g + i
+// (value(nd, i)), and m, l of row n.
+template <int D, int WAVES, typename V>
+__device__ __forceinline__ void write_piece(Pieces<D, WAVES>& pc, int k, const Cursor& c, int rows, int n, int g,
+                                            int lane, float m, float l, V value) {
+    float* piece = pc.data[k];
+    if (n < rows) {
+        if (g == 0) {
+            piece[n] = m;
+            piece[rows + n] = l;
+        }
+#pragma unroll
+        for (int nd = 0; nd < D / 16; ++nd)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) piece[2 * rows + n * D + 16 * nd + 4 * g + i] = value(nd, i);
+    }
+    if (lane == 0) {
+        pc.row[k] = c.row_start;
+        pc.b[k] = c.b;
+        pc.kvh[k] = c.kvh;
+        pc.tiles[k] = c.row.tiles;
+    }
+}
+
+template <int D, int WAVES, typename P>
+__device__ inline void merge_pieces(const P& p, Pieces<D, WAVES>& pc, int wave, int lane, int64_t wlo, int64_t whi,
+                                    int64_t total, int grid, int w) {
+    __syncthreads();
+    if (wave != 0) return;
+    const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
+    int k = 0;
+    while (k < 2 * WAVES) {
+        const int64_t row = pc.row[k];
+        if (row < 0) {
+            ++k;
+            continue;
+        }
+        // the pieces of one row are consecutive among the valid ones (rows follow the tile order)
+        uint32_t members = 0;
+        int k2 = k;
+        while (k2 < 2 * WAVES && (pc.row[k2] == row || pc.row[k2] < 0)) {
+            if (pc.row[k2] == row) members |= 1u << k2;
+            ++k2;
+        }
+        Cursor c{};
+        c.b = pc.b[k];
+        c.kvh = pc.kvh[k];
+        c.row.tiles = pc.tiles[k];
+        c.row_start = row;
+        k = k2;
+        const bool inside = row >= wlo && row + c.row.tiles <= whi;
+        float* slot = p.part + (2 * static_cast<int64_t>(w) + (wlo < row ? 1 : 0)) * stride;
+        for (int base = 0; base < p.rows * D; base += 64 * 8) {
+            const int e = base + lane * 8;
+            const bool active = e < p.rows * D;
+            const int r = active ? e / D : 0;
+            const int d = active ? e % D : 0;
+            float m = -INFINITY;
+            for (int j = 0; j < 2 * WAVES; ++j)
+                if ((members >> j) & 1u) m = fmaxf(m, pc.data[j][r]);
+            float l = 0.0f, o[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = 0.0f;
+            for (int j = 0; j < 2 * WAVES; ++j) {
+                if (!((members >> j) & 1u)) continue;
+                const float mj = pc.data[j][r];
+                if (mj == -INFINITY) continue;
+                const float cw = __builtin_amdgcn_exp2f(mj - m);
+                l += pc.data[j][p.rows + r] * cw;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o[i] += pc.data[j][2 * p.rows + r * D + d + i] * cw;
+            }
+            if (!active) continue;
+            if (inside) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) store_output(p, c.b, c.kvh, r, d + i, o[i], m, l);
+            } else {
+                if (d == 0) {
+                    coherent_store(slot + r, m);
+                    coherent_store(slot + p.rows + r, l);
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) coherent_store(slot + 2 * p.rows + r * D + d + i, o[i]);
+            }
+        }
+        if (!inside) {
+            // the workgroup's partial joins the others' in the workspace; the last workgroup to finish merges them
+            __builtin_amdgcn_s_waitcnt(0);
+            int prev = 0;
+            if (lane == 0)
+                prev = __hip_atomic_fetch_add(p.counters + c.b * p.kv_heads + c.kvh, 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+            merge_row<D>(p, c, __shfl(prev, 0), total, grid, lane);
+        }
+    }
+}
+
+
 }  // namespace
 }  // namespace eco
