@@ -471,8 +471,9 @@ __global__ __launch_bounds__((64 * kivi_wg_waves<D, NB>())) void kivi_attention_
                 }
             }
         }
-        // keys from the ring (tokens at or past kq)
-        if (t0 + KPAGE > kq) {
+        // keys from the ring (tokens at or past kq; kq counts whole 32-token key groups, so a page is either all
+        // codes or all ring)
+        if (t0 >= kq) {
             uint4 kr[2][KS];
 #pragma unroll
             for (int v = 0; v < 2; ++v) {
@@ -483,27 +484,15 @@ __global__ __launch_bounds__((64 * kivi_wg_waves<D, NB>())) void kivi_attention_
                 for (int j = 0; j < KS; ++j) kr[v][j] = *reinterpret_cast<const uint4*>(src + 8 * j);
             }
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the ring loads of this rare branch
-            f32x4 sd[2][NB];
-#pragma unroll
-            for (int v = 0; v < 2; ++v)
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) {
-                    sd[v][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                    for (int j = 0; j < KS; ++j)
-                        sd[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            __builtin_bit_cast(bf16x8, kr[v][j]),
-                            __builtin_bit_cast(bf16x8, q_bf[nb * 16 + n][g * (D / 32) + j]), sd[v][nb], 0, 0, 0);
-                }
 #pragma unroll
             for (int v = 0; v < 2; ++v)
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int token = t0 + 8 * g + 4 * v + i;
-                        if (t0 >= kq || token >= kq) s[v][nb][i] = sd[v][nb][i];
-                    }
+                    for (int j = 0; j < KS; ++j)
+                        s[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8, kr[v][j]),
+                            __builtin_bit_cast(bf16x8, q_bf[nb * 16 + n][g * (D / 32) + j]), s[v][nb], 0, 0, 0);
         }
         // scores in log2 units; masking where the tile holds a row's end, a causal limit or a missing page
 #pragma unroll

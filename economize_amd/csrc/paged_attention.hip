@@ -254,17 +254,17 @@ constexpr int waves_per_simd() {
 // Waves of a workgroup. Four for one column block at D <= 128: the workgroup's tile range is split in four
 // contiguous quarters, and the pieces of a row that lies inside the workgroup's range are merged through LDS after
 // one barrier; only rows cut at a workgroup boundary go through the counter and the workspace partials.
-template <int D, int NB, int NBUF>
+template <int D, int FMT, int NB, int NBUF>
 constexpr int wg_waves() {
     return NB == 1 && D <= 128 && NBUF <= 2 ? 4 : 1;
 }
 
 template <int D, int FMT, int NB, int NBUF>
-__global__ __launch_bounds__((64 * wg_waves<D, NB, NBUF>()))
+__global__ __launch_bounds__((64 * wg_waves<D, FMT, NB, NBUF>()))
     __attribute__((amdgpu_waves_per_eu(waves_per_simd<D, FMT, NB, NBUF>()))) void
 paged_attention_kernel(PagedParams p) {
     constexpr bool kTwoWaves = waves_per_simd<D, FMT, NB, NBUF>() == 2;
-    constexpr int WAVES = wg_waves<D, NB, NBUF>();
+    constexpr int WAVES = wg_waves<D, FMT, NB, NBUF>();
     // two buffers: the query operand is kept once per row (q_row), loaded into q_next with the row's first tile
     constexpr bool kRowQ = NBUF == 2;
     using T = Tile<D, FMT, NB, kRowQ>;
@@ -671,10 +671,10 @@ Instance kernel_of() {
     constexpr int M = max_stages<D, FMT, NB>();
     const int s = stages_cap() < M ? stages_cap() : M;
     if constexpr (M >= 3)
-        if (s == 3) return {paged_attention_kernel<D, FMT, NB, 3>, wg_waves<D, NB, 3>()};
+        if (s == 3) return {paged_attention_kernel<D, FMT, NB, 3>, wg_waves<D, FMT, NB, 3>()};
     if constexpr (M >= 2)
-        if (s >= 2) return {paged_attention_kernel<D, FMT, NB, 2>, wg_waves<D, NB, 2>()};
-    return {paged_attention_kernel<D, FMT, NB, 1>, wg_waves<D, NB, 1>()};
+        if (s >= 2) return {paged_attention_kernel<D, FMT, NB, 2>, wg_waves<D, FMT, NB, 2>()};
+    return {paged_attention_kernel<D, FMT, NB, 1>, wg_waves<D, FMT, NB, 1>()};
 }
 
 // Calls f.template run<D, FMT, NB>() for the instance of (head dim, format, 16-row column blocks).

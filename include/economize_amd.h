@@ -154,7 +154,8 @@ size_t eco_kivi_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_
 
 /* Decode attention over the paged KIVI cache and the rings: as eco_paged_decode (query [B, Q, Hq, D] bf16, out
  * [B, Q, Hq, D] bf16, causal over the last Q of seq_lens[b] tokens, soft cap, sinks), with keys below
- * keys_quantized[b] and values below values_quantized[b] read as codes. Replaces kivi_decode_attention
+ * keys_quantized[b] (whole 32-token key groups, as eco_kivi_schedule counts them) and values below
+ * values_quantized[b] read as codes. Replaces kivi_decode_attention
  * (attention/kivi.py:199-309) and paged_kivi_attention (backends/vllm/kivi/kernels.py:354-415). */
 int eco_kivi_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* blocks, int32_t num_pages,
                     const void* k_ring, const void* v_ring, int32_t ring, const int32_t* keys_quantized,
