@@ -360,17 +360,38 @@ constexpr int kivi_wg_waves() {
     return NB == 1 && D <= 128 ? 4 : 1;
 }
 
+// Waves per SIMD: two for the single-buffer instances of one column block (they fit 256 registers, and a workgroup's
+// LDS is the merge pieces alone, so two workgroups share a CU); one wave of a SIMD does not overlap its own
+// arithmetic with its outstanding loads, two waves do.
+template <int D, int NB, int NBUF>
+constexpr int kivi_waves_per_simd() {
+    return NB == 1 && D <= 128 && NBUF == 1 ? 2 : 1;
+}
+
 template <int D, int BITS, int NB, int NBUF>
-__global__ __launch_bounds__((64 * kivi_wg_waves<D, NB>())) void kivi_attention_kernel(KiviParams p) {
+__global__ __launch_bounds__((64 * kivi_wg_waves<D, NB>()))
+    __attribute__((amdgpu_waves_per_eu(kivi_waves_per_simd<D, NB, NBUF>()))) void
+kivi_attention_kernel(KiviParams p) {
     using T = KTile<D, BITS>;
     constexpr int KS = T::KS, ND = T::ND, VG = T::VG;
     constexpr int R = NB * 16;  // query rows of the MFMA columns
     constexpr int WAVES = kivi_wg_waves<D, NB>();
-    __shared__ uint4 q_lds[WAVES][R][D / 8];  // each wave's current query rows
+    using QRows = uint4[R][D / 8];  // a wave's current query rows
 
     const int lane = WAVES > 1 ? static_cast<int>(threadIdx.x) & 63 : static_cast<int>(threadIdx.x);
     const int wave = WAVES > 1 ? uniform(static_cast<int>(threadIdx.x) >> 6) : 0;
-    auto& q_bf = q_lds[wave];
+    __shared__ __align__(16) typename std::conditional<(WAVES > 1), Pieces<D, WAVES>, char>::type pieces;
+    QRows* q_rows;
+    if constexpr (WAVES > 1) {
+        // the query rows live in the data of the wave's second piece, which only the wave's last step writes, after
+        // its last read of them (the piece's row, b, kvh and tiles fields lie outside the data)
+        static_assert(sizeof(QRows) <= sizeof(pieces.data[0]), "query rows fit a piece");
+        q_rows = reinterpret_cast<QRows*>(pieces.data[2 * wave + 1]);
+    } else {
+        __shared__ QRows q_lds;
+        q_rows = &q_lds;
+    }
+    auto& q_bf = *q_rows;
     const int n = lane & 15;
     const int g = lane >> 4;
     const int w = blockIdx.x;  // workgroup
@@ -390,7 +411,6 @@ __global__ __launch_bounds__((64 * kivi_wg_waves<D, NB>())) void kivi_attention_
     const int64_t whi = total * (w + 1) / grid;
     const int64_t lo = wlo + (whi - wlo) * wave / WAVES;  // this wave's part of it
     const int64_t hi = wlo + (whi - wlo) * (wave + 1) / WAVES;
-    __shared__ typename std::conditional<(WAVES > 1), Pieces<D, WAVES>, char>::type pieces;
     if constexpr (WAVES > 1) {
         clear_pieces(pieces, wave, lane);
     } else {
@@ -659,6 +679,8 @@ __global__ __launch_bounds__((64 * kivi_wg_waves<D, NB>())) void kivi_attention_
             return;
         }
         if constexpr (WAVES > 1) {
+            // the second piece overwrites the query rows: no LDS access of the tile may move past this point
+            if (!first_segment) __asm__ volatile("" ::: "memory");
             write_piece(pieces, 2 * wave + (first_segment ? 0 : 1), c, p.rows, n, g, lane, m_i[0], l_i[0],
                         [&](int nd, int i) __attribute__((always_inline)) { return o[nd][0][i]; });
             return;
@@ -754,9 +776,21 @@ __global__ __launch_bounds__((64 * kivi_wg_waves<D, NB>())) void kivi_attention_
 
 namespace {
 
+// Tile buffers of the one-column-block instances: 1 (two waves per SIMD, the default: 57 us against 71 us at
+// B=16, L=8192, int2 and int4) or 2 (one wave per SIMD, the next tile's loads in flight); ECO_KIVI_STAGES overrides.
+int kivi_stages() {
+    static const int stages = [] {
+        const char* env = std::getenv("ECO_KIVI_STAGES");
+        const int v = env ? std::atoi(env) : 1;
+        return v <= 1 ? 1 : 2;
+    }();
+    return stages;
+}
+
 template <int D, int BITS, int NB>
 auto kivi_kernel_of() {
-    if constexpr (NB == 1) return kivi_attention_kernel<D, BITS, NB, 2>;
+    if constexpr (NB == 1)
+        return kivi_stages() == 1 ? kivi_attention_kernel<D, BITS, NB, 1> : kivi_attention_kernel<D, BITS, NB, 2>;
     return kivi_attention_kernel<D, BITS, NB, 1>;
 }
 
