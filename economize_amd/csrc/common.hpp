@@ -32,9 +32,13 @@ ECO_HD constexpr float fp8_max() {
     return FMT == FP8_E4M3 ? 448.0f : 57344.0f;
 }
 
-__device__ inline float group_max(float x) {  // max over the four lanes l, l^16, l^32, l^48
-    x = fmaxf(x, __shfl_xor(x, 16));
-    return fmaxf(x, __shfl_xor(x, 32));
+// The larger of a and b, NaN if either is NaN (v_maximum_f32 / v_maximum3_f32). Unlike fmaxf it needs no quieting
+// of its operands, which the compiler otherwise inserts wherever it cannot prove an operand is not a signalling NaN.
+__device__ inline float max_nan(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+__device__ inline float group_max(float x) {  // max over the four lanes l, l^16, l^32, l^48 (NaN if any is NaN)
+    x = max_nan(x, __shfl_xor(x, 16));
+    return max_nan(x, __shfl_xor(x, 32));
 }
 
 __device__ inline float group_sum(float x) {  // sum over the four lanes l, l^16, l^32, l^48

@@ -29,6 +29,7 @@
 // one 32-token page. The query of the current row lives in LDS, so that row changes do not put loads of varying
 // count in the tile pipeline.
 
+#include <cstdlib>
 #include <type_traits>
 
 #include "common.hpp"
@@ -458,12 +459,13 @@ kivi_attention_kernel(KiviParams p) {
         const int t0 = KPAGE * c.t;
         const bool valid = tile.page >= 0;
         f32x4 s[2][NB];
-        // keys from codes, dequantized as the reference does (code * scale + zero in fp32, two roundings, then bf16;
-        // attention/kivi.py:56-76), so that the scores see the reference's key values exactly
 #pragma unroll
         for (int v = 0; v < 2; ++v)
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) s[v][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        // keys from codes, dequantized as the reference does (code * scale + zero in fp32, two roundings, then bf16;
+        // attention/kivi.py:56-76), so that the scores see the reference's key values exactly; or, at or past kq,
+        // from the ring (kq counts whole 32-token key groups, so a page is either all codes or all ring)
         if (t0 < kq) {
 #pragma unroll
             for (int j = 0; j < KS; ++j) {
@@ -490,10 +492,7 @@ kivi_attention_kernel(KiviParams p) {
                             kv, __builtin_bit_cast(bf16x8, q_bf[nb * 16 + n][g * (D / 32) + j]), s[v][nb], 0, 0, 0);
                 }
             }
-        }
-        // keys from the ring (tokens at or past kq; kq counts whole 32-token key groups, so a page is either all
-        // codes or all ring)
-        if (t0 >= kq) {
+        } else {
             uint4 kr[2][KS];
 #pragma unroll
             for (int v = 0; v < 2; ++v) {
@@ -549,7 +548,8 @@ kivi_attention_kernel(KiviParams p) {
             float tile_max = -INFINITY;
 #pragma unroll
             for (int v = 0; v < 2; ++v)
-                tile_max = fmaxf(fmaxf(tile_max, fmaxf(s[v][nb][0], s[v][nb][1])), fmaxf(s[v][nb][2], s[v][nb][3]));
+                tile_max = max_nan(max_nan(tile_max, max_nan(s[v][nb][0], s[v][nb][1])),
+                                   max_nan(s[v][nb][2], s[v][nb][3]));
             tile_max = group_max(tile_max);
             if (__ballot(tile_max > m_i[nb] + 8.0f || m_i[nb] == -INFINITY) != 0) {
                 const bool fresh = m_i[nb] == -INFINITY;
@@ -578,39 +578,49 @@ kivi_attention_kernel(KiviParams p) {
         // values: element e of the lane's operands is token t0 + 8 g + e
         const int tok0 = t0 + 8 * g;
         if (t0 < vq) {  // from codes: O += codes . (p * s) + z . p
-            uint32_t keep = 0xFFu;
-            if (t0 + KPAGE > vq || !valid)
-                keep = valid ? (vq - tok0 >= 8 ? 0xFFu : (vq > tok0 ? (1u << (vq - tok0)) - 1u : 0u)) : 0u;
-            f16x8 pp[NB];
+            // tokens at or past vq and every token of a missing page are masked out of p, p * s and z (an unwritten
+            // scale may be inf or NaN); a tile of codes only skips the masks
+            auto from_codes = [&](auto full_tag, uint32_t keep) __attribute__((always_inline)) {
+                constexpr bool kFull = decltype(full_tag)::value;
+                auto masked = [&](uint4 x) __attribute__((always_inline)) { return kFull ? x : keep_halves(x, keep); };
+                f16x8 pp[NB];
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                uint4 w4;
-                w4.x = pack_f16x2(pw[nb][0], pw[nb][1]);
-                w4.y = pack_f16x2(pw[nb][2], pw[nb][3]);
-                w4.z = pack_f16x2(pw[nb][4], pw[nb][5]);
-                w4.w = pack_f16x2(pw[nb][6], pw[nb][7]);
-                pp[nb] = __builtin_bit_cast(f16x8, keep_halves(w4, keep));
-            }
+                for (int nb = 0; nb < NB; ++nb) {
+                    uint4 w4;
+                    w4.x = pack_f16x2(pw[nb][0], pw[nb][1]);
+                    w4.y = pack_f16x2(pw[nb][2], pw[nb][3]);
+                    w4.z = pack_f16x2(pw[nb][4], pw[nb][5]);
+                    w4.w = pack_f16x2(pw[nb][6], pw[nb][7]);
+                    pp[nb] = __builtin_bit_cast(f16x8, masked(w4));
+                }
 #pragma unroll
-            for (int grp = 0; grp < VG; ++grp) {
-                f16x8 ps[NB];
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
-                    ps[nb] = __builtin_bit_cast(
-                        f16x8, keep_halves(__builtin_bit_cast(uint4, pp[nb] * __builtin_bit_cast(f16x8, tile.vs[grp])),
-                                           keep));
-#pragma unroll
-                for (int nd = 2 * grp; nd < 2 * grp + 2; ++nd) {
-                    const f16x8 a = BITS == 4 ? codes_to_f16<BITS>(tile.vc[nd], 0)
-                                              : codes_to_f16<BITS>(tile.vc[nd], g & 1);
+                for (int grp = 0; grp < VG; ++grp) {
+                    f16x8 ps[NB];
 #pragma unroll
                     for (int nb = 0; nb < NB; ++nb)
-                        acc[nd][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ps[nb], acc[nd][nb], 0, 0, 0);
-                }
-            }
-            const f16x8 z = __builtin_bit_cast(f16x8, keep_halves(tile.vz, keep));
+                        ps[nb] = __builtin_bit_cast(
+                            f16x8, masked(__builtin_bit_cast(uint4, pp[nb] * __builtin_bit_cast(f16x8, tile.vs[grp]))));
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) gam[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(z, pp[nb], gam[nb], 0, 0, 0);
+                    for (int nd = 2 * grp; nd < 2 * grp + 2; ++nd) {
+                        const f16x8 a = BITS == 4 ? codes_to_f16<BITS>(tile.vc[nd], 0)
+                                                  : codes_to_f16<BITS>(tile.vc[nd], g & 1);
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb)
+                            acc[nd][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ps[nb], acc[nd][nb], 0, 0, 0);
+                    }
+                }
+                const f16x8 z = __builtin_bit_cast(f16x8, masked(tile.vz));
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    gam[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(z, pp[nb], gam[nb], 0, 0, 0);
+            };
+            if (NB <= 2 && t0 + KPAGE <= vq && valid) {  // (at four column blocks the second copy would spill)
+                from_codes(std::integral_constant<bool, NB <= 2>{}, 0xFFu);
+            } else {
+                const uint32_t keep =
+                    valid ? (vq - tok0 >= 8 ? 0xFFu : (vq > tok0 ? (1u << (vq - tok0)) - 1u : 0u)) : 0u;
+                from_codes(std::false_type{}, keep);
+            }
         }
         if (t0 + KPAGE > vq) {  // from the ring (tokens at or past vq, below the row's end)
             const int from = max(vq - tok0, 0), to = min(row_len - tok0, 8);

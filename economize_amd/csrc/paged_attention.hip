@@ -408,7 +408,8 @@ paged_attention_kernel(PagedParams p) {
             float tile_max = -INFINITY;
 #pragma unroll
             for (int v = 0; v < 4; ++v)
-                tile_max = fmaxf(fmaxf(tile_max, fmaxf(s[v][nb][0], s[v][nb][1])), fmaxf(s[v][nb][2], s[v][nb][3]));
+                tile_max = max_nan(max_nan(tile_max, max_nan(s[v][nb][0], s[v][nb][1])),
+                                   max_nan(s[v][nb][2], s[v][nb][3]));
             tile_max = group_max(tile_max);
             // Lazy rescaling: the reference maximum m_i moves only when a score exceeds it by more than 2^8, so that
             // the accumulators are rescaled a few times per row instead of at every tile (the weights stay below
