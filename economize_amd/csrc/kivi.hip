@@ -286,15 +286,19 @@ __device__ inline uint4 keep_halves(uint4 x, uint32_t keep) {
     return x;
 }
 
-template <int D, int BITS>
+// A lane's share of one 32-token page. SHARED: the four waves of a workgroup dequantize the key tile together, lane
+// (n, g) of wave w taking the KE operand entries (k-step j, token half v) with j * 2 + v = w * KE + e; then it holds
+// one key word per entry and the scale and zero point of its 8 channels.
+template <int D, int BITS, bool SHARED = false>
 struct KTile {
     static constexpr int KW = D * BITS / 128;  // words of a lane's key slice (D / 4 channels)
     static constexpr int ND = D / 16;          // value blocks of 16 channels
     static constexpr int KS = D / 32;          // k-steps of an S MFMA (8 channels each per lane)
     static constexpr int VG = D / 32;          // value groups
-    uint32_t kc[2][KW];
+    static constexpr int KE = KS / 2;          // key entries per lane (SHARED)
+    uint32_t kc[2][SHARED ? KE : KW];          // SHARED: kc[0][e]
     uint32_t vc[ND];
-    uint4 ks[KS], kz[KS];
+    uint4 ks[SHARED ? 1 : KS], kz[SHARED ? 1 : KS];
     uint4 vs[VG];
     uint4 vz;
     int page;  // physical page (the same in every lane), -1 for none
@@ -323,28 +327,43 @@ __device__ inline void load_words(const uint32_t* src, uint32_t (&dst)[N]) {
 
 // Issues the page loads of the tile under cursor c (the same loads in every lane and for every tile: a tile without
 // a page reads page 0 and masks it).
-template <int D, int BITS>
-__device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c, int n, int g, int lane,
-                                           PageWindow& win, KTile<D, BITS>& tile) {
-    using T = KTile<D, BITS>;
+template <int D, int BITS, bool SHARED>
+__device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c, int n, int g, int lane, int wave,
+                                           PageWindow& win, KTile<D, BITS, SHARED>& tile) {
+    using T = KTile<D, BITS, SHARED>;
     constexpr KiviLayout L{D, BITS};
     ensure_window(p, c, lane, win);
     const int phys = __builtin_amdgcn_readlane(win.physical, c.t - win.base);
     tile.page = phys;
     const uint8_t* blk = p.blocks + static_cast<int64_t>(phys >= 0 ? phys : 0) * p.blk_page + c.kvh * p.blk_head;
+    if constexpr (SHARED) {
+        const int j = (wave * T::KE) >> 1;  // the k-step of every entry of the lane
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
-        const int token = 8 * (n >> 2) + 4 * v + (n & 3);
-        load_words(reinterpret_cast<const uint32_t*>(blk + L.k_codes() + token * (D * BITS / 8)) + g * T::KW,
-                   tile.kc[v]);
+        for (int e = 0; e < T::KE; ++e) {
+            const int v = (wave * T::KE + e) & 1;
+            const int token = 8 * (n >> 2) + 4 * v + (n & 3);
+            tile.kc[0][e] = reinterpret_cast<const uint32_t*>(blk + L.k_codes() + token * (D * BITS / 8))
+                [g * T::KW + (BITS == 4 ? j : j / 2)];
+        }
+        tile.ks[0] = *reinterpret_cast<const uint4*>(blk + L.k_scale() + (g * (D / 4) + 8 * j) * 2);
+        tile.kz[0] = *reinterpret_cast<const uint4*>(blk + L.k_zero() + (g * (D / 4) + 8 * j) * 2);
+    } else {
+#pragma unroll
+        for (int v = 0; v < 2; ++v) {
+            const int token = 8 * (n >> 2) + 4 * v + (n & 3);
+            load_words(reinterpret_cast<const uint32_t*>(blk + L.k_codes() + token * (D * BITS / 8)) + g * T::KW,
+                       tile.kc[v]);
+        }
     }
     constexpr int TPW = 32 / BITS;  // tokens per value word
     const int u = 8 * g / TPW;
     load_words(reinterpret_cast<const uint32_t*>(blk + L.v_codes()) + (u * 16 + n) * T::ND, tile.vc);
+    if constexpr (!SHARED) {
 #pragma unroll
-    for (int j = 0; j < T::KS; ++j) {
-        tile.ks[j] = *reinterpret_cast<const uint4*>(blk + L.k_scale() + (g * (D / 4) + 8 * j) * 2);
-        tile.kz[j] = *reinterpret_cast<const uint4*>(blk + L.k_zero() + (g * (D / 4) + 8 * j) * 2);
+        for (int j = 0; j < T::KS; ++j) {
+            tile.ks[j] = *reinterpret_cast<const uint4*>(blk + L.k_scale() + (g * (D / 4) + 8 * j) * 2);
+            tile.kz[j] = *reinterpret_cast<const uint4*>(blk + L.k_zero() + (g * (D / 4) + 8 * j) * 2);
+        }
     }
 #pragma unroll
     for (int grp = 0; grp < T::VG; ++grp)
@@ -354,43 +373,51 @@ __device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c,
 
 }  // namespace
 
-// Waves of a workgroup: four for one column block (pieces of rows inside the workgroup merge through LDS, as in
-// paged_attention.hip), else one.
-template <int D, int NB>
+// Workgroup shapes. One column block at D <= 128: four waves split the workgroup's tile range in quarters, the
+// pieces of rows inside the workgroup merged through LDS (as in paged_attention.hip). SHARED (more than 32 query rows
+// per KV head, the verification shape): four waves walk the workgroup's range together, wave w taking query rows
+// 16 w .. 16 w + 15, and dequantize a quarter of each key tile each into LDS (one barrier per tile), so that a key
+// is dequantized once for all query rows. Otherwise one wave.
+template <int D, int NB, bool SHARED>
 constexpr int kivi_wg_waves() {
-    return NB == 1 && D <= 128 ? 4 : 1;
+    return SHARED || (NB == 1 && D <= 128) ? 4 : 1;
 }
 
-// Waves per SIMD: two for the single-buffer instances of one column block (they fit 256 registers, and a workgroup's
-// LDS is the merge pieces alone, so two workgroups share a CU); one wave of a SIMD does not overlap its own
-// arithmetic with its outstanding loads, two waves do.
+// Waves per SIMD: two for the single-buffer instances of one column block, SHARED ones included (they fit 256
+// registers, and two workgroups' LDS fit a CU); one wave of a SIMD does not overlap its own arithmetic with its
+// outstanding loads, two waves do.
 template <int D, int NB, int NBUF>
 constexpr int kivi_waves_per_simd() {
     return NB == 1 && D <= 128 && NBUF == 1 ? 2 : 1;
 }
 
-template <int D, int BITS, int NB, int NBUF>
-__global__ __launch_bounds__((64 * kivi_wg_waves<D, NB>()))
+template <int D, int BITS, int NB, int NBUF, bool SHARED>
+__global__ __launch_bounds__((64 * kivi_wg_waves<D, NB, SHARED>()))
     __attribute__((amdgpu_waves_per_eu(kivi_waves_per_simd<D, NB, NBUF>()))) void
 kivi_attention_kernel(KiviParams p) {
-    using T = KTile<D, BITS>;
+    static_assert(!SHARED || NB == 1, "a shared-tile wave holds one column block");
+    using T = KTile<D, BITS, SHARED>;
     constexpr int KS = T::KS, ND = T::ND, VG = T::VG;
     constexpr int R = NB * 16;  // query rows of the MFMA columns
-    constexpr int WAVES = kivi_wg_waves<D, NB>();
-    using QRows = uint4[R][D / 8];  // a wave's current query rows
+    constexpr int WAVES = kivi_wg_waves<D, NB, SHARED>();
+    constexpr bool kSplit = !SHARED && WAVES > 1;  // the range split in quarters, pieces merged in LDS
+    using QRows = uint4[R][D / 8];                 // a wave's current query rows
 
     const int lane = WAVES > 1 ? static_cast<int>(threadIdx.x) & 63 : static_cast<int>(threadIdx.x);
     const int wave = WAVES > 1 ? uniform(static_cast<int>(threadIdx.x) >> 6) : 0;
-    __shared__ __align__(16) typename std::conditional<(WAVES > 1), Pieces<D, WAVES>, char>::type pieces;
+    const int row0 = SHARED ? 16 * wave : 0;  // the wave's first query row
+    __shared__ __align__(16) typename std::conditional<kSplit, Pieces<D, WAVES>, char>::type pieces;
+    // SHARED: the dequantized key tile, two buffers, in MFMA operand order (entry j * 2 + v, lane)
+    __shared__ typename std::conditional<SHARED, uint4[2][2 * KS][64], char>::type kbuf;
     QRows* q_rows;
-    if constexpr (WAVES > 1) {
+    if constexpr (kSplit) {
         // the query rows live in the data of the wave's second piece, which only the wave's last step writes, after
         // its last read of them (the piece's row, b, kvh and tiles fields lie outside the data)
         static_assert(sizeof(QRows) <= sizeof(pieces.data[0]), "query rows fit a piece");
         q_rows = reinterpret_cast<QRows*>(pieces.data[2 * wave + 1]);
     } else {
-        __shared__ QRows q_lds;
-        q_rows = &q_lds;
+        __shared__ QRows q_lds[WAVES];
+        q_rows = &q_lds[wave];
     }
     auto& q_bf = *q_rows;
     const int n = lane & 15;
@@ -410,12 +437,12 @@ kivi_attention_kernel(KiviParams p) {
     }
     const int64_t wlo = total * w / grid;  // the workgroup's tile range
     const int64_t whi = total * (w + 1) / grid;
-    const int64_t lo = wlo + (whi - wlo) * wave / WAVES;  // this wave's part of it
-    const int64_t hi = wlo + (whi - wlo) * (wave + 1) / WAVES;
-    if constexpr (WAVES > 1) {
+    const int64_t lo = kSplit ? wlo + (whi - wlo) * wave / WAVES : wlo;  // this wave's part of it
+    const int64_t hi = kSplit ? wlo + (whi - wlo) * (wave + 1) / WAVES : whi;
+    if constexpr (kSplit) {
         clear_pieces(pieces, wave, lane);
     } else {
-        if (lo >= hi) return;
+        if (lo >= hi) return;  // (SHARED: the same for every wave of the workgroup)
     }
 
     // ---- row state ----
@@ -430,8 +457,8 @@ kivi_attention_kernel(KiviParams p) {
         for (int i = lane; i < R * (D / 8); i += 64) {
             const int r = i / (D / 8), k = i % (D / 8);
             uint4 x = make_uint4(0, 0, 0, 0);
-            if (r < p.rows) {
-                const int gq = r / p.queries, qi = r % p.queries;
+            if (row0 + r < p.rows) {
+                const int gq = (row0 + r) / p.queries, qi = (row0 + r) % p.queries;
                 x = *reinterpret_cast<const uint4*>(p.q + c.b * p.sq_b + qi * p.sq_q +
                                                     (c.kvh * p.groups + gq) * p.sq_h + 8 * k);
             }
@@ -444,7 +471,7 @@ kivi_attention_kernel(KiviParams p) {
         all_see = c.row.len - p.queries + 1;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            const int r = nb * 16 + n;
+            const int r = row0 + nb * 16 + n;
             limit[nb] = r < p.rows ? static_cast<float>(c.row.len - p.queries + r % p.queries + 1) : 0.0f;
             // the accumulators are cleared by the row's first rescale (m_i = -inf marks a row with no weight yet),
             // so that a row change does not give them a second register version to merge at every tile
@@ -454,8 +481,28 @@ kivi_attention_kernel(KiviParams p) {
     };
     const float score_scale = p.softcap > 0.0f ? p.scale : p.scale * kLog2e;
 
+    // ---- SHARED: the lane's entries of the key tile, dequantized into LDS buffer buf ----
+    auto share_keys = [&](const T& tile, int buf) __attribute__((always_inline)) {
+        if constexpr (SHARED) {
+            const f16x8 sh = __builtin_bit_cast(f16x8, tile.ks[0]);
+            const f16x8 zh = __builtin_bit_cast(f16x8, tile.kz[0]);
+            const int j = (wave * T::KE) >> 1;
+#pragma unroll
+            for (int e = 0; e < T::KE; ++e) {
+                float c8[8];
+                codes_to_f32<BITS>(tile.kc[0][e], j % 2, c8);
+                bf16x8 kv;
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    kv[i] = static_cast<__bf16>(
+                        __builtin_fmaf(c8[i], static_cast<float>(sh[i]), static_cast<float>(zh[i])));
+                kbuf[buf][wave * T::KE + e][lane] = __builtin_bit_cast(uint4, kv);
+            }
+        }
+    };
+
     // ---- one tile (32 tokens) of the online softmax ----
-    auto compute = [&](const T& tile, const Cursor& c) __attribute__((always_inline)) {
+    auto compute = [&](const T& tile, const Cursor& c, int buf) __attribute__((always_inline)) {
         const int t0 = KPAGE * c.t;
         const bool valid = tile.page >= 0;
         f32x4 s[2][NB];
@@ -467,29 +514,40 @@ kivi_attention_kernel(KiviParams p) {
         // attention/kivi.py:56-76), so that the scores see the reference's key values exactly; or, at or past kq,
         // from the ring (kq counts whole 32-token key groups, so a page is either all codes or all ring)
         if (t0 < kq) {
+            if constexpr (SHARED) {
 #pragma unroll
-            for (int j = 0; j < KS; ++j) {
-                const f16x8 sh = __builtin_bit_cast(f16x8, tile.ks[j]);
-                const f16x8 zh = __builtin_bit_cast(f16x8, tile.kz[j]);
-                float sf[8], zf[8];
+                for (int j = 0; j < KS; ++j)
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    sf[e] = static_cast<float>(sh[e]);
-                    zf[e] = static_cast<float>(zh[e]);
-                }
+                    for (int v = 0; v < 2; ++v)
+                        s[v][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            __builtin_bit_cast(bf16x8, kbuf[buf][2 * j + v][lane]),
+                            __builtin_bit_cast(bf16x8, q_bf[n][g * (D / 32) + j]), s[v][0], 0, 0, 0);
+            } else {
 #pragma unroll
-                for (int v = 0; v < 2; ++v) {
-                    float c8[8];
-                    codes_to_f32<BITS>(BITS == 4 ? tile.kc[v][j] : tile.kc[v][j / 2], j % 2, c8);
-                    bf16x8 kv;
-                    // code * scale is exact in fp32 (a code of at most 4 bits times an fp16), so one fused
-                    // multiply-add rounds exactly as the reference's product then sum
+                for (int j = 0; j < KS; ++j) {
+                    const f16x8 sh = __builtin_bit_cast(f16x8, tile.ks[j]);
+                    const f16x8 zh = __builtin_bit_cast(f16x8, tile.kz[j]);
+                    float sf[8], zf[8];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) kv[e] = static_cast<__bf16>(__builtin_fmaf(c8[e], sf[e], zf[e]));
+                    for (int e = 0; e < 8; ++e) {
+                        sf[e] = static_cast<float>(sh[e]);
+                        zf[e] = static_cast<float>(zh[e]);
+                    }
 #pragma unroll
-                    for (int nb = 0; nb < NB; ++nb)
-                        s[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            kv, __builtin_bit_cast(bf16x8, q_bf[nb * 16 + n][g * (D / 32) + j]), s[v][nb], 0, 0, 0);
+                    for (int v = 0; v < 2; ++v) {
+                        float c8[8];
+                        codes_to_f32<BITS>(BITS == 4 ? tile.kc[v][j] : tile.kc[v][j / 2], j % 2, c8);
+                        bf16x8 kv;
+                        // code * scale is exact in fp32 (a code of at most 4 bits times an fp16), so one fused
+                        // multiply-add rounds exactly as the reference's product then sum
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) kv[e] = static_cast<__bf16>(__builtin_fmaf(c8[e], sf[e], zf[e]));
+#pragma unroll
+                        for (int nb = 0; nb < NB; ++nb)
+                            s[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                kv, __builtin_bit_cast(bf16x8, q_bf[nb * 16 + n][g * (D / 32) + j]), s[v][nb], 0,
+                                0, 0);
+                    }
                 }
             }
         } else {
@@ -678,7 +736,7 @@ kivi_attention_kernel(KiviParams p) {
         if (seg_begin == c.row_start && seg_end == row_end) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-                const int r = nb * 16 + n;
+                const int r = row0 + nb * 16 + n;
                 if (r >= p.rows) continue;
 #pragma unroll
                 for (int nd = 0; nd < ND; ++nd)
@@ -688,7 +746,7 @@ kivi_attention_kernel(KiviParams p) {
             }
             return;
         }
-        if constexpr (WAVES > 1) {
+        if constexpr (kSplit) {
             // the second piece overwrites the query rows: no LDS access of the tile may move past this point
             if (!first_segment) __asm__ volatile("" ::: "memory");
             write_piece(pieces, 2 * wave + (first_segment ? 0 : 1), c, p.rows, n, g, lane, m_i[0], l_i[0],
@@ -699,7 +757,7 @@ kivi_attention_kernel(KiviParams p) {
         float* slot = p.part + (2 * static_cast<int64_t>(w) + (first_segment ? 0 : 1)) * stride;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            const int r = nb * 16 + n;
+            const int r = row0 + nb * 16 + n;
             if (r >= p.rows) continue;
             if (g == 0) {
                 coherent_store(slot + r, m_i[nb]);
@@ -712,6 +770,10 @@ kivi_attention_kernel(KiviParams p) {
                     coherent_store(slot + 2 * p.rows + r * D + 16 * nd + 4 * g + i, o[nd][nb][i]);
         }
         __builtin_amdgcn_s_waitcnt(0);
+        if constexpr (SHARED) {  // every wave's rows are in the workgroup's slot before the count
+            __syncthreads();
+            if (wave != 0) return;
+        }
         int prev = 0;
         if (lane == 0)
             prev = __hip_atomic_fetch_add(p.counters + c.b * p.kv_heads + c.kvh, 1, __ATOMIC_RELAXED,
@@ -738,7 +800,7 @@ kivi_attention_kernel(KiviParams p) {
         Cursor icur = cur;
         int64_t ipos = lo;
         auto issue_next = [&](T& buf, Cursor& slot) __attribute__((always_inline)) {
-            issue_tile<D, BITS>(p, icur, n, g, lane, win, buf);
+            issue_tile<D, BITS, SHARED>(p, icur, n, g, lane, wave, win, buf);
             slot = icur;
             if (ipos < hi) {
                 if (ipos + 1 < hi) advance(p, icur, small ? &rt : nullptr);
@@ -755,7 +817,13 @@ kivi_attention_kernel(KiviParams p) {
             issue_next(bufs[J], cs[J]);
             cur = cs[I];
             if (cur.t == 0 && pos != lo) begin_row(cur);
-            compute(bufs[I], cur);
+            if constexpr (SHARED) {
+                // this tile's keys into LDS buffer pos & 1; the barrier also ends every wave's reads of that buffer
+                // two tiles back (they precede the previous tile's barrier)
+                if (KPAGE * cur.t < kq) share_keys(bufs[I], static_cast<int>(pos & 1));
+                __syncthreads();
+            }
+            compute(bufs[I], cur, static_cast<int>(pos & 1));
             const bool more = pos + 1 < hi;
             if (cur.t + 1 == cur.row.tiles || !more) {
                 finish(cur, seg_begin, pos + 1, first_segment);
@@ -774,7 +842,7 @@ kivi_attention_kernel(KiviParams p) {
             }
         }
     };
-    if constexpr (WAVES == 1) {
+    if constexpr (!kSplit) {
         pipeline();
     } else {
         if (lo < hi) pipeline();
@@ -797,16 +865,40 @@ int kivi_stages() {
     return stages;
 }
 
-template <int D, int BITS, int NB>
-auto kivi_kernel_of() {
-    if constexpr (NB == 1)
-        return kivi_stages() == 1 ? kivi_attention_kernel<D, BITS, NB, 1> : kivi_attention_kernel<D, BITS, NB, 2>;
-    return kivi_attention_kernel<D, BITS, NB, 1>;
+// Column blocks from which the shared-tile instance serves (default 3: more than 32 query rows per KV head);
+// ECO_KIVI_SHARED overrides.
+int kivi_shared_from() {
+    static const int from = [] {
+        const char* env = std::getenv("ECO_KIVI_SHARED");
+        const int v = env ? std::atoi(env) : 3;
+        return v < 2 ? 2 : v;
+    }();
+    return from;
 }
 
-template <int D, int NB>
-constexpr int kivi_block_threads() {
-    return 64 * kivi_wg_waves<D, NB>();
+// An attention instance: the kernel, its threads per workgroup and the parts a workgroup's tile range is split in
+// (the grid gives every part at least four tiles).
+using KiviKernelFn = decltype(&kivi_attention_kernel<64, 2, 1, 1, false>);
+struct KiviInstance {
+    KiviKernelFn kernel;
+    int threads;
+    int parts;
+};
+
+template <int D, int BITS, int NB, int NBUF, bool SHARED>
+KiviInstance kivi_instance() {
+    constexpr int waves = kivi_wg_waves<D, NB, SHARED>();
+    return {kivi_attention_kernel<D, BITS, NB, NBUF, SHARED>, 64 * waves, SHARED ? 1 : waves};
+}
+
+// NB column blocks of query rows: one block, the split instance (one or two tile buffers); from kivi_shared_from()
+// blocks, the shared-tile instance; otherwise one wave over NB blocks.
+template <int D, int BITS, int NB>
+KiviInstance kivi_kernel_of() {
+    if constexpr (NB == 1)
+        return kivi_stages() == 1 ? kivi_instance<D, BITS, 1, 1, false>() : kivi_instance<D, BITS, 1, 2, false>();
+    if (NB >= kivi_shared_from()) return kivi_instance<D, BITS, 1, 1, true>();
+    return kivi_instance<D, BITS, NB, 1, false>();
 }
 
 template <typename F>
@@ -835,8 +927,8 @@ struct KiviLaunch {
     const KiviParams* p;
     template <int D, int BITS, int NB>
     int run() const {
-        const auto kernel = kivi_kernel_of<D, BITS, NB>();
-        hipLaunchKernelGGL(kernel, dim3(p->grid), dim3(kivi_block_threads<D, NB>()), 0, stream, *p);
+        const KiviInstance in = kivi_kernel_of<D, BITS, NB>();
+        hipLaunchKernelGGL(in.kernel, dim3(p->grid), dim3(in.threads), 0, stream, *p);
         return check_launch("kivi_attention_kernel");
     }
 };
@@ -847,13 +939,12 @@ struct KiviOccupancy {
     template <int D, int BITS, int NB>
     int run() const {
         int blocks = 0;
-        const auto kernel = kivi_kernel_of<D, BITS, NB>();
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, kernel, kivi_block_threads<D, NB>(), 0) !=
-                hipSuccess ||
+        const KiviInstance in = kivi_kernel_of<D, BITS, NB>();
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, in.kernel, in.threads, 0) != hipSuccess ||
             blocks <= 0)
             blocks = 1;
         *per_cu = blocks;
-        *waves = kivi_wg_waves<D, NB>();
+        *waves = in.parts;
         return 0;
     }
 };

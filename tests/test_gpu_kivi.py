@@ -164,6 +164,9 @@ CASES = [
     (2, 1, 8, 2, 64, [700, 129], 2),
     (2, 1, 16, 4, 64, [90, 520], 4),
     (2, 8, 64, 8, 128, [1500, 1100], 4),  # verification: 8 draft tokens x GQA 8 = 64 rows per KV head
+    (2, 5, 64, 8, 64, [900, 300], 2),  # 40 rows: the last 16-row block of the workgroup holds none
+    (1, 8, 64, 8, 128, [6000], 2),  # 64 rows of one long row cut between workgroups
+    (3, 4, 128, 8, 64, [513, 2000, 64], 4),  # GQA 16 x 4 queries = 64 rows at head dim 64
     (4, 2, 16, 2, 128, [40, 1, 160, 385], 2),  # rows shorter than the residual: no codes at all
     (1, 1, 32, 8, 128, [8192], 2),  # one long row cut into many waves' ranges
 ]
