@@ -66,12 +66,13 @@ int paged_grid(int batch, int kv_heads, int rows, int head_dim, int format, int 
     const int64_t tiles = static_cast<int64_t>(batch) * kv_heads * ((row_pages + 3) / 4);
     int per_cu = 1, waves = 1;
     if (paged_resident_groups(head_dim, format, rows, &per_cu, &waves)) return 0;
-    int64_t grid = forced > 0 ? forced : static_cast<int64_t>(device_cus()) * per_cu;
+    if (forced > 0) return forced;
+    int64_t grid = static_cast<int64_t>(device_cus()) * per_cu;
     const int64_t cap = (tiles + 4 * waves - 1) / (4 * waves);  // at least four tiles per wave
     grid = grid < cap ? grid : cap;
     // short rows (Quest's selected pages): one workgroup per row, so that every row is merged inside its workgroup
     const int64_t rows_total = static_cast<int64_t>(batch) * kv_heads;
-    if (forced <= 0 && (row_pages + 3) / 4 <= 8 * waves && rows_total < grid) grid = rows_total;
+    if ((row_pages + 3) / 4 <= 8 * waves && rows_total < grid) grid = rows_total;
     return static_cast<int>(grid < 1 ? 1 : grid);
 }
 

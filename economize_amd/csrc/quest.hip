@@ -18,6 +18,8 @@
 // whole chip), quest_topk_kernel (one workgroup per (row, KV head): a radix select over order-preserving integer keys
 // of the scores, ties to the lower index, then a compaction in page order).
 
+#include <type_traits>
+
 #include "common.hpp"
 #include "quest.hpp"
 
@@ -191,14 +193,56 @@ __device__ inline uint32_t score_key(float x) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Inclusive scan over a wave by DPP: within rows of 16 lanes by row shifts of 1, 2, 4 and 8 (a lane shifted in from
+// outside the row adds the 0 of the old operand), then across rows: row_bcast:15 adds lane 15 of rows 0 and 2 to rows
+// 1 and 3, row_bcast:31 adds lane 31 (the total of rows 0 and 1) to rows 2 and 3.
+__device__ inline int wave_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false);  // row_bcast:15
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false);  // row_bcast:31
+    return x;
+}
+
+// The largest and smallest value over a wave (by the same DPP pattern as wave_scan; lane 63 ends with the result).
+__device__ inline uint32_t wave_max_u32(uint32_t x) {
+    auto step = [&](auto ctrl, auto rows) __attribute__((always_inline)) {
+        const uint32_t y = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+            0, static_cast<int>(x), decltype(ctrl)::value, decltype(rows)::value, 0xF, false));
+        x = x > y ? x : y;
+    };
+    using std::integral_constant;
+    step(integral_constant<int, 0x111>{}, integral_constant<int, 0xF>{});  // row_shr:1
+    step(integral_constant<int, 0x112>{}, integral_constant<int, 0xF>{});  // row_shr:2
+    step(integral_constant<int, 0x114>{}, integral_constant<int, 0xF>{});  // row_shr:4
+    step(integral_constant<int, 0x118>{}, integral_constant<int, 0xF>{});  // row_shr:8
+    step(integral_constant<int, 0x142>{}, integral_constant<int, 0xA>{});  // row_bcast:15
+    step(integral_constant<int, 0x143>{}, integral_constant<int, 0xC>{});  // row_bcast:31
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 63));
+}
+
+__device__ inline uint32_t wave_min_u32(uint32_t x) {
+    auto step = [&](auto ctrl, auto rows) __attribute__((always_inline)) {
+        const uint32_t y = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+            -1, static_cast<int>(x), decltype(ctrl)::value, decltype(rows)::value, 0xF, false));
+        x = x < y ? x : y;
+    };
+    using std::integral_constant;
+    step(integral_constant<int, 0x111>{}, integral_constant<int, 0xF>{});  // row_shr:1
+    step(integral_constant<int, 0x112>{}, integral_constant<int, 0xF>{});  // row_shr:2
+    step(integral_constant<int, 0x114>{}, integral_constant<int, 0xF>{});  // row_shr:4
+    step(integral_constant<int, 0x118>{}, integral_constant<int, 0xF>{});  // row_shr:8
+    step(integral_constant<int, 0x142>{}, integral_constant<int, 0xA>{});  // row_bcast:15
+    step(integral_constant<int, 0x143>{}, integral_constant<int, 0xC>{});  // row_bcast:31
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(x), 63));
+}
+
 // Inclusive scan of one value per thread over a 256-thread workgroup; *total receives the sum.
 __device__ inline int block_scan(int x, int* lds4, int* total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(x, off);
-        if (lane >= off) x += y;
-    }
+    x = wave_scan(x);
     if (lane == 63) lds4[wave] = x;
     __syncthreads();
     int before = 0;
@@ -214,10 +258,11 @@ __device__ inline int block_scan(int x, int* lds4, int* total) {
 template <bool IN_LDS>
 __global__ __launch_bounds__(256) void quest_topk_kernel(SelectParams p) {
     extern __shared__ uint32_t lds_keys[];
-    __shared__ int hist[256];
+    __shared__ int hist[2048];
+    __shared__ __align__(16) uint32_t cand[256];
     __shared__ int lds4[4];
-    __shared__ uint32_t shared_prefix;
-    __shared__ int shared_rem;
+    __shared__ uint32_t shared_prefix, red[8];
+    __shared__ int shared_rem, shared_m, shared_d, cand_count;
     const int row = blockIdx.x;
     const int b = row / p.kv_heads;
     const int t = threadIdx.x;
@@ -227,7 +272,7 @@ __global__ __launch_bounds__(256) void quest_topk_kernel(SelectParams p) {
     int32_t* out = p.out + static_cast<int64_t>(row) * p.pages;
     const float* scores = p.scores + static_cast<int64_t>(row) * score_stride(p.max_done);
     int total = 0;
-    if (n <= count) {  // every committed page
+    if (n <= count || count <= 0) {  // every committed page (or none to select)
         for (int i = t; i < p.pages; i += 256) out[i] = i < n ? i : -1;
         return;
     }
@@ -242,58 +287,163 @@ __global__ __launch_bounds__(256) void quest_topk_kernel(SelectParams p) {
         else
             return score_key(scores[i]);
     };
-    // radix select of the count-th largest key, most significant byte first (the histogram visits keys in any order)
-    uint32_t prefix = 0, known = 0;
+    // Selection of the count-th largest key (the threshold) and of how many keys equal to it are taken (rem). The
+    // keys at issue lie in [lo_k, hi_k], at first every key. A pass counts them into 2048 buckets by a monotone map
+    // of the key over the interval and finds the bucket holding the rem-th largest; when it has at most 256 keys,
+    // they are gathered and ranked against each other, which fixes the threshold; otherwise the interval shrinks to
+    // that bucket's smallest and largest key (the interval's own smallest or largest key always falls outside it)
+    // until it holds one key value. Histograms visit keys in any order; ties are settled by the compaction below.
+    auto block_min_max = [&](uint32_t mn, uint32_t mx, uint32_t& lo_out, uint32_t& hi_out) __attribute__((always_inline)) {
+        mn = wave_min_u32(mn);
+        mx = wave_max_u32(mx);
+        const int wave = t >> 6;
+        if (lane == 0) {
+            red[wave] = mn;
+            red[4 + wave] = mx;
+        }
+        __syncthreads();
+        lo_out = min(min(red[0], red[1]), min(red[2], red[3]));
+        hi_out = max(max(red[4], red[5]), max(red[6], red[7]));
+        __syncthreads();
+    };
+    uint32_t lo_k, hi_k;
+    {
+        uint32_t mn = 0xFFFFFFFFu, mx = 0u;
+        for (int i = t; i < n; i += 256) {
+            const uint32_t key = key_at(i);
+            mn = min(mn, key);
+            mx = max(mx, key);
+        }
+        if (t == 0) cand_count = 0;
+        block_min_max(mn, mx, lo_k, hi_k);
+    }
     int rem = count;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        hist[t] = 0;
+    uint32_t prefix = lo_k;  // the threshold
+    while (lo_k != hi_k) {
+        const float scale = 2048.0f / (static_cast<float>(hi_k - lo_k) + 1.0f);
+        const uint32_t lo = lo_k, hi = hi_k;
+        auto bucket = [&](uint32_t key) __attribute__((always_inline)) {
+            return min(2047, static_cast<int>(static_cast<float>(key - lo) * scale));
+        };
+        for (int d = t; d < 2048; d += 256) hist[d] = 0;
         __syncthreads();
         for (int i0 = t - lane; i0 < n; i0 += 256) {
-            // the wave's keys of this round: lanes whose digit equals the first matching lane's add as one
+            // the wave's keys of this round: lanes whose bucket equals the first matching lane's add as one
             const int i = i0 + lane;
             const uint32_t key = i < n ? key_at(i) : 0u;
-            const bool match = i < n && ((key ^ prefix) & known) == 0;
-            const int digit = static_cast<int>((key >> shift) & 255u);
+            const bool match = i < n && key >= lo && key <= hi;
+            const int digit = match ? bucket(key) : 0;
             const uint64_t matching = __ballot(match);
             if (matching == 0) continue;
             const int leader = __builtin_ctzll(matching);
-            const int lead_digit = __shfl(digit, leader);
+            const int lead_digit = __builtin_amdgcn_readlane(digit, leader);
             const uint64_t same = __ballot(match && digit == lead_digit);
             if (lane == leader) atomicAdd(&hist[lead_digit], static_cast<int>(__popcll(same)));
             if (match && digit != lead_digit) atomicAdd(&hist[digit], 1);
         }
         __syncthreads();
-        const int c = hist[255 - t];  // thread t counts digit 255 - t: the scan runs from the largest digit down
+        int c = 0;  // thread t holds the buckets 2047 - 8 t down to 2040 - 8 t
+#pragma unroll
+        for (int k = 0; k < 8; ++k) c += hist[2047 - 8 * t - k];
         const int incl = block_scan(c, lds4, &total);
         if (incl >= rem && incl - c < rem) {
-            shared_prefix = prefix | (static_cast<uint32_t>(255 - t) << shift);
-            shared_rem = rem - (incl - c);
+            int cum = incl - c;
+            for (int k = 0; k < 8; ++k) {
+                const int d = 2047 - 8 * t - k;
+                if (cum + hist[d] >= rem) {
+                    shared_d = d;
+                    shared_rem = rem - cum;
+                    shared_m = hist[d];
+                    break;
+                }
+                cum += hist[d];
+            }
         }
         __syncthreads();
-        prefix = shared_prefix;
+        const int d = shared_d, m = shared_m;
         rem = shared_rem;
-        known |= 0xFFu << shift;
-        __syncthreads();
+        if (m <= 256) {
+            for (int i = t; i < n; i += 256) {
+                const uint32_t key = key_at(i);
+                if (key >= lo && key <= hi && bucket(key) == d) cand[atomicAdd(&cand_count, 1)] = key;  // m slots
+            }
+            __syncthreads();
+            if (t < m) {  // the candidate whose rank range holds rem is the threshold
+                const uint32_t mine = cand[t];
+                int gt = 0, ge = 0;
+#pragma unroll 4
+                for (int j = 0; j < m; j += 4) {  // four candidates per LDS read (slots from m on are not counted)
+                    const uint4 o = reinterpret_cast<const uint4*>(cand)[j / 4];
+                    const uint32_t others[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const bool in = j + e < m;
+                        gt += in && others[e] > mine ? 1 : 0;
+                        ge += in && others[e] >= mine ? 1 : 0;
+                    }
+                }
+                if (gt < rem && rem <= ge) {
+                    shared_prefix = mine;
+                    shared_rem = rem - gt;
+                }
+            }
+            __syncthreads();
+            prefix = shared_prefix;
+            rem = shared_rem;
+            break;
+        }
+        uint32_t mn = 0xFFFFFFFFu, mx = 0u;
+        for (int i = t; i < n; i += 256) {
+            const uint32_t key = key_at(i);
+            if (key >= lo && key <= hi && bucket(key) == d) {
+                mn = min(mn, key);
+                mx = max(mx, key);
+            }
+        }
+        block_min_max(mn, mx, lo_k, hi_k);
+        prefix = lo_k;
     }
     // keys above the threshold, and the first `rem` keys equal to it in page order: thread t takes a contiguous range
+    // of `per` keys, held in registers when there are at most 8
     const int per = (n + 255) / 256;
     const int i0 = min(t * per, n), i1 = min(i0 + per, n);
-    int eq = 0;
-    for (int i = i0; i < i1; ++i) eq += key_at(i) == prefix ? 1 : 0;
-    int eq_before = block_scan(eq, lds4, &total) - eq;
-    int sel = 0;
-    for (int i = i0, e = eq_before; i < i1; ++i) {
-        const uint32_t key = key_at(i);
-        if (key > prefix) ++sel;
-        else if (key == prefix) sel += e++ < rem ? 1 : 0;
-    }
-    int pos = block_scan(sel, lds4, &total) - sel;
-    for (int i = i0, e = eq_before; i < i1; ++i) {
-        const uint32_t key = key_at(i);
-        bool take = key > prefix;
-        if (key == prefix) take = e++ < rem;
-        if (take) out[pos++] = i;
-    }
+    auto compact = [&](auto cache_tag) __attribute__((always_inline)) {
+        constexpr int C = decltype(cache_tag)::value;  // keys held in registers (0: read at every use)
+        uint32_t held[C > 0 ? C : 1];
+        if constexpr (C > 0) {
+#pragma unroll
+            for (int k = 0; k < C; ++k) held[k] = i0 + k < i1 ? key_at(i0 + k) : 0u;
+        }
+        const int span = C > 0 ? C : i1 - i0;
+        auto key_of = [&](int k) __attribute__((always_inline)) { return C > 0 ? held[k] : key_at(i0 + k); };
+        int eq = 0;
+#pragma unroll
+        for (int k = 0; k < span; ++k) eq += i0 + k < i1 && key_of(k) == prefix ? 1 : 0;
+        const int eq_before = block_scan(eq, lds4, &total) - eq;
+        int sel = 0;
+        int e = eq_before;
+#pragma unroll
+        for (int k = 0; k < span; ++k) {
+            if (i0 + k >= i1) continue;
+            const uint32_t key = key_of(k);
+            if (key > prefix) ++sel;
+            else if (key == prefix) sel += e++ < rem ? 1 : 0;
+        }
+        int pos = block_scan(sel, lds4, &total) - sel;
+        e = eq_before;
+#pragma unroll
+        for (int k = 0; k < span; ++k) {
+            if (i0 + k >= i1) continue;
+            const uint32_t key = key_of(k);
+            bool take = key > prefix;
+            if (key == prefix) take = e++ < rem;
+            if (take) out[pos++] = i0 + k;
+        }
+    };
+    if (per <= 8)
+        compact(std::integral_constant<int, 8>{});
+    else
+        compact(std::integral_constant<int, 0>{});
     for (int i = count + t; i < p.pages; i += 256) out[i] = -1;
 }
 

@@ -122,6 +122,31 @@ def test_tied_scores_go_to_the_lower_page() -> None:
         assert np.array_equal(got.cpu().numpy(), want), pages
 
 
+def test_selection_narrows_crowded_buckets() -> None:
+    """Score distributions that crowd the bucket of the threshold: 1500 tied pages above the rest (the threshold is
+    their one value), a row whose pages all tie, and a cluster of 500 distinct scores between 10 far outliers and one
+    far negative page (at 255 pages the threshold's bucket of the whole range holds 394 keys, which are counted again
+    over their own range before they are ranked)."""
+    from economize_amd.quest import select_pages
+
+    rng = np.random.default_rng(9)
+    lo, hi = _random_bounds(rng, 3, 1, 2000, 128)
+    q = bf16_bits_to_f32(f32_to_bf16_bits(rng.standard_normal((3, 4, 1, 128)).astype(np.float32)))
+    lo[0, 0, 300:1800] = lo[0, 0, 5]
+    hi[0, 0, 300:1800] = lo[0, 0, 5] + 3.0
+    lo[1, 0, :] = lo[1, 0, 0]
+    hi[1, 0, :] = hi[1, 0, 0]
+    hi[2, 0, 0:10] += 500.0
+    hi[2, 0, 100:600] = lo[2, 0, 100:600] + 5.0 + 0.01 * rng.standard_normal((500, 128)).astype(np.float32)
+    lo[2, 0, 1999] = hi[2, 0, 1999] = -500.0 * np.sign(q[2].sum(axis=(0, 1)))
+    lo, hi = bf16_bits_to_f32(f32_to_bf16_bits(lo)), bf16_bits_to_f32(f32_to_bf16_bits(hi))
+    done = np.array([2000, 2000, 2000], np.int32)
+    for pages in (63, 255):
+        got = select_pages(_to_bf16(q), _to_bf16(lo), _to_bf16(hi), torch.from_numpy(done).cuda(), 2000, pages)
+        want = oquest.select_pages(q, lo, hi, done, 2000, pages)
+        assert np.array_equal(got.cpu().numpy(), want), pages
+
+
 def test_no_committed_pages_selects_nothing() -> None:
     from economize_amd.quest import select_pages
 
