@@ -179,9 +179,27 @@ __global__ __launch_bounds__(256) void quest_score_kernel(SelectParams p) {
                 s2 = i == 0 ? t2 : s2 + t2;
             }
         }
-        for (int off = L / 2; off > 0; off >>= 1) {
-            s1 += __shfl_xor(s1, off);
-            s2 += __shfl_xor(s2, off);
+        if (L == 16) {
+            // the halving tree over a DPP row: lane j < off adds lane j + off (row_shl), which for lane 0 is the
+            // xor tree below, term for term
+            auto fold = [&](float& x, auto ctrl) __attribute__((always_inline)) {
+                x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                                           decltype(ctrl)::value, 0xF, 0xF, false));
+            };
+            using std::integral_constant;
+            fold(s1, integral_constant<int, 0x108>{});  // row_shl:8
+            fold(s2, integral_constant<int, 0x108>{});
+            fold(s1, integral_constant<int, 0x104>{});  // row_shl:4
+            fold(s2, integral_constant<int, 0x104>{});
+            fold(s1, integral_constant<int, 0x102>{});  // row_shl:2
+            fold(s2, integral_constant<int, 0x102>{});
+            fold(s1, integral_constant<int, 0x101>{});  // row_shl:1
+            fold(s2, integral_constant<int, 0x101>{});
+        } else {
+            for (int off = L / 2; off > 0; off >>= 1) {
+                s1 += __shfl_xor(s1, off);
+                s2 += __shfl_xor(s2, off);
+            }
         }
         if (page < p1 && j == 0) out[page] = page < done ? s1 + s2 : -INFINITY;
     }
