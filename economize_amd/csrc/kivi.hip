@@ -27,7 +27,8 @@
 //
 // Work decomposition, pipeline and merge: the stream-K scheme of paged_attention.hip (stream_k.hpp), with tiles of
 // one 32-token page. The query of the current row lives in LDS, so that row changes do not put loads of varying
-// count in the tile pipeline.
+// count in the tile pipeline. With more than 32 query rows per KV head (speculative verification) the four waves of
+// a workgroup share each tile instead: one column block of query rows each, the keys dequantized once into LDS.
 
 #include <cstdlib>
 #include <type_traits>
