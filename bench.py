@@ -10,8 +10,14 @@ drawn N(0, 1) in bf16 from a seeded generator and quantize-appended into the cac
 * ``roofline``: the call is one kernel launch (``paged_attention_kernel``): algorithmic bytes per launch (KV + q +
   out + block table + lengths + scales) over its average launch time, against 8 TB/s.
 * ``ragged``: the same with lengths drawn uniformly from [1024, 8192] (mean 4608).
-* ``cpu_baseline``: the numpy oracle (the fp32 definition over gathered, decoded pages) on a bounded sample of rows
-  of the L = 4096 workload, one thread, extrapolated to the whole batch.
+* ``cpu_baseline``: the numpy oracle (the fp32 definition over gathered, decoded pages) over whole calls of the
+  L = 4096 workload on one thread, for about 10 s.
+
+Every path's timed calls rotate over distinct copies of the cache (1 + ceil(384 MB / bytes per call) copies of the
+K/V data, KIVI pages and rings, Quest bounds), the way a decode step reads a different layer's cache at every call
+while the layers share the block table, the lengths and, here, the query: so no call finds its cache data in the
+256 MB Infinity Cache from its previous use (with a single copy the L = 4096 call reads about a sixth of its bytes
+from that cache). ``--single-copy`` measures the single-copy figures.
 
 ``--gpus`` must be 1: the path runs on one GPU.
 """
@@ -19,6 +25,7 @@ drawn N(0, 1) in bf16 from a seeded generator and quantize-appended into the cac
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import math
 import os
@@ -99,24 +106,47 @@ def call_bytes(lens: list[int]) -> int:
     return kv_bytes(lens) + 2 * BATCH * Q_HEADS * HEAD_DIM * 2 + pages * 4 + BATCH * 4 + 2 * KV_HEADS * 4
 
 
+INFINITY_CACHE_MARGIN = 384e6  # bytes the other copies must hold, beyond the 256 MB Infinity Cache
+SINGLE_COPY = False  # --single-copy: every call on the same inputs
+
+
+def copies_for(nbytes: int) -> int:
+    """Distinct input copies the timed calls rotate over, so that a call's data has left the Infinity Cache."""
+    return 1 if SINGLE_COPY else 1 + math.ceil(INFINITY_CACHE_MARGIN / nbytes)
+
+
+def rotating(calls: list):
+    """One function that runs calls[0], calls[1], ... in turn."""
+    state = [0]
+
+    def call() -> None:
+        calls[state[0] % len(calls)]()
+        state[0] += 1
+
+    return call
+
+
 def measure(lens: list[int], steps: int, warmup: int, seed: int) -> dict:
     import torch
 
     from economize_amd.paged import new_workspace, paged_decode_attention, workspace_size
 
-    q, cache, table, seq_lens = build_workload(lens, seed)
     smax = max(lens)
+    q, cache, table, seq_lens = build_workload(lens, seed)
+    caches = [cache] + [dataclasses.replace(cache, keys=cache.keys.clone(), values=cache.values.clone())
+                        for _ in range(1, copies_for(call_bytes(lens)))]
     out = torch.empty_like(q)
     ws = new_workspace(workspace_size(BATCH, 1, Q_HEADS, KV_HEADS, HEAD_DIM, smax, 0, cache.dtype), q.device)
 
-    def call() -> None:
-        paged_decode_attention(q, cache, table, seq_lens, smax, out=out, workspace=ws)
+    def call_on(c):
+        return lambda: paged_decode_attention(q, c, table, seq_lens, smax, out=out, workspace=ws)
 
-    seconds = time_calls(call, steps, warmup)
+    seconds = time_calls(rotating([call_on(c) for c in caches]), steps, warmup)
     return {
         "seconds": seconds,
         "kv_bytes": kv_bytes(lens),
         "call_bytes": call_bytes(lens),
+        "copies": len(caches),
         "workload": (q, cache, table, seq_lens, out),
     }
 
@@ -243,22 +273,28 @@ def measure_kivi(bits: int, steps: int, warmup: int, seed: int, batch=16, querie
 
     lens = lens or [8192] * batch
     q, cache, table, seq, kq, vq = kivi_workload(batch, queries, q_heads, kv_heads, lens, bits, seed)
+    nbytes = kivi_call_bytes(lens, kq, vq, bits, batch, queries, q_heads, kv_heads)
+    caches = [cache] + [dataclasses.replace(cache, blocks=cache.blocks.clone(), k_ring=cache.k_ring.clone(),
+                                            v_ring=cache.v_ring.clone()) for _ in range(1, copies_for(nbytes))]
     out = torch.empty_like(q)
     smax = max(lens)
-    seconds = time_calls(lambda: kivi_decode_attention(q, cache, table, seq, smax, out=out), steps, warmup)
-    nbytes = kivi_call_bytes(lens, kq, vq, bits, batch, queries, q_heads, kv_heads)
+
+    def call_on(c):
+        return lambda: kivi_decode_attention(q, c, table, seq, smax, out=out)
+
+    seconds = time_calls(rotating([call_on(c) for c in caches]), steps, warmup)
     flops = sum(2 * 2 * kv_heads * (q_heads // kv_heads) * queries * n * HEAD_DIM for n in lens)
-    del cache
+    copies = len(caches)
+    del caches, cache
     return {"us_per_call": round(seconds * 1e6, 2), "algorithmic_bytes": nbytes,
             "gb_s": round(nbytes / seconds / 1e9, 1), "hbm_frac": round(nbytes / seconds / 1e9 / HBM_PEAK_GBS, 4),
-            "tflop_s": round(flops / seconds / 1e12, 2)}
+            "tflop_s": round(flops / seconds / 1e12, 2), "copies": copies}
 
 
-def measure_quest(steps: int, warmup: int, seed: int, batch=8, q_heads=32, kv_heads=8, length=32768, budget=1024,
-                  planted=32) -> dict:
-    """Quest decode: bf16 K/V in 16-token pages; per (row, KV head) `planted` pages whose keys are the group's first
-    query plus 0.1 N(0, 1); bounds of the committed pages built once (the cache maintains them); a call is the
-    selection (scores + top-k) plus the attention over the selected pages and the dense tail."""
+def quest_workload(seed: int, batch: int, q_heads: int, kv_heads: int, length: int, budget: int, planted: int):
+    """bf16 K/V in 16-token pages; per (row, KV head) `planted` pages whose keys are the group's first query plus
+    0.1 N(0, 1); the bounds of the committed pages (the cache maintains them). Returns the query [B, Hq, 1, D], the
+    cache, the block table, the lengths and the QuestPages."""
     import torch
 
     from economize_amd.paged import PagedKVCache, paged_append
@@ -287,20 +323,40 @@ def measure_quest(steps: int, warmup: int, seed: int, batch=8, q_heads=32, kv_he
     pages = budget // PAGE - 1
     qp = QuestPages(kmin, kmax, torch.full((batch,), done, dtype=torch.int32, device=device), done, done, PAGE, pages)
     seq = torch.full((batch,), length, dtype=torch.int32, device=device)
-    query = q.transpose(1, 2)
-    out = torch.empty_like(q)
+    return q.transpose(1, 2), cache, table, seq, qp
+
+
+def measure_quest(steps: int, warmup: int, seed: int, batch=8, q_heads=32, kv_heads=8, length=32768, budget=1024,
+                  planted=32) -> dict:
+    """Quest decode: a call is the selection (scores + top-k) plus the attention over the selected pages and the
+    dense tail, over the workload of quest_workload."""
+    import torch
+
     from economize_amd.quest import quest_decode_attention
 
-    seconds = time_calls(lambda: quest_decode_attention(query, cache, table, seq, length, qp, out=out), steps, warmup)
     d = HEAD_DIM
+    done = (length - 1) // PAGE
+    pages = budget // PAGE - 1
     tail = length - done * PAGE
     nbytes = (batch * kv_heads * (2 * d * 2 * done + (pages * PAGE + tail) * 2 * d * 2 + done * 4 * 2)
               + 2 * batch * q_heads * d * 2 + batch * kv_heads * pages * 4 * 2)
+    query, cache, table, seq, qp = quest_workload(seed, batch, q_heads, kv_heads, length, budget, planted)
+    loads = [(cache, qp)] + [(dataclasses.replace(cache, keys=cache.keys.clone(), values=cache.values.clone()),
+                              dataclasses.replace(qp, kmin=qp.kmin.clone(), kmax=qp.kmax.clone()))
+                             for _ in range(1, copies_for(nbytes))]
+    out = torch.empty(batch, 1, q_heads, d, dtype=torch.bfloat16, device="cuda:0")
+
+    def call_on(load):
+        c, pages_ = load
+        return lambda: quest_decode_attention(query, c, table, seq, length, pages_, out=out)
+
+    seconds = time_calls(rotating([call_on(load) for load in loads]), steps, warmup)
     torch.cuda.synchronize()
-    del cache, kmin, kmax
+    copies = len(loads)
+    del loads, cache, qp
     return {"us_per_call": round(seconds * 1e6, 2), "algorithmic_bytes": nbytes,
             "gb_s": round(nbytes / seconds / 1e9, 1), "hbm_frac": round(nbytes / seconds / 1e9 / HBM_PEAK_GBS, 4),
-            "dense_bytes_avoided": batch * kv_heads * length * 2 * d * 2}
+            "dense_bytes_avoided": batch * kv_heads * length * 2 * d * 2, "copies": copies}
 
 
 def measure_paths(steps: int, warmup: int, seed: int) -> dict:
@@ -345,6 +401,8 @@ def main() -> None:
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--fixed-only", action="store_true", help="skip the ragged-length run (for profiling)")
     parser.add_argument("--no-paths", action="store_true", help="skip the KIVI and Quest measurements")
+    parser.add_argument("--single-copy", action="store_true",
+                        help="time every call on the same inputs (partly served by the 256 MB Infinity Cache)")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run a plain device copy of 256 MiB, 20 times (the reference kernel for scaling the "
                              "FETCH_SIZE / WRITE_SIZE counters of rocprofv3)")
@@ -357,6 +415,8 @@ def main() -> None:
     import numpy as np
     import torch
 
+    global SINGLE_COPY
+    SINGLE_COPY = args.single_copy
     if args.copy_calibration:
         src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda:0")
         dst = torch.empty_like(src)
@@ -397,6 +457,7 @@ def main() -> None:
             "workload": "fp8 e4m3 paged decode attention (per-head scales), Llama-3-8B decode shape",
             "batch": BATCH, "q_len": 1, "q_heads": Q_HEADS, "kv_heads": KV_HEADS, "head_dim": HEAD_DIM,
             "seq_len": 4096, "page_size": PAGE, "kv_bytes_per_call": head["kv_bytes"],
+            "input_copies": head["copies"],
             "compute": "bf16 x bf16 MFMA for q.k, fp16 x fp16 MFMA for p.v, fp32 accumulation",
         },
         "roofline": {
