@@ -402,7 +402,8 @@ kivi_attention_kernel(KiviParams p) {
     constexpr int R = NB * 16;  // query rows of the MFMA columns
     constexpr int WAVES = kivi_wg_waves<D, NB, SHARED>();
     constexpr bool kSplit = !SHARED && WAVES > 1;  // the range split in quarters, pieces merged in LDS
-    using QRows = uint4[R][D / 8];                 // a wave's current query rows
+    using QRows = uint4[R][D / 8 + 1];             // a wave's current query rows (one word of padding: a row stride of
+                                                   // D / 8 + 1 words puts the 16 rows of a lane group in distinct banks)
 
     const int lane = WAVES > 1 ? static_cast<int>(threadIdx.x) & 63 : static_cast<int>(threadIdx.x);
     const int wave = WAVES > 1 ? uniform(static_cast<int>(threadIdx.x) >> 6) : 0;
