@@ -114,6 +114,15 @@ class PagedKIVICache:
             if counts.dtype != torch.int32 or counts.shape != (b,):
                 raise ConfigError(f"KIVI {name} must be int32 [{b}]")
 
+    def check_flags(self) -> None:
+        """The reference's pass-boundary check (techniques/kv_quant/packed.py:175-188): raises ConfigError when a
+        quantization since the last check produced a scale or zero point beyond fp16, which the packed pages cannot
+        hold, and clears the flag. It reads the device flag, so it waits for the quantizations before it."""
+        if int(self.overflow.item()):
+            self.overflow.zero_()
+            raise ConfigError(
+                "a KIVI scale or zero point exceeds the fp16 range of the packed storage; use storage='simulated'")
+
 
 def _table(block_table: torch.Tensor, batch: int) -> None:
     if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.shape[0] != batch or \
@@ -171,6 +180,12 @@ def kivi_commit(cache: PagedKIVICache, block_table: torch.Tensor, committed: tor
     not yet quantized, and advances the counts. ``max_new`` bounds the tokens a row commits since the last call (it
     sizes the launches; the rings must still hold them). Returns the int32 ``[4, B]`` ranges quantized."""
     cache.check()
+    headroom = cache.ring - cache.residual
+    if int(max_new) > headroom:  # the reference's ring check (techniques/kv_quant/packed.py:180-183)
+        raise ConfigError(
+            f"a pass of {int(max_new)} tokens is more than the KIVI ring holds beyond the residual ({cache.ring} slots "
+            f"= residual_length + headroom {headroom}) and would overwrite entries not quantized yet: increase headroom "
+            "or use storage='simulated'")
     _table(block_table, cache.batch)
     device = _lib.require_gpu(committed, block_table, cache.blocks)
     if committed.dtype != torch.int32 or committed.shape != (cache.batch,):

@@ -131,6 +131,22 @@ def test_prompt_quantization_matches_the_oracle(bits, head_dim) -> None:
     assert int(cache.overflow.item()) == 0
 
 
+def test_scales_beyond_the_fp16_range_are_refused() -> None:
+    """The reference's test_scales_beyond_the_fp16_range_are_refused (tests/techniques/test_kv_kivi_packed.py:
+    158-164): keys 1e5 times larger quantize to scales and zero points beyond fp16, which the packed pages cannot
+    hold; the device flag turns into a ConfigError at the next check, which clears it."""
+    import dataclasses
+
+    from economize_amd.errors import ConfigError
+
+    c = make_case(1, 1, 8, 2, 64, [300], 2, seed=5)
+    c = dataclasses.replace(c, k=(c.k.float() * 1e5).to(torch.bfloat16))
+    cache, _ = device_cache(c)
+    with pytest.raises(ConfigError, match="fp16"):
+        cache.check_flags()
+    cache.check_flags()
+
+
 def test_decode_time_schedule_matches_one_shot_quantization() -> None:
     """Tokens appended one at a time with the schedule run after every step (kivi_commit) leave the same pages and
     counts as quantizing the final prefixes at once."""

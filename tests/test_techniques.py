@@ -158,3 +158,15 @@ def test_cached_workspace_clears_counters_a_previous_call_may_have_dirtied() -> 
     assert int(buf[:768].sum()) == 0 and int(buf[768:].min()) == 7
     grown = ws.take(8192, counter_bytes(70, 2), "cpu")
     assert grown.numel() == 8192 and int(grown.sum()) == 0
+
+
+def test_a_kivi_pass_longer_than_the_headroom_is_refused() -> None:
+    """The reference's test_a_pass_longer_than_the_headroom_is_refused (tests/techniques/test_kv_kivi_packed.py:
+    151-155): a commit of more tokens than the ring holds beyond the residual would overwrite ring entries not yet
+    quantized, so it raises before anything runs."""
+    from economize_amd.kivi import PagedKIVICache, kivi_commit
+
+    cache = PagedKIVICache.empty(4, 1, 1, 64, 2, "cpu", residual=32, headroom=32)
+    with pytest.raises(ConfigError, match="headroom"):
+        kivi_commit(cache, torch.zeros(1, 4, dtype=torch.int32), torch.zeros(1, dtype=torch.int32), 33)
+
