@@ -450,7 +450,7 @@ kivi_attention_kernel(KiviParams p) {
     // ---- row state ----
     float limit[NB];
     int all_see = 0, kq = 0, vq = 0, row_len = 0;
-    float m_i[NB], l_i[NB];
+    float m_i[NB], l_i[NB];  // l_i: the sum over the lane's own tokens until the segment's end reduces it
     f32x4 acc[ND][NB], gam[NB];
 
     auto begin_row = [&](const Cursor& c) __attribute__((always_inline)) {
@@ -610,10 +610,10 @@ kivi_attention_kernel(KiviParams p) {
             for (int v = 0; v < 2; ++v)
                 tile_max = max_nan(max_nan(tile_max, max_nan(s[v][nb][0], s[v][nb][1])),
                                    max_nan(s[v][nb][2], s[v][nb][3]));
-            tile_max = group_max(tile_max);
+            // the ballot sees every lane's own maximum, so only a rescale needs the maximum over the lane group
             if (__ballot(tile_max > m_i[nb] + 8.0f || m_i[nb] == -INFINITY) != 0) {
                 const bool fresh = m_i[nb] == -INFINITY;
-                const float m_new = fmaxf(m_i[nb], tile_max);
+                const float m_new = fmaxf(m_i[nb], group_max(tile_max));
                 const float alpha = fresh ? 0.0f : __builtin_amdgcn_exp2f(m_i[nb] - m_new);
                 l_i[nb] *= alpha;
 #pragma unroll
@@ -633,7 +633,7 @@ kivi_attention_kernel(KiviParams p) {
                     pw[nb][4 * v + i] = __builtin_amdgcn_exp2f(s[v][nb][i] + neg_m);
                     sum += pw[nb][4 * v + i];
                 }
-            l_i[nb] += group_sum(sum);
+            l_i[nb] += sum;  // the lane's own tokens; summed over the lane group at the end of the segment
         }
         // values: element e of the lane's operands is token t0 + 8 g + e
         const int tok0 = t0 + 8 * g;
@@ -723,6 +723,8 @@ kivi_attention_kernel(KiviParams p) {
 
     // ---- end of a row segment: direct output, or a partial and (for the last wave of the row) the merge ----
     auto finish = [&](const Cursor& c, int64_t seg_begin, int64_t seg_end, bool first_segment) __attribute__((always_inline)) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) l_i[nb] = group_sum(l_i[nb]);
         // the value zero-point term of channel 16 nd + 4 g + i: row (group (16 nd) / 32) of the gamma tile, held by
         // lane group 0, column n
         float o[ND][NB][4];

@@ -308,7 +308,7 @@ paged_attention_kernel(PagedParams p) {
     float limit[NB];
     int all_see = 0;  // tokens below this are visible to every query row of the row
     float score_scale = 0.0f, vs = 1.0f;
-    float m_i[NB], l_i[NB];
+    float m_i[NB], l_i[NB];  // l_i: the sum over the lane's own tokens until the segment's end reduces it
     f32x4 acc[ND][NB];
 
     auto begin_row = [&](const Cursor& c) __attribute__((always_inline)) {
@@ -410,17 +410,17 @@ paged_attention_kernel(PagedParams p) {
             for (int v = 0; v < 4; ++v)
                 tile_max = max_nan(max_nan(tile_max, max_nan(s[v][nb][0], s[v][nb][1])),
                                    max_nan(s[v][nb][2], s[v][nb][3]));
-            tile_max = group_max(tile_max);
             // Lazy rescaling: the reference maximum m_i moves only when a score exceeds it by more than 2^8, so that
             // the accumulators are rescaled a few times per row instead of at every tile (the weights stay below
-            // 2^8, far inside fp16's range; the quotient acc / l does not depend on the reference). The bf16 instance
+            // 2^8, far inside fp16's range; the quotient acc / l does not depend on the reference). The ballot sees
+            // every lane's own maximum; only a rescale needs the maximum over the lane group. The bf16 instance
             // at D = 256 rescales at every tile: on gfx950 its lazy form (and a form with the scale folded into the
             // exponent) gave wrong results although the same source is correct in every other instance.
             constexpr float lazy = FMT == BF16 && D > 128 ? 0.0f : 8.0f;
             if constexpr (kTwoWaves) {
                 if (lazy == 0.0f || __ballot(tile_max > m_i[nb] + lazy || m_i[nb] == -INFINITY) != 0) {
                     const bool fresh = m_i[nb] == -INFINITY;
-                    const float m_new = fmaxf(m_i[nb], tile_max);
+                    const float m_new = fmaxf(m_i[nb], group_max(tile_max));
                     const float alpha = fresh ? 0.0f : __builtin_amdgcn_exp2f(m_i[nb] - m_new);
                     l_i[nb] *= alpha;
 #pragma unroll
@@ -430,7 +430,7 @@ paged_attention_kernel(PagedParams p) {
                     m_i[nb] = m_new;
                 }
             } else if (lazy == 0.0f || __ballot(tile_max > m_i[nb] + lazy) != 0) {
-                const float m_new = fmaxf(m_i[nb], tile_max);
+                const float m_new = fmaxf(m_i[nb], group_max(tile_max));
                 const float alpha = m_i[nb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_i[nb] - m_new);
                 l_i[nb] *= alpha;
 #pragma unroll
@@ -447,7 +447,7 @@ paged_attention_kernel(PagedParams p) {
                     pw[v][i] = __builtin_amdgcn_exp2f(s[v][nb][i] + neg_m);
                     sum += pw[v][i];
                 }
-            l_i[nb] += group_sum(sum);
+            l_i[nb] += sum;
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const float* a = pw[2 * u];
@@ -506,6 +506,8 @@ paged_attention_kernel(PagedParams p) {
 
     // ---- end of a row segment: direct output, or a partial and (for the last wave of the row) the merge ----
     auto finish = [&](const Cursor& c, int64_t seg_begin, int64_t seg_end, bool first_segment) __attribute__((always_inline)) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) l_i[nb] = group_sum(l_i[nb]);
         const int64_t row_end = c.row_start + c.row.tiles;
         if (seg_begin == c.row_start && seg_end == row_end) {
 #pragma unroll
