@@ -341,9 +341,11 @@ __device__ inline void merge_row(const P& p, const Cursor& c, int prev, int64_t 
 // ---- the pieces of rows inside one multi-wave workgroup ----------------------------------------------------------
 // Each wave of a workgroup takes a contiguous part of the workgroup's tile range; its first and last row segments
 // that are not whole rows are left in LDS as pieces (maxima, sums and output values of at most 16 query rows). After
-// a barrier the first wave merges the pieces of every row: a row inside the workgroup's range is written out, a row
-// cut at a range boundary becomes the workgroup's partial in the workspace (slot 0 when the row started before the
-// workgroup, else slot 1) and joins the counter merge of merge_row.
+// a barrier the pieces are merged per row, the rows taken by the waves in turn: a row inside the workgroup's range is
+// written out, a row cut at a range boundary becomes the workgroup's partial in the workspace (slot 0 when the row
+// started before the workgroup, else slot 1) and joins the counter merge of merge_row. The two rows cut at the range's
+// ends go to different waves, so that their workspace round trips (partial stores, counter, the last part's merge)
+// overlap instead of following each other.
 template <int D, int WAVES>
 struct Pieces {
     float data[2 * WAVES][16 * (D + 2)];
@@ -384,9 +386,8 @@ template <int D, int WAVES, typename P>
 __device__ inline void merge_pieces(const P& p, Pieces<D, WAVES>& pc, int wave, int lane, int64_t wlo, int64_t whi,
                                     int64_t total, int grid, int w) {
     __syncthreads();
-    if (wave != 0) return;
     const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
-    int k = 0;
+    int k = 0, group = 0;
     while (k < 2 * WAVES) {
         const int64_t row = pc.row[k];
         if (row < 0) {
@@ -406,6 +407,7 @@ __device__ inline void merge_pieces(const P& p, Pieces<D, WAVES>& pc, int wave, 
         c.row.tiles = pc.tiles[k];
         c.row_start = row;
         k = k2;
+        if (group++ % WAVES != wave) continue;
         const bool inside = row >= wlo && row + c.row.tiles <= whi;
         float* slot = p.part + (2 * static_cast<int64_t>(w) + (wlo < row ? 1 : 0)) * stride;
         for (int base = 0; base < p.rows * D; base += 64 * 8) {
