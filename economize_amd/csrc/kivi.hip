@@ -327,8 +327,8 @@ __device__ inline void load_words(const uint32_t* src, uint32_t (&dst)[N]) {
 }
 
 // Issues the page loads of the tile under cursor c (the same loads in every lane and for every tile: a tile without
-// a page reads page 0 and masks it).
-template <int D, int BITS, bool SHARED>
+// a page reads page 0 and masks it). PARTS: 1 the keys, 2 the values, 3 both.
+template <int D, int BITS, bool SHARED, int PARTS = 3>
 __device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c, int n, int g, int lane, int wave,
                                            PageWindow& win, KTile<D, BITS, SHARED>& tile) {
     using T = KTile<D, BITS, SHARED>;
@@ -337,7 +337,8 @@ __device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c,
     const int phys = __builtin_amdgcn_readlane(win.physical, c.t - win.base);
     tile.page = phys;
     const uint8_t* blk = p.blocks + static_cast<int64_t>(phys >= 0 ? phys : 0) * p.blk_page + c.kvh * p.blk_head;
-    if constexpr (SHARED) {
+    if constexpr (!(PARTS & 1)) {
+    } else if constexpr (SHARED) {
         const int j = (wave * T::KE) >> 1;  // the k-step of every entry of the lane
 #pragma unroll
         for (int e = 0; e < T::KE; ++e) {
@@ -358,18 +359,20 @@ __device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c,
     }
     constexpr int TPW = 32 / BITS;  // tokens per value word
     const int u = 8 * g / TPW;
-    load_words(reinterpret_cast<const uint32_t*>(blk + L.v_codes()) + (u * 16 + n) * T::ND, tile.vc);
-    if constexpr (!SHARED) {
+    if constexpr (PARTS & 2) load_words(reinterpret_cast<const uint32_t*>(blk + L.v_codes()) + (u * 16 + n) * T::ND, tile.vc);
+    if constexpr (!SHARED && (PARTS & 1)) {
 #pragma unroll
         for (int j = 0; j < T::KS; ++j) {
             tile.ks[j] = *reinterpret_cast<const uint4*>(blk + L.k_scale() + (g * (D / 4) + 8 * j) * 2);
             tile.kz[j] = *reinterpret_cast<const uint4*>(blk + L.k_zero() + (g * (D / 4) + 8 * j) * 2);
         }
     }
+    if constexpr (PARTS & 2) {
 #pragma unroll
-    for (int grp = 0; grp < T::VG; ++grp)
-        tile.vs[grp] = *reinterpret_cast<const uint4*>(blk + L.v_scale() + (grp * 32 + 8 * g) * 2);
-    tile.vz = *reinterpret_cast<const uint4*>(blk + L.v_zero() + ((n % T::VG) * 32 + 8 * g) * 2);
+        for (int grp = 0; grp < T::VG; ++grp)
+            tile.vs[grp] = *reinterpret_cast<const uint4*>(blk + L.v_scale() + (grp * 32 + 8 * g) * 2);
+        tile.vz = *reinterpret_cast<const uint4*>(blk + L.v_zero() + ((n % T::VG) * 32 + 8 * g) * 2);
+    }
 }
 
 }  // namespace
@@ -387,14 +390,14 @@ constexpr int kivi_wg_waves() {
 // Waves per SIMD: two for the single-buffer instances of one column block, SHARED ones included (they fit 256
 // registers, and two workgroups' LDS fit a CU); one wave of a SIMD does not overlap its own arithmetic with its
 // outstanding loads, two waves do.
-template <int D, int NB, int NBUF>
+template <int D, int NB, int NBUF, bool SHARED>
 constexpr int kivi_waves_per_simd() {
-    return NB == 1 && D <= 128 && NBUF == 1 ? 2 : 1;
+    return NB == 1 && D <= 128 && (NBUF == 1 || SHARED) ? 2 : 1;
 }
 
 template <int D, int BITS, int NB, int NBUF, bool SHARED>
 __global__ __launch_bounds__((64 * kivi_wg_waves<D, NB, SHARED>()))
-    __attribute__((amdgpu_waves_per_eu(kivi_waves_per_simd<D, NB, NBUF>()))) void
+    __attribute__((amdgpu_waves_per_eu(kivi_waves_per_simd<D, NB, NBUF, SHARED>()))) void
 kivi_attention_kernel(KiviParams p) {
     static_assert(!SHARED || NB == 1, "a shared-tile wave holds one column block");
     using T = KTile<D, BITS, SHARED>;
@@ -799,12 +802,16 @@ kivi_attention_kernel(KiviParams p) {
         }
         begin_row(cur);
 
+        // SHARED with two buffers: the buffers hold keys, issued a tile ahead; a tile's values are issued at its own
+        // step, before the next tile's keys, and arrive while its keys are shared and its scores computed
+        constexpr bool kKeysAhead = SHARED && NBUF == 2;
         T bufs[NBUF];
+        T vt;
         Cursor cs[NBUF];
         Cursor icur = cur;
         int64_t ipos = lo;
         auto issue_next = [&](T& buf, Cursor& slot) __attribute__((always_inline)) {
-            issue_tile<D, BITS, SHARED>(p, icur, n, g, lane, wave, win, buf);
+            issue_tile<D, BITS, SHARED, kKeysAhead ? 1 : 3>(p, icur, n, g, lane, wave, win, buf);
             slot = icur;
             if (ipos < hi) {
                 if (ipos + 1 < hi) advance(p, icur, small ? &rt : nullptr);
@@ -818,6 +825,7 @@ kivi_attention_kernel(KiviParams p) {
         auto step = [&](auto tag) __attribute__((always_inline)) -> bool {
             constexpr int I = decltype(tag)::value;
             constexpr int J = (I + NBUF - 1) % NBUF;
+            if constexpr (kKeysAhead) issue_tile<D, BITS, SHARED, 2>(p, cs[I], n, g, lane, wave, win, vt);
             issue_next(bufs[J], cs[J]);
             cur = cs[I];
             if (cur.t == 0 && pos != lo) begin_row(cur);
@@ -827,7 +835,10 @@ kivi_attention_kernel(KiviParams p) {
                 if (KPAGE * cur.t < kq) share_keys(bufs[I], static_cast<int>(pos & 1));
                 __syncthreads();
             }
-            compute(bufs[I], cur, static_cast<int>(pos & 1));
+            if constexpr (kKeysAhead)
+                compute(vt, cur, static_cast<int>(pos & 1));
+            else
+                compute(bufs[I], cur, static_cast<int>(pos & 1));
             const bool more = pos + 1 < hi;
             if (cur.t + 1 == cur.row.tiles || !more) {
                 finish(cur, seg_begin, pos + 1, first_segment);
@@ -869,6 +880,17 @@ int kivi_stages() {
     return stages;
 }
 
+// Key buffers of the shared-tile instance: 2 (a tile's keys issued a tile ahead, the default) or 1;
+// ECO_KIVI_SHARED_STAGES overrides.
+int kivi_shared_stages() {
+    static const int stages = [] {
+        const char* env = std::getenv("ECO_KIVI_SHARED_STAGES");
+        const int v = env ? std::atoi(env) : 2;
+        return v <= 1 ? 1 : 2;
+    }();
+    return stages;
+}
+
 // Column blocks from which the shared-tile instance serves (default 3: more than 32 query rows per KV head);
 // ECO_KIVI_SHARED overrides.
 int kivi_shared_from() {
@@ -901,7 +923,8 @@ template <int D, int BITS, int NB>
 KiviInstance kivi_kernel_of() {
     if constexpr (NB == 1)
         return kivi_stages() == 1 ? kivi_instance<D, BITS, 1, 1, false>() : kivi_instance<D, BITS, 1, 2, false>();
-    if (NB >= kivi_shared_from()) return kivi_instance<D, BITS, 1, 1, true>();
+    if (NB >= kivi_shared_from())
+        return kivi_shared_stages() == 2 ? kivi_instance<D, BITS, 1, 2, true>() : kivi_instance<D, BITS, 1, 1, true>();
     return kivi_instance<D, BITS, NB, 1, false>();
 }
 
