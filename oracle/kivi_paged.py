@@ -169,11 +169,12 @@ def write_values(blocks: np.ndarray, values: np.ndarray, b: int, start: int, sto
 
 
 def dense_view(blocks: np.ndarray, table: np.ndarray, k_ring: np.ndarray, v_ring: np.ndarray, lens, kq, vq,
-               bits: int, group: int) -> tuple[np.ndarray, np.ndarray]:
+               bits: int, group: int, round_values: bool = True) -> tuple[np.ndarray, np.ndarray]:
     """The keys and values ``[B, Hkv, max(lens), D]`` (float32 holding bf16 values) attention sees: keys below
     ``kq[b]`` and values below ``vq[b]`` dequantized as the reference's ``dequantize`` does (``code * scale + zero``
     in fp32, two roundings, then bf16; attention/kivi.py:56-76), the others from the rings (token ``t`` at slot
-    ``t % W``)."""
+    ``t % W``). ``round_values=False`` leaves the dequantized values in fp32 (not the reference: the form of a value
+    product that never rounds a dequantized value, to measure how far such a product is from the reference)."""
     batch, heads, w, dim = k_ring.shape
     lay = block_layout(dim, bits, group)
     smax = int(max(lens))
@@ -198,7 +199,8 @@ def dense_view(blocks: np.ndarray, table: np.ndarray, k_ring: np.ndarray, v_ring
                     z = blk[lay["v_zero"]:lay["size"]].view(np.float16).reshape(-1, PAGE)[:, pos]
                     s = np.repeat(s.astype(np.float32), group)
                     z = np.repeat(z.astype(np.float32), group)
-                    values[b, h, t] = round_bf16(((codes * s).astype(np.float32) + z).astype(np.float32))
+                    v = ((codes * s).astype(np.float32) + z).astype(np.float32)
+                    values[b, h, t] = round_bf16(v) if round_values else v
                 else:
                     values[b, h, t] = v_ring[b, h, :, t % w]
     return keys, values
