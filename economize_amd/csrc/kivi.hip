@@ -14,21 +14,20 @@
 // key scales and zero points [D]; value scales and zero points [D / 32][32]. A word holds 32 / bits elements,
 // element e in byte e % 4 at bit (e / 4) * bits.
 //
-// Attention. The reference dequantizes code * scale + zero in fp32 and attends over the values rounded to the model
-// dtype (attention/kivi.py:56-76, attention/_kivi_kernels.py:14-15). Keys are dequantized that way (the softmax is
-// sensitive to the rounding of the keys, most of all in outlier channels) and multiplied by q with bf16 MFMAs. For
-// the values the dequantization is folded into the matrix-core operands by linearity:
-//   sum_t p_t v_td = sum_t (p_t s_tg) c_td + sum_t p_t z_tg     (value scale and zero of token t, group g of d)
-// so the MFMA A operand is the codes themselves: a code c < 16 zero-extended to a byte is the e4m3 pattern of
-// c * 2^-9, and v_cvt_scalef32_pk_f16_fp8 with scale 2^9 turns it into the exact fp16 value c (the same conversion
-// to fp32 feeds the key dequantization). The B operand p * s is rounded to fp16 (11 significant bits; the reference
-// rounds p to bf16, 8 bits), and the zero term is an MFMA too: z (one row per value group) times p. Tokens not yet
-// quantized are read from the bf16 ring (bf16 MFMAs, p split into two bf16 terms).
+// Attention. The reference dequantizes code * scale + zero in fp32 and attends over the keys and values rounded to
+// the model dtype (attention/kivi.py:56-76, attention/_kivi_kernels.py:14-15 and the .to(DOT_DTYPE) casts of
+// _kivi_block). Both are dequantized that way here: a code c < 16 zero-extended to a byte is the e4m3 pattern of
+// c * 2^-9, so v_cvt_scalef32_pk_f32_fp8 with scale 2^9 gives the exact fp32 value c; c * s is exact in fp32 (at
+// most 4 bits times an fp16), so one fused multiply-add rounds as the reference's product then sum; the result is
+// rounded to bf16 and fed to bf16 MFMAs. The value product's B operand p is split into two bf16 terms (hi + lo,
+// about 16 significant bits), so the output carries the reference's value rounding and nothing coarser; every
+// product is in fp32 (no fp16 operand, whatever the scale). Tokens not yet quantized are read from the bf16 ring.
 //
 // Work decomposition, pipeline and merge: the stream-K scheme of paged_attention.hip (stream_k.hpp), with tiles of
 // one 32-token page. The query of the current row lives in LDS, so that row changes do not put loads of varying
 // count in the tile pipeline. With more than 32 query rows per KV head (speculative verification) the four waves of
-// a workgroup share each tile instead: one column block of query rows each, the keys dequantized once into LDS.
+// a workgroup share each tile instead: one column block of query rows each, the keys and values dequantized once
+// into LDS, a quarter of them by each wave.
 
 #include <cstdlib>
 #include <type_traits>
@@ -222,27 +221,8 @@ __global__ __launch_bounds__(256) void kivi_quant_values_kernel(KiviQuantParams 
 
 // ---- attention ----------------------------------------------------------------------------------------------
 
-// Eight codes of a word, as exact fp16 values, in element order: for 4-bit codes the word's 8 elements, for 2-bit
+// Eight codes of a word as exact fp32 values, in element order: for 4-bit codes the word's 8 elements, for 2-bit
 // codes elements 8 h .. 8 h + 7 of its 16.
-template <int BITS>
-__device__ inline f16x8 codes_to_f16(uint32_t word, int h) {
-    uint32_t lo, hi;
-    if constexpr (BITS == 4) {
-        lo = word & 0x0F0F0F0Fu;
-        hi = (word >> 4) & 0x0F0F0F0Fu;
-    } else {
-        lo = (word >> (4 * h)) & 0x03030303u;
-        hi = (word >> (4 * h + 2)) & 0x03030303u;
-    }
-    uint4 r;
-    r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, false));
-    r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 512.0f, true));
-    r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, false));
-    r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 512.0f, true));
-    return __builtin_bit_cast(f16x8, r);
-}
-
-// The same eight codes as fp32 values.
 template <int BITS>
 __device__ inline void codes_to_f32(uint32_t word, int h, float (&out)[8]) {
     uint32_t lo, hi;
@@ -268,28 +248,12 @@ __device__ inline void codes_to_f32(uint32_t word, int h, float (&out)[8]) {
     out[7] = d.y;
 }
 
-__device__ inline uint32_t pack_f16x2(float a, float b) {
-    f16x2 v = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
-    return __builtin_bit_cast(uint32_t, v);
-}
-
-__device__ inline uint32_t pack_bf16x2(float a, float b) {
-    return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
-}
-
-// Zeroes the fp16 / bf16 halves of x whose bit in keep (8 bits, element e = bit e) is clear.
-__device__ inline uint4 keep_halves(uint4 x, uint32_t keep) {
-    auto m = [&](int e) { return ((keep >> e) & 1u ? 0x0000FFFFu : 0u) | ((keep >> (e + 1)) & 1u ? 0xFFFF0000u : 0u); };
-    x.x &= m(0);
-    x.y &= m(2);
-    x.z &= m(4);
-    x.w &= m(6);
-    return x;
-}
-
-// A lane's share of one 32-token page. SHARED: the four waves of a workgroup dequantize the key tile together, lane
-// (n, g) of wave w taking the KE operand entries (k-step j, token half v) with j * 2 + v = w * KE + e; then it holds
-// one key word per entry and the scale and zero point of its 8 channels.
+// A lane's share of one 32-token page: key words of its 8-token key rows, the value word of each 16-channel block
+// (lane (n, g): channel 16 nd + n, tokens 8 g .. 8 g + 7, the P.V MFMA's A operand), key scales and zero points of
+// its channels, value scales and zero points of its 8 tokens per value group. SHARED: the four waves of a workgroup
+// dequantize the tile together, lane (n, g) of wave w taking the KE key operand entries (k-step j, token half v)
+// with j * 2 + v = w * KE + e (one key word per entry and the scale and zero point of its 8 channels) and the VE
+// value blocks w * VE .. (one value group).
 template <int D, int BITS, bool SHARED = false>
 struct KTile {
     static constexpr int KW = D * BITS / 128;  // words of a lane's key slice (D / 4 channels)
@@ -297,11 +261,11 @@ struct KTile {
     static constexpr int KS = D / 32;          // k-steps of an S MFMA (8 channels each per lane)
     static constexpr int VG = D / 32;          // value groups
     static constexpr int KE = KS / 2;          // key entries per lane (SHARED)
+    static constexpr int VE = ND / 4;          // value blocks per wave (SHARED)
     uint32_t kc[2][SHARED ? KE : KW];          // SHARED: kc[0][e]
-    uint32_t vc[ND];
+    uint32_t vc[SHARED ? VE : ND];
     uint4 ks[SHARED ? 1 : KS], kz[SHARED ? 1 : KS];
-    uint4 vs[VG];
-    uint4 vz;
+    uint4 vs[SHARED ? 1 : VG], vz[SHARED ? 1 : VG];
     int page;  // physical page (the same in every lane), -1 for none
 };
 
@@ -327,8 +291,8 @@ __device__ inline void load_words(const uint32_t* src, uint32_t (&dst)[N]) {
 }
 
 // Issues the page loads of the tile under cursor c (the same loads in every lane and for every tile: a tile without
-// a page reads page 0 and masks it). PARTS: 1 the keys, 2 the values, 3 both.
-template <int D, int BITS, bool SHARED, int PARTS = 3>
+// a page reads page 0 and masks it).
+template <int D, int BITS, bool SHARED>
 __device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c, int n, int g, int lane, int wave,
                                            PageWindow& win, KTile<D, BITS, SHARED>& tile) {
     using T = KTile<D, BITS, SHARED>;
@@ -337,8 +301,7 @@ __device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c,
     const int phys = __builtin_amdgcn_readlane(win.physical, c.t - win.base);
     tile.page = phys;
     const uint8_t* blk = p.blocks + static_cast<int64_t>(phys >= 0 ? phys : 0) * p.blk_page + c.kvh * p.blk_head;
-    if constexpr (!(PARTS & 1)) {
-    } else if constexpr (SHARED) {
+    if constexpr (SHARED) {
         const int j = (wave * T::KE) >> 1;  // the k-step of every entry of the lane
 #pragma unroll
         for (int e = 0; e < T::KE; ++e) {
@@ -359,19 +322,69 @@ __device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c,
     }
     constexpr int TPW = 32 / BITS;  // tokens per value word
     const int u = 8 * g / TPW;
-    if constexpr (PARTS & 2) load_words(reinterpret_cast<const uint32_t*>(blk + L.v_codes()) + (u * 16 + n) * T::ND, tile.vc);
-    if constexpr (!SHARED && (PARTS & 1)) {
+    const uint32_t* vwords = reinterpret_cast<const uint32_t*>(blk + L.v_codes()) + (u * 16 + n) * T::ND;
+    if constexpr (SHARED) {
+        const int nd0 = wave * T::VE;  // the wave's value blocks, all in value group nd0 / 2
+        load_words(vwords + nd0, tile.vc);
+        tile.vs[0] = *reinterpret_cast<const uint4*>(blk + L.v_scale() + ((nd0 / 2) * 32 + 8 * g) * 2);
+        tile.vz[0] = *reinterpret_cast<const uint4*>(blk + L.v_zero() + ((nd0 / 2) * 32 + 8 * g) * 2);
+    } else {
+        load_words(vwords, tile.vc);
+    }
+    if constexpr (!SHARED) {
 #pragma unroll
         for (int j = 0; j < T::KS; ++j) {
             tile.ks[j] = *reinterpret_cast<const uint4*>(blk + L.k_scale() + (g * (D / 4) + 8 * j) * 2);
             tile.kz[j] = *reinterpret_cast<const uint4*>(blk + L.k_zero() + (g * (D / 4) + 8 * j) * 2);
         }
     }
-    if constexpr (PARTS & 2) {
+    if constexpr (!SHARED) {
 #pragma unroll
-        for (int grp = 0; grp < T::VG; ++grp)
+        for (int grp = 0; grp < T::VG; ++grp) {
             tile.vs[grp] = *reinterpret_cast<const uint4*>(blk + L.v_scale() + (grp * 32 + 8 * g) * 2);
-        tile.vz = *reinterpret_cast<const uint4*>(blk + L.v_zero() + ((n % T::VG) * 32 + 8 * g) * 2);
+            tile.vz[grp] = *reinterpret_cast<const uint4*>(blk + L.v_zero() + (grp * 32 + 8 * g) * 2);
+        }
+    }
+}
+
+// The eight values (tokens 8 g .. 8 g + 7 of one channel) of a value word, dequantized as the reference does:
+// bf16(code * scale + zero) with the product and sum in fp32 (one fused multiply-add: the product is exact).
+template <int BITS>
+__device__ __forceinline__ uint4 dequant_values(uint32_t word, int g, uint4 scales, uint4 zeros) {
+    const f16x8 sh = __builtin_bit_cast(f16x8, scales);
+    const f16x8 zh = __builtin_bit_cast(f16x8, zeros);
+    float c8[8];
+    codes_to_f32<BITS>(word, BITS == 4 ? 0 : (g & 1), c8);
+    bf16x8 v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        v[i] = static_cast<__bf16>(__builtin_fmaf(c8[i], static_cast<float>(sh[i]), static_cast<float>(zh[i])));
+    return __builtin_bit_cast(uint4, v);
+}
+
+// Masks of the bf16 halves of a uint4 whose bit in keep (8 bits, element e = bit e) is set.
+struct HalfMask {
+    uint32_t m[4];
+};
+
+__device__ inline HalfMask half_mask(uint32_t keep) {
+    HalfMask h;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        h.m[j] = ((keep >> (2 * j)) & 1u ? 0x0000FFFFu : 0u) | ((keep >> (2 * j + 1)) & 1u ? 0xFFFF0000u : 0u);
+    return h;
+}
+
+__device__ inline uint4 apply_mask(uint4 x, const HalfMask& h) {
+    return make_uint4(x.x & h.m[0], x.y & h.m[1], x.z & h.m[2], x.w & h.m[3]);
+}
+
+// p (8 fp32 weights) as bf16 hi + lo: hi = bf16(p), lo = bf16(p - hi) (p - hi is exact in fp32).
+__device__ __forceinline__ void split_bf16(const float (&p)[8], bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        hi[e] = static_cast<__bf16>(p[e]);
+        lo[e] = static_cast<__bf16>(p[e] - static_cast<float>(hi[e]));
     }
 }
 
@@ -412,8 +425,10 @@ kivi_attention_kernel(KiviParams p) {
     const int wave = WAVES > 1 ? uniform(static_cast<int>(threadIdx.x) >> 6) : 0;
     const int row0 = SHARED ? 16 * wave : 0;  // the wave's first query row
     __shared__ __align__(16) typename std::conditional<kSplit, Pieces<D, WAVES>, char>::type pieces;
-    // SHARED: the dequantized key tile, two buffers, in MFMA operand order (entry j * 2 + v, lane)
+    // SHARED: the dequantized key and value tiles, two buffers, in MFMA operand order (key entry j * 2 + v, lane;
+    // value block nd, lane)
     __shared__ typename std::conditional<SHARED, uint4[2][2 * KS][64], char>::type kbuf;
+    __shared__ typename std::conditional<SHARED, uint4[2][ND][64], char>::type vbuf;
     QRows* q_rows;
     if constexpr (kSplit) {
         // the query rows live in the data of the wave's second piece, which only the wave's last step writes, after
@@ -454,7 +469,7 @@ kivi_attention_kernel(KiviParams p) {
     float limit[NB];
     int all_see = 0, kq = 0, vq = 0, row_len = 0;
     float m_i[NB], l_i[NB];  // l_i: the sum over the lane's own tokens until the segment's end reduces it
-    f32x4 acc[ND][NB], gam[NB];
+    f32x4 acc[ND][NB];
 
     auto begin_row = [&](const Cursor& c) __attribute__((always_inline)) {
         // the row's query rows into LDS (rows past the group are zero); the loads wait here, once per row, outside the
@@ -486,22 +501,41 @@ kivi_attention_kernel(KiviParams p) {
     };
     const float score_scale = p.softcap > 0.0f ? p.scale : p.scale * kLog2e;
 
-    // ---- SHARED: the lane's entries of the key tile, dequantized into LDS buffer buf ----
-    auto share_keys = [&](const T& tile, int buf) __attribute__((always_inline)) {
+    // the value tokens 8 g .. 8 g + 7 of the lane that come from codes (below vq, on a present page)
+    auto code_values = [&](const T& tile, int t0) __attribute__((always_inline)) -> uint32_t {
+        const int tok0 = t0 + 8 * g;
+        if (tile.page < 0) return 0u;
+        return vq - tok0 >= 8 ? 0xFFu : (vq > tok0 ? (1u << (vq - tok0)) - 1u : 0u);
+    };
+
+    // ---- SHARED: the lane's entries of the key and value tiles, dequantized into LDS buffer buf ----
+    auto share_tile = [&](const T& tile, const Cursor& c, int buf) __attribute__((always_inline)) {
         if constexpr (SHARED) {
-            const f16x8 sh = __builtin_bit_cast(f16x8, tile.ks[0]);
-            const f16x8 zh = __builtin_bit_cast(f16x8, tile.kz[0]);
-            const int j = (wave * T::KE) >> 1;
+            const int t0 = KPAGE * c.t;
+            if (t0 < kq) {
+                const f16x8 sh = __builtin_bit_cast(f16x8, tile.ks[0]);
+                const f16x8 zh = __builtin_bit_cast(f16x8, tile.kz[0]);
+                const int j = (wave * T::KE) >> 1;
 #pragma unroll
-            for (int e = 0; e < T::KE; ++e) {
-                float c8[8];
-                codes_to_f32<BITS>(tile.kc[0][e], j % 2, c8);
-                bf16x8 kv;
+                for (int e = 0; e < T::KE; ++e) {
+                    float c8[8];
+                    codes_to_f32<BITS>(tile.kc[0][e], j % 2, c8);
+                    bf16x8 kv;
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    kv[i] = static_cast<__bf16>(
-                        __builtin_fmaf(c8[i], static_cast<float>(sh[i]), static_cast<float>(zh[i])));
-                kbuf[buf][wave * T::KE + e][lane] = __builtin_bit_cast(uint4, kv);
+                    for (int i = 0; i < 8; ++i)
+                        kv[i] = static_cast<__bf16>(
+                            __builtin_fmaf(c8[i], static_cast<float>(sh[i]), static_cast<float>(zh[i])));
+                    kbuf[buf][wave * T::KE + e][lane] = __builtin_bit_cast(uint4, kv);
+                }
+            }
+            if (t0 < vq) {
+                // tokens at or past vq, and every token of a missing page, are zero (an unwritten scale may be inf
+                // or NaN); they come from the ring or carry no weight
+                const HalfMask mask = half_mask(code_values(tile, t0));
+#pragma unroll
+                for (int e = 0; e < T::VE; ++e)
+                    vbuf[buf][wave * T::VE + e][lane] =
+                        apply_mask(dequant_values<BITS>(tile.vc[e], g, tile.vs[0], tile.vz[0]), mask);
             }
         }
     };
@@ -620,8 +654,6 @@ kivi_attention_kernel(KiviParams p) {
                 const float alpha = fresh ? 0.0f : __builtin_amdgcn_exp2f(m_i[nb] - m_new);
                 l_i[nb] *= alpha;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) gam[nb][i] = fresh ? 0.0f : gam[nb][i] * alpha;
-#pragma unroll
                 for (int nd = 0; nd < ND; ++nd)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) acc[nd][nb][i] = fresh ? 0.0f : acc[nd][nb][i] * alpha;
@@ -638,56 +670,46 @@ kivi_attention_kernel(KiviParams p) {
                 }
             l_i[nb] += sum;  // the lane's own tokens; summed over the lane group at the end of the segment
         }
-        // values: element e of the lane's operands is token t0 + 8 g + e
+        // values: element e of the lane's operands is token t0 + 8 g + e; p as bf16 hi + lo for both sources (p is
+        // zero at every token that no query row sees)
         const int tok0 = t0 + 8 * g;
-        if (t0 < vq) {  // from codes: O += codes . (p * s) + z . p
-            // tokens at or past vq and every token of a missing page are masked out of p, p * s and z (an unwritten
-            // scale may be inf or NaN); a tile of codes only skips the masks
-            auto from_codes = [&](auto full_tag, uint32_t keep) __attribute__((always_inline)) {
-                constexpr bool kFull = decltype(full_tag)::value;
-                auto masked = [&](uint4 x) __attribute__((always_inline)) { return kFull ? x : keep_halves(x, keep); };
-                f16x8 pp[NB];
+        bf16x8 phi[NB], plo[NB];
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb) {
-                    uint4 w4;
-                    w4.x = pack_f16x2(pw[nb][0], pw[nb][1]);
-                    w4.y = pack_f16x2(pw[nb][2], pw[nb][3]);
-                    w4.z = pack_f16x2(pw[nb][4], pw[nb][5]);
-                    w4.w = pack_f16x2(pw[nb][6], pw[nb][7]);
-                    pp[nb] = __builtin_bit_cast(f16x8, masked(w4));
-                }
+        for (int nb = 0; nb < NB; ++nb) split_bf16(pw[nb], phi[nb], plo[nb]);
+        auto product = [&](int nd, uint4 a4) __attribute__((always_inline)) {
+            const bf16x8 a = __builtin_bit_cast(bf16x8, a4);
 #pragma unroll
-                for (int grp = 0; grp < VG; ++grp) {
-                    f16x8 ps[NB];
+            for (int nb = 0; nb < NB; ++nb) {
+                acc[nd][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, phi[nb], acc[nd][nb], 0, 0, 0);
+                acc[nd][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, plo[nb], acc[nd][nb], 0, 0, 0);
+            }
+        };
+        if (t0 < vq) {  // from codes: O += bf16(c * s + z) . p
+            if constexpr (SHARED) {
 #pragma unroll
-                    for (int nb = 0; nb < NB; ++nb)
-                        ps[nb] = __builtin_bit_cast(
-                            f16x8, masked(__builtin_bit_cast(uint4, pp[nb] * __builtin_bit_cast(f16x8, tile.vs[grp]))));
-#pragma unroll
-                    for (int nd = 2 * grp; nd < 2 * grp + 2; ++nd) {
-                        const f16x8 a = BITS == 4 ? codes_to_f16<BITS>(tile.vc[nd], 0)
-                                                  : codes_to_f16<BITS>(tile.vc[nd], g & 1);
-#pragma unroll
-                        for (int nb = 0; nb < NB; ++nb)
-                            acc[nd][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ps[nb], acc[nd][nb], 0, 0, 0);
-                    }
-                }
-                const f16x8 z = __builtin_bit_cast(f16x8, masked(tile.vz));
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
-                    gam[nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(z, pp[nb], gam[nb], 0, 0, 0);
-            };
-            if (NB <= 2 && t0 + KPAGE <= vq && valid) {  // (at four column blocks the second copy would spill)
-                from_codes(std::integral_constant<bool, NB <= 2>{}, 0xFFu);
+                for (int nd = 0; nd < ND; ++nd) product(nd, vbuf[buf][nd][lane]);
             } else {
-                const uint32_t keep =
-                    valid ? (vq - tok0 >= 8 ? 0xFFu : (vq > tok0 ? (1u << (vq - tok0)) - 1u : 0u)) : 0u;
-                from_codes(std::false_type{}, keep);
+                // tokens at or past vq and every token of a missing page are zero (an unwritten scale may be inf or
+                // NaN); a tile of codes only skips the masks
+                auto from_codes = [&](auto full_tag, const HalfMask& mask) __attribute__((always_inline)) {
+                    constexpr bool kFull = decltype(full_tag)::value;
+#pragma unroll
+                    for (int nd = 0; nd < ND; ++nd) {
+                        const uint4 v = dequant_values<BITS>(tile.vc[nd], g, tile.vs[nd / 2], tile.vz[nd / 2]);
+                        product(nd, kFull ? v : apply_mask(v, mask));
+                    }
+                };
+                if (NB <= 2 && t0 + KPAGE <= vq && valid) {  // (at four column blocks the second copy would spill)
+                    from_codes(std::integral_constant<bool, NB <= 2>{}, HalfMask{});
+                } else {
+                    from_codes(std::false_type{}, half_mask(code_values(tile, t0)));
+                }
             }
         }
         if (t0 + KPAGE > vq) {  // from the ring (tokens at or past vq, below the row's end)
             const int from = max(vq - tok0, 0), to = min(row_len - tok0, 8);
             const uint32_t keep = to > from ? ((to >= 8 ? 0xFFu : (1u << to) - 1u) & ~((1u << from) - 1u)) : 0u;
+            const HalfMask mask = half_mask(keep);
             uint4 vr[ND];
             const int slot = tok0 % p.ring;
 #pragma unroll
@@ -695,32 +717,8 @@ kivi_attention_kernel(KiviParams p) {
                 vr[nd] = *reinterpret_cast<const uint4*>(
                     p.v_ring + ((static_cast<int64_t>(c.b) * p.kv_heads + c.kvh) * D + 16 * nd + n) * p.ring + slot);
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the ring loads of this rare branch
-            bf16x8 phi[NB], plo[NB];
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                float pv[8], lo8[8];
-                uint32_t hw[4], lw[4];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) pv[e] = (keep >> e) & 1u ? pw[nb][e] : 0.0f;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) hw[e] = pack_bf16x2(pv[2 * e], pv[2 * e + 1]);
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    lo8[e] = pv[e] - bits_f32(e & 1 ? hw[e >> 1] & 0xFFFF0000u : hw[e >> 1] << 16);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) lw[e] = pack_bf16x2(lo8[2 * e], lo8[2 * e + 1]);
-                phi[nb] = __builtin_bit_cast(bf16x8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
-                plo[nb] = __builtin_bit_cast(bf16x8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
-            }
-#pragma unroll
-            for (int nd = 0; nd < ND; ++nd) {
-                const bf16x8 a = __builtin_bit_cast(bf16x8, keep_halves(vr[nd], keep));
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb) {
-                    acc[nd][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, phi[nb], acc[nd][nb], 0, 0, 0);
-                    acc[nd][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, plo[nb], acc[nd][nb], 0, 0, 0);
-                }
-            }
+            for (int nd = 0; nd < ND; ++nd) product(nd, apply_mask(vr[nd], mask));
         }
     };
 
@@ -728,17 +726,7 @@ kivi_attention_kernel(KiviParams p) {
     auto finish = [&](const Cursor& c, int64_t seg_begin, int64_t seg_end, bool first_segment) __attribute__((always_inline)) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) l_i[nb] = group_sum(l_i[nb]);
-        // the value zero-point term of channel 16 nd + 4 g + i: row (group (16 nd) / 32) of the gamma tile, held by
-        // lane group 0, column n
-        float o[ND][NB][4];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-            for (int nd = 0; nd < ND; ++nd) {
-                const float z = __shfl(gam[nb][(nd / 2) & 3], n);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) o[nd][nb][i] = acc[nd][nb][i] + z;
-            }
+        const auto& o = acc;
         const int64_t row_end = c.row_start + c.row.tiles;
         if (seg_begin == c.row_start && seg_end == row_end) {
 #pragma unroll
@@ -776,16 +764,13 @@ kivi_attention_kernel(KiviParams p) {
                 for (int i = 0; i < 4; ++i)
                     coherent_store(slot + 2 * p.rows + r * D + 16 * nd + 4 * g + i, o[nd][nb][i]);
         }
-        __builtin_amdgcn_s_waitcnt(0);
-        if constexpr (SHARED) {  // every wave's rows are in the workgroup's slot before the count
+        if constexpr (SHARED) {  // every wave's rows are complete before wave 0 counts the slot
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
             if (wave != 0) return;
         }
-        int prev = 0;
-        if (lane == 0)
-            prev = __hip_atomic_fetch_add(p.counters + c.b * p.kv_heads + c.kvh, 1, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-        merge_row<D>(p, c, __shfl(prev, 0), total, grid, lane);
+        hand_off<D>(p, c, total, grid, lane);
     };
 
     // ---- the tile pipeline (as in paged_attention.hip) ----
@@ -795,23 +780,18 @@ kivi_attention_kernel(KiviParams p) {
         int64_t seg_begin = lo;
         bool first_segment = true;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            gam[nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
             for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        }
         begin_row(cur);
 
-        // SHARED with two buffers: the buffers hold keys, issued a tile ahead; a tile's values are issued at its own
-        // step, before the next tile's keys, and arrive while its keys are shared and its scores computed
-        constexpr bool kKeysAhead = SHARED && NBUF == 2;
+        // with two buffers a tile's loads are issued a tile ahead (SHARED: the wave's shares of its keys and values)
         T bufs[NBUF];
-        T vt;
         Cursor cs[NBUF];
         Cursor icur = cur;
         int64_t ipos = lo;
         auto issue_next = [&](T& buf, Cursor& slot) __attribute__((always_inline)) {
-            issue_tile<D, BITS, SHARED, kKeysAhead ? 1 : 3>(p, icur, n, g, lane, wave, win, buf);
+            issue_tile<D, BITS, SHARED>(p, icur, n, g, lane, wave, win, buf);
             slot = icur;
             if (ipos < hi) {
                 if (ipos + 1 < hi) advance(p, icur, small ? &rt : nullptr);
@@ -825,20 +805,16 @@ kivi_attention_kernel(KiviParams p) {
         auto step = [&](auto tag) __attribute__((always_inline)) -> bool {
             constexpr int I = decltype(tag)::value;
             constexpr int J = (I + NBUF - 1) % NBUF;
-            if constexpr (kKeysAhead) issue_tile<D, BITS, SHARED, 2>(p, cs[I], n, g, lane, wave, win, vt);
             issue_next(bufs[J], cs[J]);
             cur = cs[I];
             if (cur.t == 0 && pos != lo) begin_row(cur);
             if constexpr (SHARED) {
-                // this tile's keys into LDS buffer pos & 1; the barrier also ends every wave's reads of that buffer
-                // two tiles back (they precede the previous tile's barrier)
-                if (KPAGE * cur.t < kq) share_keys(bufs[I], static_cast<int>(pos & 1));
+                // this tile's keys and values into LDS buffer pos & 1; the barrier also ends every wave's reads of
+                // that buffer two tiles back (they precede the previous tile's barrier)
+                share_tile(bufs[I], cur, static_cast<int>(pos & 1));
                 __syncthreads();
             }
-            if constexpr (kKeysAhead)
-                compute(vt, cur, static_cast<int>(pos & 1));
-            else
-                compute(bufs[I], cur, static_cast<int>(pos & 1));
+            compute(bufs[I], cur, static_cast<int>(pos & 1));
             const bool more = pos + 1 < hi;
             if (cur.t + 1 == cur.row.tiles || !more) {
                 finish(cur, seg_begin, pos + 1, first_segment);

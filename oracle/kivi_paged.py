@@ -23,16 +23,17 @@ The full-precision residual of every row is a ring of ``W`` slots, token ``t`` a
 ``key_ring`` / ``value_ring`` (attention/kivi.py:100-108).
 
 Pinned by (``tests/test_oracle_kivi_paged.py``): :func:`pack_words` / :func:`unpack_words` identity and the bit
-position of single codes against the definition above written per element; block offsets against sizes; the codes,
-scales and zero points inside a block against :func:`oracle.kivi.quantize_keys` / ``quantize_values`` (which the
-reference's closed-form tests pin).
+position of single codes, element by element; :func:`value_words` / :func:`value_codes` identity and the word and bit
+of single codes against the word formula above; block offsets against sizes; :func:`dense_view` of pages written by
+:func:`write_keys` / :func:`write_values` against :func:`oracle.kivi.dequantize` of the contiguous codes of
+:func:`oracle.kivi.quantize_keys` / ``quantize_values`` (the reference's ``KIVIPacked`` format, which the
+reference's closed-form tests pin), rounded to bf16, and values written in several ranges against one write.
 """
 
 from __future__ import annotations
 
 import numpy as np
 
-from .kivi import quantize_keys, quantize_values
 from .numerics import round_bf16
 
 __all__ = ["PAGE", "block_layout", "dense_view", "pack_words", "unpack_words", "value_codes", "value_words",
@@ -87,120 +88,129 @@ def _half_bytes(x: np.ndarray) -> np.ndarray:
         return np.ascontiguousarray(np.asarray(x, dtype=np.float32).astype(np.float16)).view(np.uint8)
 
 
-def write_keys(blocks: np.ndarray, keys: np.ndarray, b: int, start: int, stop: int, table: np.ndarray, bits: int,
-               group: int) -> None:
-    """Quantize keys ``start:stop`` (whole pages) of row ``b`` of ``keys`` ``[B, Hkv, S, D]`` (float32 holding the
-    bf16 values) into ``blocks`` ``[pages, Hkv, size]`` (``uint8``) through the block table."""
-    _, heads, _, dim = keys.shape
-    lay = block_layout(dim, bits, group)
-    for p0 in range(start, stop, PAGE):
-        page = table[b, p0 // PAGE]
-        _, scale, zero, _ = quantize_keys(keys[b:b + 1], p0, p0 + PAGE, bits, group)  # [1, H, 32/G, D]
-        codes = _key_codes(keys[b:b + 1], p0, bits, group)  # [H, 32, D]
-        for h in range(heads):
-            blk = blocks[page, h]
-            blk[lay["k_codes"]:lay["v_codes"]] = pack_words(codes[h], bits).reshape(-1)
-            blk[lay["k_scale"]:lay["k_zero"]] = _half_bytes(scale[0, h]).reshape(-1)
-            blk[lay["k_zero"]:lay["v_scale"]] = _half_bytes(zero[0, h]).reshape(-1)
-
-
-def _key_codes(keys: np.ndarray, p0: int, bits: int, group: int) -> np.ndarray:
-    from .kivi import quantize
-
-    block = np.asarray(keys[0, :, p0:p0 + PAGE], dtype=np.float32)  # [H, 32, D]
-    h, t, d = block.shape
-    codes, _, _ = quantize(block.reshape(h, t // group, group, d), bits, axis=2)
-    return codes.reshape(h, t, d).astype(np.int64)
-
-
 def value_words(codes: np.ndarray, bits: int) -> np.ndarray:
-    """Value codes ``[D, 32]`` (channel, token) of one page laid out as the block's value-code bytes."""
-    dim = codes.shape[0]
+    """Value codes ``[..., D, 32]`` (channel, token) of pages laid out as the blocks' value-code bytes
+    ``[..., D * 32 * bits / 8]``: word ``(u * 16 + n) * (D / 16) + nd`` holds channel ``16 nd + n``, tokens
+    ``u * 32 / bits ..`` (``32 / bits`` of them)."""
+    c = np.asarray(codes).astype(np.int64)
+    *lead, dim, tokens = c.shape
     tpw = 32 // bits
     nd = dim // 16
-    words = np.zeros((bits, 16, nd, tpw), np.int64)  # [u, n, nd, token in word]
-    for u in range(bits):
-        for n in range(16):
-            for j in range(nd):
-                words[u, n, j] = codes[16 * j + n, u * tpw:(u + 1) * tpw]
-    return pack_words(words.reshape(bits * 16 * nd, tpw), bits).reshape(-1)
+    # [..., nd, n, u, e] -> [..., u, n, nd, e]
+    w = c.reshape(*lead, nd, 16, bits, tpw)
+    k = len(lead)
+    w = np.moveaxis(w, [k, k + 1, k + 2], [k + 2, k + 1, k])
+    return pack_words(w.reshape(*lead, bits * 16 * nd * tpw), bits)
 
 
 def value_codes(raw: np.ndarray, dim: int, bits: int) -> np.ndarray:
-    """Inverse of :func:`value_words`: codes ``[D, 32]`` of a block's value-code bytes."""
+    """Inverse of :func:`value_words`: codes ``[..., D, 32]`` of value-code bytes ``[..., D * 32 * bits / 8]``."""
+    r = np.asarray(raw)
+    lead = r.shape[:-1]
     tpw = 32 // bits
     nd = dim // 16
-    words = unpack_words(raw.reshape(bits * 16 * nd, 4), bits).reshape(bits, 16, nd, tpw)
-    codes = np.zeros((dim, PAGE), np.int64)
-    for u in range(bits):
-        for n in range(16):
-            for j in range(nd):
-                codes[16 * j + n, u * tpw:(u + 1) * tpw] = words[u, n, j]
-    return codes
+    k = len(lead)
+    w = unpack_words(r, bits).reshape(*lead, bits, 16, nd, tpw)
+    w = np.moveaxis(w, [k, k + 1, k + 2], [k + 2, k + 1, k])  # [..., nd, n, u, e]
+    return w.reshape(*lead, dim, PAGE).astype(np.int64)
+
+
+def _rows_pages(table: np.ndarray, b: int, first: int, count: int) -> np.ndarray:
+    return np.asarray(table[b, first:first + count]).astype(np.int64)
+
+
+def write_keys(blocks: np.ndarray, keys: np.ndarray, b: int, start: int, stop: int, table: np.ndarray, bits: int,
+               group: int) -> None:
+    """Quantize keys ``start:stop`` (whole pages) of row ``b`` of ``keys`` ``[B, Hkv, S, D]`` (float32 holding the
+    bf16 values) into ``blocks`` ``[pages, Hkv, size]`` (``uint8``) through the block table: per channel over groups
+    of ``group`` tokens (:func:`oracle.kivi.quantize`)."""
+    from .kivi import quantize
+
+    if stop <= start:
+        return
+    _, heads, _, dim = keys.shape
+    lay = block_layout(dim, bits, group)
+    block = np.asarray(keys[b, :, start:stop], dtype=np.float32)  # [H, T, D]
+    t = block.shape[1]
+    npg = t // PAGE
+    codes, scale, low = quantize(block.reshape(heads, t // group, group, dim), bits, axis=2)
+    codes = codes.reshape(heads, npg, PAGE, dim).astype(np.int64)
+    scale = scale.reshape(heads, npg, PAGE // group, dim)
+    low = low.reshape(heads, npg, PAGE // group, dim)
+    pages = _rows_pages(table, b, start // PAGE, npg)
+    kc = pack_words(codes, bits).reshape(heads, npg, -1)
+    blocks[pages, :, lay["k_codes"]:lay["v_codes"]] = kc.transpose(1, 0, 2)
+    blocks[pages, :, lay["k_scale"]:lay["k_zero"]] = _half_bytes(scale).reshape(heads, npg, -1).transpose(1, 0, 2)
+    blocks[pages, :, lay["k_zero"]:lay["v_scale"]] = _half_bytes(low).reshape(heads, npg, -1).transpose(1, 0, 2)
 
 
 def write_values(blocks: np.ndarray, values: np.ndarray, b: int, start: int, stop: int, table: np.ndarray,
                  bits: int, group: int) -> None:
     """Quantize values ``start:stop`` (any tokens) of row ``b`` of ``values`` ``[B, Hkv, S, D]`` into ``blocks``:
-    per token over groups of ``group`` channels; codes of the page's other tokens are kept."""
-    _, heads, _, dim = values.shape
-    lay = block_layout(dim, bits, group)
-    _, scale, zero, _ = quantize_values(values[b:b + 1], start, stop, bits, group)  # [1, H, T, D/G]
+    per token over groups of ``group`` channels; codes of the pages' other tokens are kept."""
     from .kivi import quantize
 
+    if stop <= start:
+        return
+    _, heads, _, dim = values.shape
+    lay = block_layout(dim, bits, group)
     block = np.asarray(values[b, :, start:stop], dtype=np.float32)  # [H, T, D]
-    codes, _, _ = quantize(block.reshape(heads, stop - start, dim // group, group), bits, axis=3)
-    codes = codes.reshape(heads, stop - start, dim).astype(np.int64)
-    for t in range(start, stop):
-        page = table[b, t // PAGE]
-        pos = t % PAGE
-        for h in range(heads):
-            blk = blocks[page, h]
-            vc = value_codes(blk[lay["v_codes"]:lay["k_scale"]], dim, bits)  # [D, 32]
-            vc[:, pos] = codes[h, t - start]
-            blk[lay["v_codes"]:lay["k_scale"]] = value_words(vc, bits)
-            vs = blk[lay["v_scale"]:lay["v_zero"]].view(np.float16).reshape(dim // group, PAGE).copy()
-            vz = blk[lay["v_zero"]:lay["size"]].view(np.float16).reshape(dim // group, PAGE).copy()
-            with np.errstate(over="ignore"):
-                vs[:, pos] = scale[0, h, t - start].astype(np.float16)
-                vz[:, pos] = zero[0, h, t - start].astype(np.float16)
-            blk[lay["v_scale"]:lay["v_zero"]] = vs.view(np.uint8).reshape(-1)
-            blk[lay["v_zero"]:lay["size"]] = vz.view(np.uint8).reshape(-1)
+    t = block.shape[1]
+    codes, scale, low = quantize(block.reshape(heads, t, dim // group, group), bits, axis=3)
+    codes = codes.reshape(heads, t, dim).astype(np.int64)
+    scale, low = scale.reshape(heads, t, dim // group), low.reshape(heads, t, dim // group)
+    for p0 in range(start - start % PAGE, stop, PAGE):
+        page = int(table[b, p0 // PAGE])
+        lo, hi = max(start, p0), min(stop, p0 + PAGE)
+        blk = blocks[page]  # [H, size]
+        vc = value_codes(blk[:, lay["v_codes"]:lay["k_scale"]], dim, bits)  # [H, D, 32]
+        vc[:, :, lo - p0:hi - p0] = codes[:, lo - start:hi - start].transpose(0, 2, 1)
+        blk[:, lay["v_codes"]:lay["k_scale"]] = value_words(vc, bits)
+        vs = blk[:, lay["v_scale"]:lay["v_zero"]].copy().view(np.float16).reshape(heads, dim // group, PAGE)
+        vz = blk[:, lay["v_zero"]:lay["size"]].copy().view(np.float16).reshape(heads, dim // group, PAGE)
+        with np.errstate(over="ignore"):
+            vs[:, :, lo - p0:hi - p0] = scale[:, lo - start:hi - start].transpose(0, 2, 1).astype(np.float16)
+            vz[:, :, lo - p0:hi - p0] = low[:, lo - start:hi - start].transpose(0, 2, 1).astype(np.float16)
+        blk[:, lay["v_scale"]:lay["v_zero"]] = vs.view(np.uint8).reshape(heads, -1)
+        blk[:, lay["v_zero"]:lay["size"]] = vz.view(np.uint8).reshape(heads, -1)
 
 
 def dense_view(blocks: np.ndarray, table: np.ndarray, k_ring: np.ndarray, v_ring: np.ndarray, lens, kq, vq,
-               bits: int, group: int, round_values: bool = True) -> tuple[np.ndarray, np.ndarray]:
+               bits: int, group: int, rows=None) -> tuple[np.ndarray, np.ndarray]:
     """The keys and values ``[B, Hkv, max(lens), D]`` (float32 holding bf16 values) attention sees: keys below
     ``kq[b]`` and values below ``vq[b]`` dequantized as the reference's ``dequantize`` does (``code * scale + zero``
     in fp32, two roundings, then bf16; attention/kivi.py:56-76), the others from the rings (token ``t`` at slot
-    ``t % W``). ``round_values=False`` leaves the dequantized values in fp32 (not the reference: the form of a value
-    product that never rounds a dequantized value, to measure how far such a product is from the reference)."""
+    ``t % W``). ``rows`` limits the work to those batch rows (the others stay zero)."""
     batch, heads, w, dim = k_ring.shape
     lay = block_layout(dim, bits, group)
     smax = int(max(lens))
     keys = np.zeros((batch, heads, smax, dim), np.float32)
     values = np.zeros((batch, heads, smax, dim), np.float32)
-    for b, n in enumerate(lens):
-        for t in range(int(n)):
-            page, pos = table[b, t // PAGE], t % PAGE
-            for h in range(heads):
-                blk = blocks[page, h]
-                if t < kq[b]:
-                    codes = unpack_words(blk[lay["k_codes"]:lay["v_codes"]].reshape(PAGE, -1), bits)[pos]
-                    s = blk[lay["k_scale"]:lay["k_zero"]].view(np.float16).reshape(-1, dim)[pos // group]
-                    z = blk[lay["k_zero"]:lay["v_scale"]].view(np.float16).reshape(-1, dim)[pos // group]
-                    keys[b, h, t] = round_bf16(((codes * s.astype(np.float32)).astype(np.float32)
-                                                + z.astype(np.float32)).astype(np.float32))
-                else:
-                    keys[b, h, t] = k_ring[b, h, t % w]
-                if t < vq[b]:
-                    codes = value_codes(blk[lay["v_codes"]:lay["k_scale"]], dim, bits)[:, pos]
-                    s = blk[lay["v_scale"]:lay["v_zero"]].view(np.float16).reshape(-1, PAGE)[:, pos]
-                    z = blk[lay["v_zero"]:lay["size"]].view(np.float16).reshape(-1, PAGE)[:, pos]
-                    s = np.repeat(s.astype(np.float32), group)
-                    z = np.repeat(z.astype(np.float32), group)
-                    v = ((codes * s).astype(np.float32) + z).astype(np.float32)
-                    values[b, h, t] = round_bf16(v) if round_values else v
-                else:
-                    values[b, h, t] = v_ring[b, h, :, t % w]
+    for b in (range(batch) if rows is None else rows):
+        n = int(lens[b])
+        if n <= 0:
+            continue
+        npg = (n + PAGE - 1) // PAGE
+        blk = blocks[_rows_pages(table, b, 0, npg)]  # [P, H, size]
+        kc = unpack_words(blk[:, :, lay["k_codes"]:lay["v_codes"]].reshape(npg, heads, PAGE, -1), bits)
+        ks = blk[:, :, lay["k_scale"]:lay["k_zero"]].copy().view(np.float16).reshape(npg, heads, PAGE // group, dim)
+        kz = blk[:, :, lay["k_zero"]:lay["v_scale"]].copy().view(np.float16).reshape(npg, heads, PAGE // group, dim)
+        ks = np.repeat(ks.astype(np.float32), group, axis=2)
+        kz = np.repeat(kz.astype(np.float32), group, axis=2)
+        kd = round_bf16(((kc * ks).astype(np.float32) + kz).astype(np.float32))  # [P, H, 32, D]
+        kd = kd.transpose(1, 0, 2, 3).reshape(heads, npg * PAGE, dim)[:, :n]
+        vc = value_codes(blk[:, :, lay["v_codes"]:lay["k_scale"]], dim, bits)  # [P, H, D, 32]
+        vs = blk[:, :, lay["v_scale"]:lay["v_zero"]].copy().view(np.float16).reshape(npg, heads, dim // group, PAGE)
+        vz = blk[:, :, lay["v_zero"]:lay["size"]].copy().view(np.float16).reshape(npg, heads, dim // group, PAGE)
+        vs = np.repeat(vs.astype(np.float32), group, axis=2)
+        vz = np.repeat(vz.astype(np.float32), group, axis=2)
+        with np.errstate(invalid="ignore", over="ignore"):
+            vd = round_bf16(((vc * vs).astype(np.float32) + vz).astype(np.float32))  # [P, H, D, 32]
+        vd = vd.transpose(1, 0, 3, 2).reshape(heads, npg * PAGE, dim)[:, :n]
+        slots = np.arange(n) % w
+        kr = k_ring[b][:, slots]  # [H, n, D]
+        vr = v_ring[b][:, :, slots].transpose(0, 2, 1)
+        t = np.arange(n)[None, :, None]
+        keys[b, :, :n] = np.where(t < kq[b], kd, kr)
+        values[b, :, :n] = np.where(t < vq[b], vd, vr)
     return keys, values
