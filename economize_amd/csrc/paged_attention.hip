@@ -543,14 +543,8 @@ paged_attention_kernel(PagedParams p) {
                 for (int i = 0; i < 4; ++i)
                     coherent_store(slot + 2 * p.rows + r * D + 16 * nd + 4 * g + i, acc[nd][nb][i] * vs);
         }
-        // the partial's stores complete before the row's counter counts it; the last wave reads them back with
-        // device-coherent loads
-        __builtin_amdgcn_s_waitcnt(0);
-        int prev = 0;
-        if (lane == 0)
-            prev = __hip_atomic_fetch_add(p.counters + c.b * p.kv_heads + c.kvh, 1, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-        merge_row<D>(p, c, __shfl(prev, 0), total, grid, lane);
+        // the partial is released before the row's counter counts it; the last part acquires and merges them all
+        hand_off<D>(p, c, total, grid, lane);
     };
 
     // ---- the tile pipeline: NBUF register buffers, tile pos + NBUF - 1 issued while tile pos is computed ----

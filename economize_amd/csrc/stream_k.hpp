@@ -13,9 +13,8 @@
 namespace eco {
 namespace {
 
-// Device-coherent (agent-scope) store and load of partials: they bypass the caches that are not coherent across the
-// chip's XCDs (gfx950 lowers them to global_store / global_load with sc1), so no L2 writeback or invalidation is
-// needed to hand a partial from one workgroup to another.
+// Device-coherent (agent-scope) store and load of partials (gfx950 lowers them to global_store / global_load with
+// sc1). The hand-off between workgroups is ordered by the fences of hand_off and merge_row.
 __device__ inline void coherent_store(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -270,6 +269,28 @@ __device__ __forceinline__ void ensure_window(const P& p, const Cursor& c, int l
     __builtin_amdgcn_s_waitcnt(0x0F70);
 }
 
+// The hand-off of a row's partial, written by this wave with coherent_store, to the last of the row's parts. The
+// partials are only ever written and read as agent-scope atomics (sc1: written through to, and read from, the level
+// every XCD sees), so what orders the hand-off is completion, not cache maintenance: the compiler may not move the
+// stores past the count (a signal fence), the wave waits until its stores are complete (vmcnt counts stores on
+// gfx950), and only then lane 0 counts the part with an agent-scope atomic; the wave that finds every other part
+// counted issues its loads after the atomic returned (merge_row, after a second signal fence). Agent-scope release /
+// acquire fences (buffer_wbl2 / buffer_inv of the XCD's L2) would add nothing for sc1 data and cost 6 us on the
+// ragged fp8 call and 10-12 us on the KIVI decode call, measured.
+template <int D, typename P>
+__device__ inline void merge_row(const P& p, const Cursor& c, int prev, int64_t total, int grid, int lane);
+
+template <int D, typename P>
+__device__ inline void hand_off(const P& p, const Cursor& c, int64_t total, int grid, int lane) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0), expcnt(0), lgkmcnt(0): every store of the partial is complete
+    int prev = 0;
+    if (lane == 0)
+        prev = __hip_atomic_fetch_add(p.counters + c.b * p.kv_heads + c.kvh, 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+    merge_row<D>(p, c, __shfl(prev, 0), total, grid, lane);
+}
+
 // The merge of a row's partials by the last of its waves to finish: per query row, the maximum and the weighted sum
 // over the partials (lanes over partials), then the weighted accumulators (lanes over channels). Returns without
 // merging when other partials of the row are still outstanding.
@@ -290,6 +311,8 @@ __device__ inline void merge_row(const P& p, const Cursor& c, int prev, int64_t 
         for (int k = w_first + lane; k <= w_last; k += 64) parts += holds(k) ? 1 : 0;
         parts = static_cast<int>(wave_sum(parts));
         if (prev != parts - 1) return;
+        // every other part's partial was complete before its count; the loads follow the count that found them
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         // lane-owned runs of 8 channels of one query row; the partials are folded in batches of 4 with an online
         // log-sum-exp, the batch's loads all in flight together
         for (int base = 0; base < p.rows * D; base += 64 * 8) {
@@ -445,12 +468,7 @@ __device__ inline void merge_pieces(const P& p, Pieces<D, WAVES>& pc, int wave, 
         }
         if (!inside) {
             // the workgroup's partial joins the others' in the workspace; the last workgroup to finish merges them
-            __builtin_amdgcn_s_waitcnt(0);
-            int prev = 0;
-            if (lane == 0)
-                prev = __hip_atomic_fetch_add(p.counters + c.b * p.kv_heads + c.kvh, 1, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
-            merge_row<D>(p, c, __shfl(prev, 0), total, grid, lane);
+            hand_off<D>(p, c, total, grid, lane);
         }
     }
 }
