@@ -3,6 +3,7 @@
 
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/economize_amd.h"
@@ -122,7 +123,7 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
                      int32_t list_page_size, const int32_t* done, const float* sinks, void* out, int64_t so_b,
                      int64_t so_q, int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
                      int32_t head_dim, int32_t page_size, int32_t max_seq_len, float scale, float softcap,
-                     void* workspace, size_t workspace_bytes, void* stream) {
+                     void* workspace, size_t workspace_bytes, void* stream, bool validate_only = false) {
     if (!q || !k_cache || !v_cache || !block_table || !seq_lens || !out)
         return fail("paged decode: null q, cache, block table, seq_lens or out pointer");
     if (batch <= 0 || queries <= 0 || q_heads <= 0 || kv_heads <= 0 || num_pages <= 0 || bt_cols <= 0)
@@ -151,6 +152,7 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
         paged_grid(batch, kv_heads, rows, head_dim, kv_format, max_seq_len, page_list ? n_sel * span : 0, span);
     if (grid <= 0) return 1;
     const Workspace ws = paged_workspace(batch, kv_heads, rows, head_dim, grid);
+    if (validate_only) return 0;
     if (!workspace || workspace_bytes < ws.total())
         return fail("paged decode: workspace too small (" + std::to_string(workspace_bytes) + " < " +
                     std::to_string(ws.total()) + " bytes)");
@@ -201,6 +203,40 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
     p.scale = scale;
     p.softcap = softcap > 0.0f ? softcap : 0.0f;
     return paged_attention(p, static_cast<hipStream_t>(stream));
+}
+
+// ---- the static scratch of eco_paged_decode_static ---------------------------------------------------------------
+// A workspace that needs no allocation: one array per GPU, held until the process ends. Its host-side name is a
+// stand-in, not a device address: host code uses only the address hipGetSymbolAddress returns for the current
+// device (scratch_on_device), never the array's name.
+constexpr size_t kScratchBytes = size_t(32) << 20;  // 32 MiB
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+__global__ void zero_words_kernel(uint32_t* words, int count) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x) words[i] = 0;
+}
+
+// The device address of scratch on the current device (looked up once per device), or null with the error set.
+void* scratch_on_device() {
+    static std::mutex lock;
+    static void* addresses[64] = {};
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) {
+        set_error("paged decode (static scratch): no current HIP device");
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> guard(lock);
+    if (!addresses[device]) {
+        void* ptr = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !ptr) {
+            set_error(std::string("paged decode (static scratch): hipGetSymbolAddress failed: ") +
+                      hipGetErrorString(err));
+            return nullptr;
+        }
+        addresses[device] = ptr;
+    }
+    return addresses[device];
 }
 
 }  // namespace
@@ -299,6 +335,42 @@ int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
                             block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel, list_page_size,
                             done, sinks, out, so_b, so_q, so_h, batch, queries, q_heads, kv_heads, head_dim, page_size,
                             max_seq_len, scale, softcap, workspace, workspace_bytes, stream);
+}
+
+int eco_paged_decode_static(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
+                            const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
+                            const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                            const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h,
+                            int32_t n_sel, int32_t list_page_size, const int32_t* done, const float* sinks, void* out,
+                            int64_t so_b, int64_t so_q, int64_t so_h, int32_t batch, int32_t queries,
+                            int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                            int32_t max_seq_len, float scale, float softcap, void* stream) {
+    // every argument is checked before anything is launched
+    if (const int rc = run_paged_decode(q, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
+                                        block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel,
+                                        list_page_size, done, sinks, out, so_b, so_q, so_h, batch, queries, q_heads,
+                                        kv_heads, head_dim, page_size, max_seq_len, scale, softcap, nullptr, 0, stream,
+                                        true))
+        return rc;
+    const size_t need = eco_paged_decode_workspace_size(batch, queries, q_heads, kv_heads, head_dim, max_seq_len,
+                                                        page_list ? n_sel : 0, list_page_size, kv_format);
+    if (need > kScratchBytes)
+        return fail("paged decode (static scratch): the call needs " + std::to_string(need) +
+                    " bytes of scratch, more than the library's " + std::to_string(kScratchBytes) +
+                    "; use eco_paged_decode with a workspace");
+    void* ptr = scratch_on_device();
+    if (!ptr) return 2;
+    // the row counters must be zero when the call starts (the array keeps the last call's contents): cleared by a
+    // fill kernel on the call's stream (no memset node in a captured graph)
+    const int words = static_cast<int>(align256(static_cast<size_t>(batch) * kv_heads * sizeof(int32_t)) / 4);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(zero_words_kernel, dim3((words + 255) / 256), dim3(256), 0, s, static_cast<uint32_t*>(ptr),
+                       words);
+    if (const int rc = check_launch("zero_words_kernel")) return rc;
+    return run_paged_decode(q, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
+                            block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel, list_page_size,
+                            done, sinks, out, so_b, so_q, so_h, batch, queries, q_heads, kv_heads, head_dim, page_size,
+                            max_seq_len, scale, softcap, ptr, kScratchBytes, stream);
 }
 
 size_t eco_kivi_block_bytes(int32_t head_dim, int32_t bits, int32_t group) {

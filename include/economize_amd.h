@@ -86,6 +86,22 @@ int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
                      int32_t head_dim, int32_t page_size, int32_t max_seq_len, float scale, float softcap,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* eco_paged_decode without a workspace: the scratch is the library's own, so the call allocates nothing (neither the
+ * library nor the caller). No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The scratch is one static
+ * device array of 32 MiB per GPU, held until the process ends; a call whose workspace
+ * (eco_paged_decode_workspace_size) would be larger is refused before any launch. Each call clears the array's row
+ * counters with a fill kernel on its stream before the attention kernel. Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU (on other streams or host threads) race. */
+int eco_paged_decode_static(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
+                            const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
+                            const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                            const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h,
+                            int32_t n_sel, int32_t list_page_size, const int32_t* done, const float* sinks, void* out,
+                            int64_t so_b, int64_t so_q, int64_t so_h, int32_t batch, int32_t queries,
+                            int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                            int32_t max_seq_len, float scale, float softcap, void* stream);
+
 /* Quest page bounds: kmin / kmax (bf16 [B, Hkv, P, D], element strides sb_b, sb_h, sb_p, channel stride 1) of the
  * Quest pages [first, last) of every row (quest_page_size tokens each, a power of two >= 16), the channel-wise
  * smallest and largest stored key read through the block table (fp8 decoded exactly; per-head scales not applied:
