@@ -10,8 +10,9 @@ drawn N(0, 1) in bf16 from a seeded generator and quantize-appended into the cac
 * ``roofline``: the call is one kernel launch (``paged_attention_kernel``): algorithmic bytes per launch (KV + q +
   out + block table + lengths + scales) over its average launch time, against 8 TB/s.
 * ``ragged``: the same with lengths drawn uniformly from [1024, 8192] (mean 4608).
-* ``cpu_baseline``: the numpy oracle (the fp32 definition over gathered, decoded pages) over whole calls of the
-  L = 4096 workload on one thread, for about 10 s.
+* ``cpu_baseline``: the torch-CPU fp32 restatement of the call (oracle/torch_cpu.py) over whole calls of the
+  L = 4096 workload on the host's share of cores (1 warmup, median of 5), with the core count and CPU model; its
+  output is also the check of the timed GPU call's output.
 
 Every path's timed calls rotate over distinct copies of the cache (1 + ceil(384 MB / bytes per call) copies of the
 K/V data, KIVI pages and rings, Quest bounds), the way a decode step reads a different layer's cache at every call
@@ -151,55 +152,54 @@ def measure(lens: list[int], steps: int, warmup: int, seed: int) -> dict:
     }
 
 
-def cpu_baseline(workload, lens: list[int], budget_s: float = 10.0) -> dict:
-    """The numpy oracle (one BLAS thread) over the whole batch, call after call until about budget_s of CPU work; a
-    call that would not finish within the budget is sampled by rows and extrapolated to the batch."""
-    import numpy as np
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(workload, lens: list[int], reps: int = 5) -> dict:
+    """The torch-CPU fp32 restatement of the call (oracle/torch_cpu.py: page gather, exact fp8 decode times the head
+    scale, fp32 attention) over the whole batch, on the host's share of cores (OMP_NUM_THREADS, else every core):
+    one warmup call, then the median of ``reps`` whole calls. Its output is the check of the timed GPU call's output
+    (atol 2e-3 / rtol 1e-2 against this fp32 definition)."""
+    import statistics
+
     import torch
-    from threadpoolctl import threadpool_limits
 
-    from oracle import fp8 as ofp8
-    from oracle.attention import reference_attention
+    from oracle.torch_cpu import paged_fp8_decode_attention
 
-    q, cache, table, seq_lens, _ = workload
-    scale = 1.0 / math.sqrt(HEAD_DIM)
-    q_np = q.float().cpu().numpy()
-    table_np = table.cpu().numpy()
-    ks = cache.k_scale.cpu().numpy().reshape(1, -1, 1, 1)
-    vs = cache.v_scale.cpu().numpy().reshape(1, -1, 1, 1)
-    rows = []
-    for b in range(BATCH):
-        pages = table_np[b, : -(-lens[b] // PAGE)]
-        kc = cache.keys[torch.from_numpy(pages).long().to(cache.keys.device)].view(torch.uint8).cpu().numpy()
-        vc = cache.values[torch.from_numpy(pages).long().to(cache.keys.device)].view(torch.uint8).cpu().numpy()
-        rows.append((kc, vc))
-    done_rows = 0
-    elapsed = 0.0
-    with threadpool_limits(1):
-        while elapsed <= budget_s:
-            for b in range(BATCH):
-                kc, vc = rows[b]
-                t0 = time.perf_counter()
-                # gather: keys [P, H, D/16, 16, 16] -> [H, P*16, D]; values [P, H, D, 16] -> [H, P*16, D]
-                k = kc.transpose(1, 0, 3, 2, 4).reshape(KV_HEADS, -1, HEAD_DIM)[:, : lens[b]]
-                v = vc.transpose(1, 0, 3, 2).reshape(KV_HEADS, -1, HEAD_DIM)[:, : lens[b]]
-                kd = ofp8.fp8_decode(k[None], "e4m3", ks, "f32")
-                vd = ofp8.fp8_decode(v[None], "e4m3", vs, "f32")
-                reference_attention(q_np[b: b + 1].transpose(0, 2, 1, 3), kd, vd, None, scale)
-                elapsed += time.perf_counter() - t0
-                done_rows += 1
-                if elapsed > budget_s:
-                    break
-    per_call = elapsed / done_rows * BATCH
-    calls = done_rows / BATCH
+    q, cache, table, _, out = workload
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    args = (q.cpu(), cache.keys.view(torch.uint8).cpu(), cache.values.view(torch.uint8).cpu(), cache.k_scale.cpu(),
+            cache.v_scale.cpu(), table.cpu(), lens, 1.0 / math.sqrt(HEAD_DIM))
+    want = paged_fp8_decode_attention(*args)  # warmup
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        paged_fp8_decode_attention(*args)
+        times.append(time.perf_counter() - t0)
+    per_call = statistics.median(times)
+    got = out.float().cpu()
+    err = (got - want).abs()
+    within = bool((err <= 2e-3 + 1e-2 * want.abs()).all())
     return {
-        "value": kv_bytes(lens) / per_call / 1e9,
+        "value": round(kv_bytes(lens) / per_call / 1e9, 2),
         "unit": "GB/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "us_per_call": per_call * 1e6,
-        "sample": f"{done_rows} rows = {calls:.2f} calls of the L=4096 batch ({BATCH} rows; numpy oracle: page gather, "
-                  f"fp8 decode, fp32 attention), {elapsed:.1f} s of CPU work on one thread",
+        "cpu": cpu_model(),
+        "us_per_call": round(per_call * 1e6, 1),
+        "sample": f"whole calls of the timed L=4096 workload ({BATCH} rows): 1 warmup + median of {reps}, torch-CPU "
+                  f"fp32 (page gather, fp8 decode, attention) on {threads} threads",
+        "gpu_output_check": {"max_abs_err": round(float(err.max()), 6), "within_atol_2e-3_rtol_1e-2": within},
     }
 
 
