@@ -40,6 +40,9 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
     "eco_paged_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I, _I, _I]),
     "eco_paged_decode": (c_int32, _PAGED_DECODE),
     "eco_paged_decode_static": (c_int32, _PAGED_DECODE[:-3] + [_P]),
+    "eco_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I]),
+    "eco_decode": (c_int32, [_P, _I, _L, _L, _L, _P, _P, _I, _L, _L, _L, _L, _L, _L, _P, _P, _P, _L, _L, _L, _L, _P, _P,
+                             _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P, _S, _P]),
     "eco_quest_page_bounds": (c_int32, [_P, _I, _I, _P, _L, _I, _I, _I, _I, _P, _P, _L, _L, _L, _I, _I, _I, _I, _P]),
     "eco_quest_select_workspace_size": (c_size_t, [_I, _I, _I]),
     "eco_kivi_block_bytes": (c_size_t, [_I, _I, _I]),

@@ -1,6 +1,7 @@
 // extern "C" entry points of libeconomize_amd.so (declared in include/economize_amd.h): argument validation, launch
 // plans and error reporting around the kernels.
 
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -8,6 +9,7 @@
 
 #include "../../include/economize_amd.h"
 #include "common.hpp"
+#include "dense_attention.hpp"
 #include "kivi.hpp"
 #include "kv_quant.hpp"
 #include "paged_attention.hpp"
@@ -108,6 +110,30 @@ int kivi_grid(int batch, int kv_heads, int rows, int head_dim, int bits, int max
     grid = grid < cap ? grid : cap;
     return static_cast<int>(grid < 1 ? 1 : grid);
 }
+
+// The dense decode launch plan, a function of the shapes only: blocks of 16 query rows, and the key axis cut into
+// splits (multiples of 32 keys) so that about four waves per CU run.
+struct DensePlan {
+    int m_tiles, splits, split_len, padded_dim;
+    size_t workspace;
+};
+
+DensePlan dense_plan(int batch, int queries, int q_heads, int kv_heads, int keys, int head_dim, int value_dim) {
+    DensePlan d{};
+    const int rows = (q_heads / kv_heads) * queries;
+    d.m_tiles = (rows + 15) / 16;
+    d.padded_dim = dense_padded_dim(head_dim, value_dim);
+    const int64_t programs = static_cast<int64_t>(batch) * kv_heads * d.m_tiles;
+    const int64_t tiles = (std::max(keys, 1) + 31) / 32;
+    int64_t splits = (4 * static_cast<int64_t>(device_cus()) + programs - 1) / programs;
+    splits = std::max<int64_t>(1, std::min(splits, tiles));
+    d.split_len = static_cast<int>((tiles + splits - 1) / splits) * 32;
+    d.splits = static_cast<int>((std::max(keys, 1) + d.split_len - 1) / d.split_len);
+    d.workspace = align256(static_cast<size_t>(programs) * d.splits * 16 * (d.padded_dim + 2) * sizeof(float));
+    return d;
+}
+
+int element_bytes(int format) { return format == FP32 ? 4 : (format == BF16 || format == FP16 ? 2 : 1); }
 
 int check_kivi_shape(int head_dim, int bits, int group) {
     if (group != 32) return fail("kivi: the paged cache takes groups of 32 (key tokens and value channels)");
@@ -371,6 +397,93 @@ int eco_paged_decode_static(const void* q, int64_t sq_b, int64_t sq_q, int64_t s
                             block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel, list_page_size,
                             done, sinks, out, so_b, so_q, so_h, batch, queries, q_heads, kv_heads, head_dim, page_size,
                             max_seq_len, scale, softcap, ptr, kScratchBytes, stream);
+}
+
+size_t eco_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys,
+                                 int32_t head_dim, int32_t value_dim) {
+    if (batch <= 0 || queries <= 0 || q_heads <= 0 || kv_heads <= 0 || keys < 0 || q_heads % kv_heads) return 0;
+    if (dense_padded_dim(head_dim, value_dim) == 0) return 0;
+    return dense_plan(batch, queries, q_heads, kv_heads, keys, head_dim, value_dim).workspace;
+}
+
+int eco_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int64_t sq_q, const void* k,
+               const void* v, int32_t kv_format, int64_t sk_b, int64_t sk_h, int64_t sk_s, int64_t sv_b, int64_t sv_h,
+               int64_t sv_s, const float* k_scale, const float* v_scale, const uint8_t* mask, int64_t sm_b,
+               int64_t sm_h, int64_t sm_q, int64_t sm_s, const float* sinks, void* out, int64_t so_b, int64_t so_q,
+               int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys,
+               int32_t head_dim, int32_t value_dim, float scale, float softcap, void* workspace,
+               size_t workspace_bytes, void* stream) {
+    if (!q || !k || !v || !out) return fail("decode: null query, key, value or output pointer");
+    if (batch <= 0 || queries <= 0 || q_heads <= 0 || kv_heads <= 0 || keys < 0)
+        return fail("decode: batch, queries and heads must be positive, keys non-negative");
+    if (q_heads % kv_heads)
+        return fail("decode: " + std::to_string(q_heads) + " query heads are not a multiple of " +
+                    std::to_string(kv_heads) + " KV heads");
+    if (q_format != BF16 && q_format != FP16 && q_format != FP32)
+        return fail("decode: queries must be bf16, fp16 or fp32");
+    const bool fp8 = kv_format == FP8_E4M3 || kv_format == FP8_E5M2;
+    if (kv_format != q_format && !fp8) return fail("decode: K/V must be in the query's dtype or fp8");
+    if ((k_scale || v_scale) && !fp8) return fail("decode: per-head scales apply to fp8 K/V only");
+    const int es = element_bytes(kv_format), qs = element_bytes(q_format);
+    for (int dim : {head_dim, value_dim})
+        if (dim <= 0 || dim % 8 || (dim * es) % 16 || dim > 256)
+            return fail("decode: head dims must be positive multiples of 8 (of 16 for fp8), at most 256");
+    auto aligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    if (!aligned(q) || !aligned(k) || !aligned(v))
+        return fail("decode: query, key and value must be 16-byte aligned");
+    for (int64_t st : {sq_b, sq_h, sq_q})
+        if ((st * qs) % 16) return fail("decode: query strides must be multiples of 16 bytes");
+    for (int64_t st : {sk_b, sk_h, sk_s, sv_b, sv_h, sv_s})
+        if ((st * es) % 16) return fail("decode: key and value strides must be multiples of 16 bytes");
+    if (!(scale == scale)) return fail("decode: scale is NaN");
+    const DensePlan d = dense_plan(batch, queries, q_heads, kv_heads, keys, head_dim, value_dim);
+    if (!workspace || workspace_bytes < d.workspace)
+        return fail("decode: workspace too small (" + std::to_string(workspace_bytes) + " < " +
+                    std::to_string(d.workspace) + " bytes)");
+    DenseParams p;
+    std::memset(&p, 0, sizeof(p));
+    p.q = q;
+    p.sq_b = sq_b;
+    p.sq_h = sq_h;
+    p.sq_q = sq_q;
+    p.q_format = q_format;
+    p.k = k;
+    p.v = v;
+    p.kv_format = kv_format;
+    p.sk_b = sk_b;
+    p.sk_h = sk_h;
+    p.sk_s = sk_s;
+    p.sv_b = sv_b;
+    p.sv_h = sv_h;
+    p.sv_s = sv_s;
+    p.k_scale = k_scale;
+    p.v_scale = v_scale;
+    p.mask = mask;
+    p.sm_b = sm_b;
+    p.sm_h = sm_h;
+    p.sm_q = sm_q;
+    p.sm_s = sm_s;
+    p.sinks = sinks;
+    p.out = out;
+    p.so_b = so_b;
+    p.so_q = so_q;
+    p.so_h = so_h;
+    p.part = static_cast<float*>(workspace);
+    p.batch = batch;
+    p.queries = queries;
+    p.q_heads = q_heads;
+    p.kv_heads = kv_heads;
+    p.groups = q_heads / kv_heads;
+    p.rows = p.groups * queries;
+    p.keys = keys;
+    p.head_dim = head_dim;
+    p.value_dim = value_dim;
+    p.m_tiles = d.m_tiles;
+    p.splits = d.splits;
+    p.split_len = d.split_len;
+    p.scale = scale;
+    p.softcap = softcap > 0.0f ? softcap : 0.0f;
+    return dense_attention(p, d.padded_dim, static_cast<hipStream_t>(stream));
 }
 
 size_t eco_kivi_block_bytes(int32_t head_dim, int32_t bits, int32_t group) {

@@ -1,0 +1,34 @@
+// Parameters of the dense decode-attention kernels (dense_attention.hip): a few queries per row over K/V buffers
+// [B, Hkv, S, D] with any element strides (channel stride 1) and an optional boolean mask.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace eco {
+
+struct DenseParams {
+    const void* q;  // [B, Hq, Q, D], element strides sq_*, format q_format (bf16, fp16, fp32)
+    int64_t sq_b, sq_h, sq_q;
+    int q_format;
+    const void* k;  // [B, Hkv, S, D], format kv_format (q_format, or fp8 e4m3 / e5m2)
+    const void* v;  // [B, Hkv, S, Dv]
+    int kv_format;
+    int64_t sk_b, sk_h, sk_s, sv_b, sv_h, sv_s;
+    const float* k_scale;  // [Hkv] or null (fp8 only)
+    const float* v_scale;
+    const uint8_t* mask;  // bool [B, Hq, Q, S] through strides (0 = broadcast), or null: every key visible
+    int64_t sm_b, sm_h, sm_q, sm_s;
+    const float* sinks;  // [Hq] or null
+    void* out;           // [B, Q, Hq, Dv], element strides so_*, format q_format
+    int64_t so_b, so_q, so_h;
+    float* part;  // [programs][splits][16 rows][2 + padded Dv]: max, sum, accumulators
+    int batch, queries, q_heads, kv_heads, groups, rows, keys, head_dim, value_dim;
+    int m_tiles, splits, split_len;
+    float scale, softcap;
+};
+
+int dense_padded_dim(int head_dim, int value_dim);  // 64, 128 or 256; 0 when neither fits
+int dense_attention(const DenseParams& p, int padded_dim, hipStream_t stream);
+
+}  // namespace eco

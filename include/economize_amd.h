@@ -102,6 +102,28 @@ int eco_paged_decode_static(const void* q, int64_t sq_b, int64_t sq_q, int64_t s
                             int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
                             int32_t max_seq_len, float scale, float softcap, void* stream);
 
+/* Workspace bytes eco_decode needs for this shape (0 for an unsupported one). */
+size_t eco_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys,
+                                 int32_t head_dim, int32_t value_dim);
+
+/* Decode attention over dense K/V buffers: out[b, qi, h, :] (element strides so_*, the query's format) for query
+ * q[b, h, qi, :] (format q_format = bf16, fp16 or fp32; element strides sq_*), over k [b, kvh, t, :] and v
+ * [b, kvh, t, :] (t < keys; element strides sk_*, sv_*; format kv_format = the query's, or fp8 e4m3 / e5m2 with
+ * optional per-head scales k_scale / v_scale [Hkv]), query head h reading KV head h / (q_heads / kv_heads). The
+ * optional boolean mask (one byte per element, element mask[b * sm_b + h * sm_h + qi * sm_q + t * sm_s], stride 0
+ * for a broadcast dimension) hides the keys where it is 0; without it every key is visible. Scores are
+ * q . k * scale, with an optional soft cap (softcap > 0) and sinks [Hq] in the denominator; a query that sees no key
+ * gives 0. Channel strides are 1; head_dim and value_dim are multiples of 8 (of 16 for fp8), at most 256; pointers
+ * and K/V/query strides are 16-byte aligned. Replaces decode_attention (attention/decode.py:252-324; kernels
+ * attention/_decode_kernels.py:78-226): split-K over the keys, then a merge of the splits. */
+int eco_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int64_t sq_q, const void* k,
+               const void* v, int32_t kv_format, int64_t sk_b, int64_t sk_h, int64_t sk_s, int64_t sv_b, int64_t sv_h,
+               int64_t sv_s, const float* k_scale, const float* v_scale, const uint8_t* mask, int64_t sm_b,
+               int64_t sm_h, int64_t sm_q, int64_t sm_s, const float* sinks, void* out, int64_t so_b, int64_t so_q,
+               int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys,
+               int32_t head_dim, int32_t value_dim, float scale, float softcap, void* workspace,
+               size_t workspace_bytes, void* stream);
+
 /* Quest page bounds: kmin / kmax (bf16 [B, Hkv, P, D], element strides sb_b, sb_h, sb_p, channel stride 1) of the
  * Quest pages [first, last) of every row (quest_page_size tokens each, a power of two >= 16), the channel-wise
  * smallest and largest stored key read through the block table (fp8 decoded exactly; per-head scales not applied:
