@@ -29,8 +29,10 @@ _FORMATS = {
 
 # argument types of every exported function (kept in the order of include/economize_amd.h)
 _P, _I, _L, _F, _S = c_void_p, c_int32, c_int64, c_float, c_size_t
-_PAGED_DECODE = [_P, _L, _L, _L, _P, _P, _I, _I, _P, _P, _P, _L, _I, _P, _P, _L, _L, _I, _I, _P, _P, _P, _L, _L,
-                 _L, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P, _S, _P]
+_MASK = [_P, _L, _L, _L, _I]  # packed mask bits, word strides (batch, head, query), words per row
+_PAGED_ARGS = [_P, _L, _L, _L, _P, _P, _I, _I, _P, _P, _P, _L, _I, _P, _P, _L, _L, _I, _I, _P, _P, _P, _L, _L, _L,
+               _I, _I, _I, _I, _I, _I, _I, _F, _F] + _MASK
+_PAGED_DECODE = _PAGED_ARGS + [_P, _S, _P]
 SIGNATURES: dict[str, tuple[type | None, list]] = {
     "eco_last_error": (ctypes.c_char_p, []),
     "eco_abi_version": (c_int32, []),
@@ -39,7 +41,8 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
     "eco_fp8_scales_from_absmax": (c_int32, [_P, _I, _I, _P, _P]),
     "eco_paged_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I, _I, _I]),
     "eco_paged_decode": (c_int32, _PAGED_DECODE),
-    "eco_paged_decode_static": (c_int32, _PAGED_DECODE[:-3] + [_P]),
+    "eco_paged_decode_static": (c_int32, _PAGED_ARGS + [_P]),
+    "eco_mask_bits": (c_int32, [_P, _L, _L, _L, _L, _I, _I, _I, _I, _P, _I, _P]),
     "eco_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I]),
     "eco_decode": (c_int32, [_P, _I, _L, _L, _L, _P, _P, _I, _L, _L, _L, _L, _L, _L, _P, _P, _P, _L, _L, _L, _L, _P, _P,
                              _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P, _S, _P]),
@@ -52,7 +55,7 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
     "eco_kivi_ring_write": (c_int32, [_P, _P, _I, _L, _L, _L, _L, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P]),
     "eco_kivi_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I]),
     "eco_kivi_decode": (c_int32, [_P, _L, _L, _L, _P, _I, _P, _P, _I, _P, _P, _P, _L, _I, _P, _P, _P, _L, _L, _L, _I, _I,
-                                  _I, _I, _I, _I, _I, _I, _F, _F, _P, _S, _P]),
+                                  _I, _I, _I, _I, _I, _I, _F, _F] + _MASK + [_P, _S, _P]),
     "eco_quest_select": (c_int32, [_P, _L, _L, _L, _P, _P, _L, _L, _L, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _S,
                                    _P]),
 }

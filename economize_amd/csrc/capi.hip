@@ -149,6 +149,7 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
                      int32_t list_page_size, const int32_t* done, const float* sinks, void* out, int64_t so_b,
                      int64_t so_q, int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
                      int32_t head_dim, int32_t page_size, int32_t max_seq_len, float scale, float softcap,
+                     const uint32_t* mask_bits, int64_t mk_b, int64_t mk_h, int64_t mk_q, int32_t mask_words,
                      void* workspace, size_t workspace_bytes, void* stream, bool validate_only = false) {
     if (!q || !k_cache || !v_cache || !block_table || !seq_lens || !out)
         return fail("paged decode: null q, cache, block table, seq_lens or out pointer");
@@ -173,6 +174,7 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
     const int span = list_page_size / 16;
     if (max_seq_len <= 0) return fail("paged decode: max_seq_len must be positive");
     if (!(scale == scale)) return fail("paged decode: scale is NaN");
+    if (mask_bits && mask_words <= 0) return fail("paged decode: a mask needs a positive word count");
 
     const int grid =
         paged_grid(batch, kv_heads, rows, head_dim, kv_format, max_seq_len, page_list ? n_sel * span : 0, span);
@@ -210,6 +212,11 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
     p.k_scale = k_scale;
     p.v_scale = v_scale;
     p.sinks = sinks;
+    p.mask = mask_bits;
+    p.mk_b = mk_b;
+    p.mk_h = mk_h;
+    p.mk_q = mk_q;
+    p.mask_words = mask_bits ? mask_words : 0;
     char* base = static_cast<char*>(workspace);
     p.counters = reinterpret_cast<int32_t*>(base);
     p.part = reinterpret_cast<float*>(base + ws.counter_bytes);
@@ -237,6 +244,27 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
 // device (scratch_on_device), never the array's name.
 constexpr size_t kScratchBytes = size_t(32) << 20;  // 32 MiB
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// bits[((b * heads + h) * queries + q) * words + w] bit k = mask[b, h, q, 32 w + k] != 0 (0 past the keys).
+__global__ void mask_bits_kernel(const uint8_t* mask, int64_t sm_b, int64_t sm_h, int64_t sm_q, int64_t sm_s,
+                                 int batch, int heads, int queries, int keys, uint32_t* bits, int words) {
+    const int64_t total = static_cast<int64_t>(batch) * heads * queries * words;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int w = static_cast<int>(i % words);
+        const int64_t row = i / words;
+        const int q = static_cast<int>(row % queries);
+        const int h = static_cast<int>((row / queries) % heads);
+        const int b = static_cast<int>(row / (static_cast<int64_t>(queries) * heads));
+        const uint8_t* src = mask + b * sm_b + h * sm_h + q * sm_q;
+        uint32_t word = 0;
+        for (int k = 0; k < 32; ++k) {
+            const int t = 32 * w + k;
+            if (t < keys && src[static_cast<int64_t>(t) * sm_s]) word |= 1u << k;
+        }
+        bits[i] = word;
+    }
+}
 
 __global__ void zero_words_kernel(uint32_t* words, int count) {
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x) words[i] = 0;
@@ -275,7 +303,7 @@ extern "C" {
 
 const char* eco_last_error(void) { return g_error.c_str(); }
 
-int eco_abi_version(void) { return 2; }
+int eco_abi_version(void) { return 3; }
 
 int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
                      int64_t sv_t, int64_t sv_h, const int32_t* slot_mapping, int32_t tokens, void* k_cache,
@@ -356,11 +384,13 @@ int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
                      int32_t list_page_size, const int32_t* done, const float* sinks, void* out, int64_t so_b,
                      int64_t so_q, int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
                      int32_t head_dim, int32_t page_size, int32_t max_seq_len, float scale, float softcap,
+                     const uint32_t* mask_bits, int64_t mk_b, int64_t mk_h, int64_t mk_q, int32_t mask_words,
                      void* workspace, size_t workspace_bytes, void* stream) {
     return run_paged_decode(q, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
                             block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel, list_page_size,
                             done, sinks, out, so_b, so_q, so_h, batch, queries, q_heads, kv_heads, head_dim, page_size,
-                            max_seq_len, scale, softcap, workspace, workspace_bytes, stream);
+                            max_seq_len, scale, softcap, mask_bits, mk_b, mk_h, mk_q, mask_words, workspace,
+                            workspace_bytes, stream);
 }
 
 int eco_paged_decode_static(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
@@ -370,13 +400,14 @@ int eco_paged_decode_static(const void* q, int64_t sq_b, int64_t sq_q, int64_t s
                             int32_t n_sel, int32_t list_page_size, const int32_t* done, const float* sinks, void* out,
                             int64_t so_b, int64_t so_q, int64_t so_h, int32_t batch, int32_t queries,
                             int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
-                            int32_t max_seq_len, float scale, float softcap, void* stream) {
+                            int32_t max_seq_len, float scale, float softcap, const uint32_t* mask_bits, int64_t mk_b,
+                            int64_t mk_h, int64_t mk_q, int32_t mask_words, void* stream) {
     // every argument is checked before anything is launched
     if (const int rc = run_paged_decode(q, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
                                         block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel,
                                         list_page_size, done, sinks, out, so_b, so_q, so_h, batch, queries, q_heads,
-                                        kv_heads, head_dim, page_size, max_seq_len, scale, softcap, nullptr, 0, stream,
-                                        true))
+                                        kv_heads, head_dim, page_size, max_seq_len, scale, softcap, mask_bits, mk_b,
+                                        mk_h, mk_q, mask_words, nullptr, 0, stream, true))
         return rc;
     const size_t need = eco_paged_decode_workspace_size(batch, queries, q_heads, kv_heads, head_dim, max_seq_len,
                                                         page_list ? n_sel : 0, list_page_size, kv_format);
@@ -396,7 +427,8 @@ int eco_paged_decode_static(const void* q, int64_t sq_b, int64_t sq_q, int64_t s
     return run_paged_decode(q, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
                             block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel, list_page_size,
                             done, sinks, out, so_b, so_q, so_h, batch, queries, q_heads, kv_heads, head_dim, page_size,
-                            max_seq_len, scale, softcap, ptr, kScratchBytes, stream);
+                            max_seq_len, scale, softcap, mask_bits, mk_b, mk_h, mk_q, mask_words, ptr, kScratchBytes,
+                            stream);
 }
 
 size_t eco_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys,
@@ -486,6 +518,18 @@ int eco_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int6
     return dense_attention(p, d.padded_dim, static_cast<hipStream_t>(stream));
 }
 
+int eco_mask_bits(const uint8_t* mask, int64_t sm_b, int64_t sm_h, int64_t sm_q, int64_t sm_s, int32_t batch,
+                  int32_t heads, int32_t queries, int32_t keys, uint32_t* bits, int32_t words, void* stream) {
+    if (!mask || !bits) return fail("mask bits: null mask or output");
+    if (batch <= 0 || heads <= 0 || queries <= 0 || keys < 0 || words < (keys + 31) / 32 || words <= 0)
+        return fail("mask bits: sizes must be positive and words must cover the keys");
+    const int64_t total = static_cast<int64_t>(batch) * heads * queries * words;
+    const int blocks = static_cast<int>(std::min<int64_t>((total + 255) / 256, 65535));
+    hipLaunchKernelGGL(mask_bits_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), mask, sm_b,
+                       sm_h, sm_q, sm_s, batch, heads, queries, keys, bits, words);
+    return check_launch("mask_bits_kernel");
+}
+
 size_t eco_kivi_block_bytes(int32_t head_dim, int32_t bits, int32_t group) {
     if (check_kivi_shape(head_dim, bits, group)) return 0;
     return static_cast<size_t>(KiviLayout{head_dim, bits}.size());
@@ -572,8 +616,9 @@ int eco_kivi_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, con
                     const int32_t* values_quantized, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
                     const int32_t* seq_lens, const float* sinks, void* out, int64_t so_b, int64_t so_q, int64_t so_h,
                     int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
-                    int32_t bits, int32_t group, int32_t max_seq_len, float scale, float softcap, void* workspace,
-                    size_t workspace_bytes, void* stream) {
+                    int32_t bits, int32_t group, int32_t max_seq_len, float scale, float softcap,
+                    const uint32_t* mask_bits, int64_t mk_b, int64_t mk_h, int64_t mk_q, int32_t mask_words,
+                    void* workspace, size_t workspace_bytes, void* stream) {
     if (!q || !blocks || !k_ring || !v_ring || !keys_quantized || !values_quantized || !block_table || !seq_lens ||
         !out)
         return fail("kivi decode: null query, cache, ring, counts, table, lengths or output");
@@ -590,6 +635,7 @@ int eco_kivi_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, con
         return fail("kivi decode: the query must be 16-byte aligned with strides that are multiples of 8");
     if (max_seq_len <= 0) return fail("kivi decode: max_seq_len must be positive");
     if (!(scale == scale)) return fail("kivi decode: scale is NaN");
+    if (mask_bits && mask_words <= 0) return fail("kivi decode: a mask needs a positive word count");
     const int grid = kivi_grid(batch, kv_heads, rows, head_dim, bits, max_seq_len);
     if (grid <= 0) return 1;
     const Workspace ws = paged_workspace(batch, kv_heads, rows, head_dim, grid);
@@ -617,6 +663,11 @@ int eco_kivi_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, con
     p.num_pages = num_pages;
     p.seq_lens = seq_lens;
     p.sinks = sinks;
+    p.mask = mask_bits;
+    p.mk_b = mk_b;
+    p.mk_h = mk_h;
+    p.mk_q = mk_q;
+    p.mask_words = mask_bits ? mask_words : 0;
     char* base = static_cast<char*>(workspace);
     p.counters = reinterpret_cast<int32_t*>(base);
     p.part = reinterpret_cast<float*>(base + ws.counter_bytes);

@@ -266,7 +266,8 @@ struct KTile {
     uint32_t vc[SHARED ? VE : ND];
     uint4 ks[SHARED ? 1 : KS], kz[SHARED ? 1 : KS];
     uint4 vs[SHARED ? 1 : VG], vz[SHARED ? 1 : VG];
-    int page;  // physical page (the same in every lane), -1 for none
+    int page;          // physical page (the same in every lane), -1 for none
+    uint32_t mw[4];    // with a mask: bit e = token 8 g + e of the page visible to query row 16 nb + n (nb < NB)
 };
 
 template <int N>
@@ -626,7 +627,7 @@ kivi_attention_kernel(KiviParams p) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) s[v][nb][i] = soft_cap_log2(s[v][nb][i], p.softcap, inv_cap);
         }
-        if (t0 + KPAGE > all_see || (!valid && t0 < kq)) {
+        if (t0 + KPAGE > all_see || (!valid && t0 < kq) || p.mask) {
 #pragma unroll
             for (int v = 0; v < 2; ++v)
 #pragma unroll
@@ -634,7 +635,8 @@ kivi_attention_kernel(KiviParams p) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int token = t0 + 8 * g + 4 * v + i;
-                        const bool ok = static_cast<float>(token) < limit[nb] && (valid || token >= kq);
+                        bool ok = static_cast<float>(token) < limit[nb] && (valid || token >= kq);
+                        if (p.mask) ok = ok && ((tile.mw[nb] >> (4 * v + i)) & 1u);
                         s[v][nb][i] = ok ? s[v][nb][i] : -INFINITY;
                     }
         }
@@ -792,6 +794,10 @@ kivi_attention_kernel(KiviParams p) {
         int64_t ipos = lo;
         auto issue_next = [&](T& buf, Cursor& slot) __attribute__((always_inline)) {
             issue_tile<D, BITS, SHARED>(p, icur, n, g, lane, wave, win, buf);
+            if (p.mask)  // the tile is page icur.t: word icur.t of every query row's mask
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb)
+                    buf.mw[nb] = (mask_word(p, icur.b, icur.kvh, row0 + nb * 16 + n, icur.t) >> (8 * g)) & 0xFFu;
             slot = icur;
             if (ipos < hi) {
                 if (ipos + 1 < hi) advance(p, icur, small ? &rt : nullptr);

@@ -40,6 +40,9 @@ struct KiviParams {
     int bt_cols, num_pages;
     const int32_t* seq_lens;
     const float* sinks;
+    const uint32_t* mask;  // optional packed mask (stream_k.hpp mask_word): visible = causal limit and mask bit
+    int64_t mk_b, mk_h, mk_q;
+    int mask_words;
     int32_t* counters;
     float* part;
     uint16_t* out;

@@ -123,7 +123,17 @@ struct Tile {
     bf16x8 q[RQ ? 1 : NB][RQ ? 1 : KS];  // the query operand of the tile's row (an L2 hit after the row's first tile)
     int lv;    // logical page of the lane group's tile page (-1: none)
     int vcnt;  // tokens of that page inside the row (0 to 16); the V bytes of the others are cleared before use
+    uint32_t mw[NB];  // with a mask: bit k = token lv * 16 + k of query row nb * 16 + n is visible
 };
+
+// The mask bits of the lane group's tile page for each column block (loaded only with a mask).
+template <int D, int FMT, int NB, bool RQ>
+__device__ __forceinline__ void load_mask_bits(const PagedParams& p, const Cursor& c, int n, Tile<D, FMT, NB, RQ>& tile) {
+    if (!p.mask) return;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+        tile.mw[nb] = tile.lv >= 0 ? mask_word(p, c.b, c.kvh, nb * 16 + n, tile.lv >> 1) >> (16 * (tile.lv & 1)) : 0u;
+}
 
 // The query operand of row c: lane (n, g) holds query row nb * 16 + n, channels of k-step j as the K runs order them
 // (a lane of a row past the group reads row 0: its MFMA column is computed and never stored).
@@ -156,6 +166,7 @@ __device__ __forceinline__ void issue_tile(const PagedParams& p, const Cursor& c
     const int pv = __shfl(win.physical, at + g);
     tile.lv = __shfl(win.logical, at + g);
     tile.vcnt = tile.lv >= 0 ? min(max(c.row.len - tile.lv * PAGE, 0), PAGE) : 0;
+    load_mask_bits(p, c, n, tile);
     // Every lane issues the same loads whatever its pages are (a page that holds nothing reads page 0, and its
     // scores and values are masked when the tile is computed): with the same number of loads on every path, the
     // wait before a tile's use leaves the younger tiles' loads in flight.
@@ -200,6 +211,7 @@ __device__ __forceinline__ void issue_tile_rq(const PagedParams& p, const Cursor
     const int pv = __shfl(win.physical, at + g);
     tile.lv = __shfl(win.logical, at + g);
     tile.vcnt = tile.lv >= 0 ? min(max(c.row.len - tile.lv * PAGE, 0), PAGE) : 0;
+    load_mask_bits(p, c, n, tile);
     const uint8_t* kp = p.k_cache + c.kvh * p.kc_head + static_cast<int64_t>(pk >= 0 ? pk : 0) * p.kc_page;
 #pragma unroll
     for (int v = 0; v < 4; ++v)
@@ -367,7 +379,8 @@ paged_attention_kernel(PagedParams p) {
         bf16x8 pop_hi[NB][2], pop_lo[NB][2];
         const int first = tile.lv * PAGE;  // position of token 0 of tile page g
         // Scores in log2 units (times the scale, through the soft cap if one is set). Only a tile that holds a
-        // row's end, an empty page or a token some causal query row must not see is masked.
+        // row's end, an empty page or a token some causal query row must not see is masked, and every tile of a
+        // call with a mask (visible = the causal limit and the mask bit).
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -392,14 +405,15 @@ paged_attention_kernel(PagedParams p) {
                         }
                     }
         }
-        if (__ballot(tile.lv < 0 || first + PAGE > all_see) != 0) {
+        if (p.mask || __ballot(tile.lv < 0 || first + PAGE > all_see) != 0) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
                 for (int v = 0; v < 4; ++v)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        const bool ok = tile.lv >= 0 && static_cast<float>(first + 4 * v + i) < limit[nb];
+                        bool ok = tile.lv >= 0 && static_cast<float>(first + 4 * v + i) < limit[nb];
+                        if (p.mask) ok = ok && ((tile.mw[nb] >> (4 * v + i)) & 1u);
                         s[v][nb][i] = ok ? s[v][nb][i] : -INFINITY;
                     }
         }

@@ -29,6 +29,9 @@ struct PagedParams {
     const float* k_scale;  // optional [Hkv]
     const float* v_scale;
     const float* sinks;  // optional [Hq] logits
+    const uint32_t* mask;  // optional packed mask (stream_k.hpp mask_word): visible = causal limit and mask bit
+    int64_t mk_b, mk_h, mk_q;
+    int mask_words;
     int32_t* counters;  // [B * Hkv], zero between calls (the merging wave resets its row's counter)
     float* part;        // [2 * grid, rows, D + 2]: per workgroup two slots of a row segment's maxima, sums, accumulators
     uint16_t* out;  // bf16 [B, Q, Hq, D], channel stride 1

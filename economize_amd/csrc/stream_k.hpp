@@ -4,8 +4,8 @@
 //
 // A params type P provides: kPage (tokens per cache page), kTile (cache pages per tile), kPageList (whether it takes a
 // Quest page list); the fields batch, kv_heads, rows, queries, groups, seq_lens, bt_cols, block_table, bt_stride,
-// num_pages, sinks, out, so_b, so_q, so_h, counters, part; and, with kPageList, page_list, pl_b, pl_h, n_sel, span,
-// done.
+// num_pages, sinks, out, so_b, so_q, so_h, counters, part, mask, mk_b, mk_h, mk_q, mask_words; and, with kPageList,
+// page_list, pl_b, pl_h, n_sel, span, done.
 #pragma once
 
 #include "common.hpp"
@@ -64,6 +64,16 @@ __device__ inline int64_t uniform64(int64_t x) {
     const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
     const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
     return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// The optional attention mask, packed: bit t % 32 of word t / 32 of query row r of (b, kvh) says whether token t is
+// visible (words [B][Hq][Q][mask_words] through the word strides mk_b, mk_h, mk_q, 0 on a broadcast axis). The word
+// of tokens 32 w .. 32 w + 31; 0 (hidden) for a row past the group or a word past the mask.
+template <typename P>
+__device__ inline uint32_t mask_word(const P& p, int b, int kvh, int r, int w) {
+    if (r >= p.rows || w < 0 || w >= p.mask_words) return 0u;
+    const int gq = r / p.queries, qi = r % p.queries;
+    return p.mask[b * p.mk_b + (kvh * p.groups + gq) * p.mk_h + qi * p.mk_q + w];
 }
 
 // Geometry of batch row b: tokens (cut at the block table's reach), where a page list's dense tail starts, and

@@ -22,7 +22,7 @@ import torch
 
 from . import _lib
 from .errors import ConfigError
-from .paged import cached_workspace, counter_bytes
+from .paged import cached_workspace, counter_bytes, packed_mask
 
 __all__ = ["KIVI_PAGE", "PagedKIVICache", "kivi_append", "kivi_commit", "kivi_decode_attention", "kivi_quantize"]
 
@@ -207,11 +207,13 @@ def kivi_commit(cache: PagedKIVICache, block_table: torch.Tensor, committed: tor
 def kivi_decode_attention(query: torch.Tensor, cache: PagedKIVICache, block_table: torch.Tensor,
                           seq_lens: torch.Tensor, max_seq_len: int, scale: float | None = None,
                           softcap: float | None = None, sinks: torch.Tensor | None = None,
-                          out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+                          out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+                          mask: torch.Tensor | None = None) -> torch.Tensor:
     """Attention of ``query`` ``[B, Q, Hq, D]`` (bf16, contiguous channels) over the KIVI cache, ``[B, Q, Hq, D]``
     bf16 out: row ``b`` holds ``seq_lens[b]`` tokens (int32 ``[B]``), its ``Q`` queries the last of them (causal).
     Keys below ``keys_quantized[b]`` and values below ``values_quantized[b]`` are codes, the rest come from the
-    rings. ``scale`` defaults to ``1 / sqrt(D)``."""
+    rings. ``scale`` defaults to ``1 / sqrt(D)``. ``mask`` (boolean ``[B or 1, Hq or 1, Q or 1, S]``, key ``t`` =
+    token ``t``) hides keys on top of the causal limit."""
     cache.check()
     _table(block_table, cache.batch)
     device = _lib.require_gpu(query, cache.blocks, block_table, seq_lens)
@@ -237,13 +239,15 @@ def kivi_decode_attention(query: torch.Tensor, cache: PagedKIVICache, block_tabl
     if workspace is None:
         workspace = cached_workspace(need, counter_bytes(batch, cache.kv_heads), device)
     scale = 1.0 / math.sqrt(head_dim) if scale is None else float(scale)
+    bits, mk, words = packed_mask(mask, batch, q_heads, queries)
     _lib.call(
         "eco_kivi_decode", query.data_ptr(), query.stride(0), query.stride(1), query.stride(2),
         cache.blocks.data_ptr(), cache.num_pages, cache.k_ring.data_ptr(), cache.v_ring.data_ptr(), cache.ring,
         cache.keys_quantized.data_ptr(), cache.values_quantized.data_ptr(), block_table.data_ptr(),
         block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(), _lib.ptr(sinks), out.data_ptr(),
         out.stride(0), out.stride(1), out.stride(2), batch, queries, q_heads, cache.kv_heads, head_dim, cache.bits,
-        cache.group, int(max_seq_len), scale, float(softcap or 0.0), workspace.data_ptr(), workspace.numel(),
+        cache.group, int(max_seq_len), scale, float(softcap or 0.0), _lib.ptr(bits), *mk, words,
+        workspace.data_ptr(), workspace.numel(),
         _lib.stream_of(device),
     )
     return out

@@ -175,6 +175,29 @@ class CachedWorkspace:
 _workspaces: dict[tuple[torch.device, int], CachedWorkspace] = {}
 
 
+def packed_mask(mask: torch.Tensor | None, batch: int, q_heads: int, queries: int
+                ) -> tuple[torch.Tensor | None, tuple[int, int, int], int]:
+    """A boolean attention mask ``[B or 1, Hq or 1, Q or 1, S]`` (``True`` = visible; key ``t`` of the mask is token
+    ``t`` of every row) packed for the paged kernels: int32 words ``[B or 1, Hq or 1, Q or 1, ceil(S / 32)]`` (bit
+    ``t % 32`` of word ``t / 32``), their ``(batch, head, query)`` word strides (0 on a broadcast axis) and the words
+    per row; ``(None, (0, 0, 0), 0)`` without a mask."""
+    if mask is None:
+        return None, (0, 0, 0), 0
+    if mask.dtype != torch.bool or mask.dim() != 4:
+        raise ConfigError("the attention mask must be boolean [B or 1, Hq or 1, Q or 1, S]")
+    bm, hm, qm, keys = mask.shape
+    if bm not in (1, batch) or hm not in (1, q_heads) or qm not in (1, queries) or keys == 0:
+        raise ConfigError(f"mask {tuple(mask.shape)} does not broadcast to [{batch}, {q_heads}, {queries}, S]")
+    device = _lib.require_gpu(mask)
+    words = -(-keys // 32)
+    bits = torch.empty(bm, hm, qm, words, dtype=torch.int32, device=device)
+    m = mask.view(torch.uint8)
+    _lib.call("eco_mask_bits", m.data_ptr(), *m.stride(), bm, hm, qm, keys, bits.data_ptr(), words,
+              _lib.stream_of(device))
+    strides = (hm * qm * words if bm > 1 else 0, qm * words if hm > 1 else 0, words if qm > 1 else 0)
+    return bits, strides, words
+
+
 def cached_workspace(nbytes: int, counters: int, device: torch.device) -> torch.Tensor:
     """The workspace of ``device``'s current stream used when the caller passes none (see :class:`CachedWorkspace`)."""
     key = (device, torch.cuda.current_stream(device).cuda_stream)
@@ -195,6 +218,7 @@ def paged_decode_attention(
     done: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
     list_page_size: int = PAGE,
+    mask: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Attention of ``query`` ``[B, Q, Hq, D]`` (bf16, channel-contiguous) over the paged cache, ``[B, Q, Hq, D]``
     bf16 out.
@@ -207,7 +231,8 @@ def paged_decode_attention(
     (int32 ``[B]``, in the same pages) the keys read are the listed pages below ``done[b]`` and every token from page
     ``done[b]`` on (Quest's gathered attention).
     ``workspace`` (from :func:`new_workspace`, at least :func:`workspace_size` bytes) defaults to a cached one per
-    device and stream.
+    device and stream. ``mask`` (boolean ``[B or 1, Hq or 1, Q or 1, S]``, key ``t`` = token ``t`` of the row, as the
+    reference's decode_attention takes it) hides keys on top of the causal limit.
     """
     cache.check()
     device = _lib.require_gpu(query, cache.keys, block_table, seq_lens)
@@ -248,6 +273,7 @@ def paged_decode_attention(
     if workspace is None:
         workspace = cached_workspace(need, counter_bytes(batch, cache.kv_heads), device)
     scale = 1.0 / math.sqrt(head_dim) if scale is None else float(scale)
+    bits, mk, words = packed_mask(mask, batch, q_heads, queries)
     _lib.call(
         "eco_paged_decode",
         query.data_ptr(), query.stride(0), query.stride(1), query.stride(2),
@@ -259,6 +285,6 @@ def paged_decode_attention(
         _lib.ptr(sinks),
         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
         batch, queries, q_heads, cache.kv_heads, head_dim, PAGE, int(max_seq_len), scale, float(softcap or 0.0),
-        workspace.data_ptr(), workspace.numel(), _lib.stream_of(device),
+        _lib.ptr(bits), *mk, words, workspace.data_ptr(), workspace.numel(), _lib.stream_of(device),
     )
     return out

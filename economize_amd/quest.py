@@ -165,19 +165,21 @@ class QuestPages:
 
     def attend(self, query: torch.Tensor, cache: PagedKVCache, block_table: torch.Tensor, seq_lens: torch.Tensor,
                max_seq_len: int, scale: float | None = None, softcap: float | None = None,
-               sinks: torch.Tensor | None = None) -> torch.Tensor:
+               sinks: torch.Tensor | None = None, mask: torch.Tensor | None = None) -> torch.Tensor:
         """``[B, Q, Hq, D]`` attention of ``query`` ``[B, Hq, Q, D]`` over the selected pages and the dense tail; a
         query longer than :attr:`max_queries` attends densely (attention/quest.py:191-204)."""
         if query.shape[2] > self.max_queries:
             return paged_decode_attention(query.transpose(1, 2), cache, block_table, seq_lens, max_seq_len, scale,
-                                          softcap, sinks)
-        return quest_decode_attention(query, cache, block_table, seq_lens, max_seq_len, self, scale, softcap, sinks)
+                                          softcap, sinks, mask=mask)
+        return quest_decode_attention(query, cache, block_table, seq_lens, max_seq_len, self, scale, softcap, sinks,
+                                      mask=mask)
 
 
 def quest_decode_attention(query: torch.Tensor, cache: PagedKVCache, block_table: torch.Tensor,
                            seq_lens: torch.Tensor, max_seq_len: int, pages: QuestPages, scale: float | None = None,
                            softcap: float | None = None, sinks: torch.Tensor | None = None,
-                           out: torch.Tensor | None = None, index: torch.Tensor | None = None) -> torch.Tensor:
+                           out: torch.Tensor | None = None, index: torch.Tensor | None = None,
+                           mask: torch.Tensor | None = None) -> torch.Tensor:
     """Paged decode attention over the selected pages and the dense tail (attention/quest.py:239-344).
 
     Args:
@@ -190,6 +192,7 @@ def quest_decode_attention(query: torch.Tensor, cache: PagedKVCache, block_table
         sinks: Optional ``[Hq]`` attention-sink logits.
         out: Optional ``[B, Q, Hq, D]`` output buffer.
         index: Selected pages (int32 ``[B, Hkv, pages]``) to use instead of :meth:`QuestPages.select`'s.
+        mask: Optional boolean attention mask (see :func:`~economize_amd.paged.paged_decode_attention`).
 
     Returns:
         bf16 ``[B, Q, Hq, D]``.
@@ -207,4 +210,4 @@ def quest_decode_attention(query: torch.Tensor, cache: PagedKVCache, block_table
     scale = 1.0 / math.sqrt(query.shape[-1]) if scale is None else scale
     return paged_decode_attention(query.transpose(1, 2), cache, block_table, seq_lens, max_seq_len, scale, softcap,
                                   sinks, out, page_list=index.contiguous(), done=pages.done,
-                                  list_page_size=pages.page)
+                                  list_page_size=pages.page, mask=mask)

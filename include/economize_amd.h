@@ -76,7 +76,9 @@ size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q
  * (strides pl_b, pl_h; page indices of list_page_size tokens each, 0 = 16; pages below done[b] are read, others
  * read nothing) and then every token from page done[b] on (done in listed pages too). One launch: the work is cut
  * into equal contiguous ranges of 64-token tiles, one per wave, so ragged rows need no host-side plan; max_seq_len
- * (>= every seq_lens[b]) only bounds the launch. */
+ * (>= every seq_lens[b]) only bounds the launch. An optional packed attention mask (eco_mask_bits: bit t % 32 of word
+ * mask_bits[b * mk_b + h * mk_h + qi * mk_q + t / 32], word strides 0 on broadcast axes, mask_words words per row;
+ * NULL = none) hides token t from query qi of head h where its bit is 0, on top of the causal limit. */
 int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
                      const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
                      const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
@@ -84,6 +86,7 @@ int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
                      int32_t list_page_size, const int32_t* done, const float* sinks, void* out, int64_t so_b,
                      int64_t so_q, int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
                      int32_t head_dim, int32_t page_size, int32_t max_seq_len, float scale, float softcap,
+                     const uint32_t* mask_bits, int64_t mk_b, int64_t mk_h, int64_t mk_q, int32_t mask_words,
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* eco_paged_decode without a workspace: the scratch is the library's own, so the call allocates nothing (neither the
@@ -100,7 +103,16 @@ int eco_paged_decode_static(const void* q, int64_t sq_b, int64_t sq_q, int64_t s
                             int32_t n_sel, int32_t list_page_size, const int32_t* done, const float* sinks, void* out,
                             int64_t so_b, int64_t so_q, int64_t so_h, int32_t batch, int32_t queries,
                             int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t page_size,
-                            int32_t max_seq_len, float scale, float softcap, void* stream);
+                            int32_t max_seq_len, float scale, float softcap, const uint32_t* mask_bits, int64_t mk_b,
+                            int64_t mk_h, int64_t mk_q, int32_t mask_words, void* stream);
+
+/* The packed form of a boolean attention mask that the paged decode kernels take: bits[((b * heads + h) * queries +
+ * q) * words + w] has bit k set where mask[b * sm_b + h * sm_h + q * sm_q + (32 w + k) * sm_s] is nonzero (one byte
+ * per element; 0 past `keys`). words >= ceil(keys / 32). A broadcast axis of the mask is packed once (pass its size
+ * as 1) and read through a word stride of 0. No counterpart in the reference, whose kernels read the bytes
+ * (attention/_decode_kernels.py:67-74); a packed word per 32 keys is one aligned load per tile here. */
+int eco_mask_bits(const uint8_t* mask, int64_t sm_b, int64_t sm_h, int64_t sm_q, int64_t sm_s, int32_t batch,
+                  int32_t heads, int32_t queries, int32_t keys, uint32_t* bits, int32_t words, void* stream);
 
 /* Workspace bytes eco_decode needs for this shape (0 for an unsupported one). */
 size_t eco_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys,
@@ -200,8 +212,9 @@ int eco_kivi_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, con
                     const int32_t* values_quantized, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
                     const int32_t* seq_lens, const float* sinks, void* out, int64_t so_b, int64_t so_q, int64_t so_h,
                     int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
-                    int32_t bits, int32_t group, int32_t max_seq_len, float scale, float softcap, void* workspace,
-                    size_t workspace_bytes, void* stream);
+                    int32_t bits, int32_t group, int32_t max_seq_len, float scale, float softcap,
+                    const uint32_t* mask_bits, int64_t mk_b, int64_t mk_h, int64_t mk_q, int32_t mask_words,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -99,9 +99,10 @@ def device_cache(c: KiviCase, poison: bool = False):
     return cache, table
 
 
-def oracle_output(c: KiviCase, scale=None, softcap=None, sinks=None, rows=None) -> np.ndarray:
+def oracle_output(c: KiviCase, scale=None, softcap=None, sinks=None, rows=None, mask=None) -> np.ndarray:
     """The fp32 attention (decode.py:66-103) over the keys and values the reference's ``dequantize`` gives from the
-    oracle's pages, and the bf16 residual; ``[B, Q, Hq, D]``, only the batch ``rows`` given (all by default)."""
+    oracle's pages, and the bf16 residual; ``[B, Q, Hq, D]``, only the batch ``rows`` given (all by default). An
+    extra boolean ``mask`` ``[B or 1, Hq or 1, Q or 1, >= S]`` hides keys on top of the causal limit."""
     batch, kv_heads, smax, head_dim = c.k.shape
     rows = list(range(batch)) if rows is None else list(rows)
     blocks = oracle_blocks(c, head_dim, rows)
@@ -119,10 +120,12 @@ def oracle_output(c: KiviCase, scale=None, softcap=None, sinks=None, rows=None) 
     out = np.zeros((batch, c.queries, q.shape[1], head_dim), np.float32)
     for b in rows:
         n = c.lens[b]
-        mask = np.zeros((1, 1, c.queries, smax), bool)
+        causal = np.zeros((1, 1, c.queries, smax), bool)
         for qi in range(c.queries):
-            mask[0, 0, qi, : n - c.queries + qi + 1] = True
-        out[b] = reference_attention(q[b:b + 1], keys[b:b + 1], values[b:b + 1], mask, scale, softcap=softcap,
+            causal[0, 0, qi, : n - c.queries + qi + 1] = True
+        if mask is not None:
+            causal = causal & mask[b if mask.shape[0] > 1 else 0][None, ..., :smax]
+        out[b] = reference_attention(q[b:b + 1], keys[b:b + 1], values[b:b + 1], causal, scale, softcap=softcap,
                                      sinks=sinks)[0]
     return out
 
@@ -310,3 +313,22 @@ def test_softcap_and_sinks() -> None:
     got = kivi_decode_attention(c.q.cuda(), cache, table, seq, max(c.lens), scale=0.2, softcap=4.0,
                                 sinks=torch.from_numpy(sinks).cuda()).float().cpu().numpy()
     np.testing.assert_allclose(got, oracle_output(c, scale=0.2, softcap=4.0, sinks=sinks), atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("kind,queries,hq", [("broadcast", 1, 32), ("per_head", 2, 16), ("per_head", 8, 64)])
+def test_decode_with_a_mask(kind, queries, hq) -> None:
+    """An attention mask (key t = token t of the row) hides keys on top of the causal limit, as the reference's
+    kernels take a mask (attention/_kivi_kernels.py:176-183); with 64 query rows the shared-tile instance runs."""
+    from economize_amd.kivi import kivi_decode_attention
+
+    lens = [1100, 70, 600]
+    c = make_case(3, queries, hq, 8, 128, lens, 4, seed=81 + queries)
+    cache, table = device_cache(c)
+    rng = np.random.default_rng(82)
+    smax = max(lens)
+    shape = (1, 1, 1, smax + 7) if kind == "broadcast" else (3, hq, queries, smax)
+    mask = rng.random(shape) < 0.6
+    seq = torch.tensor(lens, dtype=torch.int32).cuda()
+    got = kivi_decode_attention(c.q.cuda(), cache, table, seq, smax,
+                                mask=torch.from_numpy(mask).cuda()).float().cpu().numpy()
+    np.testing.assert_allclose(got, oracle_output(c, mask=mask), atol=ATOL, rtol=RTOL)

@@ -216,3 +216,43 @@ def test_bad_arguments_raise_before_launch() -> None:
         paged_decode_attention(q, cache, table, lens, 1)
     with pytest.raises(ConfigError):
         paged_decode_attention(torch.zeros(1, 1, 4, 128, device="cuda"), cache, table, lens, 1)  # fp32 query
+
+
+@pytest.mark.parametrize("dtype,kind,queries,hq", [(torch.float8_e4m3fn, "broadcast", 1, 32),
+                                                   (torch.bfloat16, "per_head", 2, 16),
+                                                   (torch.float8_e4m3fn, "per_head", 8, 64)])
+def test_decode_with_a_mask(dtype, kind, queries, hq) -> None:
+    """An attention mask (key t = token t of the row; bool, broadcast or per head) hides keys on top of the causal
+    limit, as the reference's decode_attention takes a mask (attention/decode.py:252-300)."""
+    from oracle.attention import reference_attention
+
+    lens = [700, 90, 1500]
+    c = make_case(3, queries, hq, 8, 128, lens, dtype, seed=77 + queries)
+    rng = np.random.default_rng(78)
+    smax = max(lens)
+    shape = (1, 1, 1, smax + 5) if kind == "broadcast" else (3, hq, queries, smax)
+    mask = rng.random(shape) < 0.6
+    got = _decode(c, mask=torch.from_numpy(mask).cuda())
+    kd, vd = c.decoded()
+    causal = np.zeros((3, 1, queries, smax), bool)
+    for b, n in enumerate(lens):
+        for qi in range(queries):
+            causal[b, 0, qi, : n - queries + qi + 1] = True
+    q = to_numpy_f32(c.q).transpose(0, 2, 1, 3)
+    want = reference_attention(q, kd, vd, causal & mask[..., :smax], 1 / np.sqrt(128))
+    np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
+
+
+def test_mask_bits_pack_the_bool_mask() -> None:
+    """eco_mask_bits: bit t % 32 of word t / 32 is mask[..., t], words past the keys hold zeros."""
+    from economize_amd.paged import packed_mask
+
+    rng = np.random.default_rng(5)
+    mask = rng.random((2, 3, 4, 77)) < 0.5
+    bits, strides, words = packed_mask(torch.from_numpy(mask).cuda(), 2, 3, 4)
+    assert words == 3 and strides == (3 * 4 * 3, 4 * 3, 3)
+    got = bits.cpu().numpy().view(np.uint32)
+    want = np.zeros((2, 3, 4, 3), np.uint32)
+    for t in range(77):
+        want[..., t // 32] |= mask[..., t].astype(np.uint32) << np.uint32(t % 32)
+    assert np.array_equal(got, want)

@@ -206,3 +206,29 @@ def test_planted_workload_selection_matches_the_oracle() -> None:
     lo, hi = oquest.page_bounds(bf16_bits_to_f32(c.k_codes), 0, int(done[0]), page)
     want = oquest.select_pages(q.transpose(0, 2, 1, 3), lo, hi, done, int(done[0]), 63)
     assert np.array_equal(got.cpu().numpy(), want)
+
+
+def test_quest_attention_with_a_mask() -> None:
+    """A mask hides keys of the selected pages and of the tail alike (the reference's Quest kernel reads the mask,
+    attention/_quest_kernels.py:55-87)."""
+    from economize_amd.quest import QuestPages, page_bounds
+
+    lens, page = [3000, 900, 2500], 16
+    c = make_case(3, 1, 32, 8, 128, lens, torch.float8_e4m3fn, seed=43)
+    cache = c.device_cache()
+    table = torch.from_numpy(c.table).cuda()
+    seq = torch.tensor(lens, dtype=torch.int32).cuda()
+    done = np.array([(n - 1) // page for n in lens], np.int32)
+    max_done = int(done.max())
+    kmin, kmax = page_bounds(cache, table, 0, max_done, page)
+    qp = QuestPages(kmin, kmax, torch.from_numpy(done).cuda(), int(done.min()), max_done, page, 63)
+    mask = np.random.default_rng(44).random((3, 1, 1, max(lens))) < 0.7
+    query = c.q.cuda().transpose(1, 2)
+    got = qp.attend(query, cache, table, seq, max(lens), mask=torch.from_numpy(mask).cuda()).float().cpu().numpy()
+    q = to_numpy_f32(c.q).transpose(0, 2, 1, 3)
+    lo, hi = oquest.page_bounds(_stored_keys(c), 0, max_done, page)
+    index = oquest.select_pages(q, lo, hi, done, max_done, 63)
+    kd, vd = c.decoded()
+    visible = (np.arange(kd.shape[2])[None, :] < np.array(lens)[:, None])[:, None, None, :] & mask
+    want = oquest.quest_reference(q, kd, vd, visible, 1 / np.sqrt(128), index, done, page)
+    np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)

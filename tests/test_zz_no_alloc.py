@@ -28,6 +28,7 @@ def _args(case, cache, table, lens, out):
         None, 0, 0, 0, 16, None, None,
         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
         batch, queries, q_heads, cache.kv_heads, head_dim, 16, int(max(case.lens)), 1.0 / math.sqrt(head_dim), 0.0,
+        None, 0, 0, 0, 0,
     ]
 
 
@@ -71,7 +72,7 @@ def test_a_call_beyond_the_scratch_is_refused() -> None:
     lens = torch.tensor(case.lens, dtype=torch.int32, device="cuda")
     out = torch.zeros(tuple(case.q.shape), dtype=torch.bfloat16, device="cuda")
     q, args = _args(case, cache, table, lens, out)
-    args[-3] = 1 << 20  # max_seq_len: a launch sized for a million tokens per row needs more scratch
+    args[-8] = 1 << 20  # max_seq_len: a launch sized for a million tokens per row needs more scratch
     need = _lib.lib().eco_paged_decode_workspace_size(2, 4, 64, 4, 256, 1 << 20, 0, 16, _lib.ECO_BF16)
     assert need > 32 << 20
     with pytest.raises(ConfigError, match="more than the library's"):
