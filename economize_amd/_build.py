@@ -20,7 +20,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIBRARY = HERE / "libeconomize_amd.so"
-SOURCES = ["capi.hip", "paged_attention.hip", "kv_quant.hip", "quest.hip", "kivi.hip", "dense_attention.hip"]
+SOURCES = ["capi.hip", "paged_attention.hip", "kv_quant.hip", "quest.hip", "kivi.hip", "dense_attention.hip", "gather.hip"]
 
 FLAGS = [
     "--offload-arch=gfx950",

@@ -43,6 +43,10 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
     "eco_paged_decode": (c_int32, _PAGED_DECODE),
     "eco_paged_decode_static": (c_int32, _PAGED_ARGS + [_P]),
     "eco_mask_bits": (c_int32, [_P, _L, _L, _L, _L, _I, _I, _I, _I, _P, _I, _P]),
+    "eco_paged_gather": (c_int32, [_P, _P, _I, _I, _P, _P, _P, _L, _I, _P, _P, _I, _L, _L, _L, _L, _L, _L, _I, _I, _I,
+                                   _I, _I, _P]),
+    "eco_kivi_gather": (c_int32, [_P, _I, _P, _P, _I, _P, _P, _P, _L, _I, _P, _P, _I, _L, _L, _L, _L, _L, _L, _I, _I, _I,
+                                  _I, _I, _I, _P]),
     "eco_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I]),
     "eco_decode": (c_int32, [_P, _I, _L, _L, _L, _P, _P, _I, _L, _L, _L, _L, _L, _L, _P, _P, _P, _L, _L, _L, _L, _P, _P,
                              _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P, _S, _P]),

@@ -1,45 +1,54 @@
-"""The ``"economize"`` attention kernel registration and its forward over the paged caches.
+"""The ``"economize"`` attention kernel: its registration, the transformers attention function and ``install``.
 
 Follows attention/registry.py:36-81 (``AttentionKernel``, ``ATTENTION_KERNELS``, ``accepts_fp8_kv``,
-``accepts_packed_kv``) and attention/interface.py:416-499 (``economize_attention_forward`` and the
-``ATTENTION_KERNELS.register("economize", ...)`` call).
+``accepts_packed_kv``) and attention/interface.py:243-525 (``economize_attention_forward`` with its per-call fallback
+reasons, ``kernel_calls`` / ``kernel_usage`` / ``usage_summary``, the registration and ``install``).
 
-The reference's forward receives dense K/V tensors and reads a packed format from an object attached to the key
-(attention/packed.py:61-63). Here the layer's K/V live in a paged cache only, so the ``key`` argument is a
-:class:`PagedKV` handle: the cache, its block table, the row lengths and, for Quest, the page bounds. The forward
-dispatches on its format:
+:func:`economize_attention_forward` takes transformers' arguments: ``query`` ``[B, Hq, Q, D]``, ``key`` / ``value``
+``[B, Hkv, S, D]`` and an optional boolean mask ``[B, 1 or Hq, Q, >= S]``, and returns ``([B, Q, Hq, Dv], None)``.
 
-* ``"fp8"`` / ``"bf16"``: :class:`~economize_amd.paged.PagedKVCache` ->
-  :func:`~economize_amd.paged.paged_decode_attention`;
-* ``"quest"``: a :class:`~economize_amd.paged.PagedKVCache` with :class:`~economize_amd.quest.QuestPages` ->
-  :meth:`~economize_amd.quest.QuestPages.attend` (dense past ``max_queries``, as attention/quest.py:191-204);
-* ``"kivi"``: :class:`~economize_amd.kivi.PagedKIVICache` -> :func:`~economize_amd.kivi.kivi_decode_attention`.
-
-Like the reference's forward it takes the query ``[B, Hq, Q, D]``, the soft cap from ``kwargs["softcap"]`` and the
-sinks from ``kwargs["s_aux"]`` or ``kwargs["sinks"]`` (attention/interface.py:179-184), and returns
-``(out [B, Q, Hq, D], None)``.
+* A key that carries a paged cache's handle (:class:`PagedKV`, attached by :mod:`economize_amd.hf`'s cache; see
+  :mod:`economize_amd.packed`) attends over the paged fp8 / bf16 cache, its Quest pages or the paged KIVI cache on the
+  paged kernels (path ``"kernel_<format>"``).
+* Dense K/V (bf16 / fp16 / fp32, or fp8 views of an fp8 cache) attend on the dense decode kernel
+  (:func:`economize_amd.decode.decode_attention`, path ``"kernel"``).
+* Everything else falls back per call to transformers' ``sdpa`` (a paged cache's K/V materialized by the gather
+  kernels first, fp8 K/V upcast to the query's dtype), or to the model's eager function when the call has sinks or
+  asks for the weights: long queries (prefill), CPU tensors, training with dropout, ``output_attentions``, other
+  dtypes, masks that are not boolean ``[B, 1 or Hq, Q, S]``.
 """
 
 from __future__ import annotations
 
+import sys
 from collections import Counter
 from collections.abc import Callable
 from dataclasses import dataclass
+from typing import TypedDict
 
 import torch
 
+from .decode import FP8_DTYPES, decode_attention
 from .errors import ConfigError
-from .kivi import PagedKIVICache, kivi_decode_attention
-from .paged import PagedKVCache, paged_decode_attention
+from .kivi import PagedKIVICache, kivi_decode_attention, kivi_gather
+from .packed import materialized_kv, packed_of
+from .paged import PagedKVCache, paged_decode_attention, paged_gather
 from .quest import QuestPages
 from .techniques import Registry
 
-__all__ = ["ATTENTION_KERNELS", "AttentionKernel", "PACKED_FORMATS", "PagedKV", "accepts_fp8_kv",
-           "accepts_packed_kv", "economize_attention_forward", "kernel_calls"]
+__all__ = ["ATTENTION_KERNELS", "MAX_QUERIES", "NAME", "PACKED_FORMATS", "AttentionKernel", "PagedKV",
+           "accepts_fp8_kv", "accepts_packed_kv", "economize_attention_forward", "install", "kernel_calls",
+           "kernel_usage", "usage_summary"]
 
-#: Packed formats the ``"economize"`` kernel reads (the reference's set less ``"gathered"``, a dense gather that the
-#: paged page list replaces).
-PACKED_FORMATS = frozenset({"kivi", "quest"})
+#: Name of the implementation in transformers and in :data:`ATTENTION_KERNELS`.
+NAME = "economize"
+#: Longest query (tokens per row) the kernels take; longer ones (prefill) fall back to ``sdpa``.
+MAX_QUERIES = 64
+#: Packed formats the ``"economize"`` kernel reads (the reference's set less ``"gathered"``, eviction's compacted
+#: entries, which this path does not build; plus the paged fp8 / bf16 cache).
+PACKED_FORMATS = frozenset({"kivi", "quest", "fp8", "bf16"})
+
+_DOT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
 
 @dataclass(frozen=True)
@@ -71,7 +80,7 @@ def accepts_packed_kv(implementation: str, fmt: str) -> bool:
 
 @dataclass(frozen=True)
 class PagedKV:
-    """One layer's paged K/V as the forward reads it.
+    """One layer's paged K/V, attached to the key the cache returns (or passed as the key itself).
 
     Attributes:
         cache: A :class:`~economize_amd.paged.PagedKVCache` or :class:`~economize_amd.kivi.PagedKIVICache`.
@@ -79,6 +88,10 @@ class PagedKV:
         seq_lens: int32 ``[B]`` tokens of every row, the queries' own included.
         max_seq_len: Bound of ``seq_lens`` on the host.
         pages: Quest page bounds of a :class:`~economize_amd.paged.PagedKVCache`, or ``None``.
+        dtype: The model's dtype (of the dense view :meth:`materialize` builds).
+        current: For :meth:`materialize`: the dense K/V ``[B, Hkv, T, D]`` of the pass that is writing the last ``T``
+            tokens, when they are to be read as the pass computed them (KIVI quantizes a pass's tokens only at its
+            end), else ``None``.
     """
 
     cache: PagedKVCache | PagedKIVICache
@@ -86,6 +99,8 @@ class PagedKV:
     seq_lens: torch.Tensor
     max_seq_len: int
     pages: QuestPages | None = None
+    dtype: torch.dtype = torch.bfloat16
+    current: tuple[torch.Tensor, torch.Tensor] | None = None
 
     def __post_init__(self) -> None:
         if self.pages is not None and not isinstance(self.cache, PagedKVCache):
@@ -101,49 +116,216 @@ class PagedKV:
             return "quest"
         return "bf16" if self.cache.dtype == torch.bfloat16 else "fp8"
 
+    def attend(self, query: torch.Tensor, key: torch.Tensor | None, value: torch.Tensor | None,
+               mask: torch.Tensor | None, scale: float | None, softcap: float | None = None,
+               sinks: torch.Tensor | None = None) -> torch.Tensor:
+        """``[B, Q, Hq, D]`` bf16 attention of ``query`` ``[B, Hq, Q, D]`` over the paged cache: the ``Q`` queries
+        are the last ``Q`` tokens of every row (causal), and ``mask`` (boolean ``[B or 1, Hq or 1, Q or 1, >= S]``,
+        key ``t`` = token ``t``) hides keys on top."""
+        q = query.transpose(1, 2)
+        if self.format == "kivi":
+            return kivi_decode_attention(q, self.cache, self.block_table, self.seq_lens, self.max_seq_len, scale,
+                                         softcap, sinks, mask=mask)
+        if self.format == "quest":
+            return self.pages.attend(query, self.cache, self.block_table, self.seq_lens, self.max_seq_len, scale,
+                                     softcap, sinks, mask=mask)
+        return paged_decode_attention(q, self.cache, self.block_table, self.seq_lens, self.max_seq_len, scale,
+                                      softcap, sinks, mask=mask)
 
-_calls: Counter = Counter()
+    def materialize(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """The dense K/V ``[B, Hkv, max_seq_len, D]`` the kernels read, in :attr:`dtype` (the gather kernels)."""
+        past = self.max_seq_len - (self.current[0].shape[2] if self.current is not None else 0)
+        gather = kivi_gather if isinstance(self.cache, PagedKIVICache) else paged_gather
+        k, v = gather(self.cache, self.block_table, past if self.current is not None else self.max_seq_len,
+                      self.dtype)
+        if self.current is not None:
+            k = torch.cat([k, self.current[0].to(self.dtype)], dim=2)
+            v = torch.cat([v, self.current[1].to(self.dtype)], dim=2)
+        return k, v
+
+
+# ---- usage log (attention/interface.py:89-137) -------------------------------------------------------------------
+
+
+class UsageRecord(TypedDict):
+    layer: int | None
+    queries: int
+    path: str
+    reason: str
+    calls: int
+
+
+_calls = {"kernel": 0, "fallback": 0}
+_usage: Counter = Counter()
 
 
 def kernel_calls() -> dict[str, int]:
-    """Calls of :func:`economize_attention_forward` by format since the process started."""
+    """How many attention calls ran on the kernels and on the fallback since import."""
     return dict(_calls)
 
 
-def economize_attention_forward(module: torch.nn.Module | None, query: torch.Tensor, key: PagedKV,
-                                value: object = None, attention_mask: torch.Tensor | None = None,
-                                dropout: float = 0.0, scaling: float | None = None, is_causal: bool | None = None,
-                                **kwargs: object) -> tuple[torch.Tensor, None]:
-    """Decode attention of ``query`` ``[B, Hq, Q, D]`` (bf16) over the paged K/V that ``key`` describes; returns
-    ``(out [B, Q, Hq, D] bf16, None)``. The ``Q`` queries are the last ``Q`` tokens of every row and see keys
-    causally. ``value`` is unused (the cache holds both); a mask tensor and dropout are refused, since the paged
-    kernels take visibility from the row lengths."""
-    if not isinstance(key, PagedKV):
-        raise ConfigError("the economize kernel reads a PagedKV handle, not dense K/V tensors")
-    if attention_mask is not None:
-        raise ConfigError("the paged kernels take causal visibility from seq_lens, not an attention mask")
-    if dropout:
-        raise ConfigError("decode attention has no dropout")
+def kernel_usage(reset: bool = False) -> list[UsageRecord]:
+    """Which path each attention call took, grouped by layer, query length and fallback reason."""
+    rows: list[UsageRecord] = [{"layer": layer, "queries": queries, "path": path, "reason": reason, "calls": n}
+                               for (layer, queries, path, reason), n in _usage.items()]
+    rows.sort(key=lambda r: (-1 if r["layer"] is None else r["layer"], r["queries"], r["path"], r["reason"]))
+    if reset:
+        _usage.clear()
+    return rows
+
+
+def usage_summary() -> dict:
+    """Calls per path, per fallback reason, and the query lengths per path."""
+    paths: Counter = Counter()
+    reasons: Counter = Counter()
+    lengths: dict[str, set[int]] = {}
+    for (_, queries, path, reason), n in _usage.items():
+        paths[path] += n
+        if not path.startswith("kernel"):
+            reasons[reason] += n
+        lengths.setdefault(path, set()).add(queries)
+    return {"calls": dict(paths), "fallback_reasons": dict(reasons),
+            "queries": {path: sorted(q) for path, q in lengths.items()}}
+
+
+# ---- the forward ---------------------------------------------------------------------------------------------------
+
+
+def _sinks(kwargs: dict) -> object:
+    return kwargs.get("s_aux") if kwargs.get("s_aux") is not None else kwargs.get("sinks")
+
+
+def _fallback_reason(module, query: torch.Tensor, key, attention_mask, dropout: float, kwargs: dict,
+                     paged: PagedKV | None) -> str | None:
+    """Why this call cannot run on the kernels, or ``None`` when it can; decided per call (interface.py:243-285)."""
+    batch, q_heads, queries, _ = query.shape
+    if not query.is_cuda:
+        return "cpu"
+    if queries > MAX_QUERIES:
+        return "long_query"
+    if dropout > 0.0 and module is not None and module.training:
+        return "dropout"
+    sinks = _sinks(kwargs)
+    if sinks is not None and (not torch.is_tensor(sinks) or sinks.numel() != q_heads):
+        return "sinks"
+    if kwargs.get("output_attentions", False):
+        return "output_attentions"
+    if query.dtype not in _DOT_DTYPES:
+        return "dtype"
+    if paged is not None:
+        if query.dtype != torch.bfloat16:
+            return "dtype"  # the paged kernels take bf16 queries
+        kv_heads = paged.cache.kv_heads
+        if q_heads % kv_heads == 0 and (q_heads // kv_heads) * queries > 64:
+            return "rows"  # the paged kernels take at most 64 query rows per KV head
+    else:
+        if key.dtype != query.dtype and key.dtype not in FP8_DTYPES:
+            return "kv_dtype"
+        kv_heads = key.shape[1]
+    if q_heads % kv_heads:
+        return "heads"
+    if attention_mask is None:
+        return None if queries == 1 or paged is not None else "no_mask"  # the paged kernels are causal by length
+    if not torch.is_tensor(attention_mask) or attention_mask.dtype != torch.bool:
+        return "float_mask"
+    if attention_mask.dim() != 4:
+        return "mask_rank"
+    m_batch, m_heads, m_queries, m_keys = attention_mask.shape
+    if m_batch not in (1, batch) or m_heads not in (1, q_heads) or m_queries not in (1, queries):
+        return "mask_shape"
+    keys = paged.max_seq_len if paged is not None else key.shape[2]
+    if m_keys < keys:
+        return "mask_keys"
+    return None
+
+
+def _eager_function(module, kwargs: dict):
+    """The model's own ``eager_attention_forward`` when the call needs it (sinks, attention weights), which ``sdpa``
+    does not compute (interface.py:194-203)."""
+    if _sinks(kwargs) is None and not kwargs.get("output_attentions", False):
+        return None
+    return getattr(sys.modules.get(type(module).__module__), "eager_attention_forward", None)
+
+
+def _fallback(module, query, key, value, attention_mask, dropout, scaling, is_causal, reason, kwargs):
+    """One call on transformers' ``sdpa`` (or the model's eager function for sinks and weights), over the dense K/V:
+    a paged cache's gathered by its handle, fp8 ones upcast to the query's dtype (interface.py:206-240)."""
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward
+
+    layer = getattr(module, "layer_idx", None)
+    key, value = materialized_kv(key, value)
+    if key.dtype in FP8_DTYPES:
+        key, value = key.to(query.dtype), value.to(query.dtype)
+    if torch.is_tensor(attention_mask) and attention_mask.dim() == 4 and attention_mask.shape[-1] > key.shape[2]:
+        attention_mask = attention_mask[..., : key.shape[2]]
+    _calls["fallback"] += 1
+    eager = _eager_function(module, kwargs)
+    if eager is None:
+        _usage[(layer, query.shape[2], "sdpa", reason)] += 1
+        return sdpa_attention_forward(module, query, key, value, attention_mask, dropout=dropout, scaling=scaling,
+                                      is_causal=is_causal, **kwargs)
+    _usage[(layer, query.shape[2], "eager", reason)] += 1
+    mask = attention_mask
+    if mask is not None and mask.dtype == torch.bool:  # eager functions add the mask to the scores
+        mask = torch.zeros(mask.shape, dtype=query.dtype, device=query.device).masked_fill(
+            ~mask, torch.finfo(query.dtype).min)
+    scale = query.shape[-1] ** -0.5 if scaling is None else scaling
+    return eager(module, query, key, value, mask, scaling=scale, dropout=dropout, **kwargs)
+
+
+def economize_attention_forward(module: torch.nn.Module | None, query: torch.Tensor, key, value,
+                                attention_mask: torch.Tensor | None, dropout: float = 0.0,
+                                scaling: float | None = None, is_causal: bool | None = None,
+                                **kwargs: object) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """transformers attention function (``[B, Hq, Q, D]`` in, ``[B, Q, Hq, Dv]`` out) on the MI355X kernels
+    (interface.py:416-480); the kernel or the fallback is chosen for every call, and :func:`kernel_usage` logs it.
+    ``key`` may also be a :class:`PagedKV` itself (then ``value`` is unused)."""
     if query.dim() != 4:
         raise ConfigError(f"query must be [B, Hq, Q, D], got {tuple(query.shape)}")
+    paged = key if isinstance(key, PagedKV) else packed_of(key)
+    if paged is not None and not isinstance(paged, PagedKV):
+        paged = None
+    layer = getattr(module, "layer_idx", None)
+    queries = query.shape[2]
+    reason = _fallback_reason(module, query, key, attention_mask, dropout, kwargs, paged)
+    if reason is not None:
+        if isinstance(key, PagedKV):
+            raise ConfigError(f"a bare PagedKV handle cannot fall back ({reason}); attach it to dense stand-ins")
+        return _fallback(module, query, key, value, attention_mask, dropout, scaling, is_causal, reason, kwargs)
+    scale = query.shape[-1] ** -0.5 if scaling is None else scaling
     softcap = kwargs.get("softcap")
-    sinks = kwargs.get("s_aux") if kwargs.get("s_aux") is not None else kwargs.get("sinks")
-    fmt = key.format
-    if fmt == "kivi":
-        out = kivi_decode_attention(query.transpose(1, 2), key.cache, key.block_table, key.seq_lens, key.max_seq_len,
-                                    scaling, softcap, sinks)
-    elif fmt == "quest":
-        out = key.pages.attend(query, key.cache, key.block_table, key.seq_lens, key.max_seq_len, scaling, softcap,
-                               sinks)
+    sinks = _sinks(kwargs)
+    if paged is not None:
+        out = paged.attend(query, key, value, attention_mask, scale, softcap, sinks)
+        path = f"kernel_{paged.format}"
     else:
-        out = paged_decode_attention(query.transpose(1, 2), key.cache, key.block_table, key.seq_lens,
-                                     key.max_seq_len, scaling, softcap, sinks)
-    _calls[fmt] += 1
+        if attention_mask is not None and attention_mask.shape[-1] != key.shape[2]:
+            attention_mask = attention_mask[..., : key.shape[2]]
+        out = decode_attention(query, key, value, attention_mask, scale, softcap=softcap, sinks=sinks)
+        path = "kernel"
+    _calls["kernel"] += 1
+    _usage[(layer, queries, path, "")] += 1
     return out, None
 
 
-ATTENTION_KERNELS.register("economize", AttentionKernel(
+ATTENTION_KERNELS.register(NAME, AttentionKernel(
     family="sdpa", forward=economize_attention_forward,
-    description="MI355X decode attention over paged fp8 / bf16 / KIVI caches, with Quest page selection",
-    fp8_kv=True, packed_kv=PACKED_FORMATS,
+    description="MI355X decode attention: dense bf16/fp16/fp32/fp8 K/V with masks, paged fp8/bf16 and KIVI caches, "
+                "Quest pages",
+    fp8_kv=True, packed_kv=PACKED_FORMATS, structured_masks=False,
 ))
+
+
+def install(name: str | None = None) -> list[str]:
+    """Register the attention kernels with transformers (``AttentionInterface`` and ``AttentionMaskInterface``,
+    interface.py:502-525); afterwards ``attn_implementation="economize"`` selects the kernel. Idempotent."""
+    from transformers import AttentionInterface
+    from transformers.masking_utils import AttentionMaskInterface
+
+    names = [name] if name is not None else ATTENTION_KERNELS.names()
+    for each in names:
+        entry = ATTENTION_KERNELS.get_entry(each)
+        AttentionInterface.register(each, entry.forward)
+        mask = entry.mask_function or AttentionMaskInterface._global_mapping[entry.family]
+        AttentionMaskInterface.register(each, mask)
+    return names

@@ -10,6 +10,7 @@
 #include "../../include/economize_amd.h"
 #include "common.hpp"
 #include "dense_attention.hpp"
+#include "gather.hpp"
 #include "kivi.hpp"
 #include "kv_quant.hpp"
 #include "paged_attention.hpp"
@@ -528,6 +529,95 @@ int eco_mask_bits(const uint8_t* mask, int64_t sm_b, int64_t sm_h, int64_t sm_q,
     hipLaunchKernelGGL(mask_bits_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), mask, sm_b,
                        sm_h, sm_q, sm_s, batch, heads, queries, keys, bits, words);
     return check_launch("mask_bits_kernel");
+}
+
+int eco_paged_gather(const void* k_cache, const void* v_cache, int32_t kv_format, int32_t num_pages,
+                     const float* k_scale, const float* v_scale, const int32_t* block_table, int64_t bt_stride,
+                     int32_t bt_cols, void* k_out, void* v_out, int32_t out_format, int64_t so_kb, int64_t so_kh,
+                     int64_t so_ks, int64_t so_vb, int64_t so_vh, int64_t so_vs, int32_t batch, int32_t kv_heads,
+                     int32_t keys, int32_t head_dim, int32_t page_size, void* stream) {
+    if (!k_cache || !v_cache || !block_table || !k_out || !v_out) return fail("paged gather: null pointer");
+    if (batch <= 0 || kv_heads <= 0 || keys < 0 || num_pages <= 0 || bt_cols <= 0 || bt_stride < bt_cols)
+        return fail("paged gather: sizes must be positive");
+    if (page_size != 16) return fail("paged gather: pages must hold 16 tokens");
+    if (kv_format != BF16 && kv_format != FP8_E4M3 && kv_format != FP8_E5M2)
+        return fail("paged gather: the cache must be bf16, fp8 e4m3 or fp8 e5m2");
+    if (out_format != BF16 && out_format != FP16 && out_format != FP32)
+        return fail("paged gather: the output must be bf16, fp16 or fp32");
+    if (head_dim <= 0 || head_dim % 16) return fail("paged gather: head dim must be a positive multiple of 16");
+    const int es = kv_format == BF16 ? 2 : 1;
+    PagedGatherParams p{};
+    p.k_cache = static_cast<const uint8_t*>(k_cache);
+    p.v_cache = static_cast<const uint8_t*>(v_cache);
+    p.kc_head = static_cast<int64_t>(head_dim) * 16 * es;
+    p.kc_page = p.kc_head * kv_heads;
+    p.vc_head = p.kc_head;
+    p.vc_page = p.kc_page;
+    p.kv_format = kv_format;
+    p.k_scale = k_scale;
+    p.v_scale = v_scale;
+    p.block_table = block_table;
+    p.bt_stride = bt_stride;
+    p.bt_cols = bt_cols;
+    p.num_pages = num_pages;
+    p.k_out = k_out;
+    p.v_out = v_out;
+    p.so_kb = so_kb;
+    p.so_kh = so_kh;
+    p.so_ks = so_ks;
+    p.so_vb = so_vb;
+    p.so_vh = so_vh;
+    p.so_vs = so_vs;
+    p.out_format = out_format;
+    p.batch = batch;
+    p.kv_heads = kv_heads;
+    p.keys = keys;
+    p.head_dim = head_dim;
+    return paged_gather(p, static_cast<hipStream_t>(stream));
+}
+
+int eco_kivi_gather(const void* blocks, int32_t num_pages, const void* k_ring, const void* v_ring, int32_t ring,
+                    const int32_t* keys_quantized, const int32_t* values_quantized, const int32_t* block_table,
+                    int64_t bt_stride, int32_t bt_cols, void* k_out, void* v_out, int32_t out_format, int64_t so_kb,
+                    int64_t so_kh, int64_t so_ks, int64_t so_vb, int64_t so_vh, int64_t so_vs, int32_t batch,
+                    int32_t kv_heads, int32_t keys, int32_t head_dim, int32_t bits, int32_t group, void* stream) {
+    if (!blocks || !k_ring || !v_ring || !keys_quantized || !values_quantized || !block_table || !k_out || !v_out)
+        return fail("kivi gather: null pointer");
+    if (batch <= 0 || kv_heads <= 0 || keys < 0 || num_pages <= 0 || bt_cols <= 0 || bt_stride < bt_cols)
+        return fail("kivi gather: sizes must be positive");
+    if (int rc = check_kivi_shape(head_dim, bits, group)) return rc;
+    if (ring <= 0 || ring % 32) return fail("kivi gather: the ring must hold a positive multiple of 32 slots");
+    if (out_format != BF16 && out_format != FP16 && out_format != FP32)
+        return fail("kivi gather: the output must be bf16, fp16 or fp32");
+    const KiviLayout L{head_dim, bits};
+    KiviGatherParams p{};
+    p.blocks = static_cast<const uint8_t*>(blocks);
+    p.blk_head = L.size();
+    p.blk_page = static_cast<int64_t>(L.size()) * kv_heads;
+    p.k_ring = static_cast<const uint16_t*>(k_ring);
+    p.v_ring = static_cast<const uint16_t*>(v_ring);
+    p.ring = ring;
+    p.keys_quantized = keys_quantized;
+    p.values_quantized = values_quantized;
+    p.block_table = block_table;
+    p.bt_stride = bt_stride;
+    p.bt_cols = bt_cols;
+    p.num_pages = num_pages;
+    p.k_out = k_out;
+    p.v_out = v_out;
+    p.so_kb = so_kb;
+    p.so_kh = so_kh;
+    p.so_ks = so_ks;
+    p.so_vb = so_vb;
+    p.so_vh = so_vh;
+    p.so_vs = so_vs;
+    p.out_format = out_format;
+    p.batch = batch;
+    p.kv_heads = kv_heads;
+    p.keys = keys;
+    p.head_dim = head_dim;
+    p.bits = bits;
+    return kivi_gather(p, static_cast<hipStream_t>(stream));
 }
 
 size_t eco_kivi_block_bytes(int32_t head_dim, int32_t bits, int32_t group) {

@@ -1,0 +1,379 @@
+"""The Hugging Face drop-in of the compressed-KV path: ``apply`` attaches the techniques to a transformers causal LM
+and :class:`EconomizeCache` is its ``past_key_values``, whose layers live in the paged MI355X caches.
+
+Mirrors the reference's cache wrappers (techniques/_kv/wrapper.py:122-351: ``transform_update`` what is written for
+new K/V, ``transform_read`` what attention sees, ``pass_begin`` / ``pass_end`` at the boundaries of an exact pass)
+for the techniques of this path:
+
+* ``FP8KVConfig`` / ``FusedFP8KVConfig``: K/V encoded to fp8 on write into a paged fp8 cache (``fp8_encode``,
+  techniques/kv_quant/fp8.py:81-86 and 161-176); attention reads the bytes on the paged kernel
+  (kv_fp8_fused/fused.py:56-63 hands fp8 views over).
+* ``KIVIConfig`` / ``FusedKIVIConfig``: new tokens in the bf16 ring, the reference's schedule run at every pass
+  boundary (the tokens a pass commits are quantized when it ends, kivi.py:191-243), attention on the fused KIVI
+  kernel over codes and ring (kv_kivi_fused/fused.py:152-208).
+* ``QuestConfig``: a paged cache (fp8 with an fp8 technique on the same layer is refused, as the reference refuses
+  Quest over packed formats) whose page bounds are kept for the committed pages, ``done[b]`` = committed full pages
+  before the pass; a decoding query of a covered layer reads the selected pages and the tail
+  (quest/technique.py:116-259).
+
+A layer of no technique keeps dense K/V (transformers' ``DynamicLayer``) and attends on the dense kernel.
+
+transformers calls the cache's ``update`` once per layer and pass, with no pass boundaries; a pass's boundary is
+therefore taken at the next pass's first write of a layer: a layer's ``pass_begin`` runs when the layer is written
+with a new frontier (its committed length grows), before the write, which is when the reference's ``pass_end`` of the
+previous pass has taken effect for every later read.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+from transformers.cache_utils import Cache, CacheLayerMixin, DynamicLayer
+
+from .attention import MAX_QUERIES, NAME, PagedKV, install
+from .errors import ConfigError, IncompatibleTechniquesError
+from .kivi import KIVI_PAGE, PagedKIVICache, kivi_append, kivi_commit, kivi_quantize
+from .packed import attach_packed, stand_in
+from .paged import PAGE, PagedKVCache, paged_append
+from .quest import QuestPages, page_bounds
+from .techniques import (FP8KVConfig, KIVIConfig, QuestConfig, Technique, attn_implementation, head_dim_of,
+                         technique_for)
+
+__all__ = ["EconomizeCache", "EconomizedModel", "KIVILayer", "PagedLayer", "apply"]
+
+
+class _PagedBase(CacheLayerMixin):
+    """The part every paged layer shares: rows of equal length (transformers' positions), a block table in which
+    row ``b`` owns pages ``b * P .. b * P + P - 1``, the length written so far and the committed length (the
+    frontier of the last pass)."""
+
+    is_sliding = False
+    is_compileable = False
+    supports_early_init = False
+
+    def __init__(self, capacity: int, page: int) -> None:
+        super().__init__()
+        self.capacity = int(capacity)
+        self.page = page
+        self.length = 0
+        self.committed = 0
+        self.model_dtype = torch.bfloat16
+        self.table: torch.Tensor | None = None
+        self._lens: dict[int, torch.Tensor] = {}
+
+    def _allocate_table(self, batch: int, device: torch.device) -> int:
+        per_row = -(-self.capacity // self.page)
+        self.table = torch.arange(batch * per_row, dtype=torch.int32, device=device).view(batch, per_row)
+        return batch * per_row
+
+    def _seq_lens(self) -> torch.Tensor:
+        lens = self._lens.get(self.length)
+        if lens is None:
+            self._lens = {self.length: torch.full((self.table.shape[0],), self.length, dtype=torch.int32,
+                                                  device=self.table.device)}
+            lens = self._lens[self.length]
+        return lens
+
+    def _check_room(self, tokens: int) -> None:
+        if self.length + tokens > self.capacity:
+            raise ConfigError(f"the cache holds {self.capacity} tokens per row; writing {tokens} more after "
+                              f"{self.length} exceeds it (make the cache with a larger max_length)")
+
+    def _stand_ins(self, key_states: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        batch, heads, _, dim = key_states.shape
+        shape = (batch, heads, self.length, dim)
+        return stand_in(shape, self.model_dtype, key_states.device), stand_in(shape, self.model_dtype,
+                                                                              key_states.device)
+
+    # ---- transformers' layer API -----------------------------------------------------------------------------------
+    def get_seq_length(self) -> int:
+        return self.length
+
+    def get_mask_sizes(self, query_length: int) -> tuple[int, int]:
+        return self.length + query_length, 0
+
+    def get_max_length(self) -> int:
+        return self.capacity
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs
+               ) -> tuple[torch.Tensor, torch.Tensor]:
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        if self.length > self.committed:
+            self.pass_begin(self.length)
+        key_states, value_states = self.transform_update(key_states, value_states)
+        return self.transform_read(key_states, value_states)
+
+    # ---- the cache-wrapper hooks -----------------------------------------------------------------------------------
+    def pass_begin(self, frontier: int) -> None:
+        """A new exact pass starts writing at ``frontier``: every token below it is committed."""
+        self.committed = frontier
+
+    def transform_update(self, key_states, value_states):
+        raise NotImplementedError
+
+    def transform_read(self, key_states, value_states):
+        raise NotImplementedError
+
+    def reset(self) -> None:
+        self.length = self.committed = 0
+
+
+class PagedLayer(_PagedBase):
+    """One layer in a paged fp8 or bf16 cache (16-token pages), optionally with Quest's page bounds."""
+
+    def __init__(self, capacity: int, cache_dtype: torch.dtype | None, quest: QuestConfig | None = None) -> None:
+        super().__init__(capacity, PAGE)
+        self.cache_dtype = cache_dtype  # None: the model's dtype (bf16)
+        self.quest = quest
+        self.cache: PagedKVCache | None = None
+        self.bounds: tuple[torch.Tensor, torch.Tensor] | None = None
+        self.valid = 0  # Quest pages whose bounds are final
+        self._write_width = 0
+
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        batch, heads, _, dim = key_states.shape
+        self.model_dtype = key_states.dtype
+        dtype = self.cache_dtype or torch.bfloat16
+        pages = self._allocate_table(batch, key_states.device)
+        self.cache = PagedKVCache.empty(pages, heads, dim, dtype, key_states.device)
+        if self.quest is not None:
+            shape = (batch, heads, -(-self.capacity // self.quest.page_size), dim)
+            self.bounds = (torch.zeros(shape, dtype=torch.bfloat16, device=key_states.device),
+                           torch.zeros(shape, dtype=torch.bfloat16, device=key_states.device))
+        self.is_initialized = True
+
+    def transform_update(self, key_states, value_states):
+        """fp8_encode (or the bf16 rounding) of the new tokens into their pages, at positions ``length ..``."""
+        batch, heads, tokens, dim = key_states.shape
+        self._check_room(tokens)
+        pos = torch.arange(self.length, self.length + tokens, device=key_states.device)
+        slots = (self.table[:, pos // PAGE] * PAGE + pos % PAGE).to(torch.int32).reshape(-1)
+        paged_append(self.cache, key_states.transpose(1, 2).reshape(batch * tokens, heads, dim),
+                     value_states.transpose(1, 2).reshape(batch * tokens, heads, dim), slots)
+        self.length += tokens
+        self._write_width = tokens
+        return key_states, value_states
+
+    def transform_read(self, key_states, value_states):
+        """Stand-ins for the dense K/V with the paged handle attached; a decoding query of a Quest layer also gets
+        the page bounds of the committed pages (attached only when ``max(done) > pages``, as the reference)."""
+        pages = None
+        q = self.quest
+        if q is not None and self._write_width <= q.max_queries:
+            done = self.committed // q.page_size
+            if done > q.pages:
+                if self.valid < done:
+                    page_bounds(self.cache, self.table, self.valid, done, q.page_size, out=self.bounds)
+                    self.valid = done
+                done_t = torch.full((self.table.shape[0],), done, dtype=torch.int32, device=self.table.device)
+                pages = QuestPages(self.bounds[0], self.bounds[1], done_t, done, done, q.page_size, q.pages,
+                                   q.max_queries)
+        handle = PagedKV(self.cache, self.table, self._seq_lens(), self.length, pages, self.model_dtype)
+        keys, values = self._stand_ins(key_states)
+        return attach_packed(keys, handle), values
+
+    def reset(self) -> None:
+        super().reset()
+        self.valid = 0
+
+
+class KIVILayer(_PagedBase):
+    """One layer in the paged KIVI cache (32-token pages) with its bf16 ring of ``residual + headroom`` slots.
+
+    A pass of at most ``headroom`` tokens writes them to the ring; what it commits is quantized from the ring when
+    the next pass begins (the reference's ``kivi_commit`` at a pass boundary). A longer pass (a prompt) cannot leave
+    its tokens in the ring: what the schedule quantizes at its end is quantized as it writes, from the ring's
+    unquantized past and the pass's own K/V, and the pass itself reads its tokens as it computed them (the dense view
+    its attention falls back to, such a query being longer than the kernels take).
+    """
+
+    def __init__(self, capacity: int, config: KIVIConfig) -> None:
+        super().__init__(capacity, KIVI_PAGE)
+        if config.headroom < MAX_QUERIES:
+            raise ConfigError(f"the paged KIVI layer needs headroom >= {MAX_QUERIES} (a decoding pass's tokens stay in "
+                              f"the ring until the pass ends), got {config.headroom}")
+        self.config = config
+        self.cache: PagedKIVICache | None = None
+        self.kq = 0  # quantized keys / values of every row (the device counts' host mirror)
+        self.vq = 0
+        self._current: tuple[torch.Tensor, torch.Tensor] | None = None
+
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        batch, heads, _, dim = key_states.shape
+        if key_states.dtype != torch.bfloat16:
+            raise ConfigError(f"the paged KIVI cache takes a bf16 model, not {key_states.dtype}")
+        self.model_dtype = key_states.dtype
+        pages = self._allocate_table(batch, key_states.device)
+        c = self.config
+        self.cache = PagedKIVICache.empty(pages, batch, heads, dim, c.bits, key_states.device, group=c.group_size,
+                                          residual=c.residual_length, headroom=c.headroom)
+        self.is_initialized = True
+
+    def _schedule(self, committed: int) -> tuple[int, int]:
+        r = self.config.residual_length
+        return max(self.kq, (committed // r) * r), max(self.vq, committed - r)
+
+    def pass_begin(self, frontier: int) -> None:
+        """The previous pass ended: quantize what it committed (kivi.py:230-243), from the ring."""
+        if frontier > self.committed:
+            batch = self.table.shape[0]
+            committed = torch.full((batch,), frontier, dtype=torch.int32, device=self.table.device)
+            kivi_commit(self.cache, self.table, committed, frontier - self.committed)
+            self.kq, self.vq = self._schedule(frontier)
+        super().pass_begin(frontier)
+
+    def _quantize_pass(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        """Quantize what the schedule quantizes at the end of this long pass, from the ring's past tokens that are
+        not quantized yet (below the pass) and the pass's own K/V."""
+        from .kivi import kivi_gather
+
+        batch, heads, tokens, dim = key_states.shape
+        start = self.length
+        kq, vq = self._schedule(start + tokens)
+        lo = min(self.kq, self.vq)
+        k_src, v_src = key_states, value_states
+        if lo < start:  # at most residual + headroom tokens of the past, all in the ring
+            past_k, past_v = kivi_gather(self.cache, self.table, start, torch.bfloat16)
+            k_src = torch.cat([past_k[:, :, lo:], key_states], dim=2)
+            v_src = torch.cat([past_v[:, :, lo:], value_states], dim=2)
+        k_src, v_src = k_src.contiguous(), v_src.contiguous()
+        device = key_states.device
+
+        def rows(x: int) -> torch.Tensor:
+            return torch.full((batch,), x, dtype=torch.int32, device=device)
+
+        if kq > self.kq:
+            kivi_quantize(self.cache, self.table, k_src, "k", rows(self.kq), rows(kq), kq - self.kq, source_start=lo)
+        if vq > self.vq:
+            kivi_quantize(self.cache, self.table, v_src, "v", rows(self.vq), rows(vq), vq - self.vq, source_start=lo)
+        self.kq, self.vq = kq, vq
+        self.committed = start + tokens  # this pass's boundary is done
+
+    def transform_update(self, key_states, value_states):
+        """The new tokens into the ring (the last ``ring`` of a longer pass); a pass longer than the headroom is
+        quantized as it writes (:meth:`_quantize_pass`)."""
+        batch, heads, tokens, dim = key_states.shape
+        self._check_room(tokens)
+        start = self.length
+        device = key_states.device
+        ring = self.cache.ring
+        self._current = None
+        if tokens > self.config.headroom:
+            self._quantize_pass(key_states, value_states)
+            self._current = (key_states, value_states)
+        first = max(0, tokens - ring)
+        width = tokens - first
+        rows = torch.arange(batch, dtype=torch.int32, device=device).repeat_interleave(width)
+        pos = torch.arange(start + first, start + tokens, dtype=torch.int32, device=device).repeat(batch)
+        kivi_append(self.cache, key_states[:, :, first:].transpose(1, 2).reshape(batch * width, heads, dim),
+                    value_states[:, :, first:].transpose(1, 2).reshape(batch * width, heads, dim), rows, pos)
+        self.length += tokens
+        self.cache.keys_quantized.fill_(self.kq)
+        self.cache.values_quantized.fill_(self.vq)
+        return key_states, value_states
+
+    def transform_read(self, key_states, value_states):
+        handle = PagedKV(self.cache, self.table, self._seq_lens(), self.length, None, self.model_dtype,
+                         self._current)
+        keys, values = self._stand_ins(key_states)
+        return attach_packed(keys, handle), values
+
+    def reset(self) -> None:
+        super().reset()
+        self.kq = self.vq = 0
+
+
+class EconomizeCache(Cache):
+    """transformers ``past_key_values`` whose layers are the techniques' paged caches (dense ``DynamicLayer`` for a
+    layer no technique covers)."""
+
+    def __init__(self, layers: list[CacheLayerMixin]) -> None:
+        super().__init__(layers=layers)
+
+    def check_flags(self) -> None:
+        """The reference's pass-boundary refusal of KIVI scales beyond fp16 (packed.py:175-188), for every layer."""
+        for layer in self.layers:
+            if isinstance(layer, KIVILayer) and layer.cache is not None:
+                layer.cache.check_flags()
+
+
+@dataclass
+class EconomizedModel:
+    """A transformers causal LM with the compressed-KV techniques attached (the reference's ``apply`` result,
+    core/model.py:330-386, limited to this path): :meth:`make_cache` builds the ``past_key_values`` that hold its
+    layers in the techniques' paged caches.
+
+    Attributes:
+        model: The transformers model (its attention implementation set to ``"economize"``).
+        techniques: The attached techniques, in attach order.
+    """
+
+    model: torch.nn.Module
+    techniques: list[Technique] = field(default_factory=list)
+
+    def technique_of(self, layer: int) -> Technique | None:
+        """The technique covering 1-indexed ``layer`` (at most one per layer)."""
+        for technique in self.techniques:
+            if technique.covers(layer):
+                return technique
+        return None
+
+    def make_cache(self, max_length: int) -> EconomizeCache:
+        """A cache for generations of up to ``max_length`` tokens per row (prompt included)."""
+        config = self.model.config
+        layers: list[CacheLayerMixin] = []
+        for index in range(config.num_hidden_layers):
+            technique = self.technique_of(index + 1)
+            cfg = technique.config if technique is not None else None
+            if isinstance(cfg, KIVIConfig):
+                layers.append(KIVILayer(max_length, cfg))
+            elif isinstance(cfg, FP8KVConfig):
+                layers.append(PagedLayer(max_length, cfg.dtype))
+            elif isinstance(cfg, QuestConfig):
+                layers.append(PagedLayer(max_length, None, cfg))
+            else:
+                layers.append(DynamicLayer())
+        return EconomizeCache(layers)
+
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int, **kwargs) -> torch.Tensor:
+        """transformers' ``generate`` with a fresh :class:`EconomizeCache` (greedy unless ``kwargs`` say otherwise)."""
+        cache = self.make_cache(input_ids.shape[1] + max_new_tokens)
+        kwargs.setdefault("do_sample", False)
+        return self.model.generate(input_ids, past_key_values=cache, max_new_tokens=max_new_tokens, **kwargs)
+
+
+def apply(model: torch.nn.Module, *configs) -> EconomizedModel:
+    """Attach the techniques of ``configs`` to a transformers causal LM (core/model.py:330-356): registers the
+    ``"economize"`` kernel (:func:`~economize_amd.attention.install`), selects it as the model's attention
+    implementation, validates every configuration against the model before anything attaches
+    (``config.validate(model)``), and refuses two techniques on one layer.
+
+    Raises:
+        ConfigError: A configuration the MI355X path cannot run on this model.
+        IncompatibleTechniquesError: Two techniques cover one layer, or a technique twice.
+    """
+    install()
+    if hasattr(model, "set_attn_implementation"):
+        model.set_attn_implementation(NAME)
+    else:
+        model.config._attn_implementation = NAME
+    if attn_implementation(model) != NAME:
+        raise ConfigError(f"could not select the {NAME!r} attention implementation on {type(model).__name__}")
+    if head_dim_of(model) is None:
+        raise ConfigError(f"{type(model).__name__} has no attention head dimension in its config")
+    techniques: list[Technique] = []
+    for config in configs:
+        if any(type(t.config) is type(config) for t in techniques):
+            raise IncompatibleTechniquesError(f"{config.technique} is applied twice")
+        config.validate(model)
+        if isinstance(config, FP8KVConfig) and config.scale == "head":
+            raise ConfigError("scale='head' needs calibrated per-head scales (economize_amd.paged.head_scales); the "
+                              "generation cache takes scale='none'")
+        techniques.append(technique_for(config))
+    for layer in range(1, model.config.num_hidden_layers + 1):
+        covering = [t.config.technique for t in techniques if t.covers(layer)]
+        if len(covering) > 1:
+            raise IncompatibleTechniquesError(f"layer {layer} is covered by {covering}; one KV technique per layer")
+    return EconomizedModel(model, techniques)

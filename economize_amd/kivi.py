@@ -24,7 +24,8 @@ from . import _lib
 from .errors import ConfigError
 from .paged import cached_workspace, counter_bytes, packed_mask
 
-__all__ = ["KIVI_PAGE", "PagedKIVICache", "kivi_append", "kivi_commit", "kivi_decode_attention", "kivi_quantize"]
+__all__ = ["KIVI_PAGE", "PagedKIVICache", "kivi_append", "kivi_commit", "kivi_decode_attention", "kivi_gather",
+           "kivi_quantize"]
 
 #: Tokens per KIVI page.
 KIVI_PAGE = 32
@@ -251,3 +252,24 @@ def kivi_decode_attention(query: torch.Tensor, cache: PagedKIVICache, block_tabl
         _lib.stream_of(device),
     )
     return out
+
+
+def kivi_gather(cache: PagedKIVICache, block_table: torch.Tensor, keys: int, dtype: torch.dtype = torch.bfloat16
+                ) -> tuple[torch.Tensor, torch.Tensor]:
+    """The dense view ``[B, Hkv, keys, D]`` of the first ``keys`` tokens of every row: codes dequantized as the
+    reference's ``dequantize`` (bf16 of ``code * scale + zero``), the rest from the rings (``KIVIPacked``'s
+    materialize, attention/packed.py:66-78). The rings hold the last ``ring`` tokens of a row only."""
+    cache.check()
+    _table(block_table, cache.batch)
+    device = _lib.require_gpu(block_table, cache.blocks)
+    shape = (cache.batch, cache.kv_heads, int(keys), cache.head_dim)
+    k = torch.empty(shape, dtype=dtype, device=device)
+    v = torch.empty(shape, dtype=dtype, device=device)
+    if keys > 0:
+        _lib.call("eco_kivi_gather", cache.blocks.data_ptr(), cache.num_pages, cache.k_ring.data_ptr(),
+                  cache.v_ring.data_ptr(), cache.ring, cache.keys_quantized.data_ptr(),
+                  cache.values_quantized.data_ptr(), block_table.data_ptr(), block_table.stride(0),
+                  block_table.shape[1], k.data_ptr(), v.data_ptr(), _lib.fmt(dtype), *k.stride()[:3],
+                  *v.stride()[:3], cache.batch, cache.kv_heads, int(keys), cache.head_dim, cache.bits, cache.group,
+                  _lib.stream_of(device))
+    return k, v

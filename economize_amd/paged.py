@@ -23,7 +23,8 @@ from . import _lib
 from .errors import ConfigError
 
 __all__ = [
-    "PAGE", "PagedKVCache", "head_scales", "new_workspace", "paged_append", "paged_decode_attention", "workspace_size",
+    "PAGE", "PagedKVCache", "head_scales", "new_workspace", "packed_mask", "paged_append", "paged_decode_attention",
+    "paged_gather", "workspace_size",
 ]
 
 #: Tokens per page.
@@ -288,3 +289,25 @@ def paged_decode_attention(
         _lib.ptr(bits), *mk, words, workspace.data_ptr(), workspace.numel(), _lib.stream_of(device),
     )
     return out
+
+
+def paged_gather(cache: PagedKVCache, block_table: torch.Tensor, keys: int, dtype: torch.dtype = torch.bfloat16
+                 ) -> tuple[torch.Tensor, torch.Tensor]:
+    """The dense view ``[B, Hkv, keys, D]`` (``dtype``: bf16, fp16 or fp32) of the first ``keys`` tokens of every
+    row: fp8 decoded exactly and times the per-head scales, 0 past a row's table (``materialize()`` of
+    attention/packed.py:66-78 for this cache)."""
+    cache.check()
+    device = _lib.require_gpu(cache.keys, block_table)
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1:
+        raise ConfigError("block_table must be int32 [B, pages] with contiguous rows")
+    batch = block_table.shape[0]
+    shape = (batch, cache.kv_heads, int(keys), cache.head_dim)
+    k = torch.empty(shape, dtype=dtype, device=device)
+    v = torch.empty(shape, dtype=dtype, device=device)
+    if keys > 0:
+        _lib.call("eco_paged_gather", cache.keys.data_ptr(), cache.values.data_ptr(), _lib.fmt(cache.dtype),
+                  cache.num_pages, _lib.ptr(cache.k_scale), _lib.ptr(cache.v_scale), block_table.data_ptr(),
+                  block_table.stride(0), block_table.shape[1], k.data_ptr(), v.data_ptr(), _lib.fmt(dtype),
+                  *k.stride()[:3], *v.stride()[:3], batch, cache.kv_heads, int(keys), cache.head_dim, PAGE,
+                  _lib.stream_of(device))
+    return k, v

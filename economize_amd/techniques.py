@@ -50,6 +50,32 @@ def _layers(layers) -> None:
         raise ConfigError(f"layers are 1-indexed, got {layers!r}")
 
 
+def attn_implementation(adapter) -> str:
+    """The attention implementation a model runs: ``adapter`` is a model adapter, a transformers model or its config
+    (whatever carries ``config._attn_implementation``, as the reference's ``validate(adapter)`` reads it), or the
+    implementation's name."""
+    if isinstance(adapter, str):
+        return adapter
+    config = getattr(adapter, "config", adapter)
+    return str(getattr(config, "_attn_implementation", None) or "eager")
+
+
+def head_dim_of(adapter) -> int | None:
+    """The attention head dimension of a model (``head_dim``, else ``hidden_size / num_attention_heads``), or
+    ``None`` when ``adapter`` names no model."""
+    config = getattr(adapter, "config", adapter)
+    dim = getattr(config, "head_dim", None)
+    if dim is None and getattr(config, "hidden_size", None) and getattr(config, "num_attention_heads", None):
+        dim = config.hidden_size // config.num_attention_heads
+    return int(dim) if dim else None
+
+
+def _head_dims(technique: str, adapter, dims: tuple[int, ...]) -> None:
+    dim = head_dim_of(adapter)
+    if dim is not None and dim not in dims:
+        raise ConfigError(f"{technique}: the MI355X kernels take head dims {list(dims)}, the model has {dim}")
+
+
 def _needs_kernel(technique: str, implementation: str, accepts, what: str, instead: str | None) -> None:
     """Refuses an attention implementation that cannot read the technique's cache (fused.py:44-49)."""
     from .attention import ATTENTION_KERNELS
@@ -134,6 +160,14 @@ class FP8KVConfig(TechniqueConfig):
     def dtype(self) -> torch.dtype:
         return FP8_FORMATS[self.format]
 
+    def validate(self, adapter) -> None:
+        """Refuses, before anything attaches, what the paged fp8 cache cannot hold: per-token and per-tensor scales
+        (it keeps per-head scales) and head dims the kernels do not take."""
+        if self.scale in ("token", "tensor"):
+            raise ConfigError(f"the paged fp8 cache stores per-head scales, not scale={self.scale!r}; use 'none' or "
+                              "'head'")
+        _head_dims(self.technique, adapter, (64, 128, 256))
+
 
 @dataclass(frozen=True)
 class FusedFP8KVConfig(FP8KVConfig):
@@ -147,11 +181,12 @@ class FusedFP8KVConfig(FP8KVConfig):
         if self.scale not in ("none", "head"):
             raise ConfigError("kv_fp8_fused supports scale='none' or 'head'; use kv_fp8 for per-token scales")
 
-    def validate(self, implementation: str) -> None:
+    def validate(self, adapter) -> None:
         """Refuses an attention implementation that does not read fp8 K/V (fused.py:39-49)."""
         from .attention import accepts_fp8_kv
 
-        _needs_kernel(self.technique, implementation, accepts_fp8_kv, "fp8 K/V", "kv_fp8")
+        super().validate(adapter)
+        _needs_kernel(self.technique, attn_implementation(adapter), accepts_fp8_kv, "fp8 K/V", "kv_fp8")
 
 
 @dataclass(frozen=True)
@@ -191,6 +226,18 @@ class KIVIConfig(TechniqueConfig):
             if not self.packable and self.storage != "simulated":
                 raise ConfigError(f"{self.technique} supports only storage='simulated', got {self.storage!r}")
 
+    def validate(self, adapter) -> None:
+        """Refuses, before anything attaches, what the paged KIVI cache cannot hold: 8-bit codes, groups other than
+        32 tokens / channels (one group is one 32-token page), simulated storage and head dims the kernels do not
+        take."""
+        if self.bits not in (2, 4):
+            raise ConfigError(f"the paged KIVI cache holds 2- and 4-bit codes, not bits={self.bits}")
+        if self.group_size != 32:
+            raise ConfigError(f"the paged KIVI cache quantizes groups of 32, not group_size={self.group_size}")
+        if self.storage == "simulated" and self.packable:
+            raise ConfigError("the paged KIVI cache is packed storage, not storage='simulated'")
+        _head_dims(self.technique, adapter, (64, 128))
+
     @property
     def kivi_storage(self) -> str:
         """:attr:`storage`, else ``"packed"`` (``"simulated"`` for a configuration that is not :attr:`packable`)."""
@@ -207,12 +254,13 @@ class FusedKIVIConfig(KIVIConfig):
     technique: ClassVar[str] = "kivi_fused"
     packable: ClassVar[bool] = False
 
-    def validate(self, implementation: str) -> None:
-        """Refuses an attention implementation that does not read KIVI codes (kv_kivi_fused/fused.py:44-51)."""
+    def validate(self, adapter) -> None:
+        """Refuses an attention implementation that does not read KIVI codes (kv_kivi_fused/fused.py:43-51)."""
         from .attention import accepts_packed_kv
 
-        _needs_kernel(self.technique, implementation, lambda name: accepts_packed_kv(name, "kivi"), "KIVI codes",
-                      "kivi")
+        super().validate(adapter)
+        _needs_kernel(self.technique, attn_implementation(adapter), lambda name: accepts_packed_kv(name, "kivi"),
+                      "KIVI codes", "kivi")
 
 
 @dataclass(frozen=True)
@@ -253,11 +301,13 @@ class QuestConfig(TechniqueConfig):
         """Committed pages a decoding query reads (the page budget minus the running page)."""
         return self.token_budget // self.page_size - 1
 
-    def validate(self, implementation: str) -> None:
-        """Refuses an attention implementation that does not read Quest pages (quest/technique.py:88-97)."""
+    def validate(self, adapter) -> None:
+        """Refuses an attention implementation that does not read Quest pages (quest/technique.py:88-97) and head
+        dims the paged kernels do not take."""
         from .attention import accepts_packed_kv
 
-        _needs_kernel(self.technique, implementation, lambda name: accepts_packed_kv(name, "quest"),
+        _head_dims(self.technique, adapter, (64, 128, 256))
+        _needs_kernel(self.technique, attn_implementation(adapter), lambda name: accepts_packed_kv(name, "quest"),
                       "its pages", None)
 
 

@@ -114,6 +114,25 @@ int eco_paged_decode_static(const void* q, int64_t sq_b, int64_t sq_q, int64_t s
 int eco_mask_bits(const uint8_t* mask, int64_t sm_b, int64_t sm_h, int64_t sm_q, int64_t sm_s, int32_t batch,
                   int32_t heads, int32_t queries, int32_t keys, uint32_t* bits, int32_t words, void* stream);
 
+/* The dense view of the paged fp8 / bf16 cache: k_out / v_out [b, kvh, t, :] (element strides so_k*, so_v*; format
+ * out_format = bf16, fp16 or fp32) = the stored keys and values of tokens t < keys, fp8 decoded exactly and times
+ * the per-head scales (NULL = 1), 0 for tokens past a row's table. Replaces materialize() of a cache without dense
+ * buffers (attention/packed.py:66-78) for the attention functions that do not read the paged format. */
+int eco_paged_gather(const void* k_cache, const void* v_cache, int32_t kv_format, int32_t num_pages,
+                     const float* k_scale, const float* v_scale, const int32_t* block_table, int64_t bt_stride,
+                     int32_t bt_cols, void* k_out, void* v_out, int32_t out_format, int64_t so_kb, int64_t so_kh,
+                     int64_t so_ks, int64_t so_vb, int64_t so_vh, int64_t so_vs, int32_t batch, int32_t kv_heads,
+                     int32_t keys, int32_t head_dim, int32_t page_size, void* stream);
+
+/* The dense view of the paged KIVI cache, as eco_paged_gather: keys below keys_quantized[b] and values below
+ * values_quantized[b] dequantized as the reference's dequantize (bf16(code * scale + zero), attention/kivi.py:
+ * 56-76), the other tokens from the rings. Replaces KIVIPacked's materialize (attention/packed.py:66-78). */
+int eco_kivi_gather(const void* blocks, int32_t num_pages, const void* k_ring, const void* v_ring, int32_t ring,
+                    const int32_t* keys_quantized, const int32_t* values_quantized, const int32_t* block_table,
+                    int64_t bt_stride, int32_t bt_cols, void* k_out, void* v_out, int32_t out_format, int64_t so_kb,
+                    int64_t so_kh, int64_t so_ks, int64_t so_vb, int64_t so_vh, int64_t so_vs, int32_t batch,
+                    int32_t kv_heads, int32_t keys, int32_t head_dim, int32_t bits, int32_t group, void* stream);
+
 /* Workspace bytes eco_decode needs for this shape (0 for an unsupported one). */
 size_t eco_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys,
                                  int32_t head_dim, int32_t value_dim);

@@ -25,18 +25,18 @@ def _forward():
 
 @pytest.mark.parametrize("dtype", [torch.float8_e4m3fn, torch.bfloat16])
 def test_paged_formats(dtype) -> None:
-    from economize_amd.attention import PagedKV, kernel_calls
+    from economize_amd.attention import PagedKV, kernel_usage
 
     lens = [700, 1300]
     c = make_case(2, 1, 16, 4, 128, lens, dtype, seed=3)
     kv = PagedKV(c.device_cache(), torch.from_numpy(c.table).cuda(), torch.tensor(lens, dtype=torch.int32).cuda(),
                  max(lens))
     sinks = np.random.default_rng(2).standard_normal(16).astype(np.float32)
-    before = kernel_calls().get(kv.format, 0)
+    kernel_usage(reset=True)
     out, weights = _forward()(None, c.q.cuda().transpose(1, 2), kv, None, None, scaling=0.1, softcap=5.0,
                               s_aux=torch.from_numpy(sinks).cuda())
     assert weights is None and out.shape == (2, 1, 16, 128)
-    assert kernel_calls()[kv.format] == before + 1
+    assert [(r["path"], r["calls"]) for r in kernel_usage(reset=True)] == [(f"kernel_{kv.format}", 1)]
     np.testing.assert_allclose(out.float().cpu().numpy(), oracle_output(c, 0.1, 5.0, sinks), atol=ATOL, rtol=RTOL)
 
 
@@ -47,7 +47,7 @@ def test_kivi_format() -> None:
     cache, table = kivi_cases.device_cache(c)
     kv = PagedKV(cache, table, torch.tensor(c.lens, dtype=torch.int32).cuda(), max(c.lens))
     assert kv.format == "kivi"
-    out, _ = _forward()(None, c.q.cuda().transpose(1, 2), kv)
+    out, _ = _forward()(None, c.q.cuda().transpose(1, 2), kv, None, None)
     np.testing.assert_allclose(out.float().cpu().numpy(), kivi_cases.oracle_output(c), atol=ATOL, rtol=RTOL)
 
 
@@ -67,12 +67,12 @@ def test_quest_format_routes_by_query_length() -> None:
     kv = PagedKV(cache, table, seq, max(lens), qp)
     assert kv.format == "quest"
     query = c.q.cuda().transpose(1, 2)
-    out, _ = _forward()(None, query, kv)
+    out, _ = _forward()(None, query, kv, None, None)
     assert torch.equal(out, qp.attend(query, cache, table, seq, max(lens)))
     # two queries per row exceed max_queries: dense attention over every key
     c2 = make_case(2, 2, 16, 4, 128, lens, torch.bfloat16, seed=12)
     query2 = c2.q.cuda().transpose(1, 2)
-    out2, _ = _forward()(None, query2, PagedKV(c2.device_cache(), table, seq, max(lens), qp))
+    out2, _ = _forward()(None, query2, PagedKV(c2.device_cache(), table, seq, max(lens), qp), None, None)
     dense = paged_decode_attention(c2.q.cuda(), c2.device_cache(), table, seq, max(lens))
     assert torch.equal(out2, dense)
     np.testing.assert_allclose(out2.float().cpu().numpy(), oracle_output(c2), atol=ATOL, rtol=RTOL)

@@ -332,3 +332,27 @@ def test_decode_with_a_mask(kind, queries, hq) -> None:
     got = kivi_decode_attention(c.q.cuda(), cache, table, seq, smax,
                                 mask=torch.from_numpy(mask).cuda()).float().cpu().numpy()
     np.testing.assert_allclose(got, oracle_output(c, mask=mask), atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_gather_gives_the_dense_view(bits) -> None:
+    """eco_kivi_gather: keys below kq and values below vq dequantized as the reference's dequantize (bf16), the
+    others from the rings: the oracle's dense view of the same pages and rings, bit for bit."""
+    from economize_amd.kivi import kivi_gather
+
+    c = make_case(3, 1, 8, 2, 128, [700, 77, 450], bits, seed=90 + bits)
+    cache, table = device_cache(c)
+    k, v = kivi_gather(cache, table, max(c.lens))
+    blocks = oracle_blocks(c, 128)
+    batch, kv_heads, smax, head_dim = c.k.shape
+    kf, vf = c.k.float().numpy(), c.v.float().numpy()
+    k_ring = np.zeros((batch, kv_heads, W, head_dim), np.float32)
+    v_ring = np.zeros((batch, kv_heads, head_dim, W), np.float32)
+    for b, n in enumerate(c.lens):
+        for t in range(max(0, n - W), n):
+            k_ring[b, :, t % W] = kf[b, :, t]
+            v_ring[b, :, :, t % W] = vf[b, :, t]
+    want_k, want_v = okp.dense_view(blocks, c.table, k_ring, v_ring, c.lens, c.kq, c.vq, bits, 32)
+    for b, n in enumerate(c.lens):
+        assert np.array_equal(k[b, :, :n].float().cpu().numpy(), want_k[b, :, :n])
+        assert np.array_equal(v[b, :, :n].float().cpu().numpy(), want_v[b, :, :n])

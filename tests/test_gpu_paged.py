@@ -256,3 +256,24 @@ def test_mask_bits_pack_the_bool_mask() -> None:
     for t in range(77):
         want[..., t // 32] |= mask[..., t].astype(np.uint32) << np.uint32(t % 32)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("dtype,out", [(torch.float8_e4m3fn, torch.bfloat16), (torch.float8_e5m2, torch.float32),
+                                       (torch.bfloat16, torch.float16)])
+def test_gather_gives_the_dense_view(dtype, out) -> None:
+    """eco_paged_gather: the stored K/V of every row's tokens, fp8 decoded exactly times the head scales, in the
+    output dtype; 0 past a row's pages."""
+    from economize_amd.paged import paged_gather
+
+    lens = [300, 17, 0, 129]
+    c = make_case(4, 1, 8, 2, 64, lens, dtype, seed=61)
+    cache = c.device_cache()
+    keys = max(lens)
+    k, v = paged_gather(cache, torch.from_numpy(c.table).cuda(), keys, out)
+    assert k.dtype == out and k.shape == (4, 2, keys, 64)
+    kd, vd = c.decoded()
+    held = (np.arange(keys)[None, :] < np.array(lens)[:, None])[:, None, :, None]
+    want_k = torch.from_numpy(np.where(held, kd[:, :, :keys], 0)).to(out).float().numpy()
+    want_v = torch.from_numpy(np.where(held, vd[:, :, :keys], 0)).to(out).float().numpy()
+    got_k, got_v = k.float().cpu().numpy(), v.float().cpu().numpy()
+    assert np.array_equal(np.where(held, got_k, 0), want_k) and np.array_equal(np.where(held, got_v, 0), want_v)

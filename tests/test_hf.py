@@ -1,0 +1,96 @@
+"""The drop-in boundary on the CPU: the ``"economize"`` registration with transformers (attention/interface.py:
+502-525), ``validate(adapter)`` refusing what the MI355X path cannot run before anything attaches, ``apply``'s
+refusal of two techniques on one layer, and the forward's per-call fallback (a CPU call runs transformers' sdpa and
+is logged with its reason, attention/interface.py:243-285)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from economize_amd.errors import ConfigError, IncompatibleTechniquesError
+from economize_amd.techniques import FP8KVConfig, FusedFP8KVConfig, FusedKIVIConfig, KIVIConfig, QuestConfig
+
+
+def tiny_model(head_dim: int = 64, attn: str = "sdpa", layers: int = 4):
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+
+    config = Qwen2Config(vocab_size=128, hidden_size=128, intermediate_size=256, num_hidden_layers=layers,
+                         num_attention_heads=4, num_key_value_heads=2, head_dim=head_dim, max_position_embeddings=512,
+                         tie_word_embeddings=True, initializer_range=0.2, attn_implementation=attn)
+    torch.manual_seed(0)
+    model = Qwen2ForCausalLM(config).eval()
+    model.requires_grad_(False)
+    return model
+
+
+def test_install_registers_the_forward_with_transformers() -> None:
+    from transformers import AttentionInterface
+    from transformers.masking_utils import AttentionMaskInterface
+
+    from economize_amd.attention import economize_attention_forward, install
+
+    assert "economize" in install()
+    assert AttentionInterface._global_mapping["economize"] is economize_attention_forward
+    assert AttentionMaskInterface._global_mapping["economize"] is AttentionMaskInterface._global_mapping["sdpa"]
+
+
+def test_validate_refuses_what_the_path_cannot_run() -> None:
+    model = tiny_model()
+    model.config._attn_implementation = "economize"
+    FusedFP8KVConfig().validate(model)
+    FusedKIVIConfig().validate(model)
+    QuestConfig().validate(model.config)
+    with pytest.raises(ConfigError, match="per-head scales"):
+        FP8KVConfig(scale="token").validate(model)
+    with pytest.raises(ConfigError, match="per-head scales"):
+        FP8KVConfig(scale="tensor").validate(model)
+    with pytest.raises(ConfigError, match="bits=8"):
+        KIVIConfig(bits=8).validate(model)
+    with pytest.raises(ConfigError, match="group_size=64"):
+        KIVIConfig(group_size=64, residual_length=128).validate(model)
+    with pytest.raises(ConfigError, match="simulated"):
+        KIVIConfig(storage="simulated").validate(model)
+    with pytest.raises(ConfigError, match="head dims"):
+        FusedKIVIConfig().validate(tiny_model(head_dim=256).config)
+    with pytest.raises(IncompatibleTechniquesError, match="economize"):
+        FusedFP8KVConfig().validate(tiny_model())  # the model runs sdpa
+
+
+def test_apply_selects_the_kernel_and_refuses_conflicts() -> None:
+    from economize_amd.hf import apply
+
+    model = tiny_model()
+    em = apply(model, FusedFP8KVConfig(layers=(1, 2)), QuestConfig(dense_layers=2))
+    assert model.config._attn_implementation == "economize"
+    assert [type(t.config).__name__ if t else None for t in map(em.technique_of, [1, 2, 3, 4])] == \
+        ["FusedFP8KVConfig", "FusedFP8KVConfig", "QuestConfig", "QuestConfig"]
+    with pytest.raises(IncompatibleTechniquesError, match="one KV technique per layer"):
+        apply(tiny_model(), FusedFP8KVConfig(), FusedKIVIConfig())
+    with pytest.raises(IncompatibleTechniquesError, match="twice"):
+        apply(tiny_model(), FusedFP8KVConfig(layers=(1,)), FusedFP8KVConfig(layers=(2,)))
+    with pytest.raises(ConfigError, match="head dims"):
+        apply(tiny_model(head_dim=32), FusedFP8KVConfig())
+    with pytest.raises(ConfigError, match="scale='head'"):
+        apply(tiny_model(), FP8KVConfig(scale="head"))
+
+
+def test_a_cpu_call_falls_back_to_sdpa_and_is_logged() -> None:
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward
+
+    from economize_amd.attention import economize_attention_forward, kernel_usage
+
+    kernel_usage(reset=True)
+    module = torch.nn.Module()
+    module.layer_idx = 3
+    module.is_causal = True
+    module.num_key_value_groups = 2
+    gen = torch.Generator().manual_seed(0)
+    q = torch.randn(1, 4, 1, 64, generator=gen)
+    k = torch.randn(1, 2, 9, 64, generator=gen)
+    v = torch.randn(1, 2, 9, 64, generator=gen)
+    mask = torch.ones(1, 1, 1, 9, dtype=torch.bool)
+    got, _ = economize_attention_forward(module, q, k, v, mask, scaling=0.125)
+    want, _ = sdpa_attention_forward(module, q, k, v, mask, scaling=0.125)
+    assert torch.equal(got, want)
+    assert kernel_usage() == [{"layer": 3, "queries": 1, "path": "sdpa", "reason": "cpu", "calls": 1}]
