@@ -14,7 +14,8 @@ NaN, max 448; e5m2: bias 15, IEEE-like, max 57344).
 Pinned by (``tests/test_oracle_fp8.py``): every bf16 bit pattern and 2^20 random float32 values encoded by torch's
 own CPU ``Tensor.to(torch.float8_*)`` (the call the reference makes at fp8.py:86), the 256-byte decode table against
 torch's ``view(fp8).float()`` (fp8.py:91) and the closed-form values of a few bytes (0x38 = 1.0, 0x7E = 448,
-0x01 = 2^-9).
+0x01 = 2^-9). End to end, ``tests/test_golden_reference.py`` decodes the reference's golden model with every K/V
+through this round trip and gets the reference's own ``kv_fp8`` golden tokens (tests/golden/catalog.py:168-170).
 """
 
 from __future__ import annotations

@@ -19,7 +19,9 @@ Pinned by (``tests/test_oracle_kivi.py``): the reference's closed-form tests (te
 343-360: level counts, error bound, constant groups exact, the fp16-rounded scale formula, finite beyond the fp16
 range), a transcription-free restatement of the official KIVI quantizer's order of operations (clamp then round,
 test_kv_quant_reference.py:33-43 describes it), pack/unpack identity and the bit positions of single codes, and the
-``kivi_bytes`` example of test_kv_quant.py:95-104.
+``kivi_bytes`` example of test_kv_quant.py:95-104. End to end, ``tests/test_golden_reference.py`` decodes the
+reference's golden model with :func:`schedule`, :func:`quantize_keys` and :func:`quantize_values` at 2 bits, groups
+of 4 and residual 8, and gets the reference's own ``kv_kivi_2bit`` golden tokens (tests/golden/catalog.py:163-165).
 """
 
 from __future__ import annotations

@@ -4,7 +4,8 @@ numpy has no bfloat16, so bf16 tensors are carried as their ``uint16`` bit patte
 round-to-nearest-even on the bit pattern, which is what ``torch.Tensor.to(torch.bfloat16)`` does on the CPU (the
 reference casts with it everywhere, e.g. ``fp8_decode``'s ``.to(out)`` at techniques/kv_quant/fp8.py:92).
 
-Pinned by: ``tests/test_oracle_numerics.py`` compares every bf16 bit pattern and 2^20 random float32 values against
+Pinned by: ``tests/test_oracle_fp8.py::test_bf16_and_fp16_rounding_match_torch`` compares the widening of every bf16
+bit pattern, and the rounding of 2^20 random float32 values, exact round-half ties and special values, against
 torch's own CPU casts.
 """
 

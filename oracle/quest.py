@@ -24,8 +24,10 @@ Pinned by (``tests/test_oracle_quest.py``): a float64 computation of the per-hea
 q_hd hi_d)`` (the mathematically equal form of the official Quest selection, tests/techniques/test_quest.py:124-143
 describes it) selects the same pages whenever the gap at the k-th score exceeds the fp32 error bound; brute-force
 page masks for ``keep``; the invariants of test_quest.py:202-215 (increasing order, ``-1`` padding, every committed
-page when ``done <= pages``). The exact fp32 score bits at near-ties are parity unpinned: no independent check can fix
-them.
+page when ``done <= pages``). End to end, ``tests/test_golden_reference.py`` decodes the reference's golden model
+with :func:`page_bounds`, :func:`select_pages` and :func:`quest_reference` and gets the reference's own ``kv_quest``
+golden tokens (tests/golden/catalog.py:195-207). The exact fp32 score bits at near-ties are parity unpinned: the
+reference's own bits there depend on the backend's einsum order, so no check can fix them.
 """
 
 from __future__ import annotations

@@ -81,9 +81,22 @@ def test_scales_follow_the_reference_rules() -> None:
 
 
 def test_bf16_and_fp16_rounding_match_torch() -> None:
+    """oracle.numerics against torch's CPU casts: every bf16 bit pattern widens as torch widens it, and 2^20 random
+    float32 values plus exact round-half ties, infinities, NaN and fp16 overflow round as torch rounds them."""
+    from oracle.numerics import bf16_bits_to_f32
+
+    patterns = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    widened = torch.from_numpy(patterns.view(np.int16)).view(torch.bfloat16).float().numpy()
+    assert np.array_equal(bf16_bits_to_f32(patterns).view(np.uint32), widened.view(np.uint32))
     rng = np.random.default_rng(1)
-    x = (rng.standard_normal(1 << 18) * np.exp2(rng.integers(-30, 30, 1 << 18))).astype(np.float32)
+    x = (rng.standard_normal(1 << 20) * np.exp2(rng.integers(-30, 30, 1 << 20))).astype(np.float32)
+    # exact halfway points between neighbouring bf16 values (both parities) and special values
+    base = rng.integers(0, 1 << 16, 4096).astype(np.uint32) << 16
+    ties = (base | np.uint32(0x8000)).view(np.float32)
+    special = np.array([np.inf, -np.inf, np.nan, 0.0, -0.0, 65504.0, 65520.0, 1e6, -3.4e38], np.float32)
+    x = np.concatenate([x, ties[np.isfinite(ties)], special])
     t = torch.from_numpy(x)
-    assert np.array_equal(round_bf16(x), t.to(torch.bfloat16).float().numpy())
-    assert np.array_equal(f32_to_bf16_bits(x), t.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16))
-    assert np.array_equal(round_fp16(x), t.half().float().numpy())
+    assert np.array_equal(round_bf16(x), t.to(torch.bfloat16).float().numpy(), equal_nan=True)
+    assert np.array_equal(f32_to_bf16_bits(x)[np.isfinite(x)],
+                          t.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)[np.isfinite(x)])
+    assert np.array_equal(round_fp16(x), t.half().float().numpy(), equal_nan=True)
