@@ -37,6 +37,7 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
     "eco_last_error": (ctypes.c_char_p, []),
     "eco_abi_version": (c_int32, []),
     "eco_paged_append": (c_int32, [_P, _P, _I, _L, _L, _L, _L, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P]),
+    "eco_fp8_encode": (c_int32, [_P, _I, _L, _L, _L, _P, _I, _L, _L, _L, _I, _I, _I, _I, _P, _P, _L, _L, _L, _P]),
     "eco_kv_head_absmax": (c_int32, [_P, _I, _I, _I, _I, _I, _L, _L, _L, _L, _P, _P]),
     "eco_fp8_scales_from_absmax": (c_int32, [_P, _I, _I, _P, _P]),
     "eco_paged_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I, _I, _I]),

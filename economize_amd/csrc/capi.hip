@@ -348,6 +348,24 @@ int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, in
     return paged_append(p, static_cast<hipStream_t>(stream));
 }
 
+int eco_fp8_encode(const void* src, int32_t in_format, int64_t ss_b, int64_t ss_h, int64_t ss_t, void* dst,
+                   int32_t out_format, int64_t sd_b, int64_t sd_h, int64_t sd_t, int32_t batch, int32_t heads,
+                   int32_t tokens, int32_t head_dim, const float* head_scale, float* token_scale, int64_t st_b,
+                   int64_t st_h, int64_t st_t, void* stream) {
+    if (batch < 0 || heads < 0 || tokens < 0) return fail("fp8 encode: negative shape");
+    if (head_dim <= 0 || head_dim > 256) return fail("fp8 encode: head dim must be in 1..256");
+    if (static_cast<int64_t>(batch) * heads * tokens == 0) return 0;
+    if (!src || !dst) return fail("fp8 encode: null source or destination");
+    if (in_format != BF16 && in_format != FP16 && in_format != FP32)
+        return fail("fp8 encode: the source must be bf16, fp16 or fp32");
+    if (out_format != FP8_E4M3 && out_format != FP8_E5M2)
+        return fail("fp8 encode: the output format must be fp8 e4m3 or e5m2");
+    if (head_scale && token_scale) return fail("fp8 encode: per-head and per-token scales exclude each other");
+    EncodeParams p{src, in_format, ss_b, ss_h, ss_t, static_cast<uint8_t*>(dst), out_format, sd_b, sd_h, sd_t,
+                   batch, heads, tokens, head_dim, head_scale, token_scale, st_b, st_h, st_t};
+    return fp8_encode(p, static_cast<hipStream_t>(stream));
+}
+
 int eco_kv_head_absmax(const void* x, int32_t in_format, int32_t a, int32_t h, int32_t s, int32_t d, int64_t sa,
                        int64_t sh, int64_t ss, int64_t sd, uint32_t* absmax_bits, void* stream) {
     if (!x || !absmax_bits) return fail("head absmax: null pointer");

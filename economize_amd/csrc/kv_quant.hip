@@ -29,9 +29,8 @@ __device__ inline float load_elem(const void* base, int64_t offset, int format) 
 template <int FMT>
 __device__ inline uint8_t encode(float x, float scale, bool scaled) {
     float w = scaled ? __fdiv_rn(x, scale) : x;
-    w = fminf(fmaxf(w, -fp8_max<FMT>()), fp8_max<FMT>());  // clamp; NaN stays NaN (fminf/fmaxf would drop it)
-    if (x != x) w = x;
-    return f32_to_fp8<FMT>(w);
+    if (w != w) return f32_to_fp8<FMT>(x != x ? x : w);  // NaN stays NaN (fminf/fmaxf would drop it)
+    return f32_to_fp8<FMT>(fminf(fmaxf(w, -fp8_max<FMT>()), fp8_max<FMT>()));
 }
 
 template <int FMT>
@@ -84,6 +83,50 @@ __global__ __launch_bounds__(256) void paged_append_kernel(AppendParams p) {
     }
 }
 
+// Dense encode (fp8_encode of fp8.py:81-86 over a [B, H, T, D] block, the fused fp8 cache's dense buffers of
+// kv_fp8_fused/fused.py:56-63): one wave per (b, h, t) row, each lane a few channels. The per-token mode computes the
+// row's scale as token_scale does (fp8.py:95-97: absmax / format max with IEEE division, at least 1e-12), writes it
+// and encodes with it; the per-head mode divides by head_scale[h]; with neither the values are cast directly.
+template <int FMT>
+__global__ __launch_bounds__(256) void fp8_encode_kernel(EncodeParams p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t rows = static_cast<int64_t>(p.batch) * p.heads * p.tokens;
+    for (int64_t row = blockIdx.x * 4LL + (threadIdx.x >> 6); row < rows; row += static_cast<int64_t>(gridDim.x) * 4) {
+        const int t = static_cast<int>(row % p.tokens);
+        const int h = static_cast<int>((row / p.tokens) % p.heads);
+        const int b = static_cast<int>(row / (static_cast<int64_t>(p.tokens) * p.heads));
+        const int64_t src = b * p.ss_b + h * p.ss_h + t * p.ss_t;
+        uint8_t* dst = p.dst + b * p.sd_b + h * p.sd_h + t * p.sd_t;
+        float x[4];  // channels lane, lane + 64, .. (head dims up to 256)
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int d = lane + 64 * i;
+            x[i] = d < p.head_dim ? load_elem(p.src, src + d, p.in_format) : 0.0f;
+            amax = fmaxf(amax, fabsf(x[i]));
+        }
+        float scale = 1.0f;
+        bool scaled = false;
+        if (p.token_scale) {
+            bool nan = false;  // torch's amax propagates NaN, and so does the scale then
+#pragma unroll
+            for (int i = 0; i < 4; ++i) nan |= x[i] != x[i];
+            for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+            scale = __ballot(nan) ? __builtin_nanf("") : fmaxf(__fdiv_rn(amax, fp8_max<FMT>()), 1e-12f);
+            scaled = true;
+            if (lane == 0) p.token_scale[b * p.st_b + h * p.st_h + t * p.st_t] = scale;
+        } else if (p.head_scale) {
+            scale = p.head_scale[h];
+            scaled = true;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int d = lane + 64 * i;
+            if (d < p.head_dim) dst[d] = encode<FMT>(x[i], scale, scaled);
+        }
+    }
+}
+
 // absmax[h] = max |x[a, h, s, d]| as float bits (non-negative floats order like their bit patterns).
 __global__ __launch_bounds__(256) void head_absmax_kernel(AbsmaxParams p) {
     const int h = blockIdx.y;
@@ -122,6 +165,18 @@ int paged_append(const AppendParams& p, hipStream_t stream) {
         default: return fail("paged append: cache format must be bf16, fp8 e4m3 or fp8 e5m2");
     }
     return check_launch("paged_append_kernel");
+}
+
+int fp8_encode(const EncodeParams& p, hipStream_t stream) {
+    const int64_t rows = static_cast<int64_t>(p.batch) * p.heads * p.tokens;
+    if (rows == 0) return 0;
+    const int blocks = static_cast<int>((rows + 3) / 4 < 65535 ? (rows + 3) / 4 : 65535);
+    switch (p.out_format) {
+        case FP8_E4M3: hipLaunchKernelGGL(fp8_encode_kernel<FP8_E4M3>, dim3(blocks), dim3(256), 0, stream, p); break;
+        case FP8_E5M2: hipLaunchKernelGGL(fp8_encode_kernel<FP8_E5M2>, dim3(blocks), dim3(256), 0, stream, p); break;
+        default: return fail("fp8 encode: the output format must be fp8 e4m3 or e5m2");
+    }
+    return check_launch("fp8_encode_kernel");
 }
 
 int head_absmax(const AbsmaxParams& p, hipStream_t stream) {

@@ -29,7 +29,22 @@ struct AbsmaxParams {
     uint32_t* absmax_bits;  // [H], max-accumulated (zero it first)
 };
 
+// fp8 encode of a [B, H, T, D] block into a dense fp8 buffer (both with a contiguous channel axis).
+struct EncodeParams {
+    const void* src;
+    int in_format;
+    int64_t ss_b, ss_h, ss_t;  // element strides of the source
+    uint8_t* dst;
+    int out_format;
+    int64_t sd_b, sd_h, sd_t;  // byte strides of the destination
+    int batch, heads, tokens, head_dim;
+    const float* head_scale;  // optional [H]: one scale per head (the static / per-head modes)
+    float* token_scale;       // optional [B, H, T] output: the per-token mode computes and writes its scales
+    int64_t st_b, st_h, st_t;
+};
+
 int paged_append(const AppendParams& p, hipStream_t stream);
+int fp8_encode(const EncodeParams& p, hipStream_t stream);
 int head_absmax(const AbsmaxParams& p, hipStream_t stream);
 int scales_from_absmax(const uint32_t* absmax_bits, int heads, int format, float* scales, hipStream_t stream);
 

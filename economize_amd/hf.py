@@ -5,9 +5,12 @@ Mirrors the reference's cache wrappers (techniques/_kv/wrapper.py:122-351: ``tra
 new K/V, ``transform_read`` what attention sees, ``pass_begin`` / ``pass_end`` at the boundaries of an exact pass)
 for the techniques of this path:
 
-* ``FP8KVConfig`` / ``FusedFP8KVConfig``: K/V encoded to fp8 on write into a paged fp8 cache (``fp8_encode``,
-  techniques/kv_quant/fp8.py:81-86 and 161-176); attention reads the bytes on the paged kernel
-  (kv_fp8_fused/fused.py:56-63 hands fp8 views over).
+* ``FP8KVConfig`` / ``FusedFP8KVConfig``: K/V encoded to fp8 on write (``fp8_encode``, techniques/kv_quant/fp8.py:
+  81-86 and 161-176). Where the paged kernels take the model (bf16, head dim 64 / 128 / 256) and the scale is none,
+  static or per head, into a paged fp8 cache whose bytes attention reads on the paged kernel (kv_fp8_fused/fused.py:
+  56-63 hands fp8 views over); otherwise into dense fp8 buffers (:class:`DenseFP8Layer`, also the per-token scales
+  of fp8.py:95-97), handed to the dense kernel as fp8 views (fused) or decoded to the model's dtype (fp8.py:89-92).
+  Static scales (``"tensor"``, and ``"head"`` per KV head) are calibrated at attach time (fp8.py:100-133).
 * ``KIVIConfig`` / ``FusedKIVIConfig``: new tokens in the bf16 ring, the reference's schedule run at every pass
   boundary (the tokens a pass commits are quantized when it ends, kivi.py:191-243), attention on the fused KIVI
   kernel over codes and ring (kv_kivi_fused/fused.py:152-208).
@@ -33,11 +36,13 @@ from transformers.cache_utils import Cache, CacheLayerMixin, DynamicLayer
 
 from .attention import MAX_QUERIES, NAME, PagedKV, install
 from .errors import ConfigError, IncompatibleTechniquesError
+from .fp8 import calibrate_kv_absmax, fp8_encode, static_scales
 from .kivi import KIVI_PAGE, PagedKIVICache, kivi_append, kivi_commit, kivi_quantize
 from .packed import attach_packed, stand_in
 from .paged import PAGE, PagedKVCache, paged_append
 from .quest import QuestPages, page_bounds
-from .techniques import (FP8KVConfig, KIVIConfig, QuestConfig, Technique, attn_implementation, head_dim_of,
+from .techniques import (FP8KVConfig, FusedFP8KVConfig, KIVIConfig, QuestConfig, Technique, attn_implementation,
+                         head_dim_of,
                          technique_for)
 
 __all__ = ["EconomizeCache", "EconomizedModel", "KIVILayer", "PagedLayer", "apply"]
@@ -123,10 +128,12 @@ class _PagedBase(CacheLayerMixin):
 class PagedLayer(_PagedBase):
     """One layer in a paged fp8 or bf16 cache (16-token pages), optionally with Quest's page bounds."""
 
-    def __init__(self, capacity: int, cache_dtype: torch.dtype | None, quest: QuestConfig | None = None) -> None:
+    def __init__(self, capacity: int, cache_dtype: torch.dtype | None, quest: QuestConfig | None = None,
+                 scales: tuple[torch.Tensor, torch.Tensor] | None = None) -> None:
         super().__init__(capacity, PAGE)
         self.cache_dtype = cache_dtype  # None: the model's dtype (bf16)
         self.quest = quest
+        self.scales = scales  # fp32 [Hkv] key and value scales of an fp8 cache, or None
         self.cache: PagedKVCache | None = None
         self.bounds: tuple[torch.Tensor, torch.Tensor] | None = None
         self.valid = 0  # Quest pages whose bounds are final
@@ -137,7 +144,10 @@ class PagedLayer(_PagedBase):
         self.model_dtype = key_states.dtype
         dtype = self.cache_dtype or torch.bfloat16
         pages = self._allocate_table(batch, key_states.device)
-        self.cache = PagedKVCache.empty(pages, heads, dim, dtype, key_states.device)
+        k_scale = v_scale = None
+        if self.scales is not None:
+            k_scale, v_scale = (x.to(key_states.device, torch.float32).reshape(heads).contiguous() for x in self.scales)
+        self.cache = PagedKVCache.empty(pages, heads, dim, dtype, key_states.device, k_scale, v_scale)
         if self.quest is not None:
             shape = (batch, heads, -(-self.capacity // self.quest.page_size), dim)
             self.bounds = (torch.zeros(shape, dtype=torch.bfloat16, device=key_states.device),
@@ -177,6 +187,88 @@ class PagedLayer(_PagedBase):
     def reset(self) -> None:
         super().reset()
         self.valid = 0
+
+
+class DenseFP8Layer(CacheLayerMixin):
+    """One layer's K/V as fp8 codes in dense ``[B, Hkv, capacity, D]`` buffers (the reference's ``FP8Cache``,
+    fp8.py:143-217): new K/V are encoded on write with the configuration's scale (none, per token, or the calibrated
+    static scale per head); a read hands the fp8 buffers over as they are (``fused``: the economize kernel reads fp8
+    K/V, kv_fp8_fused/fused.py:56-63) or decoded to the model's dtype as ``fp8_decode`` does (``codes * scale`` in
+    fp32, then the model's dtype, fp8.py:89-92)."""
+
+    is_sliding = False
+    is_compileable = False
+    supports_early_init = False
+
+    def __init__(self, capacity: int, config: FP8KVConfig, fused: bool,
+                 scales: tuple[torch.Tensor, torch.Tensor] | None = None) -> None:
+        super().__init__()
+        if fused and config.scale != "none":
+            raise ConfigError("the dense fused fp8 cache takes scale='none' (kv_fp8_fused/fused.py:37-41)")
+        self.capacity = int(capacity)
+        self.config = config
+        self.fused = fused
+        self.scales = scales
+        self.length = 0
+        self.model_dtype = torch.bfloat16
+        self.codes: tuple[torch.Tensor, torch.Tensor] | None = None
+        self.token_scales: tuple[torch.Tensor, torch.Tensor] | None = None
+        self.head_scales: tuple[torch.Tensor, torch.Tensor] | None = None
+
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        batch, heads, _, dim = key_states.shape
+        device = key_states.device
+        self.model_dtype = key_states.dtype
+        self.codes = tuple(torch.zeros(batch, heads, self.capacity, dim, dtype=self.config.dtype, device=device)
+                           for _ in range(2))
+        if self.config.scale == "token":
+            self.token_scales = tuple(torch.ones(batch, heads, self.capacity, dtype=torch.float32, device=device)
+                                      for _ in range(2))
+        elif self.config.scale in ("tensor", "head"):
+            if self.scales is None:
+                raise ConfigError(f"scale={self.config.scale!r} needs calibrated scales (apply(..., calibration=))")
+            self.head_scales = tuple(x.to(device, torch.float32).reshape(heads).contiguous() for x in self.scales)
+        self.is_initialized = True
+
+    def get_seq_length(self) -> int:
+        return self.length
+
+    def get_mask_sizes(self, query_length: int) -> tuple[int, int]:
+        return self.length + query_length, 0
+
+    def get_max_length(self) -> int:
+        return self.capacity
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs
+               ) -> tuple[torch.Tensor, torch.Tensor]:
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        tokens = key_states.shape[2]
+        if self.length + tokens > self.capacity:
+            raise ConfigError(f"the cache holds {self.capacity} tokens per row; writing {tokens} more after "
+                              f"{self.length} exceeds it (make the cache with a larger max_length)")
+        new = slice(self.length, self.length + tokens)
+        for i, states in enumerate((key_states, value_states)):
+            states = states if states.stride(-1) == 1 else states.contiguous()
+            fp8_encode(states, self.config.dtype, self.codes[i][:, :, new],
+                       None if self.head_scales is None else self.head_scales[i],
+                       None if self.token_scales is None else self.token_scales[i][:, :, new])
+        self.length += tokens
+        keys, values = (c[:, :, : self.length] for c in self.codes)
+        if self.fused:
+            return keys, values
+        return self._decoded(keys, 0), self._decoded(values, 1)
+
+    def _decoded(self, codes: torch.Tensor, i: int) -> torch.Tensor:
+        work = codes.float()
+        if self.token_scales is not None:
+            work = work * self.token_scales[i][:, :, : self.length, None]
+        elif self.head_scales is not None:
+            work = work * self.head_scales[i].view(1, -1, 1, 1)
+        return work.to(self.model_dtype)
+
+    def reset(self) -> None:
+        self.length = 0
 
 
 class KIVILayer(_PagedBase):
@@ -312,6 +404,9 @@ class EconomizedModel:
 
     model: torch.nn.Module
     techniques: list[Technique] = field(default_factory=list)
+    #: Calibrated fp8 scales by 0-indexed layer: fp32 ``[Hkv]`` key and value scales (a static ``"tensor"`` scale
+    #: repeated over the heads).
+    scales: dict[int, tuple[torch.Tensor, torch.Tensor]] = field(default_factory=dict)
 
     def technique_of(self, layer: int) -> Technique | None:
         """The technique covering 1-indexed ``layer`` (at most one per layer)."""
@@ -319,6 +414,12 @@ class EconomizedModel:
             if technique.covers(layer):
                 return technique
         return None
+
+    def paged_fp8(self, config: FP8KVConfig) -> bool:
+        """Whether ``config``'s layers live in the paged fp8 cache: the paged kernels take the model (bf16, head dim
+        64 / 128 / 256) and the scale is one they read (none, or static per head); else dense fp8 buffers."""
+        dtype = next(self.model.parameters()).dtype
+        return dtype == torch.bfloat16 and head_dim_of(self.model) in (64, 128, 256) and config.scale != "token"
 
     def make_cache(self, max_length: int) -> EconomizeCache:
         """A cache for generations of up to ``max_length`` tokens per row (prompt included)."""
@@ -329,8 +430,11 @@ class EconomizedModel:
             cfg = technique.config if technique is not None else None
             if isinstance(cfg, KIVIConfig):
                 layers.append(KIVILayer(max_length, cfg))
+            elif isinstance(cfg, FP8KVConfig) and self.paged_fp8(cfg):
+                layers.append(PagedLayer(max_length, cfg.dtype, scales=self.scales.get(index)))
             elif isinstance(cfg, FP8KVConfig):
-                layers.append(PagedLayer(max_length, cfg.dtype))
+                layers.append(DenseFP8Layer(max_length, cfg, isinstance(cfg, FusedFP8KVConfig),
+                                            self.scales.get(index)))
             elif isinstance(cfg, QuestConfig):
                 layers.append(PagedLayer(max_length, None, cfg))
             else:
@@ -344,14 +448,16 @@ class EconomizedModel:
         return self.model.generate(input_ids, past_key_values=cache, max_new_tokens=max_new_tokens, **kwargs)
 
 
-def apply(model: torch.nn.Module, *configs) -> EconomizedModel:
+def apply(model: torch.nn.Module, *configs, calibration=None) -> EconomizedModel:
     """Attach the techniques of ``configs`` to a transformers causal LM (core/model.py:330-356): registers the
     ``"economize"`` kernel (:func:`~economize_amd.attention.install`), selects it as the model's attention
     implementation, validates every configuration against the model before anything attaches
-    (``config.validate(model)``), and refuses two techniques on one layer.
+    (``config.validate(model)``), refuses two techniques on one layer, and calibrates the static fp8 scales of
+    ``scale="tensor"`` / ``"head"`` on ``calibration`` (token batches; fp8.py:100-133).
 
     Raises:
-        ConfigError: A configuration the MI355X path cannot run on this model.
+        ConfigError: A configuration the MI355X path cannot run on this model, or static fp8 scales without
+            calibration batches.
         IncompatibleTechniquesError: Two techniques cover one layer, or a technique twice.
     """
     install()
@@ -368,12 +474,29 @@ def apply(model: torch.nn.Module, *configs) -> EconomizedModel:
         if any(type(t.config) is type(config) for t in techniques):
             raise IncompatibleTechniquesError(f"{config.technique} is applied twice")
         config.validate(model)
-        if isinstance(config, FP8KVConfig) and config.scale == "head":
-            raise ConfigError("scale='head' needs calibrated per-head scales (economize_amd.paged.head_scales); the "
-                              "generation cache takes scale='none'")
         techniques.append(technique_for(config))
     for layer in range(1, model.config.num_hidden_layers + 1):
         covering = [t.config.technique for t in techniques if t.covers(layer)]
         if len(covering) > 1:
             raise IncompatibleTechniquesError(f"layer {layer} is covered by {covering}; one KV technique per layer")
-    return EconomizedModel(model, techniques)
+    result = EconomizedModel(model, techniques)
+    for technique in techniques:
+        config = technique.config
+        if not isinstance(config, FP8KVConfig):
+            continue
+        if isinstance(config, FusedFP8KVConfig) and config.scale == "head" and not result.paged_fp8(config):
+            raise ConfigError("kv_fp8_fused with scale='head' needs the paged fp8 cache (a bf16 model of head dim "
+                              "64, 128 or 256); use kv_fp8 on this model")
+        if config.scale not in ("tensor", "head"):
+            continue
+        if calibration is None:
+            raise ConfigError(f"scale={config.scale!r} is calibrated at attach time: pass calibration batches to "
+                              "apply(model, ..., calibration=...)")
+        keys, values = calibrate_kv_absmax(model, calibration, per_head=config.scale == "head")
+        kv_heads = getattr(model.config, "num_key_value_heads", None) or model.config.num_attention_heads
+        for index in range(model.config.num_hidden_layers):
+            if technique.covers(index + 1):
+                k, v = (static_scales(x[index], config.dtype).reshape(-1).expand(kv_heads).contiguous()
+                        for x in (keys, values))
+                result.scales[index] = (k, v)
+    return result

@@ -161,18 +161,15 @@ class FP8KVConfig(TechniqueConfig):
         return FP8_FORMATS[self.format]
 
     def validate(self, adapter) -> None:
-        """Refuses, before anything attaches, what the paged fp8 cache cannot hold: per-token and per-tensor scales
-        (it keeps per-head scales) and head dims the kernels do not take."""
-        if self.scale in ("token", "tensor"):
-            raise ConfigError(f"the paged fp8 cache stores per-head scales, not scale={self.scale!r}; use 'none' or "
-                              "'head'")
-        _head_dims(self.technique, adapter, (64, 128, 256))
+        """Every scale mode and head dim runs: the paged fp8 cache where its kernels take the model, dense fp8
+        buffers decoded to the model's dtype otherwise (check_layers / check_positional of fp8.py:77-79 have no
+        counterpart: layers are checked when the cache is built)."""
 
 
 @dataclass(frozen=True)
 class FusedFP8KVConfig(FP8KVConfig):
     """FP8 KV cache whose bytes the attention kernel reads directly (the reference allows ``scale="none"`` only;
-    the paged kernel also reads per-head scales, ``"head"``)."""
+    the paged kernel also reads per-head scales, ``"head"``, on the models it takes)."""
 
     technique: ClassVar[str] = "kv_fp8_fused"
 
@@ -182,10 +179,14 @@ class FusedFP8KVConfig(FP8KVConfig):
             raise ConfigError("kv_fp8_fused supports scale='none' or 'head'; use kv_fp8 for per-token scales")
 
     def validate(self, adapter) -> None:
-        """Refuses an attention implementation that does not read fp8 K/V (fused.py:39-49)."""
+        """Refuses an attention implementation that does not read fp8 K/V (fused.py:39-49) and head dims beyond the
+        kernels' 256."""
         from .attention import accepts_fp8_kv
 
         super().validate(adapter)
+        dim = head_dim_of(adapter)
+        if dim is not None and dim > 256:
+            raise ConfigError(f"{self.technique}: the MI355X kernels take head dims up to 256, the model has {dim}")
         _needs_kernel(self.technique, attn_implementation(adapter), accepts_fp8_kv, "fp8 K/V", "kv_fp8")
 
 

@@ -45,6 +45,18 @@ int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, in
                      void* v_cache, int32_t num_pages, int32_t kv_heads, int32_t head_dim, int32_t page_size,
                      int32_t cache_format, const float* k_scale, const float* v_scale, void* stream);
 
+/* fp8 encode into a dense fp8 buffer (the fused fp8 cache's [B, H, S, D] buffers).
+ * Replaces the reference's fp8_encode and token_scale (techniques/kv_quant/fp8.py:81-86, 95-97) as
+ * FP8Cache.transform_update applies them (fp8.py:161-176): src [B, H, T, D] (element strides ss_b, ss_h, ss_t,
+ * channel stride 1, bf16 / fp16 / fp32) is divided by its scale, clamped to the format's maximum, rounded to nearest
+ * even and written to dst (byte strides sd_b, sd_h, sd_t, channel stride 1). Scales: head_scale [H] fp32 (the static
+ * and per-head modes), or token_scale non-NULL (the per-token mode: each (b, h, t) row's absmax / format max, at
+ * least 1e-12, written to token_scale at element strides st_b, st_h, st_t), or neither (a direct cast). */
+int eco_fp8_encode(const void* src, int32_t in_format, int64_t ss_b, int64_t ss_h, int64_t ss_t, void* dst,
+                   int32_t out_format, int64_t sd_b, int64_t sd_h, int64_t sd_t, int32_t batch, int32_t heads,
+                   int32_t tokens, int32_t head_dim, const float* head_scale, float* token_scale, int64_t st_b,
+                   int64_t st_h, int64_t st_t, void* stream);
+
 /* Per-head absolute maximum of x [A, H, S, D] (element strides sa, sh, ss, sd; format bf16, fp16 or fp32),
  * max-accumulated into absmax_bits[H] as float bit patterns (zero them before the first call). With
  * eco_fp8_scales_from_absmax it is the reference's calibrate_kv_absmax + static_scales

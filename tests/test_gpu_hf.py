@@ -312,3 +312,104 @@ def test_generate_runs_on_the_cache() -> None:
     ids = prompt()
     out = em.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=12, pad_token_id=0)
     assert out[0, PROMPT:].tolist() == greedy(model, em.make_cache(PROMPT + 13), ids, 12)
+
+
+# ---- the reference's golden model (float32, head dim 16): dense fp8 buffers on the dense kernel ------------------
+
+
+class FP8Sim(DynamicLayer):
+    """CPU K/V through the oracle's fp8 round trip with the reference's scale modes (fp8.py:81-97): ``"token"``, or
+    a static scale (``"tensor"``)."""
+
+    def __init__(self, mode: str, scales: tuple[float, float] | None = None) -> None:
+        super().__init__()
+        self.mode, self.scales = mode, scales
+
+    def update(self, key_states, value_states, *args, **kwargs):
+        from oracle import fp8 as ofp8
+
+        def trip(x: torch.Tensor, i: int) -> torch.Tensor:
+            x = x.numpy()
+            scale = ofp8.token_scale(x, "e4m3") if self.mode == "token" else np.float32(self.scales[i])
+            raw = ofp8.fp8_encode(x, "e4m3", scale)
+            return torch.from_numpy(ofp8.fp8_decode(raw, "e4m3", scale, out="f32"))
+
+        return super().update(trip(key_states, 0), trip(value_states, 1))
+
+
+@torch.no_grad()
+def golden_greedy(model, cache, device: str) -> list[int]:
+    import test_golden_reference as golden
+
+    out = model(input_ids=golden.prompt()[None].to(device), past_key_values=cache, use_cache=True)
+    tokens = []
+    for _ in range(golden.NEW_TOKENS):
+        token = out.logits[:, -1].argmax(-1, keepdim=True)
+        tokens.append(int(token))
+        out = model(input_ids=token, past_key_values=cache, use_cache=True)
+    return tokens
+
+
+def test_the_hip_path_decodes_the_reference_fp8_golden_tokens() -> None:
+    """The reference's own golden tokens of ``FP8KVConfig()`` (tests/golden/catalog.py:168-170, computed on the CPU)
+    from its golden model on the GPU: ``kv_fp8_fused``'s dense fp8 buffers written by ``eco_fp8_encode`` and read as
+    fp8 by the dense decode kernel at every decoding step (fp32 queries as exact bf16 hi + lo MFMA operands)."""
+    import test_golden_reference as golden
+
+    from economize_amd.attention import kernel_usage
+    from economize_amd.hf import DenseFP8Layer, apply
+    from economize_amd.techniques import FusedFP8KVConfig
+
+    model = golden.golden_model().cuda()
+    em = apply(model, FusedFP8KVConfig())
+    cache = em.make_cache(golden.PROMPT + golden.NEW_TOKENS + 1)
+    assert all(isinstance(layer, DenseFP8Layer) and layer.fused for layer in cache.layers)
+    kernel_usage(reset=True)
+    assert golden_greedy(model, cache, "cuda") == golden.GOLDEN["kv_fp8_tokens"].tolist()
+    assert {(r["path"], r["queries"]) for r in kernel_usage(reset=True)} >= {("kernel", 1)}
+
+
+def test_per_token_fp8_scales_decode_like_the_oracle() -> None:
+    """``FP8KVConfig(scale="token")`` on the golden model: codes and per-token scales by ``eco_fp8_encode``, decoded
+    to fp32 for the dense kernel, give the tokens of the CPU model over the oracle's per-token round trip."""
+    import test_golden_reference as golden
+
+    from economize_amd.hf import apply
+    from economize_amd.techniques import FP8KVConfig
+
+    want = golden_greedy(golden.golden_model(), Cache(layers=[FP8Sim("token") for _ in range(6)]), "cpu")
+    model = golden.golden_model().cuda()
+    em = apply(model, FP8KVConfig(scale="token"))
+    assert golden_greedy(model, em.make_cache(64), "cuda") == want
+
+
+def test_tensor_fp8_scales_are_calibrated_and_decode_like_the_oracle() -> None:
+    """``FP8KVConfig(scale="tensor")`` calibrated on token batches at ``apply`` (calibrate_kv_absmax +
+    static_scales, fp8.py:100-133): the per-layer scales are the CPU model's within fp32 noise, and decoding gives the
+    tokens of the CPU model over the oracle's round trip with the same scales."""
+    import test_golden_reference as golden
+    from transformers import DynamicCache
+
+    from economize_amd.hf import apply
+    from economize_amd.techniques import FP8KVConfig
+
+    batches = [golden._tokens(3, 8, 32)]
+    cpu_model = golden.golden_model()
+    absmax = torch.zeros(2, 6)
+
+    class Recording(DynamicCache):
+        def update(self, key_states, value_states, layer_idx, *args, **kwargs):
+            absmax[0, layer_idx] = max(absmax[0, layer_idx], key_states.abs().amax())
+            absmax[1, layer_idx] = max(absmax[1, layer_idx], value_states.abs().amax())
+            return super().update(key_states, value_states, layer_idx, *args, **kwargs)
+
+    with torch.no_grad():
+        cpu_model(input_ids=batches[0], past_key_values=Recording(config=cpu_model.config), use_cache=True)
+    model = golden.golden_model().cuda()
+    em = apply(model, FP8KVConfig(scale="tensor"), calibration=batches)
+    scales = torch.stack([torch.stack([em.scales[i][j][0] for i in range(6)]) for j in range(2)])
+    torch.testing.assert_close(scales, absmax / 448.0, rtol=1e-5, atol=0)
+    assert all((em.scales[i][j] == em.scales[i][j][0]).all() for i in range(6) for j in range(2))
+    layers = [FP8Sim("tensor", (float(em.scales[i][0][0]), float(em.scales[i][1][0]))) for i in range(6)]
+    want = golden_greedy(golden.golden_model(), Cache(layers=layers), "cpu")
+    assert golden_greedy(model, em.make_cache(64), "cuda") == want

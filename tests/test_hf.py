@@ -41,10 +41,10 @@ def test_validate_refuses_what_the_path_cannot_run() -> None:
     FusedFP8KVConfig().validate(model)
     FusedKIVIConfig().validate(model)
     QuestConfig().validate(model.config)
-    with pytest.raises(ConfigError, match="per-head scales"):
-        FP8KVConfig(scale="token").validate(model)
-    with pytest.raises(ConfigError, match="per-head scales"):
-        FP8KVConfig(scale="tensor").validate(model)
+    for scale in ("none", "token", "tensor", "head"):
+        FP8KVConfig(scale=scale).validate(tiny_model(head_dim=32))  # dense fp8 buffers take any head dim
+    with pytest.raises(ConfigError, match="up to 256"):
+        FusedFP8KVConfig().validate(tiny_model(head_dim=512, attn="economize"))
     with pytest.raises(ConfigError, match="bits=8"):
         KIVIConfig(bits=8).validate(model)
     with pytest.raises(ConfigError, match="group_size=64"):
@@ -69,10 +69,28 @@ def test_apply_selects_the_kernel_and_refuses_conflicts() -> None:
         apply(tiny_model(), FusedFP8KVConfig(), FusedKIVIConfig())
     with pytest.raises(IncompatibleTechniquesError, match="twice"):
         apply(tiny_model(), FusedFP8KVConfig(layers=(1,)), FusedFP8KVConfig(layers=(2,)))
-    with pytest.raises(ConfigError, match="head dims"):
-        apply(tiny_model(head_dim=32), FusedFP8KVConfig())
-    with pytest.raises(ConfigError, match="scale='head'"):
-        apply(tiny_model(), FP8KVConfig(scale="head"))
+    with pytest.raises(ConfigError, match="calibrated at attach time"):
+        apply(tiny_model(), FP8KVConfig(scale="tensor"))
+    with pytest.raises(ConfigError, match="needs the paged fp8 cache"):
+        apply(tiny_model(head_dim=32), FusedFP8KVConfig(scale="head"))
+
+
+def test_fp8_layers_are_paged_where_the_paged_kernels_take_the_model() -> None:
+    """bf16 models of head dim 64 / 128 / 256 keep fp8 layers in the paged cache (scale none, tensor or head); a
+    per-token scale, another head dim or another dtype gets dense fp8 buffers (kv_fp8 decodes them for attention,
+    kv_fp8_fused hands the fp8 views to the kernel)."""
+    from economize_amd.hf import DenseFP8Layer, PagedLayer, apply
+
+    def layer_types(model, config):
+        cache = apply(model, config).make_cache(64)
+        return [(type(layer).__name__, getattr(layer, "fused", None)) for layer in cache.layers[:1]]
+
+    bf16 = tiny_model().to(torch.bfloat16)
+    assert layer_types(bf16, FusedFP8KVConfig()) == [("PagedLayer", None)]
+    assert layer_types(tiny_model().to(torch.bfloat16), FP8KVConfig(scale="token")) == [("DenseFP8Layer", False)]
+    assert layer_types(tiny_model(head_dim=16).to(torch.bfloat16), FusedFP8KVConfig()) == [("DenseFP8Layer", True)]
+    assert layer_types(tiny_model(), FusedFP8KVConfig()) == [("DenseFP8Layer", True)]  # float32
+    assert PagedLayer and DenseFP8Layer
 
 
 def test_a_cpu_call_falls_back_to_sdpa_and_is_logged() -> None:
