@@ -12,6 +12,7 @@
 #include "dense_attention.hpp"
 #include "gather.hpp"
 #include "kivi.hpp"
+#include "kivi_dense.hpp"
 #include "kv_quant.hpp"
 #include "paged_attention.hpp"
 #include "quest.hpp"
@@ -692,6 +693,24 @@ int eco_kivi_quantize(int32_t kind, const void* src, int32_t src_format, int64_t
     p.bits = bits;
     p.overflow = overflow;
     return kivi_quantize(p, kind, max_tokens, static_cast<hipStream_t>(stream));
+}
+
+int eco_kivi_fake_quantize(void* buffer, int32_t format, int64_t sb, int64_t sh, int64_t ss, int32_t batch,
+                           int32_t heads, int32_t slots, int32_t head_dim, int32_t start, int32_t stop, int32_t bits,
+                           int32_t group, int32_t keys, void* stream) {
+    if (!buffer) return fail("kivi fake quantize: null buffer");
+    if (format != BF16 && format != FP16 && format != FP32)
+        return fail("kivi fake quantize: the buffer must be bf16, fp16 or fp32");
+    if (bits != 2 && bits != 4 && bits != 8) return fail("kivi fake quantize: bits must be 2, 4 or 8");
+    if (batch < 0 || heads < 0 || head_dim <= 0 || group <= 0)
+        return fail("kivi fake quantize: bad shape or group");
+    if (start < 0 || stop < start || stop > slots) return fail("kivi fake quantize: slots out of the buffer");
+    if (keys != 0 && keys != 1) return fail("kivi fake quantize: keys must be 0 or 1");
+    if (keys && (stop - start) % group)
+        return fail("kivi fake quantize: the key slots must be whole groups of tokens");
+    if (!keys && head_dim % group) return fail("kivi fake quantize: the value group must divide the head dim");
+    KiviFakeParams p{buffer, format, sb, sh, ss, batch, heads, head_dim, start, stop, bits, group, keys};
+    return kivi_fake_quantize(p, static_cast<hipStream_t>(stream));
 }
 
 int eco_kivi_ring_write(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,

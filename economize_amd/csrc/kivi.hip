@@ -34,6 +34,7 @@
 
 #include "common.hpp"
 #include "kivi.hpp"
+#include "kivi_math.hpp"
 #include "stream_k.hpp"
 
 namespace eco {
@@ -46,11 +47,6 @@ __device__ inline float load_elem(const void* base, int64_t offset, int format) 
     if (format == BF16) return bf16_to_f32(static_cast<const uint16_t*>(base)[offset]);
     if (format == FP16) return static_cast<float>(static_cast<const _Float16*>(base)[offset]);
     return static_cast<const float*>(base)[offset];
-}
-
-// fp16r of the reference: x rounded to fp16 where |x| <= 65504, else x.
-__device__ inline float fp16_rounded(float x) {
-    return fabsf(x) <= 65504.0f ? static_cast<float>(static_cast<_Float16>(x)) : x;
 }
 
 __device__ inline uint16_t f16_bits(float x) {
@@ -107,25 +103,6 @@ __device__ inline uint8_t* page_block(const KiviQuantParams& p, int b, int h, in
     const int phys = p.block_table[b * p.bt_stride + page];
     if (phys < 0 || phys >= p.num_pages) return nullptr;
     return p.blocks + static_cast<int64_t>(phys) * p.blk_page + h * p.blk_head;
-}
-
-// (code, scale, low) arithmetic of one group: low / high in fp32, scale = fp16r((high - low) / levels).
-struct Quant {
-    float scale, low, safe;
-};
-
-__device__ inline Quant make_quant(float lo, float hi, int levels, uint32_t* overflow) {
-    Quant q;
-    q.scale = fp16_rounded(__fdiv_rn(hi - lo, static_cast<float>(levels)));
-    q.low = fp16_rounded(lo);
-    q.safe = q.scale > 0.0f ? q.scale : 1.0f;
-    if (overflow && (fabsf(q.scale) > 65504.0f || fabsf(q.low) > 65504.0f)) atomicOr(overflow, 1u);
-    return q;
-}
-
-__device__ inline uint32_t code_of(float x, const Quant& q, int levels) {
-    const float c = rintf(__fdiv_rn(x - q.low, q.safe));
-    return static_cast<uint32_t>(fminf(fmaxf(c, 0.0f), static_cast<float>(levels)));
 }
 
 // Keys: one workgroup per (row, KV head) and 32-token group in [from, to) (multiples of 32).

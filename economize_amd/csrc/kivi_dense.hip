@@ -1,0 +1,86 @@
+// KIVI's simulated storage (the reference's KIVICache, techniques/kv_quant/kivi.py:178-275): committed K/V are
+// quantized in place inside the dense [B, H, S, D] buffers of the model's dtype. A key group is one channel over
+// `group` tokens, a value group `group` channels of one token (the whole head when `group` does not divide it,
+// value_group of kivi.py:143-154); every element is replaced by code * scale + low computed in fp32 (the product,
+// then the sum: kivi.py:117) and rounded to the buffer's dtype. These are the values the fused kernels dequantize, so
+// attention over the buffer is the attention over the codes. Any bits (2, 4, 8) and group size.
+//
+// Minimum and maximum propagate NaN as torch's amin / amax do, and a NaN code stays NaN, so a group holding NaN
+// becomes NaN, as in the reference. One thread per group; O(quantized tokens) bytes, off the decode path.
+
+#include "common.hpp"
+#include "kivi_dense.hpp"
+#include "kivi_math.hpp"
+
+namespace eco {
+
+namespace {
+
+__device__ inline float load_value(const void* base, int64_t offset, int format) {
+    if (format == BF16) return bf16_to_f32(static_cast<const uint16_t*>(base)[offset]);
+    if (format == FP16) return static_cast<float>(static_cast<const _Float16*>(base)[offset]);
+    return static_cast<const float*>(base)[offset];
+}
+
+__device__ inline void store_value(void* base, int64_t offset, int format, float x) {
+    if (format == BF16)
+        static_cast<uint16_t*>(base)[offset] = f32_to_bf16(x);
+    else if (format == FP16)
+        static_cast<_Float16*>(base)[offset] = static_cast<_Float16>(x);
+    else
+        static_cast<float*>(base)[offset] = x;
+}
+
+__device__ inline float dequantized(float code, const Quant& q) {
+    return __fadd_rn(__fmul_rn(code, q.scale), q.low);  // product then sum, each rounded (no contraction)
+}
+
+// Thread per group: keys (b, h, token group, channel), values (b, h, token, channel group). Elements of a group are
+// `step` apart in the buffer (the token stride for keys, 1 for values).
+__global__ __launch_bounds__(256) void kivi_fake_quant_kernel(KiviFakeParams p) {
+    const int levels = (1 << p.bits) - 1;
+    const int tokens = p.stop - p.start;
+    const int per_row = p.keys ? (tokens / p.group) * p.head_dim : tokens * (p.head_dim / p.group);
+    const int64_t total = static_cast<int64_t>(p.batch) * p.heads * per_row;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int item = static_cast<int>(i % per_row);
+        const int h = static_cast<int>((i / per_row) % p.heads);
+        const int b = static_cast<int>(i / (static_cast<int64_t>(per_row) * p.heads));
+        int64_t first, step;
+        if (p.keys) {
+            const int tg = item / p.head_dim, d = item % p.head_dim;
+            first = b * p.sb + h * p.sh + static_cast<int64_t>(p.start + tg * p.group) * p.ss + d;
+            step = p.ss;
+        } else {
+            const int t = item / (p.head_dim / p.group), g = item % (p.head_dim / p.group);
+            first = b * p.sb + h * p.sh + static_cast<int64_t>(p.start + t) * p.ss + g * p.group;
+            step = 1;
+        }
+        float lo = load_value(p.buf, first, p.format), hi = lo;
+        for (int e = 1; e < p.group; ++e) {
+            const float x = load_value(p.buf, first + e * step, p.format);
+            lo = __builtin_elementwise_minimum(lo, x);
+            hi = __builtin_elementwise_maximum(hi, x);
+        }
+        const Quant q = make_quant(lo, hi, levels, nullptr);
+        for (int e = 0; e < p.group; ++e) {
+            const float x = load_value(p.buf, first + e * step, p.format);
+            store_value(p.buf, first + e * step, p.format, dequantized(code_or_nan(x, q, levels), q));
+        }
+    }
+}
+
+}  // namespace
+
+int kivi_fake_quantize(const KiviFakeParams& p, hipStream_t stream) {
+    const int tokens = p.stop - p.start;
+    const int64_t groups = static_cast<int64_t>(p.batch) * p.heads *
+                           (p.keys ? (tokens / p.group) * p.head_dim : tokens * (p.head_dim / p.group));
+    if (groups == 0) return 0;
+    const int blocks = static_cast<int>((groups + 255) / 256 < 65535 ? (groups + 255) / 256 : 65535);
+    hipLaunchKernelGGL(kivi_fake_quant_kernel, dim3(blocks), dim3(256), 0, stream, p);
+    return check_launch("kivi_fake_quant_kernel");
+}
+
+}  // namespace eco

@@ -13,7 +13,9 @@ for the techniques of this path:
   Static scales (``"tensor"``, and ``"head"`` per KV head) are calibrated at attach time (fp8.py:100-133).
 * ``KIVIConfig`` / ``FusedKIVIConfig``: new tokens in the bf16 ring, the reference's schedule run at every pass
   boundary (the tokens a pass commits are quantized when it ends, kivi.py:191-243), attention on the fused KIVI
-  kernel over codes and ring (kv_kivi_fused/fused.py:152-208).
+  kernel over codes and ring (kv_kivi_fused/fused.py:152-208). Configurations the paged KIVI cache cannot hold
+  (8-bit codes, groups other than 32, other head dims or dtypes) use the simulated storage
+  (:class:`SimulatedKIVILayer`: dense buffers quantized in place, kivi.py:178-275).
 * ``QuestConfig``: a paged cache (fp8 with an fp8 technique on the same layer is refused, as the reference refuses
   Quest over packed formats) whose page bounds are kept for the committed pages, ``done[b]`` = committed full pages
   before the pass; a decoding query of a covered layer reads the selected pages and the tail
@@ -37,7 +39,7 @@ from transformers.cache_utils import Cache, CacheLayerMixin, DynamicLayer
 from .attention import MAX_QUERIES, NAME, PagedKV, install
 from .errors import ConfigError, IncompatibleTechniquesError
 from .fp8 import calibrate_kv_absmax, fp8_encode, static_scales
-from .kivi import KIVI_PAGE, PagedKIVICache, kivi_append, kivi_commit, kivi_quantize
+from .kivi import KIVI_PAGE, PagedKIVICache, kivi_append, kivi_commit, kivi_fake_quantize, kivi_quantize
 from .packed import attach_packed, stand_in
 from .paged import PAGE, PagedKVCache, paged_append
 from .quest import QuestPages, page_bounds
@@ -45,7 +47,8 @@ from .techniques import (FP8KVConfig, FusedFP8KVConfig, KIVIConfig, QuestConfig,
                          head_dim_of,
                          technique_for)
 
-__all__ = ["EconomizeCache", "EconomizedModel", "KIVILayer", "PagedLayer", "apply"]
+__all__ = ["DenseFP8Layer", "EconomizeCache", "EconomizedModel", "KIVILayer", "PagedLayer", "SimulatedKIVILayer",
+           "apply"]
 
 
 class _PagedBase(CacheLayerMixin):
@@ -377,6 +380,70 @@ class KIVILayer(_PagedBase):
         self.kq = self.vq = 0
 
 
+class SimulatedKIVILayer(CacheLayerMixin):
+    """KIVI's simulated storage (the reference's ``KIVICache``, kivi.py:178-275): dense ``[B, Hkv, capacity, D]``
+    buffers of the model's dtype whose committed entries are quantized in place when the next pass begins (keys below
+    ``(c // R) * R``, values below ``c - R``) by ``eco_kivi_fake_quantize``; attention reads the buffers (the dense
+    kernel). The values held are the ones the fused kernels dequantize, so any bits, group size and head dim run with
+    the paged technique's results, at the dense cache's size."""
+
+    is_sliding = False
+    is_compileable = False
+    supports_early_init = False
+
+    def __init__(self, capacity: int, config: KIVIConfig) -> None:
+        super().__init__()
+        self.capacity = int(capacity)
+        self.config = config
+        self.length = self.committed = self.kq = self.vq = 0
+        self.buffers: tuple[torch.Tensor, torch.Tensor] | None = None
+
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        batch, heads, _, dim = key_states.shape
+        self.buffers = tuple(torch.zeros(batch, heads, self.capacity, dim, dtype=key_states.dtype,
+                                         device=key_states.device) for _ in range(2))
+        self.is_initialized = True
+
+    def get_seq_length(self) -> int:
+        return self.length
+
+    def get_mask_sizes(self, query_length: int) -> tuple[int, int]:
+        return self.length + query_length, 0
+
+    def get_max_length(self) -> int:
+        return self.capacity
+
+    def pass_begin(self, frontier: int) -> None:
+        """Quantize what the schedule quantizes once ``frontier`` tokens are committed (kivi.py:230-243)."""
+        c = self.config
+        k_to, v_to = max(self.kq, (frontier // c.residual_length) * c.residual_length), max(self.vq, frontier -
+                                                                                            c.residual_length)
+        if k_to > self.kq:
+            kivi_fake_quantize(self.buffers[0], self.kq, k_to, c.bits, c.group_size, "k")
+        if v_to > self.vq:
+            kivi_fake_quantize(self.buffers[1], self.vq, v_to, c.bits, c.group_size, "v")
+        self.kq, self.vq, self.committed = k_to, v_to, frontier
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs
+               ) -> tuple[torch.Tensor, torch.Tensor]:
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        if self.length > self.committed:
+            self.pass_begin(self.length)
+        tokens = key_states.shape[2]
+        if self.length + tokens > self.capacity:
+            raise ConfigError(f"the cache holds {self.capacity} tokens per row; writing {tokens} more after "
+                              f"{self.length} exceeds it (make the cache with a larger max_length)")
+        new = slice(self.length, self.length + tokens)
+        self.buffers[0][:, :, new].copy_(key_states)
+        self.buffers[1][:, :, new].copy_(value_states)
+        self.length += tokens
+        return tuple(b[:, :, : self.length] for b in self.buffers)
+
+    def reset(self) -> None:
+        self.length = self.committed = self.kq = self.vq = 0
+
+
 class EconomizeCache(Cache):
     """transformers ``past_key_values`` whose layers are the techniques' paged caches (dense ``DynamicLayer`` for a
     layer no technique covers)."""
@@ -428,7 +495,9 @@ class EconomizedModel:
         for index in range(config.num_hidden_layers):
             technique = self.technique_of(index + 1)
             cfg = technique.config if technique is not None else None
-            if isinstance(cfg, KIVIConfig):
+            if isinstance(cfg, KIVIConfig) and cfg.simulated(self.model):
+                layers.append(SimulatedKIVILayer(max_length, cfg))
+            elif isinstance(cfg, KIVIConfig):
                 layers.append(KIVILayer(max_length, cfg))
             elif isinstance(cfg, FP8KVConfig) and self.paged_fp8(cfg):
                 layers.append(PagedLayer(max_length, cfg.dtype, scales=self.scales.get(index)))

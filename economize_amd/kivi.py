@@ -24,7 +24,8 @@ from . import _lib
 from .errors import ConfigError
 from .paged import cached_workspace, counter_bytes, packed_mask
 
-__all__ = ["KIVI_PAGE", "PagedKIVICache", "kivi_append", "kivi_commit", "kivi_decode_attention", "kivi_gather",
+__all__ = ["KIVI_PAGE", "PagedKIVICache", "kivi_append", "kivi_commit", "kivi_decode_attention", "kivi_fake_quantize",
+           "kivi_gather",
            "kivi_quantize"]
 
 #: Tokens per KIVI page.
@@ -273,3 +274,25 @@ def kivi_gather(cache: PagedKIVICache, block_table: torch.Tensor, keys: int, dty
                   *v.stride()[:3], cache.batch, cache.kv_heads, int(keys), cache.head_dim, cache.bits, cache.group,
                   _lib.stream_of(device))
     return k, v
+
+
+def value_group(dim: int, group: int) -> int:
+    """Channels per value group: ``group``, or the whole head when ``group`` does not divide it (kivi.py:143-154)."""
+    return group if dim % group == 0 else dim
+
+
+def kivi_fake_quantize(buffer: torch.Tensor, start: int, stop: int, bits: int, group: int, kind: str) -> None:
+    """KIVI's simulated storage: slots ``start:stop`` of a dense K or V buffer ``[B, H, S, D]`` (bf16, fp16 or
+    fp32, contiguous channels) quantized in place (``kind`` ``"k"``: per channel over groups of ``group`` tokens;
+    ``"v"``: per token over groups of :func:`value_group` channels), every element replaced by ``code * scale + low``
+    rounded to the buffer's dtype (``KIVICache._quantize``, techniques/kv_quant/kivi.py:257-275)."""
+    device = _lib.require_gpu(buffer)
+    if buffer.dim() != 4 or buffer.stride(3) != 1:
+        raise ConfigError("kivi_fake_quantize takes a [B, H, S, D] buffer with contiguous channels")
+    if kind not in ("k", "v"):
+        raise ConfigError(f"kind must be 'k' or 'v', not {kind!r}")
+    batch, heads, slots, dim = buffer.shape
+    g = group if kind == "k" else value_group(dim, group)
+    _lib.call("eco_kivi_fake_quantize", buffer.data_ptr(), _lib.fmt(buffer.dtype), buffer.stride(0),
+              buffer.stride(1), buffer.stride(2), batch, heads, slots, dim, int(start), int(stop), int(bits), g,
+              1 if kind == "k" else 0, _lib.stream_of(device))

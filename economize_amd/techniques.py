@@ -76,6 +76,34 @@ def _head_dims(technique: str, adapter, dims: tuple[int, ...]) -> None:
         raise ConfigError(f"{technique}: the MI355X kernels take head dims {list(dims)}, the model has {dim}")
 
 
+def model_dtype(adapter) -> torch.dtype | None:
+    """The dtype of a model's parameters, or ``None`` when ``adapter`` is no module."""
+    parameters = getattr(adapter, "parameters", None)
+    if parameters is None:
+        return None
+    first = next(iter(parameters()), None)
+    return None if first is None else first.dtype
+
+
+def kivi_paged_refusal(config, adapter) -> str | None:
+    """Why the paged KIVI cache (32-token pages of 2- or 4-bit codes read by the fused kernel) cannot hold
+    ``config``'s layers on this model, or ``None`` when it can; such layers use the simulated storage (dense buffers
+    quantized in place, any bits, group and head dim), as the reference falls back to it (kivi.py:62-66)."""
+    if config.bits not in (2, 4):
+        return f"bits={config.bits}"
+    if config.group_size != 32:
+        return f"group_size={config.group_size}"
+    dim = head_dim_of(adapter)
+    if dim is not None and dim not in (64, 128):
+        return f"head dim {dim}"
+    dtype = model_dtype(adapter)
+    if dtype is not None and dtype != torch.bfloat16:
+        return f"a {dtype} model"
+    if config.headroom < 64:
+        return f"headroom {config.headroom} (below 64 decoding queries)"
+    return None
+
+
 def _needs_kernel(technique: str, implementation: str, accepts, what: str, instead: str | None) -> None:
     """Refuses an attention implementation that cannot read the technique's cache (fused.py:44-49)."""
     from .attention import ATTENTION_KERNELS
@@ -228,16 +256,21 @@ class KIVIConfig(TechniqueConfig):
                 raise ConfigError(f"{self.technique} supports only storage='simulated', got {self.storage!r}")
 
     def validate(self, adapter) -> None:
-        """Refuses, before anything attaches, what the paged KIVI cache cannot hold: 8-bit codes, groups other than
-        32 tokens / channels (one group is one 32-token page), simulated storage and head dims the kernels do not
-        take."""
-        if self.bits not in (2, 4):
-            raise ConfigError(f"the paged KIVI cache holds 2- and 4-bit codes, not bits={self.bits}")
-        if self.group_size != 32:
-            raise ConfigError(f"the paged KIVI cache quantizes groups of 32, not group_size={self.group_size}")
-        if self.storage == "simulated" and self.packable:
-            raise ConfigError("the paged KIVI cache is packed storage, not storage='simulated'")
-        _head_dims(self.technique, adapter, (64, 128))
+        """An explicit ``storage="packed"`` the paged KIVI cache cannot hold on this model is refused (the
+        reference's explicit packed storage raises where it cannot run, kivi.py:62-66); otherwise a configuration
+        the paged cache cannot hold runs on the simulated storage, and the dense kernel takes head dims up to 256."""
+        if self.storage == "packed":
+            why = kivi_paged_refusal(self, adapter)
+            if why is not None:
+                raise ConfigError(f"storage='packed' is the paged KIVI cache, which cannot hold {why}; use storage="
+                                  "None or 'simulated'")
+        dim = head_dim_of(adapter)
+        if dim is not None and dim > 256:
+            raise ConfigError(f"{self.technique}: the MI355X kernels take head dims up to 256, the model has {dim}")
+
+    def simulated(self, adapter) -> bool:
+        """Whether this configuration's layers use the simulated storage on ``adapter``'s model."""
+        return self.storage == "simulated" or kivi_paged_refusal(self, adapter) is not None
 
     @property
     def kivi_storage(self) -> str:
@@ -254,6 +287,11 @@ class FusedKIVIConfig(KIVIConfig):
 
     technique: ClassVar[str] = "kivi_fused"
     packable: ClassVar[bool] = False
+
+    def simulated(self, adapter) -> bool:
+        """The fused kernel reads the paged codes wherever the paged cache holds them; elsewhere the simulated
+        storage holds the values that kernel would dequantize (code * scale + zero in the model's dtype)."""
+        return kivi_paged_refusal(self, adapter) is not None
 
     def validate(self, adapter) -> None:
         """Refuses an attention implementation that does not read KIVI codes (kv_kivi_fused/fused.py:43-51)."""

@@ -221,6 +221,16 @@ int eco_kivi_quantize(int32_t kind, const void* src, int32_t src_format, int64_t
                       int32_t bt_cols, int32_t batch, int32_t kv_heads, int32_t head_dim, int32_t bits,
                       int32_t group, int32_t max_tokens, uint32_t* overflow, void* stream);
 
+/* KIVI's simulated storage: quantizes slots [start, stop) of every row of a dense buffer [B, H, slots, D] (element
+ * strides sb, sh, ss, channel stride 1; bf16, fp16 or fp32) in place, keys (keys = 1: per channel over groups of
+ * `group` tokens, stop - start a multiple of group) or values (keys = 0: per token over groups of `group` channels,
+ * group dividing D), each element replaced by code * scale + low in fp32 rounded to the buffer's dtype; bits 2, 4 or
+ * 8, any group. Replaces KIVICache._quantize_block / _quantize with quantize and fake_quantize
+ * (techniques/kv_quant/kivi.py:110-140, 257-275). */
+int eco_kivi_fake_quantize(void* buffer, int32_t format, int64_t sb, int64_t sh, int64_t ss, int32_t batch,
+                           int32_t heads, int32_t slots, int32_t head_dim, int32_t start, int32_t stop, int32_t bits,
+                           int32_t group, int32_t keys, void* stream);
+
 /* Writes new tokens k_new / v_new [T, Hkv, D] (element strides, channel stride 1) into the rings at slot
  * positions[t] % ring of row rows[t] (negative positions skip), rounded to bf16 (the reference's ring writes,
  * kv_quant/packed.py:258-277). */

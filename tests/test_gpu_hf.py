@@ -413,3 +413,24 @@ def test_tensor_fp8_scales_are_calibrated_and_decode_like_the_oracle() -> None:
     layers = [FP8Sim("tensor", (float(em.scales[i][0][0]), float(em.scales[i][1][0]))) for i in range(6)]
     want = golden_greedy(golden.golden_model(), Cache(layers=layers), "cpu")
     assert golden_greedy(model, em.make_cache(64), "cuda") == want
+
+
+def test_the_hip_path_decodes_the_reference_kivi_golden_tokens() -> None:
+    """The reference's own golden tokens of ``KIVIConfig(bits=2, group_size=4, residual_length=8)``
+    (tests/golden/catalog.py:163-165) from its golden model on the GPU: groups of 4 are not the paged cache's, so the
+    layers use the simulated storage (buffers quantized in place by ``eco_kivi_fake_quantize`` at every pass
+    boundary) and every decoding step runs on the dense decode kernel."""
+    import test_golden_reference as golden
+
+    from economize_amd.attention import kernel_usage
+    from economize_amd.hf import SimulatedKIVILayer, apply
+    from economize_amd.techniques import KIVIConfig
+
+    model = golden.golden_model().cuda()
+    em = apply(model, KIVIConfig(bits=2, group_size=4, residual_length=8))
+    cache = em.make_cache(golden.PROMPT + golden.NEW_TOKENS + 1)
+    assert all(isinstance(layer, SimulatedKIVILayer) for layer in cache.layers)
+    kernel_usage(reset=True)
+    assert golden_greedy(model, cache, "cuda") == golden.GOLDEN["kv_kivi_2bit_tokens"].tolist()
+    assert {(r["path"], r["queries"]) for r in kernel_usage(reset=True)} >= {("kernel", 1)}
+    assert (cache.layers[0].kq, cache.layers[0].vq) == (32, 31)  # 39 committed tokens before the last pass

@@ -45,14 +45,15 @@ def test_validate_refuses_what_the_path_cannot_run() -> None:
         FP8KVConfig(scale=scale).validate(tiny_model(head_dim=32))  # dense fp8 buffers take any head dim
     with pytest.raises(ConfigError, match="up to 256"):
         FusedFP8KVConfig().validate(tiny_model(head_dim=512, attn="economize"))
+    for config in (KIVIConfig(bits=8), KIVIConfig(group_size=64, residual_length=128), KIVIConfig(storage="simulated"),
+                   KIVIConfig(bits=4, group_size=4, residual_length=8)):
+        config.validate(model)  # the simulated storage takes what the paged cache cannot hold
     with pytest.raises(ConfigError, match="bits=8"):
-        KIVIConfig(bits=8).validate(model)
+        KIVIConfig(bits=8, storage="packed").validate(model)
     with pytest.raises(ConfigError, match="group_size=64"):
-        KIVIConfig(group_size=64, residual_length=128).validate(model)
-    with pytest.raises(ConfigError, match="simulated"):
-        KIVIConfig(storage="simulated").validate(model)
-    with pytest.raises(ConfigError, match="head dims"):
-        FusedKIVIConfig().validate(tiny_model(head_dim=256).config)
+        KIVIConfig(group_size=64, residual_length=128, storage="packed").validate(model)
+    with pytest.raises(ConfigError, match="up to 256"):
+        FusedKIVIConfig().validate(tiny_model(head_dim=512, attn="economize"))
     with pytest.raises(IncompatibleTechniquesError, match="economize"):
         FusedFP8KVConfig().validate(tiny_model())  # the model runs sdpa
 
@@ -112,3 +113,22 @@ def test_a_cpu_call_falls_back_to_sdpa_and_is_logged() -> None:
     want, _ = sdpa_attention_forward(module, q, k, v, mask, scaling=0.125)
     assert torch.equal(got, want)
     assert kernel_usage() == [{"layer": 3, "queries": 1, "path": "sdpa", "reason": "cpu", "calls": 1}]
+
+
+def test_kivi_layers_are_paged_where_the_paged_cache_holds_them() -> None:
+    """2- and 4-bit codes in groups of 32 on a bf16 model of head dim 64 / 128 live in the paged KIVI cache; 8-bit
+    codes, other groups, head dims and dtypes, and storage='simulated' get the simulated storage (kivi.py:62-66)."""
+    from economize_amd.hf import apply
+
+    def layer_type(model, config) -> str:
+        return type(apply(model, config).make_cache(64).layers[0]).__name__
+
+    bf16 = tiny_model().to(torch.bfloat16)
+    assert layer_type(bf16, FusedKIVIConfig()) == "KIVILayer"
+    assert layer_type(tiny_model().to(torch.bfloat16), KIVIConfig(bits=4)) == "KIVILayer"
+    assert layer_type(tiny_model().to(torch.bfloat16), KIVIConfig(storage="simulated")) == "SimulatedKIVILayer"
+    assert layer_type(tiny_model().to(torch.bfloat16), KIVIConfig(bits=8)) == "SimulatedKIVILayer"
+    assert layer_type(tiny_model().to(torch.bfloat16), FusedKIVIConfig(group_size=16, residual_length=32)) == \
+        "SimulatedKIVILayer"
+    assert layer_type(tiny_model(head_dim=16).to(torch.bfloat16), KIVIConfig()) == "SimulatedKIVILayer"
+    assert layer_type(tiny_model(), FusedKIVIConfig()) == "SimulatedKIVILayer"  # float32
