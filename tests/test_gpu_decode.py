@@ -70,6 +70,8 @@ CASES = [
     (2, 8, 8, 1, 2000, 256, 256, torch.bfloat16, torch.bfloat16, "window", False),
     (2, 16, 4, 2, 77, 64, 64, torch.float16, torch.float8_e4m3fn, "empty_row", False),
     (1, 4, 1, 1, 1, 128, 128, torch.bfloat16, torch.bfloat16, None, False),
+    (2, 4, 2, 1, 300, 16, 16, torch.float32, torch.float8_e4m3fn, None, False),  # the golden model's head dim
+    (2, 8, 2, 2, 333, 48, 48, torch.bfloat16, torch.bfloat16, "causal", False),
     (2, 12, 4, 1, 3000, 128, 128, torch.float32, torch.float8_e4m3fn, "holes", True),
 ]
 
