@@ -62,6 +62,8 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
     "eco_kivi_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I]),
     "eco_kivi_decode": (c_int32, [_P, _L, _L, _L, _P, _I, _P, _P, _I, _P, _P, _P, _L, _I, _P, _P, _P, _L, _L, _L, _I, _I,
                                   _I, _I, _I, _I, _I, _I, _F, _F] + _MASK + [_P, _S, _P]),
+    "eco_quest_refresh_bounds": (c_int32, [_P, _I, _I, _P, _L, _I, _P, _P, _P, _I, _P, _P, _L, _L, _L, _I, _I, _I, _I,
+                                           _I, _P]),
     "eco_quest_select": (c_int32, [_P, _L, _L, _L, _P, _P, _L, _L, _L, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _S,
                                    _P]),
 }

@@ -851,7 +851,54 @@ int eco_quest_page_bounds(const void* k_cache, int32_t kv_format, int32_t num_pa
     p.batch = batch;
     p.kv_heads = kv_heads;
     p.head_dim = head_dim;
+    p.committed = nullptr;
+    p.valid = nullptr;
+    p.done = nullptr;
+    p.page_cap = 0;
     return quest_bounds(p, static_cast<hipStream_t>(stream));
+}
+
+int eco_quest_refresh_bounds(const void* k_cache, int32_t kv_format, int32_t num_pages, const int32_t* block_table,
+                             int64_t bt_stride, int32_t bt_cols, const int32_t* committed, int32_t* valid,
+                             int32_t* done, int32_t quest_page_size, void* kmin, void* kmax, int64_t sb_b,
+                             int64_t sb_h, int64_t sb_p, int32_t page_cap, int32_t batch, int32_t kv_heads,
+                             int32_t head_dim, int32_t page_size, void* stream) {
+    if (!k_cache || !block_table || !kmin || !kmax || !committed || !valid)
+        return fail("quest refresh: null cache, table, bounds, committed or valid");
+    if (batch <= 0 || kv_heads <= 0 || num_pages <= 0 || bt_cols <= 0 || bt_stride < bt_cols || page_cap < 0)
+        return fail("quest refresh: batch, heads, pages and block-table columns must be positive");
+    if (page_size != 16) return fail("quest refresh: cache pages must hold 16 tokens");
+    if (quest_page_size < 16 || quest_page_size % 16 || (quest_page_size & (quest_page_size - 1)))
+        return fail("quest refresh: quest pages must hold a power of two of at least 16 tokens");
+    if (kv_format != BF16 && kv_format != FP8_E4M3 && kv_format != FP8_E5M2)
+        return fail("quest refresh: KV format must be bf16, fp8 e4m3 or fp8 e5m2");
+    const int es = kv_format == BF16 ? 2 : 1;
+    if (head_dim <= 0 || (head_dim * es) % 64) return fail("quest refresh: head dim must fill whole runs");
+    BoundsParams p;
+    p.k_cache = static_cast<const uint8_t*>(k_cache);
+    p.kc_head = static_cast<int64_t>(head_dim) * 16 * es;
+    p.kc_page = p.kc_head * kv_heads;
+    p.kv_format = kv_format;
+    p.num_pages = num_pages;
+    p.block_table = block_table;
+    p.bt_stride = bt_stride;
+    p.bt_cols = bt_cols;
+    p.first = 0;
+    p.last = 0;
+    p.span = quest_page_size / 16;
+    p.kmin = static_cast<uint16_t*>(kmin);
+    p.kmax = static_cast<uint16_t*>(kmax);
+    p.sb_b = sb_b;
+    p.sb_h = sb_h;
+    p.sb_p = sb_p;
+    p.batch = batch;
+    p.kv_heads = kv_heads;
+    p.head_dim = head_dim;
+    p.committed = committed;
+    p.valid = valid;
+    p.done = done;
+    p.page_cap = page_cap;
+    return quest_refresh(p, static_cast<hipStream_t>(stream));
 }
 
 size_t eco_quest_select_workspace_size(int32_t batch, int32_t kv_heads, int32_t max_done) {

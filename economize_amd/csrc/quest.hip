@@ -48,17 +48,12 @@ __device__ inline float decode_elem(const uint8_t* p, int i) {
     }
 }
 
-// One wave per (row b, Quest page p, KV head): lane l holds token l % 16 of the runs l / 16, l / 16 + 4, ... of
-// every cache page of the Quest page; the 16 lanes of a run then reduce over the tokens.
+// The bounds of Quest page qp of (row b, KV head kvh) by one wave: lane l holds token l % 16 of the runs l / 16,
+// l / 16 + 4, ... of every cache page of the Quest page; the 16 lanes of a run then reduce over the tokens.
 template <int FMT>
-__global__ __launch_bounds__(64) void quest_bounds_kernel(BoundsParams p) {
+__device__ inline void bounds_of_page(const BoundsParams& p, int b, int qp, int kvh, int lane) {
     constexpr int ES = FMT == BF16 ? 2 : 1;
     constexpr int X = 16 / ES;  // channels per 16-byte run
-    const int pages = p.last - p.first;
-    const int b = blockIdx.x / pages;
-    const int qp = p.first + blockIdx.x % pages;
-    const int kvh = blockIdx.y;
-    const int lane = threadIdx.x;
     const int runs = p.head_dim / X;
     const int token = lane & 15;
     // every cache page of the Quest page must be held (a missing one leaves the bounds untouched)
@@ -107,6 +102,36 @@ __global__ __launch_bounds__(64) void quest_bounds_kernel(BoundsParams p) {
             }
         }
     }
+}
+
+// One wave per (row b, Quest page first + i, KV head).
+template <int FMT>
+__global__ __launch_bounds__(64) void quest_bounds_kernel(BoundsParams p) {
+    const int pages = p.last - p.first;
+    bounds_of_page<FMT>(p, blockIdx.x / pages, p.first + blockIdx.x % pages, blockIdx.y, threadIdx.x);
+}
+
+// The bounds of the pages each (row, KV head) committed since its last refresh, with every range on the device (a
+// launch of fixed shape, so a decode step that keeps its Quest metadata can be captured in a graph): workgroup
+// (b * Hkv + h, y) takes pages valid + y, valid + y + Y, ... below the row's committed pages.
+template <int FMT>
+__global__ __launch_bounds__(64) void quest_refresh_kernel(BoundsParams p) {
+    const int row = blockIdx.x;
+    const int b = row / p.kv_heads, kvh = row % p.kv_heads;
+    const int last = min(max(p.committed[b], 0) / (16 * p.span), p.page_cap);
+    for (int qp = p.valid[row] + static_cast<int>(blockIdx.y); qp < last; qp += gridDim.y)
+        bounds_of_page<FMT>(p, b, qp, kvh, threadIdx.x);
+}
+
+// After quest_refresh_kernel (the next launch on the stream): the refreshed pages are final, and done[b] is the
+// row's committed Quest pages.
+__global__ void quest_mark_kernel(BoundsParams p) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= p.batch * p.kv_heads) return;
+    const int b = row / p.kv_heads;
+    const int last = min(max(p.committed[b], 0) / (16 * p.span), p.page_cap);
+    p.valid[row] = max(p.valid[row], last);
+    if (p.done && row % p.kv_heads == 0) p.done[b] = last;
 }
 
 // Scores of pages [chunk * blockIdx.x, +chunk) of row (b, kvh) = blockIdx.y: L lanes per page (L = the run count
@@ -483,6 +508,22 @@ int quest_bounds(const BoundsParams& p, hipStream_t stream) {
         default: return fail("quest page bounds: KV format must be bf16, fp8 e4m3 or fp8 e5m2");
     }
     return check_launch("quest_bounds_kernel");
+}
+
+int quest_refresh(const BoundsParams& p, hipStream_t stream) {
+    const int rows = p.batch * p.kv_heads;
+    if (rows == 0) return 0;
+    constexpr int CHUNKS = 8;  // waves per (row, KV head): a decode step completes at most one page per row
+    dim3 grid(rows, CHUNKS);
+    switch (p.kv_format) {
+        case BF16: hipLaunchKernelGGL(quest_refresh_kernel<BF16>, grid, dim3(64), 0, stream, p); break;
+        case FP8_E4M3: hipLaunchKernelGGL(quest_refresh_kernel<FP8_E4M3>, grid, dim3(64), 0, stream, p); break;
+        case FP8_E5M2: hipLaunchKernelGGL(quest_refresh_kernel<FP8_E5M2>, grid, dim3(64), 0, stream, p); break;
+        default: return fail("quest refresh: KV format must be bf16, fp8 e4m3 or fp8 e5m2");
+    }
+    if (int rc = check_launch("quest_refresh_kernel")) return rc;
+    hipLaunchKernelGGL(quest_mark_kernel, dim3((rows + 255) / 256), dim3(256), 0, stream, p);
+    return check_launch("quest_mark_kernel");
 }
 
 int quest_select(const SelectParams& p, hipStream_t stream) {

@@ -19,6 +19,11 @@ struct BoundsParams {
     uint16_t* kmax;
     int64_t sb_b, sb_h, sb_p;
     int batch, kv_heads, head_dim;
+    // device-driven refresh (quest_refresh): pages [valid[b * Hkv + h], min(committed[b] / (16 * span), page_cap))
+    const int32_t* committed;  // [B] committed tokens
+    int32_t* valid;            // [B * Hkv] Quest pages whose bounds are final
+    int32_t* done;             // optional [B]: committed Quest pages, written for the selection and the attention
+    int page_cap;              // Quest pages the bounds hold
 };
 
 struct SelectParams {
@@ -36,6 +41,7 @@ struct SelectParams {
 };
 
 int quest_bounds(const BoundsParams& p, hipStream_t stream);
+int quest_refresh(const BoundsParams& p, hipStream_t stream);
 int quest_select(const SelectParams& p, hipStream_t stream);
 int quest_score_chunk(int head_dim);  // pages scored per workgroup
 

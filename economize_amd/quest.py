@@ -10,6 +10,9 @@ Mirrors the reference's attention/quest.py and the bound maintenance of techniqu
 * :class:`QuestPages` carries one layer's bounds like the reference's ``QuestPages`` (attention/quest.py:112-204), and
   :func:`quest_decode_attention` attends over the selected pages and the dense tail from page ``done[b]`` on
   (attention/quest.py:239-344) with the paged decode kernel.
+* :class:`QuestState` keeps a layer's bounds up to date as pages are committed with every count on the device
+  (``eco_quest_refresh_bounds``), so that a decode step of fixed shapes can be captured in a graph, which the
+  reference's host ``done`` list rules out (techniques/quest/technique.py:165-172, 229-259, 311).
 
 Every function runs on the HIP kernels of ``libeconomize_amd.so``; there is no CPU path.
 """
@@ -25,7 +28,7 @@ from . import _lib
 from .errors import ConfigError
 from .paged import PAGE, PagedKVCache, paged_decode_attention
 
-__all__ = ["QuestPages", "bounds_dtype", "page_bounds", "quest_decode_attention", "select_pages"]
+__all__ = ["QuestPages", "QuestState", "bounds_dtype", "page_bounds", "quest_decode_attention", "select_pages"]
 
 
 def bounds_dtype(key_dtype: torch.dtype) -> torch.dtype:
@@ -211,3 +214,58 @@ def quest_decode_attention(query: torch.Tensor, cache: PagedKVCache, block_table
     return paged_decode_attention(query.transpose(1, 2), cache, block_table, seq_lens, max_seq_len, scale, softcap,
                                   sinks, out, page_list=index.contiguous(), done=pages.done,
                                   list_page_size=pages.page, mask=mask)
+
+
+class QuestState:
+    """One layer's Quest metadata with every count on the device: bounds ``[B, Hkv, max_pages, D]`` (bf16), the
+    pages of every (row, KV head) whose bounds are final, and ``done`` ``[B]`` (committed Quest pages).
+    :meth:`refresh` computes the bounds of the pages committed since the last refresh from device committed lengths
+    (the reference's ``pass_begin`` + ``_layer_bounds``, techniques/quest/technique.py:165-172, 229-259), and
+    :meth:`pages` hands the selection and the attention ``max_done = max_pages``: the calls of a decode step then
+    have fixed shapes and no host value that changes from step to step. Pages past a row's ``done`` score ``-inf``,
+    so the selection equals the one with the batch's true ``max(done)`` whenever it exceeds ``pages``; a row with at
+    most ``pages`` committed pages selects all of them (dense attention, in another key order).
+    """
+
+    def __init__(self, batch: int, kv_heads: int, head_dim: int, max_pages: int, page: int, pages: int,
+                 device: torch.device | str, max_queries: int = 1) -> None:
+        _check_page(page)
+        if max_pages <= 0 or pages <= 0:
+            raise ConfigError(f"quest state needs positive max_pages and pages, got {max_pages}, {pages}")
+        shape = (batch, kv_heads, max_pages, head_dim)
+        self.kmin = torch.zeros(shape, dtype=torch.bfloat16, device=device)
+        self.kmax = torch.zeros(shape, dtype=torch.bfloat16, device=device)
+        self.valid = torch.zeros(batch * kv_heads, dtype=torch.int32, device=device)
+        self.done = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.page, self.pages, self.max_pages, self.max_queries = page, pages, max_pages, max_queries
+
+    def reset(self) -> None:
+        """Forget every page (a new generation in the same buffers)."""
+        self.valid.zero_()
+        self.done.zero_()
+
+    def refresh(self, cache: PagedKVCache, block_table: torch.Tensor, committed: torch.Tensor) -> None:
+        """Bounds of the pages below ``committed`` (int32 ``[B]`` tokens, on the device) not computed yet; ``done``
+        becomes ``committed // page`` (at most ``max_pages``)."""
+        cache.check()
+        device = _lib.require_gpu(cache.keys, block_table, committed)
+        batch = self.done.shape[0]
+        if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1 or \
+                block_table.shape[0] != batch:
+            raise ConfigError(f"block_table must be int32 [{batch}, pages] with contiguous rows")
+        if committed.dtype != torch.int32 or committed.shape != (batch,) or not committed.is_contiguous():
+            raise ConfigError(f"committed must be a contiguous int32 [{batch}]")
+        if self.kmin.shape[1] != cache.kv_heads or self.kmin.shape[3] != cache.head_dim:
+            raise ConfigError("the quest state was made for another number of KV heads or head dim")
+        _lib.call(
+            "eco_quest_refresh_bounds", cache.keys.data_ptr(), _lib.fmt(cache.dtype), cache.num_pages,
+            block_table.data_ptr(), block_table.stride(0), block_table.shape[1], committed.data_ptr(),
+            self.valid.data_ptr(), self.done.data_ptr(), self.page, self.kmin.data_ptr(), self.kmax.data_ptr(),
+            self.kmin.stride(0), self.kmin.stride(1), self.kmin.stride(2), self.max_pages, batch, cache.kv_heads,
+            cache.head_dim, PAGE, _lib.stream_of(device),
+        )
+
+    def pages_handle(self) -> QuestPages:
+        """The layer's :class:`QuestPages` with the device ``done`` and ``max_done = max_pages``."""
+        return QuestPages(self.kmin, self.kmax, self.done, 0, self.max_pages, self.page, self.pages,
+                          self.max_queries)

@@ -178,6 +178,18 @@ int eco_quest_page_bounds(const void* k_cache, int32_t kv_format, int32_t num_pa
                           void* kmin, void* kmax, int64_t sb_b, int64_t sb_h, int64_t sb_p, int32_t batch,
                           int32_t kv_heads, int32_t head_dim, int32_t page_size, void* stream);
 
+/* Quest page bounds kept on append, every range on the device: for each row b and KV head h, the bounds of the Quest
+ * pages [valid[b * Hkv + h], min(committed[b] / quest_page_size, page_cap)) are computed as eco_quest_page_bounds
+ * does, then valid advances to that end and done[b] (optional) becomes the row's committed Quest pages. The launch
+ * shape depends on the arguments only, so a decode step can be captured in a graph; valid starts at zero.
+ * Replaces QuestCache.pass_begin / _layer_bounds with its host done list (techniques/quest/technique.py:165-172,
+ * 229-259), which keeps the reference's Quest out of graphs (technique.py:311). */
+int eco_quest_refresh_bounds(const void* k_cache, int32_t kv_format, int32_t num_pages, const int32_t* block_table,
+                             int64_t bt_stride, int32_t bt_cols, const int32_t* committed, int32_t* valid,
+                             int32_t* done, int32_t quest_page_size, void* kmin, void* kmax, int64_t sb_b,
+                             int64_t sb_h, int64_t sb_p, int32_t page_cap, int32_t batch, int32_t kv_heads,
+                             int32_t head_dim, int32_t page_size, void* stream);
+
 /* Workspace bytes of eco_quest_select (the page scores, fp32 [B, Hkv, max_done]). */
 size_t eco_quest_select_workspace_size(int32_t batch, int32_t kv_heads, int32_t max_done);
 
