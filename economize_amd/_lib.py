@@ -49,6 +49,10 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
     "eco_kivi_gather": (c_int32, [_P, _I, _P, _P, _I, _P, _P, _P, _L, _I, _P, _P, _I, _L, _L, _L, _L, _L, _L, _I, _I, _I,
                                   _I, _I, _I, _P]),
     "eco_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I]),
+    "eco_gathered_decode": (c_int32, [_P, _I, _L, _L, _L, _P, _P, _L, _L, _L, _L, _L, _L,  # q .. value strides
+                                      _P, _P, _L, _L, _L, _L, _L, _L, _P, _L, _L, _P, _P, _I, _I,  # compact entries
+                                      _P, _L, _L, _L, _L, _P, _P, _L, _L, _L,  # mask, sinks, out
+                                      _I, _I, _I, _I, _I, _I, _I, _F, _F, _P, _S, _P]),
     "eco_decode": (c_int32, [_P, _I, _L, _L, _L, _P, _P, _I, _L, _L, _L, _L, _L, _L, _P, _P, _P, _L, _L, _L, _L, _P, _P,
                              _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _F, _F, _P, _S, _P]),
     "eco_quest_page_bounds": (c_int32, [_P, _I, _I, _P, _L, _I, _I, _I, _I, _P, _P, _L, _L, _L, _I, _I, _I, _I, _P]),

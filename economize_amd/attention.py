@@ -11,7 +11,9 @@ reasons, ``kernel_calls`` / ``kernel_usage`` / ``usage_summary``, the registrati
   :mod:`economize_amd.packed`) attends over the paged fp8 / bf16 cache, its Quest pages or the paged KIVI cache on the
   paged kernels (path ``"kernel_<format>"``).
 * Dense K/V (bf16 / fp16 / fp32, or fp8 views of an fp8 cache) attend on the dense decode kernel
-  (:func:`economize_amd.decode.decode_attention`, path ``"kernel"``).
+  (:func:`economize_amd.decode.decode_attention`, path ``"kernel"``); with a :class:`~economize_amd.gathered.GatheredKV`
+  attached (an eviction's compacted prompt entries), over the compact entries and the dense tail (path
+  ``"kernel_gathered"``).
 * Everything else falls back per call to transformers' ``sdpa`` (a paged cache's K/V materialized by the gather
   kernels first, fp8 K/V upcast to the query's dtype), or to the model's eager function when the call has sinks or
   asks for the weights: long queries (prefill), CPU tensors, training with dropout, ``output_attentions``, other
@@ -44,9 +46,9 @@ __all__ = ["ATTENTION_KERNELS", "MAX_QUERIES", "NAME", "PACKED_FORMATS", "Attent
 NAME = "economize"
 #: Longest query (tokens per row) the kernels take; longer ones (prefill) fall back to ``sdpa``.
 MAX_QUERIES = 64
-#: Packed formats the ``"economize"`` kernel reads (the reference's set less ``"gathered"``, eviction's compacted
-#: entries, which this path does not build; plus the paged fp8 / bf16 cache).
-PACKED_FORMATS = frozenset({"kivi", "quest", "fp8", "bf16"})
+#: Packed formats the ``"economize"`` kernel reads (the reference's set, interface.py:70, plus the paged fp8 / bf16
+#: cache).
+PACKED_FORMATS = frozenset({"kivi", "gathered", "quest", "fp8", "bf16"})
 
 _DOT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 
@@ -196,7 +198,7 @@ def _sinks(kwargs: dict) -> object:
 
 
 def _fallback_reason(module, query: torch.Tensor, key, attention_mask, dropout: float, kwargs: dict,
-                     paged: PagedKV | None) -> str | None:
+                     paged: PagedKV | None, gathered: object = None) -> str | None:
     """Why this call cannot run on the kernels, or ``None`` when it can; decided per call (interface.py:243-285)."""
     batch, q_heads, queries, _ = query.shape
     if not query.is_cuda:
@@ -219,8 +221,8 @@ def _fallback_reason(module, query: torch.Tensor, key, attention_mask, dropout: 
         if q_heads % kv_heads == 0 and (q_heads // kv_heads) * queries > 64:
             return "rows"  # the paged kernels take at most 64 query rows per KV head
     else:
-        if key.dtype != query.dtype and key.dtype not in FP8_DTYPES:
-            return "kv_dtype"
+        if key.dtype != query.dtype and (key.dtype not in FP8_DTYPES or gathered is not None):
+            return "kv_dtype"  # the gathered kernel takes K/V in the query's dtype
         kv_heads = key.shape[1]
     if q_heads % kv_heads:
         return "heads"
@@ -282,12 +284,12 @@ def economize_attention_forward(module: torch.nn.Module | None, query: torch.Ten
     ``key`` may also be a :class:`PagedKV` itself (then ``value`` is unused)."""
     if query.dim() != 4:
         raise ConfigError(f"query must be [B, Hq, Q, D], got {tuple(query.shape)}")
-    paged = key if isinstance(key, PagedKV) else packed_of(key)
-    if paged is not None and not isinstance(paged, PagedKV):
-        paged = None
+    handle = key if isinstance(key, PagedKV) else packed_of(key)
+    paged = handle if isinstance(handle, PagedKV) else None
+    gathered = handle if getattr(handle, "format", None) == "gathered" else None
     layer = getattr(module, "layer_idx", None)
     queries = query.shape[2]
-    reason = _fallback_reason(module, query, key, attention_mask, dropout, kwargs, paged)
+    reason = _fallback_reason(module, query, key, attention_mask, dropout, kwargs, paged, gathered)
     if reason is not None:
         if isinstance(key, PagedKV):
             raise ConfigError(f"a bare PagedKV handle cannot fall back ({reason}); attach it to dense stand-ins")
@@ -301,8 +303,12 @@ def economize_attention_forward(module: torch.nn.Module | None, query: torch.Ten
     else:
         if attention_mask is not None and attention_mask.shape[-1] != key.shape[2]:
             attention_mask = attention_mask[..., : key.shape[2]]
-        out = decode_attention(query, key, value, attention_mask, scale, softcap=softcap, sinks=sinks)
-        path = "kernel"
+        if gathered is not None:
+            out = gathered.attend(query, key, value, attention_mask, scale, softcap, sinks)
+            path = "kernel_gathered"
+        else:
+            out = decode_attention(query, key, value, attention_mask, scale, softcap=softcap, sinks=sinks)
+            path = "kernel"
     _calls["kernel"] += 1
     _usage[(layer, queries, path, "")] += 1
     return out, None

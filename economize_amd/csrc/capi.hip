@@ -295,6 +295,117 @@ void* scratch_on_device() {
     return addresses[device];
 }
 
+// The compact entries of a gathered cache (the reference's GatheredKV, attention/gathered.py:39-64).
+struct GatheredArgs {
+    const void* ck;
+    const void* cv;
+    int64_t sck_b, sck_h, sck_s, scv_b, scv_h, scv_s;
+    const int32_t* index;
+    int64_t si_b, si_h;
+    const int32_t* count;
+    const int32_t* start;
+    int capacity, dropped;
+};
+
+int dense_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int64_t sq_q, const void* k,
+               const void* v, int32_t kv_format, int64_t sk_b, int64_t sk_h, int64_t sk_s, int64_t sv_b, int64_t sv_h,
+               int64_t sv_s, const float* k_scale, const float* v_scale, const uint8_t* mask, int64_t sm_b,
+               int64_t sm_h, int64_t sm_q, int64_t sm_s, const float* sinks, void* out, int64_t so_b, int64_t so_q,
+               int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys,
+               int32_t head_dim, int32_t value_dim, float scale, float softcap, void* workspace,
+               size_t workspace_bytes, void* stream, const GatheredArgs* g) {
+    if (!q || !k || !v || !out) return fail("decode: null query, key, value or output pointer");
+    if (batch <= 0 || queries <= 0 || q_heads <= 0 || kv_heads <= 0 || keys < 0)
+        return fail("decode: batch, queries and heads must be positive, keys non-negative");
+    if (q_heads % kv_heads)
+        return fail("decode: " + std::to_string(q_heads) + " query heads are not a multiple of " +
+                    std::to_string(kv_heads) + " KV heads");
+    if (q_format != BF16 && q_format != FP16 && q_format != FP32)
+        return fail("decode: queries must be bf16, fp16 or fp32");
+    const bool fp8 = kv_format == FP8_E4M3 || kv_format == FP8_E5M2;
+    if (kv_format != q_format && !fp8) return fail("decode: K/V must be in the query's dtype or fp8");
+    if ((k_scale || v_scale) && !fp8) return fail("decode: per-head scales apply to fp8 K/V only");
+    const int es = element_bytes(kv_format), qs = element_bytes(q_format);
+    for (int dim : {head_dim, value_dim})
+        if (dim <= 0 || dim % 8 || (dim * es) % 16 || dim > 256)
+            return fail("decode: head dims must be positive multiples of 8 (of 16 for fp8), at most 256");
+    auto aligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+    if (!aligned(q) || !aligned(k) || !aligned(v))
+        return fail("decode: query, key and value must be 16-byte aligned");
+    for (int64_t st : {sq_b, sq_h, sq_q})
+        if ((st * qs) % 16) return fail("decode: query strides must be multiples of 16 bytes");
+    for (int64_t st : {sk_b, sk_h, sk_s, sv_b, sv_h, sv_s})
+        if ((st * es) % 16) return fail("decode: key and value strides must be multiples of 16 bytes");
+    if (!(scale == scale)) return fail("decode: scale is NaN");
+    const int plan_keys = g ? std::max(1, keys - g->dropped) : keys;  // the virtual key axis
+    const DensePlan d = dense_plan(batch, queries, q_heads, kv_heads, plan_keys, head_dim, value_dim);
+    if (!workspace || workspace_bytes < d.workspace)
+        return fail("decode: workspace too small (" + std::to_string(workspace_bytes) + " < " +
+                    std::to_string(d.workspace) + " bytes)");
+    DenseParams p;
+    std::memset(&p, 0, sizeof(p));
+    p.q = q;
+    p.sq_b = sq_b;
+    p.sq_h = sq_h;
+    p.sq_q = sq_q;
+    p.q_format = q_format;
+    p.k = k;
+    p.v = v;
+    p.kv_format = kv_format;
+    p.sk_b = sk_b;
+    p.sk_h = sk_h;
+    p.sk_s = sk_s;
+    p.sv_b = sv_b;
+    p.sv_h = sv_h;
+    p.sv_s = sv_s;
+    p.k_scale = k_scale;
+    p.v_scale = v_scale;
+    p.mask = mask;
+    p.sm_b = sm_b;
+    p.sm_h = sm_h;
+    p.sm_q = sm_q;
+    p.sm_s = sm_s;
+    p.sinks = sinks;
+    p.out = out;
+    p.so_b = so_b;
+    p.so_q = so_q;
+    p.so_h = so_h;
+    p.part = static_cast<float*>(workspace);
+    p.batch = batch;
+    p.queries = queries;
+    p.q_heads = q_heads;
+    p.kv_heads = kv_heads;
+    p.groups = q_heads / kv_heads;
+    p.rows = p.groups * queries;
+    p.keys = plan_keys;
+    p.dense_keys = keys;
+    p.head_dim = head_dim;
+    p.value_dim = value_dim;
+    p.m_tiles = d.m_tiles;
+    p.splits = d.splits;
+    p.split_len = d.split_len;
+    p.scale = scale;
+    p.softcap = softcap > 0.0f ? softcap : 0.0f;
+    if (g) {
+        p.gk = g->ck;
+        p.gv = g->cv;
+        p.sgk_b = g->sck_b;
+        p.sgk_h = g->sck_h;
+        p.sgk_s = g->sck_s;
+        p.sgv_b = g->scv_b;
+        p.sgv_h = g->scv_h;
+        p.sgv_s = g->scv_s;
+        p.g_index = g->index;
+        p.sgi_b = g->si_b;
+        p.sgi_h = g->si_h;
+        p.g_count = g->count;
+        p.g_start = g->start;
+        p.g_capacity = g->capacity;
+    }
+    return dense_attention(p, d.padded_dim, static_cast<hipStream_t>(stream));
+}
+
+
 }  // namespace
 
 }  // namespace eco
@@ -465,77 +576,35 @@ int eco_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int6
                int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys,
                int32_t head_dim, int32_t value_dim, float scale, float softcap, void* workspace,
                size_t workspace_bytes, void* stream) {
-    if (!q || !k || !v || !out) return fail("decode: null query, key, value or output pointer");
-    if (batch <= 0 || queries <= 0 || q_heads <= 0 || kv_heads <= 0 || keys < 0)
-        return fail("decode: batch, queries and heads must be positive, keys non-negative");
-    if (q_heads % kv_heads)
-        return fail("decode: " + std::to_string(q_heads) + " query heads are not a multiple of " +
-                    std::to_string(kv_heads) + " KV heads");
-    if (q_format != BF16 && q_format != FP16 && q_format != FP32)
-        return fail("decode: queries must be bf16, fp16 or fp32");
-    const bool fp8 = kv_format == FP8_E4M3 || kv_format == FP8_E5M2;
-    if (kv_format != q_format && !fp8) return fail("decode: K/V must be in the query's dtype or fp8");
-    if ((k_scale || v_scale) && !fp8) return fail("decode: per-head scales apply to fp8 K/V only");
-    const int es = element_bytes(kv_format), qs = element_bytes(q_format);
-    for (int dim : {head_dim, value_dim})
-        if (dim <= 0 || dim % 8 || (dim * es) % 16 || dim > 256)
-            return fail("decode: head dims must be positive multiples of 8 (of 16 for fp8), at most 256");
+    return dense_decode(q, q_format, sq_b, sq_h, sq_q, k, v, kv_format, sk_b, sk_h, sk_s, sv_b, sv_h, sv_s, k_scale,
+                        v_scale, mask, sm_b, sm_h, sm_q, sm_s, sinks, out, so_b, so_q, so_h, batch, queries, q_heads,
+                        kv_heads, keys, head_dim, value_dim, scale, softcap, workspace, workspace_bytes, stream,
+                        nullptr);
+}
+
+int eco_gathered_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int64_t sq_q, const void* k,
+                        const void* v, int64_t sk_b, int64_t sk_h, int64_t sk_s, int64_t sv_b, int64_t sv_h,
+                        int64_t sv_s, const void* ck, const void* cv, int64_t sck_b, int64_t sck_h, int64_t sck_s,
+                        int64_t scv_b, int64_t scv_h, int64_t scv_s, const int32_t* index, int64_t si_b,
+                        int64_t si_h, const int32_t* count, const int32_t* start, int32_t capacity, int32_t dropped,
+                        const uint8_t* mask, int64_t sm_b, int64_t sm_h, int64_t sm_q, int64_t sm_s,
+                        const float* sinks, void* out, int64_t so_b, int64_t so_q, int64_t so_h, int32_t batch,
+                        int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys, int32_t head_dim,
+                        int32_t value_dim, float scale, float softcap, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+    if (!ck || !cv || !index || !count || !start) return fail("gathered decode: null compact entries or counts");
+    if (keys <= 0 || capacity < 0 || dropped < 0 || dropped > keys)
+        return fail("gathered decode: need keys > 0, capacity >= 0 and 0 <= dropped <= keys");
+    const int es = element_bytes(q_format);
     auto aligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
-    if (!aligned(q) || !aligned(k) || !aligned(v))
-        return fail("decode: query, key and value must be 16-byte aligned");
-    for (int64_t st : {sq_b, sq_h, sq_q})
-        if ((st * qs) % 16) return fail("decode: query strides must be multiples of 16 bytes");
-    for (int64_t st : {sk_b, sk_h, sk_s, sv_b, sv_h, sv_s})
-        if ((st * es) % 16) return fail("decode: key and value strides must be multiples of 16 bytes");
-    if (!(scale == scale)) return fail("decode: scale is NaN");
-    const DensePlan d = dense_plan(batch, queries, q_heads, kv_heads, keys, head_dim, value_dim);
-    if (!workspace || workspace_bytes < d.workspace)
-        return fail("decode: workspace too small (" + std::to_string(workspace_bytes) + " < " +
-                    std::to_string(d.workspace) + " bytes)");
-    DenseParams p;
-    std::memset(&p, 0, sizeof(p));
-    p.q = q;
-    p.sq_b = sq_b;
-    p.sq_h = sq_h;
-    p.sq_q = sq_q;
-    p.q_format = q_format;
-    p.k = k;
-    p.v = v;
-    p.kv_format = kv_format;
-    p.sk_b = sk_b;
-    p.sk_h = sk_h;
-    p.sk_s = sk_s;
-    p.sv_b = sv_b;
-    p.sv_h = sv_h;
-    p.sv_s = sv_s;
-    p.k_scale = k_scale;
-    p.v_scale = v_scale;
-    p.mask = mask;
-    p.sm_b = sm_b;
-    p.sm_h = sm_h;
-    p.sm_q = sm_q;
-    p.sm_s = sm_s;
-    p.sinks = sinks;
-    p.out = out;
-    p.so_b = so_b;
-    p.so_q = so_q;
-    p.so_h = so_h;
-    p.part = static_cast<float*>(workspace);
-    p.batch = batch;
-    p.queries = queries;
-    p.q_heads = q_heads;
-    p.kv_heads = kv_heads;
-    p.groups = q_heads / kv_heads;
-    p.rows = p.groups * queries;
-    p.keys = keys;
-    p.head_dim = head_dim;
-    p.value_dim = value_dim;
-    p.m_tiles = d.m_tiles;
-    p.splits = d.splits;
-    p.split_len = d.split_len;
-    p.scale = scale;
-    p.softcap = softcap > 0.0f ? softcap : 0.0f;
-    return dense_attention(p, d.padded_dim, static_cast<hipStream_t>(stream));
+    if (!aligned(ck) || !aligned(cv)) return fail("gathered decode: compact keys and values must be 16-byte aligned");
+    for (int64_t st : {sck_b, sck_h, sck_s, scv_b, scv_h, scv_s})
+        if ((st * es) % 16) return fail("gathered decode: compact strides must be multiples of 16 bytes");
+    const GatheredArgs g{ck, cv, sck_b, sck_h, sck_s, scv_b, scv_h, scv_s, index, si_b, si_h, count, start,
+                         capacity, dropped};
+    return dense_decode(q, q_format, sq_b, sq_h, sq_q, k, v, q_format, sk_b, sk_h, sk_s, sv_b, sv_h, sv_s, nullptr,
+                        nullptr, mask, sm_b, sm_h, sm_q, sm_s, sinks, out, so_b, so_q, so_h, batch, queries, q_heads,
+                        kv_heads, keys, head_dim, value_dim, scale, softcap, workspace, workspace_bytes, stream, &g);
 }
 
 int eco_mask_bits(const uint8_t* mask, int64_t sm_b, int64_t sm_h, int64_t sm_q, int64_t sm_s, int32_t batch,

@@ -167,6 +167,30 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
     const uint8_t* kbase = static_cast<const uint8_t*>(p.k) + (b * p.sk_b + kvh * p.sk_h) * ES;
     const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.sv_b + kvh * p.sv_h) * ES;
     const uint8_t* mrow = p.mask ? p.mask + b * p.sm_b + h * p.sm_h + qi * p.sm_q : nullptr;
+    // the key axis: dense slots, or (gathered) the row's compact entries followed by its dense slots from start on
+    int count = 0, start = 0, row_keys = p.keys;
+    const uint8_t* gkbase = kbase;
+    const uint8_t* gvbase = vbase;
+    const int32_t* gidx = nullptr;
+    if (p.gk) {
+        count = min(max(p.g_count[b * p.kv_heads + kvh], 0), p.g_capacity);
+        start = min(max(p.g_start[b], 0), p.dense_keys);
+        row_keys = min(count + p.dense_keys - start, p.keys);
+        gkbase = static_cast<const uint8_t*>(p.gk) + (b * p.sgk_b + kvh * p.sgk_h) * ES;
+        gvbase = static_cast<const uint8_t*>(p.gv) + (b * p.sgv_b + kvh * p.sgv_h) * ES;
+        gidx = p.g_index + b * p.sgi_b + kvh * p.sgi_h;
+    }
+    auto key_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
+        return t < count ? gkbase + static_cast<int64_t>(t) * p.sgk_s * ES
+                         : kbase + static_cast<int64_t>(start + t - count) * p.sk_s * ES;
+    };
+    auto value_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
+        return t < count ? gvbase + static_cast<int64_t>(t) * p.sgv_s * ES
+                         : vbase + static_cast<int64_t>(start + t - count) * p.sv_s * ES;
+    };
+    auto mask_col = [&](int t) __attribute__((always_inline)) -> int64_t {
+        return t < count ? min(max(gidx[t], 0), p.dense_keys - 1) : start + t - count;
+    };
 
     float m_i = -INFINITY, l_i = 0.0f;
     f32x4 acc[ND];
@@ -174,7 +198,7 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
     for (int nd = 0; nd < ND; ++nd) acc[nd] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
     const int t_begin = split * p.split_len;
-    const int t_end = min(p.keys, t_begin + p.split_len);
+    const int t_end = min(row_keys, t_begin + p.split_len);
     constexpr int CHUNKS = TK * DP * ES / 16;  // 16-byte chunks of a staged value tile
     constexpr int CPR = DP * ES / 16;          // chunks per value row
     constexpr int CPL = (CHUNKS + 63) / 64;    // chunks per lane
@@ -187,7 +211,7 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
             const int t = chunk / CPR;
             const int c = (chunk % CPR) * (16 / ES);  // first channel of the chunk
             if (chunk < CHUNKS && t0 + t < t_end && c < p.value_dim)
-                return *reinterpret_cast<const uint4*>(vbase + (static_cast<int64_t>(t0 + t) * p.sv_s + c) * ES);
+                return *reinterpret_cast<const uint4*>(value_row(t0 + t) + c * ES);
             return make_uint4(0, 0, 0, 0);
         };
         uint4 vreg[kStage ? CPL : 1];
@@ -198,7 +222,7 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
 #pragma unroll
         for (int v = 0; v < 2; ++v) {
             const int tk = min(t0 + 8 * (n >> 2) + 4 * v + (n & 3), t_end - 1);
-            const uint8_t* krow = kbase + static_cast<int64_t>(tk) * p.sk_s * ES;
+            const uint8_t* krow = key_row(tk);
 #pragma unroll
             for (int j = 0; j < KS; ++j) {
                 const int c = 32 * j + 8 * g;
@@ -238,7 +262,7 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
         for (int e = 0; e < 8; ++e) {
             const int t = t0 + 8 * g + e;
             bool ok = r_ok && t < t_end;
-            if (ok && mrow) ok = mrow[static_cast<int64_t>(t) * p.sm_s] != 0;
+            if (ok && mrow) ok = mrow[mask_col(t) * p.sm_s] != 0;
             vis |= ok ? 1u << e : 0u;
         }
         float tile_max = -INFINITY;

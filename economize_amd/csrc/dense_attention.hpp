@@ -26,6 +26,19 @@ struct DenseParams {
     int batch, queries, q_heads, kv_heads, groups, rows, keys, head_dim, value_dim;
     int m_tiles, splits, split_len;
     float scale, softcap;
+    // Gathered mode (gk non-null; the reference's gathered_decode_attention, attention/gathered.py:96-179): `keys` is
+    // the virtual key axis. Virtual key t of (b, kvh) is compact entry t of gk / gv [B, Hkv, capacity, D] below
+    // count[b, kvh] (its mask column index[b, kvh, t]), else dense slot start[b] + t - count[b, kvh] of k / v, whose
+    // slots number dense_keys. Counts are clamped to the capacity, starts to [0, dense_keys], mask columns to the
+    // slots, so that malformed counts read wrong entries but nothing outside the buffers.
+    const void* gk;
+    const void* gv;
+    int64_t sgk_b, sgk_h, sgk_s, sgv_b, sgv_h, sgv_s;
+    const int32_t* g_index;  // [B, Hkv, capacity] with strides sgi_b, sgi_h (contiguous entries)
+    int64_t sgi_b, sgi_h;
+    const int32_t* g_count;  // [B * Hkv]
+    const int32_t* g_start;  // [B]
+    int g_capacity, dense_keys;
 };
 
 int dense_padded_dim(int head_dim, int value_dim);  // 64, 128 or 256; 0 when neither fits

@@ -118,6 +118,24 @@ int eco_paged_decode_static(const void* q, int64_t sq_b, int64_t sq_q, int64_t s
                             int32_t max_seq_len, float scale, float softcap, const uint32_t* mask_bits, int64_t mk_b,
                             int64_t mk_h, int64_t mk_q, int32_t mask_words, void* stream);
 
+/* Decode attention over a cache whose prompt entries were compacted by an eviction (the reference's
+ * gathered_decode_attention and GatheredKV, attention/gathered.py:39-179): for row b and KV head h, virtual key t is
+ * compact entry t of ck / cv [B, Hkv, capacity, D / Dv] (strides sck_*, scv_*; mask column index[b, h, t], strides
+ * si_b, si_h) below count[b * Hkv + h], else dense slot start[b] + t - count of k / v [B, Hkv, keys, D / Dv]; the
+ * virtual axis is keys - dropped long (dropped = min(start[b] - count[b, h]) on the host). Everything else as
+ * eco_decode, with K/V in the query's format; the workspace is eco_decode_workspace_size(..., keys - dropped, ...).
+ * Counts beyond the capacity and starts beyond the slots are clamped (wrong results, no access outside a buffer). */
+int eco_gathered_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int64_t sq_q, const void* k,
+                        const void* v, int64_t sk_b, int64_t sk_h, int64_t sk_s, int64_t sv_b, int64_t sv_h,
+                        int64_t sv_s, const void* ck, const void* cv, int64_t sck_b, int64_t sck_h, int64_t sck_s,
+                        int64_t scv_b, int64_t scv_h, int64_t scv_s, const int32_t* index, int64_t si_b,
+                        int64_t si_h, const int32_t* count, const int32_t* start, int32_t capacity, int32_t dropped,
+                        const uint8_t* mask, int64_t sm_b, int64_t sm_h, int64_t sm_q, int64_t sm_s,
+                        const float* sinks, void* out, int64_t so_b, int64_t so_q, int64_t so_h, int32_t batch,
+                        int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys, int32_t head_dim,
+                        int32_t value_dim, float scale, float softcap, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
 /* The packed form of a boolean attention mask that the paged decode kernels take: bits[((b * heads + h) * queries +
  * q) * words + w] has bit k set where mask[b * sm_b + h * sm_h + q * sm_q + (32 w + k) * sm_s] is nonzero (one byte
  * per element; 0 past `keys`). words >= ceil(keys / 32). A broadcast axis of the mask is packed once (pass its size

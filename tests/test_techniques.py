@@ -102,7 +102,7 @@ def test_economize_kernel_is_registered() -> None:
     assert "economize" in ATTENTION_KERNELS.names()
     assert accepts_fp8_kv("economize") and not accepts_fp8_kv("sdpa")
     assert accepts_packed_kv("economize", "kivi") and accepts_packed_kv("economize", "quest")
-    assert not accepts_packed_kv("economize", "gathered") and not accepts_packed_kv("eager", "kivi")
+    assert accepts_packed_kv("economize", "gathered") and not accepts_packed_kv("eager", "kivi")
     FusedFP8KVConfig().validate("economize")
     FusedKIVIConfig().validate("economize")
     QuestConfig().validate("economize")
