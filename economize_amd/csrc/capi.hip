@@ -12,6 +12,7 @@
 #include "dense_attention.hpp"
 #include "gather.hpp"
 #include "kivi.hpp"
+#include "kivi_cells.hpp"
 #include "kivi_dense.hpp"
 #include "kv_quant.hpp"
 #include "paged_attention.hpp"
@@ -406,6 +407,35 @@ int dense_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, in
 }
 
 
+// The cell layout of layout.py:196-213 and CellLayout's offsets (layout.py:133-193); 1 (with a message) when the
+// head size or the bits do not fit KIVI's packing.
+int make_cell_layout(int head_dim, int element_size, int bits, int group, CellLayout* out) {
+    if (bits != 2 && bits != 4 && bits != 8) return fail("kivi cells: bits must be 2, 4 or 8");
+    if (head_dim < 16 || head_dim > 256 || (head_dim & (head_dim - 1)))
+        return fail("kivi cells: the head size must be a power of two from 16 to 256");
+    if (group < 1 || group > 128 || (group & (group - 1)))
+        return fail("kivi cells: the group size must be a power of two of at most 128");
+    if (element_size != 2 && element_size != 4) return fail("kivi cells: the cache dtype must be bf16, fp16 or fp32");
+    CellLayout L;
+    L.head_dim = head_dim;
+    L.element_size = element_size;
+    L.bits = bits;
+    L.group = group;
+    L.value_group = head_dim % group == 0 ? group : head_dim;
+    L.key_aux = (2 * head_dim + group - 1) / group;
+    const int nvg = head_dim / L.value_group, code_bytes = head_dim / (8 / bits);
+    L.off_v = head_dim * element_size;
+    L.off_vs = 2 * head_dim * element_size;
+    L.off_vz = L.off_vs + 2 * nvg;
+    L.off_ka = L.off_vz + 2 * nvg;
+    L.off_kc = L.off_ka + 2 * L.key_aux;
+    L.off_vc = L.off_kc + code_bytes;
+    L.off_flag = L.off_vc + code_bytes;
+    L.size = (L.off_flag + 2 + 15) / 16 * 16;
+    *out = L;
+    return 0;
+}
+
 }  // namespace
 
 }  // namespace eco
@@ -780,6 +810,74 @@ int eco_kivi_fake_quantize(void* buffer, int32_t format, int64_t sb, int64_t sh,
     if (!keys && head_dim % group) return fail("kivi fake quantize: the value group must divide the head dim");
     KiviFakeParams p{buffer, format, sb, sh, ss, batch, heads, head_dim, start, stop, bits, group, keys};
     return kivi_fake_quantize(p, static_cast<hipStream_t>(stream));
+}
+
+int eco_kivi_cells_layout(int32_t head_dim, int32_t element_size, int32_t bits, int32_t group, int32_t* offsets) {
+    if (!offsets) return fail("kivi cells layout: null output");
+    CellLayout L;
+    if (int rc = make_cell_layout(head_dim, element_size, bits, group, &L)) return rc;
+    const int32_t values[10] = {L.value_group, L.key_aux, L.off_v, L.off_vs, L.off_vz,
+                                L.off_ka,      L.off_kc,  L.off_vc, L.off_flag, L.size};
+    std::memcpy(offsets, values, sizeof(values));
+    return 0;
+}
+
+static int cells_params(void* cache, int32_t format, int64_t sb, int64_t sh, int64_t sn, int32_t num_pages,
+                        int32_t page_size, int32_t kv_heads, int32_t head_dim, int32_t bits, int32_t group,
+                        CellsParams* p) {
+    if (!cache) return fail("kivi cells: null cache");
+    if (format != BF16 && format != FP16 && format != FP32)
+        return fail("kivi cells: the cache dtype must be bf16, fp16 or fp32");
+    if (num_pages <= 0 || page_size <= 0 || kv_heads <= 0) return fail("kivi cells: pages and heads must be positive");
+    std::memset(p, 0, sizeof(*p));
+    if (int rc = make_cell_layout(head_dim, element_bytes(format), bits, group, &p->L)) return rc;
+    if (page_size % group) return fail("kivi cells: pages must hold whole key groups");
+    if (sn < p->L.size || sn % 16 || sh % 16 || sb % 16)
+        return fail("kivi cells: cell strides must be multiples of 16 bytes, at least one cell");
+    p->cache = static_cast<uint8_t*>(cache);
+    p->sb = sb;
+    p->sh = sh;
+    p->sn = sn;
+    p->format = format;
+    p->page_size = page_size;
+    p->num_pages = num_pages;
+    p->kv_heads = kv_heads;
+    return 0;
+}
+
+int eco_kivi_cells_quantize(void* cache, int32_t format, int64_t sb, int64_t sh, int64_t sn, int32_t num_pages,
+                            int32_t page_size, int32_t kv_heads, const int32_t* block_table, int64_t bt_stride,
+                            int32_t bt_cols, const int32_t* query_start_loc, const int32_t* seq_lens,
+                            const int32_t* prefilling, int32_t requests, int32_t head_dim, int32_t bits,
+                            int32_t group, int32_t residual, void* stream) {
+    CellsParams p;
+    if (int rc = cells_params(cache, format, sb, sh, sn, num_pages, page_size, kv_heads, head_dim, bits, group, &p))
+        return rc;
+    if (requests < 0) return fail("kivi cells quantize: negative request count");
+    if (requests == 0) return 0;
+    if (!block_table || !query_start_loc || !seq_lens || !prefilling)
+        return fail("kivi cells quantize: null block table, query offsets, lengths or prefill flags");
+    if (bt_cols <= 0 || bt_stride < bt_cols) return fail("kivi cells quantize: bad block table");
+    if (residual < group || residual % group) return fail("kivi cells quantize: the residual must be whole groups");
+    p.block_table = block_table;
+    p.bt_stride = bt_stride;
+    p.bt_cols = bt_cols;
+    p.query_start_loc = query_start_loc;
+    p.seq_lens = seq_lens;
+    p.prefilling = prefilling;
+    p.requests = requests;
+    p.residual = residual;
+    return kivi_cells_quantize(p, static_cast<hipStream_t>(stream));
+}
+
+int eco_kivi_cells_clear_flags(void* cache, int32_t format, int64_t sb, int64_t sh, int64_t sn, int32_t num_pages,
+                               int32_t page_size, int32_t kv_heads, const int32_t* slots, int32_t tokens,
+                               int32_t head_dim, int32_t bits, int32_t group, void* stream) {
+    CellsParams p;
+    if (int rc = cells_params(cache, format, sb, sh, sn, num_pages, page_size, kv_heads, head_dim, bits, group, &p))
+        return rc;
+    if (tokens < 0 || (tokens > 0 && !slots)) return fail("kivi cells clear: bad slots");
+    return kivi_cells_clear_flags(p, slots, tokens, static_cast<hipStream_t>(stream));
 }
 
 int eco_kivi_ring_write(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,

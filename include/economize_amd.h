@@ -261,6 +261,29 @@ int eco_kivi_fake_quantize(void* buffer, int32_t format, int64_t sb, int64_t sh,
                            int32_t heads, int32_t slots, int32_t head_dim, int32_t start, int32_t stop, int32_t bits,
                            int32_t group, int32_t keys, void* stream);
 
+/* KIVI's cell on vLLM's paged cache (backends/vllm/kivi/layout.py:133-213): for a head size (a power of two, 16 to
+ * 256) of a cache dtype of element_size bytes, bits 2 / 4 / 8 and a power-of-two group of at most 128, writes
+ * offsets[10] = {value group, key aux slots, off_v, off_vs, off_vz, off_ka, off_kc, off_vc, off_flag, cell bytes}. */
+int eco_kivi_cells_layout(int32_t head_dim, int32_t element_size, int32_t bits, int32_t group, int32_t* offsets);
+
+/* The reference's quantize_committed (backends/vllm/kivi/kernels.py:94-207) on the cells of one layer's cache
+ * [pages, kv_heads, page_size] (cell byte strides sb, sh, sn, dense entries of format bf16 / fp16 / fp32): for every
+ * request not prefilling with a non-empty query (query_start_loc [requests + 1]) and c = seq_lens[b] - its query
+ * length > 0, keys in whole groups below (c / residual) * residual and values below c - residual, newest first, until
+ * a cell already quantized; cells laid out as write_cells does (layout.py:222-256): dense entries replaced by the
+ * dequantized values, codes, fp16 scales and zero points, flags 1 (2: a scale or zero point beyond fp16). */
+int eco_kivi_cells_quantize(void* cache, int32_t format, int64_t sb, int64_t sh, int64_t sn, int32_t num_pages,
+                            int32_t page_size, int32_t kv_heads, const int32_t* block_table, int64_t bt_stride,
+                            int32_t bt_cols, const int32_t* query_start_loc, const int32_t* seq_lens,
+                            const int32_t* prefilling, int32_t requests, int32_t head_dim, int32_t bits,
+                            int32_t group, int32_t residual, void* stream);
+
+/* clear_flags (kernels.py:58-78): the cells of slots[tokens] (page * page_size + position; negative: padding) of
+ * every KV head marked full precision (both flags 0), after vLLM's cache write filled them. */
+int eco_kivi_cells_clear_flags(void* cache, int32_t format, int64_t sb, int64_t sh, int64_t sn, int32_t num_pages,
+                               int32_t page_size, int32_t kv_heads, const int32_t* slots, int32_t tokens,
+                               int32_t head_dim, int32_t bits, int32_t group, void* stream);
+
 /* Writes new tokens k_new / v_new [T, Hkv, D] (element strides, channel stride 1) into the rings at slot
  * positions[t] % ring of row rows[t] (negative positions skip), rounded to bf16 (the reference's ring writes,
  * kv_quant/packed.py:258-277). */

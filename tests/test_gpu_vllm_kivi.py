@@ -1,0 +1,123 @@
+"""KIVI on vLLM's cell layout on the GPU (``eco_kivi_cells_quantize``, the reference's quantize_committed,
+backends/vllm/kivi/kernels.py:94-207) against the oracle's write_cells (layout.py:222-256), byte for byte: requests
+of ragged lengths in shuffled pages, a prefilling request and one without queries left untouched, bf16 / fp16 /
+fp32 entries, 2 / 4 / 8 bits, groups of 16 and 32, a second pass that quantizes only what crossed the residual since
+the first, a group whose scale overflows fp16, and clear_flags."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import vllm_cells as oc
+
+pytestmark = pytest.mark.gpu
+
+NAMES = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
+
+
+def setup(dtype, bits, group, head, page, lens, heads=2, seed=0, scale_up=None):
+    """A cache whose cells hold every request's dense K/V (flags 0), the requests' full-precision K/V, the table."""
+    from economize_amd.vllm_kivi import cell_layout
+
+    layout = cell_layout(head, dtype, bits, group)
+    es = layout.element_size
+    per_req = max(-(-n // page) for n in lens) + 1
+    pages = len(lens) * per_req + 3
+    gen = torch.Generator().manual_seed(seed)
+    table = torch.randperm(pages, generator=gen)[: len(lens) * per_req].view(len(lens), per_req).to(torch.int32)
+    cache = torch.zeros(pages, heads, page, layout.size // es, dtype=dtype)
+    u8 = cache.view(torch.uint8)
+    states = []
+    for b, n in enumerate(lens):
+        k = (torch.randn(heads, n, head, generator=gen) * 2).to(dtype)
+        v = (torch.randn(heads, n, head, generator=gen) * 2).to(dtype)
+        if scale_up is not None:
+            k[:, scale_up] *= 1e6
+        states.append((k, v))
+        for t in range(n):
+            cell = u8[table[b, t // page], :, t % page]
+            cell[:, : layout.off_v] = k[:, t].contiguous().view(torch.uint8)
+            cell[:, layout.off_v: layout.off_vs] = v[:, t].contiguous().view(torch.uint8)
+    return layout, cache, table, states
+
+
+def expected(layout, cache, table, states, bounds, dtype, page):
+    """The cache after write_cells(k, v, kq_b, vq_b) of every request."""
+    want = cache.view(torch.uint8).clone().numpy()
+    for b, ((k, v), (kq, vq)) in enumerate(zip(states, bounds)):
+        if kq == 0 and vq == 0:
+            continue
+        cells = oc.write_cells(k.float().numpy(), v.float().numpy(), kq, vq, layout, NAMES[dtype])
+        for t in range(k.shape[1]):
+            want[table[b, t // page], :, t % page, : layout.size] = cells[:, t]
+    return want
+
+
+def run(cache, layout, residual, table, qlens, lens, prefilling):
+    from economize_amd.vllm_kivi import quantize_committed
+
+    qsl = torch.tensor(np.concatenate([[0], np.cumsum(qlens)]), dtype=torch.int32).cuda()
+    quantize_committed(cache, layout, residual, table.cuda(), qsl, torch.tensor(lens, dtype=torch.int32).cuda(),
+                       torch.tensor(prefilling, dtype=torch.int32).cuda())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("bits,group,head,page", [(2, 32, 128, 32), (4, 16, 64, 32), (8, 32, 64, 64),
+                                                  (2, 16, 16, 16)])
+def test_quantized_cells_match_write_cells(dtype, bits, group, head, page) -> None:
+    residual = 2 * group
+    lens = [9 * group + 7, 3 * group + 1, 5 * group, 4 * group + 3, 2 * group]
+    qlens = [1, 4, 1, 0, 1]            # request 3 has no query this pass
+    prefilling = [0, 0, 1, 0, 0]       # request 2 is still prefilling
+    layout, cache, table, states = setup(dtype, bits, group, head, page, lens, seed=bits + group + head)
+    gpu = cache.cuda()
+    run(gpu, layout, residual, table, qlens, lens, prefilling)
+    bounds = []
+    for n, q, pre in zip(lens, qlens, prefilling):
+        c = n - q
+        bounds.append((0, 0) if pre or q == 0 or c <= 0 else ((c // residual) * residual, max(0, c - residual)))
+    want = expected(layout, cache, table, states, bounds, dtype, page)
+    got = gpu.view(torch.uint8).cpu().numpy()
+    assert np.array_equal(got, want)
+
+
+def test_a_second_pass_quantizes_what_crossed_the_residual() -> None:
+    dtype, bits, group, head, page = torch.bfloat16, 2, 32, 128, 32
+    residual = 64
+    lens = [300, 200]
+    layout, cache, table, states = setup(dtype, bits, group, head, page, lens, seed=11)
+    gpu = cache.cuda()
+    run(gpu, layout, residual, table, [1, 1], [230, 150], [0, 0])    # the first pass saw 229 and 149 tokens
+    run(gpu, layout, residual, table, [1, 1], [300, 200], [0, 0])    # then 299 and 199
+    want = expected(layout, cache, table, states, [(256, 235), (192, 135)], dtype, page)
+    # only the cells of the first 300 / 200 tokens exist; later slots of the pages stay zero on both sides
+    assert np.array_equal(gpu.view(torch.uint8).cpu().numpy(), want)
+
+
+def test_an_overflowing_key_group_is_flagged() -> None:
+    dtype, bits, group, head, page = torch.float32, 2, 32, 64, 32
+    layout, cache, table, states = setup(dtype, bits, group, head, page, [100], heads=1, seed=4, scale_up=slice(0, 32))
+    gpu = cache.cuda()
+    run(gpu, layout, 32, table, [1], [100], [0])
+    want = expected(layout, cache, table, states, [(96, 67)], dtype, page)
+    got = gpu.view(torch.uint8).cpu().numpy()
+    assert np.array_equal(got, want)
+    first_page = int(table[0, 0])
+    assert (got[first_page, 0, :, layout.off_flag] == oc.FLAG_OVERFLOW).all()
+
+
+def test_clear_flags() -> None:
+    from economize_amd.vllm_kivi import clear_flags
+
+    dtype, bits, group, head, page = torch.bfloat16, 4, 16, 64, 32
+    layout, cache, table, _ = setup(dtype, bits, group, head, page, [80], seed=2)
+    gpu = cache.cuda()
+    run(gpu, layout, 16, table, [1], [80], [0])
+    slots = torch.tensor([int(table[0, 0]) * page + 3, -1, int(table[0, 1]) * page + 10], dtype=torch.int32)
+    clear_flags(gpu, slots.cuda(), layout)
+    u8 = gpu.view(torch.uint8).cpu()
+    for slot in (int(slots[0]), int(slots[2])):
+        assert (u8[slot // page, :, slot % page, layout.off_flag: layout.off_flag + 2] == 0).all()
+    assert (u8[int(table[0, 0]), :, 4, layout.off_flag] == 1).all()
