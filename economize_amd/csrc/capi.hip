@@ -870,6 +870,85 @@ int eco_kivi_cells_quantize(void* cache, int32_t format, int64_t sb, int64_t sh,
     return kivi_cells_quantize(p, static_cast<hipStream_t>(stream));
 }
 
+size_t eco_kivi_cells_attention_workspace_size(int32_t requests, int32_t max_query_len, int32_t q_heads,
+                                               int32_t kv_heads, int32_t keys, int32_t head_dim) {
+    if (requests <= 0 || max_query_len <= 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || keys < 0)
+        return 0;
+    if (!dense_padded_dim(head_dim, head_dim)) return 0;
+    return dense_plan(requests, max_query_len, q_heads, kv_heads, std::max(keys, 1), head_dim, head_dim).workspace;
+}
+
+int eco_kivi_cells_attention(const void* q, int64_t sq_t, int64_t sq_h, const void* cache, int32_t format, int64_t sb,
+                             int64_t sh, int64_t sn, int32_t num_pages, int32_t page_size, int32_t kv_heads,
+                             const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                             const int32_t* query_start_loc, const int32_t* seq_lens, int32_t requests,
+                             int32_t max_query_len, int32_t keys, int32_t head_dim, int32_t bits, int32_t group,
+                             const float* sinks, void* out, int64_t so_t, int64_t so_h, int32_t q_heads, float scale,
+                             float softcap, void* workspace, size_t workspace_bytes, void* stream) {
+    CellsParams c;
+    if (int rc = cells_params(const_cast<void*>(cache), format, sb, sh, sn, num_pages, page_size, kv_heads, head_dim,
+                              bits, group, &c))
+        return rc;
+    if (!q || !out || !block_table || !query_start_loc || !seq_lens)
+        return fail("kivi cells attention: null query, output, block table, query offsets or lengths");
+    if (requests <= 0 || max_query_len <= 0 || q_heads <= 0 || keys <= 0)
+        return fail("kivi cells attention: requests, max_query_len, query heads and keys must be positive");
+    if (q_heads % kv_heads) return fail("kivi cells attention: query heads are not a multiple of the KV heads");
+    if (bt_cols <= 0 || bt_stride < bt_cols) return fail("kivi cells attention: bad block table");
+    const int es = element_bytes(format);
+    if ((reinterpret_cast<uintptr_t>(q) & 15) || (sq_t * es) % 16 || (sq_h * es) % 16)
+        return fail("kivi cells attention: the query must be 16-byte aligned with 16-byte strides");
+    if (!(scale == scale)) return fail("kivi cells attention: scale is NaN");
+    const DensePlan d = dense_plan(requests, max_query_len, q_heads, kv_heads, keys, head_dim, head_dim);
+    if (!d.padded_dim) return fail("kivi cells attention: head dims up to 256");
+    if (!workspace || workspace_bytes < d.workspace)
+        return fail("kivi cells attention: workspace too small (" + std::to_string(workspace_bytes) + " < " +
+                    std::to_string(d.workspace) + " bytes)");
+    DenseParams p;
+    std::memset(&p, 0, sizeof(p));
+    p.q = q;
+    p.sq_q = sq_t;
+    p.sq_h = sq_h;
+    p.q_format = format;
+    p.k = cache;
+    p.v = cache;
+    p.kv_format = format;
+    p.sinks = sinks;
+    p.out = out;
+    p.so_q = so_t;
+    p.so_h = so_h;
+    p.part = static_cast<float*>(workspace);
+    p.batch = requests;
+    p.queries = max_query_len;
+    p.q_heads = q_heads;
+    p.kv_heads = kv_heads;
+    p.groups = q_heads / kv_heads;
+    p.rows = p.groups * max_query_len;
+    p.keys = keys;
+    p.dense_keys = keys;
+    p.head_dim = head_dim;
+    p.value_dim = head_dim;
+    p.m_tiles = d.m_tiles;
+    p.splits = d.splits;
+    p.split_len = d.split_len;
+    p.scale = scale;
+    p.softcap = softcap > 0.0f ? softcap : 0.0f;
+    p.cells = static_cast<const uint8_t*>(cache);
+    p.sc_page = sb;
+    p.sc_head = sh;
+    p.sc_token = sn;
+    p.page_size = page_size;
+    p.num_pages = num_pages;
+    p.cell_off_v = c.L.off_v;
+    p.block_table = block_table;
+    p.bt_stride = bt_stride;
+    p.bt_cols = bt_cols;
+    p.seq_lens = seq_lens;
+    p.query_start_loc = query_start_loc;
+    p.causal = 1;
+    return dense_attention(p, d.padded_dim, static_cast<hipStream_t>(stream));
+}
+
 int eco_kivi_cells_clear_flags(void* cache, int32_t format, int64_t sb, int64_t sh, int64_t sn, int32_t num_pages,
                                int32_t page_size, int32_t kv_heads, const int32_t* slots, int32_t tokens,
                                int32_t head_dim, int32_t bits, int32_t group, void* stream) {

@@ -143,9 +143,14 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
     const int kvh = (prog / p.m_tiles) % p.kv_heads;
     const int b = prog / (p.m_tiles * p.kv_heads);
     const int r = mt * 16 + n;  // the lane's query row (MFMA column n)
-    const bool r_ok = r < p.rows;
-    const int gq = r_ok ? r / p.queries : 0;
-    const int qi = r_ok ? r % p.queries : 0;
+    // varlen queries: row b's queries are tokens q_start .. q_start + q_count - 1
+    const int q_start = p.query_start_loc ? p.query_start_loc[b] : 0;
+    const int q_count = p.query_start_loc ? p.query_start_loc[b + 1] - q_start : p.queries;
+    const int gq0 = r < p.rows ? r / p.queries : 0;
+    const int qi0 = r < p.rows ? r % p.queries : 0;
+    const bool r_ok = r < p.rows && qi0 < q_count;
+    const int gq = r_ok ? gq0 : 0;
+    const int qi = r_ok ? qi0 : 0;
     const int h = kvh * p.groups + gq;
 
     // the query operand: row r, channels 32 j + 8 g .. (zero past the head dim and for rows past the group)
@@ -158,7 +163,8 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
             qh[j][i] = static_cast<__bf16>(0.0f);
             ql[j][i] = static_cast<__bf16>(0.0f);
         }
-        if (r_ok && c < p.head_dim) load_query8<QF>(p, b * p.sq_b + h * p.sq_h + qi * p.sq_q + c, qh[j], ql[j]);
+        if (r_ok && c < p.head_dim)
+            load_query8<QF>(p, b * p.sq_b + h * p.sq_h + static_cast<int64_t>(q_start + qi) * p.sq_q + c, qh[j], ql[j]);
     }
     const float ks = p.k_scale ? p.k_scale[kvh] : 1.0f;
     const float vs = p.v_scale ? p.v_scale[kvh] : 1.0f;
@@ -167,8 +173,9 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
     const uint8_t* kbase = static_cast<const uint8_t*>(p.k) + (b * p.sk_b + kvh * p.sk_h) * ES;
     const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.sv_b + kvh * p.sv_h) * ES;
     const uint8_t* mrow = p.mask ? p.mask + b * p.sm_b + h * p.sm_h + qi * p.sm_q : nullptr;
-    // the key axis: dense slots, or (gathered) the row's compact entries followed by its dense slots from start on
-    int count = 0, start = 0, row_keys = p.keys;
+    // the key axis: dense slots, or (gathered) the row's compact entries followed by its dense slots from start on,
+    // or (cells) the row's seq_lens[b] tokens in its pages
+    int count = 0, start = 0, row_keys = p.cells ? min(max(p.seq_lens[b], 0), p.keys) : p.keys;
     const uint8_t* gkbase = kbase;
     const uint8_t* gvbase = vbase;
     const int32_t* gidx = nullptr;
@@ -180,14 +187,23 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
         gvbase = static_cast<const uint8_t*>(p.gv) + (b * p.sgv_b + kvh * p.sgv_h) * ES;
         gidx = p.g_index + b * p.sgi_b + kvh * p.sgi_h;
     }
+    auto cell_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
+        const int lp = min(t / p.page_size, p.bt_cols - 1);
+        const int page = min(max(p.block_table[static_cast<int64_t>(b) * p.bt_stride + lp], 0), p.num_pages - 1);
+        return p.cells + page * p.sc_page + kvh * p.sc_head + static_cast<int64_t>(t % p.page_size) * p.sc_token;
+    };
     auto key_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
+        if (p.cells) return cell_row(t);
         return t < count ? gkbase + static_cast<int64_t>(t) * p.sgk_s * ES
                          : kbase + static_cast<int64_t>(start + t - count) * p.sk_s * ES;
     };
     auto value_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
+        if (p.cells) return cell_row(t) + p.cell_off_v;
         return t < count ? gvbase + static_cast<int64_t>(t) * p.sgv_s * ES
                          : vbase + static_cast<int64_t>(start + t - count) * p.sv_s * ES;
     };
+    // causal: the last q_count keys of the row are its queries' own tokens
+    const int causal_limit = p.causal ? row_keys - q_count + qi + 1 : row_keys;
     auto mask_col = [&](int t) __attribute__((always_inline)) -> int64_t {
         return t < count ? min(max(gidx[t], 0), p.dense_keys - 1) : start + t - count;
     };
@@ -261,7 +277,7 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int t = t0 + 8 * g + e;
-            bool ok = r_ok && t < t_end;
+            bool ok = r_ok && t < t_end && t < causal_limit;
             if (ok && mrow) ok = mrow[mask_col(t) * p.sm_s] != 0;
             vis |= ok ? 1u << e : 0u;
         }
@@ -383,7 +399,10 @@ __global__ __launch_bounds__(256) void dense_merge_kernel(DenseParams p) {
             }
         }
         const int gq = r / p.queries, qi = r % p.queries;
-        store_out<QF>(p, b * p.so_b + qi * p.so_q + (kvh * p.groups + gq) * p.so_h + d, o * s_inv[rr]);
+        const int q_start = p.query_start_loc ? p.query_start_loc[b] : 0;
+        if (p.query_start_loc && qi >= p.query_start_loc[b + 1] - q_start) continue;  // an inactive query row
+        store_out<QF>(p, b * p.so_b + static_cast<int64_t>(q_start + qi) * p.so_q + (kvh * p.groups + gq) * p.so_h + d,
+                      o * s_inv[rr]);
     }
 }
 

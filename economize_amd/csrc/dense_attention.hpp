@@ -39,6 +39,23 @@ struct DenseParams {
     const int32_t* g_count;  // [B * Hkv]
     const int32_t* g_start;  // [B]
     int g_capacity, dense_keys;
+    // Cells mode (cells non-null; the reference's paged_kivi_attention over vLLM's cells, backends/vllm/kivi/
+    // kernels.py:216-415): key t of row b and KV head kvh is the dense K entry of the cell at byte
+    // block_table[b, t / page_size] * sc_page + kvh * sc_head + (t % page_size) * sc_token, its value cell_off_v bytes
+    // further; row b has seq_lens[b] keys. Page ids outside [0, num_pages) are clamped (wrong results, no access
+    // outside the cache).
+    const uint8_t* cells;
+    int64_t sc_page, sc_head, sc_token;
+    int page_size, num_pages, cell_off_v;
+    const int32_t* block_table;
+    int64_t bt_stride;
+    int bt_cols;
+    const int32_t* seq_lens;
+    // Varlen queries (query_start_loc non-null): query row qi of row b is token query_start_loc[b] + qi (strides sq_q,
+    // so_q; sq_b, so_b unused), rows qi >= that row's query count are inactive. causal: key t is visible to query row
+    // qi when t < keys_b - queries_b + qi + 1 (on top of the mask).
+    const int32_t* query_start_loc;
+    int causal;
 };
 
 int dense_padded_dim(int head_dim, int value_dim);  // 64, 128 or 256; 0 when neither fits

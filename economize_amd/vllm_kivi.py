@@ -11,11 +11,15 @@ vLLM keeps one *cell* per (page, KV head, token) of every attention layer; KIVI'
 already quantized (``eco_kivi_cells_quantize``), leaving every cell as the reference's ``write_cells`` lays it out; a
 quantized cell's dense entry holds the dequantized value, so attention over the dense entries is attention over the
 KIVI numbers. :func:`clear_flags` marks cells vLLM's cache write just filled as full precision.
+:func:`paged_kivi_attention` is the reference's attention over the cells with vLLM's varlen query layout and a
+causal bound per query (kernels.py:216-415): the dense decode kernel reading the cells' dense entries through the
+block table (``eco_kivi_cells_attention``).
 """
 
 from __future__ import annotations
 
 import ctypes
+import math
 from dataclasses import dataclass
 
 import torch
@@ -24,7 +28,7 @@ from . import _lib
 from .errors import ConfigError
 
 __all__ = ["FLAG_DENSE", "FLAG_OVERFLOW", "FLAG_PACKED", "CellLayout", "cache_views", "cell_layout", "clear_flags",
-           "quantize_committed"]
+           "paged_kivi_attention", "quantize_committed"]
 
 FLAG_DENSE, FLAG_PACKED, FLAG_OVERFLOW = 0, 1, 2
 _DTYPES = (torch.bfloat16, torch.float16, torch.float32)
@@ -132,3 +136,69 @@ def clear_flags(kv_cache: torch.Tensor, slot_mapping: torch.Tensor, layout: Cell
         raise ConfigError("slot_mapping must be a contiguous int32 [tokens]")
     _lib.call("eco_kivi_cells_clear_flags", *_cells_args(kv_cache, layout), slot_mapping.data_ptr(),
               slot_mapping.shape[0], layout.head_size, layout.bits, layout.group_size, _lib.stream_of(device))
+
+
+def paged_kivi_attention(query: torch.Tensor, kv_cache: torch.Tensor, layout: CellLayout, block_table: torch.Tensor,
+                         query_start_loc: torch.Tensor, seq_lens: torch.Tensor, max_query_len: int, keys: int,
+                         scale: float | None = None, out: torch.Tensor | None = None, softcap: float | None = None,
+                         sinks: torch.Tensor | None = None) -> torch.Tensor:
+    """Attention of vLLM's varlen queries over the cells (kernels.py:354-415).
+
+    Args:
+        query: ``[tokens, Hq, D]`` in the cache dtype (channel stride 1); request ``b``'s queries are tokens
+            ``query_start_loc[b] .. query_start_loc[b + 1] - 1``.
+        kv_cache: One layer's cache, typed ``[pages, heads, page_size, cell elements]``.
+        layout: Its cell layout.
+        block_table: int32 ``[requests, pages per request]``.
+        query_start_loc: int32 ``[requests + 1]``.
+        seq_lens: int32 ``[requests]``: query ``i`` of a request of ``n`` queries sees keys ``< seq_len - n + i + 1``.
+        max_query_len: The longest query of the batch.
+        keys: The longest ``seq_len`` of the batch.
+        scale: Multiplier of the scores (``1 / sqrt(D)`` by default).
+        out: Optional ``[tokens, Hq, D]`` output in the query's dtype.
+        softcap: Optional tanh soft cap.
+        sinks: Optional ``[Hq]`` attention-sink logits.
+
+    Returns:
+        ``[tokens, Hq, D]``.
+    """
+    device = _lib.require_gpu(query, kv_cache, block_table, query_start_loc, seq_lens)
+    typed, u8 = cache_views(kv_cache)
+    if query.dim() != 3 or query.dtype != typed.dtype or query.stride(-1) != 1:
+        raise ConfigError("paged_kivi_attention takes queries [tokens, Hq, D] in the cache dtype with contiguous "
+                          "channels")
+    tokens, q_heads, dim = query.shape
+    requests = seq_lens.shape[0]
+    if dim != layout.head_size:
+        raise ConfigError(f"queries of {dim} channels for cells of {layout.head_size}")
+    for name, t, n in (("query_start_loc", query_start_loc, requests + 1), ("seq_lens", seq_lens, requests)):
+        if t.dtype != torch.int32 or t.shape != (n,) or not t.is_contiguous():
+            raise ConfigError(f"{name} must be a contiguous int32 [{n}]")
+    if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1:
+        raise ConfigError("block_table must be int32 [requests, pages] with contiguous rows")
+    if out is None:
+        out = torch.empty_like(query)
+    elif out.shape != query.shape or out.dtype != query.dtype or out.stride(-1) != 1:
+        raise ConfigError("out must be [tokens, Hq, D] in the query's dtype with contiguous channels")
+    if requests == 0 or tokens == 0:
+        return out
+    s = None
+    if sinks is not None:
+        if sinks.numel() != q_heads:
+            raise ConfigError(f"{sinks.numel()} sink logits for {q_heads} query heads")
+        s = sinks.reshape(-1).float().contiguous()
+    need = int(_lib.lib().eco_kivi_cells_attention_workspace_size(requests, max_query_len, q_heads, u8.shape[1],
+                                                                   max(keys, 1), dim))
+    if need == 0:
+        raise ConfigError("paged_kivi_attention: unsupported shape")
+    from .decode import _workspace
+
+    ws = _workspace(need, device)
+    scale = 1.0 / math.sqrt(dim) if scale is None else scale
+    _lib.call("eco_kivi_cells_attention", query.data_ptr(), query.stride(0), query.stride(1), u8.data_ptr(),
+              _lib.fmt(typed.dtype), u8.stride(0), u8.stride(1), u8.stride(2), u8.shape[0], u8.shape[2], u8.shape[1],
+              block_table.data_ptr(), block_table.stride(0), block_table.shape[1], query_start_loc.data_ptr(),
+              seq_lens.data_ptr(), requests, int(max_query_len), max(int(keys), 1), dim, layout.bits,
+              layout.group_size, _lib.ptr(s), out.data_ptr(), out.stride(0), out.stride(1), q_heads, float(scale),
+              float(softcap or 0.0), ws.data_ptr(), ws.numel(), _lib.stream_of(device))
+    return out

@@ -278,6 +278,24 @@ int eco_kivi_cells_quantize(void* cache, int32_t format, int64_t sb, int64_t sh,
                             const int32_t* prefilling, int32_t requests, int32_t head_dim, int32_t bits,
                             int32_t group, int32_t residual, void* stream);
 
+/* The reference's paged_kivi_attention (backends/vllm/kivi/kernels.py:216-415) over the cells of one layer's cache
+ * [pages, kv_heads, page_size] (byte strides sb, sh, sn; entries and queries of format bf16 / fp16 / fp32): vLLM's
+ * varlen queries q [tokens, q_heads, D] (element strides sq_t, sq_h; request b's queries are tokens
+ * query_start_loc[b] .. query_start_loc[b + 1] - 1, at most max_query_len), each attending causally over its
+ * request's seq_lens[b] keys (query i of a request of n queries sees keys < seq_len - n + i + 1), read from the
+ * cells' dense entries, which hold every quantized key and value as its dequantized value; out [tokens, q_heads, D]
+ * (strides so_t, so_h); keys = the longest seq_len; optional sinks [q_heads] and soft cap. Workspace:
+ * eco_kivi_cells_attention_workspace_size. */
+size_t eco_kivi_cells_attention_workspace_size(int32_t requests, int32_t max_query_len, int32_t q_heads,
+                                               int32_t kv_heads, int32_t keys, int32_t head_dim);
+int eco_kivi_cells_attention(const void* q, int64_t sq_t, int64_t sq_h, const void* cache, int32_t format, int64_t sb,
+                             int64_t sh, int64_t sn, int32_t num_pages, int32_t page_size, int32_t kv_heads,
+                             const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                             const int32_t* query_start_loc, const int32_t* seq_lens, int32_t requests,
+                             int32_t max_query_len, int32_t keys, int32_t head_dim, int32_t bits, int32_t group,
+                             const float* sinks, void* out, int64_t so_t, int64_t so_h, int32_t q_heads, float scale,
+                             float softcap, void* workspace, size_t workspace_bytes, void* stream);
+
 /* clear_flags (kernels.py:58-78): the cells of slots[tokens] (page * page_size + position; negative: padding) of
  * every KV head marked full precision (both flags 0), after vLLM's cache write filled them. */
 int eco_kivi_cells_clear_flags(void* cache, int32_t format, int64_t sb, int64_t sh, int64_t sn, int32_t num_pages,

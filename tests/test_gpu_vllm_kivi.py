@@ -121,3 +121,44 @@ def test_clear_flags() -> None:
     for slot in (int(slots[0]), int(slots[2])):
         assert (u8[slot // page, :, slot % page, layout.off_flag: layout.off_flag + 2] == 0).all()
     assert (u8[int(table[0, 0]), :, 4, layout.off_flag] == 1).all()
+
+
+def gathered_cells(cache_u8: np.ndarray, table, b: int, n: int, page: int, layout) -> np.ndarray:
+    """uint8 [H, n, cell] of request b's first n tokens."""
+    return np.stack([cache_u8[int(table[b, t // page]), :, t % page, : layout.size] for t in range(n)], axis=1)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("bits,group,head,q_heads", [(2, 32, 128, 8), (4, 16, 64, 4)])
+def test_attention_over_the_cells_matches_the_oracle(dtype, bits, group, head, q_heads) -> None:
+    """vLLM's varlen queries (1, 4, 0 and 3 of them, ragged lengths) attend causally over their request's cells
+    after quantize_committed; the oracle reads the cells back (read_cells) and applies the fp32 definition."""
+    from economize_amd.vllm_kivi import paged_kivi_attention
+    from oracle.attention import reference_attention
+
+    page, residual = 32, 2 * group
+    lens = [9 * group + 7, 4 * group + 1, 6 * group, 3 * group + 3]
+    qlens = [1, 4, 0, 3]
+    layout, cache, table, _ = setup(dtype, bits, group, head, page, lens, seed=bits + head)
+    gpu = cache.cuda()
+    run(gpu, layout, residual, table, qlens, lens, [0, 0, 0, 0])
+    gen = torch.Generator().manual_seed(9)
+    query = torch.randn(sum(qlens), q_heads, head, generator=gen).to(dtype)
+    qsl = torch.tensor(np.concatenate([[0], np.cumsum(qlens)]), dtype=torch.int32)
+    sinks = torch.randn(q_heads, generator=gen) if dtype == torch.bfloat16 else None
+    out = paged_kivi_attention(query.cuda(), gpu, layout, table.cuda(), qsl.cuda(),
+                               torch.tensor(lens, dtype=torch.int32).cuda(), max(qlens), max(lens), scale=0.1,
+                               softcap=30.0 if sinks is not None else None,
+                               sinks=None if sinks is None else sinks.cuda()).float().cpu().numpy()
+    cells = gpu.view(torch.uint8).cpu().numpy()
+    for b, (n, q) in enumerate(zip(lens, qlens)):
+        if q == 0:
+            continue
+        k, v = oc.read_cells(gathered_cells(cells, table, b, n, page, layout), layout, NAMES[dtype])
+        mask = np.zeros((1, 1, q, n), bool)
+        for i in range(q):
+            mask[..., i, : n - q + i + 1] = True
+        qb = query[qsl[b]: qsl[b + 1]].float().numpy().transpose(1, 0, 2)[None]
+        want = reference_attention(qb, k[None], v[None], mask, 0.1, 30.0 if sinks is not None else None,
+                                   None if sinks is None else sinks.numpy())[0]
+        np.testing.assert_allclose(out[qsl[b]: qsl[b + 1]], want, atol=2e-3, rtol=1e-2, err_msg=f"request {b}")
