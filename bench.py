@@ -359,6 +359,173 @@ def measure_quest(steps: int, warmup: int, seed: int, batch=8, q_heads=32, kv_he
             "dense_bytes_avoided": batch * kv_heads * length * 2 * d * 2, "copies": copies}
 
 
+def _result(seconds: float, nbytes: int, copies: int, **extra) -> dict:
+    return {"us_per_call": round(seconds * 1e6, 2), "algorithmic_bytes": int(nbytes),
+            "gb_s": round(nbytes / seconds / 1e9, 1), "hbm_frac": round(nbytes / seconds / 1e9 / HBM_PEAK_GBS, 4),
+            "copies": copies, **extra}
+
+
+def measure_dense(steps: int, warmup: int, seed: int, kv_dtype, batch=32, q_heads=32, kv_heads=8, length=4096) -> dict:
+    """decode_attention over dense [B, Hkv, L, D] buffers (a model cache's own layout; fp8 views: the fused fp8 cache's
+    dense buffers): K and V read once, plus the query and output."""
+    import torch
+
+    from economize_amd.decode import decode_attention
+
+    d = HEAD_DIM
+    gen = torch.Generator(device="cuda:0").manual_seed(seed)
+    es = torch.empty((), dtype=kv_dtype).element_size()
+    nbytes = batch * kv_heads * length * 2 * d * es + 2 * batch * q_heads * d * 2
+    q = torch.randn(batch, 1, q_heads, d, generator=gen, device="cuda:0").to(torch.bfloat16).transpose(1, 2)
+    copies = copies_for(nbytes)
+    loads = []
+    for _ in range(copies):
+        k = torch.randn(batch, kv_heads, length, d, generator=gen, device="cuda:0").to(kv_dtype)
+        v = torch.randn(batch, kv_heads, length, d, generator=gen, device="cuda:0").to(kv_dtype)
+        loads.append((k, v))
+    out = torch.empty(batch, 1, q_heads, d, dtype=torch.bfloat16, device="cuda:0")
+    scale = 1 / math.sqrt(d)
+    seconds = time_calls(rotating([lambda k=k, v=v: decode_attention(q, k, v, None, scale, out=out)
+                                   for k, v in loads]), steps, warmup)
+    del loads
+    return _result(seconds, nbytes, copies)
+
+
+def measure_gathered(steps: int, warmup: int, seed: int, batch=32, q_heads=32, kv_heads=8, prompt=3968, tail=128,
+                     keep=0.5) -> dict:
+    """gathered_decode_attention: every (row, KV head) keeps a random half of its prompt entries (an eviction's
+    compacted entries) and reads them plus a dense tail of generated tokens; bytes are the entries read."""
+    import numpy as np
+    import torch
+
+    from economize_amd.gathered import GatheredKV, gathered_decode_attention
+
+    d = HEAD_DIM
+    slots = prompt + tail
+    rng = np.random.default_rng(seed)
+    cap = int(prompt * keep)
+    count = torch.full((batch, kv_heads), cap, dtype=torch.int32, device="cuda:0")
+    index = torch.from_numpy(np.sort(np.stack([rng.choice(prompt, cap, replace=False)
+                                               for _ in range(batch * kv_heads)]), axis=1).astype(np.int32)) \
+        .view(batch, kv_heads, cap).cuda()
+    start = torch.full((batch,), prompt, dtype=torch.int32, device="cuda:0")
+    nbytes = batch * kv_heads * (cap + tail) * 2 * d * 2 + 2 * batch * q_heads * d * 2 + index.numel() * 4
+    gen = torch.Generator(device="cuda:0").manual_seed(seed)
+    q = torch.randn(batch, 1, q_heads, d, generator=gen, device="cuda:0").to(torch.bfloat16).transpose(1, 2)
+    copies = copies_for(nbytes)
+    loads = []
+    for _ in range(copies):
+        k = torch.randn(batch, kv_heads, slots, d, generator=gen, device="cuda:0").to(torch.bfloat16)
+        v = torch.randn(batch, kv_heads, slots, d, generator=gen, device="cuda:0").to(torch.bfloat16)
+        ck = torch.randn(batch, kv_heads, cap, d, generator=gen, device="cuda:0").to(torch.bfloat16)
+        cv = torch.randn(batch, kv_heads, cap, d, generator=gen, device="cuda:0").to(torch.bfloat16)
+        loads.append((k, v, GatheredKV(ck, cv, index, count, start, prompt - cap)))
+    out = torch.empty(batch, 1, q_heads, d, dtype=torch.bfloat16, device="cuda:0")
+    scale = 1 / math.sqrt(d)
+    seconds = time_calls(rotating([lambda k=k, v=v, g=g: gathered_decode_attention(q, k, v, None, scale, g, out=out)
+                                   for k, v, g in loads]), steps, warmup)
+    del loads
+    return _result(seconds, nbytes, copies, dense_bytes=batch * kv_heads * slots * 2 * d * 2)
+
+
+def measure_cells(steps: int, warmup: int, seed: int, batch=16, q_heads=32, kv_heads=8, length=8192, bits=2,
+                  page=32) -> dict:
+    """paged_kivi_attention over vLLM's KIVI cells (bf16 entries, int2, groups of 32): one query per request, the
+    cells' dense entries read once (K and V, bf16), plus queries, outputs and the block table."""
+    import torch
+
+    from economize_amd.vllm_kivi import cell_layout, paged_kivi_attention
+
+    d = HEAD_DIM
+    layout = cell_layout(d, torch.bfloat16, bits, 32)
+    per_row = length // page
+    pages = batch * per_row
+    nbytes = batch * kv_heads * length * 2 * d * 2 + 2 * batch * q_heads * d * 2 + pages * 4
+    gen = torch.Generator(device="cuda:0").manual_seed(seed)
+    table = torch.randperm(pages, generator=gen, device="cuda:0").view(batch, per_row).to(torch.int32)
+    q = torch.randn(batch, q_heads, d, generator=gen, device="cuda:0").to(torch.bfloat16)
+    qsl = torch.arange(batch + 1, dtype=torch.int32, device="cuda:0")
+    seq = torch.full((batch,), length, dtype=torch.int32, device="cuda:0")
+    copies = copies_for(nbytes)
+    caches = [torch.randn(pages, kv_heads, page, layout.size // 2, generator=gen, device="cuda:0").to(torch.bfloat16)
+              for _ in range(copies)]
+    out = torch.empty_like(q)
+    seconds = time_calls(rotating([lambda c=c: paged_kivi_attention(q, c, layout, table, qsl, seq, 1, length, out=out)
+                                   for c in caches]), steps, warmup)
+    cell_bytes = pages * kv_heads * page * layout.size
+    del caches
+    return _result(seconds, nbytes, copies, cache_bytes=cell_bytes)
+
+
+def measure_quest_graph(steps: int, warmup: int, seed: int, batch=8, q_heads=32, kv_heads=8, length=32768,
+                        budget=1024) -> dict:
+    """A Quest decode step with its metadata on the device (QuestState): one appended token per row, the bounds
+    refresh, the selection with a static max_done and the page-list attention, captured once in a HIP graph and
+    replayed, against the same step launched eagerly."""
+    import torch
+
+    from economize_amd.paged import paged_append
+    from economize_amd.quest import QuestState, quest_decode_attention
+
+    d = HEAD_DIM
+    query, cache, table, seq, qp = quest_workload(seed, batch, q_heads, kv_heads, length, budget, 32)
+    pages = budget // PAGE - 1
+    state = QuestState(batch, kv_heads, d, length // PAGE, PAGE, pages, "cuda:0")  # the table's capacity
+    committed = (seq - 1).contiguous()
+    state.refresh(cache, table, committed)
+    k_new = torch.zeros(batch, kv_heads, d, dtype=torch.bfloat16, device="cuda:0")
+    slots = (table[:, -1] * PAGE + PAGE - 1).contiguous()  # each step rewrites every row's last token
+    out = torch.empty(batch, 1, q_heads, d, dtype=torch.bfloat16, device="cuda:0")
+    handle = state.pages_handle()
+
+    def step() -> None:
+        paged_append(cache, k_new, k_new, slots)
+        state.refresh(cache, table, committed)
+        quest_decode_attention(query, cache, table, seq, length, handle, out=out)  # static: the capacity
+
+    eager = time_calls(step, steps, warmup)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    replay = time_calls(graph.replay, steps, warmup)
+    done = (length - 1) // PAGE
+    tail = length - done * PAGE
+    nbytes = (batch * kv_heads * (2 * d * 2 * state.max_pages + (pages * PAGE + tail) * 2 * d * 2)
+              + 2 * batch * q_heads * d * 2)
+    del graph, cache, state
+    return {"us_per_step_graph": round(replay * 1e6, 2), "us_per_step_eager": round(eager * 1e6, 2),
+            "algorithmic_bytes": int(nbytes), "gb_s_graph": round(nbytes / replay / 1e9, 1),
+            "hbm_frac_graph": round(nbytes / replay / 1e9 / HBM_PEAK_GBS, 4), "copies": 1}
+
+
+def measure_next_rows(steps: int, warmup: int, seed: int) -> dict:
+    import torch
+
+    rows = {}
+    for name, workload, fn in (
+        ("dense_decode_bf16", "decode_attention over dense bf16 [B, Hkv, L, D] buffers, B=32 Hq=32 Hkv=8 D=128 L=4096",
+         lambda: measure_dense(steps, warmup, seed, torch.bfloat16)),
+        ("dense_decode_fp8", "decode_attention over dense fp8 e4m3 views (the fused fp8 cache), same shape",
+         lambda: measure_dense(steps, warmup, seed, torch.float8_e4m3fn)),
+        ("gathered_decode", "gathered_decode_attention, B=32 Hq=32 Hkv=8 D=128, half of a 3968-token prompt kept per "
+                            "KV head + 128 tail tokens, bf16", lambda: measure_gathered(steps, warmup, seed)),
+        ("kivi_cells_attention", "paged_kivi_attention over vLLM KIVI cells (bf16 entries, int2, G=32), B=16 Hq=32 "
+                                 "Hkv=8 D=128 L=8192, one query per request",
+         lambda: measure_cells(steps, warmup, seed)),
+        ("quest_graph_step", "Quest decode step with device metadata (append + bounds refresh + selection + "
+                             "attention), B=8 Hq=32 Hkv=8 D=128 L=32768, captured graph vs eager",
+         lambda: measure_quest_graph(steps, warmup, seed)),
+    ):
+        rows[name] = {"workload": workload, **fn()}
+        torch.cuda.empty_cache()
+    return rows
+
+
 def measure_paths(steps: int, warmup: int, seed: int) -> dict:
     import numpy as np
     import torch
@@ -379,6 +546,7 @@ def measure_paths(steps: int, warmup: int, seed: int) -> dict:
         "sum_len": int(sum(lens)),
         **measure_kivi(4, steps, warmup, seed, batch=64, queries=8, q_heads=64, kv_heads=8, lens=lens)}
     torch.cuda.empty_cache()
+    paths.update(measure_next_rows(steps, warmup, seed))
     return paths
 
 

@@ -128,7 +128,12 @@ DensePlan dense_plan(int batch, int queries, int q_heads, int kv_heads, int keys
     d.padded_dim = dense_padded_dim(head_dim, value_dim);
     const int64_t programs = static_cast<int64_t>(batch) * kv_heads * d.m_tiles;
     const int64_t tiles = (std::max(keys, 1) + 31) / 32;
-    int64_t splits = (4 * static_cast<int64_t>(device_cus()) + programs - 1) / programs;
+    // waves per CU the splits aim at (ECO_DENSE_WAVES overrides it for tuning)
+    static const int per_cu = [] {
+        const char* env = std::getenv("ECO_DENSE_WAVES");
+        return env && std::atoi(env) > 0 ? std::atoi(env) : 8;
+    }();
+    int64_t splits = (per_cu * static_cast<int64_t>(device_cus()) + programs - 1) / programs;
     splits = std::max<int64_t>(1, std::min(splits, tiles));
     d.split_len = static_cast<int>((tiles + splits - 1) / splits) * 32;
     d.splits = static_cast<int>((std::max(keys, 1) + d.split_len - 1) / d.split_len);
@@ -895,6 +900,7 @@ int eco_kivi_cells_attention(const void* q, int64_t sq_t, int64_t sq_h, const vo
         return fail("kivi cells attention: requests, max_query_len, query heads and keys must be positive");
     if (q_heads % kv_heads) return fail("kivi cells attention: query heads are not a multiple of the KV heads");
     if (bt_cols <= 0 || bt_stride < bt_cols) return fail("kivi cells attention: bad block table");
+    if (page_size % 16) return fail("kivi cells attention: pages must hold a multiple of 16 tokens");
     const int es = element_bytes(format);
     if ((reinterpret_cast<uintptr_t>(q) & 15) || (sq_t * es) % 16 || (sq_h * es) % 16)
         return fail("kivi cells attention: the query must be 16-byte aligned with 16-byte strides");

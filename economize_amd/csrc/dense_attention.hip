@@ -187,10 +187,22 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
         gvbase = static_cast<const uint8_t*>(p.gv) + (b * p.sgv_b + kvh * p.sgv_h) * ES;
         gidx = p.g_index + b * p.sgi_b + kvh * p.sgi_h;
     }
-    auto cell_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
+    // cells: the cache pages of the current tile's two 16-key halves, looked up once per tile (tile_pages)
+    int64_t cell_half[2] = {0, 0};
+    auto page_base = [&](int t) __attribute__((always_inline)) -> int64_t {
         const int lp = min(t / p.page_size, p.bt_cols - 1);
         const int page = min(max(p.block_table[static_cast<int64_t>(b) * p.bt_stride + lp], 0), p.num_pages - 1);
-        return p.cells + page * p.sc_page + kvh * p.sc_head + static_cast<int64_t>(t % p.page_size) * p.sc_token;
+        return page * p.sc_page + kvh * p.sc_head;
+    };
+    auto tile_pages = [&](int t0) __attribute__((always_inline)) {
+        if (p.cells) {
+            cell_half[0] = page_base(t0);
+            cell_half[1] = p.page_size % 32 == 0 ? cell_half[0] : page_base(t0 + 16);
+        }
+    };
+    auto cell_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
+        // a tile starts at a multiple of 32 keys and pages hold a multiple of 16, so each 16-key half lies in one page
+        return p.cells + cell_half[(t >> 4) & 1] + static_cast<int64_t>(t % p.page_size) * p.sc_token;
     };
     auto key_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
         if (p.cells) return cell_row(t);
@@ -221,6 +233,7 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
     constexpr bool kStage = CPL <= 8;          // the tile's values pass through registers (loads issued first)
     constexpr int KW = ES == 4 ? 2 : 1;        // 16-byte words of 8 key elements (fp8: the low half of one)
     for (int t0 = t_begin; t0 < t_end; t0 += TK) {
+        tile_pages(t0);
         // ---- issue the tile's loads: values (staged for LDS), then keys (A-row n of block v is key
         // t0 + 8 (n / 4) + 4 v + n % 4; a key past the split reads the split's last key and is masked) ----
         auto value_chunk = [&](int chunk) __attribute__((always_inline)) -> uint4 {
