@@ -115,10 +115,11 @@ int kivi_grid(int batch, int kv_heads, int rows, int head_dim, int bits, int max
 }
 
 // The dense decode launch plan, a function of the shapes only: blocks of 16 query rows, and the key axis cut into
-// splits (multiples of 32 keys) so that about four waves per CU run.
+// splits (multiples of 32 keys) so that about eight waves per CU run. Workspace: a counter per block (int32, zero
+// before the first call; every call leaves them zero), then each block's split partials [splits][16][D + 2] floats.
 struct DensePlan {
-    int m_tiles, splits, split_len, padded_dim;
-    size_t workspace;
+    int m_tiles, splits, padded_dim;
+    size_t counter_bytes, workspace;
 };
 
 DensePlan dense_plan(int batch, int queries, int q_heads, int kv_heads, int keys, int head_dim, int value_dim) {
@@ -135,9 +136,12 @@ DensePlan dense_plan(int batch, int queries, int q_heads, int kv_heads, int keys
     }();
     int64_t splits = (per_cu * static_cast<int64_t>(device_cus()) + programs - 1) / programs;
     splits = std::max<int64_t>(1, std::min(splits, tiles));
-    d.split_len = static_cast<int>((tiles + splits - 1) / splits) * 32;
-    d.splits = static_cast<int>((std::max(keys, 1) + d.split_len - 1) / d.split_len);
-    d.workspace = align256(static_cast<size_t>(programs) * d.splits * 16 * (d.padded_dim + 2) * sizeof(float));
+    // as many splits as an even share of the tiles needs (split s takes tiles s, s + splits, ...)
+    const int64_t share = (tiles + splits - 1) / splits;
+    d.splits = static_cast<int>((tiles + share - 1) / share);
+    d.counter_bytes = align256(static_cast<size_t>(programs) * sizeof(int32_t));
+    d.workspace = d.counter_bytes +
+                  align256(static_cast<size_t>(programs) * d.splits * 16 * (d.padded_dim + 2) * sizeof(float));
     return d;
 }
 
@@ -376,7 +380,8 @@ int dense_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, in
     p.so_b = so_b;
     p.so_q = so_q;
     p.so_h = so_h;
-    p.part = static_cast<float*>(workspace);
+    p.counters = static_cast<int32_t*>(workspace);
+    p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + d.counter_bytes);
     p.batch = batch;
     p.queries = queries;
     p.q_heads = q_heads;
@@ -389,7 +394,6 @@ int dense_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, in
     p.value_dim = value_dim;
     p.m_tiles = d.m_tiles;
     p.splits = d.splits;
-    p.split_len = d.split_len;
     p.scale = scale;
     p.softcap = softcap > 0.0f ? softcap : 0.0f;
     if (g) {
@@ -451,7 +455,7 @@ extern "C" {
 
 const char* eco_last_error(void) { return g_error.c_str(); }
 
-int eco_abi_version(void) { return 3; }
+int eco_abi_version(void) { return 4; }
 
 int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
                      int64_t sv_t, int64_t sv_h, const int32_t* slot_mapping, int32_t tokens, void* k_cache,
@@ -923,7 +927,8 @@ int eco_kivi_cells_attention(const void* q, int64_t sq_t, int64_t sq_h, const vo
     p.out = out;
     p.so_q = so_t;
     p.so_h = so_h;
-    p.part = static_cast<float*>(workspace);
+    p.counters = static_cast<int32_t*>(workspace);
+    p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + d.counter_bytes);
     p.batch = requests;
     p.queries = max_query_len;
     p.q_heads = q_heads;
@@ -936,7 +941,6 @@ int eco_kivi_cells_attention(const void* q, int64_t sq_t, int64_t sq_h, const vo
     p.value_dim = head_dim;
     p.m_tiles = d.m_tiles;
     p.splits = d.splits;
-    p.split_len = d.split_len;
     p.scale = scale;
     p.softcap = softcap > 0.0f ? softcap : 0.0f;
     p.cells = static_cast<const uint8_t*>(cache);

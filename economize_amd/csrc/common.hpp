@@ -46,6 +46,17 @@ __device__ inline float group_sum(float x) {  // sum over the four lanes l, l^16
     return x + __shfl_xor(x, 32);
 }
 
+// Device-coherent (agent-scope) store and load of partial results handed between workgroups (gfx950 lowers them to
+// global_store / global_load with sc1: written through to, and read from, the level every XCD sees). The kernels order
+// a hand-off with signal fences, a wait for the stores' completion and an agent-scope counter.
+__device__ inline void coherent_store(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ inline float coherent_load(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // cap * tanh(x / cap) in log2 units (times log2 e), with inv_cap = 1 / cap: tanh(|t|) = (1 - e) / (1 + e), e =
 // exp(-2 |t|), through the hardware exp2 and reciprocal (each within a few ulp; the reference's soft cap is the same
 // expression in fp32).

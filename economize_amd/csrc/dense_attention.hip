@@ -10,9 +10,12 @@
 // exact for fp16, 16 significant bits for fp32), and a product of two-term operands sums hi.hi + hi.lo + lo.hi
 // (the lo.lo term is below fp32 rounding of the sum). The softmax weights p are split the same way for P.V.
 //
-// Work split (flash-decoding, as the reference): the key axis is cut into splits of split_len keys; one wave takes
-// one (row, KV head, block of 16 query rows, split) and walks its split in tiles of 32 keys; a merge kernel combines
-// the splits by log-sum-exp. Per tile, S^T = K Q^T with v_mfma_f32_16x16x32_bf16: A-row m of MFMA block v is key
+// Work split (flash-decoding, as the reference): the key axis is cut into S splits; one wave takes one (row, KV
+// head, block of 16 query rows, split s) and walks the tiles of 32 keys s, s + S, s + 2 S, ... (the block's waves
+// read adjacent runs together), the next tile's loads in flight while a tile is computed (two register buffers
+// where they fit). The splits of a block combine by
+// log-sum-exp in the last of its waves to finish (an agent-scope counter per block in the workspace, left zero by
+// every call), one launch per call; a single split writes its rows directly. Per tile, S^T = K Q^T with v_mfma_f32_16x16x32_bf16: A-row m of MFMA block v is key
 // 8 (m / 4) + 4 v + m % 4, so that lane (n, g) ends with keys 8 g .. 8 g + 7 of query row n, which is exactly the B
 // operand of O^T += V^T P^T; the keys are read token-major from HBM straight into the A operand (16-byte loads).
 // V^T needs a lane to hold 8 keys of one channel: the tile's values are staged through LDS (coalesced 16-byte loads,
@@ -125,14 +128,54 @@ __device__ __forceinline__ void load_query8(const DenseParams& p, int64_t offset
     cvt8<QF>(w, hi, lo);
 }
 
-template <int DP, int FMT, int QF>
-__global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
+template <int QF>
+__device__ __forceinline__ void store_out(const DenseParams& p, int64_t offset, float x) {
+    if constexpr (QF == BF16)
+        static_cast<uint16_t*>(p.out)[offset] = f32_to_bf16(x);
+    else if constexpr (QF == FP16)
+        static_cast<_Float16*>(p.out)[offset] = static_cast<_Float16>(x);
+    else
+        static_cast<float*>(p.out)[offset] = x;
+}
+
+// The output weight of a row whose keys gave maximum m and sum l (log2 units) with the sink logit (-inf: none): the
+// accumulators times 2^(m - M), divided by l 2^(m - M) + 2^(sink - M), M = max(m, sink) (decode.py's merge,
+// attention/_decode_kernels.py:183-226); 0 where nothing is visible. Returns 2^(m - M) and sets inv = 1 / that sum.
+__device__ inline float sink_weight(float m, float l, float sink, float& inv) {
+    const float big = fmaxf(m, sink);
+    float total = 0.0f, a = 0.0f;
+    if (big != -INFINITY) {
+        if (m != -INFINITY) {
+            a = __builtin_amdgcn_exp2f(m - big);
+            total = l * a;
+        }
+        if (sink != -INFINITY) total += __builtin_amdgcn_exp2f(sink - big);
+    }
+    inv = total > 0.0f ? 1.0f / total : 0.0f;
+    return a;
+}
+
+template <int DP, int FMT, int QF, bool MASKED>
+__global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
     constexpr int ES = elem_bytes<FMT>();
     constexpr int KS = DP / 32;  // k-steps of the S MFMA
     constexpr int ND = DP / 16;  // value blocks of 16 channels
     constexpr bool KLO = two_terms<FMT>();
     constexpr bool QLO = two_terms<QF>();
-    constexpr int ROW = DP * ES + 16;  // LDS bytes per staged value row
+    constexpr int ROW = DP * ES + 16;          // LDS bytes per staged value row
+    constexpr int CHUNKS = TK * DP * ES / 16;  // 16-byte chunks of a staged value tile (a multiple of 64)
+    constexpr int CPR = DP * ES / 16;          // chunks per value row
+    constexpr int CPL = CHUNKS / 64;           // chunks per lane
+    constexpr bool kStage = CPL <= 8;          // the tile's values pass through registers (loads issued first)
+    constexpr int KW = ES == 4 ? 2 : 1;        // 16-byte words of 8 key elements (fp8: the low half of one)
+    // The next tile's loads are in flight while a tile is computed (NBUF = 2) when the registers allow: one set of
+    // staged values (moved into LDS before the next tile's values are issued into it), two sets of keys (fp8 keys
+    // fill half a word; with a mask, eight mask bytes), the accumulators and the query operand within 170 VGPRs
+    // (beyond that the second key set spills at two waves per SIMD).
+    constexpr int KEY_VGPRS = 2 * KS * KW * (ES == 1 ? 2 : 4) + (MASKED ? 8 : 0);
+    constexpr int LIVE_VGPRS = (kStage ? 4 * CPL : 0) + 2 * KEY_VGPRS + 4 * ND + 4 * KS * (QLO ? 2 : 1);
+    constexpr int NBUF = kStage && LIVE_VGPRS <= 170 ? 2 : 1;
+    static_assert(CHUNKS % 64 == 0, "value tiles of whole lane rounds");
     __shared__ __align__(16) uint8_t vtile[TK * ROW];
 
     const int lane = static_cast<int>(threadIdx.x);
@@ -172,7 +215,7 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
     const float inv_cap = p.softcap > 0.0f ? 1.0f / p.softcap : 0.0f;
     const uint8_t* kbase = static_cast<const uint8_t*>(p.k) + (b * p.sk_b + kvh * p.sk_h) * ES;
     const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.sv_b + kvh * p.sv_h) * ES;
-    const uint8_t* mrow = p.mask ? p.mask + b * p.sm_b + h * p.sm_h + qi * p.sm_q : nullptr;
+    const uint8_t* mrow = MASKED ? p.mask + b * p.sm_b + h * p.sm_h + qi * p.sm_q : nullptr;
     // the key axis: dense slots, or (gathered) the row's compact entries followed by its dense slots from start on,
     // or (cells) the row's seq_lens[b] tokens in its pages
     int count = 0, start = 0, row_keys = p.cells ? min(max(p.seq_lens[b], 0), p.keys) : p.keys;
@@ -187,21 +230,42 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
         gvbase = static_cast<const uint8_t*>(p.gv) + (b * p.sgv_b + kvh * p.sgv_h) * ES;
         gidx = p.g_index + b * p.sgi_b + kvh * p.sgi_h;
     }
-    // cells: the cache pages of the current tile's two 16-key halves, looked up once per tile (tile_pages)
-    int64_t cell_half[2] = {0, 0};
-    auto page_base = [&](int t) __attribute__((always_inline)) -> int64_t {
-        const int lp = min(t / p.page_size, p.bt_cols - 1);
-        const int page = min(max(p.block_table[static_cast<int64_t>(b) * p.bt_stride + lp], 0), p.num_pages - 1);
-        return page * p.sc_page + kvh * p.sc_head;
+    // This wave's tiles interleave with its block's other splits: tile k starts at key (split + k splits) 32, so that
+    // the block's waves (one XCD) read adjacent 8 KB runs of the K and V buffers together.
+    const int tiles_row = (row_keys + TK - 1) / TK;
+    const int my_tiles = split < tiles_row ? (tiles_row - 1 - split) / p.splits + 1 : 0;
+    auto tile_start = [&](int k) __attribute__((always_inline)) { return (split + k * p.splits) * TK; };
+    // cells: a window over this wave's next 64 tile halves (16 keys each), lane l holding the cache byte offset of
+    // the page of half win0 + l; a tile reads its halves' offsets from the window (v_readlane) and reloads the window
+    // every 32 tiles, so that the tile loads need no block-table load of their own
+    int win0 = -(1 << 30);
+    int64_t win_page = 0;
+    auto half_offset = [&](int half) __attribute__((always_inline)) -> int64_t {  // half: uniform
+        if (half < win0 || half >= win0 + 64) {
+            win0 = half;
+            const int mine = half + lane;
+            const int lp = min((tile_start(mine >> 1) + (mine & 1) * 16) / p.page_size, p.bt_cols - 1);
+            const int page = min(max(p.block_table[static_cast<int64_t>(b) * p.bt_stride + lp], 0), p.num_pages - 1);
+            win_page = page * p.sc_page + kvh * p.sc_head;
+            // wait here for the table load (vmcnt(0)), so that the common path, which reloads nothing, does not
+            // wait at the branch's join for every load in flight
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+        }
+        const int at = half - win0;
+        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(win_page), at);
+        const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(win_page) >> 32), at);
+        return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
     };
-    auto tile_pages = [&](int t0) __attribute__((always_inline)) {
+    // the cache offsets of tile k's two 16-key halves (a tile starts at a multiple of 32 keys and pages hold a
+    // multiple of 16, so each half lies in one page)
+    int64_t cell_half[2] = {0, 0};
+    auto tile_pages = [&](int k) __attribute__((always_inline)) {
         if (p.cells) {
-            cell_half[0] = page_base(t0);
-            cell_half[1] = p.page_size % 32 == 0 ? cell_half[0] : page_base(t0 + 16);
+            cell_half[0] = half_offset(2 * k);
+            cell_half[1] = p.page_size % 32 == 0 ? cell_half[0] : half_offset(2 * k + 1);
         }
     };
     auto cell_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
-        // a tile starts at a multiple of 32 keys and pages hold a multiple of 16, so each 16-key half lies in one page
         return p.cells + cell_half[(t >> 4) & 1] + static_cast<int64_t>(t % p.page_size) * p.sc_token;
     };
     auto key_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
@@ -225,61 +289,77 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
 #pragma unroll
     for (int nd = 0; nd < ND; ++nd) acc[nd] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int t_begin = split * p.split_len;
-    const int t_end = min(row_keys, t_begin + p.split_len);
-    constexpr int CHUNKS = TK * DP * ES / 16;  // 16-byte chunks of a staged value tile
-    constexpr int CPR = DP * ES / 16;          // chunks per value row
-    constexpr int CPL = (CHUNKS + 63) / 64;    // chunks per lane
-    constexpr bool kStage = CPL <= 8;          // the tile's values pass through registers (loads issued first)
-    constexpr int KW = ES == 4 ? 2 : 1;        // 16-byte words of 8 key elements (fp8: the low half of one)
-    for (int t0 = t_begin; t0 < t_end; t0 += TK) {
-        tile_pages(t0);
-        // ---- issue the tile's loads: values (staged for LDS), then keys (A-row n of block v is key
-        // t0 + 8 (n / 4) + 4 v + n % 4; a key past the split reads the split's last key and is masked) ----
-        auto value_chunk = [&](int chunk) __attribute__((always_inline)) -> uint4 {
-            const int t = chunk / CPR;
-            const int c = (chunk % CPR) * (16 / ES);  // first channel of the chunk
-            if (chunk < CHUNKS && t0 + t < t_end && c < p.value_dim)
-                return *reinterpret_cast<const uint4*>(value_row(t0 + t) + c * ES);
-            return make_uint4(0, 0, 0, 0);
-        };
-        uint4 vreg[kStage ? CPL : 1];
+    const int t_end = row_keys;
+
+    // A tile's loads in registers: its values (staged for LDS, one set), its keys (A-row n of S block v is key
+    // t0 + 8 (n / 4) + 4 v + n % 4) and, with a mask, the mask bytes of the lane's keys t0 + 8 g + e.
+    uint4 vreg[kStage ? CPL : 1];
+    struct Keys {
+        uint4 k[2][KS][KW];
+        uint32_t m[MASKED ? 8 : 1];
+    };
+    // Every load is issued unconditionally at a clamped address (a key past the split reads the split's last key, a
+    // channel past the dims reads channel 0) and what it must not contribute is zeroed where it is used: every path
+    // through the loop then issues the same loads, and the wait before a tile's use leaves the younger tile's loads
+    // in flight.
+    auto issue = [&](Keys& K, int k) __attribute__((always_inline)) {
+        const int t0 = tile_start(k);
+        tile_pages(k);
+        if constexpr (MASKED)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) K.m[e] = mrow[mask_col(min(t0 + 8 * g + e, t_end - 1)) * p.sm_s];
         if constexpr (kStage)
 #pragma unroll
-            for (int i = 0; i < CPL; ++i) vreg[i] = value_chunk(lane + 64 * i);
-        uint4 kr[2][KS][KW];
+            for (int i = 0; i < CPL; ++i) {
+                const int chunk = lane + 64 * i;
+                const int t = min(t0 + chunk / CPR, t_end - 1);
+                const int c = (chunk % CPR) * (16 / ES);
+                vreg[i] = *reinterpret_cast<const uint4*>(value_row(t) + (c < p.value_dim ? c : 0) * ES);
+            }
 #pragma unroll
         for (int v = 0; v < 2; ++v) {
-            const int tk = min(t0 + 8 * (n >> 2) + 4 * v + (n & 3), t_end - 1);
-            const uint8_t* krow = key_row(tk);
+            const uint8_t* krow = key_row(min(t0 + 8 * (n >> 2) + 4 * v + (n & 3), t_end - 1));
 #pragma unroll
             for (int j = 0; j < KS; ++j) {
                 const int c = 32 * j + 8 * g;
-#pragma unroll
-                for (int w = 0; w < KW; ++w) kr[v][j][w] = make_uint4(0, 0, 0, 0);
-                if (c < p.head_dim) load8<FMT>(krow + c * ES, kr[v][j]);
+                load8<FMT>(krow + (c < p.head_dim ? c : 0) * ES, K.k[v][j]);
             }
         }
-        // ---- the values into LDS (zero past the keys and past Dv) ----
+    };
+    // ---- the tile's values into LDS (zero past the keys and past Dv); the previous tile's reads of LDS came first ----
+    auto stage = [&](int t0) __attribute__((always_inline)) {
         if constexpr (kStage) {
 #pragma unroll
             for (int i = 0; i < CPL; ++i) {
                 const int chunk = lane + 64 * i;
-                if (chunk < CHUNKS) *reinterpret_cast<uint4*>(vtile + (chunk / CPR) * ROW + (chunk % CPR) * 16) = vreg[i];
+                const bool ok = t0 + chunk / CPR < t_end && (chunk % CPR) * (16 / ES) < p.value_dim;
+                *reinterpret_cast<uint4*>(vtile + (chunk / CPR) * ROW + (chunk % CPR) * 16) =
+                    ok ? vreg[i] : make_uint4(0, 0, 0, 0);
             }
         } else {
-            for (int chunk = lane; chunk < CHUNKS; chunk += 64)
-                *reinterpret_cast<uint4*>(vtile + (chunk / CPR) * ROW + (chunk % CPR) * 16) = value_chunk(chunk);
+            for (int chunk = lane; chunk < CHUNKS; chunk += 64) {
+                const int t = chunk / CPR;
+                const int c = (chunk % CPR) * (16 / ES);
+                uint4 x = make_uint4(0, 0, 0, 0);
+                if (t0 + t < t_end && c < p.value_dim) x = *reinterpret_cast<const uint4*>(value_row(t0 + t) + c * ES);
+                *reinterpret_cast<uint4*>(vtile + t * ROW + (chunk % CPR) * 16) = x;
+            }
         }
-        // ---- S^T = K Q^T ----
+    };
+    auto compute = [&](const Keys& K, int t0) __attribute__((always_inline)) {
+        // ---- S^T = K Q^T (key channels past the head dim zeroed) ----
         f32x4 s[2];
 #pragma unroll
         for (int v = 0; v < 2; ++v) {
             s[v] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int j = 0; j < KS; ++j) {
+                uint4 w[KW];
+                const bool ok = 32 * j + 8 * g < p.head_dim;
+#pragma unroll
+                for (int x = 0; x < KW; ++x) w[x] = ok ? K.k[v][j][x] : make_uint4(0, 0, 0, 0);
                 bf16x8 kh, kl;
-                cvt8<FMT>(kr[v][j], kh, kl);
+                cvt8<FMT>(w, kh, kl);
                 s[v] = mfma(kh, qh[j], s[v]);
                 if constexpr (QLO) s[v] = mfma(kh, ql[j], s[v]);
                 if constexpr (KLO) s[v] = mfma(kl, qh[j], s[v]);
@@ -291,7 +371,7 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
         for (int e = 0; e < 8; ++e) {
             const int t = t0 + 8 * g + e;
             bool ok = r_ok && t < t_end && t < causal_limit;
-            if (ok && mrow) ok = mrow[mask_col(t) * p.sm_s] != 0;
+            if constexpr (MASKED) ok = ok && (K.m[e] & 0xFFu) != 0;
             vis |= ok ? 1u << e : 0u;
         }
         float tile_max = -INFINITY;
@@ -343,89 +423,143 @@ __global__ __launch_bounds__(64) void dense_split_kernel(DenseParams p) {
             acc[nd] = mfma(vh, pl, acc[nd]);
             if constexpr (KLO) acc[nd] = mfma(vl, ph, acc[nd]);
         }
+    };
+
+    if (my_tiles > 0) {
+        if constexpr (NBUF == 1) {
+            for (int k = 0; k < my_tiles; ++k) {
+                Keys K;
+                issue(K, k);
+                stage(tile_start(k));
+                compute(K, tile_start(k));
+            }
+        } else {
+            // past the wave's last tile every step issues that tile again (read from L2 and never computed)
+            Keys K0, K1;
+            int ki = 0, k = 0;
+            issue(K0, ki);
+            while (true) {
+                stage(tile_start(k));
+                ki = min(ki + 1, my_tiles - 1);
+                issue(K1, ki);
+                compute(K0, tile_start(k));
+                if (++k >= my_tiles) break;
+                stage(tile_start(k));
+                ki = min(ki + 1, my_tiles - 1);
+                issue(K0, ki);
+                compute(K1, tile_start(k));
+                if (++k >= my_tiles) break;
+            }
+        }
     }
-    // ---- the split's partial: row n's max and sum (lane group 0) and its channels 16 nd + 4 g + i ----
     l_i = group_sum(l_i);
-    if (!r_ok) return;
-    float* slot = p.part + ((static_cast<int64_t>(prog) * p.splits + split) * 16 + n) * (DP + 2);
-    if (g == 0) {
-        slot[0] = m_i;
-        slot[1] = l_i;
-    }
-#pragma unroll
-    for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) slot[2 + 16 * nd + 4 * g + i] = acc[nd][i] * vs;
-}
+    const float sink = p.sinks && r_ok ? p.sinks[h] * kLog2e : -INFINITY;
+    auto out_at = [&](int row_qi, int row_h, int d) __attribute__((always_inline)) -> int64_t {
+        return b * p.so_b + static_cast<int64_t>(q_start + row_qi) * p.so_q + row_h * p.so_h + d;
+    };
 
-template <int QF>
-__device__ __forceinline__ void store_out(const DenseParams& p, int64_t offset, float x) {
-    if constexpr (QF == BF16)
-        static_cast<uint16_t*>(p.out)[offset] = f32_to_bf16(x);
-    else if constexpr (QF == FP16)
-        static_cast<_Float16*>(p.out)[offset] = static_cast<_Float16>(x);
-    else
-        static_cast<float*>(p.out)[offset] = x;
-}
+    // ---- one split: the row's output directly; lane (n, g) holds channels 16 nd + 4 g + i of row r ----
+    if (p.splits == 1) {
+        if (!r_ok) return;
+        float inv;
+        const float a = sink_weight(m_i, l_i, sink, inv);
+#pragma unroll
+        for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 16 * nd + 4 * g + i;
+                if (d < p.value_dim) store_out<QF>(p, out_at(qi, h, d), acc[nd][i] * vs * a * inv);
+            }
+        return;
+    }
 
-// One workgroup per (row, KV head, block of 16 query rows): per query row the largest split maximum M (and the sink
-// logit), the sum sum_s l_s 2^(m_s - M), then every channel's sum_s acc_s 2^(m_s - M) over it (decode.py's merge,
-// attention/_decode_kernels.py:183-226); zeros where nothing is visible.
-template <int DP, int QF>
-__global__ __launch_bounds__(256) void dense_merge_kernel(DenseParams p) {
-    __shared__ float s_m[16], s_inv[16];
-    const int prog = blockIdx.x;
-    const int mt = prog % p.m_tiles;
-    const int kvh = (prog / p.m_tiles) % p.kv_heads;
-    const int b = prog / (p.m_tiles * p.kv_heads);
-    const float* base = p.part + static_cast<int64_t>(prog) * p.splits * 16 * (DP + 2);
-    const int t = static_cast<int>(threadIdx.x);
-    if (t < 16) {
-        const int r = mt * 16 + t;
-        float big = -INFINITY;
-        for (int s = 0; s < p.splits; ++s) big = fmaxf(big, base[(s * 16 + t) * (DP + 2)]);
-        float sink = -INFINITY;
-        if (p.sinks && r < p.rows) sink = p.sinks[kvh * p.groups + r / p.queries] * kLog2e;
-        const float m = fmaxf(big, sink);
-        float l = 0.0f;
-        if (m != -INFINITY) {
-            for (int s = 0; s < p.splits; ++s) {
-                const float ms = base[(s * 16 + t) * (DP + 2)];
-                if (ms != -INFINITY) l += base[(s * 16 + t) * (DP + 2) + 1] * __builtin_amdgcn_exp2f(ms - m);
-            }
-            if (sink != -INFINITY) l += __builtin_amdgcn_exp2f(sink - m);
+    // ---- the split's partial: row n's max and sum (lane group 0) and its channels 16 nd + 4 g + i ----
+    const int64_t slot_stride = DP + 2;
+    const int64_t prog_part = static_cast<int64_t>(prog) * p.splits * 16;
+    if (r_ok) {
+        float* slot = p.part + (prog_part + split * 16 + n) * slot_stride;
+        if (g == 0) {
+            coherent_store(slot, m_i);
+            coherent_store(slot + 1, l_i);
         }
-        s_m[t] = m;
-        s_inv[t] = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+        for (int nd = 0; nd < ND; ++nd)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) coherent_store(slot + 2 + 16 * nd + 4 * g + i, acc[nd][i] * vs);
     }
-    __syncthreads();
-    for (int e = t; e < 16 * p.value_dim; e += blockDim.x) {
-        const int rr = e / p.value_dim, d = e % p.value_dim;
-        const int r = mt * 16 + rr;
-        if (r >= p.rows) break;
-        const float m = s_m[rr];
-        float o = 0.0f;
-        if (m != -INFINITY) {
-            for (int s = 0; s < p.splits; ++s) {
-                const float* slot = base + (s * 16 + rr) * (DP + 2);
-                if (slot[0] != -INFINITY) o += slot[2 + d] * __builtin_amdgcn_exp2f(slot[0] - m);
+    // The hand-off to the last split to finish: the partials are written and read as agent-scope atomics (sc1), so
+    // completion orders them; the compiler may not move the stores past the count (a signal fence), the wave waits
+    // for its stores (vmcnt counts stores on gfx950), then lane 0 counts the split; the wave that finds every other
+    // split counted loads the partials after its atomic returned and leaves the counter zero for the next call.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    int prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(p.counters + prog, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (__shfl(prev, 0) != p.splits - 1) return;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+
+    // ---- the merge by log-sum-exp: lane-owned runs of 8 channels of one query row, the splits folded in batches of 4
+    // with their loads in flight together ----
+    const int rows_here = min(16, p.rows - mt * 16);
+    for (int base = 0; base < rows_here * p.value_dim; base += 64 * 8) {
+        const int e = base + lane * 8;
+        const bool active = e < rows_here * p.value_dim;
+        const int rr = active ? e / p.value_dim : 0;
+        const int d = active ? e % p.value_dim : 0;
+        const int row = mt * 16 + rr;
+        const int row_qi = row % p.queries, row_h = kvh * p.groups + row / p.queries;
+        const bool live = active && row_qi < q_count;
+        float m_run = -INFINITY, l_run = 0.0f, o_run[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o_run[i] = 0.0f;
+        for (int s0 = 0; s0 < p.splits; s0 += 4) {
+            float mk[4], lk[4], ok[4][8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool use = live && s0 + j < p.splits;
+                const float* sk = p.part + (prog_part + (use ? s0 + j : 0) * 16 + rr) * slot_stride;
+                mk[j] = use ? coherent_load(sk) : -INFINITY;
+                lk[j] = use ? coherent_load(sk + 1) : 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) ok[j][i] = use ? coherent_load(sk + 2 + d + i) : 0.0f;
             }
+            float m_new = m_run;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) m_new = fmaxf(m_new, mk[j]);
+            if (m_new == -INFINITY) continue;
+            const float a = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= a;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o_run[i] *= a;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (mk[j] == -INFINITY) continue;
+                const float cw = __builtin_amdgcn_exp2f(mk[j] - m_new);
+                l_run += lk[j] * cw;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) o_run[i] += ok[j][i] * cw;
+            }
+            m_run = m_new;
         }
-        const int gq = r / p.queries, qi = r % p.queries;
-        const int q_start = p.query_start_loc ? p.query_start_loc[b] : 0;
-        if (p.query_start_loc && qi >= p.query_start_loc[b + 1] - q_start) continue;  // an inactive query row
-        store_out<QF>(p, b * p.so_b + static_cast<int64_t>(q_start + qi) * p.so_q + (kvh * p.groups + gq) * p.so_h + d,
-                      o * s_inv[rr]);
+        if (live) {
+            const float row_sink = p.sinks ? p.sinks[row_h] * kLog2e : -INFINITY;
+            float inv;
+            const float a = sink_weight(m_run, l_run, row_sink, inv);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) store_out<QF>(p, out_at(row_qi, row_h, d + i), o_run[i] * a * inv);
+        }
     }
+    if (lane == 0) __hip_atomic_store(p.counters + prog, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int DP, int FMT, int QF>
 int launch_dense(const DenseParams& p, hipStream_t stream) {
     const int programs = p.batch * p.kv_heads * p.m_tiles;
-    hipLaunchKernelGGL((dense_split_kernel<DP, FMT, QF>), dim3(programs, p.splits), dim3(64), 0, stream, p);
-    if (const int rc = check_launch("dense_split_kernel")) return rc;
-    hipLaunchKernelGGL((dense_merge_kernel<DP, QF>), dim3(programs), dim3(256), 0, stream, p);
-    return check_launch("dense_merge_kernel");
+    if (p.mask)
+        hipLaunchKernelGGL((dense_split_kernel<DP, FMT, QF, true>), dim3(programs, p.splits), dim3(64), 0, stream, p);
+    else
+        hipLaunchKernelGGL((dense_split_kernel<DP, FMT, QF, false>), dim3(programs, p.splits), dim3(64), 0, stream, p);
+    return check_launch("dense_split_kernel");
 }
 
 template <int DP, int QF>

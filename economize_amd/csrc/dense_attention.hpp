@@ -22,9 +22,10 @@ struct DenseParams {
     const float* sinks;  // [Hq] or null
     void* out;           // [B, Q, Hq, Dv], element strides so_*, format q_format
     int64_t so_b, so_q, so_h;
-    float* part;  // [programs][splits][16 rows][2 + padded Dv]: max, sum, accumulators
+    int32_t* counters;  // [programs]: splits finished (zero when a call starts; the last split leaves it zero)
+    float* part;        // [programs][splits][16 rows][2 + padded Dv]: max, sum, accumulators
     int batch, queries, q_heads, kv_heads, groups, rows, keys, head_dim, value_dim;
-    int m_tiles, splits, split_len;
+    int m_tiles, splits;  // blocks of 16 query rows; split s takes the 32-key tiles s, s + splits, ...
     float scale, softcap;
     // Gathered mode (gk non-null; the reference's gathered_decode_attention, attention/gathered.py:96-179): `keys` is
     // the virtual key axis. Virtual key t of (b, kvh) is compact entry t of gk / gv [B, Hkv, capacity, D] below

@@ -13,16 +13,6 @@
 namespace eco {
 namespace {
 
-// Device-coherent (agent-scope) store and load of partials (gfx950 lowers them to global_store / global_load with
-// sc1). The hand-off between workgroups is ordered by the fences of hand_off and merge_row.
-__device__ inline void coherent_store(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ inline float coherent_load(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 __device__ inline int64_t wave_sum(int64_t x) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);

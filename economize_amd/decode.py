@@ -14,6 +14,7 @@ import torch
 
 from . import _lib
 from .errors import ConfigError
+from .paged import cached_workspace
 
 __all__ = ["FP8_DTYPES", "decode_attention", "mask_operand", "sinks_operand"]
 
@@ -21,19 +22,17 @@ __all__ = ["FP8_DTYPES", "decode_attention", "mask_operand", "sinks_operand"]
 DOT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
 FP8_DTYPES = (torch.float8_e4m3fn, torch.float8_e5m2)
 
-_workspaces: dict[tuple[torch.device, int], torch.Tensor] = {}
+def dense_counter_bytes(batch: int, queries: int, q_heads: int, kv_heads: int) -> int:
+    """Bytes of the counters at the start of a dense decode workspace: int32 per batch row, KV head and block of 16
+    query rows, padded to 256 bytes. They must be zero when a call starts; a call leaves them zero."""
+    blocks = batch * kv_heads * -(-(q_heads // kv_heads) * queries // 16)
+    return (4 * blocks + 255) // 256 * 256
 
 
-def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
-    """A scratch buffer of at least ``nbytes`` for ``device``'s current stream (the kernels leave nothing in it that
-    a later call reads)."""
-    key = (device, torch.cuda.current_stream(device).cuda_stream)
-    buf = _workspaces.get(key)
-    if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 2 * (buf.numel() if buf is not None else 0), 256), dtype=torch.uint8,
-                          device=device)
-        _workspaces[key] = buf
-    return buf
+def _workspace(nbytes: int, device: torch.device, batch: int, queries: int, q_heads: int,
+               kv_heads: int) -> torch.Tensor:
+    """The workspace of ``device``'s current stream for a dense decode call of this shape, its counters zero."""
+    return cached_workspace(nbytes, dense_counter_bytes(batch, queries, q_heads, kv_heads), device)
 
 
 def mask_operand(mask: torch.Tensor | None, keys: int) -> tuple[torch.Tensor | None, tuple[int, int, int, int]]:
@@ -129,7 +128,7 @@ def decode_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor
     need = int(_lib.lib().eco_decode_workspace_size(batch, queries, q_heads, kv_heads, keys, head_dim, head_dv))
     if need == 0:
         raise ConfigError(f"decode_attention supports head dims up to 256, got {head_dim} / {head_dv}")
-    ws = _workspace(need, device)
+    ws = _workspace(need, device, batch, queries, q_heads, kv_heads)
     ks = None if k_scale is None else k_scale.float().contiguous()
     vs = None if v_scale is None else v_scale.float().contiguous()
     _lib.call(

@@ -117,7 +117,7 @@ def gathered_decode_attention(query: torch.Tensor, key: torch.Tensor, value: tor
     need = int(_lib.lib().eco_decode_workspace_size(batch, queries, q_heads, kv_heads, virtual, head_dim, head_dv))
     if need == 0:
         raise ConfigError(f"gathered_decode_attention supports head dims up to 256, got {head_dim} / {head_dv}")
-    ws = _workspace(need, device)
+    ws = _workspace(need, device, batch, queries, q_heads, kv_heads)
     idx = gathered.index
     _lib.call(
         "eco_gathered_decode", query.data_ptr(), _lib.fmt(query.dtype), query.stride(0), query.stride(1),

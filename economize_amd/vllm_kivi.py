@@ -193,7 +193,7 @@ def paged_kivi_attention(query: torch.Tensor, kv_cache: torch.Tensor, layout: Ce
         raise ConfigError("paged_kivi_attention: unsupported shape")
     from .decode import _workspace
 
-    ws = _workspace(need, device)
+    ws = _workspace(need, device, requests, int(max_query_len), q_heads, u8.shape[1])
     scale = 1.0 / math.sqrt(dim) if scale is None else scale
     _lib.call("eco_kivi_cells_attention", query.data_ptr(), query.stride(0), query.stride(1), u8.data_ptr(),
               _lib.fmt(typed.dtype), u8.stride(0), u8.stride(1), u8.stride(2), u8.shape[0], u8.shape[2], u8.shape[1],

@@ -123,7 +123,8 @@ int eco_paged_decode_static(const void* q, int64_t sq_b, int64_t sq_q, int64_t s
  * compact entry t of ck / cv [B, Hkv, capacity, D / Dv] (strides sck_*, scv_*; mask column index[b, h, t], strides
  * si_b, si_h) below count[b * Hkv + h], else dense slot start[b] + t - count of k / v [B, Hkv, keys, D / Dv]; the
  * virtual axis is keys - dropped long (dropped = min(start[b] - count[b, h]) on the host). Everything else as
- * eco_decode, with K/V in the query's format; the workspace is eco_decode_workspace_size(..., keys - dropped, ...).
+ * eco_decode, with K/V in the query's format; the workspace is eco_decode_workspace_size(..., keys - dropped, ...)
+ * bytes under eco_decode's counter rule.
  * Counts beyond the capacity and starts beyond the slots are clamped (wrong results, no access outside a buffer). */
 int eco_gathered_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int64_t sq_q, const void* k,
                         const void* v, int64_t sk_b, int64_t sk_h, int64_t sk_s, int64_t sv_b, int64_t sv_h,
@@ -163,7 +164,10 @@ int eco_kivi_gather(const void* blocks, int32_t num_pages, const void* k_ring, c
                     int64_t so_kh, int64_t so_ks, int64_t so_vb, int64_t so_vh, int64_t so_vs, int32_t batch,
                     int32_t kv_heads, int32_t keys, int32_t head_dim, int32_t bits, int32_t group, void* stream);
 
-/* Workspace bytes eco_decode needs for this shape (0 for an unsupported one). */
+/* Workspace bytes eco_decode needs for this shape (0 for an unsupported one). The workspace starts with a counter per
+ * block of 16 query rows, int32 per batch row, KV head and block of 16 of the (q_heads / kv_heads) * queries rows,
+ * padded to 256 bytes, which must be zero when a call starts; every call leaves them zero and may write anything after
+ * them (the counter rule of eco_paged_decode's workspace). One workspace serves one stream at a time. */
 size_t eco_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys,
                                  int32_t head_dim, int32_t value_dim);
 
@@ -176,7 +180,7 @@ size_t eco_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads
  * q . k * scale, with an optional soft cap (softcap > 0) and sinks [Hq] in the denominator; a query that sees no key
  * gives 0. Channel strides are 1; head_dim and value_dim are multiples of 8 (of 16 for fp8), at most 256; pointers
  * and K/V/query strides are 16-byte aligned. Replaces decode_attention (attention/decode.py:252-324; kernels
- * attention/_decode_kernels.py:78-226): split-K over the keys, then a merge of the splits. */
+ * attention/_decode_kernels.py:78-226): split-K over the keys, the splits merged by the last of their waves. */
 int eco_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int64_t sq_q, const void* k,
                const void* v, int32_t kv_format, int64_t sk_b, int64_t sk_h, int64_t sk_s, int64_t sv_b, int64_t sv_h,
                int64_t sv_s, const float* k_scale, const float* v_scale, const uint8_t* mask, int64_t sm_b,
@@ -285,7 +289,8 @@ int eco_kivi_cells_quantize(void* cache, int32_t format, int64_t sb, int64_t sh,
  * request's seq_lens[b] keys (query i of a request of n queries sees keys < seq_len - n + i + 1), read from the
  * cells' dense entries, which hold every quantized key and value as its dequantized value; out [tokens, q_heads, D]
  * (strides so_t, so_h); keys = the longest seq_len; optional sinks [q_heads] and soft cap. Workspace:
- * eco_kivi_cells_attention_workspace_size. */
+ * eco_kivi_cells_attention_workspace_size bytes, with eco_decode's counter rule (batch = requests, queries =
+ * max_query_len). */
 size_t eco_kivi_cells_attention_workspace_size(int32_t requests, int32_t max_query_len, int32_t q_heads,
                                                int32_t kv_heads, int32_t keys, int32_t head_dim);
 int eco_kivi_cells_attention(const void* q, int64_t sq_t, int64_t sq_h, const void* cache, int32_t format, int64_t sb,
