@@ -75,8 +75,8 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
                                   _I, _I, _I, _I, _I, _I, _F, _F] + _MASK + [_P, _S, _P]),
     "eco_quest_refresh_bounds": (c_int32, [_P, _I, _I, _P, _L, _I, _P, _P, _P, _I, _P, _P, _L, _L, _L, _I, _I, _I, _I,
                                            _I, _P]),
-    "eco_quest_select": (c_int32, [_P, _L, _L, _L, _P, _P, _L, _L, _L, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _S,
-                                   _P]),
+    "eco_quest_select": (c_int32, [_P, _L, _L, _L, _P, _P, _L, _L, _L, _P, _I, _I, _I, _P, _I, _I, _I, _I, _I, _P,
+                                   _S, _P]),
 }
 
 _lib: ctypes.CDLL | None = None

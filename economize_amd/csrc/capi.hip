@@ -1165,8 +1165,8 @@ size_t eco_quest_select_workspace_size(int32_t batch, int32_t kv_heads, int32_t 
 
 int eco_quest_select(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* kmin, const void* kmax,
                      int64_t sb_b, int64_t sb_h, int64_t sb_p, const int32_t* done, int32_t max_done, int32_t pages,
-                     int32_t* out, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
-                     int32_t head_dim, void* workspace, size_t workspace_bytes, void* stream) {
+                     int32_t first_page, int32_t* out, int32_t batch, int32_t queries, int32_t q_heads,
+                     int32_t kv_heads, int32_t head_dim, void* workspace, size_t workspace_bytes, void* stream) {
     if (!q || !done || !out) return fail("quest select: null query, done or output");
     if (batch <= 0 || queries <= 0 || q_heads <= 0 || kv_heads <= 0 || pages < 0 || max_done < 0)
         return fail("quest select: batch, queries and heads must be positive, pages and max_done non-negative");
@@ -1194,6 +1194,7 @@ int eco_quest_select(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
     p.done = done;
     p.max_done = max_done;
     p.pages = pages;
+    p.first_page = first_page != 0;
     p.out = out;
     p.scores = static_cast<float*>(workspace);
     p.batch = batch;

@@ -226,7 +226,8 @@ __global__ __launch_bounds__(256) void quest_score_kernel(SelectParams p) {
                 s2 += __shfl_xor(s2, off);
             }
         }
-        if (page < p1 && j == 0) out[page] = page < done ? s1 + s2 : -INFINITY;
+        if (page < p1 && j == 0)
+            out[page] = page < done ? (page == 0 && p.first_page ? INFINITY : s1 + s2) : -INFINITY;
     }
 }
 

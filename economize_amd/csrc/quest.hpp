@@ -34,6 +34,7 @@ struct SelectParams {
     int64_t sb_b, sb_h, sb_p;
     const int32_t* done;  // [B] committed Quest pages of every row
     int max_done, pages;
+    int first_page;   // nonzero: a row's page 0 is always selected (it scores +inf)
     int32_t* out;     // [B, Hkv, pages]
     float* scores;    // workspace [B, Hkv, max_done]
     int batch, queries, q_heads, kv_heads, groups, head_dim;

@@ -182,7 +182,7 @@ class PagedLayer(_PagedBase):
                     self.valid = done
                 done_t = torch.full((self.table.shape[0],), done, dtype=torch.int32, device=self.table.device)
                 pages = QuestPages(self.bounds[0], self.bounds[1], done_t, done, done, q.page_size, q.pages,
-                                   q.max_queries)
+                                   q.max_queries, q.first_page)
         handle = PagedKV(self.cache, self.table, self._seq_lens(), self.length, pages, self.model_dtype)
         keys, values = self._stand_ins(key_states)
         return attach_packed(keys, handle), values

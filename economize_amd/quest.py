@@ -92,7 +92,7 @@ def page_bounds(cache: PagedKVCache, block_table: torch.Tensor, first: int, last
 
 
 def select_pages(query: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, done: torch.Tensor, max_done: int,
-                 pages: int) -> torch.Tensor:
+                 pages: int, first_page: bool = False) -> torch.Tensor:
     """The committed pages every row and KV head reads.
 
     Args:
@@ -102,6 +102,8 @@ def select_pages(query: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, do
         done: int32 ``[B]`` committed pages of every row.
         max_done: ``max(done)``, on the host.
         pages: Pages to select per row and KV head.
+        first_page: Always select a row's page 0 (the "first and last pages" variant; the reference's selection,
+            the default, has no such rule).
 
     Returns:
         int32 ``[B, Hkv, pages]``: the selected pages in increasing order, then ``-1``. A row with at most ``pages``
@@ -131,7 +133,7 @@ def select_pages(query: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, do
     _lib.call(
         "eco_quest_select", query.data_ptr(), query.stride(0), query.stride(2), query.stride(1), kmin.data_ptr(),
         kmax.data_ptr(), kmin.stride(0), kmin.stride(1), kmin.stride(2), done.data_ptr(), max_done, pages,
-        out.data_ptr(), batch, queries, q_heads, kv_heads, head_dim, scores.data_ptr(), scores.numel() * 4,
+        int(bool(first_page)), out.data_ptr(), batch, queries, q_heads, kv_heads, head_dim, scores.data_ptr(), scores.numel() * 4,
         _lib.stream_of(device),
     )
     return out
@@ -150,6 +152,7 @@ class QuestPages:
         page: Tokens per Quest page (a power of two, at least 16).
         pages: Committed pages every row and KV head reads.
         max_queries: Longest query that is restricted to the pages; longer ones see every key.
+        first_page: Always select a row's page 0 (off in the reference).
     """
 
     kmin: torch.Tensor
@@ -160,11 +163,12 @@ class QuestPages:
     page: int
     pages: int
     max_queries: int = 1
+    first_page: bool = False
     format: str = "quest"
 
     def select(self, query: torch.Tensor) -> torch.Tensor:
         """int32 ``[B, Hkv, pages]`` selected pages for ``query`` ``[B, Hq, Q, D]`` (see :func:`select_pages`)."""
-        return select_pages(query, self.kmin, self.kmax, self.done, self.max_done, self.pages)
+        return select_pages(query, self.kmin, self.kmax, self.done, self.max_done, self.pages, self.first_page)
 
     def attend(self, query: torch.Tensor, cache: PagedKVCache, block_table: torch.Tensor, seq_lens: torch.Tensor,
                max_seq_len: int, scale: float | None = None, softcap: float | None = None,
@@ -228,7 +232,7 @@ class QuestState:
     """
 
     def __init__(self, batch: int, kv_heads: int, head_dim: int, max_pages: int, page: int, pages: int,
-                 device: torch.device | str, max_queries: int = 1) -> None:
+                 device: torch.device | str, max_queries: int = 1, first_page: bool = False) -> None:
         _check_page(page)
         if max_pages <= 0 or pages <= 0:
             raise ConfigError(f"quest state needs positive max_pages and pages, got {max_pages}, {pages}")
@@ -238,6 +242,7 @@ class QuestState:
         self.valid = torch.zeros(batch * kv_heads, dtype=torch.int32, device=device)
         self.done = torch.zeros(batch, dtype=torch.int32, device=device)
         self.page, self.pages, self.max_pages, self.max_queries = page, pages, max_pages, max_queries
+        self.first_page = first_page
 
     def reset(self) -> None:
         """Forget every page (a new generation in the same buffers)."""
@@ -268,4 +273,4 @@ class QuestState:
     def pages_handle(self) -> QuestPages:
         """The layer's :class:`QuestPages` with the device ``done`` and ``max_done = max_pages``."""
         return QuestPages(self.kmin, self.kmax, self.done, 0, self.max_pages, self.page, self.pages,
-                          self.max_queries)
+                          self.max_queries, self.first_page)

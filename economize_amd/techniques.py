@@ -313,6 +313,8 @@ class QuestConfig(TechniqueConfig):
         max_queries: Longest query restricted to the pages.
         layers: 1-indexed layers Quest acts on (empty: every layer).
         include_sliding: Also restrict sliding-window layers.
+        first_page: Always select every row's first page (the "first and last pages" variant of Quest). The
+            reference has no such rule (quest/technique.py:84-86 selects by score only), so it is off by default.
     """
 
     technique: ClassVar[str] = "quest"
@@ -322,6 +324,7 @@ class QuestConfig(TechniqueConfig):
     max_queries: int = 1
     layers: tuple[int, ...] = ()
     include_sliding: bool = False
+    first_page: bool = False
 
     def __post_init__(self) -> None:
         if self.page_size < 16 or self.page_size & (self.page_size - 1):

@@ -219,11 +219,13 @@ size_t eco_quest_select_workspace_size(int32_t batch, int32_t kv_heads, int32_t 
  * sum_d qsum_d (lo + hi) / 2 + qabs_d (hi - lo) / 2 among its committed pages [0, done[b]) (pages >= max_done never),
  * min(pages, max_done) of them in increasing order, then -1; ties go to the lower page. qsum / qabs are the sums of
  * q / |q| (q [B, Q, Hq, D] bf16, element strides sq_*, channel stride 1) over the KV head's query rows; lo / hi are
- * the page bounds (bf16, 16-byte aligned, strides multiples of 8). Replaces select_pages (attention/quest.py:73-108). */
+ * the page bounds (bf16, 16-byte aligned, strides multiples of 8). Replaces select_pages (attention/quest.py:73-108).
+ * first_page nonzero always selects a row's page 0 (it scores +inf), the "first and last pages" variant of Quest;
+ * the reference has no such rule, so 0 gives its selection. */
 int eco_quest_select(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* kmin, const void* kmax,
                      int64_t sb_b, int64_t sb_h, int64_t sb_p, const int32_t* done, int32_t max_done, int32_t pages,
-                     int32_t* out, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
-                     int32_t head_dim, void* workspace, size_t workspace_bytes, void* stream);
+                     int32_t first_page, int32_t* out, int32_t batch, int32_t queries, int32_t q_heads,
+                     int32_t kv_heads, int32_t head_dim, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- KIVI (2- and 4-bit KV codes) --------------------------------------------------------------------------
  * Paged KIVI cache, per layer: blocks [num_pages, Hkv, eco_kivi_block_bytes] (one block per 32-token page and KV

@@ -93,9 +93,10 @@ def page_scores(query: np.ndarray, kmin: np.ndarray, kmax: np.ndarray, max_done:
 
 
 def select_pages(query: np.ndarray, kmin: np.ndarray, kmax: np.ndarray, done: np.ndarray, max_done: int,
-                 pages: int) -> np.ndarray:
+                 pages: int, first_page: bool = False) -> np.ndarray:
     """``int32`` ``[B, Hkv, pages]``: the selected pages of every row and KV head in increasing order, then ``-1``
-    (quest.py:73-108, ties to the lower index)."""
+    (quest.py:73-108, ties to the lower index). ``first_page`` gives page 0 of a row the score +inf (a build option,
+    not the reference's rule)."""
     batch, kv_heads = kmin.shape[:2]
     out = np.full((batch, kv_heads, max(pages, 0)), -1, dtype=np.int32)
     if max_done <= 0 or pages <= 0:
@@ -107,6 +108,8 @@ def select_pages(query: np.ndarray, kmin: np.ndarray, kmax: np.ndarray, done: np
         for h in range(kv_heads):
             s = score[b, h].astype(np.float64)
             s[done[b]:] = -np.inf
+            if first_page and done[b] > 0:
+                s[0] = np.inf
             order = np.argsort(-s, kind="stable")[:count]
             chosen = np.sort(order[order < done[b]])
             out[b, h, : chosen.size] = chosen

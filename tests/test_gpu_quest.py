@@ -232,3 +232,26 @@ def test_quest_attention_with_a_mask() -> None:
     visible = (np.arange(kd.shape[2])[None, :] < np.array(lens)[:, None])[:, None, None, :] & mask
     want = oquest.quest_reference(q, kd, vd, visible, 1 / np.sqrt(128), index, done, page)
     np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("shape", [(2, 8, 2, 1, 128, 64, 8), (1, 4, 1, 1, 64, 3000, 63)])
+def test_forced_first_page_matches_the_oracle(shape) -> None:
+    """``first_page`` selects page 0 of every row with a committed page, also where it scores lowest."""
+    from economize_amd.quest import select_pages
+
+    batch, hq, hkv, nq, d, npages, pages = shape
+    rng = np.random.default_rng(7 + npages)
+    lo, hi = _random_bounds(rng, batch, hkv, npages, d)
+    q = bf16_bits_to_f32(f32_to_bf16_bits(rng.standard_normal((batch, hq, nq, d)).astype(np.float32)))
+    qsum = q[0, :, 0].reshape(hkv, hq // hkv, d).sum(1)
+    lo[0, :, 0] = hi[0, :, 0] = bf16_bits_to_f32(f32_to_bf16_bits(-8.0 * np.sign(qsum).astype(np.float32)))
+    done = np.full(batch, npages, np.int32)
+    if batch > 1:
+        done[1] = 0  # nothing committed: nothing selected
+    got = select_pages(_to_bf16(q), _to_bf16(lo), _to_bf16(hi), torch.from_numpy(done).cuda(), npages, pages,
+                       first_page=True)
+    want = oquest.select_pages(q, lo, hi, done, npages, pages, first_page=True)
+    assert np.array_equal(got.cpu().numpy(), want)
+    assert (want[0, :, 0] == 0).all()
+    plain = oquest.select_pages(q, lo, hi, done, npages, pages)
+    assert not (plain[0, :, 0] == 0).any()  # the planted page 0 is selected only when forced

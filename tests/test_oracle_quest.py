@@ -99,3 +99,24 @@ def test_keep_and_restricted_attention() -> None:
     got = quest.quest_reference(q, k, v, None, 0.25, index, np.array([4]), 16)
     mask = np.repeat(keep, 2, axis=1)[:, :, None, :]
     assert np.array_equal(got, reference_attention(q, k, v, mask, 0.25))
+
+
+def test_forced_first_page_is_page_zero_plus_the_rest_by_score() -> None:
+    """With ``first_page`` the selection is page 0 plus the selection of ``pages - 1`` among pages 1.. (the same
+    rule over the bounds without page 0, shifted back), including a row whose page 0 scores lowest."""
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((2, 8, 1, 32)).astype(np.float32)
+    k = rng.standard_normal((2, 2, 30 * 16, 32)).astype(np.float32)
+    lo, hi = quest.page_bounds(k, 0, 30, 16)
+    qsum = q[0, :, 0].reshape(2, 4, 32).sum(1)  # per KV head, over its query heads
+    lo[0, :, 0] = hi[0, :, 0] = -100.0 * np.sign(qsum)  # row 0: page 0 scores far below every other page
+    done, pages = np.array([30, 12]), 6
+    got = quest.select_pages(q, lo, hi, done, 30, pages, first_page=True)
+    rest = quest.select_pages(q, lo[:, :, 1:], hi[:, :, 1:], done - 1, 29, pages - 1)
+    for b in range(2):
+        for h in range(2):
+            want = [0] + [p + 1 for p in rest[b, h] if p >= 0]
+            assert got[b, h].tolist() == want
+    assert 0 not in quest.select_pages(q, lo, hi, done, 30, pages)[0, 0].tolist()
+    # a row with no committed page selects nothing, forced or not
+    assert (quest.select_pages(q, lo, hi, np.array([0, 0]), 30, pages, first_page=True) == -1).all()
