@@ -198,33 +198,6 @@ __global__ __launch_bounds__(256) void kivi_quant_values_kernel(KiviQuantParams 
 
 // ---- attention ----------------------------------------------------------------------------------------------
 
-// Eight codes of a word as exact fp32 values, in element order: for 4-bit codes the word's 8 elements, for 2-bit
-// codes elements 8 h .. 8 h + 7 of its 16.
-template <int BITS>
-__device__ inline void codes_to_f32(uint32_t word, int h, float (&out)[8]) {
-    uint32_t lo, hi;
-    if constexpr (BITS == 4) {
-        lo = word & 0x0F0F0F0Fu;
-        hi = (word >> 4) & 0x0F0F0F0Fu;
-    } else {
-        lo = (word >> (4 * h)) & 0x03030303u;
-        hi = (word >> (4 * h + 2)) & 0x03030303u;
-    }
-    typedef float f32x2 __attribute__((ext_vector_type(2)));
-    const f32x2 a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, 512.0f, false);
-    const f32x2 b = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, 512.0f, true);
-    const f32x2 c = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 512.0f, false);
-    const f32x2 d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 512.0f, true);
-    out[0] = a.x;
-    out[1] = a.y;
-    out[2] = b.x;
-    out[3] = b.y;
-    out[4] = c.x;
-    out[5] = c.y;
-    out[6] = d.x;
-    out[7] = d.y;
-}
-
 // A lane's share of one 32-token page: key words of its 8-token key rows, the value word of each 16-channel block
 // (lane (n, g): channel 16 nd + n, tokens 8 g .. 8 g + 7, the P.V MFMA's A operand), key scales and zero points of
 // its channels, value scales and zero points of its 8 tokens per value group. SHARED: the four waves of a workgroup
@@ -861,6 +834,16 @@ int kivi_shared_from() {
     return from;
 }
 
+// The two-page-tile kernel of kivi_verify.hip for the shared-tile shapes (default 1; ECO_KIVI_VERIFY=0 keeps the
+// one-page shared-tile instance here).
+bool kivi_verify_enabled() {
+    static const bool on = [] {
+        const char* env = std::getenv("ECO_KIVI_VERIFY");
+        return env ? std::atoi(env) != 0 : true;
+    }();
+    return on;
+}
+
 // An attention instance: the kernel, its threads per workgroup and the parts a workgroup's tile range is split in
 // (the grid gives every part at least four tiles).
 using KiviKernelFn = decltype(&kivi_attention_kernel<64, 2, 1, 1, false>);
@@ -913,6 +896,7 @@ struct KiviLaunch {
     const KiviParams* p;
     template <int D, int BITS, int NB>
     int run() const {
+        if (NB >= kivi_shared_from() && kivi_verify_enabled()) return kivi_verify_attention(*p, stream);
         const KiviInstance in = kivi_kernel_of<D, BITS, NB>();
         hipLaunchKernelGGL(in.kernel, dim3(p->grid), dim3(in.threads), 0, stream, *p);
         return check_launch("kivi_attention_kernel");
@@ -924,6 +908,10 @@ struct KiviOccupancy {
     int* waves;
     template <int D, int BITS, int NB>
     int run() const {
+        if (NB >= kivi_shared_from() && kivi_verify_enabled()) {
+            *waves = 2;  // two-page tiles: four tiles per workgroup are eight pages
+            return kivi_verify_resident_groups(D, BITS, per_cu);
+        }
         int blocks = 0;
         const KiviInstance in = kivi_kernel_of<D, BITS, NB>();
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, in.kernel, in.threads, 0) != hipSuccess ||

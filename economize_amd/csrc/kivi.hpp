@@ -87,5 +87,8 @@ int kivi_ring_write(const KiviRingParams& p, hipStream_t stream);
 int kivi_quantize(const KiviQuantParams& p, int kind, int max_tokens, hipStream_t stream);
 int kivi_resident_groups(int head_dim, int bits, int rows, int* per_cu, int* waves);  // workgroups per CU, waves per workgroup
 int kivi_attention(const KiviParams& p, hipStream_t stream);
+// The attention of more than 32 query rows per KV head over two-page tiles (kivi_verify.hip).
+int kivi_verify_resident_groups(int head_dim, int bits, int* per_cu);
+int kivi_verify_attention(const KiviParams& p, hipStream_t stream);
 
 }  // namespace eco
