@@ -198,26 +198,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             }
         }
         // values: token t from codes below vq on a present page, from the ring in [vq, row_len), else zero (an
-        // unwritten scale may be inf or NaN)
+        // unwritten scale may be inf or NaN); a present page of codes only (the common case) needs no selection
         const int tok0 = t0p + 8 * vo;
-        const uint32_t below_vq = vq - tok0 >= 8 ? 0xFFu : (vq > tok0 ? (1u << (vq - tok0)) - 1u : 0u);
-        const uint32_t from_codes = s.page >= 0 ? below_vq : 0u;
-        const int end = min(row_len - tok0, 8);
-        const uint32_t below_end = end >= 8 ? 0xFFu : (end > 0 ? (1u << end) - 1u : 0u);
-        const uint32_t from_ring = below_end & ~below_vq;
-        uint4 vals[CPT];
         float sf[8], zf[8];
         halves_to_f32(s.vs, sf);
         halves_to_f32(s.vz, zf);
+        uint4 vals[CPT];
+        if (t0p + VPAGE <= vq && s.page >= 0) {
 #pragma unroll
-        for (int k = 0; k < CPT; ++k)
-            vals[k] = select8(from_codes, dequant8<BITS>(s.vw[k], BITS == 4 ? 0 : (vo & 1), sf, zf), make_uint4(0, 0, 0, 0));
-        if (__ballot(from_ring != 0u) != 0) {  // the ring's tokens (the rows' last pages only)
+            for (int k = 0; k < CPT; ++k) vals[k] = dequant8<BITS>(s.vw[k], BITS == 4 ? 0 : (vo & 1), sf, zf);
+        } else {
+            const uint32_t below_vq = vq - tok0 >= 8 ? 0xFFu : (vq > tok0 ? (1u << (vq - tok0)) - 1u : 0u);
+            const uint32_t from_codes = s.page >= 0 ? below_vq : 0u;
+            const int end = min(row_len - tok0, 8);
+            const uint32_t below_end = end >= 8 ? 0xFFu : (end > 0 ? (1u << end) - 1u : 0u);
+            const uint32_t from_ring = below_end & ~below_vq;
 #pragma unroll
-            for (int k = 0; k < CPT; ++k) {
-                const int c = CPT * cq + k;
-                const uint4 x = *reinterpret_cast<const uint4*>(p.v_ring + (row_kv * D + c) * p.ring + tok0 % p.ring);
-                vals[k] = select8(from_ring, x, vals[k]);
+            for (int k = 0; k < CPT; ++k)
+                vals[k] = select8(from_codes, dequant8<BITS>(s.vw[k], BITS == 4 ? 0 : (vo & 1), sf, zf),
+                                  make_uint4(0, 0, 0, 0));
+            if (__ballot(from_ring != 0u) != 0) {  // the ring's tokens (the rows' last pages only)
+#pragma unroll
+                for (int k = 0; k < CPT; ++k) {
+                    const int c = CPT * cq + k;
+                    const uint4 x =
+                        *reinterpret_cast<const uint4*>(p.v_ring + (row_kv * D + c) * p.ring + tok0 % p.ring);
+                    vals[k] = select8(from_ring, x, vals[k]);
+                }
             }
         }
 #pragma unroll
@@ -316,7 +323,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
     };
 
-    // ---- end of a row segment: direct output, or a partial and (last part of the row) the merge ----
     // ---- end of a row segment: a whole row's output directly, else the segment's partial (max, sum, accumulators
     // of every query row) into the workgroup's slot for kivi_verify_merge_kernel ----
     auto finish = [&](const Cursor& c, int64_t seg_begin, int64_t seg_end, bool first_segment) __attribute__((always_inline)) {
@@ -329,16 +335,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                     for (int i = 0; i < 4; ++i) store_output(p, c.b, c.kvh, r, 16 * nd + 4 * g + i, acc[nd][i], m_i, l);
             return;
         }
+        // slot layout: accumulators [rows][D] first (8-byte aligned runs), then the maxima and the sums [rows]
         float* slot = p.part + (2 * static_cast<int64_t>(w) + (first_segment ? 0 : 1)) * p.rows * (D + 2);
         if (r < p.rows) {
             if (g == 0) {
-                slot[r] = m_i;
-                slot[p.rows + r] = l;
+                slot[p.rows * D + r] = m_i;
+                slot[p.rows * D + p.rows + r] = l;
             }
 #pragma unroll
-            for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) slot[2 * p.rows + r * D + 16 * nd + 4 * g + i] = acc[nd][i];
+            for (int nd = 0; nd < ND; ++nd) {
+                float2* run = reinterpret_cast<float2*>(slot + r * D + 16 * nd + 4 * g);
+                run[0] = make_float2(acc[nd][0], acc[nd][1]);
+                run[1] = make_float2(acc[nd][2], acc[nd][3]);
+            }
         }
     };
 
@@ -371,8 +380,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
 }
 
 // The rows cut between workgroups, merged after the attention kernel (a second launch on the same stream, so the
-// partials need no hand-off inside the first): one workgroup per (row, KV head); a row whose tiles lie in one
-// workgroup's range was written directly and is skipped. The parts are the workgroups whose ranges meet the row (slot
+// partials need no hand-off inside the first): one workgroup per (row, KV head) and 2048 of its rows x D outputs
+// (blockIdx.y), so that a workgroup's loads are one round trip; a row whose tiles lie in one workgroup's range was
+// written directly and is skipped. The parts are the workgroups whose ranges meet the row (slot
 // 1 of a workgroup whose range starts before the row, else slot 0), folded by log-sum-exp four at a time, lane-owned
 // runs of 8 channels of one query row, with the sinks in the denominator (attention/_decode_kernels.py:183-226).
 template <int D>
@@ -390,57 +400,62 @@ __global__ __launch_bounds__(256) void kivi_verify_merge_kernel(VerifyParams p) 
         const int bb = b0 + lane;
         total += wave_sum(bb < p.batch ? row_of(p, bb).tiles : 0);
     }
-    total *= p.kv_heads;
+    total = uniform64(total * p.kv_heads);
     const int tiles = row_of<true>(p, b).tiles;
     if (tiles == 0) return;
-    const int64_t row_start = before * p.kv_heads + static_cast<int64_t>(kvh) * tiles;
+    const int64_t row_start = uniform64(before * p.kv_heads + static_cast<int64_t>(kvh) * tiles);
     const int grid = p.grid;
-    const int w_first = wave_of(row_start, total, grid);
-    const int w_last = wave_of(row_start + tiles - 1, total, grid);
+    // the 64-bit divisions below are the same in every lane: done once per wave on uniform values
+    const int w_first = uniform(wave_of(row_start, total, grid));
+    const int w_last = uniform(wave_of(row_start + tiles - 1, total, grid));
     if (w_first == w_last) return;  // written directly
-    auto holds = [&](int k) { return total * k / grid < total * (k + 1) / grid; };
     const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
-    for (int base = 0; base < p.rows * D; base += 256 * 8) {
-        const int e = base + tid * 8;
-        if (e >= p.rows * D) break;
-        const int rr = e / D, d = e % D;
-        float m_run = -INFINITY, l_run = 0.0f, o_run[8];
+    const int e = (static_cast<int>(blockIdx.y) * 256 + tid) * 8;
+    if (e >= p.rows * D) return;
+    const int rr = e / D, d = e % D;
+    float m_run = -INFINITY, l_run = 0.0f, o_run[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o_run[i] = 0.0f;
-        for (int k0 = w_first; k0 <= w_last; k0 += 4) {
-            float mk[4], lk[4], ok[4][8];
+    for (int i = 0; i < 8; ++i) o_run[i] = 0.0f;
+    int64_t start_k = uniform64(total * w_first / grid);  // the first tile of workgroup k's range
+    for (int k0 = w_first; k0 <= w_last; k0 += 4) {
+        float mk[4], lk[4], ok[4][8];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int k = k0 + u;
-                const bool use = k <= w_last && holds(k);
-                const int kk = use ? k : w_first;
-                const float* sk = p.part + (2 * static_cast<int64_t>(kk) + (total * kk / grid < row_start ? 1 : 0)) * stride;
-                mk[u] = use ? sk[rr] : -INFINITY;
-                lk[u] = use ? sk[p.rows + rr] : 0.0f;
+        for (int u = 0; u < 4; ++u) {
+            const int k = k0 + u;
+            const int64_t end_k = uniform64(total * (k + 1) / grid);
+            const bool use = k <= w_last && start_k < end_k;  // workgroup k holds a part of the row
+            const float* sk = p.part + (2 * static_cast<int64_t>(use ? k : w_first) +
+                                        (use && start_k < row_start ? 1 : 0)) * stride;
+            mk[u] = use ? sk[p.rows * D + rr] : -INFINITY;
+            lk[u] = use ? sk[p.rows * D + p.rows + rr] : 0.0f;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) ok[u][i] = use ? sk[2 * p.rows + rr * D + d + i] : 0.0f;
+            for (int i = 0; i < 8; i += 2) {
+                const float2 x = use ? *reinterpret_cast<const float2*>(sk + rr * D + d + i) : make_float2(0.0f, 0.0f);
+                ok[u][i] = x.x;
+                ok[u][i + 1] = x.y;
             }
-            float m_new = m_run;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) m_new = fmaxf(m_new, mk[u]);
-            if (m_new == -INFINITY) continue;
-            const float a = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-            l_run *= a;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) o_run[i] *= a;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                if (mk[u] == -INFINITY) continue;
-                const float cw = __builtin_amdgcn_exp2f(mk[u] - m_new);
-                l_run += lk[u] * cw;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) o_run[i] += ok[u][i] * cw;
-            }
-            m_run = m_new;
+            start_k = end_k;
         }
+        float m_new = m_run;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) store_output(p, b, kvh, rr, d + i, o_run[i], m_run, l_run);
+        for (int u = 0; u < 4; ++u) m_new = fmaxf(m_new, mk[u]);
+        if (m_new == -INFINITY) continue;
+        const float a = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= a;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o_run[i] *= a;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (mk[u] == -INFINITY) continue;
+            const float cw = __builtin_amdgcn_exp2f(mk[u] - m_new);
+            l_run += lk[u] * cw;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o_run[i] += ok[u][i] * cw;
+        }
+        m_run = m_new;
     }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) store_output(p, b, kvh, rr, d + i, o_run[i], m_run, l_run);
 }
 
 template <typename F>
@@ -461,7 +476,8 @@ struct VerifyLaunch {
         static_cast<KiviParams&>(vp) = *p;
         hipLaunchKernelGGL((kivi_verify_kernel<D, BITS>), dim3(p->grid), dim3(256), 0, stream, vp);
         if (const int rc = check_launch("kivi_verify_kernel")) return rc;
-        hipLaunchKernelGGL((kivi_verify_merge_kernel<D>), dim3(p->batch * p->kv_heads), dim3(256), 0, stream, vp);
+        hipLaunchKernelGGL((kivi_verify_merge_kernel<D>), dim3(p->batch * p->kv_heads, (p->rows * D + 2047) / 2048),
+                           dim3(256), 0, stream, vp);
         return check_launch("kivi_verify_merge_kernel");
     }
 };
