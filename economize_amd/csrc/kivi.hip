@@ -25,9 +25,7 @@
 //
 // Work decomposition, pipeline and merge: the stream-K scheme of paged_attention.hip (stream_k.hpp), with tiles of
 // one 32-token page. The query of the current row lives in LDS, so that row changes do not put loads of varying
-// count in the tile pipeline. With more than 32 query rows per KV head (speculative verification) the four waves of
-// a workgroup share each tile instead: one column block of query rows each, the keys and values dequantized once
-// into LDS, a quarter of them by each wave.
+// count in the tile pipeline. More than 32 query rows per KV head (speculative verification) go to kivi_verify.hip.
 
 #include <cstdlib>
 #include <type_traits>
@@ -200,22 +198,17 @@ __global__ __launch_bounds__(256) void kivi_quant_values_kernel(KiviQuantParams 
 
 // A lane's share of one 32-token page: key words of its 8-token key rows, the value word of each 16-channel block
 // (lane (n, g): channel 16 nd + n, tokens 8 g .. 8 g + 7, the P.V MFMA's A operand), key scales and zero points of
-// its channels, value scales and zero points of its 8 tokens per value group. SHARED: the four waves of a workgroup
-// dequantize the tile together, lane (n, g) of wave w taking the KE key operand entries (k-step j, token half v)
-// with j * 2 + v = w * KE + e (one key word per entry and the scale and zero point of its 8 channels) and the VE
-// value blocks w * VE .. (one value group).
-template <int D, int BITS, bool SHARED = false>
+// its channels, value scales and zero points of its 8 tokens per value group.
+template <int D, int BITS>
 struct KTile {
     static constexpr int KW = D * BITS / 128;  // words of a lane's key slice (D / 4 channels)
     static constexpr int ND = D / 16;          // value blocks of 16 channels
     static constexpr int KS = D / 32;          // k-steps of an S MFMA (8 channels each per lane)
     static constexpr int VG = D / 32;          // value groups
-    static constexpr int KE = KS / 2;          // key entries per lane (SHARED)
-    static constexpr int VE = ND / 4;          // value blocks per wave (SHARED)
-    uint32_t kc[2][SHARED ? KE : KW];          // SHARED: kc[0][e]
-    uint32_t vc[SHARED ? VE : ND];
-    uint4 ks[SHARED ? 1 : KS], kz[SHARED ? 1 : KS];
-    uint4 vs[SHARED ? 1 : VG], vz[SHARED ? 1 : VG];
+    uint32_t kc[2][KW];
+    uint32_t vc[ND];
+    uint4 ks[KS], kz[KS];
+    uint4 vs[VG], vz[VG];
     int page;          // physical page (the same in every lane), -1 for none
     uint32_t mw[4];    // with a mask: bit e = token 8 g + e of the page visible to query row 16 nb + n (nb < NB)
 };
@@ -243,58 +236,32 @@ __device__ inline void load_words(const uint32_t* src, uint32_t (&dst)[N]) {
 
 // Issues the page loads of the tile under cursor c (the same loads in every lane and for every tile: a tile without
 // a page reads page 0 and masks it).
-template <int D, int BITS, bool SHARED>
-__device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c, int n, int g, int lane, int wave,
-                                           PageWindow& win, KTile<D, BITS, SHARED>& tile) {
-    using T = KTile<D, BITS, SHARED>;
+template <int D, int BITS>
+__device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c, int n, int g, int lane, PageWindow& win,
+                                           KTile<D, BITS>& tile) {
+    using T = KTile<D, BITS>;
     constexpr KiviLayout L{D, BITS};
     ensure_window(p, c, lane, win);
     const int phys = __builtin_amdgcn_readlane(win.physical, c.t - win.base);
     tile.page = phys;
     const uint8_t* blk = p.blocks + static_cast<int64_t>(phys >= 0 ? phys : 0) * p.blk_page + c.kvh * p.blk_head;
-    if constexpr (SHARED) {
-        const int j = (wave * T::KE) >> 1;  // the k-step of every entry of the lane
 #pragma unroll
-        for (int e = 0; e < T::KE; ++e) {
-            const int v = (wave * T::KE + e) & 1;
-            const int token = 8 * (n >> 2) + 4 * v + (n & 3);
-            tile.kc[0][e] = reinterpret_cast<const uint32_t*>(blk + L.k_codes() + token * (D * BITS / 8))
-                [g * T::KW + (BITS == 4 ? j : j / 2)];
-        }
-        tile.ks[0] = *reinterpret_cast<const uint4*>(blk + L.k_scale() + (g * (D / 4) + 8 * j) * 2);
-        tile.kz[0] = *reinterpret_cast<const uint4*>(blk + L.k_zero() + (g * (D / 4) + 8 * j) * 2);
-    } else {
-#pragma unroll
-        for (int v = 0; v < 2; ++v) {
-            const int token = 8 * (n >> 2) + 4 * v + (n & 3);
-            load_words(reinterpret_cast<const uint32_t*>(blk + L.k_codes() + token * (D * BITS / 8)) + g * T::KW,
-                       tile.kc[v]);
-        }
+    for (int v = 0; v < 2; ++v) {
+        const int token = 8 * (n >> 2) + 4 * v + (n & 3);
+        load_words(reinterpret_cast<const uint32_t*>(blk + L.k_codes() + token * (D * BITS / 8)) + g * T::KW, tile.kc[v]);
     }
     constexpr int TPW = 32 / BITS;  // tokens per value word
     const int u = 8 * g / TPW;
-    const uint32_t* vwords = reinterpret_cast<const uint32_t*>(blk + L.v_codes()) + (u * 16 + n) * T::ND;
-    if constexpr (SHARED) {
-        const int nd0 = wave * T::VE;  // the wave's value blocks, all in value group nd0 / 2
-        load_words(vwords + nd0, tile.vc);
-        tile.vs[0] = *reinterpret_cast<const uint4*>(blk + L.v_scale() + ((nd0 / 2) * 32 + 8 * g) * 2);
-        tile.vz[0] = *reinterpret_cast<const uint4*>(blk + L.v_zero() + ((nd0 / 2) * 32 + 8 * g) * 2);
-    } else {
-        load_words(vwords, tile.vc);
-    }
-    if constexpr (!SHARED) {
+    load_words(reinterpret_cast<const uint32_t*>(blk + L.v_codes()) + (u * 16 + n) * T::ND, tile.vc);
 #pragma unroll
-        for (int j = 0; j < T::KS; ++j) {
-            tile.ks[j] = *reinterpret_cast<const uint4*>(blk + L.k_scale() + (g * (D / 4) + 8 * j) * 2);
-            tile.kz[j] = *reinterpret_cast<const uint4*>(blk + L.k_zero() + (g * (D / 4) + 8 * j) * 2);
-        }
+    for (int j = 0; j < T::KS; ++j) {
+        tile.ks[j] = *reinterpret_cast<const uint4*>(blk + L.k_scale() + (g * (D / 4) + 8 * j) * 2);
+        tile.kz[j] = *reinterpret_cast<const uint4*>(blk + L.k_zero() + (g * (D / 4) + 8 * j) * 2);
     }
-    if constexpr (!SHARED) {
 #pragma unroll
-        for (int grp = 0; grp < T::VG; ++grp) {
-            tile.vs[grp] = *reinterpret_cast<const uint4*>(blk + L.v_scale() + (grp * 32 + 8 * g) * 2);
-            tile.vz[grp] = *reinterpret_cast<const uint4*>(blk + L.v_zero() + (grp * 32 + 8 * g) * 2);
-        }
+    for (int grp = 0; grp < T::VG; ++grp) {
+        tile.vs[grp] = *reinterpret_cast<const uint4*>(blk + L.v_scale() + (grp * 32 + 8 * g) * 2);
+        tile.vz[grp] = *reinterpret_cast<const uint4*>(blk + L.v_zero() + (grp * 32 + 8 * g) * 2);
     }
 }
 
@@ -342,44 +309,35 @@ __device__ __forceinline__ void split_bf16(const float (&p)[8], bf16x8& hi, bf16
 }  // namespace
 
 // Workgroup shapes. One column block at D <= 128: four waves split the workgroup's tile range in quarters, the
-// pieces of rows inside the workgroup merged through LDS (as in paged_attention.hip). SHARED (more than 32 query rows
-// per KV head, the verification shape): four waves walk the workgroup's range together, wave w taking query rows
-// 16 w .. 16 w + 15, and dequantize a quarter of each key tile each into LDS (one barrier per tile), so that a key
-// is dequantized once for all query rows. Otherwise one wave.
-template <int D, int NB, bool SHARED>
+// pieces of rows inside the workgroup merged through LDS (as in paged_attention.hip). Otherwise one wave.
+template <int D, int NB>
 constexpr int kivi_wg_waves() {
-    return SHARED || (NB == 1 && D <= 128) ? 4 : 1;
+    return NB == 1 && D <= 128 ? 4 : 1;
 }
 
-// Waves per SIMD: two for the single-buffer instances of one column block, SHARED ones included (they fit 256
-// registers, and two workgroups' LDS fit a CU); one wave of a SIMD does not overlap its own arithmetic with its
-// outstanding loads, two waves do.
-template <int D, int NB, int NBUF, bool SHARED>
+// Waves per SIMD: two for the single-buffer instances of one column block (they fit 256 registers); one wave of a
+// SIMD does not overlap its own arithmetic with its outstanding loads, two waves do.
+template <int D, int NB, int NBUF>
 constexpr int kivi_waves_per_simd() {
-    return NB == 1 && D <= 128 && (NBUF == 1 || SHARED) ? 2 : 1;
+    return NB == 1 && D <= 128 && NBUF == 1 ? 2 : 1;
 }
 
-template <int D, int BITS, int NB, int NBUF, bool SHARED>
-__global__ __launch_bounds__((64 * kivi_wg_waves<D, NB, SHARED>()))
-    __attribute__((amdgpu_waves_per_eu(kivi_waves_per_simd<D, NB, NBUF, SHARED>()))) void
+template <int D, int BITS, int NB, int NBUF>
+__global__ __launch_bounds__((64 * kivi_wg_waves<D, NB>()))
+    __attribute__((amdgpu_waves_per_eu(kivi_waves_per_simd<D, NB, NBUF>()))) void
 kivi_attention_kernel(KiviParams p) {
-    static_assert(!SHARED || NB == 1, "a shared-tile wave holds one column block");
-    using T = KTile<D, BITS, SHARED>;
+    using T = KTile<D, BITS>;
     constexpr int KS = T::KS, ND = T::ND, VG = T::VG;
     constexpr int R = NB * 16;  // query rows of the MFMA columns
-    constexpr int WAVES = kivi_wg_waves<D, NB, SHARED>();
-    constexpr bool kSplit = !SHARED && WAVES > 1;  // the range split in quarters, pieces merged in LDS
+    constexpr int WAVES = kivi_wg_waves<D, NB>();
+    constexpr bool kSplit = WAVES > 1;  // the range split in quarters, pieces merged in LDS
     using QRows = uint4[R][D / 8 + 1];             // a wave's current query rows (one word of padding: a row stride of
                                                    // D / 8 + 1 words puts the 16 rows of a lane group in distinct banks)
 
     const int lane = WAVES > 1 ? static_cast<int>(threadIdx.x) & 63 : static_cast<int>(threadIdx.x);
     const int wave = WAVES > 1 ? uniform(static_cast<int>(threadIdx.x) >> 6) : 0;
-    const int row0 = SHARED ? 16 * wave : 0;  // the wave's first query row
+    constexpr int row0 = 0;  // the first query row of the wave's columns
     __shared__ __align__(16) typename std::conditional<kSplit, Pieces<D, WAVES>, char>::type pieces;
-    // SHARED: the dequantized key and value tiles, two buffers, in MFMA operand order (key entry j * 2 + v, lane;
-    // value block nd, lane)
-    __shared__ typename std::conditional<SHARED, uint4[2][2 * KS][64], char>::type kbuf;
-    __shared__ typename std::conditional<SHARED, uint4[2][ND][64], char>::type vbuf;
     QRows* q_rows;
     if constexpr (kSplit) {
         // the query rows live in the data of the wave's second piece, which only the wave's last step writes, after
@@ -413,7 +371,7 @@ kivi_attention_kernel(KiviParams p) {
     if constexpr (kSplit) {
         clear_pieces(pieces, wave, lane);
     } else {
-        if (lo >= hi) return;  // (SHARED: the same for every wave of the workgroup)
+        if (lo >= hi) return;
     }
 
     // ---- row state ----
@@ -459,40 +417,8 @@ kivi_attention_kernel(KiviParams p) {
         return vq - tok0 >= 8 ? 0xFFu : (vq > tok0 ? (1u << (vq - tok0)) - 1u : 0u);
     };
 
-    // ---- SHARED: the lane's entries of the key and value tiles, dequantized into LDS buffer buf ----
-    auto share_tile = [&](const T& tile, const Cursor& c, int buf) __attribute__((always_inline)) {
-        if constexpr (SHARED) {
-            const int t0 = KPAGE * c.t;
-            if (t0 < kq) {
-                const f16x8 sh = __builtin_bit_cast(f16x8, tile.ks[0]);
-                const f16x8 zh = __builtin_bit_cast(f16x8, tile.kz[0]);
-                const int j = (wave * T::KE) >> 1;
-#pragma unroll
-                for (int e = 0; e < T::KE; ++e) {
-                    float c8[8];
-                    codes_to_f32<BITS>(tile.kc[0][e], j % 2, c8);
-                    bf16x8 kv;
-#pragma unroll
-                    for (int i = 0; i < 8; ++i)
-                        kv[i] = static_cast<__bf16>(
-                            __builtin_fmaf(c8[i], static_cast<float>(sh[i]), static_cast<float>(zh[i])));
-                    kbuf[buf][wave * T::KE + e][lane] = __builtin_bit_cast(uint4, kv);
-                }
-            }
-            if (t0 < vq) {
-                // tokens at or past vq, and every token of a missing page, are zero (an unwritten scale may be inf
-                // or NaN); they come from the ring or carry no weight
-                const HalfMask mask = half_mask(code_values(tile, t0));
-#pragma unroll
-                for (int e = 0; e < T::VE; ++e)
-                    vbuf[buf][wave * T::VE + e][lane] =
-                        apply_mask(dequant_values<BITS>(tile.vc[e], g, tile.vs[0], tile.vz[0]), mask);
-            }
-        }
-    };
-
     // ---- one tile (32 tokens) of the online softmax ----
-    auto compute = [&](const T& tile, const Cursor& c, int buf) __attribute__((always_inline)) {
+    auto compute = [&](const T& tile, const Cursor& c) __attribute__((always_inline)) {
         const int t0 = KPAGE * c.t;
         const bool valid = tile.page >= 0;
         f32x4 s[2][NB];
@@ -504,40 +430,30 @@ kivi_attention_kernel(KiviParams p) {
         // attention/kivi.py:56-76), so that the scores see the reference's key values exactly; or, at or past kq,
         // from the ring (kq counts whole 32-token key groups, so a page is either all codes or all ring)
         if (t0 < kq) {
-            if constexpr (SHARED) {
 #pragma unroll
-                for (int j = 0; j < KS; ++j)
+            for (int j = 0; j < KS; ++j) {
+                const f16x8 sh = __builtin_bit_cast(f16x8, tile.ks[j]);
+                const f16x8 zh = __builtin_bit_cast(f16x8, tile.kz[j]);
+                float sf[8], zf[8];
 #pragma unroll
-                    for (int v = 0; v < 2; ++v)
-                        s[v][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            __builtin_bit_cast(bf16x8, kbuf[buf][2 * j + v][lane]),
-                            __builtin_bit_cast(bf16x8, q_bf[n][g * (D / 32) + j]), s[v][0], 0, 0, 0);
-            } else {
+                for (int e = 0; e < 8; ++e) {
+                    sf[e] = static_cast<float>(sh[e]);
+                    zf[e] = static_cast<float>(zh[e]);
+                }
 #pragma unroll
-                for (int j = 0; j < KS; ++j) {
-                    const f16x8 sh = __builtin_bit_cast(f16x8, tile.ks[j]);
-                    const f16x8 zh = __builtin_bit_cast(f16x8, tile.kz[j]);
-                    float sf[8], zf[8];
+                for (int v = 0; v < 2; ++v) {
+                    float c8[8];
+                    codes_to_f32<BITS>(BITS == 4 ? tile.kc[v][j] : tile.kc[v][j / 2], j % 2, c8);
+                    bf16x8 kv;
+                    // code * scale is exact in fp32 (a code of at most 4 bits times an fp16), so one fused
+                    // multiply-add rounds exactly as the reference's product then sum
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        sf[e] = static_cast<float>(sh[e]);
-                        zf[e] = static_cast<float>(zh[e]);
-                    }
+                    for (int e = 0; e < 8; ++e) kv[e] = static_cast<__bf16>(__builtin_fmaf(c8[e], sf[e], zf[e]));
 #pragma unroll
-                    for (int v = 0; v < 2; ++v) {
-                        float c8[8];
-                        codes_to_f32<BITS>(BITS == 4 ? tile.kc[v][j] : tile.kc[v][j / 2], j % 2, c8);
-                        bf16x8 kv;
-                        // code * scale is exact in fp32 (a code of at most 4 bits times an fp16), so one fused
-                        // multiply-add rounds exactly as the reference's product then sum
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) kv[e] = static_cast<__bf16>(__builtin_fmaf(c8[e], sf[e], zf[e]));
-#pragma unroll
-                        for (int nb = 0; nb < NB; ++nb)
-                            s[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                                kv, __builtin_bit_cast(bf16x8, q_bf[nb * 16 + n][g * (D / 32) + j]), s[v][nb], 0,
-                                0, 0);
-                    }
+                    for (int nb = 0; nb < NB; ++nb)
+                        s[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                            kv, __builtin_bit_cast(bf16x8, q_bf[nb * 16 + n][g * (D / 32) + j]), s[v][nb], 0,
+                            0, 0);
                 }
             }
         } else {
@@ -637,25 +553,20 @@ kivi_attention_kernel(KiviParams p) {
             }
         };
         if (t0 < vq) {  // from codes: O += bf16(c * s + z) . p
-            if constexpr (SHARED) {
+            // tokens at or past vq and every token of a missing page are zero (an unwritten scale may be inf or
+            // NaN); a tile of codes only skips the masks
+            auto from_codes = [&](auto full_tag, const HalfMask& mask) __attribute__((always_inline)) {
+                constexpr bool kFull = decltype(full_tag)::value;
 #pragma unroll
-                for (int nd = 0; nd < ND; ++nd) product(nd, vbuf[buf][nd][lane]);
-            } else {
-                // tokens at or past vq and every token of a missing page are zero (an unwritten scale may be inf or
-                // NaN); a tile of codes only skips the masks
-                auto from_codes = [&](auto full_tag, const HalfMask& mask) __attribute__((always_inline)) {
-                    constexpr bool kFull = decltype(full_tag)::value;
-#pragma unroll
-                    for (int nd = 0; nd < ND; ++nd) {
-                        const uint4 v = dequant_values<BITS>(tile.vc[nd], g, tile.vs[nd / 2], tile.vz[nd / 2]);
-                        product(nd, kFull ? v : apply_mask(v, mask));
-                    }
-                };
-                if (NB <= 2 && t0 + KPAGE <= vq && valid) {  // (at four column blocks the second copy would spill)
-                    from_codes(std::integral_constant<bool, NB <= 2>{}, HalfMask{});
-                } else {
-                    from_codes(std::false_type{}, half_mask(code_values(tile, t0)));
+                for (int nd = 0; nd < ND; ++nd) {
+                    const uint4 v = dequant_values<BITS>(tile.vc[nd], g, tile.vs[nd / 2], tile.vz[nd / 2]);
+                    product(nd, kFull ? v : apply_mask(v, mask));
                 }
+            };
+            if (NB <= 2 && t0 + KPAGE <= vq && valid) {  // (at four column blocks the second copy would spill)
+                from_codes(std::integral_constant<bool, NB <= 2>{}, HalfMask{});
+            } else {
+                from_codes(std::false_type{}, half_mask(code_values(tile, t0)));
             }
         }
         if (t0 + KPAGE > vq) {  // from the ring (tokens at or past vq, below the row's end)
@@ -716,12 +627,6 @@ kivi_attention_kernel(KiviParams p) {
                 for (int i = 0; i < 4; ++i)
                     coherent_store(slot + 2 * p.rows + r * D + 16 * nd + 4 * g + i, o[nd][nb][i]);
         }
-        if constexpr (SHARED) {  // every wave's rows are complete before wave 0 counts the slot
-            __atomic_signal_fence(__ATOMIC_SEQ_CST);
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
-            if (wave != 0) return;
-        }
         hand_off<D>(p, c, total, grid, lane);
     };
 
@@ -737,13 +642,13 @@ kivi_attention_kernel(KiviParams p) {
             for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         begin_row(cur);
 
-        // with two buffers a tile's loads are issued a tile ahead (SHARED: the wave's shares of its keys and values)
+        // with two buffers a tile's loads are issued a tile ahead
         T bufs[NBUF];
         Cursor cs[NBUF];
         Cursor icur = cur;
         int64_t ipos = lo;
         auto issue_next = [&](T& buf, Cursor& slot) __attribute__((always_inline)) {
-            issue_tile<D, BITS, SHARED>(p, icur, n, g, lane, wave, win, buf);
+            issue_tile<D, BITS>(p, icur, n, g, lane, win, buf);
             if (p.mask)  // the tile is page icur.t: word icur.t of every query row's mask
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
@@ -764,13 +669,7 @@ kivi_attention_kernel(KiviParams p) {
             issue_next(bufs[J], cs[J]);
             cur = cs[I];
             if (cur.t == 0 && pos != lo) begin_row(cur);
-            if constexpr (SHARED) {
-                // this tile's keys and values into LDS buffer pos & 1; the barrier also ends every wave's reads of
-                // that buffer two tiles back (they precede the previous tile's barrier)
-                share_tile(bufs[I], cur, static_cast<int>(pos & 1));
-                __syncthreads();
-            }
-            compute(bufs[I], cur, static_cast<int>(pos & 1));
+            compute(bufs[I], cur);
             const bool more = pos + 1 < hi;
             if (cur.t + 1 == cur.row.tiles || !more) {
                 finish(cur, seg_begin, pos + 1, first_segment);
@@ -812,19 +711,8 @@ int kivi_stages() {
     return stages;
 }
 
-// Key buffers of the shared-tile instance: 2 (a tile's keys issued a tile ahead, the default) or 1;
-// ECO_KIVI_SHARED_STAGES overrides.
-int kivi_shared_stages() {
-    static const int stages = [] {
-        const char* env = std::getenv("ECO_KIVI_SHARED_STAGES");
-        const int v = env ? std::atoi(env) : 2;
-        return v <= 1 ? 1 : 2;
-    }();
-    return stages;
-}
-
-// Column blocks from which the shared-tile instance serves (default 3: more than 32 query rows per KV head);
-// ECO_KIVI_SHARED overrides.
+// Column blocks of 16 query rows from which the verification kernel (kivi_verify.hip: two-page tiles shared by four
+// waves) serves (default 3: more than 32 query rows per KV head); ECO_KIVI_SHARED overrides.
 int kivi_shared_from() {
     static const int from = [] {
         const char* env = std::getenv("ECO_KIVI_SHARED");
@@ -834,40 +722,28 @@ int kivi_shared_from() {
     return from;
 }
 
-// The two-page-tile kernel of kivi_verify.hip for the shared-tile shapes (default 1; ECO_KIVI_VERIFY=0 keeps the
-// one-page shared-tile instance here).
-bool kivi_verify_enabled() {
-    static const bool on = [] {
-        const char* env = std::getenv("ECO_KIVI_VERIFY");
-        return env ? std::atoi(env) != 0 : true;
-    }();
-    return on;
-}
-
 // An attention instance: the kernel, its threads per workgroup and the parts a workgroup's tile range is split in
 // (the grid gives every part at least four tiles).
-using KiviKernelFn = decltype(&kivi_attention_kernel<64, 2, 1, 1, false>);
+using KiviKernelFn = decltype(&kivi_attention_kernel<64, 2, 1, 1>);
 struct KiviInstance {
     KiviKernelFn kernel;
     int threads;
     int parts;
 };
 
-template <int D, int BITS, int NB, int NBUF, bool SHARED>
+template <int D, int BITS, int NB, int NBUF>
 KiviInstance kivi_instance() {
-    constexpr int waves = kivi_wg_waves<D, NB, SHARED>();
-    return {kivi_attention_kernel<D, BITS, NB, NBUF, SHARED>, 64 * waves, SHARED ? 1 : waves};
+    constexpr int waves = kivi_wg_waves<D, NB>();
+    return {kivi_attention_kernel<D, BITS, NB, NBUF>, 64 * waves, waves};
 }
 
-// NB column blocks of query rows: one block, the split instance (one or two tile buffers); from kivi_shared_from()
-// blocks, the shared-tile instance; otherwise one wave over NB blocks.
+// NB column blocks of query rows below kivi_shared_from(): one block, the split instance (one or two tile buffers);
+// otherwise one wave over NB blocks.
 template <int D, int BITS, int NB>
 KiviInstance kivi_kernel_of() {
     if constexpr (NB == 1)
-        return kivi_stages() == 1 ? kivi_instance<D, BITS, 1, 1, false>() : kivi_instance<D, BITS, 1, 2, false>();
-    if (NB >= kivi_shared_from())
-        return kivi_shared_stages() == 2 ? kivi_instance<D, BITS, 1, 2, true>() : kivi_instance<D, BITS, 1, 1, true>();
-    return kivi_instance<D, BITS, NB, 1, false>();
+        return kivi_stages() == 1 ? kivi_instance<D, BITS, 1, 1>() : kivi_instance<D, BITS, 1, 2>();
+    return kivi_instance<D, BITS, NB, 1>();
 }
 
 template <typename F>
@@ -896,7 +772,7 @@ struct KiviLaunch {
     const KiviParams* p;
     template <int D, int BITS, int NB>
     int run() const {
-        if (NB >= kivi_shared_from() && kivi_verify_enabled()) return kivi_verify_attention(*p, stream);
+        if (NB >= kivi_shared_from()) return kivi_verify_attention(*p, stream);
         const KiviInstance in = kivi_kernel_of<D, BITS, NB>();
         hipLaunchKernelGGL(in.kernel, dim3(p->grid), dim3(in.threads), 0, stream, *p);
         return check_launch("kivi_attention_kernel");
@@ -908,7 +784,7 @@ struct KiviOccupancy {
     int* waves;
     template <int D, int BITS, int NB>
     int run() const {
-        if (NB >= kivi_shared_from() && kivi_verify_enabled()) {
+        if (NB >= kivi_shared_from()) {
             *waves = 2;  // two-page tiles: four tiles per workgroup are eight pages
             return kivi_verify_resident_groups(D, BITS, per_cu);
         }
