@@ -218,8 +218,8 @@ def _fallback_reason(module, query: torch.Tensor, key, attention_mask, dropout: 
         if query.dtype != torch.bfloat16:
             return "dtype"  # the paged kernels take bf16 queries
         kv_heads = paged.cache.kv_heads
-        if q_heads % kv_heads == 0 and (q_heads // kv_heads) * queries > 64:
-            return "rows"  # the paged kernels take at most 64 query rows per KV head
+        if q_heads % kv_heads == 0 and q_heads // kv_heads > 64:
+            return "heads_per_kv"  # the paged kernels take at most 64 query heads per KV head
     else:
         if key.dtype != query.dtype and (key.dtype not in FP8_DTYPES or gathered is not None):
             return "kv_dtype"  # the gathered kernel takes K/V in the query's dtype

@@ -57,6 +57,22 @@ int device_cus() {
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
+// The attention kernels hold at most 64 query rows per KV head (four column blocks of 16). A call with more (query
+// heads per KV head x queries, at most 64 heads per KV head) is launched in query chunks of floor(64 / groups), one
+// after the other on the stream, each chunk's causal limits shifted by the queries after it (query qi of Q sees the
+// tokens below L - Q + qi + 1).
+struct QueryChunks {
+    int per, count, last;  // queries per chunk, chunks, queries of the last chunk
+};
+
+QueryChunks query_chunks(int groups, int queries) {
+    QueryChunks c;
+    c.per = std::min(std::max(1, 64 / std::max(groups, 1)), queries);
+    c.count = (queries + c.per - 1) / c.per;
+    c.last = queries - (c.count - 1) * c.per;
+    return c;
+}
+
 // Workgroups of a launch: every CU's resident workgroups of the kernel instance, but at least four tiles (256 tokens)
 // per wave over the longest possible tile sequence, which bounds the partials a row can be cut into
 // (ECO_PAGED_GRID overrides the count for tuning).
@@ -175,8 +191,8 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
     if (kv_format != BF16 && kv_format != FP8_E4M3 && kv_format != FP8_E5M2)
         return fail("paged decode: KV format must be bf16, fp8 e4m3 or fp8 e5m2");
     const int groups = q_heads / kv_heads;
-    const int rows = groups * queries;
-    if (rows > 64) return fail("paged decode: at most 64 query rows per KV head (query heads per KV head x queries)");
+    if (groups > 64) return fail("paged decode: at most 64 query heads per KV head");
+    const QueryChunks qc = query_chunks(groups, queries);
     if ((reinterpret_cast<uintptr_t>(q) & 15) || (sq_b & 7) || (sq_q & 7) || (sq_h & 7))
         return fail("paged decode: the query must be 16-byte aligned with strides that are multiples of 8");
     if (page_list && (!done || n_sel < 0)) return fail("paged decode: a page list needs done[] and n_sel >= 0");
@@ -188,14 +204,20 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
     if (!(scale == scale)) return fail("paged decode: scale is NaN");
     if (mask_bits && mask_words <= 0) return fail("paged decode: a mask needs a positive word count");
 
-    const int grid =
-        paged_grid(batch, kv_heads, rows, head_dim, kv_format, max_seq_len, page_list ? n_sel * span : 0, span);
-    if (grid <= 0) return 1;
-    const Workspace ws = paged_workspace(batch, kv_heads, rows, head_dim, grid);
+    // the launch plan of each chunk shape (every chunk but the last, then the last)
+    const int listed = page_list ? n_sel * span : 0;
+    int grids[2];
+    size_t need = 0;
+    for (int i = 0; i < 2; ++i) {
+        const int rows_i = groups * (i == 0 ? qc.per : qc.last);
+        grids[i] = paged_grid(batch, kv_heads, rows_i, head_dim, kv_format, max_seq_len, listed, span);
+        if (grids[i] <= 0) return 1;
+        need = std::max(need, paged_workspace(batch, kv_heads, rows_i, head_dim, grids[i]).total());
+    }
     if (validate_only) return 0;
-    if (!workspace || workspace_bytes < ws.total())
+    if (!workspace || workspace_bytes < need)
         return fail("paged decode: workspace too small (" + std::to_string(workspace_bytes) + " < " +
-                    std::to_string(ws.total()) + " bytes)");
+                    std::to_string(need) + " bytes)");
 
     const int es = kv_format == BF16 ? 2 : 1;
     PagedParams p;
@@ -231,23 +253,30 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
     p.mask_words = mask_bits ? mask_words : 0;
     char* base = static_cast<char*>(workspace);
     p.counters = reinterpret_cast<int32_t*>(base);
-    p.part = reinterpret_cast<float*>(base + ws.counter_bytes);
-    p.out = static_cast<uint16_t*>(out);
+    p.part = reinterpret_cast<float*>(base + paged_workspace(batch, kv_heads, 1, head_dim, 1).counter_bytes);
     p.so_b = so_b;
     p.so_q = so_q;
     p.so_h = so_h;
     p.batch = batch;
-    p.queries = queries;
     p.q_heads = q_heads;
     p.kv_heads = kv_heads;
     p.groups = groups;
-    p.rows = rows;
     p.head_dim = head_dim;
     p.kv_format = kv_format;
-    p.grid = grid;
     p.scale = scale;
     p.softcap = softcap > 0.0f ? softcap : 0.0f;
-    return paged_attention(p, static_cast<hipStream_t>(stream));
+    for (int c = 0; c < qc.count; ++c) {
+        const int q0 = c * qc.per, k = c + 1 < qc.count ? qc.per : qc.last;
+        p.q = static_cast<const uint16_t*>(q) + q0 * sq_q;
+        p.out = static_cast<uint16_t*>(out) + q0 * so_q;
+        p.mask = mask_bits ? mask_bits + q0 * mk_q : nullptr;
+        p.queries = k;
+        p.queries_after = queries - q0 - k;
+        p.rows = groups * k;
+        p.grid = grids[c + 1 < qc.count ? 0 : 1];
+        if (const int rc = paged_attention(p, static_cast<hipStream_t>(stream))) return rc;
+    }
+    return 0;
 }
 
 // ---- the static scratch of eco_paged_decode_static ---------------------------------------------------------------
@@ -539,12 +568,17 @@ size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q
                                        int32_t head_dim, int32_t max_seq_len, int32_t n_sel, int32_t list_page_size,
                                        int32_t kv_format) {
     if (batch <= 0 || queries <= 0 || kv_heads <= 0 || q_heads <= 0 || head_dim <= 0 || max_seq_len <= 0) return 0;
-    const int rows = (q_heads / kv_heads) * queries;
+    const int groups = q_heads / kv_heads;
+    const QueryChunks qc = query_chunks(groups, queries);
     const int span = list_page_size >= 16 ? list_page_size / 16 : 1;
-    const int grid =
-        paged_grid(batch, kv_heads, rows, head_dim, kv_format, max_seq_len, n_sel > 0 ? n_sel * span : 0, span);
-    if (grid <= 0) return 0;
-    return paged_workspace(batch, kv_heads, rows, head_dim, grid).total();
+    size_t need = 0;
+    for (const int k : {qc.per, qc.last}) {
+        const int grid =
+            paged_grid(batch, kv_heads, groups * k, head_dim, kv_format, max_seq_len, n_sel > 0 ? n_sel * span : 0, span);
+        if (grid <= 0) return 0;
+        need = std::max(need, paged_workspace(batch, kv_heads, groups * k, head_dim, grid).total());
+    }
+    return need;
 }
 
 int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
@@ -988,10 +1022,15 @@ size_t eco_kivi_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_
                                       int32_t head_dim, int32_t max_seq_len, int32_t bits) {
     if (batch <= 0 || queries <= 0 || kv_heads <= 0 || q_heads <= 0 || max_seq_len <= 0) return 0;
     if (check_kivi_shape(head_dim, bits, 32)) return 0;
-    const int rows = (q_heads / kv_heads) * queries;
-    const int grid = kivi_grid(batch, kv_heads, rows, head_dim, bits, max_seq_len);
-    if (grid <= 0) return 0;
-    return paged_workspace(batch, kv_heads, rows, head_dim, grid).total();
+    const int groups = q_heads / kv_heads;
+    const QueryChunks qc = query_chunks(groups, queries);
+    size_t need = 0;
+    for (const int k : {qc.per, qc.last}) {
+        const int grid = kivi_grid(batch, kv_heads, groups * k, head_dim, bits, max_seq_len);
+        if (grid <= 0) return 0;
+        need = std::max(need, paged_workspace(batch, kv_heads, groups * k, head_dim, grid).total());
+    }
+    return need;
 }
 
 int eco_kivi_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* blocks, int32_t num_pages,
@@ -1012,19 +1051,25 @@ int eco_kivi_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, con
     if (int rc = check_kivi_shape(head_dim, bits, group)) return rc;
     if (ring <= 0 || ring % 32) return fail("kivi decode: the ring must hold a positive multiple of 32 slots");
     const int groups = q_heads / kv_heads;
-    const int rows = groups * queries;
-    if (rows > 64) return fail("kivi decode: at most 64 query rows per KV head (query heads per KV head x queries)");
+    if (groups > 64) return fail("kivi decode: at most 64 query heads per KV head");
+    const QueryChunks qc = query_chunks(groups, queries);
     if ((reinterpret_cast<uintptr_t>(q) & 15) || (sq_b & 7) || (sq_q & 7) || (sq_h & 7))
         return fail("kivi decode: the query must be 16-byte aligned with strides that are multiples of 8");
     if (max_seq_len <= 0) return fail("kivi decode: max_seq_len must be positive");
     if (!(scale == scale)) return fail("kivi decode: scale is NaN");
     if (mask_bits && mask_words <= 0) return fail("kivi decode: a mask needs a positive word count");
-    const int grid = kivi_grid(batch, kv_heads, rows, head_dim, bits, max_seq_len);
-    if (grid <= 0) return 1;
-    const Workspace ws = paged_workspace(batch, kv_heads, rows, head_dim, grid);
-    if (!workspace || workspace_bytes < ws.total())
+    // the launch plan of each chunk shape (every chunk but the last, then the last)
+    int grids[2];
+    size_t need = 0;
+    for (int i = 0; i < 2; ++i) {
+        const int rows_i = groups * (i == 0 ? qc.per : qc.last);
+        grids[i] = kivi_grid(batch, kv_heads, rows_i, head_dim, bits, max_seq_len);
+        if (grids[i] <= 0) return 1;
+        need = std::max(need, paged_workspace(batch, kv_heads, rows_i, head_dim, grids[i]).total());
+    }
+    if (!workspace || workspace_bytes < need)
         return fail("kivi decode: workspace too small (" + std::to_string(workspace_bytes) + " < " +
-                    std::to_string(ws.total()) + " bytes)");
+                    std::to_string(need) + " bytes)");
     const KiviLayout L{head_dim, bits};
     KiviParams p;
     std::memset(&p, 0, sizeof(p));
@@ -1053,23 +1098,30 @@ int eco_kivi_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, con
     p.mask_words = mask_bits ? mask_words : 0;
     char* base = static_cast<char*>(workspace);
     p.counters = reinterpret_cast<int32_t*>(base);
-    p.part = reinterpret_cast<float*>(base + ws.counter_bytes);
-    p.out = static_cast<uint16_t*>(out);
+    p.part = reinterpret_cast<float*>(base + paged_workspace(batch, kv_heads, 1, head_dim, 1).counter_bytes);
     p.so_b = so_b;
     p.so_q = so_q;
     p.so_h = so_h;
     p.batch = batch;
-    p.queries = queries;
     p.q_heads = q_heads;
     p.kv_heads = kv_heads;
     p.groups = groups;
-    p.rows = rows;
     p.head_dim = head_dim;
     p.bits = bits;
-    p.grid = grid;
     p.scale = scale;
     p.softcap = softcap > 0.0f ? softcap : 0.0f;
-    return kivi_attention(p, static_cast<hipStream_t>(stream));
+    for (int c = 0; c < qc.count; ++c) {
+        const int q0 = c * qc.per, k = c + 1 < qc.count ? qc.per : qc.last;
+        p.q = static_cast<const uint16_t*>(q) + q0 * sq_q;
+        p.out = static_cast<uint16_t*>(out) + q0 * so_q;
+        p.mask = mask_bits ? mask_bits + q0 * mk_q : nullptr;
+        p.queries = k;
+        p.queries_after = queries - q0 - k;
+        p.rows = groups * k;
+        p.grid = grids[c + 1 < qc.count ? 0 : 1];
+        if (const int rc = kivi_attention(p, static_cast<hipStream_t>(stream))) return rc;
+    }
+    return 0;
 }
 
 int eco_quest_page_bounds(const void* k_cache, int32_t kv_format, int32_t num_pages, const int32_t* block_table,

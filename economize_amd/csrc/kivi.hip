@@ -397,11 +397,11 @@ kivi_attention_kernel(KiviParams p) {
         kq = scalar_load(p.keys_quantized, c.b);
         vq = scalar_load(p.values_quantized, c.b);
         row_len = c.row.len;
-        all_see = c.row.len - p.queries + 1;
+        all_see = c.row.len - p.queries - p.queries_after + 1;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             const int r = row0 + nb * 16 + n;
-            limit[nb] = r < p.rows ? static_cast<float>(c.row.len - p.queries + r % p.queries + 1) : 0.0f;
+            limit[nb] = r < p.rows ? static_cast<float>(c.row.len - p.queries - p.queries_after + r % p.queries + 1) : 0.0f;
             // the accumulators are cleared by the row's first rescale (m_i = -inf marks a row with no weight yet),
             // so that a row change does not give them a second register version to merge at every tile
             m_i[nb] = -INFINITY;

@@ -48,6 +48,7 @@ struct KiviParams {
     uint16_t* out;
     int64_t so_b, so_q, so_h;
     int batch, queries, q_heads, kv_heads, groups, rows, head_dim, bits;
+    int queries_after;  // queries of the call after this launch's (a call cut in query chunks): they shift the causal limit
     int grid;
     float scale, softcap;
 };

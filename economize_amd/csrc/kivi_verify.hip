@@ -142,8 +142,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         kq = scalar_load(p.keys_quantized, c.b);
         vq = scalar_load(p.values_quantized, c.b);
         row_len = c.row.len;
-        all_see = c.row.len - p.queries + 1;
-        limit = r < p.rows ? static_cast<float>(c.row.len - p.queries + r % p.queries + 1) : 0.0f;
+        all_see = c.row.len - p.queries - p.queries_after + 1;
+        limit = r < p.rows ? static_cast<float>(c.row.len - p.queries - p.queries_after + r % p.queries + 1) : 0.0f;
         m_i = -INFINITY;
         l_i = 0.0f;
 #pragma unroll

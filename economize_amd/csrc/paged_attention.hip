@@ -327,7 +327,7 @@ paged_attention_kernel(PagedParams p) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             const int r = nb * 16 + n;
-            limit[nb] = r < p.rows ? static_cast<float>(c.row.len - p.queries + r % p.queries + 1) : 0.0f;
+            limit[nb] = r < p.rows ? static_cast<float>(c.row.len - p.queries - p.queries_after + r % p.queries + 1) : 0.0f;
             m_i[nb] = -INFINITY;
             l_i[nb] = 0.0f;
             // two-wave instances: the accumulators are cleared by the row's first rescale (m_i = -inf marks a row
@@ -337,7 +337,7 @@ paged_attention_kernel(PagedParams p) {
 #pragma unroll
                 for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         }
-        all_see = c.row.len - p.queries + 1;
+        all_see = c.row.len - p.queries - p.queries_after + 1;
         const float ks = p.k_scale ? scalar_load(p.k_scale, c.kvh) : 1.0f;
         vs = p.v_scale ? scalar_load(p.v_scale, c.kvh) : 1.0f;
         score_scale = p.softcap > 0.0f ? p.scale * ks : p.scale * ks * kLog2e;

@@ -37,6 +37,7 @@ struct PagedParams {
     uint16_t* out;  // bf16 [B, Q, Hq, D], channel stride 1
     int64_t so_b, so_q, so_h;
     int batch, queries, q_heads, kv_heads, groups, rows, head_dim, kv_format;
+    int queries_after;  // queries of the call after this launch's (a call cut in query chunks): they shift the causal limit
     int grid;  // workgroups launched
     float scale, softcap;
 };

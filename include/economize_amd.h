@@ -90,7 +90,9 @@ size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q
  * into equal contiguous ranges of 64-token tiles, one per wave, so ragged rows need no host-side plan; max_seq_len
  * (>= every seq_lens[b]) only bounds the launch. An optional packed attention mask (eco_mask_bits: bit t % 32 of word
  * mask_bits[b * mk_b + h * mk_h + qi * mk_q + t / 32], word strides 0 on broadcast axes, mask_words words per row;
- * NULL = none) hides token t from query qi of head h where its bit is 0, on top of the causal limit. */
+ * NULL = none) hides token t from query qi of head h where its bit is 0, on top of the causal limit. At most 64
+ * query heads per KV head; a call of more than 64 query rows per KV head (query heads per KV head x queries) runs as
+ * consecutive launches over chunks of floor(64 / (q_heads / kv_heads)) queries on the stream. */
 int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
                      const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
                      const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
@@ -324,8 +326,8 @@ size_t eco_kivi_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_
 /* Decode attention over the paged KIVI cache and the rings: as eco_paged_decode (query [B, Q, Hq, D] bf16, out
  * [B, Q, Hq, D] bf16, causal over the last Q of seq_lens[b] tokens, soft cap, sinks), with keys below
  * keys_quantized[b] (whole 32-token key groups, as eco_kivi_schedule counts them) and values below
- * values_quantized[b] read as codes. Replaces kivi_decode_attention
- * (attention/kivi.py:199-309) and paged_kivi_attention (backends/vllm/kivi/kernels.py:354-415). */
+ * values_quantized[b] read as codes; more than 64 query rows per KV head in query chunks as eco_paged_decode. Replaces
+ * kivi_decode_attention (attention/kivi.py:199-309) and paged_kivi_attention (backends/vllm/kivi/kernels.py:354-415). */
 int eco_kivi_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* blocks, int32_t num_pages,
                     const void* k_ring, const void* v_ring, int32_t ring, const int32_t* keys_quantized,
                     const int32_t* values_quantized, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,

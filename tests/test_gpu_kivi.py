@@ -196,6 +196,8 @@ CASES = [
     (3, 4, 128, 8, 64, [513, 2000, 64], 4),  # GQA 16 x 4 queries = 64 rows at head dim 64
     (4, 2, 16, 2, 128, [40, 1, 160, 385], 2),  # rows shorter than the residual: no codes at all
     (1, 1, 32, 8, 128, [8192], 2),  # one long row cut into many waves' ranges
+    (2, 12, 64, 8, 128, [1300, 400], 4),  # 96 rows per KV head: query chunks of 8 (64 rows) + 4 (32 rows)
+    (2, 5, 128, 4, 64, [700, 150], 2),  # 32 query heads per KV head x 5 queries: chunks of 2, 2, 1
 ]
 
 
@@ -315,10 +317,12 @@ def test_softcap_and_sinks() -> None:
     np.testing.assert_allclose(got, oracle_output(c, scale=0.2, softcap=4.0, sinks=sinks), atol=ATOL, rtol=RTOL)
 
 
-@pytest.mark.parametrize("kind,queries,hq", [("broadcast", 1, 32), ("per_head", 2, 16), ("per_head", 8, 64)])
+@pytest.mark.parametrize("kind,queries,hq", [("broadcast", 1, 32), ("per_head", 2, 16), ("per_head", 8, 64),
+                                             ("per_head", 12, 64)])
 def test_decode_with_a_mask(kind, queries, hq) -> None:
     """An attention mask (key t = token t of the row) hides keys on top of the causal limit, as the reference's
-    kernels take a mask (attention/_kivi_kernels.py:176-183); with 64 query rows the shared-tile instance runs."""
+    kernels take a mask (attention/_kivi_kernels.py:176-183); with 64 query rows the verification kernel runs, with
+    96 two query chunks."""
     from economize_amd.kivi import kivi_decode_attention
 
     lens = [1100, 70, 600]

@@ -51,6 +51,8 @@ CASES = [
     (40, 1, 8, 1, 128, [3 + 97 * i for i in range(40)], torch.float8_e4m3fn),  # many short rows per wave
     (5, 2, 8, 2, 64, [300, 0, 0, 17, 1], torch.bfloat16),  # empty rows between others
     (70, 1, 8, 2, 64, [(37 * i) % 700 for i in range(70)], torch.float8_e4m3fn),  # more than 64 batch rows
+    (2, 6, 64, 4, 128, [300, 90], torch.float8_e4m3fn),  # 96 rows per KV head: query chunks of 4 + 2
+    (2, 12, 16, 2, 64, [500, 40], torch.bfloat16),  # 96 rows per KV head: query chunks of 8 + 4
 ]
 
 
@@ -220,7 +222,8 @@ def test_bad_arguments_raise_before_launch() -> None:
 
 @pytest.mark.parametrize("dtype,kind,queries,hq", [(torch.float8_e4m3fn, "broadcast", 1, 32),
                                                    (torch.bfloat16, "per_head", 2, 16),
-                                                   (torch.float8_e4m3fn, "per_head", 8, 64)])
+                                                   (torch.float8_e4m3fn, "per_head", 8, 64),
+                                                   (torch.float8_e4m3fn, "per_head", 12, 64)])  # query chunks
 def test_decode_with_a_mask(dtype, kind, queries, hq) -> None:
     """An attention mask (key t = token t of the row; bool, broadcast or per head) hides keys on top of the causal
     limit, as the reference's decode_attention takes a mask (attention/decode.py:252-300)."""
