@@ -121,3 +121,43 @@ def test_refusals() -> None:
         decode_attention(q[:, :4], k, k, torch.ones(1, 1, 1, 10, device="cuda"), 1.0)
     with pytest.raises(ConfigError, match="keys"):
         decode_attention(q[:, :4], k, k, torch.ones(1, 1, 1, 11, dtype=torch.bool, device="cuda"), 1.0)
+
+
+def sweep_case(i: int):
+    """Randomized dense decode case ``i``: query and K/V dtypes (fp8 views with or without per-head scales), head dims
+    (D and Dv apart), GQA, query count, key count and mask kind, drawn from a seeded generator on the CPU."""
+    rng = np.random.default_rng(70_000 + i)
+    qdt = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(0, 3))]
+    kvdt = [qdt, qdt, torch.float8_e4m3fn, torch.float8_e5m2][int(rng.integers(0, 4))]
+    d = int(rng.choice([16, 48, 64, 96, 128, 256]))
+    dv = d if rng.random() < 0.8 else int(rng.choice([32, 64, 128]))
+    if kvdt in FP8:  # fp8 rows are multiples of 16 bytes
+        d, dv = max(16, d // 16 * 16), max(16, dv // 16 * 16)
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    groups = int(rng.choice([1, 2, 4, 8]))
+    queries = int(rng.integers(1, 5))
+    keys = int(rng.choice([1, 31, 33, 200, 1000, 2500]))
+    mask_kind = [None, "holes", "per_head", "causal", "empty_row"][int(rng.integers(0, 5))]
+    if mask_kind == "causal" and keys < queries:
+        mask_kind = None
+    scaled = kvdt in FP8 and rng.random() < 0.5
+    return int(rng.integers(1, 4)), groups * hkv, hkv, queries, keys, d, dv, qdt, kvdt, mask_kind, scaled, 80_000 + i
+
+
+SWEEP = [sweep_case(i) for i in range(150)]
+
+
+@pytest.mark.parametrize("case", SWEEP, ids=[f"{i}-b{c[0]}h{c[1]}k{c[2]}q{c[3]}s{c[4]}d{c[5]}v{c[6]}-"
+                                             f"{str(c[7])[6:]}-{str(c[8])[6:]}-{c[9]}" for i, c in enumerate(SWEEP)])
+def test_randomized_sweep(case) -> None:
+    from economize_amd.decode import decode_attention
+
+    batch, hq, hkv, queries, keys, d, dv, qdt, kvdt, mask_kind, scaled, seed = case
+    q, k, v, kf, vf, mask, ks, vs = _case(batch, hq, hkv, queries, keys, d, dv, qdt, kvdt, seed=seed,
+                                          mask_kind=mask_kind, scaled=scaled)
+    m = None if mask is None else torch.from_numpy(mask).cuda()
+    got = decode_attention(q.cuda(), k.cuda(), v.cuda(), m, 1 / np.sqrt(d),
+                           k_scale=None if ks is None else torch.from_numpy(ks).cuda(),
+                           v_scale=None if vs is None else torch.from_numpy(vs).cuda())
+    want = reference_attention(q.float().numpy(), kf, vf, mask, 1 / np.sqrt(d))
+    np.testing.assert_allclose(got.float().cpu().numpy(), want, atol=ATOL, rtol=RTOL)

@@ -280,3 +280,56 @@ def test_gather_gives_the_dense_view(dtype, out) -> None:
     want_v = torch.from_numpy(np.where(held, vd[:, :, :keys], 0)).to(out).float().numpy()
     got_k, got_v = k.float().cpu().numpy(), v.float().cpu().numpy()
     assert np.array_equal(np.where(held, got_k, 0), want_k) and np.array_equal(np.where(held, got_v, 0), want_v)
+
+
+def sweep_case(i: int):
+    """Randomized paged decode case ``i``: cache dtype, head dim, GQA, query count (up to 96 rows per KV head, so
+    query chunks), batch and lengths (empty, shorter than a tile, long), and whether a per-query mask applies, drawn
+    from a seeded generator on the CPU."""
+    rng = np.random.default_rng(50_000 + i)
+    dtype = [torch.float8_e4m3fn, torch.float8_e5m2, torch.bfloat16][int(rng.integers(0, 3))]
+    d = int(rng.choice([64, 128, 256]))
+    hkv = int(rng.choice([1, 2, 4, 8]))
+    groups = int(rng.choice([1, 2, 4, 8, 16]))
+    queries = int(rng.integers(1, 7))
+    batch = int(rng.integers(1, 6))
+    lens = []
+    for _ in range(batch):
+        kind = rng.random()
+        if kind < 0.1:
+            lens.append(0)
+        elif kind < 0.3:
+            lens.append(int(rng.integers(max(queries, 1), 80)))
+        else:
+            lens.append(int(rng.integers(80, 2500)))
+    return batch, queries, groups * hkv, hkv, d, lens, dtype, bool(rng.random() < 0.25), 60_000 + i
+
+
+SWEEP = [sweep_case(i) for i in range(200)]
+
+
+@pytest.mark.parametrize("case", SWEEP, ids=[f"{i}-b{c[0]}q{c[1]}h{c[2]}k{c[3]}d{c[4]}-{str(c[6])[6:]}"
+                                             f"{'-mask' if c[7] else ''}" for i, c in enumerate(SWEEP)])
+def test_randomized_sweep(case) -> None:
+    from oracle.attention import reference_attention
+
+    batch, queries, hq, hkv, d, lens, dtype, masked, seed = case
+    if max(lens) == 0:
+        lens = lens[:-1] + [1]
+    c = make_case(batch, queries, hq, hkv, d, lens, dtype, seed=seed)
+    mask = None
+    if masked:
+        mask = np.random.default_rng(seed + 1).random((batch, hq, queries, max(lens))) < 0.7
+    got = _decode(c, mask=None if mask is None else torch.from_numpy(mask).cuda())
+    if mask is None:
+        want = oracle_output(c)
+    else:
+        kd, vd = c.decoded()
+        smax = max(lens)
+        causal = np.zeros((batch, 1, queries, smax), bool)
+        for b, n in enumerate(lens):
+            for qi in range(queries):
+                causal[b, 0, qi, : max(n - queries + qi + 1, 0)] = True
+        q = to_numpy_f32(c.q).transpose(0, 2, 1, 3)
+        want = reference_attention(q, kd, vd, causal & mask, 1 / np.sqrt(d))
+    np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
