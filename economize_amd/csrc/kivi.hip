@@ -197,18 +197,23 @@ __global__ __launch_bounds__(256) void kivi_quant_values_kernel(KiviQuantParams 
 // ---- attention ----------------------------------------------------------------------------------------------
 
 // A lane's share of one 32-token page: key words of its 8-token key rows, the value word of each 16-channel block
-// (lane (n, g): channel 16 nd + n, tokens 8 g .. 8 g + 7, the P.V MFMA's A operand), key scales and zero points of
-// its channels, value scales and zero points of its 8 tokens per value group.
+// (lane (n, g): channel 16 nd + n, tokens 8 g .. 8 g + 7, the P.V MFMA's A operand) and D / 8 bytes of the page's
+// scales and zero points (8 D contiguous bytes of the page block: key scales, key zero points, value scales, value
+// zero points; lane l holds bytes l D / 8 ..). The 16 lanes of a lane group use the same scales, so the tile's compute
+// writes the 64 lanes' shares to an LDS slot of the wave and each lane reads what it uses from there: four registers
+// per tile buffer instead of sixty-four.
 template <int D, int BITS>
 struct KTile {
     static constexpr int KW = D * BITS / 128;  // words of a lane's key slice (D / 4 channels)
     static constexpr int ND = D / 16;          // value blocks of 16 channels
     static constexpr int KS = D / 32;          // k-steps of an S MFMA (8 channels each per lane)
     static constexpr int VG = D / 32;          // value groups
+    static constexpr int SCALE_BYTES = 8 * D;  // the page's scales and zero points
+    using Share = typename std::conditional<D == 128, uint4, uint2>::type;  // a lane's D / 8 bytes of them
+    static_assert(sizeof(Share) * 64 == SCALE_BYTES, "64 lanes hold the scales");
     uint32_t kc[2][KW];
     uint32_t vc[ND];
-    uint4 ks[KS], kz[KS];
-    uint4 vs[VG], vz[VG];
+    Share sc;
     int page;          // physical page (the same in every lane), -1 for none
     uint32_t mw[4];    // with a mask: bit e = token 8 g + e of the page visible to query row 16 nb + n (nb < NB)
 };
@@ -253,22 +258,14 @@ __device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c,
     constexpr int TPW = 32 / BITS;  // tokens per value word
     const int u = 8 * g / TPW;
     load_words(reinterpret_cast<const uint32_t*>(blk + L.v_codes()) + (u * 16 + n) * T::ND, tile.vc);
-#pragma unroll
-    for (int j = 0; j < T::KS; ++j) {
-        tile.ks[j] = *reinterpret_cast<const uint4*>(blk + L.k_scale() + (g * (D / 4) + 8 * j) * 2);
-        tile.kz[j] = *reinterpret_cast<const uint4*>(blk + L.k_zero() + (g * (D / 4) + 8 * j) * 2);
-    }
-#pragma unroll
-    for (int grp = 0; grp < T::VG; ++grp) {
-        tile.vs[grp] = *reinterpret_cast<const uint4*>(blk + L.v_scale() + (grp * 32 + 8 * g) * 2);
-        tile.vz[grp] = *reinterpret_cast<const uint4*>(blk + L.v_zero() + (grp * 32 + 8 * g) * 2);
-    }
+    static_assert(L.k_zero() == L.k_scale() + 2 * D && L.v_zero() == L.k_scale() + 6 * D, "scales contiguous");
+    tile.sc = *reinterpret_cast<const typename T::Share*>(blk + L.k_scale() + lane * sizeof(typename T::Share));
 }
 
 // The eight values (tokens 8 g .. 8 g + 7 of one channel) of a value word, dequantized as the reference does:
 // bf16(code * scale + zero) with the product and sum in fp32 (one fused multiply-add: the product is exact).
 template <int BITS>
-__device__ __forceinline__ uint4 dequant_values(uint32_t word, int g, uint4 scales, uint4 zeros) {
+__device__ __forceinline__ uint4 dequant_values(uint32_t word, int g, const uint4& scales, const uint4& zeros) {
     const f16x8 sh = __builtin_bit_cast(f16x8, scales);
     const f16x8 zh = __builtin_bit_cast(f16x8, zeros);
     float c8[8];
@@ -315,29 +312,37 @@ constexpr int kivi_wg_waves() {
     return NB == 1 && D <= 128 ? 4 : 1;
 }
 
-// Waves per SIMD: two for the single-buffer instances of one column block (they fit 256 registers); one wave of a
-// SIMD does not overlap its own arithmetic with its outstanding loads, two waves do.
-template <int D, int NB, int NBUF>
+// Waves per SIMD of the one-column-block instances: two with two tile buffers; with one, three where the pieces hold
+// at most 8 query rows and the registers fit (D = 64), else two. One wave of a SIMD does not overlap its own
+// arithmetic with its outstanding loads, more waves do.
+template <int D, int NB, int NBUF, int PR>
 constexpr int kivi_waves_per_simd() {
-    return NB == 1 && D <= 128 && NBUF == 1 ? 2 : 1;
+    return NB == 1 && D <= 128 ? (NBUF == 1 && PR <= 8 && D == 64 ? 3 : 2) : 1;
 }
 
-template <int D, int BITS, int NB, int NBUF>
+// PR: the query rows a piece of the split instances holds (4, 8 or 16; at least the shape's rows): the LDS of a
+// workgroup, and with it the workgroups a CU holds, follows the rows a shape has instead of the MFMA's 16 columns.
+template <int D, int BITS, int NB, int NBUF, int PR>
 __global__ __launch_bounds__((64 * kivi_wg_waves<D, NB>()))
-    __attribute__((amdgpu_waves_per_eu(kivi_waves_per_simd<D, NB, NBUF>()))) void
+    __attribute__((amdgpu_waves_per_eu(kivi_waves_per_simd<D, NB, NBUF, PR>()))) void
 kivi_attention_kernel(KiviParams p) {
     using T = KTile<D, BITS>;
     constexpr int KS = T::KS, ND = T::ND, VG = T::VG;
     constexpr int R = NB * 16;  // query rows of the MFMA columns
     constexpr int WAVES = kivi_wg_waves<D, NB>();
     constexpr bool kSplit = WAVES > 1;  // the range split in quarters, pieces merged in LDS
-    using QRows = uint4[R][D / 8 + 1];             // a wave's current query rows (one word of padding: a row stride of
-                                                   // D / 8 + 1 words puts the 16 rows of a lane group in distinct banks)
+    static_assert(PR == 16 || (kSplit && NB == 1), "pieces of fewer rows only for the split instances");
+    // a wave's current query rows (one word of padding: a row stride of D / 8 + 1 words puts the 16 rows of a lane
+    // group in distinct banks); with pieces of PR < 16 rows, the PR rows and a zero row read by MFMA columns PR .. 15
+    constexpr int QR = PR < 16 ? PR + 1 : R;
+    using QRows = uint4[QR][D / 8 + 1];
 
     const int lane = WAVES > 1 ? static_cast<int>(threadIdx.x) & 63 : static_cast<int>(threadIdx.x);
     const int wave = WAVES > 1 ? uniform(static_cast<int>(threadIdx.x) >> 6) : 0;
     constexpr int row0 = 0;  // the first query row of the wave's columns
-    __shared__ __align__(16) typename std::conditional<kSplit, Pieces<D, WAVES>, char>::type pieces;
+    __shared__ __align__(16) typename std::conditional<kSplit, Pieces<D, WAVES, PR>, char>::type pieces;
+    // the scales and zero points of the tile a wave computes
+    __shared__ __align__(16) uint8_t scale_slots[WAVES][T::SCALE_BYTES];
     QRows* q_rows;
     if constexpr (kSplit) {
         // the query rows live in the data of the wave's second piece, which only the wave's last step writes, after
@@ -351,6 +356,7 @@ kivi_attention_kernel(KiviParams p) {
     auto& q_bf = *q_rows;
     const int n = lane & 15;
     const int g = lane >> 4;
+    const int qn = PR < 16 ? min(n, PR) : n;  // the query row of MFMA column n
     const int w = blockIdx.x;  // workgroup
     const int grid = gridDim.x;
 
@@ -383,7 +389,7 @@ kivi_attention_kernel(KiviParams p) {
     auto begin_row = [&](const Cursor& c) __attribute__((always_inline)) {
         // the row's query rows into LDS (rows past the group are zero); the loads wait here, once per row, outside the
         // tile pipeline
-        for (int i = lane; i < R * (D / 8); i += 64) {
+        for (int i = lane; i < QR * (D / 8); i += 64) {
             const int r = i / (D / 8), k = i % (D / 8);
             uint4 x = make_uint4(0, 0, 0, 0);
             if (row0 + r < p.rows) {
@@ -419,6 +425,10 @@ kivi_attention_kernel(KiviParams p) {
 
     // ---- one tile (32 tokens) of the online softmax ----
     auto compute = [&](const T& tile, const Cursor& c) __attribute__((always_inline)) {
+        // the tile's scales into the wave's slot (the previous tile's reads of it came first: one wave's LDS accesses
+        // are in order)
+        uint8_t* sl = scale_slots[wave];
+        reinterpret_cast<typename T::Share*>(sl)[lane] = tile.sc;
         const int t0 = KPAGE * c.t;
         const bool valid = tile.page >= 0;
         f32x4 s[2][NB];
@@ -432,8 +442,8 @@ kivi_attention_kernel(KiviParams p) {
         if (t0 < kq) {
 #pragma unroll
             for (int j = 0; j < KS; ++j) {
-                const f16x8 sh = __builtin_bit_cast(f16x8, tile.ks[j]);
-                const f16x8 zh = __builtin_bit_cast(f16x8, tile.kz[j]);
+                const f16x8 sh = *reinterpret_cast<const f16x8*>(sl + (g * (D / 4) + 8 * j) * 2);
+                const f16x8 zh = *reinterpret_cast<const f16x8*>(sl + 2 * D + (g * (D / 4) + 8 * j) * 2);
                 float sf[8], zf[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
@@ -452,7 +462,7 @@ kivi_attention_kernel(KiviParams p) {
 #pragma unroll
                     for (int nb = 0; nb < NB; ++nb)
                         s[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                            kv, __builtin_bit_cast(bf16x8, q_bf[nb * 16 + n][g * (D / 32) + j]), s[v][nb], 0,
+                            kv, __builtin_bit_cast(bf16x8, q_bf[nb * 16 + qn][g * (D / 32) + j]), s[v][nb], 0,
                             0, 0);
                 }
             }
@@ -475,7 +485,7 @@ kivi_attention_kernel(KiviParams p) {
                     for (int j = 0; j < KS; ++j)
                         s[v][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                             __builtin_bit_cast(bf16x8, kr[v][j]),
-                            __builtin_bit_cast(bf16x8, q_bf[nb * 16 + n][g * (D / 32) + j]), s[v][nb], 0, 0, 0);
+                            __builtin_bit_cast(bf16x8, q_bf[nb * 16 + qn][g * (D / 32) + j]), s[v][nb], 0, 0, 0);
         }
         // scores in log2 units; masking where the tile holds a row's end, a causal limit or a missing page
 #pragma unroll
@@ -559,7 +569,9 @@ kivi_attention_kernel(KiviParams p) {
                 constexpr bool kFull = decltype(full_tag)::value;
 #pragma unroll
                 for (int nd = 0; nd < ND; ++nd) {
-                    const uint4 v = dequant_values<BITS>(tile.vc[nd], g, tile.vs[nd / 2], tile.vz[nd / 2]);
+                    const int at = ((nd / 2) * 32 + 8 * g) * 2;
+                    const uint4 v = dequant_values<BITS>(tile.vc[nd], g, *reinterpret_cast<const uint4*>(sl + 4 * D + at),
+                                                         *reinterpret_cast<const uint4*>(sl + 6 * D + at));
                     product(nd, kFull ? v : apply_mask(v, mask));
                 }
             };
@@ -700,15 +712,16 @@ kivi_attention_kernel(KiviParams p) {
 
 namespace {
 
-// Tile buffers of the one-column-block instances: 1 (two waves per SIMD, the default: 57 us against 71 us at
-// B=16, L=8192, int2 and int4) or 2 (one wave per SIMD, the next tile's loads in flight); ECO_KIVI_STAGES overrides.
-int kivi_stages() {
-    static const int stages = [] {
+// Tile buffers of the one-column-block instances (ECO_KIVI_STAGES = 1 or 2 overrides): at D = 128 two (the next
+// tile's loads in flight; two waves per SIMD since a tile's scales pass through LDS: int4 63-64 us against 65-67 us
+// with one buffer at B=16, L=8192), at D = 64 one (three waves per SIMD).
+int kivi_stages(int head_dim) {
+    static const int forced = [] {
         const char* env = std::getenv("ECO_KIVI_STAGES");
-        const int v = env ? std::atoi(env) : 1;
-        return v <= 1 ? 1 : 2;
+        const int v = env ? std::atoi(env) : 0;
+        return v <= 0 ? 0 : (v == 1 ? 1 : 2);
     }();
-    return stages;
+    return forced ? forced : (head_dim == 128 ? 2 : 1);
 }
 
 // Column blocks of 16 query rows from which the verification kernel (kivi_verify.hip: two-page tiles shared by four
@@ -724,26 +737,26 @@ int kivi_shared_from() {
 
 // An attention instance: the kernel, its threads per workgroup and the parts a workgroup's tile range is split in
 // (the grid gives every part at least four tiles).
-using KiviKernelFn = decltype(&kivi_attention_kernel<64, 2, 1, 1>);
+using KiviKernelFn = decltype(&kivi_attention_kernel<64, 2, 1, 1, 16>);
 struct KiviInstance {
     KiviKernelFn kernel;
     int threads;
     int parts;
 };
 
-template <int D, int BITS, int NB, int NBUF>
+template <int D, int BITS, int NB, int NBUF, int PR>
 KiviInstance kivi_instance() {
     constexpr int waves = kivi_wg_waves<D, NB>();
-    return {kivi_attention_kernel<D, BITS, NB, NBUF>, 64 * waves, waves};
+    return {kivi_attention_kernel<D, BITS, NB, NBUF, PR>, 64 * waves, waves};
 }
 
-// NB column blocks of query rows below kivi_shared_from(): one block, the split instance (one or two tile buffers);
-// otherwise one wave over NB blocks.
-template <int D, int BITS, int NB>
+// NB column blocks of query rows below kivi_shared_from(): one block, the split instance (one or two tile buffers,
+// pieces of PR rows); otherwise one wave over NB blocks.
+template <int D, int BITS, int NB, int PR>
 KiviInstance kivi_kernel_of() {
     if constexpr (NB == 1)
-        return kivi_stages() == 1 ? kivi_instance<D, BITS, 1, 1>() : kivi_instance<D, BITS, 1, 2>();
-    return kivi_instance<D, BITS, NB, 1>();
+        return kivi_stages(D) == 1 ? kivi_instance<D, BITS, 1, 1, PR>() : kivi_instance<D, BITS, 1, 2, PR>();
+    return kivi_instance<D, BITS, NB, 1, 16>();
 }
 
 template <typename F>
@@ -752,9 +765,13 @@ int kivi_dispatch(int head_dim, int bits, int rows, const F& f) {
     auto by_nb = [&](auto d_tag, auto b_tag) -> int {
         constexpr int D = decltype(d_tag)::value;
         constexpr int BITS = decltype(b_tag)::value;
-        if (nb == 1) return f.template run<D, BITS, 1>();
-        if (nb == 2) return f.template run<D, BITS, 2>();
-        if (nb <= 4) return f.template run<D, BITS, 4>();
+        if (nb == 1) {
+            if (rows <= 4) return f.template run<D, BITS, 1, 4>();
+            if (rows <= 8) return f.template run<D, BITS, 1, 8>();
+            return f.template run<D, BITS, 1, 16>();
+        }
+        if (nb == 2) return f.template run<D, BITS, 2, 16>();
+        if (nb <= 4) return f.template run<D, BITS, 4, 16>();
         return fail("kivi decode attention takes at most 64 query rows per KV head");
     };
     auto by_bits = [&](auto d_tag) -> int {
@@ -770,10 +787,10 @@ int kivi_dispatch(int head_dim, int bits, int rows, const F& f) {
 struct KiviLaunch {
     hipStream_t stream;
     const KiviParams* p;
-    template <int D, int BITS, int NB>
+    template <int D, int BITS, int NB, int PR>
     int run() const {
         if (NB >= kivi_shared_from()) return kivi_verify_attention(*p, stream);
-        const KiviInstance in = kivi_kernel_of<D, BITS, NB>();
+        const KiviInstance in = kivi_kernel_of<D, BITS, NB, PR>();
         hipLaunchKernelGGL(in.kernel, dim3(p->grid), dim3(in.threads), 0, stream, *p);
         return check_launch("kivi_attention_kernel");
     }
@@ -782,14 +799,14 @@ struct KiviLaunch {
 struct KiviOccupancy {
     int* per_cu;
     int* waves;
-    template <int D, int BITS, int NB>
+    template <int D, int BITS, int NB, int PR>
     int run() const {
         if (NB >= kivi_shared_from()) {
             *waves = 2;  // two-page tiles: four tiles per workgroup are eight pages
             return kivi_verify_resident_groups(D, BITS, per_cu);
         }
         int blocks = 0;
-        const KiviInstance in = kivi_kernel_of<D, BITS, NB>();
+        const KiviInstance in = kivi_kernel_of<D, BITS, NB, PR>();
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, in.kernel, in.threads, 0) != hipSuccess ||
             blocks <= 0)
             blocks = 1;

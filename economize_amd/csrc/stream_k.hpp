@@ -363,28 +363,28 @@ __device__ inline void merge_row(const P& p, const Cursor& c, int prev, int64_t 
 
 // ---- the pieces of rows inside one multi-wave workgroup ----------------------------------------------------------
 // Each wave of a workgroup takes a contiguous part of the workgroup's tile range; its first and last row segments
-// that are not whole rows are left in LDS as pieces (maxima, sums and output values of at most 16 query rows). After
+// that are not whole rows are left in LDS as pieces (maxima, sums and output values of at most PR query rows). After
 // a barrier the pieces are merged per row, the rows taken by the waves in turn: a row inside the workgroup's range is
 // written out, a row cut at a range boundary becomes the workgroup's partial in the workspace (slot 0 when the row
 // started before the workgroup, else slot 1) and joins the counter merge of merge_row. The two rows cut at the range's
 // ends go to different waves, so that their workspace round trips (partial stores, counter, the last part's merge)
 // overlap instead of following each other.
-template <int D, int WAVES>
+template <int D, int WAVES, int PR = 16>
 struct Pieces {
-    float data[2 * WAVES][16 * (D + 2)];
+    float data[2 * WAVES][PR * (D + 2)];
     int64_t row[2 * WAVES];  // row_start of the piece's row, -1 for none
     int b[2 * WAVES], kvh[2 * WAVES], tiles[2 * WAVES];
 };
 
-template <int D, int WAVES>
-__device__ inline void clear_pieces(Pieces<D, WAVES>& pc, int wave, int lane) {
+template <int D, int WAVES, int PR>
+__device__ inline void clear_pieces(Pieces<D, WAVES, PR>& pc, int wave, int lane) {
     if (lane < 2) pc.row[2 * wave + lane] = -1;
 }
 
 // Stores the segment of row c as piece k: lane (n, g) holds query row n's output channels 16 nd + 4 g + i
 // (value(nd, i)), and m, l of row n.
-template <int D, int WAVES, typename V>
-__device__ __forceinline__ void write_piece(Pieces<D, WAVES>& pc, int k, const Cursor& c, int rows, int n, int g,
+template <int D, int WAVES, int PR, typename V>
+__device__ __forceinline__ void write_piece(Pieces<D, WAVES, PR>& pc, int k, const Cursor& c, int rows, int n, int g,
                                             int lane, float m, float l, V value) {
     float* piece = pc.data[k];
     if (n < rows) {
@@ -405,8 +405,8 @@ __device__ __forceinline__ void write_piece(Pieces<D, WAVES>& pc, int k, const C
     }
 }
 
-template <int D, int WAVES, typename P>
-__device__ inline void merge_pieces(const P& p, Pieces<D, WAVES>& pc, int wave, int lane, int64_t wlo, int64_t whi,
+template <int D, int WAVES, int PR, typename P>
+__device__ inline void merge_pieces(const P& p, Pieces<D, WAVES, PR>& pc, int wave, int lane, int64_t wlo, int64_t whi,
                                     int64_t total, int grid, int w) {
     __syncthreads();
     const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
