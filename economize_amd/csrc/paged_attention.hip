@@ -427,12 +427,10 @@ paged_attention_kernel(PagedParams p) {
             // Lazy rescaling: the reference maximum m_i moves only when a score exceeds it by more than 2^8, so that
             // the accumulators are rescaled a few times per row instead of at every tile (the weights stay below
             // 2^8, far inside fp16's range; the quotient acc / l does not depend on the reference). The ballot sees
-            // every lane's own maximum; only a rescale needs the maximum over the lane group. The bf16 instance
-            // at D = 256 rescales at every tile: on gfx950 its lazy form (and a form with the scale folded into the
-            // exponent) gave wrong results although the same source is correct in every other instance.
-            constexpr float lazy = FMT == BF16 && D > 128 ? 0.0f : 8.0f;
+            // every lane's own maximum; only a rescale needs the maximum over the lane group.
+            constexpr float lazy = 8.0f;
             if constexpr (kTwoWaves) {
-                if (lazy == 0.0f || __ballot(tile_max > m_i[nb] + lazy || m_i[nb] == -INFINITY) != 0) {
+                if (__ballot(tile_max > m_i[nb] + lazy || m_i[nb] == -INFINITY) != 0) {
                     const bool fresh = m_i[nb] == -INFINITY;
                     const float m_new = fmaxf(m_i[nb], group_max(tile_max));
                     const float alpha = fresh ? 0.0f : __builtin_amdgcn_exp2f(m_i[nb] - m_new);
@@ -443,7 +441,7 @@ paged_attention_kernel(PagedParams p) {
                         for (int i = 0; i < 4; ++i) acc[nd][nb][i] = fresh ? 0.0f : acc[nd][nb][i] * alpha;
                     m_i[nb] = m_new;
                 }
-            } else if (lazy == 0.0f || __ballot(tile_max > m_i[nb] + lazy) != 0) {
+            } else if (__ballot(tile_max > m_i[nb] + lazy) != 0) {
                 const float m_new = fmaxf(m_i[nb], group_max(tile_max));
                 const float alpha = m_i[nb] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_i[nb] - m_new);
                 l_i[nb] *= alpha;
