@@ -239,14 +239,19 @@ __device__ inline void load_words(const uint32_t* src, uint32_t (&dst)[N]) {
     }
 }
 
-// Issues the page loads of the tile under cursor c (the same loads in every lane and for every tile: a tile without
-// a page reads page 0 and masks it).
+// A row's tiles are walked from its last one down (at_tile: position t of the cursor is tile tiles - 1 - t). The
+// row's newest tokens, its bf16 ring tiles (not yet quantized; their loads are issued inside the tile step and
+// waited for at once), then come first, while every wave's pipeline is filling anyway, instead of in the last part
+// of the row, whose workgroup would then also finish last and run the row's merge.
+
+// Issues the page loads of tile c.t of c's row (the same loads in every lane and for every tile: a tile without a
+// page reads page 0 and masks it).
 template <int D, int BITS>
 __device__ __forceinline__ void issue_tile(const KiviParams& p, const Cursor& c, int n, int g, int lane, PageWindow& win,
                                            KTile<D, BITS>& tile) {
     using T = KTile<D, BITS>;
     constexpr KiviLayout L{D, BITS};
-    ensure_window(p, c, lane, win);
+    ensure_window<KiviParams, true>(p, c, lane, win);
     const int phys = __builtin_amdgcn_readlane(win.physical, c.t - win.base);
     tile.page = phys;
     const uint8_t* blk = p.blocks + static_cast<int64_t>(phys >= 0 ? phys : 0) * p.blk_page + c.kvh * p.blk_head;
@@ -429,7 +434,7 @@ kivi_attention_kernel(KiviParams p) {
         // are in order)
         uint8_t* sl = scale_slots[wave];
         reinterpret_cast<typename T::Share*>(sl)[lane] = tile.sc;
-        const int t0 = KPAGE * c.t;
+        const int t0 = KPAGE * at_tile(c).t;
         const bool valid = tile.page >= 0;
         f32x4 s[2][NB];
 #pragma unroll
@@ -660,11 +665,11 @@ kivi_attention_kernel(KiviParams p) {
         Cursor icur = cur;
         int64_t ipos = lo;
         auto issue_next = [&](T& buf, Cursor& slot) __attribute__((always_inline)) {
-            issue_tile<D, BITS>(p, icur, n, g, lane, win, buf);
-            if (p.mask)  // the tile is page icur.t: word icur.t of every query row's mask
+            issue_tile<D, BITS>(p, at_tile(icur), n, g, lane, win, buf);
+            if (p.mask)  // the tile is one page: its word of every query row's mask
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb)
-                    buf.mw[nb] = (mask_word(p, icur.b, icur.kvh, row0 + nb * 16 + n, icur.t) >> (8 * g)) & 0xFFu;
+                    buf.mw[nb] = (mask_word(p, icur.b, icur.kvh, row0 + nb * 16 + n, at_tile(icur).t) >> (8 * g)) & 0xFFu;
             slot = icur;
             if (ipos < hi) {
                 if (ipos + 1 < hi) advance(p, icur, small ? &rt : nullptr);

@@ -220,6 +220,14 @@ __device__ inline void advance(const P& p, Cursor& c, const RowTable* table = nu
     } while (c.row.tiles == 0 && c.b + 1 < p.batch);
 }
 
+// The tile at cursor position c.t of a row walked from its last tile down (position t is tile tiles - 1 - t): the
+// cursor, the ranges and the merges count positions; the loads, token offsets and masks use the tile.
+__device__ inline Cursor at_tile(const Cursor& c) {
+    Cursor t = c;
+    t.t = c.row.tiles - 1 - c.t;
+    return t;
+}
+
 // The wave whose range holds sequence offset x.
 __device__ inline int wave_of(int64_t x, int64_t total, int grid) {
     return static_cast<int>(((x + 1) * grid - 1) / total);
@@ -252,14 +260,15 @@ struct PageWindow {
     int logical = -1, physical = -1;
 };
 
-template <typename P>
+// DESCENDING: the row is walked from its last tile down, so a reload covers the 64 pages that end with the tile.
+template <typename P, bool DESCENDING = false>
 __device__ __forceinline__ void ensure_window(const P& p, const Cursor& c, int lane, PageWindow& win) {
     const int first = P::kTile * c.t;
     if (c.b == win.b && c.kvh == win.kvh && first >= win.base && first + P::kTile <= win.base + 64) return;
     win.b = c.b;
     win.kvh = c.kvh;
-    win.base = first;
-    const int lp = logical_page(p, c.row, c.b, c.kvh, first + lane);
+    win.base = DESCENDING ? max(first + P::kTile - 64, 0) : first;
+    const int lp = logical_page(p, c.row, c.b, c.kvh, win.base + lane);
     int pp = lp >= 0 ? p.block_table[c.b * p.bt_stride + lp] : -1;
     pp = pp < p.num_pages ? pp : -1;  // a table entry outside the cache reads nothing
     win.logical = pp >= 0 ? lp : -1;
