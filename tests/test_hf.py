@@ -15,6 +15,9 @@ from economize_amd.techniques import FP8KVConfig, FusedFP8KVConfig, FusedKIVICon
 def tiny_model(head_dim: int = 64, attn: str = "sdpa", layers: int = 4):
     from transformers import Qwen2Config, Qwen2ForCausalLM
 
+    from economize_amd.attention import install
+
+    install()  # a model built with attn="economize" needs the registration, whatever ran before in this process
     config = Qwen2Config(vocab_size=128, hidden_size=128, intermediate_size=256, num_hidden_layers=layers,
                          num_attention_heads=4, num_key_value_heads=2, head_dim=head_dim, max_position_embeddings=512,
                          tie_word_embeddings=True, initializer_range=0.2, attn_implementation=attn)
