@@ -26,8 +26,14 @@ describes it) selects the same pages whenever the gap at the k-th score exceeds 
 page masks for ``keep``; the invariants of test_quest.py:202-215 (increasing order, ``-1`` padding, every committed
 page when ``done <= pages``). End to end, ``tests/test_golden_reference.py`` decodes the reference's golden model
 with :func:`page_bounds`, :func:`select_pages` and :func:`quest_reference` and gets the reference's own ``kv_quest``
-golden tokens (tests/golden/catalog.py:195-207). The exact fp32 score bits at near-ties are parity unpinned: the
-reference's own bits there depend on the backend's einsum order, so no check can fix them.
+golden tokens (tests/golden/catalog.py:195-207). The reference's own ``select_pages``, run on the CPU, wrote the
+selections of ``tests/golden/quest_select_vectors.npz`` (``tests/test_oracle_quest_vectors.py``): random keys at
+head dims 64 / 128, fp8 keys, four query rows, a planted workload and short rows select exactly its pages. Two cases
+differ by what the definition leaves open: exact ties, where torch's CPU ``topk`` keeps higher-index members of a
+tied group (same scores selected, lower index here), and near ties of about one fp32 unit, where torch's CPU einsum
+rounds 127 of 320 scores differently from the fixed order above (every page the selections disagree on lies within
+the fp32 error bound of the k-th score). The exact fp32 score bits at such near ties are parity unpinned: the
+reference's own bits there follow its backend's einsum order (CPU and GPU differ), so no check can fix them.
 """
 
 from __future__ import annotations

@@ -255,3 +255,26 @@ def test_forced_first_page_matches_the_oracle(shape) -> None:
     assert (want[0, :, 0] == 0).all()
     plain = oquest.select_pages(q, lo, hi, done, npages, pages)
     assert not (plain[0, :, 0] == 0).any()  # the planted page 0 is selected only when forced
+
+
+def _vector_ids():
+    from quest_vectors import load
+
+    return [v.name for v in load()]
+
+
+@pytest.mark.parametrize("name", _vector_ids())
+def test_selection_matches_the_reference_vectors(name) -> None:
+    """The selection kernel on the reference's own CPU selections (``tests/golden/quest_select_vectors.npz``):
+    indices equal the oracle's bit for bit, and the reference's, up to the tie order and the fp32-unit near ties the
+    definition leaves open (``quest_vectors.check_selection``)."""
+    from economize_amd.quest import select_pages
+    from quest_vectors import check_selection, load
+
+    v = next(x for x in load() if x.name == name)
+    bf16 = lambda bits: torch.from_numpy(bits.astype(np.int16)).view(torch.bfloat16).cuda()  # noqa: E731
+    got = select_pages(bf16(v.query_bits), bf16(v.kmin_bits), bf16(v.kmax_bits), torch.from_numpy(v.done).cuda(),
+                       v.max_done, v.pages).cpu().numpy()
+    want = oquest.select_pages(v.query, v.kmin, v.kmax, v.done, v.max_done, v.pages)
+    assert np.array_equal(got, want)
+    check_selection(v, got)
