@@ -375,13 +375,23 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
             vis |= ok ? 1u << e : 0u;
         }
         float tile_max = -INFINITY;
+        // the soft cap tested once per tile, not per score (the compiler keeps a uniform test inside an unrolled loop)
+        if (p.softcap > 0.0f) {
+#pragma unroll
+            for (int v = 0; v < 2; ++v)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s[v][i] = soft_cap_log2(s[v][i] * score_scale, p.softcap, inv_cap);
+        } else {
+#pragma unroll
+            for (int v = 0; v < 2; ++v)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) s[v][i] *= score_scale;
+        }
 #pragma unroll
         for (int v = 0; v < 2; ++v)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                float x = s[v][i] * score_scale;
-                if (p.softcap > 0.0f) x = soft_cap_log2(x, p.softcap, inv_cap);
-                x = (vis >> (4 * v + i)) & 1u ? x : -INFINITY;
+                const float x = (vis >> (4 * v + i)) & 1u ? s[v][i] : -INFINITY;
                 s[v][i] = x;
                 tile_max = max_nan(tile_max, x);
             }

@@ -250,17 +250,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
                         __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(krow + 16 * j)), qreg[j], s[kk][v],
                         0, 0, 0);
             }
-        const float inv_cap = p.softcap > 0.0f ? 1.0f / p.softcap : 0.0f;
+        // the soft cap tested once per tile, not per score (the compiler keeps a uniform test inside an unrolled loop)
+        if (p.softcap > 0.0f) {
+            const float inv_cap = 1.0f / p.softcap;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
+            for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-            for (int v = 0; v < 2; ++v)
+                for (int v = 0; v < 2; ++v)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float x = s[kk][v][i] * score_scale;
-                    if (p.softcap > 0.0f) x = soft_cap_log2(x, p.softcap, inv_cap);
-                    s[kk][v][i] = x;
-                }
+                    for (int i = 0; i < 4; ++i)
+                        s[kk][v][i] = soft_cap_log2(s[kk][v][i] * score_scale, p.softcap, inv_cap);
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int v = 0; v < 2; ++v)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s[kk][v][i] *= score_scale;
+        }
         // masking where the tile holds a row's end, a causal limit, a missing codes page or a mask
         const bool missing = (!page0 && t0 < kq) || (!page1 && t0 + VPAGE < kq);
         if (t0 + VTILE > all_see || missing || p.mask) {
