@@ -429,26 +429,38 @@ def measure_gathered(steps: int, warmup: int, seed: int, batch=32, q_heads=32, k
 
 
 def measure_cells(steps: int, warmup: int, seed: int, batch=16, q_heads=32, kv_heads=8, length=8192, bits=2,
-                  page=32) -> dict:
-    """paged_kivi_attention over vLLM's KIVI cells (bf16 entries, int2, groups of 32): one query per request, the
-    cells' dense entries read once (K and V, bf16), plus queries, outputs and the block table."""
+                  page=32, residual=128) -> dict:
+    """paged_kivi_attention over vLLM's KIVI cells (bf16 entries, groups of 32), one query per request, after
+    quantize_committed at this step's schedule (residual 128): keys below ((L - 1) / R) R and values below L - 1 - R
+    are read through their codes, scales and flags as the reference's kernel reads them, the rest from their dense
+    entries. Algorithmic bytes: per (request, KV head) kq (D bits / 8 + 2 (2 D) / G + 1) + vq (D bits / 8 + 4 D / vg +
+    1) + (2 L - kq - vq) 2 D, plus queries, outputs and the block table."""
     import torch
 
-    from economize_amd.vllm_kivi import cell_layout, paged_kivi_attention
+    from economize_amd.vllm_kivi import cell_layout, paged_kivi_attention, quantize_committed
 
-    d = HEAD_DIM
-    layout = cell_layout(d, torch.bfloat16, bits, 32)
+    d, group = HEAD_DIM, 32
+    layout = cell_layout(d, torch.bfloat16, bits, group)
     per_row = length // page
     pages = batch * per_row
-    nbytes = batch * kv_heads * length * 2 * d * 2 + 2 * batch * q_heads * d * 2 + pages * 4
+    c = length - 1  # tokens committed before the step
+    kq, vq = (c // residual) * residual, max(0, c - residual)
+    per_head = (kq * (d * bits // 8 + 2 * 2 * d // group + 1) + vq * (d * bits // 8 + 2 * 2 * (d // group) + 1)
+                + (2 * length - kq - vq) * 2 * d)
+    nbytes = batch * kv_heads * per_head + 2 * batch * q_heads * d * 2 + pages * 4
     gen = torch.Generator(device="cuda:0").manual_seed(seed)
     table = torch.randperm(pages, generator=gen, device="cuda:0").view(batch, per_row).to(torch.int32)
     q = torch.randn(batch, q_heads, d, generator=gen, device="cuda:0").to(torch.bfloat16)
     qsl = torch.arange(batch + 1, dtype=torch.int32, device="cuda:0")
     seq = torch.full((batch,), length, dtype=torch.int32, device="cuda:0")
     copies = copies_for(nbytes)
-    caches = [torch.randn(pages, kv_heads, page, layout.size // 2, generator=gen, device="cuda:0").to(torch.bfloat16)
-              for _ in range(copies)]
+    caches = []
+    for _ in range(copies):
+        cache = torch.randn(pages, kv_heads, page, layout.size // 2, generator=gen, device="cuda:0").to(torch.bfloat16)
+        cache.view(torch.uint8)[..., layout.off_flag: layout.off_flag + 2] = 0  # every cell full precision
+        quantize_committed(cache, layout, residual, table, qsl, seq, torch.zeros(batch, dtype=torch.int32,
+                                                                                 device="cuda:0"))
+        caches.append(cache)
     out = torch.empty_like(q)
     seconds = time_calls(rotating([lambda c=c: paged_kivi_attention(q, c, layout, table, qsl, seq, 1, length, out=out)
                                    for c in caches]), steps, warmup)
@@ -514,8 +526,9 @@ def measure_next_rows(steps: int, warmup: int, seed: int) -> dict:
          lambda: measure_dense(steps, warmup, seed, torch.float8_e4m3fn)),
         ("gathered_decode", "gathered_decode_attention, B=32 Hq=32 Hkv=8 D=128, half of a 3968-token prompt kept per "
                             "KV head + 128 tail tokens, bf16", lambda: measure_gathered(steps, warmup, seed)),
-        ("kivi_cells_attention", "paged_kivi_attention over vLLM KIVI cells (bf16 entries, int2, G=32), B=16 Hq=32 "
-                                 "Hkv=8 D=128 L=8192, one query per request",
+        ("kivi_cells_attention", "paged_kivi_attention over vLLM KIVI cells (bf16 entries, int2, G=32, R=128, "
+                                 "quantized by quantize_committed), B=16 Hq=32 Hkv=8 D=128 L=8192, one query per "
+                                 "request",
          lambda: measure_cells(steps, warmup, seed)),
         ("quest_graph_step", "Quest decode step with device metadata (append + bounds refresh + selection + "
                              "attention), B=8 Hq=32 Hkv=8 D=128 L=32768, captured graph vs eager",

@@ -990,6 +990,21 @@ int eco_kivi_cells_attention(const void* q, int64_t sq_t, int64_t sq_h, const vo
     p.seq_lens = seq_lens;
     p.query_start_loc = query_start_loc;
     p.causal = 1;
+    // quantized cells through their codes (the reference's kernel reads them so) where the instance exists: bf16
+    // cells of 128 channels, key groups of 32 (one 32-key tile is one group, whose 2 D scales and zero points sit in
+    // the 8 aux slots of its 32 cells); otherwise every key and value from its dense entry, which quantize_committed
+    // left holding the same dequantized numbers. ECO_CELLS_DENSE=1 forces the dense entries.
+    const char* dense_env = std::getenv("ECO_CELLS_DENSE");
+    if (format == BF16 && head_dim == 128 && group == 32 && c.L.key_aux == 8 && c.L.value_group == 32 &&
+        (bits == 2 || bits == 4) && page_size % 32 == 0 && c.L.off_vz == c.L.off_vs + 8 &&
+        !(dense_env && dense_env[0] == '1')) {
+        p.code_bits = bits;
+        p.cell_off_vs = c.L.off_vs;
+        p.cell_off_ka = c.L.off_ka;
+        p.cell_off_kc = c.L.off_kc;
+        p.cell_off_vc = c.L.off_vc;
+        p.cell_off_flag = c.L.off_flag;
+    }
     return dense_attention(p, d.padded_dim, static_cast<hipStream_t>(stream));
 }
 

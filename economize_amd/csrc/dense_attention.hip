@@ -155,8 +155,31 @@ __device__ inline float sink_weight(float m, float l, float sink, float& inv) {
     return a;
 }
 
-template <int DP, int FMT, int QF, bool MASKED>
+// Eight codes of channels c .. c + 7 packed along bytes (channel c + i at bit i BITS of x), as exact floats.
+template <int BITS>
+__device__ __forceinline__ void cell_codes8(uint32_t x, float (&c)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = static_cast<float>((x >> (BITS * i)) & ((1u << BITS) - 1u));
+}
+
+// bf16(code * scale + zero) of eight channels, the product and the sum in fp32 (one fused multiply-add, the product
+// of a code and an fp16 scale being exact), as the reference's _dequant and its .to(DOT_DTYPE).
+__device__ __forceinline__ bf16x8 dequant_cell8(const float (&c)[8], const float (&sc)[8], const float (&zr)[8]) {
+    bf16x8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = static_cast<__bf16>(__builtin_fmaf(c[i], sc[i], zr[i]));
+    return r;
+}
+
+__device__ __forceinline__ uint32_t word_of(uint4 x, int i) {
+    return i == 0 ? x.x : (i == 1 ? x.y : (i == 2 ? x.z : x.w));
+}
+
+// CB: 0, or the code bits of a cells instance that reads quantized keys and values through their codes.
+template <int DP, int FMT, int QF, bool MASKED, int CB = 0>
 __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
+    static_assert(CB == 0 || (DP == 128 && FMT == BF16 && QF == BF16 && !MASKED),
+                  "codes are read for bf16 cells of 128 channels only");
     constexpr int ES = elem_bytes<FMT>();
     constexpr int KS = DP / 32;  // k-steps of the S MFMA
     constexpr int ND = DP / 16;  // value blocks of 16 channels
@@ -174,9 +197,10 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
     // (beyond that the second key set spills at two waves per SIMD).
     constexpr int KEY_VGPRS = 2 * KS * KW * (ES == 1 ? 2 : 4) + (MASKED ? 8 : 0);
     constexpr int LIVE_VGPRS = (kStage ? 4 * CPL : 0) + 2 * KEY_VGPRS + 4 * ND + 4 * KS * (QLO ? 2 : 1);
-    constexpr int NBUF = kStage && LIVE_VGPRS <= 170 ? 2 : 1;
+    constexpr int NBUF = CB != 0 || (kStage && LIVE_VGPRS <= 170) ? 2 : 1;
     static_assert(CHUNKS % 64 == 0, "value tiles of whole lane rounds");
     __shared__ __align__(16) uint8_t vtile[TK * ROW];
+    __shared__ __align__(16) uint8_t auxl[CB != 0 ? 32 * 16 : 16];  // codes: the tile's key scales and zero points
 
     const int lane = static_cast<int>(threadIdx.x);
     const int n = lane & 15, g = lane >> 4;
@@ -236,17 +260,20 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
     const int my_tiles = split < tiles_row ? (tiles_row - 1 - split) / p.splits + 1 : 0;
     auto tile_start = [&](int k) __attribute__((always_inline)) { return (split + k * p.splits) * TK; };
     // cells: a window over this wave's next 64 tile halves (16 keys each), lane l holding the cache byte offset of
-    // the page of half win0 + l; a tile reads its halves' offsets from the window (v_readlane) and reloads the window
-    // every 32 tiles, so that the tile loads need no block-table load of their own
+    // the first cell of half win0 + l (its page's cells of this KV head, plus the half's place in the page: a
+    // multiple of 16 tokens); a tile reads its halves' offsets from the window (v_readlane) and reloads the window
+    // every 32 tiles, so that the tile loads need no block-table load, and no division by the page size, of their
+    // own
     int win0 = -(1 << 30);
     int64_t win_page = 0;
     auto half_offset = [&](int half) __attribute__((always_inline)) -> int64_t {  // half: uniform
         if (half < win0 || half >= win0 + 64) {
             win0 = half;
             const int mine = half + lane;
-            const int lp = min((tile_start(mine >> 1) + (mine & 1) * 16) / p.page_size, p.bt_cols - 1);
+            const int first = tile_start(mine >> 1) + (mine & 1) * 16;
+            const int lp = min(first / p.page_size, p.bt_cols - 1);
             const int page = min(max(p.block_table[static_cast<int64_t>(b) * p.bt_stride + lp], 0), p.num_pages - 1);
-            win_page = page * p.sc_page + kvh * p.sc_head;
+            win_page = page * p.sc_page + kvh * p.sc_head + static_cast<int64_t>(first % p.page_size) * p.sc_token;
             // wait here for the table load (vmcnt(0)), so that the common path, which reloads nothing, does not
             // wait at the branch's join for every load in flight
             __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -256,17 +283,17 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
         const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(win_page) >> 32), at);
         return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
     };
-    // the cache offsets of tile k's two 16-key halves (a tile starts at a multiple of 32 keys and pages hold a
-    // multiple of 16, so each half lies in one page)
-    int64_t cell_half[2] = {0, 0};
+    // the cache offsets of the first cells of tile k's two 16-key halves (a tile starts at a multiple of 32 keys and
+    // pages hold a multiple of 16, so each half lies in one page)
+    int64_t cell_h0 = 0, cell_h1 = 0;  // (two variables, not an array: a lane-dependent index of one goes to scratch)
     auto tile_pages = [&](int k) __attribute__((always_inline)) {
         if (p.cells) {
-            cell_half[0] = half_offset(2 * k);
-            cell_half[1] = p.page_size % 32 == 0 ? cell_half[0] : half_offset(2 * k + 1);
+            cell_h0 = half_offset(2 * k);
+            cell_h1 = p.page_size % 32 == 0 ? cell_h0 + 16 * p.sc_token : half_offset(2 * k + 1);
         }
     };
-    auto cell_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
-        return p.cells + cell_half[(t >> 4) & 1] + static_cast<int64_t>(t % p.page_size) * p.sc_token;
+    auto cell_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {  // t inside the current tile
+        return p.cells + ((t >> 4) & 1 ? cell_h1 : cell_h0) + static_cast<int64_t>(t & 15) * p.sc_token;
     };
     auto key_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
         if (p.cells) return cell_row(t);
@@ -293,10 +320,17 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
 
     // A tile's loads in registers: its values (staged for LDS, one set), its keys (A-row n of S block v is key
     // t0 + 8 (n / 4) + 4 v + n % 4) and, with a mask, the mask bytes of the lane's keys t0 + 8 g + e.
-    uint4 vreg[kStage ? CPL : 1];
+    uint4 vreg[kStage && CB == 0 ? CPL : 1];
+    // codes: the lane's value token (t0 + lane / 2, channels 64 (lane % 2) ..): its codes, its scales and zero points
+    // and its flags; and the key-aux slot of the tile's cell t0 + lane % 32
+    uint4 vcw[CB == 4 ? 2 : 1], vsz, vaux;
+    uint32_t vfl = 0;
     struct Keys {
-        uint4 k[2][KS][KW];
+        uint4 k[CB != 0 ? 1 : 2][CB != 0 ? 1 : KS][KW];
         uint32_t m[MASKED ? 8 : 1];
+        uint32_t kc[2][CB != 0 ? KS : 1];  // codes: the code word of the lane's channels 32 j + 8 g .. of its key v
+        uint32_t kf[2];                    // codes: the flag byte of its key v
+        int64_t h0, h1;                    // codes: the tile's half offsets (the next tile's issue moves cell_h*)
     };
     // Every load is issued unconditionally at a clamped address (a key past the split reads the split's last key, a
     // channel past the dims reads channel 0) and what it must not contribute is zeroed where it is used: every path
@@ -305,6 +339,27 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
     auto issue = [&](Keys& K, int k) __attribute__((always_inline)) {
         const int t0 = tile_start(k);
         tile_pages(k);
+        if constexpr (CB != 0) {
+            K.h0 = cell_h0;
+            K.h1 = cell_h1;
+            const uint8_t* vc = cell_row(min(t0 + (lane >> 1), t_end - 1));
+#pragma unroll
+            for (int i = 0; i < (CB == 4 ? 2 : 1); ++i)
+                vcw[i] = *reinterpret_cast<const uint4*>(vc + p.cell_off_vc + 16 * (CB / 2) * (lane & 1) + 16 * i);
+            vsz = *reinterpret_cast<const uint4*>(vc + p.cell_off_vs);
+            vfl = *(vc + p.cell_off_flag + 1);
+            vaux = *reinterpret_cast<const uint4*>(cell_row(min(t0 + (lane & 31), t_end - 1)) + p.cell_off_ka);
+#pragma unroll
+            for (int v = 0; v < 2; ++v) {
+                const uint8_t* krow = cell_row(min(t0 + 8 * (n >> 2) + 4 * v + (n & 3), t_end - 1));
+                K.kf[v] = *(krow + p.cell_off_flag);
+#pragma unroll
+                for (int j = 0; j < KS; ++j)
+                    K.kc[v][j] = *reinterpret_cast<const uint32_t*>(
+                        krow + p.cell_off_kc + (CB == 2 ? 4 * (2 * j + (g >> 1)) : 16 * j + 4 * g));
+            }
+            return;
+        }
         if constexpr (MASKED)
 #pragma unroll
             for (int e = 0; e < 8; ++e) K.m[e] = mrow[mask_col(min(t0 + 8 * g + e, t_end - 1)) * p.sm_s];
@@ -328,6 +383,47 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
     };
     // ---- the tile's values into LDS (zero past the keys and past Dv); the previous tile's reads of LDS came first ----
     auto stage = [&](int t0) __attribute__((always_inline)) {
+        if constexpr (CB != 0) {
+            if (lane < 32) *reinterpret_cast<uint4*>(auxl + 16 * lane) = vaux;
+            const int tl = lane >> 1, hh = lane & 1;
+            const int t = t0 + tl;
+            const bool vok = t < t_end;
+            const f16x8 sz = __builtin_bit_cast(f16x8, vsz);  // the token's scales [4] then zero points [4]
+            uint4 out[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {  // channels 64 hh + 8 q .., value group 2 hh + q / 4
+                // (selects, not an index by the lane's half: a vector indexed at run time goes to scratch)
+                const float sc = static_cast<float>(hh ? sz[2 + q / 4] : sz[q / 4]);
+                const float zr = static_cast<float>(hh ? sz[6 + q / 4] : sz[4 + q / 4]);
+                const uint32_t x = CB == 2 ? (word_of(vcw[0], q >> 1) >> (16 * (q & 1))) & 0xFFFFu
+                                           : word_of(vcw[CB == 4 ? (q >> 2) : 0], q & 3);
+                float c[8], scs[8], zrs[8];
+                cell_codes8<CB>(x, c);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    scs[i] = sc;
+                    zrs[i] = zr;
+                }
+                out[q] = __builtin_bit_cast(uint4, dequant_cell8(c, scs, zrs));
+            }
+            uint8_t* dst = vtile + tl * ROW + 128 * hh;
+            const bool dense = vok && vfl != 1u;  // a cell not quantized: its dense entry
+            if (__ballot(dense) != 0) {  // (the loads and their uses stay inside this rare branch)
+                if (dense) {
+                    const uint8_t* row = cell_row(t) + p.cell_off_v + 128 * hh;
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) out[q] = *reinterpret_cast<const uint4*>(row + 16 * q);
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    *reinterpret_cast<uint4*>(dst + 16 * q) = vok ? out[q] : make_uint4(0, 0, 0, 0);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 8; ++q)
+                    *reinterpret_cast<uint4*>(dst + 16 * q) = vok ? out[q] : make_uint4(0, 0, 0, 0);
+            }
+            return;
+        }
         if constexpr (kStage) {
 #pragma unroll
             for (int i = 0; i < CPL; ++i) {
@@ -349,6 +445,45 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
     auto compute = [&](const Keys& K, int t0) __attribute__((always_inline)) {
         // ---- S^T = K Q^T (key channels past the head dim zeroed) ----
         f32x4 s[2];
+        if constexpr (CB != 0) {
+            // the lane's key scales and zero points (channels 32 j + 8 g ..: entries of the group's aux in the slots
+            // of cells 4 j + g and 16 + 4 j + g), then the keys from their codes, or their dense entries where the
+            // flag is not 1 (a rare branch that keeps its loads and their uses to itself)
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the aux stores of this tile (one wave: in order)
+            auto scores = [&](bool dense) __attribute__((always_inline)) {
+#pragma unroll
+                for (int v = 0; v < 2; ++v) s[v] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < KS; ++j) {
+                    const f16x8 sj = *reinterpret_cast<const f16x8*>(auxl + 16 * (4 * j + g));
+                    const f16x8 zj = *reinterpret_cast<const f16x8*>(auxl + 16 * (16 + 4 * j + g));
+                    float scs[8], zrs[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        scs[i] = static_cast<float>(sj[i]);
+                        zrs[i] = static_cast<float>(zj[i]);
+                    }
+#pragma unroll
+                    for (int v = 0; v < 2; ++v) {
+                        const uint32_t x = CB == 2 ? (K.kc[v][j] >> (16 * (g & 1))) & 0xFFFFu : K.kc[v][j];
+                        float c[8];
+                        cell_codes8<CB>(x, c);
+                        bf16x8 kh = dequant_cell8(c, scs, zrs);
+                        if (dense && K.kf[v] != 1u) {
+                            const int tk = min(t0 + 8 * (n >> 2) + 4 * v + (n & 3), t_end - 1);
+                            const uint8_t* row = p.cells + ((tk >> 4) & 1 ? K.h1 : K.h0) +
+                                                 static_cast<int64_t>(tk & 15) * p.sc_token;
+                            kh = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(row + 2 * (32 * j + 8 * g)));
+                        }
+                        s[v] = mfma(kh, qh[j], s[v]);
+                    }
+                }
+            };
+            if (__ballot(K.kf[0] != 1u || K.kf[1] != 1u) != 0)
+                scores(true);
+            else
+                scores(false);
+        } else
 #pragma unroll
         for (int v = 0; v < 2; ++v) {
             s[v] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -565,6 +700,19 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
 template <int DP, int FMT, int QF>
 int launch_dense(const DenseParams& p, hipStream_t stream) {
     const int programs = p.batch * p.kv_heads * p.m_tiles;
+    if constexpr (DP == 128 && FMT == BF16 && QF == BF16) {
+        if (p.code_bits == 2 && !p.mask) {
+            hipLaunchKernelGGL((dense_split_kernel<DP, FMT, QF, false, 2>), dim3(programs, p.splits), dim3(64), 0,
+                               stream, p);
+            return check_launch("dense_split_kernel");
+        }
+        if (p.code_bits == 4 && !p.mask) {
+            hipLaunchKernelGGL((dense_split_kernel<DP, FMT, QF, false, 4>), dim3(programs, p.splits), dim3(64), 0,
+                               stream, p);
+            return check_launch("dense_split_kernel");
+        }
+    }
+    if (p.code_bits) return fail("decode: codes are read for bf16 cells of 128 channels without a mask only");
     if (p.mask)
         hipLaunchKernelGGL((dense_split_kernel<DP, FMT, QF, true>), dim3(programs, p.splits), dim3(64), 0, stream, p);
     else

@@ -52,6 +52,13 @@ struct DenseParams {
     int64_t bt_stride;
     int bt_cols;
     const int32_t* seq_lens;
+    // Cells read through their codes (code_bits 2 or 4; bf16 cells of 128 channels, key groups of 32 tokens, eight
+    // key-aux slots per cell): a key or value whose cell flag is 1 is dequantized from the cell's codes (byte offsets
+    // cell_off_kc / cell_off_vc, channels packed along the bytes), its value scales and zero points (cell_off_vs: the
+    // token's fp16 scales, then its zero points) and its group's key scales and zero points (cell_off_ka: entry e of
+    // the group's 2 D in the cell of the group's token e / 8), as the reference's kernel does; any other flag reads
+    // the dense entry. code_bits 0: every key and value from its dense entry.
+    int code_bits, cell_off_vs, cell_off_ka, cell_off_kc, cell_off_vc, cell_off_flag;
     // Varlen queries (query_start_loc non-null): query row qi of row b is token query_start_loc[b] + qi (strides sq_q,
     // so_q; sq_b, so_b unused), rows qi >= that row's query count are inactive. causal: key t is visible to query row
     // qi when t < keys_b - queries_b + qi + 1 (on top of the mask).

@@ -162,3 +162,64 @@ def test_attention_over_the_cells_matches_the_oracle(dtype, bits, group, head, q
         want = reference_attention(qb, k[None], v[None], mask, 0.1, 30.0 if sinks is not None else None,
                                    None if sinks is None else sinks.numpy())[0]
         np.testing.assert_allclose(out[qsl[b]: qsl[b + 1]], want, atol=2e-3, rtol=1e-2, err_msg=f"request {b}")
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_attention_reads_the_codes_of_quantized_cells(bits) -> None:
+    """bf16 cells of 128 channels in key groups of 32 are attended through their codes wherever a flag is 1, as the
+    reference's kernel reads them (kernels.py:274-296): with the dense entries of every quantized cell poisoned (NaN)
+    the output still equals the oracle's read_cells definition. A group flagged as overflowed (2) and a cell whose
+    flags were cleared (0), both holding their full-precision dense entries, are read from those entries."""
+    from economize_amd.vllm_kivi import paged_kivi_attention
+    from oracle.attention import reference_attention
+
+    dtype, group, head, q_heads, page = torch.bfloat16, 32, 128, 8, 32
+    residual = 2 * group
+    lens = [9 * group + 7, 4 * group + 1, 6 * group, 3 * group + 3, 20 * group + 5]
+    qlens = [1, 4, 2, 3, 1]
+    layout, cache, table, states = setup(dtype, bits, group, head, page, lens, seed=40 + bits)
+    gpu = cache.cuda()
+    run(gpu, layout, residual, table, qlens, lens, [0] * len(lens))
+    u8 = gpu.view(torch.uint8).cpu().numpy().copy()
+    nan = np.array([0x7FC0], np.uint16).view(np.uint8)  # bf16 quiet NaN, little-endian bytes
+    kflag = u8[..., layout.off_flag]
+    vflag = u8[..., layout.off_flag + 1]
+    assert (kflag == oc.FLAG_PACKED).sum() > 0 and (vflag == oc.FLAG_PACKED).sum() > 0
+    k_entries = u8[..., : layout.off_v].reshape(*u8.shape[:3], head, 2)
+    v_entries = u8[..., layout.off_v: layout.off_vs].reshape(*u8.shape[:3], head, 2)
+    k_entries[kflag == oc.FLAG_PACKED] = nan
+    v_entries[vflag == oc.FLAG_PACKED] = nan
+    u8[..., : layout.off_v] = k_entries.reshape(*u8.shape[:3], -1)
+    u8[..., layout.off_v: layout.off_vs] = v_entries.reshape(*u8.shape[:3], -1)
+
+    def restore(b, h, t, key_flag, value_flag):
+        cell = u8[int(table[b, t // page]), h, t % page]
+        k, v = states[b]
+        cell[: layout.off_v] = k[h, t].contiguous().view(torch.uint8).numpy()
+        cell[layout.off_v: layout.off_vs] = v[h, t].contiguous().view(torch.uint8).numpy()
+        cell[layout.off_flag] = key_flag
+        cell[layout.off_flag + 1] = value_flag
+
+    for t in range(group, 2 * group):  # request 0, KV head 0: key group 1 as overflowed
+        restore(0, 0, t, oc.FLAG_OVERFLOW, u8[int(table[0, t // page]), 0, t % page, layout.off_flag + 1])
+        if u8[int(table[0, t // page]), 0, t % page, layout.off_flag + 1] == oc.FLAG_PACKED:
+            cell = u8[int(table[0, t // page]), 0, t % page]
+            cell[layout.off_v: layout.off_vs] = np.tile(nan, head)
+    restore(4, 1, 70, 0, 0)  # request 4, KV head 1: a cleared cell inside a quantized group
+    gpu = torch.from_numpy(u8).view(dtype).cuda()
+
+    gen = torch.Generator().manual_seed(bits)
+    query = torch.randn(sum(qlens), q_heads, head, generator=gen).to(dtype)
+    qsl = torch.tensor(np.concatenate([[0], np.cumsum(qlens)]), dtype=torch.int32)
+    out = paged_kivi_attention(query.cuda(), gpu, layout, table.cuda(), qsl.cuda(),
+                               torch.tensor(lens, dtype=torch.int32).cuda(), max(qlens), max(lens),
+                               scale=head ** -0.5).float().cpu().numpy()
+    assert np.isfinite(out).all()
+    for b, (n, q) in enumerate(zip(lens, qlens)):
+        k, v = oc.read_cells(gathered_cells(u8, table, b, n, page, layout), layout, NAMES[dtype])
+        mask = np.zeros((1, 1, q, n), bool)
+        for i in range(q):
+            mask[..., i, : n - q + i + 1] = True
+        qb = query[qsl[b]: qsl[b + 1]].float().numpy().transpose(1, 0, 2)[None]
+        want = reference_attention(qb, k[None], v[None], mask, head ** -0.5)[0]
+        np.testing.assert_allclose(out[qsl[b]: qsl[b + 1]], want, atol=2e-3, rtol=1e-2, err_msg=f"request {b}")
