@@ -994,10 +994,12 @@ int eco_kivi_cells_attention(const void* q, int64_t sq_t, int64_t sq_h, const vo
     // cells of 128 channels, key groups of 32 (one 32-key tile is one group, whose 2 D scales and zero points sit in
     // the 8 aux slots of its 32 cells); otherwise every key and value from its dense entry, which quantize_committed
     // left holding the same dequantized numbers. ECO_CELLS_DENSE=1 forces the dense entries.
-    const char* dense_env = std::getenv("ECO_CELLS_DENSE");
+    static const bool force_dense = [] {
+        const char* env = std::getenv("ECO_CELLS_DENSE");
+        return env && env[0] == '1';
+    }();
     if (format == BF16 && head_dim == 128 && group == 32 && c.L.key_aux == 8 && c.L.value_group == 32 &&
-        (bits == 2 || bits == 4) && page_size % 32 == 0 && c.L.off_vz == c.L.off_vs + 8 &&
-        !(dense_env && dense_env[0] == '1')) {
+        (bits == 2 || bits == 4) && page_size % 32 == 0 && c.L.off_vz == c.L.off_vs + 8 && !force_dense) {
         p.code_bits = bits;
         p.cell_off_vs = c.L.off_vs;
         p.cell_off_ka = c.L.off_ka;
