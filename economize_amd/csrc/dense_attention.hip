@@ -155,11 +155,34 @@ __device__ inline float sink_weight(float m, float l, float sink, float& inv) {
     return a;
 }
 
-// Eight codes of channels c .. c + 7 packed along bytes (channel c + i at bit i BITS of x), as exact floats.
+// Eight codes of channels c .. c + 7 packed along bytes (channel c + i at bit i BITS of x), as exact floats. The
+// codes are spread one per byte (even channels in lo, odd ones in hi); a code below 16 in a byte is the e4m3 pattern
+// of code 2^-9, which v_cvt_scalef32_pk_f32_fp8 with scale 2^9 turns into the exact float, two bytes at a time.
 template <int BITS>
 __device__ __forceinline__ void cell_codes8(uint32_t x, float (&c)[8]) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) c[i] = static_cast<float>((x >> (BITS * i)) & ((1u << BITS) - 1u));
+    uint32_t lo, hi;
+    if constexpr (BITS == 4) {  // nibbles: channel i at bit 4 i
+        lo = x & 0x0F0F0F0Fu;          // channels 0, 2, 4, 6
+        hi = (x >> 4) & 0x0F0F0F0Fu;   // channels 1, 3, 5, 7
+    } else {  // 2-bit fields of the low 16 bits: channel i at bit 2 i
+        const uint32_t u = __builtin_amdgcn_perm(0u, x, 0x0C010C00u);  // bytes: x.byte0, 0, x.byte1, 0
+        const uint32_t v = (u | (u << 4)) & 0x0F0F0F0Fu;                // bytes: channels 0-1, 2-3, 4-5, 6-7
+        lo = v & 0x03030303u;          // channels 0, 2, 4, 6
+        hi = (v >> 2) & 0x03030303u;   // channels 1, 3, 5, 7
+    }
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f32x2 l0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, 512.0f, false);
+    const f32x2 l1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, 512.0f, true);
+    const f32x2 h0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 512.0f, false);
+    const f32x2 h1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 512.0f, true);
+    c[0] = l0.x;
+    c[2] = l0.y;
+    c[4] = l1.x;
+    c[6] = l1.y;
+    c[1] = h0.x;
+    c[3] = h0.y;
+    c[5] = h1.x;
+    c[7] = h1.y;
 }
 
 // bf16(code * scale + zero) of eight channels, the product and the sum in fp32 (one fused multiply-add, the product
@@ -457,18 +480,16 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
                 for (int j = 0; j < KS; ++j) {
                     const f16x8 sj = *reinterpret_cast<const f16x8*>(auxl + 16 * (4 * j + g));
                     const f16x8 zj = *reinterpret_cast<const f16x8*>(auxl + 16 * (16 + 4 * j + g));
-                    float scs[8], zrs[8];
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) {
-                        scs[i] = static_cast<float>(sj[i]);
-                        zrs[i] = static_cast<float>(zj[i]);
-                    }
 #pragma unroll
                     for (int v = 0; v < 2; ++v) {
                         const uint32_t x = CB == 2 ? (K.kc[v][j] >> (16 * (g & 1))) & 0xFFFFu : K.kc[v][j];
                         float c[8];
                         cell_codes8<CB>(x, c);
-                        bf16x8 kh = dequant_cell8(c, scs, zrs);
+                        bf16x8 kh;  // (the fp16 scales widened inside each product: v_fma_mix_f32)
+#pragma unroll
+                        for (int i = 0; i < 8; ++i)
+                            kh[i] = static_cast<__bf16>(
+                                __builtin_fmaf(c[i], static_cast<float>(sj[i]), static_cast<float>(zj[i])));
                         if (dense && K.kf[v] != 1u) {
                             const int tk = min(t0 + 8 * (n >> 2) + 4 * v + (n & 3), t_end - 1);
                             const uint8_t* row = p.cells + ((tk >> 4) & 1 ? K.h1 : K.h0) +
