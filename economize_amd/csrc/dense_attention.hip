@@ -580,11 +580,17 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
         for (int nd = 0; nd < ND; ++nd) {
             const int c = 16 * nd + n;
             if (16 * nd >= p.value_dim) break;
-            float x[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) x[e] = elem_f32<FMT>(vtile + (8 * g + e) * ROW + c * ES);
             bf16x8 vh, vl;
-            split8(x, vh, vl);
+            if constexpr (FMT == BF16) {  // the staged bits are the operand (no widening and rounding back)
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    vh[e] = __builtin_bit_cast(__bf16, *reinterpret_cast<const uint16_t*>(vtile + (8 * g + e) * ROW + c * 2));
+            } else {
+                float x[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) x[e] = elem_f32<FMT>(vtile + (8 * g + e) * ROW + c * ES);
+                split8(x, vh, vl);
+            }
             acc[nd] = mfma(vh, ph, acc[nd]);
             acc[nd] = mfma(vh, pl, acc[nd]);
             if constexpr (KLO) acc[nd] = mfma(vl, ph, acc[nd]);
