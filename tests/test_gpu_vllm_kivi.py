@@ -129,14 +129,15 @@ def gathered_cells(cache_u8: np.ndarray, table, b: int, n: int, page: int, layou
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("bits,group,head,q_heads", [(2, 32, 128, 8), (4, 16, 64, 4)])
-def test_attention_over_the_cells_matches_the_oracle(dtype, bits, group, head, q_heads) -> None:
+@pytest.mark.parametrize("bits,group,head,q_heads,page", [(2, 32, 128, 8, 32), (4, 16, 64, 4, 32), (4, 16, 64, 4, 16)])
+def test_attention_over_the_cells_matches_the_oracle(dtype, bits, group, head, q_heads, page) -> None:
     """vLLM's varlen queries (1, 4, 0 and 3 of them, ragged lengths) attend causally over their request's cells
-    after quantize_committed; the oracle reads the cells back (read_cells) and applies the fp32 definition."""
+    after quantize_committed; the oracle reads the cells back (read_cells) and applies the fp32 definition. Pages of
+    16 tokens put a 32-key tile's two halves in different pages."""
     from economize_amd.vllm_kivi import paged_kivi_attention
     from oracle.attention import reference_attention
 
-    page, residual = 32, 2 * group
+    residual = 2 * group
     lens = [9 * group + 7, 4 * group + 1, 6 * group, 3 * group + 3]
     qlens = [1, 4, 0, 3]
     layout, cache, table, _ = setup(dtype, bits, group, head, page, lens, seed=bits + head)
