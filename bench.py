@@ -298,7 +298,7 @@ def quest_workload(seed: int, batch: int, q_heads: int, kv_heads: int, length: i
     import torch
 
     from economize_amd.paged import PagedKVCache, paged_append
-    from economize_amd.quest import QuestPages, page_bounds
+    from economize_amd.quest import QuestPages, paged_page_bounds
 
     device = torch.device("cuda:0")
     gen = torch.Generator(device=device).manual_seed(seed)
@@ -319,7 +319,7 @@ def quest_workload(seed: int, batch: int, q_heads: int, kv_heads: int, length: i
         slots = (table[b, t // PAGE] * PAGE + t % PAGE).to(torch.int32)
         paged_append(cache, k.to(torch.bfloat16), v.to(torch.bfloat16), slots)
     done = (length - 1) // PAGE
-    kmin, kmax = page_bounds(cache, table, 0, done, PAGE)
+    kmin, kmax = paged_page_bounds(cache, table, 0, done, PAGE)
     pages = budget // PAGE - 1
     qp = QuestPages(kmin, kmax, torch.full((batch,), done, dtype=torch.int32, device=device), done, done, PAGE, pages)
     seq = torch.full((batch,), length, dtype=torch.int32, device=device)
@@ -332,7 +332,7 @@ def measure_quest(steps: int, warmup: int, seed: int, batch=8, q_heads=32, kv_he
     dense tail, over the workload of quest_workload."""
     import torch
 
-    from economize_amd.quest import quest_decode_attention
+    from economize_amd.quest import paged_quest_decode_attention
 
     d = HEAD_DIM
     done = (length - 1) // PAGE
@@ -348,7 +348,7 @@ def measure_quest(steps: int, warmup: int, seed: int, batch=8, q_heads=32, kv_he
 
     def call_on(load):
         c, pages_ = load
-        return lambda: quest_decode_attention(query, c, table, seq, length, pages_, out=out)
+        return lambda: paged_quest_decode_attention(query, c, table, seq, length, pages_, out=out)
 
     seconds = time_calls(rotating([call_on(load) for load in loads]), steps, warmup)
     torch.cuda.synchronize()
@@ -471,13 +471,12 @@ def measure_cells(steps: int, warmup: int, seed: int, batch=16, q_heads=32, kv_h
 
 def measure_quest_graph(steps: int, warmup: int, seed: int, batch=8, q_heads=32, kv_heads=8, length=32768,
                         budget=1024) -> dict:
-    """A Quest decode step with its metadata on the device (QuestState): one appended token per row, the bounds
-    refresh, the selection with a static max_done and the page-list attention, captured once in a HIP graph and
-    replayed, against the same step launched eagerly."""
+    """A Quest decode step with its metadata on the device (QuestState): one appended token per row with the bounds
+    refresh in the same launch (eco_paged_append_quest), the selection with a static max_done and the page-list
+    attention, captured once in a HIP graph and replayed, against the same step launched eagerly."""
     import torch
 
-    from economize_amd.paged import paged_append
-    from economize_amd.quest import QuestState, quest_decode_attention
+    from economize_amd.quest import QuestState, paged_quest_decode_attention
 
     d = HEAD_DIM
     query, cache, table, seq, qp = quest_workload(seed, batch, q_heads, kv_heads, length, budget, 32)
@@ -491,9 +490,8 @@ def measure_quest_graph(steps: int, warmup: int, seed: int, batch=8, q_heads=32,
     handle = state.pages_handle()
 
     def step() -> None:
-        paged_append(cache, k_new, k_new, slots)
-        state.refresh(cache, table, committed)
-        quest_decode_attention(query, cache, table, seq, length, handle, out=out)  # static: the capacity
+        state.append(cache, k_new, k_new, slots, table, committed)
+        paged_quest_decode_attention(query, cache, table, seq, length, handle, out=out)  # static: the capacity
 
     eager = time_calls(step, steps, warmup)
     side = torch.cuda.Stream()
@@ -530,8 +528,8 @@ def measure_next_rows(steps: int, warmup: int, seed: int) -> dict:
                                  "quantized by quantize_committed), B=16 Hq=32 Hkv=8 D=128 L=8192, one query per "
                                  "request",
          lambda: measure_cells(steps, warmup, seed)),
-        ("quest_graph_step", "Quest decode step with device metadata (append + bounds refresh + selection + "
-                             "attention), B=8 Hq=32 Hkv=8 D=128 L=32768, captured graph vs eager",
+        ("quest_graph_step", "Quest decode step with device metadata (append with the bounds refresh in one launch "
+                             "+ selection + attention), B=8 Hq=32 Hkv=8 D=128 L=32768, captured graph vs eager",
          lambda: measure_quest_graph(steps, warmup, seed)),
     ):
         rows[name] = {"workload": workload, **fn()}

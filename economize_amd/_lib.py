@@ -37,6 +37,8 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
     "eco_last_error": (ctypes.c_char_p, []),
     "eco_abi_version": (c_int32, []),
     "eco_paged_append": (c_int32, [_P, _P, _I, _L, _L, _L, _L, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P, _P]),
+    "eco_paged_append_quest": (c_int32, [_P, _P, _I, _L, _L, _L, _L, _P, _I, _P, _P, _I, _I, _I, _I, _I, _P, _P,
+                                         _P, _L, _I, _P, _P, _P, _P, _I, _P, _P, _L, _L, _L, _I, _I, _P]),
     "eco_fp8_encode": (c_int32, [_P, _I, _L, _L, _L, _P, _I, _L, _L, _L, _I, _I, _I, _I, _P, _P, _L, _L, _L, _P]),
     "eco_kv_head_absmax": (c_int32, [_P, _I, _I, _I, _I, _I, _L, _L, _L, _L, _P, _P]),
     "eco_fp8_scales_from_absmax": (c_int32, [_P, _I, _I, _P, _P]),
@@ -75,8 +77,14 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
                                   _I, _I, _I, _I, _I, _I, _F, _F] + _MASK + [_P, _S, _P]),
     "eco_quest_refresh_bounds": (c_int32, [_P, _I, _I, _P, _L, _I, _P, _P, _P, _I, _P, _P, _L, _L, _L, _I, _I, _I, _I,
                                            _I, _P]),
-    "eco_quest_select": (c_int32, [_P, _L, _L, _L, _P, _P, _L, _L, _L, _P, _I, _I, _I, _P, _I, _I, _I, _I, _I, _P,
-                                   _S, _P]),
+    "eco_quest_select": (c_int32, [_P, _I, _L, _L, _L, _P, _P, _I, _L, _L, _L, _P, _I, _I, _I, _P, _I, _I, _I, _I, _I,
+                                   _P, _S, _P]),
+    "eco_quest_dense_bounds": (c_int32, [_P, _I, _L, _L, _L, _I, _I, _I, _I, _P, _P, _I, _L, _L, _L, _I, _I, _I, _P]),
+    "eco_quest_decode_workspace_size": (c_size_t, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _I]),
+    "eco_quest_decode": (c_int32, [_P, _I, _L, _L, _L, _P, _P, _I, _L, _L, _L, _L, _L, _L, _P, _P,  # q .. scales
+                                   _P, _L, _L, _I, _P, _I, _I,  # index, pages, done, page size, min_done
+                                   _P, _L, _L, _L, _L, _P, _P, _L, _L, _L,  # mask, sinks, out
+                                   _I, _I, _I, _I, _I, _I, _I, _F, _F, _P, _S, _P]),
 }
 
 _lib: ctypes.CDLL | None = None

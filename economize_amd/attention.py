@@ -13,11 +13,13 @@ reasons, ``kernel_calls`` / ``kernel_usage`` / ``usage_summary``, the registrati
 * Dense K/V (bf16 / fp16 / fp32, or fp8 views of an fp8 cache) attend on the dense decode kernel
   (:func:`economize_amd.decode.decode_attention`, path ``"kernel"``); with a :class:`~economize_amd.gathered.GatheredKV`
   attached (an eviction's compacted prompt entries), over the compact entries and the dense tail (path
-  ``"kernel_gathered"``).
+  ``"kernel_gathered"``); with :class:`~economize_amd.quest.QuestPages` attached, over the selected pages and the
+  dense tail (path ``"kernel_quest"``).
 * Everything else falls back per call to transformers' ``sdpa`` (a paged cache's K/V materialized by the gather
-  kernels first, fp8 K/V upcast to the query's dtype), or to the model's eager function when the call has sinks or
-  asks for the weights: long queries (prefill), CPU tensors, training with dropout, ``output_attentions``, other
-  dtypes, masks that are not boolean ``[B, 1 or Hq, Q, S]``.
+  kernels first, fp8 K/V upcast to the query's dtype, Quest's unselected pages hidden in the mask as the reference's
+  fallback hides them, interface.py:216-222), or to the model's eager function when the call has sinks or asks for
+  the weights: long queries (prefill), CPU tensors, training with dropout, ``output_attentions``, other dtypes, masks
+  that are not boolean ``[B, 1 or Hq, Q, S]``.
 """
 
 from __future__ import annotations
@@ -129,10 +131,18 @@ class PagedKV:
             return kivi_decode_attention(q, self.cache, self.block_table, self.seq_lens, self.max_seq_len, scale,
                                          softcap, sinks, mask=mask)
         if self.format == "quest":
-            return self.pages.attend(query, self.cache, self.block_table, self.seq_lens, self.max_seq_len, scale,
-                                     softcap, sinks, mask=mask)
+            return self.pages.attend_paged(query, self.cache, self.block_table, self.seq_lens, self.max_seq_len,
+                                           scale, softcap, sinks, mask=mask)
         return paged_decode_attention(q, self.cache, self.block_table, self.seq_lens, self.max_seq_len, scale,
                                       softcap, sinks, mask=mask)
+
+    def restrict_mask(self, query: torch.Tensor, key: torch.Tensor, mask: torch.Tensor | None,
+                      is_causal: bool = False) -> torch.Tensor | None:
+        """For a fallback over the materialized K/V: ``mask`` with the pages Quest does not select hidden
+        (:meth:`~economize_amd.quest.QuestPages.restrict_mask`), or ``mask`` itself without Quest pages."""
+        if self.pages is None:
+            return mask
+        return self.pages.restrict_mask(query, key, mask, is_causal)
 
     def materialize(self) -> tuple[torch.Tensor, torch.Tensor]:
         """The dense K/V ``[B, Hkv, max_seq_len, D]`` the kernels read, in :attr:`dtype` (the gather kernels)."""
@@ -256,10 +266,15 @@ def _fallback(module, query, key, value, attention_mask, dropout, scaling, is_ca
 
     layer = getattr(module, "layer_idx", None)
     key, value = materialized_kv(key, value)
-    if key.dtype in FP8_DTYPES:
-        key, value = key.to(query.dtype), value.to(query.dtype)
     if torch.is_tensor(attention_mask) and attention_mask.dim() == 4 and attention_mask.shape[-1] > key.shape[2]:
         attention_mask = attention_mask[..., : key.shape[2]]
+    restrict = getattr(packed_of(key), "restrict_mask", None)
+    if restrict is not None:  # a sparse cache (Quest) hides what its kernel would not read (interface.py:216-222)
+        restricted = restrict(query, key, attention_mask, bool(is_causal))
+        if restricted is not attention_mask:
+            attention_mask, is_causal = restricted, False
+    if key.dtype in FP8_DTYPES:
+        key, value = key.to(query.dtype), value.to(query.dtype)
     _calls["fallback"] += 1
     eager = _eager_function(module, kwargs)
     if eager is None:
@@ -286,7 +301,9 @@ def economize_attention_forward(module: torch.nn.Module | None, query: torch.Ten
         raise ConfigError(f"query must be [B, Hq, Q, D], got {tuple(query.shape)}")
     handle = key if isinstance(key, PagedKV) else packed_of(key)
     paged = handle if isinstance(handle, PagedKV) else None
-    gathered = handle if getattr(handle, "format", None) == "gathered" else None
+    # packed K/V over dense buffers: a gathered cache's compact entries, Quest's pages of a dense cache
+    dense_packed = handle if paged is None and getattr(handle, "format", None) in ("gathered", "quest") else None
+    gathered = dense_packed if getattr(dense_packed, "format", None) == "gathered" else None
     layer = getattr(module, "layer_idx", None)
     queries = query.shape[2]
     reason = _fallback_reason(module, query, key, attention_mask, dropout, kwargs, paged, gathered)
@@ -303,9 +320,9 @@ def economize_attention_forward(module: torch.nn.Module | None, query: torch.Ten
     else:
         if attention_mask is not None and attention_mask.shape[-1] != key.shape[2]:
             attention_mask = attention_mask[..., : key.shape[2]]
-        if gathered is not None:
-            out = gathered.attend(query, key, value, attention_mask, scale, softcap, sinks)
-            path = "kernel_gathered"
+        if dense_packed is not None:
+            out = dense_packed.attend(query, key, value, attention_mask, scale, softcap, sinks)
+            path = f"kernel_{dense_packed.format}"
         else:
             out = decode_attention(query, key, value, attention_mask, scale, softcap=softcap, sinks=sinks)
             path = "kernel"

@@ -346,13 +346,22 @@ struct GatheredArgs {
     int capacity, dropped;
 };
 
+// The selected pages of a Quest call over a dense cache (the reference's quest_decode_attention arguments,
+// attention/quest.py:239-344): index [B, Hkv, pages], done [B], pages of 2^shift slots, min(done) for the plan.
+struct QuestListArgs {
+    const int32_t* index;
+    int64_t si_b, si_h;
+    int pages, shift, min_done;
+    const int32_t* done;
+};
+
 int dense_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int64_t sq_q, const void* k,
                const void* v, int32_t kv_format, int64_t sk_b, int64_t sk_h, int64_t sk_s, int64_t sv_b, int64_t sv_h,
                int64_t sv_s, const float* k_scale, const float* v_scale, const uint8_t* mask, int64_t sm_b,
                int64_t sm_h, int64_t sm_q, int64_t sm_s, const float* sinks, void* out, int64_t so_b, int64_t so_q,
                int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys,
                int32_t head_dim, int32_t value_dim, float scale, float softcap, void* workspace,
-               size_t workspace_bytes, void* stream, const GatheredArgs* g) {
+               size_t workspace_bytes, void* stream, const GatheredArgs* g, const QuestListArgs* ql = nullptr) {
     if (!q || !k || !v || !out) return fail("decode: null query, key, value or output pointer");
     if (batch <= 0 || queries <= 0 || q_heads <= 0 || kv_heads <= 0 || keys < 0)
         return fail("decode: batch, queries and heads must be positive, keys non-negative");
@@ -376,7 +385,11 @@ int dense_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, in
     for (int64_t st : {sk_b, sk_h, sk_s, sv_b, sv_h, sv_s})
         if ((st * es) % 16) return fail("decode: key and value strides must be multiples of 16 bytes");
     if (!(scale == scale)) return fail("decode: scale is NaN");
-    const int plan_keys = g ? std::max(1, keys - g->dropped) : keys;  // the virtual key axis
+    // the virtual key axis: gathered, keys - dropped; Quest, the selected pages' slots and the longest tail
+    int plan_keys = g ? std::max(1, keys - g->dropped) : keys;
+    if (ql)
+        plan_keys = static_cast<int>(std::max<int64_t>(
+            1, (static_cast<int64_t>(ql->pages) << ql->shift) + keys - (static_cast<int64_t>(ql->min_done) << ql->shift)));
     const DensePlan d = dense_plan(batch, queries, q_heads, kv_heads, plan_keys, head_dim, value_dim);
     if (!workspace || workspace_bytes < d.workspace)
         return fail("decode: workspace too small (" + std::to_string(workspace_bytes) + " < " +
@@ -441,6 +454,14 @@ int dense_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, in
         p.g_start = g->start;
         p.g_capacity = g->capacity;
     }
+    if (ql) {
+        p.qp_list = ql->index;
+        p.sqp_b = ql->si_b;
+        p.sqp_h = ql->si_h;
+        p.qp_pages = ql->pages;
+        p.qp_shift = ql->shift;
+        p.qp_done = ql->done;
+    }
     return dense_attention(p, d.padded_dim, static_cast<hipStream_t>(stream));
 }
 
@@ -480,19 +501,13 @@ int make_cell_layout(int head_dim, int element_size, int bits, int group, CellLa
 
 using namespace eco;
 
-extern "C" {
-
-const char* eco_last_error(void) { return g_error.c_str(); }
-
-int eco_abi_version(void) { return 4; }
-
-int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
-                     int64_t sv_t, int64_t sv_h, const int32_t* slot_mapping, int32_t tokens, void* k_cache,
-                     void* v_cache, int32_t num_pages, int32_t kv_heads, int32_t head_dim, int32_t page_size,
-                     int32_t cache_format, const float* k_scale, const float* v_scale, void* stream) {
+// The append's arguments as AppendParams (1 with a message when they are invalid; tokens may be 0).
+static int append_params(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
+                         int64_t sv_t, int64_t sv_h, const int32_t* slot_mapping, int32_t tokens, void* k_cache,
+                         void* v_cache, int32_t num_pages, int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                         int32_t cache_format, const float* k_scale, const float* v_scale, AppendParams& p) {
     if (tokens < 0) return fail("paged append: negative token count");
-    if (tokens == 0) return 0;
-    if (!k_new || !v_new || !slot_mapping || !k_cache || !v_cache)
+    if ((tokens > 0 && (!k_new || !v_new || !slot_mapping)) || !k_cache || !v_cache)
         return fail("paged append: null input, slot mapping or cache pointer");
     if (in_format != BF16 && in_format != FP16 && in_format != FP32)
         return fail("paged append: inputs must be bf16, fp16 or fp32");
@@ -503,7 +518,6 @@ int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, in
         return fail("paged append: head dim must be a positive multiple of 16, heads and pages positive");
     if (cache_format == BF16 && (k_scale || v_scale)) return fail("paged append: a bf16 cache takes no scales");
     const int es = cache_format == BF16 ? 2 : 1;
-    AppendParams p;
     p.k_new = k_new;
     p.v_new = v_new;
     p.in_format = in_format;
@@ -525,7 +539,72 @@ int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, in
     p.cache_format = cache_format;
     p.k_scale = k_scale;
     p.v_scale = v_scale;
+    return 0;
+}
+
+extern "C" {
+
+const char* eco_last_error(void) { return g_error.c_str(); }
+
+int eco_abi_version(void) { return 5; }
+
+int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
+                     int64_t sv_t, int64_t sv_h, const int32_t* slot_mapping, int32_t tokens, void* k_cache,
+                     void* v_cache, int32_t num_pages, int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                     int32_t cache_format, const float* k_scale, const float* v_scale, void* stream) {
+    if (tokens == 0) return 0;
+    AppendParams p;
+    if (int rc = append_params(k_new, v_new, in_format, sk_t, sk_h, sv_t, sv_h, slot_mapping, tokens, k_cache, v_cache,
+                               num_pages, kv_heads, head_dim, page_size, cache_format, k_scale, v_scale, p))
+        return rc;
     return paged_append(p, static_cast<hipStream_t>(stream));
+}
+
+int eco_paged_append_quest(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
+                           int64_t sv_t, int64_t sv_h, const int32_t* slot_mapping, int32_t tokens, void* k_cache,
+                           void* v_cache, int32_t num_pages, int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                           int32_t cache_format, const float* k_scale, const float* v_scale,
+                           const int32_t* block_table, int64_t bt_stride, int32_t bt_cols, const int32_t* committed,
+                           int32_t* valid, int32_t* done, int32_t* counters, int32_t quest_page_size, void* kmin,
+                           void* kmax, int64_t sb_b, int64_t sb_h, int64_t sb_p, int32_t page_cap, int32_t batch,
+                           void* stream) {
+    AppendParams p;
+    if (int rc = append_params(k_new, v_new, in_format, sk_t, sk_h, sv_t, sv_h, slot_mapping, tokens, k_cache, v_cache,
+                               num_pages, kv_heads, head_dim, page_size, cache_format, k_scale, v_scale, p))
+        return rc;
+    if (!block_table || !committed || !valid || !counters || !kmin || !kmax)
+        return fail("paged append (quest): null block table, committed, valid, counters or bounds");
+    if (batch <= 0 || bt_cols <= 0 || bt_stride < bt_cols || page_cap < 0)
+        return fail("paged append (quest): batch and block-table columns must be positive");
+    if (quest_page_size < 16 || quest_page_size % 16 || (quest_page_size & (quest_page_size - 1)))
+        return fail("paged append (quest): quest pages must hold a power of two of at least 16 tokens");
+    const int es = cache_format == BF16 ? 2 : 1;
+    if ((head_dim * es) % 64) return fail("paged append (quest): head dim must fill whole runs");
+    BoundsParams q;
+    q.k_cache = p.k_cache;
+    q.kc_head = p.kc_head;
+    q.kc_page = p.kc_page;
+    q.kv_format = cache_format;
+    q.num_pages = num_pages;
+    q.block_table = block_table;
+    q.bt_stride = bt_stride;
+    q.bt_cols = bt_cols;
+    q.first = 0;
+    q.last = 0;
+    q.span = quest_page_size / 16;
+    q.kmin = static_cast<uint16_t*>(kmin);
+    q.kmax = static_cast<uint16_t*>(kmax);
+    q.sb_b = sb_b;
+    q.sb_h = sb_h;
+    q.sb_p = sb_p;
+    q.batch = batch;
+    q.kv_heads = kv_heads;
+    q.head_dim = head_dim;
+    q.committed = committed;
+    q.valid = valid;
+    q.done = done;
+    q.page_cap = page_cap;
+    return paged_append_quest(p, q, counters, static_cast<hipStream_t>(stream));
 }
 
 int eco_fp8_encode(const void* src, int32_t in_format, int64_t ss_b, int64_t ss_h, int64_t ss_t, void* dst,
@@ -1226,17 +1305,92 @@ int eco_quest_refresh_bounds(const void* k_cache, int32_t kv_format, int32_t num
     return quest_refresh(p, static_cast<hipStream_t>(stream));
 }
 
+int eco_quest_dense_bounds(const void* keys, int32_t kv_format, int64_t sk_b, int64_t sk_h, int64_t sk_s,
+                           int32_t slots, int32_t first, int32_t last, int32_t page_size, void* kmin, void* kmax,
+                           int32_t bounds_format, int64_t sb_b, int64_t sb_h, int64_t sb_p, int32_t batch,
+                           int32_t kv_heads, int32_t head_dim, void* stream) {
+    if (!keys || !kmin || !kmax) return fail("quest page bounds: null keys or bounds");
+    if (batch <= 0 || kv_heads <= 0 || head_dim <= 0 || slots < 0)
+        return fail("quest page bounds: batch, heads and head dim must be positive, slots non-negative");
+    if (page_size < 16 || (page_size & (page_size - 1)))
+        return fail("quest page bounds: pages must hold a power of two of at least 16 slots");
+    if (first < 0 || last < first || static_cast<int64_t>(last) * page_size > slots)
+        return fail("quest page bounds: need 0 <= first <= last and last pages within the " + std::to_string(slots) +
+                    " slots");
+    const bool fp8 = kv_format == FP8_E4M3 || kv_format == FP8_E5M2;
+    if (kv_format != BF16 && kv_format != FP16 && kv_format != FP32 && !fp8)
+        return fail("quest page bounds: keys must be bf16, fp16, fp32, fp8 e4m3 or fp8 e5m2");
+    const int want = fp8 ? BF16 : kv_format;  // bounds_dtype (attention/quest.py:68-70)
+    if (bounds_format != want) return fail("quest page bounds: bounds must be bf16 for bf16 and fp8 keys, else the keys' dtype");
+    DenseBoundsParams p;
+    p.keys = keys;
+    p.sk_b = sk_b;
+    p.sk_h = sk_h;
+    p.sk_s = sk_s;
+    p.kv_format = kv_format;
+    p.first = first;
+    p.last = last;
+    p.page = page_size;
+    p.kmin = kmin;
+    p.kmax = kmax;
+    p.sb_b = sb_b;
+    p.sb_h = sb_h;
+    p.sb_p = sb_p;
+    p.bounds_format = bounds_format;
+    p.batch = batch;
+    p.kv_heads = kv_heads;
+    p.head_dim = head_dim;
+    return quest_dense_bounds(p, static_cast<hipStream_t>(stream));
+}
+
+int eco_quest_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int64_t sq_q, const void* k,
+                     const void* v, int32_t kv_format, int64_t sk_b, int64_t sk_h, int64_t sk_s, int64_t sv_b,
+                     int64_t sv_h, int64_t sv_s, const float* k_scale, const float* v_scale, const int32_t* index,
+                     int64_t si_b, int64_t si_h, int32_t pages, const int32_t* done, int32_t page_size,
+                     int32_t min_done, const uint8_t* mask, int64_t sm_b, int64_t sm_h, int64_t sm_q, int64_t sm_s,
+                     const float* sinks, void* out, int64_t so_b, int64_t so_q, int64_t so_h, int32_t batch,
+                     int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys, int32_t head_dim,
+                     int32_t value_dim, float scale, float softcap, void* workspace, size_t workspace_bytes,
+                     void* stream) {
+    if (!index || !done) return fail("quest decode: null page index or done");
+    if (page_size < 16 || (page_size & (page_size - 1)))
+        return fail("quest decode: pages must hold a power of two of at least 16 slots");
+    if (pages < 0 || min_done < 0 || static_cast<int64_t>(min_done) * page_size > keys)
+        return fail("quest decode: need pages >= 0 and 0 <= min_done * page <= keys");
+    int shift = 0;
+    while ((1 << shift) < page_size) ++shift;
+    const QuestListArgs ql{index, si_b, si_h, pages, shift, min_done, done};
+    return dense_decode(q, q_format, sq_b, sq_h, sq_q, k, v, kv_format, sk_b, sk_h, sk_s, sv_b, sv_h, sv_s, k_scale,
+                        v_scale, mask, sm_b, sm_h, sm_q, sm_s, sinks, out, so_b, so_q, so_h, batch, queries, q_heads,
+                        kv_heads, keys, head_dim, value_dim, scale, softcap, workspace, workspace_bytes, stream,
+                        nullptr, &ql);
+}
+
+size_t eco_quest_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
+                                       int32_t keys, int32_t pages, int32_t page_size, int32_t min_done,
+                                       int32_t head_dim, int32_t value_dim) {
+    if (page_size < 16 || pages < 0 || min_done < 0) return 0;
+    const int64_t virt = std::max<int64_t>(1, static_cast<int64_t>(pages) * page_size + keys -
+                                                  static_cast<int64_t>(min_done) * page_size);
+    if (virt > INT32_MAX) return 0;
+    return eco_decode_workspace_size(batch, queries, q_heads, kv_heads, static_cast<int32_t>(virt), head_dim,
+                                     value_dim);
+}
+
 size_t eco_quest_select_workspace_size(int32_t batch, int32_t kv_heads, int32_t max_done) {
     if (batch <= 0 || kv_heads <= 0 || max_done < 0) return 0;
     const size_t stride = (static_cast<size_t>(max_done > 0 ? max_done : 1) + 3) / 4 * 4;  // 16-byte aligned rows
     return align256(static_cast<size_t>(batch) * kv_heads * stride * sizeof(float));
 }
 
-int eco_quest_select(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* kmin, const void* kmax,
-                     int64_t sb_b, int64_t sb_h, int64_t sb_p, const int32_t* done, int32_t max_done, int32_t pages,
-                     int32_t first_page, int32_t* out, int32_t batch, int32_t queries, int32_t q_heads,
-                     int32_t kv_heads, int32_t head_dim, void* workspace, size_t workspace_bytes, void* stream) {
+int eco_quest_select(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* kmin,
+                     const void* kmax, int32_t bounds_format, int64_t sb_b, int64_t sb_h, int64_t sb_p,
+                     const int32_t* done, int32_t max_done, int32_t pages, int32_t first_page, int32_t* out,
+                     int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                     void* workspace, size_t workspace_bytes, void* stream) {
     if (!q || !done || !out) return fail("quest select: null query, done or output");
+    for (int f : {q_format, bounds_format})
+        if (f != BF16 && f != FP16 && f != FP32) return fail("quest select: queries and bounds must be bf16, fp16 or fp32");
     if (batch <= 0 || queries <= 0 || q_heads <= 0 || kv_heads <= 0 || pages < 0 || max_done < 0)
         return fail("quest select: batch, queries and heads must be positive, pages and max_done non-negative");
     if (q_heads % kv_heads) return fail("quest select: query heads are not a multiple of the KV heads");
@@ -1244,19 +1398,21 @@ int eco_quest_select(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
     if (max_done > 0 && (!kmin || !kmax)) return fail("quest select: null page bounds");
     if ((reinterpret_cast<uintptr_t>(kmin) & 15) || (reinterpret_cast<uintptr_t>(kmax) & 15) || (sb_b & 7) ||
         (sb_h & 7) || (sb_p & 7))
-        return fail("quest select: page bounds must be 16-byte aligned with strides that are multiples of 8");
+        return fail("quest select: page bounds must be 16-byte aligned with strides that are multiples of 8 elements");
     if (pages == 0) return 0;
     const size_t need = eco_quest_select_workspace_size(batch, kv_heads, max_done);
     if (max_done > 0 && (!workspace || workspace_bytes < need))
         return fail("quest select: workspace too small (" + std::to_string(workspace_bytes) + " < " +
                     std::to_string(need) + " bytes)");
     SelectParams p;
-    p.q = static_cast<const uint16_t*>(q);
+    p.q = q;
+    p.q_format = q_format;
     p.sq_b = sq_b;
     p.sq_q = sq_q;
     p.sq_h = sq_h;
-    p.kmin = static_cast<const uint16_t*>(kmin);
-    p.kmax = static_cast<const uint16_t*>(kmax);
+    p.kmin = kmin;
+    p.kmax = kmax;
+    p.bounds_format = bounds_format;
     p.sb_b = sb_b;
     p.sb_h = sb_h;
     p.sb_p = sb_p;

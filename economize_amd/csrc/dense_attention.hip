@@ -277,6 +277,20 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
         gvbase = static_cast<const uint8_t*>(p.gv) + (b * p.sgv_b + kvh * p.sgv_h) * ES;
         gidx = p.g_index + b * p.sgi_b + kvh * p.sgi_h;
     }
+    // Quest: the row's selected pages (a prefix of its list) come first, then its slots from done[b] pages on
+    const int32_t* qlist = nullptr;
+    const int page_cap = p.qp_list ? p.dense_keys >> p.qp_shift : 0;  // whole pages in the buffer
+    if (p.qp_list) {
+        qlist = p.qp_list + b * p.sqp_b + kvh * p.sqp_h;
+        int valid = 0;
+        for (int i = 0; i < p.qp_pages; i += 64) {
+            const int e = i + lane < p.qp_pages ? qlist[i + lane] : -1;
+            valid += static_cast<int>(__popcll(__ballot(e >= 0)));
+        }
+        count = min(valid, page_cap) << p.qp_shift;
+        start = min(max(p.qp_done[b], 0), page_cap) << p.qp_shift;
+        row_keys = min(count + p.dense_keys - start, p.keys);
+    }
     // This wave's tiles interleave with its block's other splits: tile k starts at key (split + k splits) 32, so that
     // the block's waves (one XCD) read adjacent 8 KB runs of the K and V buffers together.
     const int tiles_row = (row_keys + TK - 1) / TK;
@@ -286,7 +300,8 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
     // the first cell of half win0 + l (its page's cells of this KV head, plus the half's place in the page: a
     // multiple of 16 tokens); a tile reads its halves' offsets from the window (v_readlane) and reloads the window
     // every 32 tiles, so that the tile loads need no block-table load, and no division by the page size, of their
-    // own
+    // own. Quest uses the same window for the slot of each half's first key (page-list entries instead of the
+    // block table).
     int win0 = -(1 << 30);
     int64_t win_page = 0;
     auto half_offset = [&](int half) __attribute__((always_inline)) -> int64_t {  // half: uniform
@@ -294,9 +309,18 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
             win0 = half;
             const int mine = half + lane;
             const int first = tile_start(mine >> 1) + (mine & 1) * 16;
-            const int lp = min(first / p.page_size, p.bt_cols - 1);
-            const int page = min(max(p.block_table[static_cast<int64_t>(b) * p.bt_stride + lp], 0), p.num_pages - 1);
-            win_page = page * p.sc_page + kvh * p.sc_head + static_cast<int64_t>(first % p.page_size) * p.sc_token;
+            if (p.cells) {
+                const int lp = min(first / p.page_size, p.bt_cols - 1);
+                const int page =
+                    min(max(p.block_table[static_cast<int64_t>(b) * p.bt_stride + lp], 0), p.num_pages - 1);
+                win_page = page * p.sc_page + kvh * p.sc_head + static_cast<int64_t>(first % p.page_size) * p.sc_token;
+            } else if (first < count) {  // Quest: the slot of the half's first key (a half lies in one page)
+                const int e = qlist[min(first >> p.qp_shift, p.qp_pages - 1)];
+                win_page = (static_cast<int64_t>(min(max(e, 0), page_cap - 1)) << p.qp_shift) +
+                           (first & ((1 << p.qp_shift) - 1));
+            } else {
+                win_page = start + first - count;
+            }
             // wait here for the table load (vmcnt(0)), so that the common path, which reloads nothing, does not
             // wait at the branch's join for every load in flight
             __builtin_amdgcn_s_waitcnt(0x0F70);
@@ -309,28 +333,39 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
     // the cache offsets of the first cells of tile k's two 16-key halves (a tile starts at a multiple of 32 keys and
     // pages hold a multiple of 16, so each half lies in one page)
     int64_t cell_h0 = 0, cell_h1 = 0;  // (two variables, not an array: a lane-dependent index of one goes to scratch)
+    // (Quest: the slots of the halves' first keys; pages of 32 or more slots, and the tail, keep a tile's halves
+    // adjacent)
     auto tile_pages = [&](int k) __attribute__((always_inline)) {
         if (p.cells) {
             cell_h0 = half_offset(2 * k);
             cell_h1 = p.page_size % 32 == 0 ? cell_h0 + 16 * p.sc_token : half_offset(2 * k + 1);
+        } else if (p.qp_list) {
+            cell_h0 = half_offset(2 * k);
+            cell_h1 = p.qp_shift >= 5 ? cell_h0 + 16 : half_offset(2 * k + 1);
         }
+    };
+    auto quest_slot = [&](int t) __attribute__((always_inline)) -> int64_t {  // t inside the current tile
+        return ((t >> 4) & 1 ? cell_h1 : cell_h0) + (t & 15);
     };
     auto cell_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {  // t inside the current tile
         return p.cells + ((t >> 4) & 1 ? cell_h1 : cell_h0) + static_cast<int64_t>(t & 15) * p.sc_token;
     };
     auto key_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
         if (p.cells) return cell_row(t);
+        if (p.qp_list) return kbase + quest_slot(t) * p.sk_s * ES;
         return t < count ? gkbase + static_cast<int64_t>(t) * p.sgk_s * ES
                          : kbase + static_cast<int64_t>(start + t - count) * p.sk_s * ES;
     };
     auto value_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
         if (p.cells) return cell_row(t) + p.cell_off_v;
+        if (p.qp_list) return vbase + quest_slot(t) * p.sv_s * ES;
         return t < count ? gvbase + static_cast<int64_t>(t) * p.sgv_s * ES
                          : vbase + static_cast<int64_t>(start + t - count) * p.sv_s * ES;
     };
     // causal: the last q_count keys of the row are its queries' own tokens
     const int causal_limit = p.causal ? row_keys - q_count + qi + 1 : row_keys;
     auto mask_col = [&](int t) __attribute__((always_inline)) -> int64_t {
+        if (p.qp_list) return quest_slot(t);
         return t < count ? min(max(gidx[t], 0), p.dense_keys - 1) : start + t - count;
     };
 

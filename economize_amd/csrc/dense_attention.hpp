@@ -64,6 +64,16 @@ struct DenseParams {
     // qi when t < keys_b - queries_b + qi + 1 (on top of the mask).
     const int32_t* query_start_loc;
     int causal;
+    // Quest mode (qp_list non-null; the reference's quest_decode_attention over a dense cache, attention/quest.py:
+    // 239-344 and _quest_kernels.py:13-97): virtual key t of (b, kvh) is slot qp_list[b, kvh, t >> qp_shift] *
+    // 2^qp_shift + t % 2^qp_shift of k / v while t < count (the page size times the list's non-negative entries,
+    // which lead it: pages in increasing order, then -1), else slot qp_done[b] * 2^qp_shift + t - count; `keys` bounds
+    // the virtual axis and dense_keys the slots. Entries and done are clamped to the buffer's whole pages, so a
+    // malformed list reads wrong slots but nothing outside the buffers.
+    const int32_t* qp_list;
+    int64_t sqp_b, sqp_h;
+    int qp_pages, qp_shift;
+    const int32_t* qp_done;
 };
 
 int dense_padded_dim(int head_dim, int value_dim);  // 64, 128 or 256; 0 when neither fits

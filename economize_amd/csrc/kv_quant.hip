@@ -13,6 +13,7 @@
 
 #include "common.hpp"
 #include "kv_quant.hpp"
+#include "quest_page.hpp"
 
 namespace eco {
 
@@ -33,11 +34,11 @@ __device__ inline uint8_t encode(float x, float scale, bool scaled) {
     return f32_to_fp8<FMT>(fminf(fmaxf(w, -fp8_max<FMT>()), fp8_max<FMT>()));
 }
 
+// New token t into its slot, by one workgroup.
 template <int FMT>
-__global__ __launch_bounds__(256) void paged_append_kernel(AppendParams p) {
+__device__ inline void append_token(const AppendParams& p, int t) {
     constexpr int ES = FMT == BF16 ? 2 : 1;
     constexpr int E = 16 / ES;  // channels per 16-byte run of the key layout
-    const int t = blockIdx.x;
     const int slot = p.slots[t];
     if (slot < 0 || slot / PAGE >= p.num_pages) return;
     const int page = slot / PAGE;
@@ -80,6 +81,43 @@ __global__ __launch_bounds__(256) void paged_append_kernel(AppendParams p) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) vp[(d0 + i) * PAGE + pos] = encode<FMT>(v[i], vs, vscaled);
         }
+    }
+}
+
+template <int FMT>
+__global__ __launch_bounds__(256) void paged_append_kernel(AppendParams p) {
+    append_token<FMT>(p, blockIdx.x);
+}
+
+// The append with Quest's metadata kept on the device, in one launch: workgroups below `tokens` append a token each;
+// the others are four waves each of the refresh, kRefreshWaves waves per (row, KV head) taking the Quest pages
+// valid + y, valid + y + kRefreshWaves, ... below the row's committed pages (the bounds of pages that became committed,
+// quest_refresh_kernel's work). The last of a row's waves to finish (a counter per row, agent-scope atomics; every
+// wave has read valid before it counts itself) advances valid and writes done, then leaves the counter zero. The
+// tokens appended lie at or past the committed ones, so no page this launch refreshes is written by it.
+constexpr int kRefreshWaves = 8;
+
+template <int FMT>
+__global__ __launch_bounds__(256) void paged_append_quest_kernel(AppendParams p, BoundsParams q, int32_t* counters) {
+    if (static_cast<int>(blockIdx.x) < p.tokens) {
+        append_token<FMT>(p, blockIdx.x);
+        return;
+    }
+    const int wave = (static_cast<int>(blockIdx.x) - p.tokens) * 4 + static_cast<int>(threadIdx.x >> 6);
+    const int lane = static_cast<int>(threadIdx.x & 63);
+    if (wave >= q.batch * q.kv_heads * kRefreshWaves) return;
+    const int row = wave / kRefreshWaves, y = wave % kRefreshWaves;
+    const int b = row / q.kv_heads, kvh = row % q.kv_heads;
+    const int last = min(max(q.committed[b], 0) / (16 * q.span), q.page_cap);
+    const int from = q.valid[row];
+    for (int qp = from + y; qp < last; qp += kRefreshWaves) quest_bounds_of_page<FMT>(q, b, qp, kvh, lane);
+    int prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(counters + row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (__shfl(prev, 0) != kRefreshWaves - 1) return;
+    if (lane == 0) {
+        q.valid[row] = max(from, last);
+        if (q.done && kvh == 0) q.done[b] = last;
+        __hip_atomic_store(counters + row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -165,6 +203,22 @@ int paged_append(const AppendParams& p, hipStream_t stream) {
         default: return fail("paged append: cache format must be bf16, fp8 e4m3 or fp8 e5m2");
     }
     return check_launch("paged_append_kernel");
+}
+
+int paged_append_quest(const AppendParams& p, const BoundsParams& q, int32_t* counters, hipStream_t stream) {
+    const int refresh = (q.batch * q.kv_heads * kRefreshWaves + 3) / 4;
+    dim3 grid(p.tokens + refresh);
+    switch (p.cache_format) {
+        case BF16: hipLaunchKernelGGL(paged_append_quest_kernel<BF16>, grid, dim3(256), 0, stream, p, q, counters); break;
+        case FP8_E4M3:
+            hipLaunchKernelGGL(paged_append_quest_kernel<FP8_E4M3>, grid, dim3(256), 0, stream, p, q, counters);
+            break;
+        case FP8_E5M2:
+            hipLaunchKernelGGL(paged_append_quest_kernel<FP8_E5M2>, grid, dim3(256), 0, stream, p, q, counters);
+            break;
+        default: return fail("paged append: cache format must be bf16, fp8 e4m3 or fp8 e5m2");
+    }
+    return check_launch("paged_append_quest_kernel");
 }
 
 int fp8_encode(const EncodeParams& p, hipStream_t stream) {

@@ -44,6 +44,10 @@ struct EncodeParams {
 };
 
 int paged_append(const AppendParams& p, hipStream_t stream);
+// paged_append plus the Quest refresh of BoundsParams (committed, valid, done, bounds) in one launch; counters: one
+// int32 per (row, KV head), zero between calls.
+struct BoundsParams;
+int paged_append_quest(const AppendParams& p, const BoundsParams& q, int32_t* counters, hipStream_t stream);
 int fp8_encode(const EncodeParams& p, hipStream_t stream);
 int head_absmax(const AbsmaxParams& p, hipStream_t stream);
 int scales_from_absmax(const uint32_t* absmax_bits, int heads, int format, float* scales, hipStream_t stream);

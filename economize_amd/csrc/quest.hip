@@ -1,7 +1,8 @@
 // Quest page bounds and query-aware page selection (gfx950).
 //
 // Page bounds follow page_bounds (attention/quest.py:54-65): the channel-wise smallest and largest key of every page,
-// fp8 keys decoded exactly (bf16 holds every fp8 value), written as bf16. They are computed from the stored cache
+// fp8 keys decoded exactly (bf16 holds every fp8 value), written as bf16 (fp16 and fp32 keys of a dense buffer: in
+// their own format, as bounds_dtype, attention/quest.py:68-70). They are computed from the stored cache
 // elements; a per-head fp8 scale is positive and multiplies every score of a (row, KV head) alike, so it does not
 // change which pages are selected and is not applied.
 //
@@ -13,7 +14,8 @@
 // to fp32, sequential sums over runs of 8 channels, then a halving tree over the runs, run j plus run j + n / 2, n
 // the run count padded to a power of two) and ties (equal scores are taken lowest page first).
 //
-// Kernels: quest_bounds_kernel (one wave per row, Quest page and KV head), quest_score_kernel (a chunk of pages of
+// Kernels: quest_bounds_kernel (one wave per row, Quest page and KV head, over the paged cache),
+// quest_dense_bounds_kernel (the same over a dense key buffer of any format), quest_score_kernel (a chunk of pages of
 // one (row, KV head) per workgroup: the bounds are the bytes a selection reads, so the scoring is spread over the
 // whole chip), quest_topk_kernel (one workgroup per (row, KV head): a radix select over order-preserving integer keys
 // of the scores, ties to the lower index, then a compaction in page order).
@@ -22,93 +24,23 @@
 
 #include "common.hpp"
 #include "quest.hpp"
+#include "quest_page.hpp"
 
 namespace eco {
 
 namespace {
 
-constexpr int PAGE = 16;
 constexpr int SCORE_PASSES = 4;  // pages per scoring thread
 
 // Scores of a (row, KV head) in the workspace: max_done floats, rows 16-byte aligned.
 __host__ __device__ inline int64_t score_stride(int max_done) { return (max_done + 3) & ~3; }
 constexpr int TOPK_LDS_KEYS = 15360;  // rows of at most this many committed pages select from keys held in LDS (60 KiB)
 
-template <int FMT>
-__device__ inline float decode_elem(const uint8_t* p, int i) {
-    if constexpr (FMT == BF16) {
-        return bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
-    } else {
-        // exact fp8 value, through the hardware converter (scale 1)
-        const uint32_t word = p[i];
-        if constexpr (FMT == FP8_E4M3)
-            return __builtin_amdgcn_cvt_scalef32_f32_fp8(word, 1.0f, 0);
-        else
-            return __builtin_amdgcn_cvt_scalef32_f32_bf8(word, 1.0f, 0);
-    }
-}
-
-// The bounds of Quest page qp of (row b, KV head kvh) by one wave: lane l holds token l % 16 of the runs l / 16,
-// l / 16 + 4, ... of every cache page of the Quest page; the 16 lanes of a run then reduce over the tokens.
-template <int FMT>
-__device__ inline void bounds_of_page(const BoundsParams& p, int b, int qp, int kvh, int lane) {
-    constexpr int ES = FMT == BF16 ? 2 : 1;
-    constexpr int X = 16 / ES;  // channels per 16-byte run
-    const int runs = p.head_dim / X;
-    const int token = lane & 15;
-    // every cache page of the Quest page must be held (a missing one leaves the bounds untouched)
-    for (int s = 0; s < p.span; ++s) {
-        const int lp = qp * p.span + s;
-        if (lp >= p.bt_cols) return;
-        const int phys = p.block_table[b * p.bt_stride + lp];
-        if (phys < 0 || phys >= p.num_pages) return;
-    }
-    for (int r0 = 0; r0 < runs; r0 += 4) {
-        const int run = r0 + (lane >> 4);
-        float lo[X], hi[X];
-#pragma unroll
-        for (int i = 0; i < X; ++i) {
-            lo[i] = INFINITY;
-            hi[i] = -INFINITY;
-        }
-        if (run < runs) {
-            for (int s = 0; s < p.span; ++s) {
-                const int phys = p.block_table[b * p.bt_stride + qp * p.span + s];
-                const uint8_t* src = p.k_cache + static_cast<int64_t>(phys) * p.kc_page + kvh * p.kc_head +
-                                     (run * PAGE + token) * 16;
-                uint8_t raw[16];
-                *reinterpret_cast<uint4*>(raw) = *reinterpret_cast<const uint4*>(src);
-#pragma unroll
-                for (int i = 0; i < X; ++i) {
-                    const float v = decode_elem<FMT>(raw, i);
-                    lo[i] = fminf(lo[i], v);
-                    hi[i] = fmaxf(hi[i], v);
-                }
-            }
-        }
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1)
-#pragma unroll
-            for (int i = 0; i < X; ++i) {
-                lo[i] = fminf(lo[i], __shfl_xor(lo[i], off));
-                hi[i] = fmaxf(hi[i], __shfl_xor(hi[i], off));
-            }
-        if (run < runs && token == 0) {
-            const int64_t at = b * p.sb_b + kvh * p.sb_h + qp * p.sb_p + run * X;
-#pragma unroll
-            for (int i = 0; i < X; ++i) {
-                p.kmin[at + i] = f32_to_bf16(lo[i]);
-                p.kmax[at + i] = f32_to_bf16(hi[i]);
-            }
-        }
-    }
-}
-
 // One wave per (row b, Quest page first + i, KV head).
 template <int FMT>
 __global__ __launch_bounds__(64) void quest_bounds_kernel(BoundsParams p) {
     const int pages = p.last - p.first;
-    bounds_of_page<FMT>(p, blockIdx.x / pages, p.first + blockIdx.x % pages, blockIdx.y, threadIdx.x);
+    quest_bounds_of_page<FMT>(p, blockIdx.x / pages, p.first + blockIdx.x % pages, blockIdx.y, threadIdx.x);
 }
 
 // The bounds of the pages each (row, KV head) committed since its last refresh, with every range on the device (a
@@ -120,7 +52,7 @@ __global__ __launch_bounds__(64) void quest_refresh_kernel(BoundsParams p) {
     const int b = row / p.kv_heads, kvh = row % p.kv_heads;
     const int last = min(max(p.committed[b], 0) / (16 * p.span), p.page_cap);
     for (int qp = p.valid[row] + static_cast<int>(blockIdx.y); qp < last; qp += gridDim.y)
-        bounds_of_page<FMT>(p, b, qp, kvh, threadIdx.x);
+        quest_bounds_of_page<FMT>(p, b, qp, kvh, threadIdx.x);
 }
 
 // After quest_refresh_kernel (the next launch on the stream): the refreshed pages are final, and done[b] is the
@@ -134,10 +66,80 @@ __global__ void quest_mark_kernel(BoundsParams p) {
     if (p.done && row % p.kv_heads == 0) p.done[b] = last;
 }
 
+// One key element of format KF as fp32 (exact; fp8 decoded by the hardware converter at scale 1).
+template <int KF>
+__device__ inline float key_f32(const uint8_t* base, int64_t i) {
+    if constexpr (KF == BF16) return bf16_to_f32(reinterpret_cast<const uint16_t*>(base)[i]);
+    if constexpr (KF == FP16) return static_cast<float>(reinterpret_cast<const _Float16*>(base)[i]);
+    if constexpr (KF == FP32) return reinterpret_cast<const float*>(base)[i];
+    if constexpr (KF == FP8_E4M3) return __builtin_amdgcn_cvt_scalef32_f32_fp8(base[i], 1.0f, 0);
+    return __builtin_amdgcn_cvt_scalef32_f32_bf8(base[i], 1.0f, 0);
+}
+
+// The bounds of pages [first, last) of a dense key buffer, one wave per (row, page, KV head): lane l takes channels
+// l, l + 64, ... and walks the page's slots (adjacent lanes read adjacent channels of one slot). Minimum and maximum
+// propagate NaN, as torch's amin / amax do; the results are exact in the bounds' format (bf16 holds every bf16 and
+// fp8 value, fp16 and fp32 keys keep their own format).
+template <int KF, int BF>
+__global__ __launch_bounds__(64) void quest_dense_bounds_kernel(DenseBoundsParams p) {
+    const int pages = p.last - p.first;
+    const int b = blockIdx.x / pages;
+    const int pg = p.first + blockIdx.x % pages;
+    const int kvh = blockIdx.y;
+    const uint8_t* keys = static_cast<const uint8_t*>(p.keys);
+    const int64_t base = b * p.sk_b + kvh * p.sk_h + static_cast<int64_t>(pg) * p.page * p.sk_s;
+    for (int c = threadIdx.x; c < p.head_dim; c += 64) {
+        float lo = INFINITY, hi = -INFINITY;
+        for (int t = 0; t < p.page; ++t) {
+            const float x = key_f32<KF>(keys, base + static_cast<int64_t>(t) * p.sk_s + c);
+            lo = __builtin_elementwise_minimum(lo, x);
+            hi = __builtin_elementwise_maximum(hi, x);
+        }
+        const int64_t at = b * p.sb_b + kvh * p.sb_h + static_cast<int64_t>(pg) * p.sb_p + c;
+        if constexpr (BF == BF16) {
+            static_cast<uint16_t*>(p.kmin)[at] = f32_to_bf16(lo);
+            static_cast<uint16_t*>(p.kmax)[at] = f32_to_bf16(hi);
+        } else if constexpr (BF == FP16) {
+            static_cast<_Float16*>(p.kmin)[at] = static_cast<_Float16>(lo);
+            static_cast<_Float16*>(p.kmax)[at] = static_cast<_Float16>(hi);
+        } else {
+            static_cast<float*>(p.kmin)[at] = lo;
+            static_cast<float*>(p.kmax)[at] = hi;
+        }
+    }
+}
+
+// One element of a query or of page bounds as fp32 (exact): bf16, fp16 or fp32.
+template <int F>
+__device__ inline float elem_f32(const void* base, int64_t i) {
+    if constexpr (F == BF16) return bf16_to_f32(static_cast<const uint16_t*>(base)[i]);
+    if constexpr (F == FP16) return static_cast<float>(static_cast<const _Float16*>(base)[i]);
+    return static_cast<const float*>(base)[i];
+}
+
+// Eight consecutive bounds (16-byte words: one for bf16 / fp16, two for fp32) as fp32.
+template <int BF>
+__device__ inline float bound_of(const uint4 (&w)[BF == FP32 ? 2 : 1], int i) {
+    if constexpr (BF == FP32) {
+        const uint4 x = w[i >> 2];
+        const uint32_t u = (i & 3) == 0 ? x.x : ((i & 3) == 1 ? x.y : ((i & 3) == 2 ? x.z : x.w));
+        return bits_f32(u);
+    } else {
+        const uint32_t words[4] = {w[0].x, w[0].y, w[0].z, w[0].w};
+        const uint16_t h = static_cast<uint16_t>(words[i >> 1] >> (16 * (i & 1)));
+        if constexpr (BF == BF16) return bf16_to_f32(h);
+        return static_cast<float>(__builtin_bit_cast(_Float16, h));
+    }
+}
+
 // Scores of pages [chunk * blockIdx.x, +chunk) of row (b, kvh) = blockIdx.y: L lanes per page (L = the run count
 // padded to a power of two), lane j holding channels 8 j .. 8 j + 7; a workgroup covers SCORE_PASSES * 256 / L
-// pages, and every thread issues the bound loads of all its pages before it sums the query rows.
+// pages, and every thread issues the bound loads of all its pages before it sums the query rows. QF / BF: the
+// formats of the query and of the bounds (bf16, fp16, fp32), both widened exactly to fp32.
+template <int QF, int BF>
 __global__ __launch_bounds__(256) void quest_score_kernel(SelectParams p) {
+    constexpr int BW = BF == FP32 ? 2 : 1;  // 16-byte words per 8 bounds
+    constexpr int BES = BF == FP32 ? 4 : 2;
     __shared__ float qsum[512], qabs[512];
     const int row = blockIdx.y;
     const int b = row / p.kv_heads;
@@ -151,15 +153,19 @@ __global__ __launch_bounds__(256) void quest_score_kernel(SelectParams p) {
     const int done = min(max(p.done[b], 0), p.max_done);
     const int p0 = blockIdx.x * p.chunk;
     const int p1 = min(p0 + p.chunk, p.max_done);
-    uint4 lw[SCORE_PASSES], hw[SCORE_PASSES];
+    uint4 lw[SCORE_PASSES][BW], hw[SCORE_PASSES][BW];
 #pragma unroll
     for (int k = 0; k < SCORE_PASSES; ++k) {
         const int page = p0 + k * per_pass + static_cast<int>(threadIdx.x) / L;
-        lw[k] = hw[k] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int w = 0; w < BW; ++w) lw[k][w] = hw[k][w] = make_uint4(0, 0, 0, 0);
         if (page < p1 && j < runs) {
             const int64_t at = b * p.sb_b + kvh * p.sb_h + static_cast<int64_t>(page) * p.sb_p + 8 * j;
-            lw[k] = *reinterpret_cast<const uint4*>(p.kmin + at);
-            hw[k] = *reinterpret_cast<const uint4*>(p.kmax + at);
+#pragma unroll
+            for (int w = 0; w < BW; ++w) {
+                lw[k][w] = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(p.kmin) + at * BES)[w];
+                hw[k][w] = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(p.kmax) + at * BES)[w];
+            }
         }
     }
     for (int d = threadIdx.x; d < p.head_dim; d += blockDim.x) {
@@ -171,7 +177,7 @@ __global__ __launch_bounds__(256) void quest_score_kernel(SelectParams p) {
             for (int u = 0; u < 8; ++u) {
                 const int r = r0 + u < rows ? r0 + u : r0;
                 const int g = r / p.queries, qi = r % p.queries;
-                x[u] = bf16_to_f32(p.q[b * p.sq_b + qi * p.sq_q + (kvh * p.groups + g) * p.sq_h + d]);
+                x[u] = elem_f32<QF>(p.q, b * p.sq_b + qi * p.sq_q + (kvh * p.groups + g) * p.sq_h + d);
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
@@ -190,12 +196,10 @@ __global__ __launch_bounds__(256) void quest_score_kernel(SelectParams p) {
         const int page = p0 + k * per_pass + static_cast<int>(threadIdx.x) / L;
         float s1 = 0.0f, s2 = 0.0f;
         if (j < runs) {
-            const uint32_t lo_w[4] = {lw[k].x, lw[k].y, lw[k].z, lw[k].w};
-            const uint32_t hi_w[4] = {hw[k].x, hw[k].y, hw[k].z, hw[k].w};
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const float lo = bf16_to_f32(static_cast<uint16_t>(lo_w[i >> 1] >> (16 * (i & 1))));
-                const float hi = bf16_to_f32(static_cast<uint16_t>(hi_w[i >> 1] >> (16 * (i & 1))));
+                const float lo = bound_of<BF>(lw[k], i);
+                const float hi = bound_of<BF>(hw[k], i);
                 const float mid = (lo + hi) * 0.5f;
                 const float half = (hi - lo) * 0.5f;
                 const float t1 = qsum[8 * j + i] * mid;
@@ -511,6 +515,24 @@ int quest_bounds(const BoundsParams& p, hipStream_t stream) {
     return check_launch("quest_bounds_kernel");
 }
 
+int quest_dense_bounds(const DenseBoundsParams& p, hipStream_t stream) {
+    if (p.last <= p.first) return 0;
+    dim3 grid(static_cast<unsigned>(p.batch) * (p.last - p.first), p.kv_heads);
+    switch (p.kv_format) {
+        case BF16: hipLaunchKernelGGL((quest_dense_bounds_kernel<BF16, BF16>), grid, dim3(64), 0, stream, p); break;
+        case FP16: hipLaunchKernelGGL((quest_dense_bounds_kernel<FP16, FP16>), grid, dim3(64), 0, stream, p); break;
+        case FP32: hipLaunchKernelGGL((quest_dense_bounds_kernel<FP32, FP32>), grid, dim3(64), 0, stream, p); break;
+        case FP8_E4M3:
+            hipLaunchKernelGGL((quest_dense_bounds_kernel<FP8_E4M3, BF16>), grid, dim3(64), 0, stream, p);
+            break;
+        case FP8_E5M2:
+            hipLaunchKernelGGL((quest_dense_bounds_kernel<FP8_E5M2, BF16>), grid, dim3(64), 0, stream, p);
+            break;
+        default: return fail("quest page bounds: keys must be bf16, fp16, fp32, fp8 e4m3 or fp8 e5m2");
+    }
+    return check_launch("quest_dense_bounds_kernel");
+}
+
 int quest_refresh(const BoundsParams& p, hipStream_t stream) {
     const int rows = p.batch * p.kv_heads;
     if (rows == 0) return 0;
@@ -532,7 +554,20 @@ int quest_select(const SelectParams& p, hipStream_t stream) {
     if (p.max_done > 0) {
         if (p.chunk != quest_score_chunk(p.head_dim)) return fail("quest select: score chunk does not match the head dim");
         dim3 grid((p.max_done + p.chunk - 1) / p.chunk, rows);
-        hipLaunchKernelGGL(quest_score_kernel, grid, dim3(256), 0, stream, p);
+        auto launch = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(256), 0, stream, p); };
+        const int formats = p.q_format * 8 + p.bounds_format;
+        switch (formats) {
+            case BF16 * 8 + BF16: launch(quest_score_kernel<BF16, BF16>); break;
+            case BF16 * 8 + FP16: launch(quest_score_kernel<BF16, FP16>); break;
+            case BF16 * 8 + FP32: launch(quest_score_kernel<BF16, FP32>); break;
+            case FP16 * 8 + BF16: launch(quest_score_kernel<FP16, BF16>); break;
+            case FP16 * 8 + FP16: launch(quest_score_kernel<FP16, FP16>); break;
+            case FP16 * 8 + FP32: launch(quest_score_kernel<FP16, FP32>); break;
+            case FP32 * 8 + BF16: launch(quest_score_kernel<FP32, BF16>); break;
+            case FP32 * 8 + FP16: launch(quest_score_kernel<FP32, FP16>); break;
+            case FP32 * 8 + FP32: launch(quest_score_kernel<FP32, FP32>); break;
+            default: return fail("quest select: queries and bounds must be bf16, fp16 or fp32");
+        }
         if (int rc = check_launch("quest_score_kernel")) return rc;
     }
     if (p.max_done <= TOPK_LDS_KEYS) {

@@ -27,11 +27,13 @@ struct BoundsParams {
 };
 
 struct SelectParams {
-    const uint16_t* q;  // bf16 [B, Q, Hq, D], channel stride 1
+    const void* q;  // [B, Q, Hq, D] in q_format (bf16, fp16, fp32), channel stride 1
     int64_t sq_b, sq_q, sq_h;
-    const uint16_t* kmin;  // bf16 [B, Hkv, P, D], channel stride 1
-    const uint16_t* kmax;
+    int q_format;
+    const void* kmin;  // [B, Hkv, P, D] in bounds_format (bf16, fp16, fp32), channel stride 1
+    const void* kmax;
     int64_t sb_b, sb_h, sb_p;
+    int bounds_format;
     const int32_t* done;  // [B] committed Quest pages of every row
     int max_done, pages;
     int first_page;   // nonzero: a row's page 0 is always selected (it scores +inf)
@@ -41,7 +43,21 @@ struct SelectParams {
     int chunk;        // pages scored per workgroup
 };
 
+// Page bounds over a dense key buffer [B, Hkv, S, D] (the reference's own cache layout).
+struct DenseBoundsParams {
+    const void* keys;  // format kv_format (bf16, fp16, fp32, fp8 e4m3 / e5m2), element strides sk_*, channel stride 1
+    int64_t sk_b, sk_h, sk_s;
+    int kv_format;
+    int first, last, page;  // pages [first, last) of `page` slots each
+    void* kmin;             // [B, Hkv, P, D] in bounds_format, element strides sb_*; page p at p * sb_p
+    void* kmax;
+    int64_t sb_b, sb_h, sb_p;
+    int bounds_format;  // bf16 for bf16 and fp8 keys, else the keys' format
+    int batch, kv_heads, head_dim;
+};
+
 int quest_bounds(const BoundsParams& p, hipStream_t stream);
+int quest_dense_bounds(const DenseBoundsParams& p, hipStream_t stream);
 int quest_refresh(const BoundsParams& p, hipStream_t stream);
 int quest_select(const SelectParams& p, hipStream_t stream);
 int quest_score_chunk(int head_dim);  // pages scored per workgroup

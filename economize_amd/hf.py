@@ -16,10 +16,12 @@ for the techniques of this path:
   kernel over codes and ring (kv_kivi_fused/fused.py:152-208). Configurations the paged KIVI cache cannot hold
   (8-bit codes, groups other than 32, other head dims or dtypes) use the simulated storage
   (:class:`SimulatedKIVILayer`: dense buffers quantized in place, kivi.py:178-275).
-* ``QuestConfig``: a paged cache (fp8 with an fp8 technique on the same layer is refused, as the reference refuses
-  Quest over packed formats) whose page bounds are kept for the committed pages, ``done[b]`` = committed full pages
-  before the pass; a decoding query of a covered layer reads the selected pages and the tail
-  (quest/technique.py:116-259).
+* ``QuestConfig``: on a bf16 model of head dim 64 / 128 / 256 a paged bf16 cache whose page bounds live on the
+  device (:class:`~economize_amd.quest.QuestState`: the append of a pass also computes the bounds of the pages
+  committed before it, one launch); on other models dense buffers of the model's dtype (:class:`DenseQuestLayer`,
+  bounds kept incrementally). ``done[b]`` = committed full pages before the pass; a decoding query of a covered layer
+  reads the selected pages and the tail (quest/technique.py:116-259), and a layer whose attached pages no attention
+  function read raises when it is written next (quest/technique.py:174-182).
 
 A layer of no technique keeps dense K/V (transformers' ``DynamicLayer``) and attends on the dense kernel.
 
@@ -42,13 +44,13 @@ from .fp8 import calibrate_kv_absmax, fp8_encode, static_scales
 from .kivi import KIVI_PAGE, PagedKIVICache, kivi_append, kivi_commit, kivi_fake_quantize, kivi_quantize
 from .packed import attach_packed, stand_in
 from .paged import PAGE, PagedKVCache, paged_append
-from .quest import QuestPages, page_bounds
+from .quest import QuestPages, QuestState, bounds_dtype, page_bounds
 from .techniques import (FP8KVConfig, FusedFP8KVConfig, KIVIConfig, QuestConfig, Technique, attn_implementation,
                          head_dim_of,
                          technique_for)
 
-__all__ = ["DenseFP8Layer", "EconomizeCache", "EconomizedModel", "KIVILayer", "PagedLayer", "SimulatedKIVILayer",
-           "apply"]
+__all__ = ["DenseFP8Layer", "DenseQuestLayer", "EconomizeCache", "EconomizedModel", "KIVILayer", "PagedLayer",
+           "SimulatedKIVILayer", "apply"]
 
 
 class _PagedBase(CacheLayerMixin):
@@ -128,19 +130,52 @@ class _PagedBase(CacheLayerMixin):
         self.length = self.committed = 0
 
 
-class PagedLayer(_PagedBase):
-    """One layer in a paged fp8 or bf16 cache (16-token pages), optionally with Quest's page bounds."""
+class _UnreadCheck:
+    """The reference's check that every attached page list was read (techniques/quest/technique.py:174-182): a Quest
+    layer notes an attachment and its reading; a layer whose attachment no attention function read (another
+    attention implementation, or a technique that copied the keys) raises when it is written next, so that Quest
+    never decodes densely without a word."""
+
+    def _init_unread(self, layer: int) -> None:
+        self.layer_idx = layer
+        self._unread = False
+
+    def _attached(self) -> None:
+        self._unread = True
+
+    def _read(self, layer: int) -> None:
+        self._unread = False
+
+    def _check_read(self) -> None:
+        if self._unread:
+            self._unread = False
+            raise IncompatibleTechniquesError(
+                f"quest attached pages to cache layer {self.layer_idx} that no attention function read: run the model "
+                "with attn_implementation='economize' (economize_amd.attention.install()) and let no technique copy "
+                "the keys after quest")
+
+
+class PagedLayer(_PagedBase, _UnreadCheck):
+    """One layer in a paged fp8 or bf16 cache (16-token pages), optionally with Quest's page bounds, which live in a
+    :class:`~economize_amd.quest.QuestState` on the device: the append of a pass also computes the bounds of the pages
+    the previous passes committed (one launch, ``eco_paged_append_quest``), and ``done`` is a device tensor."""
 
     def __init__(self, capacity: int, cache_dtype: torch.dtype | None, quest: QuestConfig | None = None,
-                 scales: tuple[torch.Tensor, torch.Tensor] | None = None) -> None:
+                 scales: tuple[torch.Tensor, torch.Tensor] | None = None, layer: int = 0) -> None:
         super().__init__(capacity, PAGE)
         self.cache_dtype = cache_dtype  # None: the model's dtype (bf16)
         self.quest = quest
         self.scales = scales  # fp32 [Hkv] key and value scales of an fp8 cache, or None
         self.cache: PagedKVCache | None = None
-        self.bounds: tuple[torch.Tensor, torch.Tensor] | None = None
-        self.valid = 0  # Quest pages whose bounds are final
+        self.state: QuestState | None = None
+        self._committed: dict[int, torch.Tensor] = {}
         self._write_width = 0
+        self._init_unread(layer)
+
+    @property
+    def bounds(self) -> tuple[torch.Tensor, torch.Tensor] | None:
+        """Quest's ``(kmin, kmax)`` bf16 ``[B, Hkv, pages, D]``; pages below ``committed // page_size`` are valid."""
+        return None if self.state is None else (self.state.kmin, self.state.kmax)
 
     def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
         batch, heads, _, dim = key_states.shape
@@ -151,20 +186,38 @@ class PagedLayer(_PagedBase):
         if self.scales is not None:
             k_scale, v_scale = (x.to(key_states.device, torch.float32).reshape(heads).contiguous() for x in self.scales)
         self.cache = PagedKVCache.empty(pages, heads, dim, dtype, key_states.device, k_scale, v_scale)
-        if self.quest is not None:
-            shape = (batch, heads, -(-self.capacity // self.quest.page_size), dim)
-            self.bounds = (torch.zeros(shape, dtype=torch.bfloat16, device=key_states.device),
-                           torch.zeros(shape, dtype=torch.bfloat16, device=key_states.device))
+        q = self.quest
+        if q is not None:
+            self.state = QuestState(batch, heads, dim, max(1, self.capacity // q.page_size), q.page_size, q.pages,
+                                    key_states.device, q.max_queries, q.first_page)
         self.is_initialized = True
 
+    def _committed_rows(self) -> torch.Tensor:
+        lens = self._committed.get(self.committed)
+        if lens is None:
+            self._committed = {self.committed: torch.full((self.table.shape[0],), self.committed, dtype=torch.int32,
+                                                          device=self.table.device)}
+            lens = self._committed[self.committed]
+        return lens
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs
+               ) -> tuple[torch.Tensor, torch.Tensor]:
+        self._check_read()
+        return super().update(key_states, value_states, *args, **kwargs)
+
     def transform_update(self, key_states, value_states):
-        """fp8_encode (or the bf16 rounding) of the new tokens into their pages, at positions ``length ..``."""
+        """fp8_encode (or the bf16 rounding) of the new tokens into their pages, at positions ``length ..``; with
+        Quest, the bounds of the pages committed since the last pass in the same launch."""
         batch, heads, tokens, dim = key_states.shape
         self._check_room(tokens)
         pos = torch.arange(self.length, self.length + tokens, device=key_states.device)
         slots = (self.table[:, pos // PAGE] * PAGE + pos % PAGE).to(torch.int32).reshape(-1)
-        paged_append(self.cache, key_states.transpose(1, 2).reshape(batch * tokens, heads, dim),
-                     value_states.transpose(1, 2).reshape(batch * tokens, heads, dim), slots)
+        k = key_states.transpose(1, 2).reshape(batch * tokens, heads, dim)
+        v = value_states.transpose(1, 2).reshape(batch * tokens, heads, dim)
+        if self.state is not None:
+            self.state.append(self.cache, k, v, slots, self.table, self._committed_rows())
+        else:
+            paged_append(self.cache, k, v, slots)
         self.length += tokens
         self._write_width = tokens
         return key_states, value_states
@@ -175,21 +228,106 @@ class PagedLayer(_PagedBase):
         pages = None
         q = self.quest
         if q is not None and self._write_width <= q.max_queries:
-            done = self.committed // q.page_size
+            done = min(self.committed // q.page_size, self.state.max_pages)
             if done > q.pages:
-                if self.valid < done:
-                    page_bounds(self.cache, self.table, self.valid, done, q.page_size, out=self.bounds)
-                    self.valid = done
-                done_t = torch.full((self.table.shape[0],), done, dtype=torch.int32, device=self.table.device)
-                pages = QuestPages(self.bounds[0], self.bounds[1], done_t, done, done, q.page_size, q.pages,
-                                   q.max_queries, q.first_page)
+                pages = QuestPages(self.state.kmin, self.state.kmax, self.state.done, done, done, q.page_size, q.pages,
+                                   max_queries=q.max_queries, on_use=self._read, layer=self.layer_idx,
+                                   first_page=q.first_page)
+                self._attached()
         handle = PagedKV(self.cache, self.table, self._seq_lens(), self.length, pages, self.model_dtype)
         keys, values = self._stand_ins(key_states)
         return attach_packed(keys, handle), values
 
     def reset(self) -> None:
         super().reset()
-        self.valid = 0
+        self._unread = False
+        if self.state is not None:
+            self.state.reset()
+
+
+class DenseQuestLayer(CacheLayerMixin, _UnreadCheck):
+    """Quest over dense ``[B, Hkv, capacity, D]`` K/V buffers of the model's dtype: the reference's own cache layout
+    (runtime/cache.py:359-432) under its ``QuestCache`` (techniques/quest/technique.py:116-259), for the models the
+    paged kernels do not take (fp16 / fp32, head dims other than 64 / 128 / 256). At a new pass every token before
+    it is committed (``done = committed // page_size``); a decoding query (at most ``max_queries`` tokens) of a layer
+    with more than ``pages`` committed pages gets the bounds of the committed pages (kept incrementally by
+    ``eco_quest_dense_bounds``) attached to its keys, and attends over the selected pages and the tail on the dense
+    decode kernel (``eco_quest_decode``)."""
+
+    is_sliding = False
+    is_compileable = False
+    supports_early_init = False
+
+    def __init__(self, capacity: int, config: QuestConfig, layer: int = 0) -> None:
+        super().__init__()
+        self.capacity = int(capacity)
+        self.config = config
+        self.length = self.committed = self.valid = 0
+        self.buffers: tuple[torch.Tensor, torch.Tensor] | None = None
+        self.bounds: tuple[torch.Tensor, torch.Tensor] | None = None
+        self._done: dict[int, torch.Tensor] = {}
+        self._init_unread(layer)
+
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        batch, heads, _, dim = key_states.shape
+        device = key_states.device
+        self.buffers = (torch.zeros(batch, heads, self.capacity, dim, dtype=key_states.dtype, device=device),
+                        torch.zeros(batch, heads, self.capacity, value_states.shape[3], dtype=value_states.dtype,
+                                    device=device))
+        shape = (batch, heads, max(1, self.capacity // self.config.page_size), dim)
+        dtype = bounds_dtype(key_states.dtype)
+        self.bounds = (torch.zeros(shape, dtype=dtype, device=device), torch.zeros(shape, dtype=dtype, device=device))
+        self.is_initialized = True
+
+    def get_seq_length(self) -> int:
+        return self.length
+
+    def get_mask_sizes(self, query_length: int) -> tuple[int, int]:
+        return self.length + query_length, 0
+
+    def get_max_length(self) -> int:
+        return self.capacity
+
+    def _done_rows(self, done: int) -> torch.Tensor:
+        rows = self._done.get(done)
+        if rows is None:
+            self._done = {done: torch.full((self.buffers[0].shape[0],), done, dtype=torch.int32,
+                                           device=self.buffers[0].device)}
+            rows = self._done[done]
+        return rows
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs
+               ) -> tuple[torch.Tensor, torch.Tensor]:
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        self._check_read()
+        if self.length > self.committed:
+            self.committed = self.length  # pass_begin: everything written before this pass is committed
+        tokens = key_states.shape[2]
+        if self.length + tokens > self.capacity:
+            raise ConfigError(f"the cache holds {self.capacity} tokens per row; writing {tokens} more after "
+                              f"{self.length} exceeds it (make the cache with a larger max_length)")
+        new = slice(self.length, self.length + tokens)
+        self.buffers[0][:, :, new].copy_(key_states)
+        self.buffers[1][:, :, new].copy_(value_states)
+        self.length += tokens
+        keys, values = (b[:, :, : self.length] for b in self.buffers)
+        c = self.config
+        done = self.committed // c.page_size
+        if tokens > c.max_queries or done <= c.pages:
+            return keys, values
+        if self.valid < done:  # the bounds of the pages committed since the last refresh
+            page_bounds(self.buffers[0], self.valid, done, c.page_size, out=self.bounds)
+            self.valid = done
+        pages = QuestPages(self.bounds[0], self.bounds[1], self._done_rows(done), done, done, c.page_size, c.pages,
+                           max_queries=c.max_queries, on_use=self._read, layer=self.layer_idx,
+                           first_page=c.first_page)
+        self._attached()
+        return attach_packed(keys, pages), values
+
+    def reset(self) -> None:
+        self.length = self.committed = self.valid = 0
+        self._unread = False
 
 
 class DenseFP8Layer(CacheLayerMixin):
@@ -488,6 +626,12 @@ class EconomizedModel:
         dtype = next(self.model.parameters()).dtype
         return dtype == torch.bfloat16 and head_dim_of(self.model) in (64, 128, 256) and config.scale != "token"
 
+    def paged_quest(self) -> bool:
+        """Whether Quest layers live in the paged bf16 cache (a bf16 model of head dim 64 / 128 / 256, which the paged
+        kernels take); else in dense buffers of the model's dtype (:class:`DenseQuestLayer`)."""
+        dtype = next(self.model.parameters()).dtype
+        return dtype == torch.bfloat16 and head_dim_of(self.model) in (64, 128, 256)
+
     def make_cache(self, max_length: int) -> EconomizeCache:
         """A cache for generations of up to ``max_length`` tokens per row (prompt included)."""
         config = self.model.config
@@ -504,8 +648,10 @@ class EconomizedModel:
             elif isinstance(cfg, FP8KVConfig):
                 layers.append(DenseFP8Layer(max_length, cfg, isinstance(cfg, FusedFP8KVConfig),
                                             self.scales.get(index)))
+            elif isinstance(cfg, QuestConfig) and self.paged_quest():
+                layers.append(PagedLayer(max_length, None, cfg, layer=index))
             elif isinstance(cfg, QuestConfig):
-                layers.append(PagedLayer(max_length, None, cfg))
+                layers.append(DenseQuestLayer(max_length, cfg, layer=index))
             else:
                 layers.append(DynamicLayer())
         return EconomizeCache(layers)

@@ -345,10 +345,14 @@ class QuestConfig(TechniqueConfig):
 
     def validate(self, adapter) -> None:
         """Refuses an attention implementation that does not read Quest pages (quest/technique.py:88-97) and head
-        dims the paged kernels do not take."""
+        dims no Quest kernel takes: the paged kernels take bf16 models of head dim 64 / 128 / 256, the dense ones any
+        dtype and any head dim up to 256 that is a multiple of 8."""
         from .attention import accepts_packed_kv
 
-        _head_dims(self.technique, adapter, (64, 128, 256))
+        dim = head_dim_of(adapter)
+        if dim is not None and (dim % 8 or dim > 256):
+            raise ConfigError(f"{self.technique}: the MI355X kernels take head dims that are multiples of 8 up to 256, "
+                              f"the model has {dim}")
         _needs_kernel(self.technique, attn_implementation(adapter), lambda name: accepts_packed_kv(name, "quest"),
                       "its pages", None)
 

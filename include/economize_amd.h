@@ -45,6 +45,25 @@ int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, in
                      void* v_cache, int32_t num_pages, int32_t kv_heads, int32_t head_dim, int32_t page_size,
                      int32_t cache_format, const float* k_scale, const float* v_scale, void* stream);
 
+/* eco_paged_append plus Quest's page bounds kept on the device, in one launch: the new tokens are appended as
+ * eco_paged_append does, and the bounds of the Quest pages each row b and KV head h committed since the last call
+ * (pages [valid[b * Hkv + h], min(committed[b] / quest_page_size, page_cap))) are computed as
+ * eco_quest_refresh_bounds does, after which valid advances and done[b] (optional) becomes the row's committed Quest
+ * pages. counters (int32 [B * Hkv]) must be zero before the first call; every call leaves them zero. The appended
+ * tokens must lie at or past the committed ones (the launch refreshes pages it does not write). tokens may be 0 (a
+ * refresh only). The launch shape depends on the arguments only, so a decode step can be captured in a graph.
+ * Replaces FP8Cache.transform_update (techniques/kv_quant/fp8.py:161-176) together with QuestCache.pass_begin and
+ * _layer_bounds (techniques/quest/technique.py:165-172, 229-259), whose host done list keeps the reference's Quest
+ * out of graphs (technique.py:311). */
+int eco_paged_append_quest(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
+                           int64_t sv_t, int64_t sv_h, const int32_t* slot_mapping, int32_t tokens, void* k_cache,
+                           void* v_cache, int32_t num_pages, int32_t kv_heads, int32_t head_dim, int32_t page_size,
+                           int32_t cache_format, const float* k_scale, const float* v_scale,
+                           const int32_t* block_table, int64_t bt_stride, int32_t bt_cols, const int32_t* committed,
+                           int32_t* valid, int32_t* done, int32_t* counters, int32_t quest_page_size, void* kmin,
+                           void* kmax, int64_t sb_b, int64_t sb_h, int64_t sb_p, int32_t page_cap, int32_t batch,
+                           void* stream);
+
 /* fp8 encode into a dense fp8 buffer (the fused fp8 cache's [B, H, S, D] buffers).
  * Replaces the reference's fp8_encode and token_scale (techniques/kv_quant/fp8.py:81-86, 95-97) as
  * FP8Cache.transform_update applies them (fp8.py:161-176): src [B, H, T, D] (element strides ss_b, ss_h, ss_t,
@@ -219,15 +238,53 @@ size_t eco_quest_select_workspace_size(int32_t batch, int32_t kv_heads, int32_t 
 
 /* Quest page selection: out[b, kvh, 0..pages) (int32, contiguous) = the pages of row b with the largest scores
  * sum_d qsum_d (lo + hi) / 2 + qabs_d (hi - lo) / 2 among its committed pages [0, done[b]) (pages >= max_done never),
- * min(pages, max_done) of them in increasing order, then -1; ties go to the lower page. qsum / qabs are the sums of
- * q / |q| (q [B, Q, Hq, D] bf16, element strides sq_*, channel stride 1) over the KV head's query rows; lo / hi are
- * the page bounds (bf16, 16-byte aligned, strides multiples of 8). Replaces select_pages (attention/quest.py:73-108).
+ * min(pages, max_done) of them in increasing order, then -1; ties go to the lower page. qsum / qabs are the fp32
+ * sums of q / |q| (q [B, Q, Hq, D] in q_format = bf16, fp16 or fp32, element strides sq_*, channel stride 1) over
+ * the KV head's query rows; lo / hi are the page bounds (bounds_format = bf16, fp16 or fp32, 16-byte aligned,
+ * strides multiples of 8 elements), all widened to fp32 exactly. Replaces select_pages (attention/quest.py:73-108).
  * first_page nonzero always selects a row's page 0 (it scores +inf), the "first and last pages" variant of Quest;
  * the reference has no such rule, so 0 gives its selection. */
-int eco_quest_select(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* kmin, const void* kmax,
-                     int64_t sb_b, int64_t sb_h, int64_t sb_p, const int32_t* done, int32_t max_done, int32_t pages,
-                     int32_t first_page, int32_t* out, int32_t batch, int32_t queries, int32_t q_heads,
-                     int32_t kv_heads, int32_t head_dim, void* workspace, size_t workspace_bytes, void* stream);
+int eco_quest_select(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* kmin,
+                     const void* kmax, int32_t bounds_format, int64_t sb_b, int64_t sb_h, int64_t sb_p,
+                     const int32_t* done, int32_t max_done, int32_t pages, int32_t first_page, int32_t* out,
+                     int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Quest page bounds over a dense key buffer (the reference's own cache layout): kmin / kmax [b, h, p, :] (element
+ * strides sb_*, channel stride 1; page p written at p * sb_p) of pages [first, last) of page_size slots (a power of
+ * two >= 16; last * page_size <= slots), the channel-wise smallest and largest key of keys [b, h, s, :] (element
+ * strides sk_*, channel stride 1; format kv_format = bf16, fp16, fp32 or fp8) with NaN propagated as torch's amin /
+ * amax do. bounds_format must be bounds_dtype's: bf16 for bf16 and fp8 keys (exact), else the keys' format.
+ * Replaces page_bounds and bounds_dtype (attention/quest.py:54-70) as QuestCache._layer_bounds calls them
+ * (techniques/quest/technique.py:229-259). */
+int eco_quest_dense_bounds(const void* keys, int32_t kv_format, int64_t sk_b, int64_t sk_h, int64_t sk_s,
+                           int32_t slots, int32_t first, int32_t last, int32_t page_size, void* kmin, void* kmax,
+                           int32_t bounds_format, int64_t sb_b, int64_t sb_h, int64_t sb_p, int32_t batch,
+                           int32_t kv_heads, int32_t head_dim, void* stream);
+
+/* Workspace bytes of eco_quest_decode: eco_decode_workspace_size over the virtual key axis
+ * pages * page_size + keys - min_done * page_size (at least 1), with eco_decode's counter rule. */
+size_t eco_quest_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads,
+                                       int32_t keys, int32_t pages, int32_t page_size, int32_t min_done,
+                                       int32_t head_dim, int32_t value_dim);
+
+/* Quest decode attention over dense K/V buffers: eco_decode over the virtual key axis of (row b, KV head h) made of
+ * the selected pages index[b, h, 0 .. pages) (element strides si_b, si_h; increasing, then -1; page i covers slots
+ * i * page_size .. + page_size) in slot order, then the dense tail, slots done[b] * page_size .. keys. The optional
+ * mask is over slots (a selected page's key carries its slot's mask column). min_done = min(done) on the host sizes
+ * the split plan; the launch shape is a function of the shapes and min_done. Everything else as eco_decode (query
+ * bf16 / fp16 / fp32, K/V in its format or fp8 with per-head scales, soft cap, sinks, a query that sees no key gives
+ * 0). Entries outside the buffer's whole pages are clamped (wrong results, no access outside a buffer). Replaces
+ * quest_decode_attention (attention/quest.py:239-344; kernel attention/_quest_kernels.py:13-97). */
+int eco_quest_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int64_t sq_q, const void* k,
+                     const void* v, int32_t kv_format, int64_t sk_b, int64_t sk_h, int64_t sk_s, int64_t sv_b,
+                     int64_t sv_h, int64_t sv_s, const float* k_scale, const float* v_scale, const int32_t* index,
+                     int64_t si_b, int64_t si_h, int32_t pages, const int32_t* done, int32_t page_size,
+                     int32_t min_done, const uint8_t* mask, int64_t sm_b, int64_t sm_h, int64_t sm_q, int64_t sm_s,
+                     const float* sinks, void* out, int64_t so_b, int64_t so_q, int64_t so_h, int32_t batch,
+                     int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys, int32_t head_dim,
+                     int32_t value_dim, float scale, float softcap, void* workspace, size_t workspace_bytes,
+                     void* stream);
 
 /* ---- KIVI (2- and 4-bit KV codes) --------------------------------------------------------------------------
  * Paged KIVI cache, per layer: blocks [num_pages, Hkv, eco_kivi_block_bytes] (one block per 32-token page and KV

@@ -54,7 +54,7 @@ def test_kivi_format() -> None:
 def test_quest_format_routes_by_query_length() -> None:
     from economize_amd.attention import PagedKV
     from economize_amd.paged import paged_decode_attention
-    from economize_amd.quest import QuestPages, page_bounds
+    from economize_amd.quest import QuestPages, paged_page_bounds
 
     lens = [2000, 1500]
     c = make_case(2, 1, 16, 4, 128, lens, torch.bfloat16, seed=12)
@@ -62,13 +62,13 @@ def test_quest_format_routes_by_query_length() -> None:
     table = torch.from_numpy(c.table).cuda()
     seq = torch.tensor(lens, dtype=torch.int32).cuda()
     done = np.array([(n - 1) // 16 for n in lens], np.int32)
-    kmin, kmax = page_bounds(cache, table, 0, int(done.max()), 16)
+    kmin, kmax = paged_page_bounds(cache, table, 0, int(done.max()), 16)
     qp = QuestPages(kmin, kmax, torch.from_numpy(done).cuda(), int(done.min()), int(done.max()), 16, 31)
     kv = PagedKV(cache, table, seq, max(lens), qp)
     assert kv.format == "quest"
     query = c.q.cuda().transpose(1, 2)
     out, _ = _forward()(None, query, kv, None, None)
-    assert torch.equal(out, qp.attend(query, cache, table, seq, max(lens)))
+    assert torch.equal(out, qp.attend_paged(query, cache, table, seq, max(lens)))
     # two queries per row exceed max_queries: dense attention over every key
     c2 = make_case(2, 2, 16, 4, 128, lens, torch.bfloat16, seed=12)
     query2 = c2.q.cuda().transpose(1, 2)

@@ -120,7 +120,7 @@ def test_kivi_int4_verification_at_b64_q8() -> None:
 def test_quest_at_b8_l32768_planted() -> None:
     from paged_cases import make_case, to_numpy_f32
 
-    from economize_amd.quest import QuestPages, page_bounds
+    from economize_amd.quest import QuestPages, paged_page_bounds
 
     batch, length, planted, budget = 8, 32768, 32, 1024
     c = make_case(batch, 1, HQ, HKV, D, [length] * batch, torch.bfloat16, seed=90)
@@ -138,12 +138,12 @@ def test_quest_at_b8_l32768_planted() -> None:
     done = np.full(batch, (length - 1) // PAGE, np.int32)
     max_done = int(done.max())
     pages = budget // PAGE - 1
-    kmin, kmax = page_bounds(cache, table, 0, max_done, PAGE)
+    kmin, kmax = paged_page_bounds(cache, table, 0, max_done, PAGE)
     qp = QuestPages(kmin, kmax, torch.from_numpy(done).cuda(), int(done.min()), max_done, PAGE, pages)
     query = c.q.cuda().transpose(1, 2)  # [B, Hq, 1, D]
     seq = torch.full((batch,), length, dtype=torch.int32, device="cuda")
     got_index = qp.select(query).cpu().numpy()
-    got = qp.attend(query, cache, table, seq, length).float().cpu().numpy()
+    got = qp.attend_paged(query, cache, table, seq, length).float().cpu().numpy()
 
     qn = q.transpose(0, 2, 1, 3)
     lo, hi = oquest.page_bounds(k, 0, max_done, PAGE)

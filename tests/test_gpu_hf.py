@@ -11,7 +11,8 @@ test_kv_kivi_fused.py:124-138). Three checks:
   caches' dense view (the gather kernels) and attend with ``sdpa`` (Quest: over the oracle's select_pages and the
   tail, attention/quest.py) gives the logits of the economize run within a stated tolerance;
 * that the paths run: the prompt (70 tokens, longer than the kernels take) on the fallback, every decoding step of a
-  covered layer on the paged kernels, as the usage log shows.
+  covered layer on the paged kernels (Quest on fp16 / fp32 models: the dense kernel's page list), as the usage log
+  shows.
 
 The dense runs of KIVI and Quest are not compared token for token: the later layers' K/V carry the rounding of the
 earlier layers' attention (a bf16 MFMA kernel against ``sdpa``), and a 2-bit code or a page choice that this rounding
@@ -35,14 +36,14 @@ pytestmark = pytest.mark.gpu
 PROMPT, STEPS = 70, 40
 
 
-def tiny_model(attn: str):
+def tiny_model(attn: str, dtype: torch.dtype = torch.bfloat16):
     from transformers import Qwen2Config, Qwen2ForCausalLM
 
     config = Qwen2Config(vocab_size=128, hidden_size=128, intermediate_size=256, num_hidden_layers=4,
                          num_attention_heads=4, num_key_value_heads=2, head_dim=64, max_position_embeddings=512,
                          tie_word_embeddings=True, initializer_range=0.2, attn_implementation=attn)
     torch.manual_seed(0)
-    model = Qwen2ForCausalLM(config).to(torch.bfloat16).cuda().eval()
+    model = Qwen2ForCausalLM(config).to(dtype).cuda().eval()
     model.requires_grad_(False)
     return model
 
@@ -145,31 +146,38 @@ class Mirror(CacheLayerMixin):
         return -1
 
     def update(self, key_states, value_states, *args, **kwargs):
+        from economize_amd.hf import DenseQuestLayer
         from economize_amd.packed import materialized_kv
 
         if isinstance(self.source, DynamicLayer):
             return self.source.keys, self.source.values
-        keys, values = materialized_kv(*self.source.transform_read(key_states, value_states))
+        if isinstance(self.source, DenseQuestLayer):
+            keys, values = (b[:, :, : self.source.length] for b in self.source.buffers)
+        else:
+            keys, values = materialized_kv(*self.source.transform_read(key_states, value_states))
+            if getattr(self.source, "quest", None) is not None:
+                self.source._read(self.source.layer_idx)  # the mirror reads the same pages (through the oracle)
         keys = keys.view(keys.shape)
         if self.selected is not None:
             keys._quest = self.selected
         return keys, values
 
 
-def mirrored_decode(configs, attn: str) -> tuple[list[float], list[float], set, int]:
+def mirrored_decode(configs, attn: str, dtype: torch.dtype = torch.bfloat16
+                    ) -> tuple[list[float], list[float], set, int]:
     """Greedy decoding on the economize caches; after every pass the mirror model runs the same tokens over the
     caches' dense view. Every Quest selection of the economize pass is checked against the oracle's select_pages on
     the same query and bounds, and the mirror attends over the pages it chose. Returns each decoding step's largest
     logit difference, the mirror's top-2 gap at that step, the kernel paths the economize passes took and the number
     of selections checked."""
     from economize_amd.attention import kernel_usage
-    from economize_amd.hf import apply
+    from economize_amd.hf import DenseQuestLayer, apply
     from economize_amd.quest import QuestPages
 
-    model = tiny_model("sdpa")
+    model = tiny_model("sdpa", dtype)
     em = apply(model, *configs)
     cache = em.make_cache(PROMPT + STEPS + 1)
-    mirror_model = tiny_model(attn)
+    mirror_model = tiny_model(attn, dtype)
     layers = [Mirror(layer) for layer in cache.layers]
     mirror = Cache(layers=layers)
     selections = []
@@ -189,7 +197,8 @@ def mirrored_decode(configs, attn: str) -> tuple[list[float], list[float], set, 
             for step in range(STEPS + 1):
                 selections.clear()
                 out = model(input_ids=ids, past_key_values=cache, use_cache=True)
-                quest_layers = [m for m in layers if getattr(m.source, "quest", None) is not None]
+                quest_layers = [m for m in layers if isinstance(m.source, DenseQuestLayer) or
+                                getattr(m.source, "quest", None) is not None]
                 for layer in layers:
                     layer.tokens, layer.selected = ids.shape[1], None
                 if selections:
@@ -274,14 +283,18 @@ def test_kivi_first_layer_holds_the_fake_quantization(bits: int) -> None:
 LOGIT_TOL = 0.5
 
 
-@pytest.mark.parametrize("technique", ["fp8", "kivi2", "kivi4", "quest"])
+@pytest.mark.parametrize("technique", ["fp8", "kivi2", "kivi4", "quest", "quest_fp16", "quest_fp32"])
 def test_decoding_logits_match_sdpa_over_the_cache(technique: str) -> None:
     from transformers import AttentionInterface
     from transformers.masking_utils import AttentionMaskInterface
 
     from economize_amd.techniques import FusedFP8KVConfig, FusedKIVIConfig, QuestConfig
 
-    attn, path = "sdpa", "kernel_fp8"
+    attn, path, dtype = "sdpa", "kernel_fp8", torch.bfloat16
+    if technique == "quest_fp16":
+        dtype = torch.float16
+    elif technique == "quest_fp32":
+        dtype = torch.float32
     if technique == "fp8":
         configs = (FusedFP8KVConfig(),)
     elif technique.startswith("kivi"):
@@ -292,10 +305,10 @@ def test_decoding_logits_match_sdpa_over_the_cache(technique: str) -> None:
         attn, path = "quest_oracle", "kernel_quest"
         AttentionInterface.register("quest_oracle", quest_oracle_forward)
         AttentionMaskInterface.register("quest_oracle", AttentionMaskInterface._global_mapping["sdpa"])
-    deltas, gaps, paths, checked = mirrored_decode(configs, attn)
+    deltas, gaps, paths, checked = mirrored_decode(configs, attn, dtype)
     print(technique, "max delta", max(deltas), "deltas", [round(d, 4) for d in deltas])
     assert (path, 1) in paths and ("sdpa", PROMPT) in paths
-    if technique == "quest":
+    if technique.startswith("quest"):  # (fp16 / fp32 models keep dense buffers: the dense kernel's page list)
         assert ("kernel", 1) in paths  # the dense first layer: the dense kernel
         # every decoding step commits at least 70 tokens, 4 full 16-token pages > 3 read: 3 covered layers select
         assert checked == 3 * STEPS
@@ -434,3 +447,131 @@ def test_the_hip_path_decodes_the_reference_kivi_golden_tokens() -> None:
     assert golden_greedy(model, cache, "cuda") == golden.GOLDEN["kv_kivi_2bit_tokens"].tolist()
     assert {(r["path"], r["queries"]) for r in kernel_usage(reset=True)} >= {("kernel", 1)}
     assert (cache.layers[0].kq, cache.layers[0].vq) == (32, 31)  # 39 committed tokens before the last pass
+
+
+def test_the_hip_path_decodes_the_reference_quest_golden_tokens() -> None:
+    """The reference's own golden tokens of ``QuestConfig(page_size=16, token_budget=32, dense_layers=0)``
+    (tests/golden/catalog.py:195-207) from its golden model on the GPU: float32 at head dim 16, so the layers keep
+    dense buffers (:class:`DenseQuestLayer`) with their bounds computed by ``eco_quest_dense_bounds``, and every
+    decoding step past two committed pages selects its page by ``eco_quest_select`` and attends over it and the tail
+    by ``eco_quest_decode``."""
+    import test_golden_reference as golden
+
+    from economize_amd.attention import kernel_usage
+    from economize_amd.hf import DenseQuestLayer, apply
+    from economize_amd.techniques import QuestConfig
+
+    model = golden.golden_model().cuda()
+    em = apply(model, QuestConfig(page_size=16, token_budget=32, dense_layers=0))
+    cache = em.make_cache(golden.PROMPT + golden.NEW_TOKENS + 1)
+    assert all(isinstance(layer, DenseQuestLayer) for layer in cache.layers)
+    kernel_usage(reset=True)
+    assert golden_greedy(model, cache, "cuda") == golden.GOLDEN["kv_quest_tokens"].tolist()
+    usage = kernel_usage(reset=True)
+    quest_calls = sum(row["calls"] for row in usage if row["path"] == "kernel_quest")
+    # steps at 32 .. 39 committed tokens: two committed pages, more than the one page read, in each of 6 layers
+    assert quest_calls == 6 * (golden.PROMPT + golden.NEW_TOKENS - 32)
+    assert {(row["path"], row["queries"]) for row in usage} >= {("kernel", 1), ("kernel_quest", 1)}
+
+
+def _quest_call(layer: int, dtype: torch.dtype, paged: bool):
+    """A decoding call of a Quest layer: the module, a query, and K/V carrying the layer's pages (a paged bf16 cache's
+    handle, or QuestPages on dense buffers), with the oracle's inputs."""
+    from economize_amd.attention import PagedKV
+    from economize_amd.packed import attach_packed, stand_in
+    from economize_amd.paged import PAGE, PagedKVCache, paged_append
+    from economize_amd.quest import QuestPages, page_bounds, paged_page_bounds
+
+    model = tiny_model("economize", dtype)
+    module = model.model.layers[layer].self_attn
+    gen = torch.Generator().manual_seed(layer)
+    batch, hq, hkv, slots, d, page, pages = 2, 4, 2, 300, 64, 16, 4
+    q = torch.randn(batch, hq, 1, d, generator=gen).to(dtype).cuda()
+    k = torch.randn(batch, hkv, slots, d, generator=gen).to(dtype).cuda()
+    v = torch.randn(batch, hkv, slots, d, generator=gen).to(dtype).cuda()
+    done = slots // page
+    done_t = torch.full((batch,), done, dtype=torch.int32, device="cuda")
+    if not paged:
+        kmin, kmax = page_bounds(k, 0, done, page)
+        qp = QuestPages(kmin, kmax, done_t, done, done, page, pages)
+        return module, q, attach_packed(k, qp), v, k, v, qp
+    table = torch.arange(batch * -(-slots // PAGE), dtype=torch.int32, device="cuda").view(batch, -1)
+    cache = PagedKVCache.empty(table.numel(), hkv, d, torch.bfloat16, "cuda")
+    pos = torch.arange(slots, device="cuda")
+    slot_ids = (table[:, pos // PAGE] * PAGE + pos % PAGE).to(torch.int32).reshape(-1)
+    paged_append(cache, k.transpose(1, 2).reshape(-1, hkv, d), v.transpose(1, 2).reshape(-1, hkv, d), slot_ids)
+    kmin, kmax = paged_page_bounds(cache, table, 0, done, page)
+    qp = QuestPages(kmin, kmax, done_t, done, done, page, pages)
+    lens = torch.full((batch,), slots, dtype=torch.int32, device="cuda")
+    handle = PagedKV(cache, table, lens, slots, qp, dtype)
+    stand = stand_in((batch, hkv, slots, d), dtype, q.device)
+    return module, q, attach_packed(stand, handle), stand, k, v, qp
+
+
+@pytest.mark.parametrize("paged", [False, True])
+@pytest.mark.parametrize("why", ["output_attentions", "float_mask"])
+def test_a_quest_call_that_falls_back_reads_the_selected_pages_only(paged: bool, why: str) -> None:
+    """A Quest call the kernels do not run (attention weights asked for: the model's eager function; an additive
+    float mask: sdpa) hides the unselected pages in its mask before it attends, as the reference's fallback does
+    (interface.py:216-222, QuestPages.restrict_mask): its output equals the oracle's quest_reference over the same
+    pages, not the dense attention."""
+    from economize_amd.attention import economize_attention_forward, kernel_usage
+    from oracle.attention import reference_attention
+
+    dtype = torch.bfloat16
+    module, q, key, value, k, v, qp = _quest_call(1, dtype, paged)
+    kwargs, mask = {}, None
+    if why == "output_attentions":
+        kwargs["output_attentions"] = True
+    else:
+        mask = torch.zeros(q.shape[0], 1, 1, k.shape[2], dtype=dtype, device="cuda")
+    kernel_usage(reset=True)
+    got, _ = economize_attention_forward(module, q, key, value, mask, scaling=0.125, **kwargs)
+    assert [row["reason"] for row in kernel_usage(reset=True)] == [why]
+    index = qp.select(q).cpu().numpy()
+    f = lambda t: t.float().cpu().numpy()  # noqa: E731
+    done = qp.done.cpu().numpy()
+    want = oquest.quest_reference(f(q), f(k), f(v), None, 0.125, index, done, qp.page)
+    np.testing.assert_allclose(got.float().cpu().numpy(), want, atol=2e-2, rtol=2e-2)
+    dense = reference_attention(f(q), f(k), f(v), None, 0.125)
+    assert np.abs(want - dense).max() > 0.05  # the restriction is visible at this tolerance
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_quest_on_dense_buffers_runs_on_the_kernel(dtype) -> None:
+    """The forward routes a dense key carrying QuestPages (an fp16 / fp32 model's Quest layer) to eco_quest_decode
+    (path "kernel_quest"), within atol 2e-3 / rtol 1e-2 of the oracle."""
+    from economize_amd.attention import economize_attention_forward, kernel_usage
+
+    module, q, key, value, k, v, qp = _quest_call(2, dtype, paged=False)
+    kernel_usage(reset=True)
+    got, _ = economize_attention_forward(module, q, key, value, None, scaling=0.125)
+    assert [(row["path"], row["reason"]) for row in kernel_usage(reset=True)] == [("kernel_quest", "")]
+    f = lambda t: t.float().cpu().numpy()  # noqa: E731
+    want = oquest.quest_reference(f(q), f(k), f(v), None, 0.125, qp.select(q).cpu().numpy(), qp.done.cpu().numpy(),
+                                  qp.page)
+    np.testing.assert_allclose(got.float().cpu().numpy(), want, atol=2e-3, rtol=1e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_quest_pages_no_attention_function_read_raise(dtype) -> None:
+    """The reference's unread-pages check (techniques/quest/technique.py:174-182): a Quest layer whose attached pages
+    no attention function read (the model switched to sdpa after apply) raises when it is written next, instead of
+    decoding densely without a word; with the economize kernel the same steps run."""
+    from economize_amd.errors import IncompatibleTechniquesError
+    from economize_amd.hf import apply
+    from economize_amd.techniques import QuestConfig
+
+    model = tiny_model("sdpa", dtype)
+    em = apply(model, QuestConfig(page_size=16, token_budget=32, dense_layers=0))
+    ids = prompt()
+    with torch.no_grad():
+        greedy(model, em.make_cache(PROMPT + 4), ids, 3)  # the economize kernel reads every attachment
+        model.set_attn_implementation("sdpa")
+        cache = em.make_cache(PROMPT + 4)
+        out = model(input_ids=ids, past_key_values=cache, use_cache=True)  # the prompt: nothing attached
+        token = out.logits[:, -1].argmax(-1, keepdim=True)
+        model(input_ids=token, past_key_values=cache, use_cache=True)  # pages attached, read by nobody
+        with pytest.raises(IncompatibleTechniquesError, match="no attention function read"):
+            model(input_ids=token, past_key_values=cache, use_cache=True)
+    model.set_attn_implementation("economize")

@@ -35,14 +35,14 @@ def _stored_keys(case) -> np.ndarray:
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn, torch.float8_e5m2])
 @pytest.mark.parametrize("page", [16, 32])
 def test_page_bounds_match_the_oracle(dtype, page) -> None:
-    from economize_amd.quest import page_bounds
+    from economize_amd.quest import paged_page_bounds
 
     lens = [700, 64, 1025, 130]
     c = make_case(4, 1, 16, 4, 128, lens, dtype, seed=31)
     cache = c.device_cache()
     table = torch.from_numpy(c.table).cuda()
     last = max(lens) // page
-    kmin, kmax = page_bounds(cache, table, 0, last, page)
+    kmin, kmax = paged_page_bounds(cache, table, 0, last, page)
     torch.cuda.synchronize()
     want_lo, want_hi = oquest.page_bounds(_stored_keys(c), 0, last, page)
     got_lo, got_hi = kmin.float().cpu().numpy(), kmax.float().cpu().numpy()
@@ -55,14 +55,14 @@ def test_page_bounds_match_the_oracle(dtype, page) -> None:
 def test_page_bounds_update_a_window_in_place() -> None:
     """Bounds of pages [first, last) written into existing tensors, the others untouched (the incremental update of
     techniques/quest/technique.py:229-259)."""
-    from economize_amd.quest import page_bounds
+    from economize_amd.quest import paged_page_bounds
 
     c = make_case(2, 1, 8, 2, 64, [512, 400], torch.float8_e4m3fn, seed=3)
     cache = c.device_cache()
     table = torch.from_numpy(c.table).cuda()
     kmin = torch.full((2, 2, 32, 64), 7.0, dtype=torch.bfloat16, device="cuda")
     kmax = kmin.clone()
-    page_bounds(cache, table, 5, 20, 16, out=(kmin, kmax))
+    paged_page_bounds(cache, table, 5, 20, 16, out=(kmin, kmax))
     want_lo, want_hi = oquest.page_bounds(_stored_keys(c), 0, 25, 16)
     lo = kmin.float().cpu().numpy()
     assert np.array_equal(lo[:, :, 5:20], want_lo[:, :, 5:20])
@@ -158,7 +158,7 @@ def test_no_committed_pages_selects_nothing() -> None:
 
 @pytest.mark.parametrize("dtype,page", [(torch.bfloat16, 16), (torch.float8_e4m3fn, 16), (torch.bfloat16, 32)])
 def test_quest_attention_matches_the_oracle(dtype, page) -> None:
-    from economize_amd.quest import QuestPages, page_bounds
+    from economize_amd.quest import QuestPages, paged_page_bounds
 
     lens = [3000, 900, 2500]
     c = make_case(3, 1, 32, 8, 128, lens, dtype, seed=41 + page)
@@ -168,10 +168,10 @@ def test_quest_attention_matches_the_oracle(dtype, page) -> None:
     done = np.array([(n - 1) // page for n in lens], np.int32)
     max_done = int(done.max())
     pages = 1024 // page - 1
-    kmin, kmax = page_bounds(cache, table, 0, max_done, page)
+    kmin, kmax = paged_page_bounds(cache, table, 0, max_done, page)
     qp = QuestPages(kmin, kmax, torch.from_numpy(done).cuda(), int(done.min()), max_done, page, pages)
     query = c.q.cuda().transpose(1, 2)  # [B, Hq, 1, D]
-    got = qp.attend(query, cache, table, seq, max(lens)).float().cpu().numpy()
+    got = qp.attend_paged(query, cache, table, seq, max(lens)).float().cpu().numpy()
     q = to_numpy_f32(c.q).transpose(0, 2, 1, 3)
     lo, hi = oquest.page_bounds(_stored_keys(c), 0, max_done, page)
     index = oquest.select_pages(q, lo, hi, done, max_done, pages)
@@ -186,7 +186,7 @@ def test_planted_workload_selection_matches_the_oracle() -> None:
     """The Quest decode workload: keys of 32 planted pages per (row, KV head) are the group's first query plus
     0.1 N(0, 1). The selection equals the oracle's. (Quest's score is an upper bound: a planted page's keys are
     close together, so its bound's width term is small, and random pages with wide bounds can outrank it.)"""
-    from economize_amd.quest import page_bounds, select_pages
+    from economize_amd.quest import paged_page_bounds, select_pages
 
     batch, hq, hkv, d, length, page = 2, 32, 8, 128, 4096, 16
     c = make_case(batch, 1, hq, hkv, d, [length] * batch, torch.bfloat16, seed=9)
@@ -201,7 +201,7 @@ def test_planted_workload_selection_matches_the_oracle() -> None:
     cache = c.device_cache()
     table = torch.from_numpy(c.table).cuda()
     done = np.full(batch, (length - 1) // page, np.int32)
-    kmin, kmax = page_bounds(cache, table, 0, int(done[0]), page)
+    kmin, kmax = paged_page_bounds(cache, table, 0, int(done[0]), page)
     got = select_pages(c.q.cuda().transpose(1, 2), kmin, kmax, torch.from_numpy(done).cuda(), int(done[0]), 63)
     lo, hi = oquest.page_bounds(bf16_bits_to_f32(c.k_codes), 0, int(done[0]), page)
     want = oquest.select_pages(q.transpose(0, 2, 1, 3), lo, hi, done, int(done[0]), 63)
@@ -211,7 +211,7 @@ def test_planted_workload_selection_matches_the_oracle() -> None:
 def test_quest_attention_with_a_mask() -> None:
     """A mask hides keys of the selected pages and of the tail alike (the reference's Quest kernel reads the mask,
     attention/_quest_kernels.py:55-87)."""
-    from economize_amd.quest import QuestPages, page_bounds
+    from economize_amd.quest import QuestPages, paged_page_bounds
 
     lens, page = [3000, 900, 2500], 16
     c = make_case(3, 1, 32, 8, 128, lens, torch.float8_e4m3fn, seed=43)
@@ -220,11 +220,11 @@ def test_quest_attention_with_a_mask() -> None:
     seq = torch.tensor(lens, dtype=torch.int32).cuda()
     done = np.array([(n - 1) // page for n in lens], np.int32)
     max_done = int(done.max())
-    kmin, kmax = page_bounds(cache, table, 0, max_done, page)
+    kmin, kmax = paged_page_bounds(cache, table, 0, max_done, page)
     qp = QuestPages(kmin, kmax, torch.from_numpy(done).cuda(), int(done.min()), max_done, page, 63)
     mask = np.random.default_rng(44).random((3, 1, 1, max(lens))) < 0.7
     query = c.q.cuda().transpose(1, 2)
-    got = qp.attend(query, cache, table, seq, max(lens), mask=torch.from_numpy(mask).cuda()).float().cpu().numpy()
+    got = qp.attend_paged(query, cache, table, seq, max(lens), mask=torch.from_numpy(mask).cuda()).float().cpu().numpy()
     q = to_numpy_f32(c.q).transpose(0, 2, 1, 3)
     lo, hi = oquest.page_bounds(_stored_keys(c), 0, max_done, page)
     index = oquest.select_pages(q, lo, hi, done, max_done, 63)

@@ -3,7 +3,8 @@ the bounds of committed pages equal the oracle's page_bounds as rows grow by sin
 (techniques/quest/technique.py:229-259: pages below ``done`` are final once computed), ``done`` follows
 ``committed // page``, the selection with the static ``max_done`` equals the one with the batch's true maximum, and
 a whole decode step (append, bounds refresh, selection, page-list attention) captured in a HIP graph gives the eager
-result at every replay while the rows grow."""
+result at every replay while the rows grow; the append that refreshes the bounds in its own launch
+(``eco_paged_append_quest``) equals the append and the refresh as two launches."""
 
 from __future__ import annotations
 
@@ -62,6 +63,42 @@ def test_refresh_keeps_the_committed_bounds_of_the_oracle(dtype, page) -> None:
             assert np.array_equal(kmin[b, :, : done[b]], lo[0]) and np.array_equal(kmax[b, :, : done[b]], hi[0])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("page", [16, 32])
+def test_the_append_with_the_refresh_equals_the_two_launches(dtype, page) -> None:
+    """eco_paged_append_quest (one launch) against eco_paged_append + eco_quest_refresh_bounds on a twin cache: the
+    same cache bytes, bounds, valid pages and done at every step, with the counters left zero, while rows grow by
+    single tokens, by jumps (a prompt's pages at once) and not at all (a refresh with nothing appended)."""
+    from economize_amd.paged import paged_append
+    from economize_amd.quest import QuestState
+
+    (c0, t0, keys, values), (c1, t1, _, _) = make_cache(dtype, seed=3 + page), make_cache(dtype, seed=3 + page)
+    assert torch.equal(t0, t1)
+    s0 = QuestState(B, HKV, D, CAP // page, page, 3, "cuda")
+    s1 = QuestState(B, HKV, D, CAP // page, page, 3, "cuda")
+    gen = torch.Generator().manual_seed(page)
+    committed = np.zeros(B, np.int64)
+    tab = t0.cpu()
+    for step, grow in enumerate([(0, 0, 0), (70, 3, 200), (1, 1, 1), (0, 0, 0), (40, 300, 5), (16, 16, 16)]):
+        committed = np.minimum(committed + np.array(grow), CAP - 1)
+        tokens = step % 3  # new tokens per row at positions committed .. (the tokens of this pass)
+        pos = [[min(int(committed[b]) + i, CAP - 1) for i in range(tokens)] for b in range(B)]
+        slots = torch.tensor([int(tab[b, p // 16]) * 16 + p % 16 for b in range(B) for p in pos[b]],
+                             dtype=torch.int32).cuda()
+        k_new = torch.randn(B * tokens, HKV, D, generator=gen).to(torch.bfloat16).cuda()
+        v_new = torch.randn(B * tokens, HKV, D, generator=gen).to(torch.bfloat16).cuda()
+        lens = torch.tensor(committed, dtype=torch.int32).cuda()
+        paged_append(c0, k_new, v_new, slots)
+        s0.refresh(c0, t0, lens)
+        s1.append(c1, k_new, v_new, slots, t1, lens)
+        torch.cuda.synchronize()
+        assert torch.equal(c0.keys, c1.keys) and torch.equal(c0.values, c1.values), step
+        for name in ("kmin", "kmax", "valid", "done"):
+            assert torch.equal(getattr(s0, name), getattr(s1, name)), (step, name)
+        assert int(s1.counters.abs().sum()) == 0
+    assert s1.done.cpu().tolist() == (committed // page).tolist()
+
+
 def test_static_max_done_selects_as_the_true_maximum() -> None:
     from economize_amd.quest import QuestState, select_pages
 
@@ -79,12 +116,13 @@ def test_static_max_done_selects_as_the_true_maximum() -> None:
     assert got[2].cpu().tolist() == [[0, 1, 2, 3, -1]] * HKV
 
 
-def test_a_captured_quest_decode_step_replays_like_the_eager_one() -> None:
-    """Each replay appends one token per row, refreshes the bounds, selects and attends, all from device buffers
-    filled between replays (the graph holds no host count); an identical eager pipeline on a twin cache gives the
-    same bits at every step, across page boundaries of every row."""
+@pytest.mark.parametrize("fused", [False, True])
+def test_a_captured_quest_decode_step_replays_like_the_eager_one(fused: bool) -> None:
+    """Each replay appends one token per row, refreshes the bounds (in the append's launch when fused), selects and
+    attends, all from device buffers filled between replays (the graph holds no host count); an identical eager
+    pipeline on a twin cache gives the same bits at every step, across page boundaries of every row."""
     from economize_amd.paged import paged_append
-    from economize_amd.quest import QuestState, quest_decode_attention
+    from economize_amd.quest import QuestState, paged_quest_decode_attention
 
     page, pages = 16, 3
     caches, states = [], []
@@ -106,10 +144,13 @@ def test_a_captured_quest_decode_step_replays_like_the_eager_one() -> None:
     out = torch.zeros(B, 1, HQ, D, dtype=torch.bfloat16, device="cuda")
 
     def step(cache, table, state, out_buf):
-        paged_append(cache, k_new, v_new, slots)
-        state.refresh(cache, table, committed)
-        quest_decode_attention(q.transpose(1, 2), cache, table, seq_lens, CAP, state.pages_handle(),
-                               out=out_buf)
+        if fused:
+            state.append(cache, k_new, v_new, slots, table, committed)
+        else:
+            paged_append(cache, k_new, v_new, slots)
+            state.refresh(cache, table, committed)
+        paged_quest_decode_attention(q.transpose(1, 2), cache, table, seq_lens, CAP, state.pages_handle(),
+                                     out=out_buf)
 
     def fill(length: torch.Tensor, table: torch.Tensor) -> None:
         q.copy_(torch.randn(B, 1, HQ, D, generator=gen).to(torch.bfloat16))

@@ -135,3 +135,22 @@ def test_kivi_layers_are_paged_where_the_paged_cache_holds_them() -> None:
         "SimulatedKIVILayer"
     assert layer_type(tiny_model(head_dim=16).to(torch.bfloat16), KIVIConfig()) == "SimulatedKIVILayer"
     assert layer_type(tiny_model(), FusedKIVIConfig()) == "SimulatedKIVILayer"  # float32
+
+
+def test_quest_layers_are_paged_where_the_paged_kernels_take_the_model() -> None:
+    """Quest on a bf16 model of head dim 64 / 128 / 256 keeps its layers in the paged bf16 cache; fp16 / fp32 models
+    and other head dims keep dense buffers of the model's dtype (the dense kernel's page list), and head dims the
+    kernels do not take are refused before anything attaches."""
+    from economize_amd.hf import DenseQuestLayer, PagedLayer, apply
+
+    def layer_types(model) -> list[str]:
+        cache = apply(model, QuestConfig(dense_layers=1)).make_cache(64)
+        return [type(layer).__name__ for layer in cache.layers[:2]]
+
+    assert layer_types(tiny_model().to(torch.bfloat16)) == ["DynamicLayer", "PagedLayer"]
+    assert layer_types(tiny_model().to(torch.float16)) == ["DynamicLayer", "DenseQuestLayer"]
+    assert layer_types(tiny_model()) == ["DynamicLayer", "DenseQuestLayer"]  # float32
+    assert layer_types(tiny_model(head_dim=32).to(torch.bfloat16)) == ["DynamicLayer", "DenseQuestLayer"]
+    with pytest.raises(ConfigError, match="multiples of 8 up to 256"):
+        apply(tiny_model(head_dim=512), QuestConfig())
+    assert PagedLayer and DenseQuestLayer
