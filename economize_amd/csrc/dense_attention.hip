@@ -406,7 +406,9 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
                 vcw[i] = *reinterpret_cast<const uint4*>(vc + p.cell_off_vc + 16 * (CB / 2) * (lane & 1) + 16 * i);
             vsz = *reinterpret_cast<const uint4*>(vc + p.cell_off_vs);
             vfl = *(vc + p.cell_off_flag + 1);
-            vaux = *reinterpret_cast<const uint4*>(cell_row(min(t0 + (lane & 31), t_end - 1)) + p.cell_off_ka);
+            // (every cell of the tile's key group: the tile's 32 cells lie in one page, page_size being a multiple
+            // of 32, and a visible key's group aux may sit in a cell past the row's keys)
+            vaux = *reinterpret_cast<const uint4*>(cell_row(t0 + (lane & 31)) + p.cell_off_ka);
 #pragma unroll
             for (int v = 0; v < 2; ++v) {
                 const uint8_t* krow = cell_row(min(t0 + 8 * (n >> 2) + 4 * v + (n & 3), t_end - 1));

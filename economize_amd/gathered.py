@@ -25,15 +25,18 @@ __all__ = ["GatheredKV", "gathered_decode_attention"]
 
 @dataclass
 class GatheredKV:
-    """Compacted prompt entries of one layer (a packed K/V of format ``"gathered"``, attention/gathered.py:39-64).
+    """One layer's prompt after an eviction kept part of it: the attachment of format ``"gathered"`` that
+    :func:`gathered_decode_attention` reads (the reference's GatheredKV fields, attention/gathered.py:39-64).
 
     Attributes:
-        key: ``[B, Hkv, C, D]`` kept prompt keys of every row and KV head, in slot order (``C >= count[b, h]``).
-        value: ``[B, Hkv, C, Dv]`` the matching values.
-        index: int32 ``[B, Hkv, C]`` original slot of every compact entry (its mask column).
-        count: int32 ``[B, Hkv]`` compact entries of every row and KV head.
-        start: int32 ``[B]`` first dense slot read for row ``b``.
-        dropped: ``min(start[b] - count[b, h])``, on the host: the virtual key axis is ``keys - dropped`` long.
+        key: ``[B, Hkv, C, D]``: row ``b`` and KV head ``h`` keep their surviving prompt keys in the first
+            ``count[b, h]`` entries, in slot order; the entries past the count are never read.
+        value: ``[B, Hkv, C, Dv]``: the values of those entries.
+        index: int32 ``[B, Hkv, C]``: the slot each kept entry came from, which is the mask column it is read with.
+        count: int32 ``[B, Hkv]``: how many entries each row and KV head kept.
+        start: int32 ``[B]``: the first slot of row ``b`` read from the dense buffers (the end of its prompt).
+        dropped: The smallest ``start[b] - count[b, h]`` over the batch, a host int: the virtual key axis of a call is
+            ``S - dropped`` keys long.
     """
 
     key: torch.Tensor
@@ -49,45 +52,49 @@ class GatheredKV:
         return gathered_decode_attention(query, key, value, mask, scale, self, softcap=softcap, sinks=sinks)
 
 
-def _check(g: GatheredKV, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> None:
-    """The reference's layout checks (attention/gathered.py:67-93)."""
-    batch, kv_heads = key.shape[:2]
-    capacity = g.key.shape[2]
-    expected = {
-        "key": ((batch, kv_heads, capacity, key.shape[3]), key.dtype),
-        "value": ((batch, kv_heads, capacity, value.shape[3]), value.dtype),
-        "index": ((batch, kv_heads, capacity), torch.int32),
-        "count": ((batch, kv_heads), torch.int32),
-        "start": ((batch,), torch.int32),
-    }
-    for name, (shape, dtype) in expected.items():
-        t = getattr(g, name)
-        if tuple(t.shape) != shape or t.dtype != dtype or t.device != query.device:
-            raise ConfigError(f"gathered {name} is {tuple(t.shape)} {t.dtype} on {t.device}, expected {shape} {dtype} "
-                              f"on {query.device}")
-        if (t.stride(-1) != 1) if name in ("key", "value") else not t.is_contiguous():
-            raise ConfigError(f"gathered {name} is not laid out for the kernel (strides {t.stride()})")
-    if g.dropped < 0 or g.dropped > key.shape[2]:
-        raise ConfigError(f"gathered cache drops {g.dropped} of {key.shape[2]} slots")
+def _validate(g: GatheredKV, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> None:
+    """What ``eco_gathered_decode`` needs of the attachment, checked before the launch: the compact entries share the
+    dense buffers' rows, heads, channels, dtype and device and have unit channel strides; the slot index has unit
+    stride along the entries; the counts and starts are dense int32 vectors the kernel addresses as ``b * Hkv + h``
+    and ``b``; ``dropped`` lies within the slots."""
+    batch, kv_heads, slots = key.shape[:3]
+    entries = g.key.shape[2] if g.key.dim() == 4 else -1
+    for what, compact, dense in (("keys", g.key, key), ("values", g.value, value)):
+        if compact.dim() != 4 or tuple(compact.shape) != (batch, kv_heads, entries, dense.shape[3]):
+            raise ConfigError(f"the gathered {what} {tuple(compact.shape)} do not fit the cache's "
+                              f"{tuple(dense.shape)} ({entries} kept entries)")
+        if compact.dtype != dense.dtype or compact.device != query.device or compact.stride(3) != 1:
+            raise ConfigError(f"the gathered {what} must be {dense.dtype} on {query.device} with unit channel stride")
+    if g.index.dtype != torch.int32 or tuple(g.index.shape) != (batch, kv_heads, entries) or \
+            g.index.device != query.device or g.index.stride(2) != 1:
+        raise ConfigError(f"the gathered slot index must be int32 [{batch}, {kv_heads}, {entries}] with unit stride "
+                          f"along the entries on {query.device}")
+    for what, t, shape in (("counts", g.count, (batch, kv_heads)), ("starts", g.start, (batch,))):
+        if t.dtype != torch.int32 or tuple(t.shape) != shape or not t.is_contiguous() or t.device != query.device:
+            raise ConfigError(f"the gathered {what} must be a contiguous int32 {list(shape)} on {query.device}")
+    if not 0 <= g.dropped <= slots:
+        raise ConfigError(f"a gathered cache of {slots} slots cannot drop {g.dropped} of them")
 
 
 def gathered_decode_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, mask: torch.Tensor | None,
                               scale: float, gathered: GatheredKV, softcap: float | None = None,
                               out: torch.Tensor | None = None, sinks: torch.Tensor | None = None,
                               launch: object = None) -> torch.Tensor:
-    """Decode attention over the compact entries and the dense tail (attention/gathered.py:96-179).
+    """Attention of a few queries per row over the kept prompt entries followed by the dense slots from ``start[b]``
+    on: the reference's gathered_decode_attention (attention/gathered.py:96-179) on ``eco_gathered_decode``.
 
     Args:
-        query: ``[B, Hq, Q, D]``, bf16, fp16 or fp32.
-        key: Dense ``[B, Hkv, S, D]`` in the query's dtype; read only at slots ``>= gathered.start[b]``.
-        value: Dense ``[B, Hkv, S, Dv]``; likewise.
-        mask: Boolean ``[B, 1 or Hq, Q, S]`` over the original slots, or ``None``.
-        scale: Multiplier of the scores.
-        gathered: The compact entries.
-        softcap: Optional tanh soft cap of the scaled scores.
-        out: Optional ``[B, Q, Hq, Dv]`` output buffer.
-        sinks: Optional ``[Hq]`` attention-sink logits.
-        launch: The reference's launch override; the plan here is a function of the shapes, so it is ignored.
+        query: ``[B, Hq, Q, D]``; bf16, fp16 or fp32.
+        key: ``[B, Hkv, S, D]`` dense keys in the query's dtype; the kernel reads only their slots from ``start[b]`` on.
+        value: ``[B, Hkv, S, Dv]`` dense values, read the same way.
+        mask: ``None``, or a boolean ``[B, 1 or Hq, Q, S]`` over the original slots (a kept entry reads the column of
+            the slot it came from).
+        scale: The score multiplier.
+        gathered: The kept prompt entries.
+        softcap: Optional tanh soft cap on the scaled scores.
+        out: Optional ``[B, Q, Hq, Dv]`` destination.
+        sinks: Optional ``[Hq]`` sink logits in the softmax denominator.
+        launch: Accepted for the reference's signature; the launch plan here follows from the shapes alone.
 
     Returns:
         ``[B, Q, Hq, Dv]`` in the query's dtype.
@@ -103,7 +110,7 @@ def gathered_decode_attention(query: torch.Tensor, key: torch.Tensor, value: tor
         raise ConfigError(f"gathered_decode_attention takes K/V in the query's dtype, got {key.dtype} / {value.dtype}")
     if keys == 0:
         raise ConfigError("gathered_decode_attention needs a cache of at least one slot")
-    _check(gathered, query, key, value)
+    _validate(gathered, query, key, value)
     m, mask_strides = mask_operand(mask, keys)
     sinks = sinks_operand(sinks, q_heads)
     if out is not None and (out.shape != (batch, queries, q_heads, head_dv) or out.dtype != query.dtype or

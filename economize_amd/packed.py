@@ -2,11 +2,14 @@
 
 A cache that stores a layer in a format an attention kernel reads directly (here: the paged fp8 / bf16 cache, the
 paged KIVI cache, Quest's pages over a paged cache) returns stand-ins for the layer's dense K/V and attaches the
-format's handle to a fresh view of the key. :func:`economize_amd.attention.economize_attention_forward` finds it with
-:func:`packed_of` and calls its ``attend``; an attention function that does not read the format calls
-:func:`materialized_kv`, which builds the dense K/V through the handle's ``materialize`` (the gather kernels), so the
-fallbacks compute the same attention. The attachment lives on a view, so it disappears as soon as anything copies,
-slices or reorders the tensor, and a stale attachment cannot be read.
+format's handle to a fresh view of the key; a cache that keeps dense buffers but lets the kernel read less of them
+(Quest's pages over a dense cache, an eviction's kept entries) attaches its handle to the key buffer's view itself.
+:func:`economize_amd.attention.economize_attention_forward` finds the handle with :func:`packed_of` and calls its
+``attend``; an attention function that does not read the format calls :func:`materialized_kv`, which builds the
+dense K/V through the handle's ``materialize`` (the gather kernels), and applies the handle's ``restrict_mask`` when
+it has one, so the fallbacks compute the same attention. The handle is an attribute of one view object only: any new
+tensor made from the key (a copy, a slice, a reordering of rows) is a different object without it, so a handle can
+only ever be read together with the exact tensor it was attached to.
 """
 
 from __future__ import annotations
@@ -34,7 +37,7 @@ class PackedKV(Protocol):
 
 
 def attach_packed(key: torch.Tensor, packed: object) -> torch.Tensor:
-    """A view of ``key`` that carries ``packed`` (the buffer itself is left untouched)."""
+    """``key`` as a new view object with ``packed`` as its attribute; ``key`` and its storage are not modified."""
     view = key.view(key.shape)
     setattr(view, _ATTR, packed)
     return view

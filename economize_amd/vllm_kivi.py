@@ -12,8 +12,12 @@ already quantized (``eco_kivi_cells_quantize``), leaving every cell as the refer
 quantized cell's dense entry holds the dequantized value, so attention over the dense entries is attention over the
 KIVI numbers. :func:`clear_flags` marks cells vLLM's cache write just filled as full precision.
 :func:`paged_kivi_attention` is the reference's attention over the cells with vLLM's varlen query layout and a
-causal bound per query (kernels.py:216-415): the dense decode kernel reading the cells' dense entries through the
-block table (``eco_kivi_cells_attention``).
+causal bound per query (kernels.py:216-415): the dense decode kernel reading the cells through the block table
+(``eco_kivi_cells_attention``). As the reference's kernel does (kernels.py:274-296), a key or value whose cell flag is
+1 is read through its codes, scales and zero points, and its dense entry is ignored, for bf16 cells of 128 channels
+with key groups of 32, 2- or 4-bit codes and pages of a multiple of 32 tokens; every other cell (flag 0 or 2), every
+other cell shape, and every cell when the environment sets ``ECO_CELLS_DENSE=1``, is read from its dense entry, which
+quantize_committed left holding the same dequantized number.
 """
 
 from __future__ import annotations
@@ -176,6 +180,8 @@ def paged_kivi_attention(query: torch.Tensor, kv_cache: torch.Tensor, layout: Ce
             raise ConfigError(f"{name} must be a contiguous int32 [{n}]")
     if block_table.dtype != torch.int32 or block_table.dim() != 2 or block_table.stride(1) != 1:
         raise ConfigError("block_table must be int32 [requests, pages] with contiguous rows")
+    if block_table.shape[0] < requests:
+        raise ConfigError(f"block_table has {block_table.shape[0]} rows for {requests} requests")
     if out is None:
         out = torch.empty_like(query)
     elif out.shape != query.shape or out.dtype != query.dtype or out.stride(-1) != 1:

@@ -347,9 +347,14 @@ int eco_kivi_cells_quantize(void* cache, int32_t format, int64_t sb, int64_t sh,
  * [pages, kv_heads, page_size] (byte strides sb, sh, sn; entries and queries of format bf16 / fp16 / fp32): vLLM's
  * varlen queries q [tokens, q_heads, D] (element strides sq_t, sq_h; request b's queries are tokens
  * query_start_loc[b] .. query_start_loc[b + 1] - 1, at most max_query_len), each attending causally over its
- * request's seq_lens[b] keys (query i of a request of n queries sees keys < seq_len - n + i + 1), read from the
- * cells' dense entries, which hold every quantized key and value as its dequantized value; out [tokens, q_heads, D]
- * (strides so_t, so_h); keys = the longest seq_len; optional sinks [q_heads] and soft cap. Workspace:
+ * request's seq_lens[b] keys (query i of a request of n queries sees keys < seq_len - n + i + 1); out
+ * [tokens, q_heads, D] (strides so_t, so_h); keys = the longest seq_len (at least every seq_lens[b]); optional sinks
+ * [q_heads] and soft cap. As the reference's kernel (kernels.py:274-296), a key or value whose cell flag is 1 is read
+ * through its codes, value scales and zero points and its key group's scales and zero points, and its dense entry is
+ * ignored, for bf16 cells of 128 channels, key groups of 32, 2- or 4-bit codes and page_size a multiple of 32; any
+ * other flag, any other cell shape, and every cell when the environment sets ECO_CELLS_DENSE=1, is read from its
+ * dense entry (which eco_kivi_cells_quantize leaves holding the dequantized value). block_table has a row per
+ * request. Workspace:
  * eco_kivi_cells_attention_workspace_size bytes, with eco_decode's counter rule (batch = requests, queries =
  * max_query_len). */
 size_t eco_kivi_cells_attention_workspace_size(int32_t requests, int32_t max_query_len, int32_t q_heads,

@@ -182,8 +182,8 @@ def test_keep_and_restrict_mask_hide_the_unselected_pages(kind) -> None:
     else:
         base = torch.randn(batch, 1, 1, slots, generator=gen).to(torch.bfloat16)
         got = qp.restrict_mask(q, k, base.cuda()).cpu()
-        want_f = base.expand(batch, hq, 1, slots).masked_fill(~torch.from_numpy(np.ascontiguousarray(np.broadcast_to(full, got.shape))),
-                                                              torch.finfo(torch.bfloat16).min)
+        hidden = ~torch.from_numpy(np.broadcast_to(full, got.shape).copy())
+        want_f = base.expand(batch, hq, 1, slots).masked_fill(hidden, torch.finfo(torch.bfloat16).min)
         assert torch.equal(got, want_f)
     assert used == [7]
     # a longer query than max_queries sees every key: the mask comes back untouched, and nothing is read

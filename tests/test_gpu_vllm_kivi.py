@@ -224,3 +224,89 @@ def test_attention_reads_the_codes_of_quantized_cells(bits) -> None:
         qb = query[qsl[b]: qsl[b + 1]].float().numpy().transpose(1, 0, 2)[None]
         want = reference_attention(qb, k[None], v[None], mask, head ** -0.5)[0]
         np.testing.assert_allclose(out[qsl[b]: qsl[b + 1]], want, atol=2e-3, rtol=1e-2, err_msg=f"request {b}")
+
+
+def _poisoned_cells(requests, kv_heads, lens, bits, page, seed, residual=64, qlens=None):
+    """A cache of random bf16 cells of 128 channels (groups of 32) built on the GPU, quantize_committed at the pass's
+    schedule, then the dense entries of every quantized key and value set to NaN: only the codes path can read it."""
+    from economize_amd.vllm_kivi import cell_layout
+
+    head = 128
+    layout = cell_layout(head, torch.bfloat16, bits, 32)
+    per_row = max(-(-n // page) for n in lens)
+    pages = requests * per_row + 7
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    table = torch.randperm(pages, generator=gen, device="cuda")[: requests * per_row].view(requests, per_row)
+    table = table.to(torch.int32).contiguous()
+    cache = (torch.randn(pages, kv_heads, page, layout.size // 2, generator=gen, device="cuda") * 2).to(torch.bfloat16)
+    u8 = cache.view(torch.uint8)
+    u8[..., layout.off_flag: layout.off_flag + 2] = 0
+    qlens = qlens or [1] * requests
+    run(cache, layout, residual, table.cpu(), qlens, lens, [0] * requests)
+    nan = torch.tensor([0x7FC0], dtype=torch.int16).view(torch.bfloat16).cuda()
+    typed = cache.view(pages, kv_heads, page, layout.size // 2)
+    kflag = u8[..., layout.off_flag] == oc.FLAG_PACKED
+    vflag = u8[..., layout.off_flag + 1] == oc.FLAG_PACKED
+    assert int(kflag.sum()) > 0 and int(vflag.sum()) > 0
+    k_entries = typed[..., :head]
+    v_entries = typed[..., head: 2 * head]
+    k_entries[kflag] = nan
+    v_entries[vflag] = nan
+    return layout, cache, table, qlens
+
+
+def _check_requests(out, query, qsl, cache, layout, table, lens, qlens, page, scale, requests_to_check):
+    from oracle.attention import reference_attention
+
+    cells = cache.view(torch.uint8).cpu().numpy()
+    tab = table.cpu()
+    for b in requests_to_check:
+        n, q = lens[b], qlens[b]
+        k, v = oc.read_cells(gathered_cells(cells, tab, b, n, page, layout), layout, "bf16")
+        mask = np.zeros((1, 1, q, n), bool)
+        for i in range(q):
+            mask[..., i, : n - q + i + 1] = True
+        qb = query[qsl[b]: qsl[b + 1]].float().cpu().numpy().transpose(1, 0, 2)[None]
+        want = reference_attention(qb, k[None], v[None], mask, scale)[0]
+        np.testing.assert_allclose(out[qsl[b]: qsl[b + 1]], want, atol=2e-3, rtol=1e-2, err_msg=f"request {b}")
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_codes_path_with_single_splits_and_long_waves(bits) -> None:
+    """2048 programs (8 requests x 8 KV heads x 32 blocks of 16 query rows: 64 queries of 8 heads per KV head) leave
+    one split per program, so every wave walks its row's ~66 tiles: the two-buffer handover of the codes state
+    between consecutive tiles and the page window's reload past 32 tiles both run, over cells whose quantized dense
+    entries are NaN."""
+    from economize_amd.vllm_kivi import paged_kivi_attention
+
+    requests, kv_heads, q_heads, page = 8, 8, 64, 32
+    lens = [2100, 2117, 2048, 2090, 2133, 2101, 2060, 2111]
+    qlens = [64, 64, 50, 64, 33, 64, 64, 64]
+    layout, cache, table, qlens = _poisoned_cells(requests, kv_heads, lens, bits, page, seed=bits, qlens=qlens)
+    gen = torch.Generator().manual_seed(bits)
+    query = torch.randn(sum(qlens), q_heads, 128, generator=gen).to(torch.bfloat16)
+    qsl = torch.tensor(np.concatenate([[0], np.cumsum(qlens)]), dtype=torch.int32)
+    out = paged_kivi_attention(query.cuda(), cache, layout, table, qsl.cuda(),
+                               torch.tensor(lens, dtype=torch.int32).cuda(), max(qlens), max(lens),
+                               scale=128 ** -0.5).float().cpu().numpy()
+    assert np.isfinite(out).all()
+    _check_requests(out, query, qsl, cache, layout, table, lens, qlens, page, 128 ** -0.5, [0, 2, 4, 7])
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_codes_path_at_the_benchmark_shape(bits) -> None:
+    """The measured cells workload: 16 requests of 8192 tokens, 32 query heads over 8 KV heads, one query each,
+    residual 128, every quantized dense entry NaN; sampled requests against read_cells and the fp32 definition."""
+    from economize_amd.vllm_kivi import paged_kivi_attention
+
+    requests, kv_heads, q_heads, page, length = 16, 8, 32, 32, 8192
+    lens = [length] * requests
+    layout, cache, table, qlens = _poisoned_cells(requests, kv_heads, lens, bits, page, seed=10 + bits, residual=128)
+    gen = torch.Generator().manual_seed(bits)
+    query = torch.randn(requests, q_heads, 128, generator=gen).to(torch.bfloat16)
+    qsl = torch.arange(requests + 1, dtype=torch.int32)
+    out = paged_kivi_attention(query.cuda(), cache, layout, table, qsl.cuda(),
+                               torch.tensor(lens, dtype=torch.int32).cuda(), 1, length,
+                               scale=128 ** -0.5).float().cpu().numpy()
+    assert np.isfinite(out).all()
+    _check_requests(out, query, qsl, cache, layout, table, lens, qlens, page, 128 ** -0.5, [0, 9])
