@@ -96,6 +96,9 @@ class PagedKV:
         current: For :meth:`materialize`: the dense K/V ``[B, Hkv, T, D]`` of the pass that is writing the last ``T``
             tokens, when they are to be read as the pass computed them (KIVI quantizes a pass's tokens only at its
             end), else ``None``.
+        static: ``max_seq_len`` is the cache's capacity, not the rows' length (a static cache's reads have fixed
+            shapes): the dense view is capacity-long, and a fallback without a mask hides the slots past each
+            row's ``seq_lens`` (:meth:`visible_mask`).
     """
 
     cache: PagedKVCache | PagedKIVICache
@@ -105,6 +108,7 @@ class PagedKV:
     pages: QuestPages | None = None
     dtype: torch.dtype = torch.bfloat16
     current: tuple[torch.Tensor, torch.Tensor] | None = None
+    static: bool = False
 
     def __post_init__(self) -> None:
         if self.pages is not None and not isinstance(self.cache, PagedKVCache):
@@ -143,6 +147,13 @@ class PagedKV:
         if self.pages is None:
             return mask
         return self.pages.restrict_mask(query, key, mask, is_causal)
+
+    def visible_mask(self, queries: int) -> torch.Tensor:
+        """Boolean ``[B, 1, Q, max_seq_len]``: key ``t`` visible to query ``qi`` of row ``b`` when
+        ``t < seq_lens[b] - Q + qi + 1`` (the causal rule of the paged kernels), from the device lengths."""
+        t = torch.arange(self.max_seq_len, device=self.seq_lens.device).view(1, 1, 1, -1)
+        qi = torch.arange(queries, device=self.seq_lens.device).view(1, 1, -1, 1)
+        return t < self.seq_lens.view(-1, 1, 1, 1) - queries + qi + 1
 
     def materialize(self) -> tuple[torch.Tensor, torch.Tensor]:
         """The dense K/V ``[B, Hkv, max_seq_len, D]`` the kernels read, in :attr:`dtype` (the gather kernels)."""
@@ -265,9 +276,12 @@ def _fallback(module, query, key, value, attention_mask, dropout, scaling, is_ca
     from transformers.integrations.sdpa_attention import sdpa_attention_forward
 
     layer = getattr(module, "layer_idx", None)
+    handle = packed_of(key)
     key, value = materialized_kv(key, value)
     if torch.is_tensor(attention_mask) and attention_mask.dim() == 4 and attention_mask.shape[-1] > key.shape[2]:
         attention_mask = attention_mask[..., : key.shape[2]]
+    if attention_mask is None and getattr(handle, "static", False):  # capacity-long K/V: hide the unwritten slots
+        attention_mask, is_causal = handle.visible_mask(query.shape[2]), False
     restrict = getattr(packed_of(key), "restrict_mask", None)
     if restrict is not None:  # a sparse cache (Quest) hides what its kernel would not read (interface.py:216-222)
         restricted = restrict(query, key, attention_mask, bool(is_causal))

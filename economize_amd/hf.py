@@ -161,7 +161,7 @@ class PagedLayer(_PagedBase, _UnreadCheck):
     the previous passes committed (one launch, ``eco_paged_append_quest``), and ``done`` is a device tensor."""
 
     def __init__(self, capacity: int, cache_dtype: torch.dtype | None, quest: QuestConfig | None = None,
-                 scales: tuple[torch.Tensor, torch.Tensor] | None = None, layer: int = 0) -> None:
+                 scales: tuple[torch.Tensor, torch.Tensor] | None = None, layer: int = 0, static: bool = False) -> None:
         super().__init__(capacity, PAGE)
         self.cache_dtype = cache_dtype  # None: the model's dtype (bf16)
         self.quest = quest
@@ -171,6 +171,12 @@ class PagedLayer(_PagedBase, _UnreadCheck):
         self._committed: dict[int, torch.Tensor] = {}
         self._write_width = 0
         self._init_unread(layer)
+        # static: the written length, the committed lengths and the sequence lengths live on the device, and reads
+        # hand over capacity-long stand-ins, so that a decode step has fixed shapes and can be captured in a graph
+        self.static = static
+        self._length_dev: torch.Tensor | None = None
+        self._committed_dev: torch.Tensor | None = None
+        self._lens_dev: torch.Tensor | None = None
 
     @property
     def bounds(self) -> tuple[torch.Tensor, torch.Tensor] | None:
@@ -190,7 +196,22 @@ class PagedLayer(_PagedBase, _UnreadCheck):
         if q is not None:
             self.state = QuestState(batch, heads, dim, max(1, self.capacity // q.page_size), q.page_size, q.pages,
                                     key_states.device, q.max_queries, q.first_page)
+        if self.static:
+            self._length_dev = torch.zeros(1, dtype=torch.int32, device=key_states.device)
+            self._committed_dev = torch.zeros(batch, dtype=torch.int32, device=key_states.device)
+            self._lens_dev = torch.zeros(batch, dtype=torch.int32, device=key_states.device)
         self.is_initialized = True
+
+    def get_mask_sizes(self, query_length: int) -> tuple[int, int]:
+        return (self.capacity, 0) if self.static else (self.length + query_length, 0)
+
+    def get_seq_length(self) -> int | torch.Tensor:
+        """The tokens written; a static layer gives its device count (int32 ``[1]``), as transformers' static layers
+        do, so that the positions and the causal mask transformers derives from it follow the device in a replayed
+        graph."""
+        if self.static and self._length_dev is not None:
+            return self._length_dev.clone()
+        return self.length
 
     def _committed_rows(self) -> torch.Tensor:
         lens = self._committed.get(self.committed)
@@ -203,7 +224,46 @@ class PagedLayer(_PagedBase, _UnreadCheck):
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs
                ) -> tuple[torch.Tensor, torch.Tensor]:
         self._check_read()
+        if self.static:
+            return self._static_update(key_states, value_states)
         return super().update(key_states, value_states, *args, **kwargs)
+
+    def _static_update(self, key_states: torch.Tensor, value_states: torch.Tensor
+                       ) -> tuple[torch.Tensor, torch.Tensor]:
+        """A pass of the static layer, every count on the device: the tokens written before it are committed, the
+        new ones go to positions ``length ..`` (with Quest, the append also computes the bounds of the committed
+        pages), and attention gets capacity-long stand-ins whose handle carries the device lengths. The host
+        ``length`` counts eager passes only (a replayed graph advances the device one): callers pass position ids."""
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        batch, heads, tokens, dim = key_states.shape
+        self._check_room(tokens)
+        device = key_states.device
+        self._committed_dev.copy_(self._length_dev.expand(batch))
+        pos = torch.arange(tokens, dtype=torch.int32, device=device) + self._length_dev
+        # a position past the capacity (a graph replayed too often) writes nothing instead of indexing past the table
+        page_of = (pos // PAGE).clamp(max=self.table.shape[1] - 1).long()
+        slots = torch.where(pos < self.capacity, self.table[:, page_of] * PAGE + pos % PAGE, -1)
+        slots = slots.to(torch.int32).reshape(-1)
+        k = key_states.transpose(1, 2).reshape(batch * tokens, heads, dim)
+        v = value_states.transpose(1, 2).reshape(batch * tokens, heads, dim)
+        if self.state is not None:
+            self.state.append(self.cache, k, v, slots, self.table, self._committed_dev)
+        else:
+            paged_append(self.cache, k, v, slots)
+        self._length_dev.add_(tokens)
+        self._lens_dev.copy_(self._length_dev.expand(batch))
+        self.committed, self.length, self._write_width = self.length, self.length + tokens, tokens
+        pages = None
+        q = self.quest
+        if q is not None and tokens <= q.max_queries:
+            pages = self.state.pages_handle(on_use=self._read, layer=self.layer_idx)
+            self._attached()
+        handle = PagedKV(self.cache, self.table, self._lens_dev, self.capacity, pages, self.model_dtype,
+                         static=True)
+        shape = (batch, heads, self.capacity, dim)
+        keys = stand_in(shape, self.model_dtype, device)
+        return attach_packed(keys, handle), stand_in(shape, self.model_dtype, device)
 
     def transform_update(self, key_states, value_states):
         """fp8_encode (or the bf16 rounding) of the new tokens into their pages, at positions ``length ..``; with
@@ -243,6 +303,9 @@ class PagedLayer(_PagedBase, _UnreadCheck):
         self._unread = False
         if self.state is not None:
             self.state.reset()
+        for t in (self._length_dev, self._committed_dev, self._lens_dev):
+            if t is not None:
+                t.zero_()
 
 
 class DenseQuestLayer(CacheLayerMixin, _UnreadCheck):
@@ -632,13 +695,33 @@ class EconomizedModel:
         dtype = next(self.model.parameters()).dtype
         return dtype == torch.bfloat16 and head_dim_of(self.model) in (64, 128, 256)
 
-    def make_cache(self, max_length: int) -> EconomizeCache:
-        """A cache for generations of up to ``max_length`` tokens per row (prompt included)."""
+    def make_cache(self, max_length: int, static: bool = False) -> EconomizeCache:
+        """A cache for generations of up to ``max_length`` tokens per row (prompt included).
+
+        ``static``: every layer in a paged cache whose lengths live on the device and whose reads have fixed shapes
+        (:class:`PagedLayer` with ``static=True``), so that a decoding step, ``model(input_ids=..., position_ids=...,
+        past_key_values=cache)`` with position ids from a device buffer, can be captured in a HIP graph and replayed;
+        layers without a technique keep bf16 pages. It takes a bf16 model of head dim 64 / 128 / 256 and the fp8
+        (none or per-head scale) and Quest techniques.
+        """
         config = self.model.config
         layers: list[CacheLayerMixin] = []
+        if static:
+            dtype = next(self.model.parameters()).dtype
+            if dtype != torch.bfloat16 or head_dim_of(self.model) not in (64, 128, 256):
+                raise ConfigError("a static cache takes a bf16 model of head dim 64, 128 or 256")
         for index in range(config.num_hidden_layers):
             technique = self.technique_of(index + 1)
             cfg = technique.config if technique is not None else None
+            if static:
+                if isinstance(cfg, KIVIConfig) or (isinstance(cfg, FP8KVConfig) and not self.paged_fp8(cfg)):
+                    raise ConfigError(f"a static cache holds layers of no technique, paged fp8 and Quest, not "
+                                      f"{type(cfg).__name__} on layer {index + 1}")
+                fp8 = cfg.dtype if isinstance(cfg, FP8KVConfig) else None
+                quest = cfg if isinstance(cfg, QuestConfig) else None
+                layers.append(PagedLayer(max_length, fp8, quest, scales=self.scales.get(index), layer=index,
+                                         static=True))
+                continue
             if isinstance(cfg, KIVIConfig) and cfg.simulated(self.model):
                 layers.append(SimulatedKIVILayer(max_length, cfg))
             elif isinstance(cfg, KIVIConfig):

@@ -575,3 +575,66 @@ def test_quest_pages_no_attention_function_read_raise(dtype) -> None:
         with pytest.raises(IncompatibleTechniquesError, match="no attention function read"):
             model(input_ids=token, past_key_values=cache, use_cache=True)
     model.set_attn_implementation("economize")
+
+
+def test_a_captured_decode_step_of_a_quest_model_replays_like_eager() -> None:
+    """Quest's metadata on the device inside the drop-in: a bf16 Qwen2 whose layers live in a static cache (paged,
+    every length on the device; Quest's bounds refreshed by the append's own launch) is captured once, decoding step
+    ``model(input_ids=token, position_ids=position, past_key_values=cache)`` with the token and position in device
+    buffers, and replayed; a twin model stepping eagerly over a twin cache gives bit-identical logits at every step
+    while the rows cross page boundaries (80, 96, 112 and 128 tokens) and Quest selects among more and more pages."""
+    from economize_amd.attention import kernel_usage
+    from economize_amd.hf import PagedLayer, apply
+    from economize_amd.techniques import QuestConfig
+
+    cap, steps = 200, 60
+
+    def build():
+        model = tiny_model("sdpa")
+        em = apply(model, QuestConfig(page_size=16, token_budget=64, dense_layers=1))
+        return model, em.make_cache(cap, static=True)
+
+    (m0, c0), (m1, c1) = build(), build()
+    assert all(isinstance(layer, PagedLayer) and layer.static for layer in c0.layers)
+    assert [layer.quest is not None for layer in c0.layers] == [False, True, True, True]
+    ids = prompt()
+    pos = torch.arange(PROMPT, device="cuda")[None]
+    kernel_usage(reset=True)
+    with torch.no_grad():
+        first = m0(input_ids=ids, position_ids=pos, past_key_values=c0, use_cache=True).logits
+        assert torch.equal(first, m1(input_ids=ids, position_ids=pos, past_key_values=c1, use_cache=True).logits)
+        token = torch.zeros(1, 1, dtype=torch.long, device="cuda")
+        position = torch.zeros(1, 1, dtype=torch.long, device="cuda")
+        token.copy_(first[:, -1].argmax(-1, keepdim=True))
+        position.fill_(PROMPT)
+
+        def step(model, cache):
+            return model(input_ids=token, position_ids=position, past_key_values=cache, use_cache=True).logits
+
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # warm-up on a side stream: workspaces exist before the capture
+            warm = step(m0, c0)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        assert torch.equal(warm, step(m1, c1))
+        token.copy_(warm[:, -1].argmax(-1, keepdim=True))
+        position += 1
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            captured = step(m0, c0)
+        # the capture recorded the step without running it: the first replay runs it
+        for i in range(steps):
+            graph.replay()
+            torch.cuda.synchronize()
+            eager = step(m1, c1)
+            torch.cuda.synchronize()
+            assert torch.equal(captured, eager), f"step {i}, position {int(position)}"
+            token.copy_(eager[:, -1].argmax(-1, keepdim=True))
+            position += 1
+    assert int(position) == PROMPT + 1 + steps
+    paths = {(row["path"], row["queries"]) for row in kernel_usage(reset=True)}
+    assert ("kernel_quest", 1) in paths and ("kernel_bf16", 1) in paths
+    for a, b in zip(c0.layers[1:], c1.layers[1:]):
+        assert torch.equal(a.state.done, b.state.done) and torch.equal(a.state.kmin, b.state.kmin)
+    assert int(c1.layers[1].state.done[0]) == (PROMPT + 1 + steps) // 16

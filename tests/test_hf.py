@@ -154,3 +154,22 @@ def test_quest_layers_are_paged_where_the_paged_kernels_take_the_model() -> None
     with pytest.raises(ConfigError, match="multiples of 8 up to 256"):
         apply(tiny_model(head_dim=512), QuestConfig())
     assert PagedLayer and DenseQuestLayer
+
+
+def test_a_static_cache_holds_paged_layers_only() -> None:
+    """``make_cache(static=True)``: every layer paged with device lengths (no technique: bf16 pages; fp8; Quest), and
+    a refusal for what a static cache cannot hold (another dtype, KIVI, per-token fp8 scales)."""
+    from economize_amd.hf import PagedLayer, apply
+
+    bf16 = tiny_model().to(torch.bfloat16)
+    cache = apply(bf16, FusedFP8KVConfig(layers=(1,)), QuestConfig(dense_layers=2)).make_cache(64, static=True)
+    assert all(isinstance(layer, PagedLayer) and layer.static for layer in cache.layers)
+    assert [layer.cache_dtype for layer in cache.layers] == [torch.float8_e4m3fn, None, None, None]
+    assert [layer.quest is not None for layer in cache.layers] == [False, False, True, True]
+    assert cache.layers[0].get_mask_sizes(1) == (64, 0)
+    with pytest.raises(ConfigError, match="static cache takes a bf16 model"):
+        apply(tiny_model(), QuestConfig()).make_cache(64, static=True)
+    with pytest.raises(ConfigError, match="KIVIConfig"):
+        apply(tiny_model().to(torch.bfloat16), KIVIConfig()).make_cache(64, static=True)
+    with pytest.raises(ConfigError, match="FP8KVConfig"):
+        apply(tiny_model().to(torch.bfloat16), FP8KVConfig(scale="token")).make_cache(64, static=True)
