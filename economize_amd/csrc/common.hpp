@@ -69,4 +69,13 @@ __device__ inline float soft_cap_log2(float x, float cap, float inv_cap) {
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// A 16-byte load of cache data read once per call (K/V tiles, codes): nontemporal, so the line is streamed rather than
+// kept in the caches. A load-only copy of the fp8 decode's access pattern (2 KB page blocks through a shuffled table,
+// 268 MB per call over three copies) takes 39.6 us this way against 45.8 us with plain loads.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ inline uint4 stream_load16(const void* p) {
+    const u32x4_t x = __builtin_nontemporal_load(static_cast<const u32x4_t*>(p));
+    return make_uint4(x.x, x.y, x.z, x.w);
+}
+
 }  // namespace eco

@@ -81,7 +81,9 @@ __device__ __forceinline__ void cvt8(const uint4 (&w)[FMT == FP32 ? 2 : 1], bf16
     }
 }
 
-// The raw words of eight consecutive elements of format FMT at p (16-byte aligned; fp8: 8-byte aligned).
+// The raw words of eight consecutive elements of format FMT at p (16-byte aligned; fp8: 8-byte aligned). The
+// 16-byte loads are streamed (stream_load16: bf16 dense decode at B=32 L=4096 112 -> 103 us); fp8's 8-byte loads stay
+// plain (streamed, the fp8 views took 78.6 us against 67.2).
 template <int FMT>
 __device__ __forceinline__ void load8(const uint8_t* p, uint4 (&w)[FMT == FP32 ? 2 : 1]) {
     if constexpr (FMT == FP8_E4M3 || FMT == FP8_E5M2) {
@@ -89,7 +91,7 @@ __device__ __forceinline__ void load8(const uint8_t* p, uint4 (&w)[FMT == FP32 ?
         w[0] = make_uint4(x.x, x.y, 0, 0);
     } else {
 #pragma unroll
-        for (int i = 0; i < (FMT == FP32 ? 2 : 1); ++i) w[i] = reinterpret_cast<const uint4*>(p)[i];
+        for (int i = 0; i < (FMT == FP32 ? 2 : 1); ++i) w[i] = stream_load16(p + 16 * i);
     }
 }
 
@@ -429,7 +431,7 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
                 const int chunk = lane + 64 * i;
                 const int t = min(t0 + chunk / CPR, t_end - 1);
                 const int c = (chunk % CPR) * (16 / ES);
-                vreg[i] = *reinterpret_cast<const uint4*>(value_row(t) + (c < p.value_dim ? c : 0) * ES);
+                vreg[i] = stream_load16(value_row(t) + (c < p.value_dim ? c : 0) * ES);
             }
 #pragma unroll
         for (int v = 0; v < 2; ++v) {

@@ -218,19 +218,23 @@ struct KTile {
     uint32_t mw[4];    // with a mask: bit e = token 8 g + e of the page visible to query row 16 nb + n (nb < NB)
 };
 
+// N code words from src, streamed (codes are read once per call; C3 at L=8192, int2 / int4: 55.7 / 57.6 us plain,
+// 52.6 / 55.1 us streamed).
 template <int N>
 __device__ inline void load_words(const uint32_t* src, uint32_t (&dst)[N]) {
     if constexpr (N % 4 == 0) {
 #pragma unroll
         for (int i = 0; i < N; i += 4) {
-            const uint4 w = reinterpret_cast<const uint4*>(src)[i / 4];
+            const uint4 w = stream_load16(src + i);
             dst[i] = w.x;
             dst[i + 1] = w.y;
             dst[i + 2] = w.z;
             dst[i + 3] = w.w;
         }
     } else if constexpr (N == 2) {
-        const uint2 w = *reinterpret_cast<const uint2*>(src);
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        const u32x2_t x = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(src));
+        const uint2 w = make_uint2(x.x, x.y);
         dst[0] = w.x;
         dst[1] = w.y;
     } else {

@@ -158,21 +158,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         const int phys = __builtin_amdgcn_readlane(win.physical, VerifyParams::kTile * c.t + pg - win.base);
         s.page = phys;
         const uint8_t* blk = p.blocks + static_cast<int64_t>(phys >= 0 ? phys : 0) * p.blk_page + c.kvh * p.blk_head;
+        // codes, scales and zero points are read once per call: streamed loads
 #pragma unroll
         for (int i = 0; i < TPT; ++i)
-            s.kw[i] = reinterpret_cast<const uint32_t*>(blk + L.k_codes() + (TPT * tg + i) * (D * BITS / 8))
-                [BITS == 4 ? co : co / 2];
-        s.ks = *reinterpret_cast<const uint4*>(blk + L.k_scale() + 16 * co);
-        s.kz = *reinterpret_cast<const uint4*>(blk + L.k_zero() + 16 * co);
+            s.kw[i] = __builtin_nontemporal_load(
+                reinterpret_cast<const uint32_t*>(blk + L.k_codes() + (TPT * tg + i) * (D * BITS / 8)) +
+                (BITS == 4 ? co : co / 2));
+        s.ks = stream_load16(blk + L.k_scale() + 16 * co);
+        s.kz = stream_load16(blk + L.k_zero() + 16 * co);
         const int u = BITS == 4 ? vo : vo >> 1;  // value word of tokens 8 vo ..
         const uint32_t* vwords = reinterpret_cast<const uint32_t*>(blk + L.v_codes());
 #pragma unroll
         for (int k = 0; k < CPT; ++k) {
             const int c = CPT * cq + k;
-            s.vw[k] = vwords[(u * 16 + c % 16) * ND + c / 16];
+            s.vw[k] = __builtin_nontemporal_load(vwords + (u * 16 + c % 16) * ND + c / 16);
         }
-        s.vs = *reinterpret_cast<const uint4*>(blk + L.v_scale() + (vgrp * 32 + 8 * vo) * 2);
-        s.vz = *reinterpret_cast<const uint4*>(blk + L.v_zero() + (vgrp * 32 + 8 * vo) * 2);
+        s.vs = stream_load16(blk + L.v_scale() + (vgrp * 32 + 8 * vo) * 2);
+        s.vz = stream_load16(blk + L.v_zero() + (vgrp * 32 + 8 * vo) * 2);
     };
 
     // ---- the lane's items of tile c into LDS buffer buf ----

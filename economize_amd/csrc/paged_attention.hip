@@ -100,7 +100,14 @@ __device__ inline uint32_t pack_bf16x2(float a, float b) {
     return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
 }
 
-__device__ inline uint4 load16(const uint8_t* p) { return *reinterpret_cast<const uint4*>(p); }
+// A tile's 16-byte K/V load: nontemporal (streamed) where the call reads whole rows; plain for Quest's page lists,
+// whose few tiles per wave are latency-bound (measured at the Quest workload: 61 us per call with streamed loads
+// against 50 us plain).
+template <bool NT>
+__device__ inline uint4 load16(const uint8_t* p) {
+    if constexpr (NT) return stream_load16(p);
+    return *reinterpret_cast<const uint4*>(p);
+}
 
 // First channel of k-step j (8 channels) for lane group g: run 4u + g of E channels, half h of it.
 template <int E>
@@ -156,7 +163,7 @@ __device__ __forceinline__ void load_query(const PagedParams& p, const Cursor& c
 
 // Issues the loads of the tile under cursor c (lane (n, g): K rows of tile page n / 4, V channel n of page g), and
 // the query operand of its row into the tile.
-template <int D, int FMT, int NB>
+template <int D, int FMT, int NB, bool NT>
 __device__ __forceinline__ void issue_tile(const PagedParams& p, const Cursor& c, int n, int g, int lane, PageWindow& win,
                                   Tile<D, FMT, NB>& tile) {
     using T = Tile<D, FMT, NB>;
@@ -174,12 +181,12 @@ __device__ __forceinline__ void issue_tile(const PagedParams& p, const Cursor& c
 #pragma unroll
     for (int v = 0; v < 4; ++v)
 #pragma unroll
-        for (int u = 0; u < T::NU; ++u) tile.k[v][u] = load16(kp + ((4 * u + g) * PAGE + 4 * v + (n & 3)) * 16);
+        for (int u = 0; u < T::NU; ++u) tile.k[v][u] = load16<NT>(kp + ((4 * u + g) * PAGE + 4 * v + (n & 3)) * 16);
     const uint8_t* vp = p.v_cache + c.kvh * p.vc_head + static_cast<int64_t>(pv >= 0 ? pv : 0) * p.vc_page;
 #pragma unroll
     for (int nd = 0; nd < T::ND; ++nd)
 #pragma unroll
-        for (int w = 0; w < T::NV; ++w) tile.v[nd][w] = load16(vp + (16 * nd + n) * PAGE * T::ES + 16 * w);
+        for (int w = 0; w < T::NV; ++w) tile.v[nd][w] = load16<NT>(vp + (16 * nd + n) * PAGE * T::ES + 16 * w);
     // the query operand: lane (n, g) holds query row nb * 16 + n, channels of k-step j as the K runs order them (a lane
     // of a row past the group reads row 0: its MFMA column is computed and never stored)
     constexpr int E = 16 / T::ES;
@@ -199,7 +206,7 @@ __device__ __forceinline__ void issue_tile(const PagedParams& p, const Cursor& c
 // As issue_tile for a tile without a query operand: the row's query operand goes to q_next, only when load_q is set
 // (the first tile of a row, or of the wave's range), and those loads come first, so that waiting for them does not
 // wait for the tile's K/V.
-template <int D, int FMT, int NB>
+template <int D, int FMT, int NB, bool NT>
 __device__ __forceinline__ void issue_tile_rq(const PagedParams& p, const Cursor& c, int n, int g, int lane,
                                               PageWindow& win, Tile<D, FMT, NB, true>& tile,
                                               bf16x8 (&q_next)[NB][D / 32], bool load_q) {
@@ -216,12 +223,12 @@ __device__ __forceinline__ void issue_tile_rq(const PagedParams& p, const Cursor
 #pragma unroll
     for (int v = 0; v < 4; ++v)
 #pragma unroll
-        for (int u = 0; u < T::NU; ++u) tile.k[v][u] = load16(kp + ((4 * u + g) * PAGE + 4 * v + (n & 3)) * 16);
+        for (int u = 0; u < T::NU; ++u) tile.k[v][u] = load16<NT>(kp + ((4 * u + g) * PAGE + 4 * v + (n & 3)) * 16);
     const uint8_t* vp = p.v_cache + c.kvh * p.vc_head + static_cast<int64_t>(pv >= 0 ? pv : 0) * p.vc_page;
 #pragma unroll
     for (int nd = 0; nd < T::ND; ++nd)
 #pragma unroll
-        for (int w = 0; w < T::NV; ++w) tile.v[nd][w] = load16(vp + (16 * nd + n) * PAGE * T::ES + 16 * w);
+        for (int w = 0; w < T::NV; ++w) tile.v[nd][w] = load16<NT>(vp + (16 * nd + n) * PAGE * T::ES + 16 * w);
 }
 
 // Clears the V bytes of the tokens a tile page does not hold (past the row's end, or the whole page when it holds
@@ -271,7 +278,7 @@ constexpr int wg_waves() {
     return NB == 1 && D <= 128 && NBUF <= 2 ? 4 : 1;
 }
 
-template <int D, int FMT, int NB, int NBUF>
+template <int D, int FMT, int NB, int NBUF, bool NT>
 __global__ __launch_bounds__((64 * wg_waves<D, FMT, NB, NBUF>()))
     __attribute__((amdgpu_waves_per_eu(waves_per_simd<D, FMT, NB, NBUF>()))) void
 paged_attention_kernel(PagedParams p) {
@@ -582,9 +589,9 @@ paged_attention_kernel(PagedParams p) {
         // counts the younger tiles' loads and leaves them in flight.
         auto issue_next = [&](T& buf, Cursor& slot) __attribute__((always_inline)) {
             if constexpr (kRowQ)
-                issue_tile_rq<D, FMT, NB>(p, icur, n, g, lane, win, buf, q_next, icur.t == 0 || ipos == lo);
+                issue_tile_rq<D, FMT, NB, NT>(p, icur, n, g, lane, win, buf, q_next, icur.t == 0 || ipos == lo);
             else
-                issue_tile<D, FMT, NB>(p, icur, n, g, lane, win, buf);
+                issue_tile<D, FMT, NB, NT>(p, icur, n, g, lane, win, buf);
             slot = icur;
             if (ipos < hi) {
                 if (ipos + 1 < hi) advance(p, icur, small ? &rt : nullptr);
@@ -669,21 +676,27 @@ int stages_cap() {
 }
 
 // The kernel instance for the tile-buffer count, and its waves per workgroup.
-using KernelFn = decltype(&paged_attention_kernel<64, BF16, 1, 1>);
+using KernelFn = decltype(&paged_attention_kernel<64, BF16, 1, 1, false>);
 struct Instance {
     KernelFn kernel;
     int waves;
 };
 
-template <int D, int FMT, int NB>
+template <int D, int FMT, int NB, bool NT>
 Instance kernel_of() {
     constexpr int M = max_stages<D, FMT, NB>();
     const int s = stages_cap() < M ? stages_cap() : M;
     if constexpr (M >= 3)
-        if (s == 3) return {paged_attention_kernel<D, FMT, NB, 3>, wg_waves<D, FMT, NB, 3>()};
+        if (s == 3) return {paged_attention_kernel<D, FMT, NB, 3, NT>, wg_waves<D, FMT, NB, 3>()};
     if constexpr (M >= 2)
-        if (s >= 2) return {paged_attention_kernel<D, FMT, NB, 2>, wg_waves<D, FMT, NB, 2>()};
-    return {paged_attention_kernel<D, FMT, NB, 1>, wg_waves<D, FMT, NB, 1>()};
+        if (s >= 2) return {paged_attention_kernel<D, FMT, NB, 2, NT>, wg_waves<D, FMT, NB, 2>()};
+    return {paged_attention_kernel<D, FMT, NB, 1, NT>, wg_waves<D, FMT, NB, 1>()};
+}
+
+// Streamed tile loads for calls that read whole rows; plain ones for page lists (see load16).
+template <int D, int FMT, int NB>
+Instance kernel_of(bool page_list) {
+    return page_list ? kernel_of<D, FMT, NB, false>() : kernel_of<D, FMT, NB, true>();
 }
 
 // Calls f.template run<D, FMT, NB>() for the instance of (head dim, format, 16-row column blocks).
@@ -720,7 +733,7 @@ struct Launch {
     const PagedParams* p;
     template <int D, int FMT, int NB>
     int run() const {
-        const Instance in = kernel_of<D, FMT, NB>();
+        const Instance in = kernel_of<D, FMT, NB>(p->page_list != nullptr);
         hipLaunchKernelGGL(in.kernel, dim3(p->grid), dim3(64 * in.waves), 0, stream, *p);
         return check_launch("paged_attention_kernel");
     }
@@ -732,7 +745,7 @@ struct Occupancy {
     template <int D, int FMT, int NB>
     int run() const {
         int blocks = 0;
-        const Instance in = kernel_of<D, FMT, NB>();
+        const Instance in = kernel_of<D, FMT, NB>(false);
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, in.kernel, 64 * in.waves, 0) != hipSuccess ||
             blocks <= 0)
             blocks = 1;
