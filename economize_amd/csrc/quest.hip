@@ -161,10 +161,11 @@ __global__ __launch_bounds__(256) void quest_score_kernel(SelectParams p) {
         for (int w = 0; w < BW; ++w) lw[k][w] = hw[k][w] = make_uint4(0, 0, 0, 0);
         if (page < p1 && j < runs) {
             const int64_t at = b * p.sb_b + kvh * p.sb_h + static_cast<int64_t>(page) * p.sb_p + 8 * j;
+            // the bounds are read once per selection: streamed loads
 #pragma unroll
             for (int w = 0; w < BW; ++w) {
-                lw[k][w] = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(p.kmin) + at * BES)[w];
-                hw[k][w] = reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(p.kmax) + at * BES)[w];
+                lw[k][w] = stream_load16(static_cast<const uint8_t*>(p.kmin) + at * BES + 16 * w);
+                hw[k][w] = stream_load16(static_cast<const uint8_t*>(p.kmax) + at * BES + 16 * w);
             }
         }
     }
