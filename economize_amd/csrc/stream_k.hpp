@@ -380,7 +380,8 @@ __device__ inline void merge_row(const P& p, const Cursor& c, int prev, int64_t 
 // overlap instead of following each other.
 template <int D, int WAVES, int PR = 16>
 struct Pieces {
-    float data[2 * WAVES][PR * (D + 2)];
+    // a piece: the output values of `rows` query rows [r * D + d], then their maxima [rows * D + r], then their sums
+    __align__(16) float data[2 * WAVES][PR * (D + 2)];
     int64_t row[2 * WAVES];  // row_start of the piece's row, -1 for none
     int b[2 * WAVES], kvh[2 * WAVES], tiles[2 * WAVES];
 };
@@ -391,20 +392,20 @@ __device__ inline void clear_pieces(Pieces<D, WAVES, PR>& pc, int wave, int lane
 }
 
 // Stores the segment of row c as piece k: lane (n, g) holds query row n's output channels 16 nd + 4 g + i
-// (value(nd, i)), and m, l of row n.
+// (value(nd, i)), and m, l of row n; four channels per 16-byte LDS store.
 template <int D, int WAVES, int PR, typename V>
 __device__ __forceinline__ void write_piece(Pieces<D, WAVES, PR>& pc, int k, const Cursor& c, int rows, int n, int g,
                                             int lane, float m, float l, V value) {
     float* piece = pc.data[k];
     if (n < rows) {
         if (g == 0) {
-            piece[n] = m;
-            piece[rows + n] = l;
+            piece[rows * D + n] = m;
+            piece[rows * D + rows + n] = l;
         }
 #pragma unroll
         for (int nd = 0; nd < D / 16; ++nd)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) piece[2 * rows + n * D + 16 * nd + 4 * g + i] = value(nd, i);
+            *reinterpret_cast<float4*>(piece + n * D + 16 * nd + 4 * g) =
+                make_float4(value(nd, 0), value(nd, 1), value(nd, 2), value(nd, 3));
     }
     if (lane == 0) {
         pc.row[k] = c.row_start;
@@ -414,11 +415,38 @@ __device__ __forceinline__ void write_piece(Pieces<D, WAVES, PR>& pc, int k, con
     }
 }
 
+// out[b, qi, h, d .. d + 1] of query row r (d even) from its merged accumulators o0, o1, maximum m and sum l (log2
+// units), with the sink logit of head h in the denominator: one 4-byte store where the address allows.
+template <typename P>
+__device__ inline void store_output2(const P& p, int b, int kvh, int r, int d, float o0, float o1, float m, float l) {
+    const int gq = r / p.queries;
+    const int qi = r % p.queries;
+    const int h = kvh * p.groups + gq;
+    if (p.sinks) {
+        const float sink = p.sinks[h] * kLog2e;
+        const float m_new = fmaxf(m, sink);
+        const float a = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - m_new);
+        o0 *= a;
+        o1 *= a;
+        l = l * a + __builtin_amdgcn_exp2f(sink - m_new);
+    }
+    const float inv = l > 0.0f ? 1.0f / fmaxf(l, 1e-30f) : 0.0f;
+    uint16_t* out = p.out + b * p.so_b + qi * p.so_q + h * p.so_h + d;
+    const uint32_t pair = static_cast<uint32_t>(f32_to_bf16(o0 * inv)) | (static_cast<uint32_t>(f32_to_bf16(o1 * inv)) << 16);
+    if ((reinterpret_cast<uintptr_t>(out) & 3) == 0) {
+        *reinterpret_cast<uint32_t*>(out) = pair;
+    } else {
+        out[0] = static_cast<uint16_t>(pair);
+        out[1] = static_cast<uint16_t>(pair >> 16);
+    }
+}
+
 template <int D, int WAVES, int PR, typename P>
 __device__ inline void merge_pieces(const P& p, Pieces<D, WAVES, PR>& pc, int wave, int lane, int64_t wlo, int64_t whi,
                                     int64_t total, int grid, int w) {
     __syncthreads();
     const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
+    const int vals = p.rows * D;  // offset of a piece's maxima (its sums follow them)
     int k = 0, group = 0;
     while (k < 2 * WAVES) {
         const int64_t row = pc.row[k];
@@ -439,46 +467,63 @@ __device__ inline void merge_pieces(const P& p, Pieces<D, WAVES, PR>& pc, int wa
         c.row.tiles = pc.tiles[k];
         c.row_start = row;
         k = k2;
-        if (group++ % WAVES != wave) continue;
         const bool inside = row >= wlo && row + c.row.tiles <= whi;
+        if (inside) {
+            // a row inside the workgroup: every wave merges a share of its outputs, two channels per lane, and writes
+            // them (at the end of the call this merge is on the critical path of the workgroup)
+            for (int e = 2 * (wave * 64 + lane); e < vals; e += 2 * 64 * WAVES) {
+                const int r = e / D, d = e % D;
+                float m = -INFINITY;
+                for (int j = 0; j < 2 * WAVES; ++j)
+                    if ((members >> j) & 1u) m = fmaxf(m, pc.data[j][vals + r]);
+                float l = 0.0f, o0 = 0.0f, o1 = 0.0f;
+                for (int j = 0; j < 2 * WAVES; ++j) {
+                    if (!((members >> j) & 1u)) continue;
+                    const float mj = pc.data[j][vals + r];
+                    if (mj == -INFINITY) continue;
+                    const float cw = __builtin_amdgcn_exp2f(mj - m);
+                    l += pc.data[j][vals + p.rows + r] * cw;
+                    const float2 v = *reinterpret_cast<const float2*>(&pc.data[j][r * D + d]);
+                    o0 += v.x * cw;
+                    o1 += v.y * cw;
+                }
+                store_output2(p, c.b, c.kvh, r, d, o0, o1, m, l);
+            }
+            continue;
+        }
+        // a row cut at the workgroup's range: one wave writes the workgroup's partial and joins the row's merge
+        if (group++ % WAVES != wave) continue;
         float* slot = p.part + (2 * static_cast<int64_t>(w) + (wlo < row ? 1 : 0)) * stride;
-        for (int base = 0; base < p.rows * D; base += 64 * 8) {
+        for (int base = 0; base < vals; base += 64 * 8) {
             const int e = base + lane * 8;
-            const bool active = e < p.rows * D;
+            const bool active = e < vals;
             const int r = active ? e / D : 0;
             const int d = active ? e % D : 0;
             float m = -INFINITY;
             for (int j = 0; j < 2 * WAVES; ++j)
-                if ((members >> j) & 1u) m = fmaxf(m, pc.data[j][r]);
+                if ((members >> j) & 1u) m = fmaxf(m, pc.data[j][vals + r]);
             float l = 0.0f, o[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = 0.0f;
             for (int j = 0; j < 2 * WAVES; ++j) {
                 if (!((members >> j) & 1u)) continue;
-                const float mj = pc.data[j][r];
+                const float mj = pc.data[j][vals + r];
                 if (mj == -INFINITY) continue;
                 const float cw = __builtin_amdgcn_exp2f(mj - m);
-                l += pc.data[j][p.rows + r] * cw;
+                l += pc.data[j][vals + p.rows + r] * cw;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) o[i] += pc.data[j][2 * p.rows + r * D + d + i] * cw;
+                for (int i = 0; i < 8; ++i) o[i] += pc.data[j][r * D + d + i] * cw;
             }
             if (!active) continue;
-            if (inside) {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) store_output(p, c.b, c.kvh, r, d + i, o[i], m, l);
-            } else {
-                if (d == 0) {
-                    coherent_store(slot + r, m);
-                    coherent_store(slot + p.rows + r, l);
-                }
-#pragma unroll
-                for (int i = 0; i < 8; ++i) coherent_store(slot + 2 * p.rows + r * D + d + i, o[i]);
+            if (d == 0) {
+                coherent_store(slot + r, m);
+                coherent_store(slot + p.rows + r, l);
             }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) coherent_store(slot + 2 * p.rows + r * D + d + i, o[i]);
         }
-        if (!inside) {
-            // the workgroup's partial joins the others' in the workspace; the last workgroup to finish merges them
-            hand_off<D>(p, c, total, grid, lane);
-        }
+        // the workgroup's partial joins the others' in the workspace; the last workgroup to finish merges them
+        hand_off<D>(p, c, total, grid, lane);
     }
 }
 
