@@ -366,7 +366,7 @@ kivi_attention_kernel(KiviParams p) {
     const int n = lane & 15;
     const int g = lane >> 4;
     const int qn = PR < 16 ? min(n, PR) : n;  // the query row of MFMA column n
-    const int w = blockIdx.x;  // workgroup
+    const int w = xcd_range(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));  // the workgroup's range
     const int grid = gridDim.x;
 
     // row geometry: one load of the lengths for batches of at most 64 rows

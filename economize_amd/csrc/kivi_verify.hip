@@ -97,7 +97,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const int wave = uniform(tid >> 6);
     const int n = lane & 15, g = lane >> 4;
     const int r = 16 * wave + n;  // the lane's query row (MFMA column n)
-    const int w = blockIdx.x;
+    const int w = xcd_range(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));  // the workgroup's range
     const int grid = gridDim.x;
     // the lane's dequantization items (pg is the same in a wave)
     const int pg = wave >> 1;

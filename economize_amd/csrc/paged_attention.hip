@@ -161,32 +161,42 @@ __device__ __forceinline__ void load_query(const PagedParams& p, const Cursor& c
     }
 }
 
-// Issues the loads of the tile under cursor c (lane (n, g): K rows of tile page n / 4, V channel n of page g), and
-// the query operand of its row into the tile.
-template <int D, int FMT, int NB, bool NT>
-__device__ __forceinline__ void issue_tile(const PagedParams& p, const Cursor& c, int n, int g, int lane, PageWindow& win,
-                                  Tile<D, FMT, NB>& tile) {
-    using T = Tile<D, FMT, NB>;
-    ensure_window(p, c, lane, win);
-    const int at = TILE * c.t - win.base;
-    const int pk = __shfl(win.physical, at + (n >> 2));
-    const int pv = __shfl(win.physical, at + g);
+// The K/V loads of the tile at window offset `at`. K is read page-major: for tile page v, lane (n, g) loads token n,
+// runs 4 u + g (one page per load instruction, four runs of 256 contiguous bytes: whole 128-byte lines; a mapping
+// that put four pages in one instruction read half lines and streamed 2.5 us slower over the fp8 Llama-3-8B decode
+// shape, 42.1 against 39.6 us for the loads alone). V: lane (n, g) loads channels 16 nd + n of tile page g. A page
+// that holds nothing reads page 0 (its scores and values are masked when the tile is computed), and so does a dummy
+// issue past the end of a wave's range: every path issues the same loads.
+template <int D, int FMT, int NB, bool RQ, bool NT>
+__device__ __forceinline__ void issue_kv(const PagedParams& p, const Cursor& c, int n, int g, int at,
+                                         const PageWindow& win, Tile<D, FMT, NB, RQ>& tile, bool dummy) {
+    using T = Tile<D, FMT, NB, RQ>;
+    const int pv = dummy ? 0 : __shfl(win.physical, at + g);
     tile.lv = __shfl(win.logical, at + g);
     tile.vcnt = tile.lv >= 0 ? min(max(c.row.len - tile.lv * PAGE, 0), PAGE) : 0;
     load_mask_bits(p, c, n, tile);
-    // Every lane issues the same loads whatever its pages are (a page that holds nothing reads page 0, and its
-    // scores and values are masked when the tile is computed): with the same number of loads on every path, the
-    // wait before a tile's use leaves the younger tiles' loads in flight.
-    const uint8_t* kp = p.k_cache + c.kvh * p.kc_head + static_cast<int64_t>(pk >= 0 ? pk : 0) * p.kc_page;
+    const uint8_t* kh = p.k_cache + c.kvh * p.kc_head;
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
+    for (int v = 0; v < 4; ++v) {
+        const int pk = dummy ? 0 : __builtin_amdgcn_readlane(win.physical, at + v);
+        const uint8_t* kp = kh + static_cast<int64_t>(pk >= 0 ? pk : 0) * p.kc_page;
 #pragma unroll
-        for (int u = 0; u < T::NU; ++u) tile.k[v][u] = load16<NT>(kp + ((4 * u + g) * PAGE + 4 * v + (n & 3)) * 16);
+        for (int u = 0; u < T::NU; ++u) tile.k[v][u] = load16<NT>(kp + ((4 * u + g) * PAGE + n) * 16);
+    }
     const uint8_t* vp = p.v_cache + c.kvh * p.vc_head + static_cast<int64_t>(pv >= 0 ? pv : 0) * p.vc_page;
 #pragma unroll
     for (int nd = 0; nd < T::ND; ++nd)
 #pragma unroll
         for (int w = 0; w < T::NV; ++w) tile.v[nd][w] = load16<NT>(vp + (16 * nd + n) * PAGE * T::ES + 16 * w);
+}
+
+// Issues the loads of the tile under cursor c and the query operand of its row into the tile.
+template <int D, int FMT, int NB, bool NT>
+__device__ __forceinline__ void issue_tile(const PagedParams& p, const Cursor& c, int n, int g, int lane, PageWindow& win,
+                                  Tile<D, FMT, NB>& tile, bool dummy) {
+    using T = Tile<D, FMT, NB>;
+    ensure_window(p, c, lane, win);
+    issue_kv<D, FMT, NB, false, NT>(p, c, n, g, TILE * c.t - win.base, win, tile, dummy);
     // the query operand: lane (n, g) holds query row nb * 16 + n, channels of k-step j as the K runs order them (a lane
     // of a row past the group reads row 0: its MFMA column is computed and never stored)
     constexpr int E = 16 / T::ES;
@@ -209,26 +219,24 @@ __device__ __forceinline__ void issue_tile(const PagedParams& p, const Cursor& c
 template <int D, int FMT, int NB, bool NT>
 __device__ __forceinline__ void issue_tile_rq(const PagedParams& p, const Cursor& c, int n, int g, int lane,
                                               PageWindow& win, Tile<D, FMT, NB, true>& tile,
-                                              bf16x8 (&q_next)[NB][D / 32], bool load_q) {
-    using T = Tile<D, FMT, NB, true>;
+                                              bf16x8 (&q_next)[NB][D / 32], bool load_q, bool dummy) {
     if (load_q) load_query<D, FMT, NB>(p, c, n, g, q_next);
     ensure_window(p, c, lane, win);
-    const int at = TILE * c.t - win.base;
-    const int pk = __shfl(win.physical, at + (n >> 2));
-    const int pv = __shfl(win.physical, at + g);
-    tile.lv = __shfl(win.logical, at + g);
-    tile.vcnt = tile.lv >= 0 ? min(max(c.row.len - tile.lv * PAGE, 0), PAGE) : 0;
-    load_mask_bits(p, c, n, tile);
-    const uint8_t* kp = p.k_cache + c.kvh * p.kc_head + static_cast<int64_t>(pk >= 0 ? pk : 0) * p.kc_page;
-#pragma unroll
-    for (int v = 0; v < 4; ++v)
-#pragma unroll
-        for (int u = 0; u < T::NU; ++u) tile.k[v][u] = load16<NT>(kp + ((4 * u + g) * PAGE + 4 * v + (n & 3)) * 16);
-    const uint8_t* vp = p.v_cache + c.kvh * p.vc_head + static_cast<int64_t>(pv >= 0 ? pv : 0) * p.vc_page;
-#pragma unroll
-    for (int nd = 0; nd < T::ND; ++nd)
-#pragma unroll
-        for (int w = 0; w < T::NV; ++w) tile.v[nd][w] = load16<NT>(vp + (16 * nd + n) * PAGE * T::ES + 16 * w);
+    issue_kv<D, FMT, NB, true, NT>(p, c, n, g, TILE * c.t - win.base, win, tile, dummy);
+}
+
+// The 4 x 4 transpose of dword blocks over the lane rows (16 lanes each): row g's x[v] becomes row v's x[g], that is
+// after the call row g holds in x[v] what row v held in x[g]. Two stages of lane swaps (the upper and lower 32
+// lanes, then odd and even rows).
+__device__ __forceinline__ void transpose_rows4(uint32_t (&x)[4]) {
+    const auto a = __builtin_amdgcn_permlane32_swap(x[0], x[2], false, false);
+    const auto b = __builtin_amdgcn_permlane32_swap(x[1], x[3], false, false);
+    const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+    const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+    x[0] = c[0];
+    x[1] = c[1];
+    x[2] = d[0];
+    x[3] = d[1];
 }
 
 // Clears the V bytes of the tokens a tile page does not hold (past the row's end, or the whole page when it holds
@@ -297,7 +305,7 @@ paged_attention_kernel(PagedParams p) {
     const int wave = WAVES > 1 ? uniform(static_cast<int>(threadIdx.x) >> 6) : 0;
     const int n = lane & 15;
     const int g = lane >> 4;
-    const int w = blockIdx.x;  // workgroup
+    const int w = xcd_range(static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x));  // the workgroup's range
     const int grid = gridDim.x;
 
     // row geometry: one load of the lengths for batches of at most 64 rows
@@ -413,16 +421,21 @@ paged_attention_kernel(PagedParams p) {
                     }
         }
         if (p.mask || __ballot(tile.lv < 0 || first + PAGE > all_see) != 0) {
+            // score (v, i) of lane (n, g) is token 4 g + i of tile page v, whose logical page row v of the lanes holds
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
+            for (int v = 0; v < 4; ++v) {
+                const int lv = __builtin_amdgcn_readlane(tile.lv, 16 * v);
 #pragma unroll
-                for (int v = 0; v < 4; ++v)
+                for (int nb = 0; nb < NB; ++nb) {
+                    const uint32_t bits = p.mask ? static_cast<uint32_t>(__shfl(static_cast<int>(tile.mw[nb]), 16 * v + n)) >> (4 * g) : 0u;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        bool ok = tile.lv >= 0 && static_cast<float>(first + 4 * v + i) < limit[nb];
-                        if (p.mask) ok = ok && ((tile.mw[nb] >> (4 * v + i)) & 1u);
+                        bool ok = lv >= 0 && static_cast<float>(lv * PAGE + 4 * g + i) < limit[nb];
+                        if (p.mask) ok = ok && ((bits >> i) & 1u);
                         s[v][nb][i] = ok ? s[v][nb][i] : -INFINITY;
                     }
+                }
+            }
         }
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
@@ -467,37 +480,40 @@ paged_attention_kernel(PagedParams p) {
                     sum += pw[v][i];
                 }
             l_i[nb] += sum;
+            // lane (n, g) holds the weights of tokens 4 g .. 4 g + 3 of every tile page; the P operand of lane (n, g)
+            // is tile page g's 16 tokens (the page whose V channels it loads): a transpose of 4-token blocks over the
+            // lane rows
+            if constexpr (FMT == BF16) {
+                uint32_t hi[2][4], lo[2][4];
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const float* a = pw[2 * u];
-                const float* c = pw[2 * u + 1];
-                if constexpr (FMT == BF16) {
-                    uint4 hi4;
-                    hi4.x = pack_bf16x2(a[0], a[1]);
-                    hi4.y = pack_bf16x2(a[2], a[3]);
-                    hi4.z = pack_bf16x2(c[0], c[1]);
-                    hi4.w = pack_bf16x2(c[2], c[3]);
-                    const uint32_t words[4] = {hi4.x, hi4.y, hi4.z, hi4.w};
-                    const float vals[8] = {a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
-                    float lo8[8];
+                for (int v = 0; v < 4; ++v)
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        lo8[e] = vals[e] - bits_f32(e & 1 ? words[e >> 1] & 0xFFFF0000u : words[e >> 1] << 16);
-                    uint4 lo4;
-                    lo4.x = pack_bf16x2(lo8[0], lo8[1]);
-                    lo4.y = pack_bf16x2(lo8[2], lo8[3]);
-                    lo4.z = pack_bf16x2(lo8[4], lo8[5]);
-                    lo4.w = pack_bf16x2(lo8[6], lo8[7]);
-                    pop_hi[nb][u] = __builtin_bit_cast(bf16x8, hi4);
-                    pop_lo[nb][u] = __builtin_bit_cast(bf16x8, lo4);
-                } else {
-                    uint4 w4;
-                    w4.x = pack_f16x2(a[0], a[1]);
-                    w4.y = pack_f16x2(a[2], a[3]);
-                    w4.z = pack_f16x2(c[0], c[1]);
-                    w4.w = pack_f16x2(c[2], c[3]);
-                    pop_h[nb][u] = __builtin_bit_cast(f16x8, w4);
+                    for (int h = 0; h < 2; ++h) {
+                        const float x0 = pw[v][2 * h], x1 = pw[v][2 * h + 1];
+                        hi[h][v] = pack_bf16x2(x0, x1);
+                        lo[h][v] = pack_bf16x2(x0 - bits_f32(hi[h][v] << 16), x1 - bits_f32(hi[h][v] & 0xFFFF0000u));
+                    }
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    transpose_rows4(hi[h]);
+                    transpose_rows4(lo[h]);
                 }
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    pop_hi[nb][u] = __builtin_bit_cast(bf16x8, make_uint4(hi[0][2 * u], hi[1][2 * u], hi[0][2 * u + 1], hi[1][2 * u + 1]));
+                    pop_lo[nb][u] = __builtin_bit_cast(bf16x8, make_uint4(lo[0][2 * u], lo[1][2 * u], lo[0][2 * u + 1], lo[1][2 * u + 1]));
+                }
+            } else {
+                uint32_t w[2][4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) w[h][v] = pack_f16x2(pw[v][2 * h], pw[v][2 * h + 1]);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) transpose_rows4(w[h]);
+#pragma unroll
+                for (int u = 0; u < 2; ++u)
+                    pop_h[nb][u] = __builtin_bit_cast(f16x8, make_uint4(w[0][2 * u], w[1][2 * u], w[0][2 * u + 1], w[1][2 * u + 1]));
             }
         }
         // O^T += V^T P^T: lane (n, g) supplies channel 16 nd + n of tile page g
@@ -584,14 +600,17 @@ paged_attention_kernel(PagedParams p) {
         Cursor icur = cur;  // the next tile to issue, at sequence offset ipos
         int64_t ipos = lo;
 
-        // Every step issues one tile, past the end of the range a repeat of the range's last tile (read from L2 and never
-        // computed): with the same number of loads issued on every path through the loop, the wait before a tile's use
-        // counts the younger tiles' loads and leaves them in flight.
+        // Every step issues one tile, past the end of the range a dummy that reads cache page 0 (never computed): with
+        // the same number of loads issued on every path through the loop, the wait before a tile's use counts the
+        // younger tiles' loads and leaves them in flight. (A branch around the issue, with a wait for every load on
+        // the path that issues nothing, measured no faster at the fp8 Llama-3-8B decode shape and 4 us slower for
+        // Quest's page lists.)
         auto issue_next = [&](T& buf, Cursor& slot) __attribute__((always_inline)) {
+            const bool dummy = ipos >= hi;
             if constexpr (kRowQ)
-                issue_tile_rq<D, FMT, NB, NT>(p, icur, n, g, lane, win, buf, q_next, icur.t == 0 || ipos == lo);
+                issue_tile_rq<D, FMT, NB, NT>(p, icur, n, g, lane, win, buf, q_next, icur.t == 0 || ipos == lo, dummy);
             else
-                issue_tile<D, FMT, NB, NT>(p, icur, n, g, lane, win, buf);
+                issue_tile<D, FMT, NB, NT>(p, icur, n, g, lane, win, buf, dummy);
             slot = icur;
             if (ipos < hi) {
                 if (ipos + 1 < hi) advance(p, icur, small ? &rt : nullptr);

@@ -42,6 +42,17 @@ __device__ inline int64_t wave_inclusive_sum(int64_t x, int lane) {
 
 __device__ inline int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
+// The tile range of workgroup `block` of `grid`. Workgroups go to the 8 XCDs in turn (XCD block % 8); here each XCD
+// takes a contiguous block of the ranges, so that neighbouring ranges (the same rows, the next KV heads) share an
+// XCD's L2 and every XCD reads rows of every KV head. With range = block and one row per workgroup, XCD x read only
+// KV head x of 8, a fixed 2 KB slot of every 16 KB page group: at the fp8 Llama-3-8B decode shape the even XCDs
+// then finished their tiles 1.7 us before the odd ones.
+__device__ inline int xcd_range(int block, int grid) {
+    const int x = block & 7, k = block >> 3;
+    const int q = grid >> 3, r = grid & 7;
+    return x * q + min(x, r) + k;
+}
+
 // ptr[index] for a wave-uniform index through the scalar cache (a scalar load waits on its own counter, not on the
 // vector loads in flight). Only for data no kernel of the call writes.
 template <typename T>
@@ -444,48 +455,56 @@ __device__ inline void store_output2(const P& p, int b, int kvh, int r, int d, f
 template <int D, int WAVES, int PR, typename P>
 __device__ inline void merge_pieces(const P& p, Pieces<D, WAVES, PR>& pc, int wave, int lane, int64_t wlo, int64_t whi,
                                     int64_t total, int grid, int w) {
+    constexpr int K = 2 * WAVES;  // piece slots
     __syncthreads();
     const int64_t stride = static_cast<int64_t>(p.rows) * (D + 2);
     const int vals = p.rows * D;  // offset of a piece's maxima (its sums follow them)
-    int k = 0, group = 0;
-    while (k < 2 * WAVES) {
-        const int64_t row = pc.row[k];
-        if (row < 0) {
-            ++k;
-            continue;
-        }
-        // the pieces of one row are consecutive among the valid ones (rows follow the tile order)
-        uint32_t members = 0;
-        int k2 = k;
-        while (k2 < 2 * WAVES && (pc.row[k2] == row || pc.row[k2] < 0)) {
-            if (pc.row[k2] == row) members |= 1u << k2;
-            ++k2;
-        }
+    // The piece table in one read (lane j < K holds piece j), so that finding the rows and their pieces takes no
+    // further LDS round trip: at the end of the call this merge is on the critical path of the workgroup.
+    const bool holder = lane < K;
+    int64_t prow = holder ? pc.row[lane] : -1;
+    const int pb = holder ? pc.b[lane] : 0;
+    const int pkvh = holder ? pc.kvh[lane] : 0;
+    const int ptiles = holder ? pc.tiles[lane] : 0;
+    int group = 0;
+    for (;;) {
+        const uint64_t live = __ballot(prow >= 0);
+        if (live == 0) break;
+        const int k = static_cast<int>(__builtin_ctzll(live));  // the first piece of the next row (pieces follow the tiles)
+        const int64_t row = uniform64(__shfl(prow, k));
+        const uint32_t members = static_cast<uint32_t>(__ballot(prow == row));
+        if (prow == row) prow = -1;
         Cursor c{};
-        c.b = pc.b[k];
-        c.kvh = pc.kvh[k];
-        c.row.tiles = pc.tiles[k];
+        c.b = uniform(__shfl(pb, k));
+        c.kvh = uniform(__shfl(pkvh, k));
+        c.row.tiles = uniform(__shfl(ptiles, k));
         c.row_start = row;
-        k = k2;
         const bool inside = row >= wlo && row + c.row.tiles <= whi;
         if (inside) {
             // a row inside the workgroup: every wave merges a share of its outputs, two channels per lane, and writes
-            // them (at the end of the call this merge is on the critical path of the workgroup)
+            // them; every slot is read (the reads in flight together) and a slot outside the row weighs nothing
             for (int e = 2 * (wave * 64 + lane); e < vals; e += 2 * 64 * WAVES) {
                 const int r = e / D, d = e % D;
+                float mj[K], lj[K];
+                float2 vj[K];
+#pragma unroll
+                for (int j = 0; j < K; ++j) {
+                    mj[j] = pc.data[j][vals + r];
+                    lj[j] = pc.data[j][vals + p.rows + r];
+                    vj[j] = *reinterpret_cast<const float2*>(&pc.data[j][r * D + d]);
+                }
                 float m = -INFINITY;
-                for (int j = 0; j < 2 * WAVES; ++j)
-                    if ((members >> j) & 1u) m = fmaxf(m, pc.data[j][vals + r]);
+#pragma unroll
+                for (int j = 0; j < K; ++j)
+                    if ((members >> j) & 1u) m = fmaxf(m, mj[j]);
                 float l = 0.0f, o0 = 0.0f, o1 = 0.0f;
-                for (int j = 0; j < 2 * WAVES; ++j) {
-                    if (!((members >> j) & 1u)) continue;
-                    const float mj = pc.data[j][vals + r];
-                    if (mj == -INFINITY) continue;
-                    const float cw = __builtin_amdgcn_exp2f(mj - m);
-                    l += pc.data[j][vals + p.rows + r] * cw;
-                    const float2 v = *reinterpret_cast<const float2*>(&pc.data[j][r * D + d]);
-                    o0 += v.x * cw;
-                    o1 += v.y * cw;
+#pragma unroll
+                for (int j = 0; j < K; ++j) {
+                    if (!((members >> j) & 1u) || mj[j] == -INFINITY) continue;
+                    const float cw = __builtin_amdgcn_exp2f(mj[j] - m);
+                    l += lj[j] * cw;
+                    o0 += vj[j].x * cw;
+                    o1 += vj[j].y * cw;
                 }
                 store_output2(p, c.b, c.kvh, r, d, o0, o1, m, l);
             }
@@ -499,20 +518,31 @@ __device__ inline void merge_pieces(const P& p, Pieces<D, WAVES, PR>& pc, int wa
             const bool active = e < vals;
             const int r = active ? e / D : 0;
             const int d = active ? e % D : 0;
+            float mj[K];
+#pragma unroll
+            for (int j = 0; j < K; ++j) mj[j] = pc.data[j][vals + r];
             float m = -INFINITY;
-            for (int j = 0; j < 2 * WAVES; ++j)
-                if ((members >> j) & 1u) m = fmaxf(m, pc.data[j][vals + r]);
+#pragma unroll
+            for (int j = 0; j < K; ++j)
+                if ((members >> j) & 1u) m = fmaxf(m, mj[j]);
             float l = 0.0f, o[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) o[i] = 0.0f;
-            for (int j = 0; j < 2 * WAVES; ++j) {
-                if (!((members >> j) & 1u)) continue;
-                const float mj = pc.data[j][vals + r];
-                if (mj == -INFINITY) continue;
-                const float cw = __builtin_amdgcn_exp2f(mj - m);
-                l += pc.data[j][vals + p.rows + r] * cw;
 #pragma unroll
-                for (int i = 0; i < 8; ++i) o[i] += pc.data[j][r * D + d + i] * cw;
+            for (int j = 0; j < K; ++j) {
+                if (!((members >> j) & 1u) || mj[j] == -INFINITY) continue;
+                const float cw = __builtin_amdgcn_exp2f(mj[j] - m);
+                l += pc.data[j][vals + p.rows + r] * cw;
+                const float4 v0 = *reinterpret_cast<const float4*>(&pc.data[j][r * D + d]);
+                const float4 v1 = *reinterpret_cast<const float4*>(&pc.data[j][r * D + d + 4]);
+                o[0] += v0.x * cw;
+                o[1] += v0.y * cw;
+                o[2] += v0.z * cw;
+                o[3] += v0.w * cw;
+                o[4] += v1.x * cw;
+                o[5] += v1.y * cw;
+                o[6] += v1.z * cw;
+                o[7] += v1.w * cw;
             }
             if (!active) continue;
             if (d == 0) {
