@@ -301,6 +301,25 @@ __device__ inline int block_scan(int x, int* lds4, int* total) {
     return x + before;
 }
 
+// Inclusive scans of two values per thread over a 256-thread workgroup, through one exchange (lds8: 8 ints).
+__device__ inline int2 block_scan2(int x, int y, int* lds8) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    x = wave_scan(x);
+    y = wave_scan(y);
+    if (lane == 63) {
+        lds8[wave] = x;
+        lds8[4 + wave] = y;
+    }
+    __syncthreads();
+    int bx = 0, by = 0;
+    for (int w = 0; w < wave; ++w) {
+        bx += lds8[w];
+        by += lds8[4 + w];
+    }
+    __syncthreads();
+    return make_int2(x + bx, y + by);
+}
+
 // One workgroup of 256 threads per (row, KV head): the top `count` of the row's committed pages by score, written in
 // increasing page order, then -1. With IN_LDS the row's keys are read from global memory once, into LDS; otherwise
 // (rows of more than TOPK_LDS_KEYS pages) every pass reads them from global memory again.
@@ -309,27 +328,28 @@ __global__ __launch_bounds__(256) void quest_topk_kernel(SelectParams p) {
     extern __shared__ uint32_t lds_keys[];
     __shared__ int hist[2048];
     __shared__ __align__(16) uint32_t cand[256];
-    __shared__ int lds4[4];
+    __shared__ int lds4[4], lds8[8];
     __shared__ uint32_t shared_prefix, red[8];
     __shared__ int shared_rem, shared_m, shared_d, cand_count;
     const int row = blockIdx.x;
     const int b = row / p.kv_heads;
     const int t = threadIdx.x;
     const int lane = t & 63;
+    const float* scores = p.scores + static_cast<int64_t>(row) * score_stride(p.max_done);
+    if constexpr (IN_LDS) {
+        // every page below max_done has a score (-inf from done on): the loads go out with the read of done[b]
+#pragma unroll 8
+        for (int i = t; i < p.max_done; i += 256) lds_keys[i] = score_key(scores[i]);
+    }
     const int n = min(max(p.done[b], 0), p.max_done);
     const int count = min(p.pages, p.max_done);
     int32_t* out = p.out + static_cast<int64_t>(row) * p.pages;
-    const float* scores = p.scores + static_cast<int64_t>(row) * score_stride(p.max_done);
     int total = 0;
     if (n <= count || count <= 0) {  // every committed page (or none to select)
         for (int i = t; i < p.pages; i += 256) out[i] = i < n ? i : -1;
         return;
     }
-    if constexpr (IN_LDS) {
-#pragma unroll 8
-        for (int i = t; i < n; i += 256) lds_keys[i] = score_key(scores[i]);
-        __syncthreads();
-    }
+    if constexpr (IN_LDS) __syncthreads();
     auto key_at = [&](int i) __attribute__((always_inline)) -> uint32_t {
         if constexpr (IN_LDS)
             return lds_keys[i];
@@ -465,27 +485,27 @@ __global__ __launch_bounds__(256) void quest_topk_kernel(SelectParams p) {
         }
         const int span = C > 0 ? C : i1 - i0;
         auto key_of = [&](int k) __attribute__((always_inline)) { return C > 0 ? held[k] : key_at(i0 + k); };
-        int eq = 0;
-#pragma unroll
-        for (int k = 0; k < span; ++k) eq += i0 + k < i1 && key_of(k) == prefix ? 1 : 0;
-        const int eq_before = block_scan(eq, lds4, &total) - eq;
-        int sel = 0;
-        int e = eq_before;
+        // one scan of the thread's keys above the threshold and of those equal to it: the threads before t hold
+        // keys above it, all taken, and eq_before equal ones, of which the first rem are taken
+        int eq = 0, above = 0;
 #pragma unroll
         for (int k = 0; k < span; ++k) {
             if (i0 + k >= i1) continue;
             const uint32_t key = key_of(k);
-            if (key > prefix) ++sel;
-            else if (key == prefix) sel += e++ < rem ? 1 : 0;
+            eq += key == prefix ? 1 : 0;
+            above += key > prefix ? 1 : 0;
         }
-        int pos = block_scan(sel, lds4, &total) - sel;
-        e = eq_before;
+        const int2 incl = block_scan2(above, eq, lds8);
+        const int eq_before = incl.y - eq;
+        const int eq_taken = min(max(rem - eq_before, 0), eq);  // this thread's first eq_taken equal keys
+        int pos = incl.x - above + min(eq_before, rem);
+        int e = 0;
 #pragma unroll
         for (int k = 0; k < span; ++k) {
             if (i0 + k >= i1) continue;
             const uint32_t key = key_of(k);
             bool take = key > prefix;
-            if (key == prefix) take = e++ < rem;
+            if (key == prefix) take = e++ < eq_taken;
             if (take) out[pos++] = i0 + k;
         }
     };

@@ -86,6 +86,7 @@ def _to_bf16(x: np.ndarray) -> torch.Tensor:
     (2, 8, 8, 1, 64, 40, 9),
     (2, 16, 4, 2, 128, 2048, 63),
     (2, 8, 2, 1, 256, 77, 100),  # more pages asked than exist
+    (2, 8, 2, 1, 128, 4096, 127),  # 16 keys per selecting thread
     (1, 4, 1, 3, 64, 5000, 255),
     (2, 8, 2, 1, 512, 100, 20),  # 64 lanes per page, 16 pages per scoring workgroup
     (1, 4, 1, 1, 64, 20000, 511),  # more committed pages than the selection holds in LDS
