@@ -375,8 +375,8 @@ int dense_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, in
     if ((k_scale || v_scale) && !fp8) return fail("decode: per-head scales apply to fp8 K/V only");
     const int es = element_bytes(kv_format), qs = element_bytes(q_format);
     for (int dim : {head_dim, value_dim})
-        if (dim <= 0 || dim % 8 || (dim * es) % 16 || dim > 256)
-            return fail("decode: head dims must be positive multiples of 8 (of 16 for fp8), at most 256");
+        if (dim <= 0 || dim % 8 || (dim * es) % 16 || dim > (es == 4 ? 256 : 512))
+            return fail("decode: head dims must be positive multiples of 8 (of 16 for fp8), at most 512 (256 for fp32)");
     auto aligned = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
     if (!aligned(q) || !aligned(k) || !aligned(v))
         return fail("decode: query, key and value must be 16-byte aligned");
@@ -612,7 +612,7 @@ int eco_fp8_encode(const void* src, int32_t in_format, int64_t ss_b, int64_t ss_
                    int32_t tokens, int32_t head_dim, const float* head_scale, float* token_scale, int64_t st_b,
                    int64_t st_h, int64_t st_t, void* stream) {
     if (batch < 0 || heads < 0 || tokens < 0) return fail("fp8 encode: negative shape");
-    if (head_dim <= 0 || head_dim > 256) return fail("fp8 encode: head dim must be in 1..256");
+    if (head_dim <= 0 || head_dim > 512) return fail("fp8 encode: head dim must be in 1..512");
     if (static_cast<int64_t>(batch) * heads * tokens == 0) return 0;
     if (!src || !dst) return fail("fp8 encode: null source or destination");
     if (in_format != BF16 && in_format != FP16 && in_format != FP32)

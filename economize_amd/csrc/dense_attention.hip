@@ -201,18 +201,23 @@ __device__ __forceinline__ uint32_t word_of(uint4 x, int i) {
 }
 
 // CB: 0, or the code bits of a cells instance that reads quantized keys and values through their codes.
+// Heads wider than 256 channels (DP = 512; Gemma-4's global layers, attention/decode.py:216-232): a wave computes its
+// rows' full scores and accumulates one slice of DV = 256 value channels, slice blockIdx.z (the reference's value
+// tiles), at one wave per SIMD; the slices of a block and its splits count on the block's one counter, and the last
+// of them merges every channel.
 template <int DP, int FMT, int QF, bool MASKED, int CB = 0>
-__global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
+__global__ __launch_bounds__(64, DP > 256 ? 1 : 2) void dense_split_kernel(DenseParams p) {
     static_assert(CB == 0 || (DP == 128 && FMT == BF16 && QF == BF16 && !MASKED),
                   "codes are read for bf16 cells of 128 channels only");
     constexpr int ES = elem_bytes<FMT>();
+    constexpr int DV = DP > 256 ? 256 : DP;  // value channels of a wave
     constexpr int KS = DP / 32;  // k-steps of the S MFMA
-    constexpr int ND = DP / 16;  // value blocks of 16 channels
+    constexpr int ND = DV / 16;  // value blocks of 16 channels
     constexpr bool KLO = two_terms<FMT>();
     constexpr bool QLO = two_terms<QF>();
-    constexpr int ROW = DP * ES + 16;          // LDS bytes per staged value row
-    constexpr int CHUNKS = TK * DP * ES / 16;  // 16-byte chunks of a staged value tile (a multiple of 64)
-    constexpr int CPR = DP * ES / 16;          // chunks per value row
+    constexpr int ROW = DV * ES + 16;          // LDS bytes per staged value row
+    constexpr int CHUNKS = TK * DV * ES / 16;  // 16-byte chunks of a staged value tile (a multiple of 64)
+    constexpr int CPR = DV * ES / 16;          // chunks per value row
     constexpr int CPL = CHUNKS / 64;           // chunks per lane
     constexpr bool kStage = CPL <= 8;          // the tile's values pass through registers (loads issued first)
     constexpr int KW = ES == 4 ? 2 : 1;        // 16-byte words of 8 key elements (fp8: the low half of one)
@@ -231,6 +236,7 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
     const int n = lane & 15, g = lane >> 4;
     const int prog = blockIdx.x;
     const int split = blockIdx.y;
+    const int v0 = static_cast<int>(blockIdx.z) * DV;  // the wave's first value channel
     const int mt = prog % p.m_tiles;
     const int kvh = (prog / p.m_tiles) % p.kv_heads;
     const int b = prog / (p.m_tiles * p.kv_heads);
@@ -430,7 +436,7 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
             for (int i = 0; i < CPL; ++i) {
                 const int chunk = lane + 64 * i;
                 const int t = min(t0 + chunk / CPR, t_end - 1);
-                const int c = (chunk % CPR) * (16 / ES);
+                const int c = v0 + (chunk % CPR) * (16 / ES);
                 vreg[i] = stream_load16(value_row(t) + (c < p.value_dim ? c : 0) * ES);
             }
 #pragma unroll
@@ -490,7 +496,7 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
 #pragma unroll
             for (int i = 0; i < CPL; ++i) {
                 const int chunk = lane + 64 * i;
-                const bool ok = t0 + chunk / CPR < t_end && (chunk % CPR) * (16 / ES) < p.value_dim;
+                const bool ok = t0 + chunk / CPR < t_end && v0 + (chunk % CPR) * (16 / ES) < p.value_dim;
                 *reinterpret_cast<uint4*>(vtile + (chunk / CPR) * ROW + (chunk % CPR) * 16) =
                     ok ? vreg[i] : make_uint4(0, 0, 0, 0);
             }
@@ -499,7 +505,8 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
                 const int t = chunk / CPR;
                 const int c = (chunk % CPR) * (16 / ES);
                 uint4 x = make_uint4(0, 0, 0, 0);
-                if (t0 + t < t_end && c < p.value_dim) x = *reinterpret_cast<const uint4*>(value_row(t0 + t) + c * ES);
+                if (t0 + t < t_end && v0 + c < p.value_dim)
+                    x = *reinterpret_cast<const uint4*>(value_row(t0 + t) + (v0 + c) * ES);
                 *reinterpret_cast<uint4*>(vtile + t * ROW + (chunk % CPR) * 16) = x;
             }
         }
@@ -617,8 +624,8 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the tile's LDS stores (one wave: in order)
 #pragma unroll
         for (int nd = 0; nd < ND; ++nd) {
-            const int c = 16 * nd + n;
-            if (16 * nd >= p.value_dim) break;
+            const int c = 16 * nd + n;  // (of the wave's slice)
+            if (v0 + 16 * nd >= p.value_dim) break;
             bf16x8 vh, vl;
             if constexpr (FMT == BF16) {  // the staged bits are the operand (no widening and rounding back)
 #pragma unroll
@@ -678,7 +685,7 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
         for (int nd = 0; nd < ND; ++nd)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int d = 16 * nd + 4 * g + i;
+                const int d = v0 + 16 * nd + 4 * g + i;
                 if (d < p.value_dim) store_out<QF>(p, out_at(qi, h, d), acc[nd][i] * vs * a * inv);
             }
         return;
@@ -689,14 +696,15 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
     const int64_t prog_part = static_cast<int64_t>(prog) * p.splits * 16;
     if (r_ok) {
         float* slot = p.part + (prog_part + split * 16 + n) * slot_stride;
-        if (g == 0) {
+        if (g == 0 && blockIdx.z == 0) {  // (every value slice has the same maximum and sum)
             coherent_store(slot, m_i);
             coherent_store(slot + 1, l_i);
         }
 #pragma unroll
         for (int nd = 0; nd < ND; ++nd)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) coherent_store(slot + 2 + 16 * nd + 4 * g + i, acc[nd][i] * vs);
+            for (int i = 0; i < 4; ++i)
+                if (v0 + 16 * nd < p.value_dim) coherent_store(slot + 2 + v0 + 16 * nd + 4 * g + i, acc[nd][i] * vs);
     }
     // The hand-off to the last split to finish: the partials are written and read as agent-scope atomics (sc1), so
     // completion orders them; the compiler may not move the stores past the count (a signal fence), the wave waits
@@ -706,7 +714,7 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
     __builtin_amdgcn_s_waitcnt(0);
     int prev = 0;
     if (lane == 0) prev = __hip_atomic_fetch_add(p.counters + prog, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (__shfl(prev, 0) != p.splits - 1) return;
+    if (__shfl(prev, 0) != p.splits * static_cast<int>(gridDim.z) - 1) return;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 
     // ---- the merge by log-sum-exp: lane-owned runs of 8 channels of one query row, the splits folded in batches of 4
@@ -766,6 +774,10 @@ __global__ __launch_bounds__(64, 2) void dense_split_kernel(DenseParams p) {
 template <int DP, int FMT, int QF>
 int launch_dense(const DenseParams& p, hipStream_t stream) {
     const int programs = p.batch * p.kv_heads * p.m_tiles;
+    if constexpr (DP > 256 && FMT == FP32) {
+        return fail("decode: fp32 keys and values take head dims up to 256 (bf16, fp16 or fp8 ones up to 512)");
+    } else {
+    const int slices = DP > 256 ? (p.value_dim + 255) / 256 : 1;  // value slices of 256 channels
     if constexpr (DP == 128 && FMT == BF16 && QF == BF16) {
         if (p.code_bits == 2 && !p.mask) {
             hipLaunchKernelGGL((dense_split_kernel<DP, FMT, QF, false, 2>), dim3(programs, p.splits), dim3(64), 0,
@@ -780,10 +792,13 @@ int launch_dense(const DenseParams& p, hipStream_t stream) {
     }
     if (p.code_bits) return fail("decode: codes are read for bf16 cells of 128 channels without a mask only");
     if (p.mask)
-        hipLaunchKernelGGL((dense_split_kernel<DP, FMT, QF, true>), dim3(programs, p.splits), dim3(64), 0, stream, p);
+        hipLaunchKernelGGL((dense_split_kernel<DP, FMT, QF, true>), dim3(programs, p.splits, slices), dim3(64), 0,
+                           stream, p);
     else
-        hipLaunchKernelGGL((dense_split_kernel<DP, FMT, QF, false>), dim3(programs, p.splits), dim3(64), 0, stream, p);
+        hipLaunchKernelGGL((dense_split_kernel<DP, FMT, QF, false>), dim3(programs, p.splits, slices), dim3(64), 0,
+                           stream, p);
     return check_launch("dense_split_kernel");
+    }
 }
 
 template <int DP, int QF>
@@ -812,6 +827,7 @@ int dense_padded_dim(int head_dim, int value_dim) {
     if (d <= 64) return 64;
     if (d <= 128) return 128;
     if (d <= 256) return 256;
+    if (d <= 512) return 512;
     return 0;
 }
 
@@ -820,7 +836,8 @@ int dense_attention(const DenseParams& p, int padded_dim, hipStream_t stream) {
         case 64: return by_q_format<64>(p, stream);
         case 128: return by_q_format<128>(p, stream);
         case 256: return by_q_format<256>(p, stream);
-        default: return fail("decode: head dims above 256 are not supported");
+        case 512: return by_q_format<512>(p, stream);
+        default: return fail("decode: head dims above 512 are not supported");
     }
 }
 

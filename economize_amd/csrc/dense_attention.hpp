@@ -76,7 +76,7 @@ struct DenseParams {
     const int32_t* qp_done;
 };
 
-int dense_padded_dim(int head_dim, int value_dim);  // 64, 128 or 256; 0 when neither fits
+int dense_padded_dim(int head_dim, int value_dim);  // 64, 128, 256 or 512; 0 when none fits
 int dense_attention(const DenseParams& p, int padded_dim, hipStream_t stream);
 
 }  // namespace eco

@@ -135,10 +135,10 @@ __global__ __launch_bounds__(256) void fp8_encode_kernel(EncodeParams p) {
         const int b = static_cast<int>(row / (static_cast<int64_t>(p.tokens) * p.heads));
         const int64_t src = b * p.ss_b + h * p.ss_h + t * p.ss_t;
         uint8_t* dst = p.dst + b * p.sd_b + h * p.sd_h + t * p.sd_t;
-        float x[4];  // channels lane, lane + 64, .. (head dims up to 256)
+        float x[8];  // channels lane, lane + 64, .. (head dims up to 512)
         float amax = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 8; ++i) {
             const int d = lane + 64 * i;
             x[i] = d < p.head_dim ? load_elem(p.src, src + d, p.in_format) : 0.0f;
             amax = fmaxf(amax, fabsf(x[i]));
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void fp8_encode_kernel(EncodeParams p) {
         if (p.token_scale) {
             bool nan = false;  // torch's amax propagates NaN, and so does the scale then
 #pragma unroll
-            for (int i = 0; i < 4; ++i) nan |= x[i] != x[i];
+            for (int i = 0; i < 8; ++i) nan |= x[i] != x[i];
             for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
             scale = __ballot(nan) ? __builtin_nanf("") : fmaxf(__fdiv_rn(amax, fp8_max<FMT>()), 1e-12f);
             scaled = true;
@@ -158,7 +158,7 @@ __global__ __launch_bounds__(256) void fp8_encode_kernel(EncodeParams p) {
             scaled = true;
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 8; ++i) {
             const int d = lane + 64 * i;
             if (d < p.head_dim) dst[d] = encode<FMT>(x[i], scale, scaled);
         }

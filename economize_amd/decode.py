@@ -127,7 +127,7 @@ def decode_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor
         out = torch.empty(batch, queries, q_heads, head_dv, dtype=query.dtype, device=device)
     need = int(_lib.lib().eco_decode_workspace_size(batch, queries, q_heads, kv_heads, keys, head_dim, head_dv))
     if need == 0:
-        raise ConfigError(f"decode_attention supports head dims up to 256, got {head_dim} / {head_dv}")
+        raise ConfigError(f"decode_attention supports head dims up to 512, got {head_dim} / {head_dv}")
     ws = _workspace(need, device, batch, queries, q_heads, kv_heads)
     ks = None if k_scale is None else k_scale.float().contiguous()
     vs = None if v_scale is None else v_scale.float().contiguous()

@@ -123,7 +123,7 @@ def gathered_decode_attention(query: torch.Tensor, key: torch.Tensor, value: tor
     virtual = max(1, keys - gathered.dropped)
     need = int(_lib.lib().eco_decode_workspace_size(batch, queries, q_heads, kv_heads, virtual, head_dim, head_dv))
     if need == 0:
-        raise ConfigError(f"gathered_decode_attention supports head dims up to 256, got {head_dim} / {head_dv}")
+        raise ConfigError(f"gathered_decode_attention supports head dims up to 512, got {head_dim} / {head_dv}")
     ws = _workspace(need, device, batch, queries, q_heads, kv_heads)
     idx = gathered.index
     _lib.call(

@@ -386,7 +386,7 @@ def quest_decode_attention(query: torch.Tensor, key: torch.Tensor, value: torch.
     need = int(_lib.lib().eco_quest_decode_workspace_size(batch, queries, q_heads, kv_heads, keys, pages.pages,
                                                             pages.page, pages.min_done, head_dim, head_dv))
     if need == 0:
-        raise ConfigError(f"quest_decode_attention supports head dims up to 256, got {head_dim} / {head_dv}")
+        raise ConfigError(f"quest_decode_attention supports head dims up to 512, got {head_dim} / {head_dv}")
     ws = _workspace(need, device, batch, queries, q_heads, kv_heads)
     _lib.call(
         "eco_quest_decode", query.data_ptr(), _lib.fmt(query.dtype), query.stride(0), query.stride(1),

@@ -76,6 +76,18 @@ def _head_dims(technique: str, adapter, dims: tuple[int, ...]) -> None:
         raise ConfigError(f"{technique}: the MI355X kernels take head dims {list(dims)}, the model has {dim}")
 
 
+def _dense_head_dim(technique: str, adapter, kv_in_model_dtype: bool) -> None:
+    """Refuses head dims the dense decode kernel does not take: at most 512 channels (heads wider than 256 run as two
+    value slices, attention/decode.py:216-232), and at most 256 when the K/V buffers are fp32 (a model's own dtype on
+    an fp32 model)."""
+    dim = head_dim_of(adapter)
+    if dim is None:
+        return
+    limit = 256 if kv_in_model_dtype and model_dtype(adapter) == torch.float32 else 512
+    if dim > limit:
+        raise ConfigError(f"{technique}: the MI355X kernels take head dims up to {limit} here, the model has {dim}")
+
+
 def model_dtype(adapter) -> torch.dtype | None:
     """The dtype of a model's parameters, or ``None`` when ``adapter`` is no module."""
     parameters = getattr(adapter, "parameters", None)
@@ -208,13 +220,11 @@ class FusedFP8KVConfig(FP8KVConfig):
 
     def validate(self, adapter) -> None:
         """Refuses an attention implementation that does not read fp8 K/V (fused.py:39-49) and head dims beyond the
-        kernels' 256."""
+        dense kernel's 512 (its fp8 buffers)."""
         from .attention import accepts_fp8_kv
 
         super().validate(adapter)
-        dim = head_dim_of(adapter)
-        if dim is not None and dim > 256:
-            raise ConfigError(f"{self.technique}: the MI355X kernels take head dims up to 256, the model has {dim}")
+        _dense_head_dim(self.technique, adapter, kv_in_model_dtype=False)
         _needs_kernel(self.technique, attn_implementation(adapter), accepts_fp8_kv, "fp8 K/V", "kv_fp8")
 
 
@@ -258,15 +268,14 @@ class KIVIConfig(TechniqueConfig):
     def validate(self, adapter) -> None:
         """An explicit ``storage="packed"`` the paged KIVI cache cannot hold on this model is refused (the
         reference's explicit packed storage raises where it cannot run, kivi.py:62-66); otherwise a configuration
-        the paged cache cannot hold runs on the simulated storage, and the dense kernel takes head dims up to 256."""
+        the paged cache cannot hold runs on the simulated storage, whose buffers (the model's dtype) the dense kernel
+        reads at head dims up to 512 (256 on fp32 models)."""
         if self.storage == "packed":
             why = kivi_paged_refusal(self, adapter)
             if why is not None:
                 raise ConfigError(f"storage='packed' is the paged KIVI cache, which cannot hold {why}; use storage="
                                   "None or 'simulated'")
-        dim = head_dim_of(adapter)
-        if dim is not None and dim > 256:
-            raise ConfigError(f"{self.technique}: the MI355X kernels take head dims up to 256, the model has {dim}")
+        _dense_head_dim(self.technique, adapter, kv_in_model_dtype=True)
 
     def simulated(self, adapter) -> bool:
         """Whether this configuration's layers use the simulated storage on ``adapter``'s model."""
@@ -346,13 +355,14 @@ class QuestConfig(TechniqueConfig):
     def validate(self, adapter) -> None:
         """Refuses an attention implementation that does not read Quest pages (quest/technique.py:88-97) and head
         dims no Quest kernel takes: the paged kernels take bf16 models of head dim 64 / 128 / 256, the dense ones any
-        dtype and any head dim up to 256 that is a multiple of 8."""
+        dtype and any head dim that is a multiple of 8, up to 512 (256 on fp32 models)."""
         from .attention import accepts_packed_kv
 
         dim = head_dim_of(adapter)
-        if dim is not None and (dim % 8 or dim > 256):
-            raise ConfigError(f"{self.technique}: the MI355X kernels take head dims that are multiples of 8 up to 256, "
-                              f"the model has {dim}")
+        if dim is not None and dim % 8:
+            raise ConfigError(f"{self.technique}: the MI355X kernels take head dims that are multiples of 8, the model "
+                              f"has {dim}")
+        _dense_head_dim(self.technique, adapter, kv_in_model_dtype=True)
         _needs_kernel(self.technique, attn_implementation(adapter), lambda name: accepts_packed_kv(name, "quest"),
                       "its pages", None)
 

@@ -199,7 +199,8 @@ size_t eco_decode_workspace_size(int32_t batch, int32_t queries, int32_t q_heads
  * optional boolean mask (one byte per element, element mask[b * sm_b + h * sm_h + qi * sm_q + t * sm_s], stride 0
  * for a broadcast dimension) hides the keys where it is 0; without it every key is visible. Scores are
  * q . k * scale, with an optional soft cap (softcap > 0) and sinks [Hq] in the denominator; a query that sees no key
- * gives 0. Channel strides are 1; head_dim and value_dim are multiples of 8 (of 16 for fp8), at most 256; pointers
+ * gives 0. Channel strides are 1; head_dim and value_dim are multiples of 8 (of 16 for fp8), at most 512 (at most 256
+ * for fp32 K/V; heads wider than 256 run as value slices of 256 channels, attention/decode.py:216-232); pointers
  * and K/V/query strides are 16-byte aligned. Replaces decode_attention (attention/decode.py:252-324; kernels
  * attention/_decode_kernels.py:78-226): split-K over the keys, the splits merged by the last of their waves. */
 int eco_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int64_t sq_q, const void* k,

@@ -2,7 +2,7 @@
 decode_attention, attention/decode.py:252-324) with the fp32 definition (attention/decode.py:66-103, the oracle's
 reference_attention) on the GPU: bf16 / fp16 / fp32 queries and K/V, fp8 K/V views (with and without per-head
 scales), boolean masks broadcast over heads or per head, causal draft masks, rows that see nothing, sinks, soft caps,
-more than 16 query rows per KV head, head dims 64 / 96 / 128 / 256 and Dv != D, the HF query layout
+more than 16 query rows per KV head, head dims 64 / 96 / 128 / 256, heads wider than 256 (up to 512) and Dv != D, the HF query layout
 ([B, Q, Hq, D].transpose(1, 2)), key counts that are not multiples of the tile. Tolerance atol 2e-3 / rtol 1e-2."""
 
 from __future__ import annotations
@@ -73,6 +73,14 @@ CASES = [
     (2, 4, 2, 1, 300, 16, 16, torch.float32, torch.float8_e4m3fn, None, False),  # the golden model's head dim
     (2, 8, 2, 2, 333, 48, 48, torch.bfloat16, torch.bfloat16, "causal", False),
     (2, 12, 4, 1, 3000, 128, 128, torch.float32, torch.float8_e4m3fn, "holes", True),
+    # heads wider than 256: two value slices of 256 channels (or one, Dv <= 256)
+    (2, 8, 2, 1, 1000, 512, 512, torch.bfloat16, torch.bfloat16, None, False),
+    (2, 8, 4, 2, 700, 512, 512, torch.float16, torch.float16, "causal", False),
+    (1, 8, 1, 1, 2500, 512, 512, torch.float32, torch.float8_e4m3fn, "holes", True),
+    (2, 16, 4, 3, 333, 320, 320, torch.bfloat16, torch.float8_e5m2, "per_head", False),
+    (2, 8, 2, 1, 129, 384, 256, torch.bfloat16, torch.bfloat16, "empty_row", False),
+    (2, 4, 2, 1, 100, 264, 512, torch.float16, torch.float16, None, False),  # Dv above D
+    (1, 40, 2, 1, 5000, 512, 512, torch.bfloat16, torch.bfloat16, "window", False),  # 20 rows per KV head, splits
 ]
 
 
@@ -107,6 +115,18 @@ def test_softcap_and_sinks() -> None:
     np.testing.assert_allclose(got.float().cpu().numpy(), want, atol=ATOL, rtol=RTOL)
 
 
+def test_wide_heads_with_softcap_and_sinks() -> None:
+    from economize_amd.decode import decode_attention
+
+    q, k, v, kf, vf, mask, _, _ = _case(2, 8, 2, 2, 900, 512, 512, torch.bfloat16, torch.bfloat16, seed=5,
+                                        mask_kind="empty_row")
+    sinks = np.random.default_rng(6).standard_normal(8).astype(np.float32)
+    got = decode_attention(q.cuda(), k.cuda(), v.cuda(), torch.from_numpy(mask).cuda(), 0.05, softcap=4.0,
+                           sinks=torch.from_numpy(sinks).cuda())
+    want = reference_attention(q.float().numpy(), kf, vf, mask, 0.05, softcap=4.0, sinks=sinks)
+    np.testing.assert_allclose(got.float().cpu().numpy(), want, atol=ATOL, rtol=RTOL)
+
+
 def test_refusals() -> None:
     from economize_amd.decode import decode_attention
     from economize_amd.errors import ConfigError
@@ -121,6 +141,13 @@ def test_refusals() -> None:
         decode_attention(q[:, :4], k, k, torch.ones(1, 1, 1, 10, device="cuda"), 1.0)
     with pytest.raises(ConfigError, match="keys"):
         decode_attention(q[:, :4], k, k, torch.ones(1, 1, 1, 11, dtype=torch.bool, device="cuda"), 1.0)
+    wide = torch.zeros(1, 4, 1, 512, dtype=torch.float32, device="cuda")
+    with pytest.raises(ConfigError, match="256 for fp32"):  # fp32 K/V: heads up to 256
+        decode_attention(wide, wide, wide, None, 1.0)
+    with pytest.raises(ConfigError, match="up to 512"):
+        decode_attention(torch.zeros(1, 4, 1, 528, dtype=torch.bfloat16, device="cuda"),
+                         torch.zeros(1, 4, 1, 528, dtype=torch.bfloat16, device="cuda"),
+                         torch.zeros(1, 4, 1, 528, dtype=torch.bfloat16, device="cuda"), None, 1.0)
 
 
 def sweep_case(i: int):

@@ -31,7 +31,7 @@ def codes_of(buffer: torch.Tensor) -> np.ndarray:
 
 @pytest.mark.parametrize("dtype", list(FORMATS))
 @pytest.mark.parametrize("in_dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("head_dim", [16, 100, 128, 256])
+@pytest.mark.parametrize("head_dim", [16, 100, 128, 256, 456, 512])
 def test_unscaled_and_per_head_codes_match_the_oracle(dtype, in_dtype, head_dim) -> None:
     from economize_amd.fp8 import fp8_encode
 
@@ -48,7 +48,7 @@ def test_unscaled_and_per_head_codes_match_the_oracle(dtype, in_dtype, head_dim)
 
 
 @pytest.mark.parametrize("dtype", list(FORMATS))
-@pytest.mark.parametrize("head_dim", [16, 64, 200])
+@pytest.mark.parametrize("head_dim", [16, 64, 200, 512])
 def test_per_token_scales_and_codes_match_the_oracle(dtype, head_dim) -> None:
     """token_scale's rule (absmax / format max, at least 1e-12) written beside the codes, for finite rows, an
     all-zero row and rows of huge values."""

@@ -92,6 +92,8 @@ CASES = [
     (2, 8, 2, 3, 640, 64, 64, torch.bfloat16, torch.bfloat16, 16, 6, [39, 30], "causal", None, False),
     (1, 32, 8, 1, 4096, 128, 128, torch.float16, torch.float16, 16, 63, [256], None, None, False),
     (2, 4, 1, 1, 129, 48, 48, torch.float32, torch.float8_e5m2, 32, 1, [4, 3], None, None, False),
+    (2, 8, 2, 1, 800, 512, 512, torch.bfloat16, torch.bfloat16, 16, 9, [48, 30], "holes", None, True),  # wide heads
+    (2, 8, 4, 2, 300, 320, 320, torch.float16, torch.float16, 32, 3, [9, 7], None, None, False),
 ]
 
 

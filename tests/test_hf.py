@@ -46,8 +46,9 @@ def test_validate_refuses_what_the_path_cannot_run() -> None:
     QuestConfig().validate(model.config)
     for scale in ("none", "token", "tensor", "head"):
         FP8KVConfig(scale=scale).validate(tiny_model(head_dim=32))  # dense fp8 buffers take any head dim
-    with pytest.raises(ConfigError, match="up to 256"):
-        FusedFP8KVConfig().validate(tiny_model(head_dim=512, attn="economize"))
+    FusedFP8KVConfig().validate(tiny_model(head_dim=512, attn="economize"))  # fp8 buffers: up to 512
+    with pytest.raises(ConfigError, match="up to 512"):
+        FusedFP8KVConfig().validate(tiny_model(head_dim=640, attn="economize"))
     for config in (KIVIConfig(bits=8), KIVIConfig(group_size=64, residual_length=128), KIVIConfig(storage="simulated"),
                    KIVIConfig(bits=4, group_size=4, residual_length=8)):
         config.validate(model)  # the simulated storage takes what the paged cache cannot hold
@@ -55,8 +56,11 @@ def test_validate_refuses_what_the_path_cannot_run() -> None:
         KIVIConfig(bits=8, storage="packed").validate(model)
     with pytest.raises(ConfigError, match="group_size=64"):
         KIVIConfig(group_size=64, residual_length=128, storage="packed").validate(model)
-    with pytest.raises(ConfigError, match="up to 256"):
+    with pytest.raises(ConfigError, match="up to 256"):  # simulated buffers in the model's fp32
         FusedKIVIConfig().validate(tiny_model(head_dim=512, attn="economize"))
+    FusedKIVIConfig().validate(tiny_model(head_dim=512, attn="economize").to(torch.bfloat16))
+    with pytest.raises(ConfigError, match="up to 512"):
+        FusedKIVIConfig().validate(tiny_model(head_dim=640, attn="economize").to(torch.bfloat16))
     with pytest.raises(IncompatibleTechniquesError, match="economize"):
         FusedFP8KVConfig().validate(tiny_model())  # the model runs sdpa
 
@@ -151,8 +155,11 @@ def test_quest_layers_are_paged_where_the_paged_kernels_take_the_model() -> None
     assert layer_types(tiny_model().to(torch.float16)) == ["DynamicLayer", "DenseQuestLayer"]
     assert layer_types(tiny_model()) == ["DynamicLayer", "DenseQuestLayer"]  # float32
     assert layer_types(tiny_model(head_dim=32).to(torch.bfloat16)) == ["DynamicLayer", "DenseQuestLayer"]
-    with pytest.raises(ConfigError, match="multiples of 8 up to 256"):
+    assert layer_types(tiny_model(head_dim=512).to(torch.bfloat16)) == ["DynamicLayer", "DenseQuestLayer"]
+    with pytest.raises(ConfigError, match="up to 256"):  # dense buffers in the model's fp32
         apply(tiny_model(head_dim=512), QuestConfig())
+    with pytest.raises(ConfigError, match="multiples of 8"):
+        apply(tiny_model(head_dim=36), QuestConfig())
     assert PagedLayer and DenseQuestLayer
 
 
