@@ -36,11 +36,11 @@ pytestmark = pytest.mark.gpu
 PROMPT, STEPS = 70, 40
 
 
-def tiny_model(attn: str, dtype: torch.dtype = torch.bfloat16):
+def tiny_model(attn: str, dtype: torch.dtype = torch.bfloat16, head_dim: int = 64):
     from transformers import Qwen2Config, Qwen2ForCausalLM
 
     config = Qwen2Config(vocab_size=128, hidden_size=128, intermediate_size=256, num_hidden_layers=4,
-                         num_attention_heads=4, num_key_value_heads=2, head_dim=64, max_position_embeddings=512,
+                         num_attention_heads=4, num_key_value_heads=2, head_dim=head_dim, max_position_embeddings=512,
                          tie_word_embeddings=True, initializer_range=0.2, attn_implementation=attn)
     torch.manual_seed(0)
     model = Qwen2ForCausalLM(config).to(dtype).cuda().eval()
@@ -146,13 +146,16 @@ class Mirror(CacheLayerMixin):
         return -1
 
     def update(self, key_states, value_states, *args, **kwargs):
-        from economize_amd.hf import DenseQuestLayer
+        from economize_amd.hf import DenseFP8Layer, DenseQuestLayer, SimulatedKIVILayer
         from economize_amd.packed import materialized_kv
 
         if isinstance(self.source, DynamicLayer):
             return self.source.keys, self.source.values
-        if isinstance(self.source, DenseQuestLayer):
+        if isinstance(self.source, (DenseQuestLayer, SimulatedKIVILayer)):
             keys, values = (b[:, :, : self.source.length] for b in self.source.buffers)
+        elif isinstance(self.source, DenseFP8Layer):  # the codes decoded to the model's dtype
+            keys, values = (self.source._decoded(c[:, :, : self.source.length], i)
+                            for i, c in enumerate(self.source.codes))
         else:
             keys, values = materialized_kv(*self.source.transform_read(key_states, value_states))
             if getattr(self.source, "quest", None) is not None:
@@ -163,7 +166,7 @@ class Mirror(CacheLayerMixin):
         return keys, values
 
 
-def mirrored_decode(configs, attn: str, dtype: torch.dtype = torch.bfloat16
+def mirrored_decode(configs, attn: str, dtype: torch.dtype = torch.bfloat16, head_dim: int = 64
                     ) -> tuple[list[float], list[float], set, int]:
     """Greedy decoding on the economize caches; after every pass the mirror model runs the same tokens over the
     caches' dense view. Every Quest selection of the economize pass is checked against the oracle's select_pages on
@@ -174,10 +177,10 @@ def mirrored_decode(configs, attn: str, dtype: torch.dtype = torch.bfloat16
     from economize_amd.hf import DenseQuestLayer, apply
     from economize_amd.quest import QuestPages
 
-    model = tiny_model("sdpa", dtype)
+    model = tiny_model("sdpa", dtype, head_dim)
     em = apply(model, *configs)
     cache = em.make_cache(PROMPT + STEPS + 1)
-    mirror_model = tiny_model(attn, dtype)
+    mirror_model = tiny_model(attn, dtype, head_dim)
     layers = [Mirror(layer) for layer in cache.layers]
     mirror = Cache(layers=layers)
     selections = []
@@ -283,14 +286,19 @@ def test_kivi_first_layer_holds_the_fake_quantization(bits: int) -> None:
 LOGIT_TOL = 0.5
 
 
-@pytest.mark.parametrize("technique", ["fp8", "kivi2", "kivi4", "quest", "quest_fp16", "quest_fp32"])
+@pytest.mark.parametrize("technique", ["fp8", "kivi2", "kivi4", "quest", "quest_fp16", "quest_fp32", "fp8_d512",
+                                       "kivi2_d512", "quest_d512"])
 def test_decoding_logits_match_sdpa_over_the_cache(technique: str) -> None:
+    """Heads of 512 channels (``_d512``) run on the dense kernel's two value slices: dense fp8 buffers, KIVI's
+    simulated storage and Quest over dense buffers."""
     from transformers import AttentionInterface
     from transformers.masking_utils import AttentionMaskInterface
 
     from economize_amd.techniques import FusedFP8KVConfig, FusedKIVIConfig, QuestConfig
 
     attn, path, dtype = "sdpa", "kernel_fp8", torch.bfloat16
+    head_dim = 512 if technique.endswith("_d512") else 64
+    technique = technique.removesuffix("_d512")
     if technique == "quest_fp16":
         dtype = torch.float16
     elif technique == "quest_fp32":
@@ -305,8 +313,10 @@ def test_decoding_logits_match_sdpa_over_the_cache(technique: str) -> None:
         attn, path = "quest_oracle", "kernel_quest"
         AttentionInterface.register("quest_oracle", quest_oracle_forward)
         AttentionMaskInterface.register("quest_oracle", AttentionMaskInterface._global_mapping["sdpa"])
-    deltas, gaps, paths, checked = mirrored_decode(configs, attn, dtype)
-    print(technique, "max delta", max(deltas), "deltas", [round(d, 4) for d in deltas])
+    if head_dim == 512 and not technique.startswith("quest"):
+        path = "kernel"  # dense fp8 buffers / KIVI's simulated storage
+    deltas, gaps, paths, checked = mirrored_decode(configs, attn, dtype, head_dim)
+    print(technique, head_dim, "max delta", max(deltas), "deltas", [round(d, 4) for d in deltas])
     assert (path, 1) in paths and ("sdpa", PROMPT) in paths
     if technique.startswith("quest"):  # (fp16 / fp32 models keep dense buffers: the dense kernel's page list)
         assert ("kernel", 1) in paths  # the dense first layer: the dense kernel
