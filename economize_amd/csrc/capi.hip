@@ -546,7 +546,7 @@ extern "C" {
 
 const char* eco_last_error(void) { return g_error.c_str(); }
 
-int eco_abi_version(void) { return 5; }
+int eco_abi_version(void) { return 6; }
 
 int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
                      int64_t sv_t, int64_t sv_h, const int32_t* slot_mapping, int32_t tokens, void* k_cache,
@@ -971,14 +971,14 @@ int eco_kivi_cells_quantize(void* cache, int32_t format, int64_t sb, int64_t sh,
                             int32_t page_size, int32_t kv_heads, const int32_t* block_table, int64_t bt_stride,
                             int32_t bt_cols, const int32_t* query_start_loc, const int32_t* seq_lens,
                             const int32_t* prefilling, int32_t requests, int32_t head_dim, int32_t bits,
-                            int32_t group, int32_t residual, void* stream) {
+                            int32_t group, int32_t residual, int32_t* plan, void* stream) {
     CellsParams p;
     if (int rc = cells_params(cache, format, sb, sh, sn, num_pages, page_size, kv_heads, head_dim, bits, group, &p))
         return rc;
     if (requests < 0) return fail("kivi cells quantize: negative request count");
     if (requests == 0) return 0;
-    if (!block_table || !query_start_loc || !seq_lens || !prefilling)
-        return fail("kivi cells quantize: null block table, query offsets, lengths or prefill flags");
+    if (!block_table || !query_start_loc || !seq_lens || !prefilling || !plan)
+        return fail("kivi cells quantize: null block table, query offsets, lengths, prefill flags or plan");
     if (bt_cols <= 0 || bt_stride < bt_cols) return fail("kivi cells quantize: bad block table");
     if (residual < group || residual % group) return fail("kivi cells quantize: the residual must be whole groups");
     p.block_table = block_table;
@@ -989,7 +989,7 @@ int eco_kivi_cells_quantize(void* cache, int32_t format, int64_t sb, int64_t sh,
     p.prefilling = prefilling;
     p.requests = requests;
     p.residual = residual;
-    return kivi_cells_quantize(p, static_cast<hipStream_t>(stream));
+    return kivi_cells_quantize(p, plan, static_cast<hipStream_t>(stream));
 }
 
 size_t eco_kivi_cells_attention_workspace_size(int32_t requests, int32_t max_query_len, int32_t q_heads,

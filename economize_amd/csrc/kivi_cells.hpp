@@ -28,7 +28,8 @@ struct CellsParams {
     CellLayout L;
 };
 
-int kivi_cells_quantize(const CellsParams& p, hipStream_t stream);
+// plan: device scratch of 4 int32 per (request, KV head)
+int kivi_cells_quantize(const CellsParams& p, int32_t* plan, hipStream_t stream);
 int kivi_cells_clear_flags(const CellsParams& p, const int32_t* slots, int tokens, hipStream_t stream);
 
 }  // namespace eco

@@ -127,9 +127,11 @@ def quantize_committed(kv_cache: torch.Tensor, layout: CellLayout, residual_leng
     if args[6] % layout.group_size:
         raise ConfigError(f"KIVI needs pages of whole key groups: {args[6]} tokens per page, groups of "
                           f"{layout.group_size}")
+    # the walk's stopping points per (request, KV head), found before any cell changes
+    plan = torch.empty(4 * requests * args[7], dtype=torch.int32, device=device)
     _lib.call("eco_kivi_cells_quantize", *args, block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
               query_start_loc.data_ptr(), seq_lens.data_ptr(), prefilling.data_ptr(), requests, layout.head_size,
-              layout.bits, layout.group_size, residual_length, _lib.stream_of(device))
+              layout.bits, layout.group_size, residual_length, plan.data_ptr(), _lib.stream_of(device))
 
 
 def clear_flags(kv_cache: torch.Tensor, slot_mapping: torch.Tensor, layout: CellLayout) -> None:

@@ -337,12 +337,14 @@ int eco_kivi_cells_layout(int32_t head_dim, int32_t element_size, int32_t bits, 
  * request not prefilling with a non-empty query (query_start_loc [requests + 1]) and c = seq_lens[b] - its query
  * length > 0, keys in whole groups below (c / residual) * residual and values below c - residual, newest first, until
  * a cell already quantized; cells laid out as write_cells does (layout.py:222-256): dense entries replaced by the
- * dequantized values, codes, fp16 scales and zero points, flags 1 (2: a scale or zero point beyond fp16). */
+ * dequantized values, codes, fp16 scales and zero points, flags 1 (2: a scale or zero point beyond fp16). plan: device
+ * scratch of 4 int32 per (request, KV head), any contents (the walk's stopping points, found over the flags before
+ * any cell changes; the groups and tokens are then quantized by many workgroups per request and head). */
 int eco_kivi_cells_quantize(void* cache, int32_t format, int64_t sb, int64_t sh, int64_t sn, int32_t num_pages,
                             int32_t page_size, int32_t kv_heads, const int32_t* block_table, int64_t bt_stride,
                             int32_t bt_cols, const int32_t* query_start_loc, const int32_t* seq_lens,
                             const int32_t* prefilling, int32_t requests, int32_t head_dim, int32_t bits,
-                            int32_t group, int32_t residual, void* stream);
+                            int32_t group, int32_t residual, int32_t* plan, void* stream);
 
 /* The reference's paged_kivi_attention (backends/vllm/kivi/kernels.py:216-415) over the cells of one layer's cache
  * [pages, kv_heads, page_size] (byte strides sb, sh, sn; entries and queries of format bf16 / fp16 / fp32): vLLM's
