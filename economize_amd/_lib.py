@@ -85,6 +85,12 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
                                    _P, _L, _L, _I, _P, _I, _I,  # index, pages, done, page size, min_done
                                    _P, _L, _L, _L, _L, _P, _P, _L, _L, _L,  # mask, sinks, out
                                    _I, _I, _I, _I, _I, _I, _I, _F, _F, _P, _S, _P]),
+    "eco_kivi_packed_decode": (c_int32, [_P, _I, _L, _L, _L, _P, _P, _L, _L, _L, _L, _L, _L, _I,  # q .. ring
+                                         _P, _L, _L, _L, _P, _P, _L, _L, _L,  # key codes, scales, zero points
+                                         _P, _L, _L, _L, _P, _P, _L, _L, _L,  # value codes, scales, zero points
+                                         _P, _P, _I, _I, _I,  # counts, bits, groups
+                                         _P, _L, _L, _L, _L, _P, _P, _L, _L, _L,  # mask, sinks, out
+                                         _I, _I, _I, _I, _I, _I, _I, _F, _F, _P, _S, _P]),
 }
 
 _lib: ctypes.CDLL | None = None

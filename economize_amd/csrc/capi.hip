@@ -355,13 +355,31 @@ struct QuestListArgs {
     const int32_t* done;
 };
 
+// The codes of a KIVI packed call (the reference's KIVIPacked record, attention/kivi.py:80-132).
+struct KiviPackedArgs {
+    const uint8_t* kc;
+    int64_t skc_b, skc_h, skc_s;
+    const uint16_t* ks;
+    const uint16_t* kz;
+    int64_t sks_b, sks_h, sks_g;
+    const uint8_t* vc;
+    int64_t svc_b, svc_h, svc_s;
+    const uint16_t* vs;
+    const uint16_t* vz;
+    int64_t svs_b, svs_h, svs_s;
+    const int32_t* kq;
+    const int32_t* vq;
+    int bits, key_group, value_group, ring;
+};
+
 int dense_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int64_t sq_q, const void* k,
                const void* v, int32_t kv_format, int64_t sk_b, int64_t sk_h, int64_t sk_s, int64_t sv_b, int64_t sv_h,
                int64_t sv_s, const float* k_scale, const float* v_scale, const uint8_t* mask, int64_t sm_b,
                int64_t sm_h, int64_t sm_q, int64_t sm_s, const float* sinks, void* out, int64_t so_b, int64_t so_q,
                int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads, int32_t kv_heads, int32_t keys,
                int32_t head_dim, int32_t value_dim, float scale, float softcap, void* workspace,
-               size_t workspace_bytes, void* stream, const GatheredArgs* g, const QuestListArgs* ql = nullptr) {
+               size_t workspace_bytes, void* stream, const GatheredArgs* g, const QuestListArgs* ql = nullptr,
+               const KiviPackedArgs* kp = nullptr) {
     if (!q || !k || !v || !out) return fail("decode: null query, key, value or output pointer");
     if (batch <= 0 || queries <= 0 || q_heads <= 0 || kv_heads <= 0 || keys < 0)
         return fail("decode: batch, queries and heads must be positive, keys non-negative");
@@ -462,6 +480,33 @@ int dense_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, in
         p.qp_shift = ql->shift;
         p.qp_done = ql->done;
     }
+    if (kp) {
+        p.kp_kc = kp->kc;
+        p.skc_b = kp->skc_b;
+        p.skc_h = kp->skc_h;
+        p.skc_s = kp->skc_s;
+        p.kp_ks = kp->ks;
+        p.kp_kz = kp->kz;
+        p.sks_b = kp->sks_b;
+        p.sks_h = kp->sks_h;
+        p.sks_g = kp->sks_g;
+        p.kp_vc = kp->vc;
+        p.svc_b = kp->svc_b;
+        p.svc_h = kp->svc_h;
+        p.svc_s = kp->svc_s;
+        p.kp_vs = kp->vs;
+        p.kp_vz = kp->vz;
+        p.svs_b = kp->svs_b;
+        p.svs_h = kp->svs_h;
+        p.svs_s = kp->svs_s;
+        p.kp_kq = kp->kq;
+        p.kp_vq = kp->vq;
+        p.kp_bits = kp->bits;
+        p.kp_kg = kp->key_group;
+        p.kp_vg = kp->value_group;
+        p.kp_ring = kp->ring;
+        return kivi_packed_attention(p, d.padded_dim, static_cast<hipStream_t>(stream));
+    }
     return dense_attention(p, d.padded_dim, static_cast<hipStream_t>(stream));
 }
 
@@ -546,7 +591,7 @@ extern "C" {
 
 const char* eco_last_error(void) { return g_error.c_str(); }
 
-int eco_abi_version(void) { return 6; }
+int eco_abi_version(void) { return 7; }
 
 int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
                      int64_t sv_t, int64_t sv_h, const int32_t* slot_mapping, int32_t tokens, void* k_cache,
@@ -1375,6 +1420,51 @@ size_t eco_quest_decode_workspace_size(int32_t batch, int32_t queries, int32_t q
     if (virt > INT32_MAX) return 0;
     return eco_decode_workspace_size(batch, queries, q_heads, kv_heads, static_cast<int32_t>(virt), head_dim,
                                      value_dim);
+}
+
+int eco_kivi_packed_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int64_t sq_q, const void* k,
+                           const void* v, int64_t sk_b, int64_t sk_h, int64_t sk_s, int64_t sv_b, int64_t sv_h,
+                           int64_t sv_s, int32_t ring, const uint8_t* key_codes, int64_t skc_b, int64_t skc_h,
+                           int64_t skc_s, const void* key_scale, const void* key_zero, int64_t sks_b, int64_t sks_h,
+                           int64_t sks_g, const uint8_t* value_codes, int64_t svc_b, int64_t svc_h, int64_t svc_s,
+                           const void* value_scale, const void* value_zero, int64_t svs_b, int64_t svs_h,
+                           int64_t svs_s, const int32_t* keys_quantized, const int32_t* values_quantized,
+                           int32_t bits, int32_t key_group, int32_t value_group, const uint8_t* mask, int64_t sm_b,
+                           int64_t sm_h, int64_t sm_q, int64_t sm_s, const float* sinks, void* out, int64_t so_b,
+                           int64_t so_q, int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads,
+                           int32_t kv_heads, int32_t keys, int32_t head_dim, int32_t value_dim, float scale,
+                           float softcap, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!key_codes || !key_scale || !key_zero || !value_codes || !value_scale || !value_zero)
+        return fail("kivi decode: null codes, scales or zero points");
+    if (!keys_quantized || !values_quantized) return fail("kivi decode: null quantized counts");
+    if (bits != 2 && bits != 4 && bits != 8) return fail("kivi decode: bits must be 2, 4 or 8");
+    if (keys <= 0) return fail("kivi decode: need keys > 0");
+    if (ring < 0) return fail("kivi decode: ring must be non-negative");
+    if (key_group <= 0 || value_group <= 0 || value_dim <= 0 || value_dim % value_group)
+        return fail("kivi decode: the value group must divide the value head dim (groups positive)");
+    if (q_format != BF16 && q_format != FP16 && q_format != FP32)
+        return fail("kivi decode: queries must be bf16, fp16 or fp32");
+    const int ce = 16 / element_bytes(q_format);  // elements per 16-byte chunk of the kernel
+    const int nb = ce * bits / 8;                  // code bytes of a chunk
+    auto aligned_to = [](const void* ptr, int bytes) { return (reinterpret_cast<uintptr_t>(ptr) % bytes) == 0; };
+    if (!aligned_to(key_codes, nb) || !aligned_to(value_codes, nb))
+        return fail("kivi decode: codes must be aligned to " + std::to_string(nb) + " bytes");
+    for (int64_t st : {skc_b, skc_h, skc_s, svc_b, svc_h, svc_s})
+        if (st % nb) return fail("kivi decode: code strides must be multiples of " + std::to_string(nb) + " bytes");
+    if (!aligned_to(key_scale, 2 * ce) || !aligned_to(key_zero, 2 * ce))
+        return fail("kivi decode: key scales and zero points must be aligned to " + std::to_string(2 * ce) + " bytes");
+    for (int64_t st : {sks_b, sks_h, sks_g})
+        if (st % ce) return fail("kivi decode: key scale strides must be multiples of " + std::to_string(ce) + " elements");
+    if (!aligned_to(value_scale, 2) || !aligned_to(value_zero, 2))
+        return fail("kivi decode: value scales and zero points must be fp16-aligned");
+    const KiviPackedArgs kp{key_codes, skc_b, skc_h, skc_s, static_cast<const uint16_t*>(key_scale),
+                            static_cast<const uint16_t*>(key_zero), sks_b, sks_h, sks_g, value_codes, svc_b, svc_h,
+                            svc_s, static_cast<const uint16_t*>(value_scale), static_cast<const uint16_t*>(value_zero),
+                            svs_b, svs_h, svs_s, keys_quantized, values_quantized, bits, key_group, value_group, ring};
+    return dense_decode(q, q_format, sq_b, sq_h, sq_q, k, v, q_format, sk_b, sk_h, sk_s, sv_b, sv_h, sv_s, nullptr,
+                        nullptr, mask, sm_b, sm_h, sm_q, sm_s, sinks, out, so_b, so_q, so_h, batch, queries, q_heads,
+                        kv_heads, keys, head_dim, value_dim, scale, softcap, workspace, workspace_bytes, stream,
+                        nullptr, nullptr, &kp);
 }
 
 size_t eco_quest_select_workspace_size(int32_t batch, int32_t kv_heads, int32_t max_done) {

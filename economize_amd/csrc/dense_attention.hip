@@ -1,775 +1,11 @@
-// Dense decode attention on CDNA4 matrix cores (gfx950): the reference's decode_attention (attention/decode.py:
-// 252-324 and its kernels, attention/_decode_kernels.py:78-226) over K/V buffers [B, Hkv, S, D] / [B, Hkv, S, Dv]
-// with any element strides, a boolean mask [B, 1 or Hq, Q or 1, S] (broadcast strides allowed), a soft cap and
-// attention sinks. It is what the economize attention function runs for a model cache that keeps dense buffers
-// (the fused fp8 cache's fp8 views, bf16 / fp16 / fp32 caches); the paged kernels serve the paged caches.
-//
-// Definition (attention/decode.py:66-103): out[b, qi, h] = softmax_t(q . k_t * scale, masked) v_t, query head h
-// reading KV head h / G, zeros for a query that sees no key, fp32 accumulation. Every product runs on the bf16 MFMA:
-// a bf16 or fp8 element is one bf16 operand (exact), an fp16 or fp32 element two (hi = bf16(x), lo = bf16(x - hi);
-// exact for fp16, 16 significant bits for fp32), and a product of two-term operands sums hi.hi + hi.lo + lo.hi
-// (the lo.lo term is below fp32 rounding of the sum). The softmax weights p are split the same way for P.V.
-//
-// Work split (flash-decoding, as the reference): the key axis is cut into S splits; one wave takes one (row, KV
-// head, block of 16 query rows, split s) and walks the tiles of 32 keys s, s + S, s + 2 S, ... (the block's waves
-// read adjacent runs together), the next tile's loads in flight while a tile is computed (two register buffers
-// where they fit). The splits of a block combine by
-// log-sum-exp in the last of its waves to finish (an agent-scope counter per block in the workspace, left zero by
-// every call), one launch per call; a single split writes its rows directly. Per tile, S^T = K Q^T with v_mfma_f32_16x16x32_bf16: A-row m of MFMA block v is key
-// 8 (m / 4) + 4 v + m % 4, so that lane (n, g) ends with keys 8 g .. 8 g + 7 of query row n, which is exactly the B
-// operand of O^T += V^T P^T; the keys are read token-major from HBM straight into the A operand (16-byte loads).
-// V^T needs a lane to hold 8 keys of one channel: the tile's values are staged through LDS (coalesced 16-byte loads,
-// rows padded by 16 bytes so that the four lane groups' reads fall in different banks) and read back transposed.
+// The launches of the dense decode-attention kernel (dense_kernel.hpp): the instance for the head dim, the query
+// and K/V formats and the mask, in one launch per call.
 
-#include <type_traits>
-
-#include "common.hpp"
-#include "dense_attention.hpp"
+#include "dense_kernel.hpp"
 
 namespace eco {
 
 namespace {
-
-constexpr int TK = 32;  // keys per tile
-
-template <int FMT>
-constexpr int elem_bytes() {
-    return FMT == FP32 ? 4 : (FMT == BF16 || FMT == FP16 ? 2 : 1);
-}
-
-template <int FMT>
-constexpr bool two_terms() {
-    return FMT == FP16 || FMT == FP32;
-}
-
-// Eight consecutive elements of format FMT held in w (16 bytes per word; fp32: two words; fp8: w[0].x, w[0].y), as
-// bf16 hi (+ lo for two-term formats).
-template <int FMT>
-__device__ __forceinline__ void cvt8(const uint4 (&w)[FMT == FP32 ? 2 : 1], bf16x8& hi, bf16x8& lo) {
-    if constexpr (FMT == BF16) {
-        hi = __builtin_bit_cast(bf16x8, w[0]);
-    } else if constexpr (FMT == FP16) {
-        const f16x8 x = __builtin_bit_cast(f16x8, w[0]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float f = static_cast<float>(x[i]);
-            hi[i] = static_cast<__bf16>(f);
-            lo[i] = static_cast<__bf16>(f - static_cast<float>(hi[i]));
-        }
-    } else if constexpr (FMT == FP32) {
-        const float f[8] = {bits_f32(w[0].x), bits_f32(w[0].y), bits_f32(w[0].z), bits_f32(w[0].w),
-                            bits_f32(w[1].x), bits_f32(w[1].y), bits_f32(w[1].z), bits_f32(w[1].w)};
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            hi[i] = static_cast<__bf16>(f[i]);
-            lo[i] = static_cast<__bf16>(f[i] - static_cast<float>(hi[i]));
-        }
-    } else {
-        uint4 r;
-        if constexpr (FMT == FP8_E4M3) {
-            r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0].x, 1.0f, false));
-            r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0].x, 1.0f, true));
-            r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0].y, 1.0f, false));
-            r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w[0].y, 1.0f, true));
-        } else {
-            r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w[0].x, 1.0f, false));
-            r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w[0].x, 1.0f, true));
-            r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w[0].y, 1.0f, false));
-            r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w[0].y, 1.0f, true));
-        }
-        hi = __builtin_bit_cast(bf16x8, r);
-    }
-}
-
-// The raw words of eight consecutive elements of format FMT at p (16-byte aligned; fp8: 8-byte aligned). The
-// 16-byte loads are streamed (stream_load16: bf16 dense decode at B=32 L=4096 112 -> 103 us); fp8's 8-byte loads stay
-// plain (streamed, the fp8 views took 78.6 us against 67.2).
-template <int FMT>
-__device__ __forceinline__ void load8(const uint8_t* p, uint4 (&w)[FMT == FP32 ? 2 : 1]) {
-    if constexpr (FMT == FP8_E4M3 || FMT == FP8_E5M2) {
-        const uint2 x = *reinterpret_cast<const uint2*>(p);
-        w[0] = make_uint4(x.x, x.y, 0, 0);
-    } else {
-#pragma unroll
-        for (int i = 0; i < (FMT == FP32 ? 2 : 1); ++i) w[i] = stream_load16(p + 16 * i);
-    }
-}
-
-// One element of format FMT as fp32 (exact).
-template <int FMT>
-__device__ __forceinline__ float elem_f32(const uint8_t* p) {
-    if constexpr (FMT == BF16) return bf16_to_f32(*reinterpret_cast<const uint16_t*>(p));
-    if constexpr (FMT == FP16) return static_cast<float>(*reinterpret_cast<const _Float16*>(p));
-    if constexpr (FMT == FP32) return *reinterpret_cast<const float*>(p);
-    typedef float f32x2 __attribute__((ext_vector_type(2)));
-    const uint32_t w = *p;
-    f32x2 r;
-    if constexpr (FMT == FP8_E4M3)
-        r = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(w, 1.0f, false);
-    else
-        r = __builtin_amdgcn_cvt_scalef32_pk_f32_bf8(w, 1.0f, false);
-    return r.x;
-}
-
-__device__ __forceinline__ void split8(const float (&x)[8], bf16x8& hi, bf16x8& lo) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        hi[i] = static_cast<__bf16>(x[i]);
-        lo[i] = static_cast<__bf16>(x[i] - static_cast<float>(hi[i]));
-    }
-}
-
-__device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-template <int QF>
-__device__ __forceinline__ void load_query8(const DenseParams& p, int64_t offset, bf16x8& hi, bf16x8& lo) {
-    uint4 w[QF == FP32 ? 2 : 1];
-    load8<QF>(static_cast<const uint8_t*>(p.q) + offset * elem_bytes<QF>(), w);
-    cvt8<QF>(w, hi, lo);
-}
-
-template <int QF>
-__device__ __forceinline__ void store_out(const DenseParams& p, int64_t offset, float x) {
-    if constexpr (QF == BF16)
-        static_cast<uint16_t*>(p.out)[offset] = f32_to_bf16(x);
-    else if constexpr (QF == FP16)
-        static_cast<_Float16*>(p.out)[offset] = static_cast<_Float16>(x);
-    else
-        static_cast<float*>(p.out)[offset] = x;
-}
-
-// The output weight of a row whose keys gave maximum m and sum l (log2 units) with the sink logit (-inf: none): the
-// accumulators times 2^(m - M), divided by l 2^(m - M) + 2^(sink - M), M = max(m, sink) (decode.py's merge,
-// attention/_decode_kernels.py:183-226); 0 where nothing is visible. Returns 2^(m - M) and sets inv = 1 / that sum.
-__device__ inline float sink_weight(float m, float l, float sink, float& inv) {
-    const float big = fmaxf(m, sink);
-    float total = 0.0f, a = 0.0f;
-    if (big != -INFINITY) {
-        if (m != -INFINITY) {
-            a = __builtin_amdgcn_exp2f(m - big);
-            total = l * a;
-        }
-        if (sink != -INFINITY) total += __builtin_amdgcn_exp2f(sink - big);
-    }
-    inv = total > 0.0f ? 1.0f / total : 0.0f;
-    return a;
-}
-
-// Eight codes of channels c .. c + 7 packed along bytes (channel c + i at bit i BITS of x), as exact floats. The
-// codes are spread one per byte (even channels in lo, odd ones in hi); a code below 16 in a byte is the e4m3 pattern
-// of code 2^-9, which v_cvt_scalef32_pk_f32_fp8 with scale 2^9 turns into the exact float, two bytes at a time.
-template <int BITS>
-__device__ __forceinline__ void cell_codes8(uint32_t x, float (&c)[8]) {
-    uint32_t lo, hi;
-    if constexpr (BITS == 4) {  // nibbles: channel i at bit 4 i
-        lo = x & 0x0F0F0F0Fu;          // channels 0, 2, 4, 6
-        hi = (x >> 4) & 0x0F0F0F0Fu;   // channels 1, 3, 5, 7
-    } else {  // 2-bit fields of the low 16 bits: channel i at bit 2 i
-        const uint32_t u = __builtin_amdgcn_perm(0u, x, 0x0C010C00u);  // bytes: x.byte0, 0, x.byte1, 0
-        const uint32_t v = (u | (u << 4)) & 0x0F0F0F0Fu;                // bytes: channels 0-1, 2-3, 4-5, 6-7
-        lo = v & 0x03030303u;          // channels 0, 2, 4, 6
-        hi = (v >> 2) & 0x03030303u;   // channels 1, 3, 5, 7
-    }
-    typedef float f32x2 __attribute__((ext_vector_type(2)));
-    const f32x2 l0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, 512.0f, false);
-    const f32x2 l1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(lo, 512.0f, true);
-    const f32x2 h0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 512.0f, false);
-    const f32x2 h1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(hi, 512.0f, true);
-    c[0] = l0.x;
-    c[2] = l0.y;
-    c[4] = l1.x;
-    c[6] = l1.y;
-    c[1] = h0.x;
-    c[3] = h0.y;
-    c[5] = h1.x;
-    c[7] = h1.y;
-}
-
-// bf16(code * scale + zero) of eight channels, the product and the sum in fp32 (one fused multiply-add, the product
-// of a code and an fp16 scale being exact), as the reference's _dequant and its .to(DOT_DTYPE).
-__device__ __forceinline__ bf16x8 dequant_cell8(const float (&c)[8], const float (&sc)[8], const float (&zr)[8]) {
-    bf16x8 r;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = static_cast<__bf16>(__builtin_fmaf(c[i], sc[i], zr[i]));
-    return r;
-}
-
-__device__ __forceinline__ uint32_t word_of(uint4 x, int i) {
-    return i == 0 ? x.x : (i == 1 ? x.y : (i == 2 ? x.z : x.w));
-}
-
-// CB: 0, or the code bits of a cells instance that reads quantized keys and values through their codes.
-// Heads wider than 256 channels (DP = 512; Gemma-4's global layers, attention/decode.py:216-232): a wave computes its
-// rows' full scores and accumulates one slice of DV = 256 value channels, slice blockIdx.z (the reference's value
-// tiles), at one wave per SIMD; the slices of a block and its splits count on the block's one counter, and the last
-// of them merges every channel.
-template <int DP, int FMT, int QF, bool MASKED, int CB = 0>
-__global__ __launch_bounds__(64, DP > 256 ? 1 : 2) void dense_split_kernel(DenseParams p) {
-    static_assert(CB == 0 || (DP == 128 && FMT == BF16 && QF == BF16 && !MASKED),
-                  "codes are read for bf16 cells of 128 channels only");
-    constexpr int ES = elem_bytes<FMT>();
-    constexpr int DV = DP > 256 ? 256 : DP;  // value channels of a wave
-    constexpr int KS = DP / 32;  // k-steps of the S MFMA
-    constexpr int ND = DV / 16;  // value blocks of 16 channels
-    constexpr bool KLO = two_terms<FMT>();
-    constexpr bool QLO = two_terms<QF>();
-    constexpr int ROW = DV * ES + 16;          // LDS bytes per staged value row
-    constexpr int CHUNKS = TK * DV * ES / 16;  // 16-byte chunks of a staged value tile (a multiple of 64)
-    constexpr int CPR = DV * ES / 16;          // chunks per value row
-    constexpr int CPL = CHUNKS / 64;           // chunks per lane
-    constexpr bool kStage = CPL <= 8;          // the tile's values pass through registers (loads issued first)
-    constexpr int KW = ES == 4 ? 2 : 1;        // 16-byte words of 8 key elements (fp8: the low half of one)
-    // The next tile's loads are in flight while a tile is computed (NBUF = 2) when the registers allow: one set of
-    // staged values (moved into LDS before the next tile's values are issued into it), two sets of keys (fp8 keys
-    // fill half a word; with a mask, eight mask bytes), the accumulators and the query operand within 170 VGPRs
-    // (beyond that the second key set spills at two waves per SIMD).
-    constexpr int KEY_VGPRS = 2 * KS * KW * (ES == 1 ? 2 : 4) + (MASKED ? 8 : 0);
-    constexpr int LIVE_VGPRS = (kStage ? 4 * CPL : 0) + 2 * KEY_VGPRS + 4 * ND + 4 * KS * (QLO ? 2 : 1);
-    constexpr int NBUF = CB != 0 || (kStage && LIVE_VGPRS <= 170) ? 2 : 1;
-    static_assert(CHUNKS % 64 == 0, "value tiles of whole lane rounds");
-    __shared__ __align__(16) uint8_t vtile[TK * ROW];
-    __shared__ __align__(16) uint8_t auxl[CB != 0 ? 32 * 16 : 16];  // codes: the tile's key scales and zero points
-
-    const int lane = static_cast<int>(threadIdx.x);
-    const int n = lane & 15, g = lane >> 4;
-    const int prog = blockIdx.x;
-    const int split = blockIdx.y;
-    const int v0 = static_cast<int>(blockIdx.z) * DV;  // the wave's first value channel
-    const int mt = prog % p.m_tiles;
-    const int kvh = (prog / p.m_tiles) % p.kv_heads;
-    const int b = prog / (p.m_tiles * p.kv_heads);
-    const int r = mt * 16 + n;  // the lane's query row (MFMA column n)
-    // varlen queries: row b's queries are tokens q_start .. q_start + q_count - 1
-    const int q_start = p.query_start_loc ? p.query_start_loc[b] : 0;
-    const int q_count = p.query_start_loc ? p.query_start_loc[b + 1] - q_start : p.queries;
-    const int gq0 = r < p.rows ? r / p.queries : 0;
-    const int qi0 = r < p.rows ? r % p.queries : 0;
-    const bool r_ok = r < p.rows && qi0 < q_count;
-    const int gq = r_ok ? gq0 : 0;
-    const int qi = r_ok ? qi0 : 0;
-    const int h = kvh * p.groups + gq;
-
-    // the query operand: row r, channels 32 j + 8 g .. (zero past the head dim and for rows past the group)
-    bf16x8 qh[KS], ql[KS];
-#pragma unroll
-    for (int j = 0; j < KS; ++j) {
-        const int c = 32 * j + 8 * g;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            qh[j][i] = static_cast<__bf16>(0.0f);
-            ql[j][i] = static_cast<__bf16>(0.0f);
-        }
-        if (r_ok && c < p.head_dim)
-            load_query8<QF>(p, b * p.sq_b + h * p.sq_h + static_cast<int64_t>(q_start + qi) * p.sq_q + c, qh[j], ql[j]);
-    }
-    const float ks = p.k_scale ? p.k_scale[kvh] : 1.0f;
-    const float vs = p.v_scale ? p.v_scale[kvh] : 1.0f;
-    const float score_scale = p.softcap > 0.0f ? p.scale * ks : p.scale * ks * kLog2e;
-    const float inv_cap = p.softcap > 0.0f ? 1.0f / p.softcap : 0.0f;
-    const uint8_t* kbase = static_cast<const uint8_t*>(p.k) + (b * p.sk_b + kvh * p.sk_h) * ES;
-    const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.sv_b + kvh * p.sv_h) * ES;
-    const uint8_t* mrow = MASKED ? p.mask + b * p.sm_b + h * p.sm_h + qi * p.sm_q : nullptr;
-    // the key axis: dense slots, or (gathered) the row's compact entries followed by its dense slots from start on,
-    // or (cells) the row's seq_lens[b] tokens in its pages
-    int count = 0, start = 0, row_keys = p.cells ? min(max(p.seq_lens[b], 0), p.keys) : p.keys;
-    const uint8_t* gkbase = kbase;
-    const uint8_t* gvbase = vbase;
-    const int32_t* gidx = nullptr;
-    if (p.gk) {
-        count = min(max(p.g_count[b * p.kv_heads + kvh], 0), p.g_capacity);
-        start = min(max(p.g_start[b], 0), p.dense_keys);
-        row_keys = min(count + p.dense_keys - start, p.keys);
-        gkbase = static_cast<const uint8_t*>(p.gk) + (b * p.sgk_b + kvh * p.sgk_h) * ES;
-        gvbase = static_cast<const uint8_t*>(p.gv) + (b * p.sgv_b + kvh * p.sgv_h) * ES;
-        gidx = p.g_index + b * p.sgi_b + kvh * p.sgi_h;
-    }
-    // Quest: the row's selected pages (a prefix of its list) come first, then its slots from done[b] pages on
-    const int32_t* qlist = nullptr;
-    const int page_cap = p.qp_list ? p.dense_keys >> p.qp_shift : 0;  // whole pages in the buffer
-    if (p.qp_list) {
-        qlist = p.qp_list + b * p.sqp_b + kvh * p.sqp_h;
-        int valid = 0;
-        for (int i = 0; i < p.qp_pages; i += 64) {
-            const int e = i + lane < p.qp_pages ? qlist[i + lane] : -1;
-            valid += static_cast<int>(__popcll(__ballot(e >= 0)));
-        }
-        count = min(valid, page_cap) << p.qp_shift;
-        start = min(max(p.qp_done[b], 0), page_cap) << p.qp_shift;
-        row_keys = min(count + p.dense_keys - start, p.keys);
-    }
-    // This wave's tiles interleave with its block's other splits: tile k starts at key (split + k splits) 32, so that
-    // the block's waves (one XCD) read adjacent 8 KB runs of the K and V buffers together.
-    const int tiles_row = (row_keys + TK - 1) / TK;
-    const int my_tiles = split < tiles_row ? (tiles_row - 1 - split) / p.splits + 1 : 0;
-    auto tile_start = [&](int k) __attribute__((always_inline)) { return (split + k * p.splits) * TK; };
-    // cells: a window over this wave's next 64 tile halves (16 keys each), lane l holding the cache byte offset of
-    // the first cell of half win0 + l (its page's cells of this KV head, plus the half's place in the page: a
-    // multiple of 16 tokens); a tile reads its halves' offsets from the window (v_readlane) and reloads the window
-    // every 32 tiles, so that the tile loads need no block-table load, and no division by the page size, of their
-    // own. Quest uses the same window for the slot of each half's first key (page-list entries instead of the
-    // block table).
-    int win0 = -(1 << 30);
-    int64_t win_page = 0;
-    auto half_offset = [&](int half) __attribute__((always_inline)) -> int64_t {  // half: uniform
-        if (half < win0 || half >= win0 + 64) {
-            win0 = half;
-            const int mine = half + lane;
-            const int first = tile_start(mine >> 1) + (mine & 1) * 16;
-            if (p.cells) {
-                const int lp = min(first / p.page_size, p.bt_cols - 1);
-                const int page =
-                    min(max(p.block_table[static_cast<int64_t>(b) * p.bt_stride + lp], 0), p.num_pages - 1);
-                win_page = page * p.sc_page + kvh * p.sc_head + static_cast<int64_t>(first % p.page_size) * p.sc_token;
-            } else if (first < count) {  // Quest: the slot of the half's first key (a half lies in one page)
-                const int e = qlist[min(first >> p.qp_shift, p.qp_pages - 1)];
-                win_page = (static_cast<int64_t>(min(max(e, 0), page_cap - 1)) << p.qp_shift) +
-                           (first & ((1 << p.qp_shift) - 1));
-            } else {
-                win_page = start + first - count;
-            }
-            // wait here for the table load (vmcnt(0)), so that the common path, which reloads nothing, does not
-            // wait at the branch's join for every load in flight
-            __builtin_amdgcn_s_waitcnt(0x0F70);
-        }
-        const int at = half - win0;
-        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(win_page), at);
-        const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(win_page) >> 32), at);
-        return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
-    };
-    // the cache offsets of the first cells of tile k's two 16-key halves (a tile starts at a multiple of 32 keys and
-    // pages hold a multiple of 16, so each half lies in one page)
-    int64_t cell_h0 = 0, cell_h1 = 0;  // (two variables, not an array: a lane-dependent index of one goes to scratch)
-    // (Quest: the slots of the halves' first keys; pages of 32 or more slots, and the tail, keep a tile's halves
-    // adjacent)
-    auto tile_pages = [&](int k) __attribute__((always_inline)) {
-        if (p.cells) {
-            cell_h0 = half_offset(2 * k);
-            cell_h1 = p.page_size % 32 == 0 ? cell_h0 + 16 * p.sc_token : half_offset(2 * k + 1);
-        } else if (p.qp_list) {
-            cell_h0 = half_offset(2 * k);
-            cell_h1 = p.qp_shift >= 5 ? cell_h0 + 16 : half_offset(2 * k + 1);
-        }
-    };
-    auto quest_slot = [&](int t) __attribute__((always_inline)) -> int64_t {  // t inside the current tile
-        return ((t >> 4) & 1 ? cell_h1 : cell_h0) + (t & 15);
-    };
-    auto cell_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {  // t inside the current tile
-        return p.cells + ((t >> 4) & 1 ? cell_h1 : cell_h0) + static_cast<int64_t>(t & 15) * p.sc_token;
-    };
-    auto key_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
-        if (p.cells) return cell_row(t);
-        if (p.qp_list) return kbase + quest_slot(t) * p.sk_s * ES;
-        return t < count ? gkbase + static_cast<int64_t>(t) * p.sgk_s * ES
-                         : kbase + static_cast<int64_t>(start + t - count) * p.sk_s * ES;
-    };
-    auto value_row = [&](int t) __attribute__((always_inline)) -> const uint8_t* {
-        if (p.cells) return cell_row(t) + p.cell_off_v;
-        if (p.qp_list) return vbase + quest_slot(t) * p.sv_s * ES;
-        return t < count ? gvbase + static_cast<int64_t>(t) * p.sgv_s * ES
-                         : vbase + static_cast<int64_t>(start + t - count) * p.sv_s * ES;
-    };
-    // causal: the last q_count keys of the row are its queries' own tokens
-    const int causal_limit = p.causal ? row_keys - q_count + qi + 1 : row_keys;
-    auto mask_col = [&](int t) __attribute__((always_inline)) -> int64_t {
-        if (p.qp_list) return quest_slot(t);
-        return t < count ? min(max(gidx[t], 0), p.dense_keys - 1) : start + t - count;
-    };
-
-    float m_i = -INFINITY, l_i = 0.0f;
-    f32x4 acc[ND];
-#pragma unroll
-    for (int nd = 0; nd < ND; ++nd) acc[nd] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-
-    const int t_end = row_keys;
-
-    // A tile's loads in registers: its values (staged for LDS, one set), its keys (A-row n of S block v is key
-    // t0 + 8 (n / 4) + 4 v + n % 4) and, with a mask, the mask bytes of the lane's keys t0 + 8 g + e.
-    uint4 vreg[kStage && CB == 0 ? CPL : 1];
-    // codes: the lane's value token (t0 + lane / 2, channels 64 (lane % 2) ..): its codes, its scales and zero points
-    // and its flags; and the key-aux slot of the tile's cell t0 + lane % 32
-    uint4 vcw[CB == 4 ? 2 : 1], vsz, vaux;
-    uint32_t vfl = 0;
-    struct Keys {
-        uint4 k[CB != 0 ? 1 : 2][CB != 0 ? 1 : KS][KW];
-        uint32_t m[MASKED ? 8 : 1];
-        uint32_t kc[2][CB != 0 ? KS : 1];  // codes: the code word of the lane's channels 32 j + 8 g .. of its key v
-        uint32_t kf[2];                    // codes: the flag byte of its key v
-        int64_t h0, h1;                    // codes: the tile's half offsets (the next tile's issue moves cell_h*)
-    };
-    // Every load is issued unconditionally at a clamped address (a key past the split reads the split's last key, a
-    // channel past the dims reads channel 0) and what it must not contribute is zeroed where it is used: every path
-    // through the loop then issues the same loads, and the wait before a tile's use leaves the younger tile's loads
-    // in flight.
-    auto issue = [&](Keys& K, int k) __attribute__((always_inline)) {
-        const int t0 = tile_start(k);
-        tile_pages(k);
-        if constexpr (CB != 0) {
-            K.h0 = cell_h0;
-            K.h1 = cell_h1;
-            const uint8_t* vc = cell_row(min(t0 + (lane >> 1), t_end - 1));
-#pragma unroll
-            for (int i = 0; i < (CB == 4 ? 2 : 1); ++i)
-                vcw[i] = *reinterpret_cast<const uint4*>(vc + p.cell_off_vc + 16 * (CB / 2) * (lane & 1) + 16 * i);
-            vsz = *reinterpret_cast<const uint4*>(vc + p.cell_off_vs);
-            vfl = *(vc + p.cell_off_flag + 1);
-            // (every cell of the tile's key group: the tile's 32 cells lie in one page, page_size being a multiple
-            // of 32, and a visible key's group aux may sit in a cell past the row's keys)
-            vaux = *reinterpret_cast<const uint4*>(cell_row(t0 + (lane & 31)) + p.cell_off_ka);
-#pragma unroll
-            for (int v = 0; v < 2; ++v) {
-                const uint8_t* krow = cell_row(min(t0 + 8 * (n >> 2) + 4 * v + (n & 3), t_end - 1));
-                K.kf[v] = *(krow + p.cell_off_flag);
-#pragma unroll
-                for (int j = 0; j < KS; ++j)
-                    K.kc[v][j] = *reinterpret_cast<const uint32_t*>(
-                        krow + p.cell_off_kc + (CB == 2 ? 4 * (2 * j + (g >> 1)) : 16 * j + 4 * g));
-            }
-            return;
-        }
-        if constexpr (MASKED)
-#pragma unroll
-            for (int e = 0; e < 8; ++e) K.m[e] = mrow[mask_col(min(t0 + 8 * g + e, t_end - 1)) * p.sm_s];
-        if constexpr (kStage)
-#pragma unroll
-            for (int i = 0; i < CPL; ++i) {
-                const int chunk = lane + 64 * i;
-                const int t = min(t0 + chunk / CPR, t_end - 1);
-                const int c = v0 + (chunk % CPR) * (16 / ES);
-                vreg[i] = stream_load16(value_row(t) + (c < p.value_dim ? c : 0) * ES);
-            }
-#pragma unroll
-        for (int v = 0; v < 2; ++v) {
-            const uint8_t* krow = key_row(min(t0 + 8 * (n >> 2) + 4 * v + (n & 3), t_end - 1));
-#pragma unroll
-            for (int j = 0; j < KS; ++j) {
-                const int c = 32 * j + 8 * g;
-                load8<FMT>(krow + (c < p.head_dim ? c : 0) * ES, K.k[v][j]);
-            }
-        }
-    };
-    // ---- the tile's values into LDS (zero past the keys and past Dv); the previous tile's reads of LDS came first ----
-    auto stage = [&](int t0) __attribute__((always_inline)) {
-        if constexpr (CB != 0) {
-            if (lane < 32) *reinterpret_cast<uint4*>(auxl + 16 * lane) = vaux;
-            const int tl = lane >> 1, hh = lane & 1;
-            const int t = t0 + tl;
-            const bool vok = t < t_end;
-            const f16x8 sz = __builtin_bit_cast(f16x8, vsz);  // the token's scales [4] then zero points [4]
-            uint4 out[8];
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {  // channels 64 hh + 8 q .., value group 2 hh + q / 4
-                // (selects, not an index by the lane's half: a vector indexed at run time goes to scratch)
-                const float sc = static_cast<float>(hh ? sz[2 + q / 4] : sz[q / 4]);
-                const float zr = static_cast<float>(hh ? sz[6 + q / 4] : sz[4 + q / 4]);
-                const uint32_t x = CB == 2 ? (word_of(vcw[0], q >> 1) >> (16 * (q & 1))) & 0xFFFFu
-                                           : word_of(vcw[CB == 4 ? (q >> 2) : 0], q & 3);
-                float c[8], scs[8], zrs[8];
-                cell_codes8<CB>(x, c);
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    scs[i] = sc;
-                    zrs[i] = zr;
-                }
-                out[q] = __builtin_bit_cast(uint4, dequant_cell8(c, scs, zrs));
-            }
-            uint8_t* dst = vtile + tl * ROW + 128 * hh;
-            const bool dense = vok && vfl != 1u;  // a cell not quantized: its dense entry
-            if (__ballot(dense) != 0) {  // (the loads and their uses stay inside this rare branch)
-                if (dense) {
-                    const uint8_t* row = cell_row(t) + p.cell_off_v + 128 * hh;
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) out[q] = *reinterpret_cast<const uint4*>(row + 16 * q);
-                }
-#pragma unroll
-                for (int q = 0; q < 8; ++q)
-                    *reinterpret_cast<uint4*>(dst + 16 * q) = vok ? out[q] : make_uint4(0, 0, 0, 0);
-            } else {
-#pragma unroll
-                for (int q = 0; q < 8; ++q)
-                    *reinterpret_cast<uint4*>(dst + 16 * q) = vok ? out[q] : make_uint4(0, 0, 0, 0);
-            }
-            return;
-        }
-        if constexpr (kStage) {
-#pragma unroll
-            for (int i = 0; i < CPL; ++i) {
-                const int chunk = lane + 64 * i;
-                const bool ok = t0 + chunk / CPR < t_end && v0 + (chunk % CPR) * (16 / ES) < p.value_dim;
-                *reinterpret_cast<uint4*>(vtile + (chunk / CPR) * ROW + (chunk % CPR) * 16) =
-                    ok ? vreg[i] : make_uint4(0, 0, 0, 0);
-            }
-        } else {
-            for (int chunk = lane; chunk < CHUNKS; chunk += 64) {
-                const int t = chunk / CPR;
-                const int c = (chunk % CPR) * (16 / ES);
-                uint4 x = make_uint4(0, 0, 0, 0);
-                if (t0 + t < t_end && v0 + c < p.value_dim)
-                    x = *reinterpret_cast<const uint4*>(value_row(t0 + t) + (v0 + c) * ES);
-                *reinterpret_cast<uint4*>(vtile + t * ROW + (chunk % CPR) * 16) = x;
-            }
-        }
-    };
-    auto compute = [&](const Keys& K, int t0) __attribute__((always_inline)) {
-        // ---- S^T = K Q^T (key channels past the head dim zeroed) ----
-        f32x4 s[2];
-        if constexpr (CB != 0) {
-            // the lane's key scales and zero points (channels 32 j + 8 g ..: entries of the group's aux in the slots
-            // of cells 4 j + g and 16 + 4 j + g), then the keys from their codes, or their dense entries where the
-            // flag is not 1 (a rare branch that keeps its loads and their uses to itself)
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the aux stores of this tile (one wave: in order)
-            auto scores = [&](bool dense) __attribute__((always_inline)) {
-#pragma unroll
-                for (int v = 0; v < 2; ++v) s[v] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int j = 0; j < KS; ++j) {
-                    const f16x8 sj = *reinterpret_cast<const f16x8*>(auxl + 16 * (4 * j + g));
-                    const f16x8 zj = *reinterpret_cast<const f16x8*>(auxl + 16 * (16 + 4 * j + g));
-#pragma unroll
-                    for (int v = 0; v < 2; ++v) {
-                        const uint32_t x = CB == 2 ? (K.kc[v][j] >> (16 * (g & 1))) & 0xFFFFu : K.kc[v][j];
-                        float c[8];
-                        cell_codes8<CB>(x, c);
-                        bf16x8 kh;  // (the fp16 scales widened inside each product: v_fma_mix_f32)
-#pragma unroll
-                        for (int i = 0; i < 8; ++i)
-                            kh[i] = static_cast<__bf16>(
-                                __builtin_fmaf(c[i], static_cast<float>(sj[i]), static_cast<float>(zj[i])));
-                        if (dense && K.kf[v] != 1u) {
-                            const int tk = min(t0 + 8 * (n >> 2) + 4 * v + (n & 3), t_end - 1);
-                            const uint8_t* row = p.cells + ((tk >> 4) & 1 ? K.h1 : K.h0) +
-                                                 static_cast<int64_t>(tk & 15) * p.sc_token;
-                            kh = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(row + 2 * (32 * j + 8 * g)));
-                        }
-                        s[v] = mfma(kh, qh[j], s[v]);
-                    }
-                }
-            };
-            if (__ballot(K.kf[0] != 1u || K.kf[1] != 1u) != 0)
-                scores(true);
-            else
-                scores(false);
-        } else
-#pragma unroll
-        for (int v = 0; v < 2; ++v) {
-            s[v] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int j = 0; j < KS; ++j) {
-                uint4 w[KW];
-                const bool ok = 32 * j + 8 * g < p.head_dim;
-#pragma unroll
-                for (int x = 0; x < KW; ++x) w[x] = ok ? K.k[v][j][x] : make_uint4(0, 0, 0, 0);
-                bf16x8 kh, kl;
-                cvt8<FMT>(w, kh, kl);
-                s[v] = mfma(kh, qh[j], s[v]);
-                if constexpr (QLO) s[v] = mfma(kh, ql[j], s[v]);
-                if constexpr (KLO) s[v] = mfma(kl, qh[j], s[v]);
-            }
-        }
-        // ---- scores in log2 units, masked: lane (n, g) holds keys t0 + 8 g + 4 v + i of row r ----
-        uint32_t vis = 0;  // bit 4 v + i
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int t = t0 + 8 * g + e;
-            bool ok = r_ok && t < t_end && t < causal_limit;
-            if constexpr (MASKED) ok = ok && (K.m[e] & 0xFFu) != 0;
-            vis |= ok ? 1u << e : 0u;
-        }
-        float tile_max = -INFINITY;
-        // the soft cap tested once per tile, not per score (the compiler keeps a uniform test inside an unrolled loop)
-        if (p.softcap > 0.0f) {
-#pragma unroll
-            for (int v = 0; v < 2; ++v)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) s[v][i] = soft_cap_log2(s[v][i] * score_scale, p.softcap, inv_cap);
-        } else {
-#pragma unroll
-            for (int v = 0; v < 2; ++v)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) s[v][i] *= score_scale;
-        }
-#pragma unroll
-        for (int v = 0; v < 2; ++v)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float x = (vis >> (4 * v + i)) & 1u ? s[v][i] : -INFINITY;
-                s[v][i] = x;
-                tile_max = max_nan(tile_max, x);
-            }
-        // ---- online softmax, lazy rescaling (the reference maximum moves when a score exceeds it by 2^8) ----
-        if (__ballot(tile_max > m_i + 8.0f || m_i == -INFINITY) != 0) {
-            const bool fresh = m_i == -INFINITY;
-            const float m_new = fmaxf(m_i, group_max(tile_max));
-            const float alpha = fresh ? 0.0f : __builtin_amdgcn_exp2f(m_i - m_new);
-            l_i *= alpha;
-#pragma unroll
-            for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[nd][i] = fresh ? 0.0f : acc[nd][i] * alpha;
-            m_i = m_new;
-        }
-        const float neg_m = m_i == -INFINITY ? 0.0f : -m_i;
-        float pw[8];
-#pragma unroll
-        for (int v = 0; v < 2; ++v)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                pw[4 * v + i] = __builtin_amdgcn_exp2f(s[v][i] + neg_m);
-                l_i += pw[4 * v + i];
-            }
-        bf16x8 ph, pl;
-        split8(pw, ph, pl);
-        // ---- O^T += V^T P^T: lane (n, g) supplies channel 16 nd + n of keys 8 g .. 8 g + 7 ----
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the tile's LDS stores (one wave: in order)
-#pragma unroll
-        for (int nd = 0; nd < ND; ++nd) {
-            const int c = 16 * nd + n;  // (of the wave's slice)
-            if (v0 + 16 * nd >= p.value_dim) break;
-            bf16x8 vh, vl;
-            if constexpr (FMT == BF16) {  // the staged bits are the operand (no widening and rounding back)
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    vh[e] = __builtin_bit_cast(__bf16, *reinterpret_cast<const uint16_t*>(vtile + (8 * g + e) * ROW + c * 2));
-            } else {
-                float x[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) x[e] = elem_f32<FMT>(vtile + (8 * g + e) * ROW + c * ES);
-                split8(x, vh, vl);
-            }
-            acc[nd] = mfma(vh, ph, acc[nd]);
-            acc[nd] = mfma(vh, pl, acc[nd]);
-            if constexpr (KLO) acc[nd] = mfma(vl, ph, acc[nd]);
-        }
-    };
-
-    if (my_tiles > 0) {
-        if constexpr (NBUF == 1) {
-            for (int k = 0; k < my_tiles; ++k) {
-                Keys K;
-                issue(K, k);
-                stage(tile_start(k));
-                compute(K, tile_start(k));
-            }
-        } else {
-            // past the wave's last tile every step issues that tile again (read from L2 and never computed)
-            Keys K0, K1;
-            int ki = 0, k = 0;
-            issue(K0, ki);
-            while (true) {
-                stage(tile_start(k));
-                ki = min(ki + 1, my_tiles - 1);
-                issue(K1, ki);
-                compute(K0, tile_start(k));
-                if (++k >= my_tiles) break;
-                stage(tile_start(k));
-                ki = min(ki + 1, my_tiles - 1);
-                issue(K0, ki);
-                compute(K1, tile_start(k));
-                if (++k >= my_tiles) break;
-            }
-        }
-    }
-    l_i = group_sum(l_i);
-    const float sink = p.sinks && r_ok ? p.sinks[h] * kLog2e : -INFINITY;
-    auto out_at = [&](int row_qi, int row_h, int d) __attribute__((always_inline)) -> int64_t {
-        return b * p.so_b + static_cast<int64_t>(q_start + row_qi) * p.so_q + row_h * p.so_h + d;
-    };
-
-    // ---- one split: the row's output directly; lane (n, g) holds channels 16 nd + 4 g + i of row r ----
-    if (p.splits == 1) {
-        if (!r_ok) return;
-        float inv;
-        const float a = sink_weight(m_i, l_i, sink, inv);
-#pragma unroll
-        for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int d = v0 + 16 * nd + 4 * g + i;
-                if (d < p.value_dim) store_out<QF>(p, out_at(qi, h, d), acc[nd][i] * vs * a * inv);
-            }
-        return;
-    }
-
-    // ---- the split's partial: row n's max and sum (lane group 0) and its channels 16 nd + 4 g + i ----
-    const int64_t slot_stride = DP + 2;
-    const int64_t prog_part = static_cast<int64_t>(prog) * p.splits * 16;
-    if (r_ok) {
-        float* slot = p.part + (prog_part + split * 16 + n) * slot_stride;
-        if (g == 0 && blockIdx.z == 0) {  // (every value slice has the same maximum and sum)
-            coherent_store(slot, m_i);
-            coherent_store(slot + 1, l_i);
-        }
-#pragma unroll
-        for (int nd = 0; nd < ND; ++nd)
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (v0 + 16 * nd < p.value_dim) coherent_store(slot + 2 + v0 + 16 * nd + 4 * g + i, acc[nd][i] * vs);
-    }
-    // The hand-off to the last split to finish: the partials are written and read as agent-scope atomics (sc1), so
-    // completion orders them; the compiler may not move the stores past the count (a signal fence), the wave waits
-    // for its stores (vmcnt counts stores on gfx950), then lane 0 counts the split; the wave that finds every other
-    // split counted loads the partials after its atomic returned and leaves the counter zero for the next call.
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    int prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(p.counters + prog, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (__shfl(prev, 0) != p.splits * static_cast<int>(gridDim.z) - 1) return;
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-
-    // ---- the merge by log-sum-exp: lane-owned runs of 8 channels of one query row, the splits folded in batches of 4
-    // with their loads in flight together ----
-    const int rows_here = min(16, p.rows - mt * 16);
-    for (int base = 0; base < rows_here * p.value_dim; base += 64 * 8) {
-        const int e = base + lane * 8;
-        const bool active = e < rows_here * p.value_dim;
-        const int rr = active ? e / p.value_dim : 0;
-        const int d = active ? e % p.value_dim : 0;
-        const int row = mt * 16 + rr;
-        const int row_qi = row % p.queries, row_h = kvh * p.groups + row / p.queries;
-        const bool live = active && row_qi < q_count;
-        float m_run = -INFINITY, l_run = 0.0f, o_run[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o_run[i] = 0.0f;
-        for (int s0 = 0; s0 < p.splits; s0 += 4) {
-            float mk[4], lk[4], ok[4][8];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const bool use = live && s0 + j < p.splits;
-                const float* sk = p.part + (prog_part + (use ? s0 + j : 0) * 16 + rr) * slot_stride;
-                mk[j] = use ? coherent_load(sk) : -INFINITY;
-                lk[j] = use ? coherent_load(sk + 1) : 0.0f;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) ok[j][i] = use ? coherent_load(sk + 2 + d + i) : 0.0f;
-            }
-            float m_new = m_run;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) m_new = fmaxf(m_new, mk[j]);
-            if (m_new == -INFINITY) continue;
-            const float a = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-            l_run *= a;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) o_run[i] *= a;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if (mk[j] == -INFINITY) continue;
-                const float cw = __builtin_amdgcn_exp2f(mk[j] - m_new);
-                l_run += lk[j] * cw;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) o_run[i] += ok[j][i] * cw;
-            }
-            m_run = m_new;
-        }
-        if (live) {
-            const float row_sink = p.sinks ? p.sinks[row_h] * kLog2e : -INFINITY;
-            float inv;
-            const float a = sink_weight(m_run, l_run, row_sink, inv);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) store_out<QF>(p, out_at(row_qi, row_h, d + i), o_run[i] * a * inv);
-        }
-    }
-    if (lane == 0) __hip_atomic_store(p.counters + prog, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 template <int DP, int FMT, int QF>
 int launch_dense(const DenseParams& p, hipStream_t stream) {

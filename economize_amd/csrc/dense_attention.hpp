@@ -74,9 +74,30 @@ struct DenseParams {
     int64_t sqp_b, sqp_h;
     int qp_pages, qp_shift;
     const int32_t* qp_done;
+    // KIVI packed mode (kp_kc non-null; the reference's kivi_decode_attention over a KIVIPacked record,
+    // attention/kivi.py:80-309): key t of (b, kvh) below kp_kq[b] is code * scale + zero of its codes (bits per
+    // channel, channel d in byte d * bits / 8 at bit (d % (8 / bits)) * bits) and of its key group's fp16 scales and
+    // zero points (group t / kp_kg), value t below kp_vq[b] likewise with its own scales and zero points (channel
+    // group d / kp_vg), computed in fp32 and rounded to the K/V format; every other key or value is read from k / v,
+    // at slot t, or at slot t % kp_ring of the rings k / v when kp_ring > 0. Counts are clamped to [0, keys].
+    const uint8_t* kp_kc;  // key codes [B, Hkv, S, D * bits / 8], byte strides skc_*
+    int64_t skc_b, skc_h, skc_s;
+    const uint16_t* kp_ks;  // key scales [B, Hkv, ceil(S / kp_kg), D] (fp16 bits), element strides sks_*
+    const uint16_t* kp_kz;  // key zero points, in the scales' layout
+    int64_t sks_b, sks_h, sks_g;
+    const uint8_t* kp_vc;  // value codes [B, Hkv, S, Dv * bits / 8], byte strides svc_*
+    int64_t svc_b, svc_h, svc_s;
+    const uint16_t* kp_vs;  // value scales [B, Hkv, S, Dv / kp_vg] (fp16 bits), element strides svs_*
+    const uint16_t* kp_vz;  // value zero points, in the scales' layout
+    int64_t svs_b, svs_h, svs_s;
+    const int32_t* kp_kq;  // [B]
+    const int32_t* kp_vq;  // [B]
+    int kp_bits, kp_kg, kp_vg, kp_ring;
 };
 
 int dense_padded_dim(int head_dim, int value_dim);  // 64, 128, 256 or 512; 0 when none fits
 int dense_attention(const DenseParams& p, int padded_dim, hipStream_t stream);
+// The KIVI packed mode (kp_kc set): bf16, fp16 or fp32 queries with K/V in the query's format (kivi_packed.hip).
+int kivi_packed_attention(const DenseParams& p, int padded_dim, hipStream_t stream);
 
 }  // namespace eco

@@ -402,6 +402,34 @@ int eco_kivi_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, con
                     const uint32_t* mask_bits, int64_t mk_b, int64_t mk_h, int64_t mk_q, int32_t mask_words,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Decode attention over a KIVI packed record of dense-layout codes (the reference's KIVIPacked, attention/kivi.py:
+ * 80-132): eco_decode's call (query q_format = bf16, fp16 or fp32 with k / v in the same format, mask, soft cap,
+ * sinks, workspace of eco_decode_workspace_size) where, for row b, keys t < keys_quantized[b] and values t <
+ * values_quantized[b] (int32 [B] on the device, clamped to [0, keys]) are code * scale + zero computed in fp32 and
+ * rounded to the query's format, from
+ *   key_codes   uint8 [B, Hkv, keys, D * bits / 8] (byte strides skc_*; channel d in byte d * bits / 8 at bit
+ *               (d % (8 / bits)) * bits, as pack_codes packs them, attention/kivi.py:38-45),
+ *   key_scale / key_zero   fp16 [B, Hkv, ceil(keys / key_group), D] (element strides sks_*, shared),
+ *   value_codes uint8 [B, Hkv, keys, Dv * bits / 8] (byte strides svc_*),
+ *   value_scale / value_zero   fp16 [B, Hkv, keys, Dv / value_group] (element strides svs_*, shared),
+ * bits 2, 4 or 8, any key group, a value group dividing Dv; every other key and value is read from k / v at slot t,
+ * or, with ring > 0, from the rings k / v at slot t % ring (the reference's key_ring / value_ring). The result is
+ * bit-identical to eco_decode over buffers holding the dequantized values. Alignment: codes and their strides to the
+ * bytes of 16 / element_size codes, key scales to 16 / (8 for fp32) bytes with strides in multiples of 8 (4)
+ * elements. Replaces kivi_decode_attention (attention/kivi.py:199-309; kernel attention/_kivi_kernels.py:14-326). */
+int eco_kivi_packed_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_h, int64_t sq_q, const void* k,
+                           const void* v, int64_t sk_b, int64_t sk_h, int64_t sk_s, int64_t sv_b, int64_t sv_h,
+                           int64_t sv_s, int32_t ring, const uint8_t* key_codes, int64_t skc_b, int64_t skc_h,
+                           int64_t skc_s, const void* key_scale, const void* key_zero, int64_t sks_b, int64_t sks_h,
+                           int64_t sks_g, const uint8_t* value_codes, int64_t svc_b, int64_t svc_h, int64_t svc_s,
+                           const void* value_scale, const void* value_zero, int64_t svs_b, int64_t svs_h,
+                           int64_t svs_s, const int32_t* keys_quantized, const int32_t* values_quantized,
+                           int32_t bits, int32_t key_group, int32_t value_group, const uint8_t* mask, int64_t sm_b,
+                           int64_t sm_h, int64_t sm_q, int64_t sm_s, const float* sinks, void* out, int64_t so_b,
+                           int64_t so_q, int64_t so_h, int32_t batch, int32_t queries, int32_t q_heads,
+                           int32_t kv_heads, int32_t keys, int32_t head_dim, int32_t value_dim, float scale,
+                           float softcap, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
