@@ -315,8 +315,10 @@ def economize_attention_forward(module: torch.nn.Module | None, query: torch.Ten
         raise ConfigError(f"query must be [B, Hq, Q, D], got {tuple(query.shape)}")
     handle = key if isinstance(key, PagedKV) else packed_of(key)
     paged = handle if isinstance(handle, PagedKV) else None
-    # packed K/V over dense buffers: a gathered cache's compact entries, Quest's pages of a dense cache
-    dense_packed = handle if paged is None and getattr(handle, "format", None) in ("gathered", "quest") else None
+    # packed K/V over dense buffers: a gathered cache's compact entries, Quest's pages of a dense cache, KIVI codes in
+    # the reference's layout
+    dense_packed = handle if paged is None and getattr(handle, "format", None) in ("gathered", "quest", "kivi") \
+        else None
     gathered = dense_packed if getattr(dense_packed, "format", None) == "gathered" else None
     layer = getattr(module, "layer_idx", None)
     queries = query.shape[2]

@@ -979,6 +979,53 @@ int eco_kivi_fake_quantize(void* buffer, int32_t format, int64_t sb, int64_t sh,
     return kivi_fake_quantize(p, static_cast<hipStream_t>(stream));
 }
 
+int eco_kivi_pack_quantize(int32_t kind, void* src, int32_t format, int64_t ss_b, int64_t ss_h, int64_t ss_s,
+                           int32_t src_ring, int32_t write_back, void* codes, int64_t sc_b, int64_t sc_h, int64_t sc_s,
+                           void* scale, void* zero, int64_t sz_b, int64_t sz_h, int64_t sz_s, const int32_t* from,
+                           const int32_t* to, int32_t batch, int32_t heads, int32_t slots, int32_t head_dim,
+                           int32_t bits, int32_t group, int32_t max_tokens, uint32_t* overflow, void* stream) {
+    if (!src || !codes || !scale || !zero || !from || !to) return fail("kivi pack: null pointer");
+    if (format != BF16 && format != FP16 && format != FP32)
+        return fail("kivi pack: the source must be bf16, fp16 or fp32");
+    if (bits != 2 && bits != 4 && bits != 8) return fail("kivi pack: bits must be 2, 4 or 8");
+    if (kind != 0 && kind != 1) return fail("kivi pack: kind must be 0 (keys) or 1 (values)");
+    if (batch < 0 || heads < 0 || slots < 0 || head_dim <= 0 || group <= 0 || max_tokens < 0 || src_ring < 0)
+        return fail("kivi pack: bad shape, group or token count");
+    if (head_dim % (8 / bits)) return fail("kivi pack: the head dim does not pack into whole bytes");
+    if (kind == 0 && max_tokens % group) return fail("kivi pack: keys are quantized in whole groups of tokens");
+    if (kind == 1 && head_dim % group) return fail("kivi pack: the value group must divide the head dim");
+    if (write_back && src_ring) return fail("kivi pack: a ring source is not written back");
+    KiviPackParams p{};
+    p.src = src;
+    p.format = format;
+    p.ss_b = ss_b;
+    p.ss_h = ss_h;
+    p.ss_s = ss_s;
+    p.src_ring = src_ring;
+    p.write_back = write_back != 0;
+    p.codes = static_cast<uint8_t*>(codes);
+    p.sc_b = sc_b;
+    p.sc_h = sc_h;
+    p.sc_s = sc_s;
+    p.scale = static_cast<uint16_t*>(scale);
+    p.zero = static_cast<uint16_t*>(zero);
+    p.sz_b = sz_b;
+    p.sz_h = sz_h;
+    p.sz_s = sz_s;
+    p.from = from;
+    p.to = to;
+    p.batch = batch;
+    p.heads = heads;
+    p.head_dim = head_dim;
+    p.bits = bits;
+    p.group = group;
+    p.max_tokens = max_tokens;
+    p.keys = kind == 0;
+    p.slots = slots;
+    p.overflow = overflow;
+    return kivi_pack_quantize(p, static_cast<hipStream_t>(stream));
+}
+
 int eco_kivi_cells_layout(int32_t head_dim, int32_t element_size, int32_t bits, int32_t group, int32_t* offsets) {
     if (!offsets) return fail("kivi cells layout: null output");
     CellLayout L;

@@ -71,7 +71,113 @@ __global__ __launch_bounds__(256) void kivi_fake_quant_kernel(KiviFakeParams p) 
     }
 }
 
+__device__ inline uint16_t half_bits(float x) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x)); }
+
+// Keys into the packed record: a thread per (b, h, key group after from[b], code byte j), the 8 / bits channels of
+// byte j over the group's tokens (their quantization first, then the tokens' code bytes), so that no two threads
+// write one byte.
+__global__ __launch_bounds__(256) void kivi_pack_keys_kernel(KiviPackParams p) {
+    const int levels = (1 << p.bits) - 1;
+    const int per_byte = 8 / p.bits;
+    const int bytes = p.head_dim / per_byte;
+    const int groups = p.max_tokens / p.group;
+    const int64_t total = static_cast<int64_t>(p.batch) * p.heads * groups * bytes;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int j = static_cast<int>(i % bytes);
+        const int gi = static_cast<int>((i / bytes) % groups);
+        const int h = static_cast<int>((i / (static_cast<int64_t>(bytes) * groups)) % p.heads);
+        const int b = static_cast<int>(i / (static_cast<int64_t>(bytes) * groups * p.heads));
+        const int s0 = p.from[b] + gi * p.group;
+        if (s0 < 0 || s0 + p.group > min(p.to[b], p.slots)) continue;
+        const int64_t base = b * p.ss_b + h * p.ss_h;
+        auto at = [&](int s, int d) {
+            const int slot = p.src_ring > 0 ? s % p.src_ring : s;
+            return base + static_cast<int64_t>(slot) * p.ss_s + d;
+        };
+        Quant q[4];
+        for (int c = 0; c < per_byte; ++c) {
+            const int d = j * per_byte + c;
+            float lo = load_value(p.src, at(s0, d), p.format), hi = lo;
+            for (int e = 1; e < p.group; ++e) {
+                const float x = load_value(p.src, at(s0 + e, d), p.format);
+                lo = __builtin_elementwise_minimum(lo, x);
+                hi = __builtin_elementwise_maximum(hi, x);
+            }
+            q[c] = make_quant(lo, hi, levels, p.overflow);
+            const int64_t so = b * p.sz_b + h * p.sz_h + static_cast<int64_t>(s0 / p.group) * p.sz_s + d;
+            p.scale[so] = half_bits(q[c].scale);
+            p.zero[so] = half_bits(q[c].low);
+        }
+        uint8_t* crow = p.codes + b * p.sc_b + h * p.sc_h + j;
+        for (int e = 0; e < p.group; ++e) {
+            uint32_t byte = 0;
+            for (int c = 0; c < per_byte; ++c) {
+                const int64_t o = at(s0 + e, j * per_byte + c);
+                const float x = load_value(p.src, o, p.format);
+                byte |= code_of(x, q[c], levels) << (c * p.bits);
+                if (p.write_back) store_value(p.src, o, p.format, dequantized(code_or_nan(x, q[c], levels), q[c]));
+            }
+            crow[static_cast<int64_t>(s0 + e) * p.sc_s] = static_cast<uint8_t>(byte);
+        }
+    }
+}
+
+// Values into the packed record: a thread per (b, h, token after from[b]), its groups in order, the code bytes
+// assembled across group boundaries.
+__global__ __launch_bounds__(256) void kivi_pack_values_kernel(KiviPackParams p) {
+    const int levels = (1 << p.bits) - 1;
+    const int per_byte = 8 / p.bits;
+    const int64_t total = static_cast<int64_t>(p.batch) * p.heads * p.max_tokens;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int ti = static_cast<int>(i % p.max_tokens);
+        const int h = static_cast<int>((i / p.max_tokens) % p.heads);
+        const int b = static_cast<int>(i / (static_cast<int64_t>(p.max_tokens) * p.heads));
+        const int s = p.from[b] + ti;
+        if (s < 0 || s >= min(p.to[b], p.slots)) continue;
+        const int slot = p.src_ring > 0 ? s % p.src_ring : s;
+        const int64_t row = b * p.ss_b + h * p.ss_h + static_cast<int64_t>(slot) * p.ss_s;
+        uint8_t* crow = p.codes + b * p.sc_b + h * p.sc_h + static_cast<int64_t>(s) * p.sc_s;
+        const int64_t srow = b * p.sz_b + h * p.sz_h + static_cast<int64_t>(s) * p.sz_s;
+        uint32_t byte = 0;
+        for (int g0 = 0; g0 < p.head_dim; g0 += p.group) {
+            float lo = load_value(p.src, row + g0, p.format), hi = lo;
+            for (int e = 1; e < p.group; ++e) {
+                const float x = load_value(p.src, row + g0 + e, p.format);
+                lo = __builtin_elementwise_minimum(lo, x);
+                hi = __builtin_elementwise_maximum(hi, x);
+            }
+            const Quant q = make_quant(lo, hi, levels, p.overflow);
+            p.scale[srow + g0 / p.group] = half_bits(q.scale);
+            p.zero[srow + g0 / p.group] = half_bits(q.low);
+            for (int e = 0; e < p.group; ++e) {
+                const int d = g0 + e;
+                const float x = load_value(p.src, row + d, p.format);
+                byte |= code_of(x, q, levels) << ((d % per_byte) * p.bits);
+                if (d % per_byte == per_byte - 1) {
+                    crow[d / per_byte] = static_cast<uint8_t>(byte);
+                    byte = 0;
+                }
+                if (p.write_back) store_value(p.src, row + d, p.format, dequantized(code_or_nan(x, q, levels), q));
+            }
+        }
+    }
+}
+
 }  // namespace
+
+int kivi_pack_quantize(const KiviPackParams& p, hipStream_t stream) {
+    const int64_t items = static_cast<int64_t>(p.batch) * p.heads *
+                          (p.keys ? (p.max_tokens / p.group) * (p.head_dim * p.bits / 8) : p.max_tokens);
+    if (items == 0) return 0;
+    const int blocks = static_cast<int>((items + 255) / 256 < 65535 ? (items + 255) / 256 : 65535);
+    if (p.keys)
+        hipLaunchKernelGGL(kivi_pack_keys_kernel, dim3(blocks), dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(kivi_pack_values_kernel, dim3(blocks), dim3(256), 0, stream, p);
+    return check_launch(p.keys ? "kivi_pack_keys_kernel" : "kivi_pack_values_kernel");
+}
 
 int kivi_fake_quantize(const KiviFakeParams& p, hipStream_t stream) {
     const int tokens = p.stop - p.start;

@@ -15,7 +15,9 @@ for the techniques of this path:
   boundary (the tokens a pass commits are quantized when it ends, kivi.py:191-243), attention on the fused KIVI
   kernel over codes and ring (kv_kivi_fused/fused.py:152-208). Configurations the paged KIVI cache cannot hold
   (8-bit codes, groups other than 32, other head dims or dtypes) use the simulated storage
-  (:class:`SimulatedKIVILayer`: dense buffers quantized in place, kivi.py:178-275).
+  (:class:`SimulatedKIVILayer`: dense buffers quantized in place, kivi.py:178-275); for ``FusedKIVIConfig`` the
+  buffers also carry the reference's packed codes, which the kernel reads (:class:`FusedKIVIDenseLayer`,
+  kv_kivi_fused/fused.py:104-250).
 * ``QuestConfig``: on a bf16 model of head dim 64 / 128 / 256 a paged bf16 cache whose page bounds live on the
   device (:class:`~economize_amd.quest.QuestState`: the append of a pass also computes the bounds of the pages
   committed before it, one launch); on other models dense buffers of the model's dtype (:class:`DenseQuestLayer`,
@@ -45,12 +47,11 @@ from .kivi import KIVI_PAGE, PagedKIVICache, kivi_append, kivi_commit, kivi_fake
 from .packed import attach_packed, stand_in
 from .paged import PAGE, PagedKVCache, paged_append
 from .quest import QuestPages, QuestState, bounds_dtype, page_bounds
-from .techniques import (FP8KVConfig, FusedFP8KVConfig, KIVIConfig, QuestConfig, Technique, attn_implementation,
-                         head_dim_of,
-                         technique_for)
+from .techniques import (FP8KVConfig, FusedFP8KVConfig, FusedKIVIConfig, KIVIConfig, QuestConfig, Technique,
+                         attn_implementation, head_dim_of, technique_for)
 
-__all__ = ["DenseFP8Layer", "DenseQuestLayer", "EconomizeCache", "EconomizedModel", "KIVILayer", "PagedLayer",
-           "SimulatedKIVILayer", "apply"]
+__all__ = ["DenseFP8Layer", "DenseQuestLayer", "EconomizeCache", "EconomizedModel", "FusedKIVIDenseLayer", "KIVILayer",
+           "PagedLayer", "SimulatedKIVILayer", "apply"]
 
 
 class _PagedBase(CacheLayerMixin):
@@ -645,6 +646,69 @@ class SimulatedKIVILayer(CacheLayerMixin):
         self.length = self.committed = self.kq = self.vq = 0
 
 
+class FusedKIVIDenseLayer(SimulatedKIVILayer):
+    """``FusedKIVIConfig`` where the paged KIVI cache cannot hold the layer (the reference's ``FusedKIVICache``,
+    kv_kivi_fused/fused.py:104-250): the simulated storage's dense buffers, plus the codes, fp16 scales and zero
+    points of every quantized entry in the reference's ``KIVIPacked`` layout (:class:`~economize_amd.kivi_packed.
+    KIVIPackedStore`). A pass boundary quantizes the committed entries once, writing the codes and the dequantized
+    values into the buffers (``eco_kivi_pack_quantize``); attention gets the buffers with the record attached, and the
+    kernel reads the quantized prefix as codes (``eco_kivi_packed_decode``), the rest from the buffers. A scale or
+    zero point beyond fp16 stops the attachment for the rest of the generation (its fp16 copy would not give the
+    buffer's values), as the reference stops it (fused.py:132-141); attention then reads the buffers."""
+
+    def __init__(self, capacity: int, config: KIVIConfig) -> None:
+        super().__init__(capacity, config)
+        self.store = None
+        self.packable = True
+
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        from .kivi_packed import KIVIPackedStore
+
+        super().lazy_initialization(key_states, value_states)
+        batch, heads, _, dim = key_states.shape
+        c = self.config
+        self.store = KIVIPackedStore(batch, heads, self.capacity, dim, value_states.shape[3], c.bits, c.group_size,
+                                     key_states.device)
+
+    def pass_begin(self, frontier: int) -> None:
+        """Quantize what the schedule quantizes once ``frontier`` tokens are committed (kivi.py:230-243), into the
+        record and the buffers."""
+        c = self.config
+        k_to = max(self.kq, (frontier // c.residual_length) * c.residual_length)
+        v_to = max(self.vq, frontier - c.residual_length)
+        store = self.store
+        batch = self.buffers[0].shape[0]
+        device = self.buffers[0].device
+
+        def rows(x: int) -> torch.Tensor:
+            return torch.full((batch,), x, dtype=torch.int32, device=device)
+
+        if k_to > self.kq:
+            store.quantize(self.buffers[0], "k", rows(self.kq), rows(k_to), k_to - self.kq, write_back=True)
+            store.keys_quantized.fill_(k_to)
+        if v_to > self.vq:
+            store.quantize(self.buffers[1], "v", rows(self.vq), rows(v_to), v_to - self.vq, write_back=True)
+            store.values_quantized.fill_(v_to)
+        if (k_to > self.kq or v_to > self.vq) and self.packable and int(store.overflow.item()):
+            self.packable = False
+        self.kq, self.vq, self.committed = k_to, v_to, frontier
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs
+               ) -> tuple[torch.Tensor, torch.Tensor]:
+        keys, values = super().update(key_states, value_states, *args, **kwargs)
+        if not self.packable or (self.kq == 0 and self.vq == 0):
+            return keys, values
+        return attach_packed(keys, self.store.record(self.length)), values
+
+    def reset(self) -> None:
+        super().reset()
+        self.packable = True
+        if self.store is not None:
+            self.store.keys_quantized.zero_()
+            self.store.values_quantized.zero_()
+            self.store.overflow.zero_()
+
+
 class EconomizeCache(Cache):
     """transformers ``past_key_values`` whose layers are the techniques' paged caches (dense ``DynamicLayer`` for a
     layer no technique covers)."""
@@ -722,7 +786,9 @@ class EconomizedModel:
                 layers.append(PagedLayer(max_length, fp8, quest, scales=self.scales.get(index), layer=index,
                                          static=True))
                 continue
-            if isinstance(cfg, KIVIConfig) and cfg.simulated(self.model):
+            if isinstance(cfg, FusedKIVIConfig) and cfg.simulated(self.model):
+                layers.append(FusedKIVIDenseLayer(max_length, cfg))
+            elif isinstance(cfg, KIVIConfig) and cfg.simulated(self.model):
                 layers.append(SimulatedKIVILayer(max_length, cfg))
             elif isinstance(cfg, KIVIConfig):
                 layers.append(KIVILayer(max_length, cfg))

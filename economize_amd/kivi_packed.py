@@ -25,7 +25,7 @@ from . import _lib
 from .decode import DOT_DTYPES, _channel_contiguous, _workspace, mask_operand, sinks_operand
 from .errors import ConfigError
 
-__all__ = ["KIVIPacked", "kivi_decode_attention"]
+__all__ = ["KIVIPacked", "KIVIPackedStore", "kivi_decode_attention"]
 
 
 @dataclass
@@ -188,3 +188,78 @@ def kivi_decode_attention(query: torch.Tensor, key: torch.Tensor, value: torch.T
         ws.data_ptr(), ws.numel(), _lib.stream_of(device),
     )
     return out
+
+
+class KIVIPackedStore:
+    """The codes, fp16 scales and zero points of one layer in the :class:`KIVIPacked` layout, for ``slots`` slots
+    per row (the reference's ``_LayerStore``, techniques/kv_kivi_fused/fused.py:58-78), with the rows' quantized
+    counts on the device and an overflow flag (a scale or zero point beyond fp16).
+
+    Args:
+        batch, heads, slots: Rows, KV heads and slots per row.
+        head_dim, value_dim: Channels of keys and values (each packing into whole bytes at ``bits``).
+        bits: 2, 4 or 8.
+        group: Tokens per key group; channels per value group (the whole value head when it does not divide it,
+            ``value_group`` of techniques/kv_quant/kivi.py:143-154).
+    """
+
+    def __init__(self, batch: int, heads: int, slots: int, head_dim: int, value_dim: int, bits: int, group: int,
+                 device: torch.device) -> None:
+        if bits not in (2, 4, 8):
+            raise ConfigError(f"KIVI codes have 2, 4 or 8 bits, not {bits}")
+        per_byte = 8 // bits
+        for name, d in (("key", head_dim), ("value", value_dim)):
+            if d % per_byte:
+                raise ConfigError(f"the {name} head dim {d} does not pack into whole bytes at {bits} bits")
+        self.bits, self.key_group = bits, group
+        self.value_group = group if value_dim % group == 0 else value_dim
+        self.slots = slots
+        u8, f16 = torch.uint8, torch.float16
+        self.key_codes = torch.zeros(batch, heads, slots, head_dim // per_byte, dtype=u8, device=device)
+        self.key_scale = torch.zeros(batch, heads, -(-slots // group), head_dim, dtype=f16, device=device)
+        self.key_zero = torch.zeros_like(self.key_scale)
+        self.value_codes = torch.zeros(batch, heads, slots, value_dim // per_byte, dtype=u8, device=device)
+        self.value_scale = torch.zeros(batch, heads, slots, value_dim // self.value_group, dtype=f16, device=device)
+        self.value_zero = torch.zeros_like(self.value_scale)
+        self.keys_quantized = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.values_quantized = torch.zeros(batch, dtype=torch.int32, device=device)
+        self.overflow = torch.zeros(1, dtype=torch.int32, device=device)
+
+    def quantize(self, source: torch.Tensor, kind: str, start: torch.Tensor, stop: torch.Tensor, max_tokens: int,
+                 write_back: bool = False, ring: int = 0) -> None:
+        """Quantize slots ``[start[b], stop[b])`` of every row of ``source`` ``[B, H, *, D]`` (bf16, fp16 or fp32,
+        slot ``s`` at ``s % ring`` with a ring) into the record: ``kind`` ``"k"`` per channel over key groups (start
+        and stop multiples of the group), ``"v"`` per token over value groups. ``write_back`` replaces the source's
+        elements by their dequantized values (the dense buffers of the reference's fused cache). ``max_tokens``
+        bounds ``stop - start`` over the rows."""
+        if kind not in ("k", "v"):
+            raise ConfigError(f"kind must be 'k' or 'v', not {kind!r}")
+        if source.dim() != 4 or source.stride(-1) != 1:
+            raise ConfigError("the source must be [B, H, slots, D] with a contiguous last axis")
+        codes = self.key_codes if kind == "k" else self.value_codes
+        scale, zero = (self.key_scale, self.key_zero) if kind == "k" else (self.value_scale, self.value_zero)
+        group = self.key_group if kind == "k" else self.value_group
+        batch, heads, _, dim = source.shape
+        device = _lib.require_gpu(source, start, stop)
+        start = start.to(torch.int32).contiguous()
+        stop = stop.to(torch.int32).contiguous()
+        _lib.call(
+            "eco_kivi_pack_quantize", 0 if kind == "k" else 1, source.data_ptr(), _lib.fmt(source.dtype),
+            source.stride(0), source.stride(1), source.stride(2), int(ring), int(write_back), codes.data_ptr(),
+            codes.stride(0), codes.stride(1), codes.stride(2), scale.data_ptr(), zero.data_ptr(), scale.stride(0),
+            scale.stride(1), scale.stride(2), start.data_ptr(), stop.data_ptr(), batch, heads, self.slots, dim,
+            self.bits, group, int(max_tokens), self.overflow.data_ptr(), _lib.stream_of(device),
+        )
+
+    def record(self, length: int, key_ring: torch.Tensor | None = None, value_ring: torch.Tensor | None = None,
+               ring: int = 0, materialize=None) -> KIVIPacked:
+        """The :class:`KIVIPacked` view of the first ``length`` slots (views of the store, no copy)."""
+        g = self.key_group
+        return KIVIPacked(
+            bits=self.bits, key_group=g, value_group=self.value_group,
+            key_codes=self.key_codes[:, :, :length], key_scale=self.key_scale[:, :, : -(-length // g)],
+            key_zero=self.key_zero[:, :, : -(-length // g)], value_codes=self.value_codes[:, :, :length],
+            value_scale=self.value_scale[:, :, :length], value_zero=self.value_zero[:, :, :length],
+            keys_quantized=self.keys_quantized, values_quantized=self.values_quantized, key_ring=key_ring,
+            value_ring=value_ring, ring=ring, materialize=materialize,
+        )

@@ -327,6 +327,25 @@ int eco_kivi_fake_quantize(void* buffer, int32_t format, int64_t sb, int64_t sh,
                            int32_t heads, int32_t slots, int32_t head_dim, int32_t start, int32_t stop, int32_t bits,
                            int32_t group, int32_t keys, void* stream);
 
+/* KIVI's packed record (the reference's KIVIPacked layout, attention/kivi.py:80-132) written from a dense buffer or a
+ * ring: for every row b, slots [from[b], to[b]) (int32 [B] on the device, clamped to [0, slots); keys: multiples of
+ * group) of src [B, H, *, D] (element strides ss_*, channel stride 1; bf16, fp16 or fp32; slot s at s % src_ring when
+ * src_ring > 0) are quantized as the reference's quantize (techniques/kv_quant/kivi.py:121-140): keys (kind 0) per
+ * channel over groups of `group` tokens, values (kind 1) per token over groups of `group` channels (group dividing
+ * D). Codes go to codes [B, H, slots, D * bits / 8] (byte strides sc_*; packed as pack_codes, attention/kivi.py:
+ * 38-45), fp16 scales and zero points to scale / zero (element strides sz_*; keys [B, H, ceil(slots / group), D] at
+ * row s / group, values [B, H, slots, D / group]). write_back (not with a ring): every source element is replaced by
+ * code * scale + low in fp32 rounded to its format, the dense values of the reference's fused cache. max_tokens bounds
+ * to - from over the rows (it sizes the launch; keys: a multiple of group). *overflow (optional) is set to 1 when a
+ * scale or zero point lies beyond fp16 (its fp16 copy is then not the value the codes were made with). Replaces
+ * FusedKIVICache._quantize_block and PackedKIVICache._pack_block (techniques/kv_kivi_fused/fused.py:152-175,
+ * techniques/kv_quant/packed.py:213-230). */
+int eco_kivi_pack_quantize(int32_t kind, void* src, int32_t format, int64_t ss_b, int64_t ss_h, int64_t ss_s,
+                           int32_t src_ring, int32_t write_back, void* codes, int64_t sc_b, int64_t sc_h, int64_t sc_s,
+                           void* scale, void* zero, int64_t sz_b, int64_t sz_h, int64_t sz_s, const int32_t* from,
+                           const int32_t* to, int32_t batch, int32_t heads, int32_t slots, int32_t head_dim,
+                           int32_t bits, int32_t group, int32_t max_tokens, uint32_t* overflow, void* stream);
+
 /* KIVI's cell on vLLM's paged cache (backends/vllm/kivi/layout.py:133-213): for a head size (a power of two, 16 to
  * 256) of a cache dtype of element_size bytes, bits 2 / 4 / 8 and a power-of-two group of at most 128, writes
  * offsets[10] = {value group, key aux slots, off_v, off_vs, off_vz, off_ka, off_kc, off_vc, off_flag, cell bytes}. */

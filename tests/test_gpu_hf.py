@@ -287,10 +287,12 @@ LOGIT_TOL = 0.5
 
 
 @pytest.mark.parametrize("technique", ["fp8", "kivi2", "kivi4", "quest", "quest_fp16", "quest_fp32", "fp8_d512",
-                                       "kivi2_d512", "quest_d512"])
+                                       "kivi2_d512", "quest_d512", "kivi8_fp16", "kivi4_g16"])
 def test_decoding_logits_match_sdpa_over_the_cache(technique: str) -> None:
-    """Heads of 512 channels (``_d512``) run on the dense kernel's two value slices: dense fp8 buffers, KIVI's
-    simulated storage and Quest over dense buffers."""
+    """Heads of 512 channels (``_d512``) run on the dense kernel's two value slices: dense fp8 buffers, KIVI codes in
+    the reference's dense layout and Quest over dense buffers. ``kivi8_fp16`` (8-bit codes on an fp16 model) and
+    ``kivi4_g16`` (groups of 16) are configurations the paged KIVI cache does not hold: the codes beside dense
+    buffers, read by the kernel."""
     from transformers import AttentionInterface
     from transformers.masking_utils import AttentionMaskInterface
 
@@ -299,22 +301,23 @@ def test_decoding_logits_match_sdpa_over_the_cache(technique: str) -> None:
     attn, path, dtype = "sdpa", "kernel_fp8", torch.bfloat16
     head_dim = 512 if technique.endswith("_d512") else 64
     technique = technique.removesuffix("_d512")
-    if technique == "quest_fp16":
+    if technique in ("quest_fp16", "kivi8_fp16"):
         dtype = torch.float16
     elif technique == "quest_fp32":
         dtype = torch.float32
     if technique == "fp8":
         configs = (FusedFP8KVConfig(),)
     elif technique.startswith("kivi"):
-        configs = (FusedKIVIConfig(bits=int(technique[-1]), residual_length=32, headroom=64),)
+        group = 16 if technique.endswith("_g16") else 32
+        configs = (FusedKIVIConfig(bits=int(technique[4]), group_size=group, residual_length=32, headroom=64),)
         path = "kernel_kivi"
     else:
         configs = (QuestConfig(page_size=16, token_budget=64, dense_layers=1),)
         attn, path = "quest_oracle", "kernel_quest"
         AttentionInterface.register("quest_oracle", quest_oracle_forward)
         AttentionMaskInterface.register("quest_oracle", AttentionMaskInterface._global_mapping["sdpa"])
-    if head_dim == 512 and not technique.startswith("quest"):
-        path = "kernel"  # dense fp8 buffers / KIVI's simulated storage
+    if head_dim == 512 and technique == "fp8":
+        path = "kernel"  # dense fp8 buffers
     deltas, gaps, paths, checked = mirrored_decode(configs, attn, dtype, head_dim)
     print(technique, head_dim, "max delta", max(deltas), "deltas", [round(d, 4) for d in deltas])
     assert (path, 1) in paths and ("sdpa", PROMPT) in paths
@@ -457,6 +460,28 @@ def test_the_hip_path_decodes_the_reference_kivi_golden_tokens() -> None:
     assert golden_greedy(model, cache, "cuda") == golden.GOLDEN["kv_kivi_2bit_tokens"].tolist()
     assert {(r["path"], r["queries"]) for r in kernel_usage(reset=True)} >= {("kernel", 1)}
     assert (cache.layers[0].kq, cache.layers[0].vq) == (32, 31)  # 39 committed tokens before the last pass
+
+
+def test_the_reference_kivi_golden_tokens_through_the_codes() -> None:
+    """The same golden case as ``FusedKIVIConfig``: the layers keep the reference's packed codes beside the dense
+    buffers (:class:`FusedKIVIDenseLayer`) and every decoding step's kernel reads the quantized prefix through the
+    codes (``eco_kivi_packed_decode``); the tokens are the reference's ``kv_kivi_2bit`` ones."""
+    import test_golden_reference as golden
+
+    from economize_amd.attention import kernel_usage
+    from economize_amd.hf import FusedKIVIDenseLayer, apply
+    from economize_amd.techniques import FusedKIVIConfig
+
+    model = golden.golden_model().cuda()
+    em = apply(model, FusedKIVIConfig(bits=2, group_size=4, residual_length=8))
+    cache = em.make_cache(golden.PROMPT + golden.NEW_TOKENS + 1)
+    assert all(isinstance(layer, FusedKIVIDenseLayer) for layer in cache.layers)
+    kernel_usage(reset=True)
+    assert golden_greedy(model, cache, "cuda") == golden.GOLDEN["kv_kivi_2bit_tokens"].tolist()
+    assert {(r["path"], r["queries"]) for r in kernel_usage(reset=True)} >= {("kernel_kivi", 1)}
+    layer = cache.layers[0]
+    assert (layer.kq, layer.vq) == (32, 31) and layer.packable
+    assert layer.store.keys_quantized.tolist() == [32] and layer.store.values_quantized.tolist() == [31]
 
 
 def test_the_hip_path_decodes_the_reference_quest_golden_tokens() -> None:

@@ -213,3 +213,85 @@ def test_refusals() -> None:
     bad = type(packed)(**{**packed.__dict__, "ring": 16})
     with pytest.raises(ConfigError, match="key_ring"):
         kivi_decode_attention(query, k, k, None, 0.125, bad)
+
+
+# ---- the packed record written by the GPU (eco_kivi_pack_quantize) ------------------------------------------------
+
+PACK_CASES = [
+    # bits, dtype, head dim, group
+    (2, torch.bfloat16, 128, 32),
+    (4, torch.bfloat16, 64, 16),
+    (8, torch.float16, 64, 32),
+    (2, torch.float16, 48, 24),
+    (4, torch.float32, 64, 128),
+    (8, torch.float32, 48, 12),
+    (2, torch.bfloat16, 64, 4),
+]
+
+
+@pytest.mark.parametrize("case", PACK_CASES, ids=[f"b{c[0]}-{str(c[1])[6:]}-d{c[2]}-g{c[3]}" for c in PACK_CASES])
+@pytest.mark.parametrize("ring", [0, 1])
+def test_pack_quantize_matches_the_oracle(case, ring) -> None:
+    """Codes, fp16 scales and zero points bit-exact with the oracle's quantize + pack_codes (the reference's
+    FusedKIVICache._quantize_block layout), per-row ranges, from a dense buffer written back with the dequantized
+    values, or from a ring (slot s at s % ring) left as it was."""
+    from economize_amd.kivi_packed import KIVIPackedStore
+
+    bits, dtype, d, group = case
+    batch, heads = 2, 2
+    slots = 3 * max(group, 32)
+    gen = torch.Generator().manual_seed(bits * 100 + d + group)
+    data = torch.randn(batch, heads, slots, d, generator=gen) * 3
+    data[..., 1] += 15
+    data = data.to(dtype)
+    vg = group if d % group == 0 else d
+    kstart, kstop = [0, group], [2 * group, 3 * group]
+    vstart, vstop = [5, 0], [slots - 3, slots - 40]
+    store = KIVIPackedStore(batch, heads, slots, d, d, bits, group, "cuda")
+    width = 2 * max(group, 32) + 8  # ring slots: more than the longest key range
+    if ring:  # a ring of `width` slots that holds each range's slots (and later ones) at s % width
+        src_k = torch.full((batch, heads, width, d), float("nan"), dtype=dtype)
+        src_v = src_k.clone()
+        for b in range(batch):
+            for s in range(kstart[b], kstop[b]):
+                src_k[b, :, s % width] = data[b, :, s]
+        src_k, src_v = src_k.cuda(), src_v.cuda()
+    else:
+        src_k, src_v = data.clone().cuda(), data.clone().cuda()
+    rows = lambda x: torch.tensor(x, dtype=torch.int32, device="cuda")  # noqa: E731
+    store.quantize(src_k, "k", rows(kstart), rows(kstop), 2 * group, write_back=not ring, ring=width if ring else 0)
+    if not ring:
+        store.quantize(src_v, "v", rows(vstart), rows(vstop), slots, write_back=True)
+    torch.cuda.synchronize()
+    assert int(store.overflow.item()) == 0
+    f = data.float().numpy()
+    for b in range(batch):
+        pk, ks, kz, kd = okivi.quantize_keys(f[b:b + 1], kstart[b], kstop[b], bits, group)
+        g0, g1 = kstart[b] // group, kstop[b] // group
+        np.testing.assert_array_equal(store.key_codes[b, :, kstart[b]:kstop[b]].cpu().numpy(), pk[0])
+        np.testing.assert_array_equal(store.key_scale[b, :, g0:g1].cpu().numpy(), ks[0].astype(np.float16))
+        np.testing.assert_array_equal(store.key_zero[b, :, g0:g1].cpu().numpy(), kz[0].astype(np.float16))
+        if not ring:
+            got = src_k[b, :, kstart[b]:kstop[b]].cpu()
+            assert torch.equal(got, torch.from_numpy(kd[0]).to(dtype))
+            assert torch.equal(src_k[b, :, kstop[b]:].cpu(), data[b, :, kstop[b]:])  # untouched
+            pv, vs, vz, vd = okivi.quantize_values(f[b:b + 1], vstart[b], vstop[b], bits, group)
+            np.testing.assert_array_equal(store.value_codes[b, :, vstart[b]:vstop[b]].cpu().numpy(), pv[0])
+            np.testing.assert_array_equal(store.value_scale[b, :, vstart[b]:vstop[b]].cpu().numpy(),
+                                          vs[0].astype(np.float16))
+            np.testing.assert_array_equal(store.value_zero[b, :, vstart[b]:vstop[b]].cpu().numpy(),
+                                          vz[0].astype(np.float16))
+            assert store.value_scale.shape[3] == d // vg
+            assert torch.equal(src_v[b, :, vstart[b]:vstop[b]].cpu(), torch.from_numpy(vd[0]).to(dtype))
+            assert torch.equal(src_v[b, :, :vstart[b]].cpu(), data[b, :, :vstart[b]])
+
+
+def test_pack_quantize_flags_scales_beyond_fp16() -> None:
+    from economize_amd.kivi_packed import KIVIPackedStore
+
+    data = torch.zeros(1, 1, 32, 64)
+    data[0, 0, 0, 5] = 2e6  # a key group whose scale (2e6 / 3) lies beyond fp16
+    store = KIVIPackedStore(1, 1, 32, 64, 64, 2, 32, "cuda")
+    rows = lambda x: torch.tensor([x], dtype=torch.int32, device="cuda")  # noqa: E731
+    store.quantize(data.cuda(), "k", rows(0), rows(32), 32)
+    assert int(store.overflow.item()) == 1

@@ -124,7 +124,8 @@ def test_a_cpu_call_falls_back_to_sdpa_and_is_logged() -> None:
 
 def test_kivi_layers_are_paged_where_the_paged_cache_holds_them() -> None:
     """2- and 4-bit codes in groups of 32 on a bf16 model of head dim 64 / 128 live in the paged KIVI cache; 8-bit
-    codes, other groups, head dims and dtypes, and storage='simulated' get the simulated storage (kivi.py:62-66)."""
+    codes, other groups, head dims and dtypes, and storage='simulated' get the simulated storage (kivi.py:62-66),
+    with the reference's packed codes beside its buffers for FusedKIVIConfig (kv_kivi_fused/fused.py:104-250)."""
     from economize_amd.hf import apply
 
     def layer_type(model, config) -> str:
@@ -136,9 +137,9 @@ def test_kivi_layers_are_paged_where_the_paged_cache_holds_them() -> None:
     assert layer_type(tiny_model().to(torch.bfloat16), KIVIConfig(storage="simulated")) == "SimulatedKIVILayer"
     assert layer_type(tiny_model().to(torch.bfloat16), KIVIConfig(bits=8)) == "SimulatedKIVILayer"
     assert layer_type(tiny_model().to(torch.bfloat16), FusedKIVIConfig(group_size=16, residual_length=32)) == \
-        "SimulatedKIVILayer"
+        "FusedKIVIDenseLayer"
     assert layer_type(tiny_model(head_dim=16).to(torch.bfloat16), KIVIConfig()) == "SimulatedKIVILayer"
-    assert layer_type(tiny_model(), FusedKIVIConfig()) == "SimulatedKIVILayer"  # float32
+    assert layer_type(tiny_model(), FusedKIVIConfig()) == "FusedKIVIDenseLayer"  # float32
 
 
 def test_quest_layers_are_paged_where_the_paged_kernels_take_the_model() -> None:
