@@ -64,6 +64,8 @@ SIGNATURES: dict[str, tuple[type | None, list]] = {
     "eco_kivi_fake_quantize": (c_int32, [_P, _I, _L, _L, _L, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P]),
     "eco_kivi_pack_quantize": (c_int32, [_I, _P, _I, _L, _L, _L, _I, _I, _P, _L, _L, _L, _P, _P, _L, _L, _L, _P, _P,
                                          _I, _I, _I, _I, _I, _I, _I, _P, _P]),
+    "eco_kivi_packed_gather": (c_int32, [_I, _P, _L, _L, _L, _P, _P, _L, _L, _L, _P, _P, _L, _L, _L, _I, _P, _I, _L, _L,
+                                         _L, _I, _I, _I, _I, _I, _I, _P]),
     "eco_kivi_cells_layout": (c_int32, [_I, _I, _I, _I, _P]),
     "eco_kivi_cells_quantize": (c_int32, [_P, _I, _L, _L, _L, _I, _I, _I, _P, _L, _I, _P, _P, _P, _I, _I, _I, _I, _I,
                                           _P, _P]),

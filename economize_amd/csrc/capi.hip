@@ -1026,6 +1026,52 @@ int eco_kivi_pack_quantize(int32_t kind, void* src, int32_t format, int64_t ss_b
     return kivi_pack_quantize(p, static_cast<hipStream_t>(stream));
 }
 
+int eco_kivi_packed_gather(int32_t kind, const uint8_t* codes, int64_t sc_b, int64_t sc_h, int64_t sc_s,
+                           const void* scale, const void* zero, int64_t sz_b, int64_t sz_h, int64_t sz_s,
+                           const int32_t* quantized, const void* ring, int64_t sr_b, int64_t sr_h, int64_t sr_s,
+                           int32_t ring_slots, void* out, int32_t format, int64_t so_b, int64_t so_h, int64_t so_s,
+                           int32_t batch, int32_t heads, int32_t slots, int32_t head_dim, int32_t bits, int32_t group,
+                           void* stream) {
+    if (!codes || !scale || !zero || !quantized || !ring || !out) return fail("kivi gather: null pointer");
+    if (format != BF16 && format != FP16 && format != FP32)
+        return fail("kivi gather: the ring and the output must be bf16, fp16 or fp32");
+    if (bits != 2 && bits != 4 && bits != 8) return fail("kivi gather: bits must be 2, 4 or 8");
+    if (kind != 0 && kind != 1) return fail("kivi gather: kind must be 0 (keys) or 1 (values)");
+    if (batch < 0 || heads < 0 || slots < 0 || head_dim <= 0 || group <= 0 || ring_slots < 0)
+        return fail("kivi gather: bad shape, group or ring");
+    if (head_dim % (8 / bits) || (kind == 1 && head_dim % group))
+        return fail("kivi gather: the head dim must pack into bytes (and hold whole value groups)");
+    KiviRecordGatherParams p{};
+    p.codes = codes;
+    p.sc_b = sc_b;
+    p.sc_h = sc_h;
+    p.sc_s = sc_s;
+    p.scale = static_cast<const uint16_t*>(scale);
+    p.zero = static_cast<const uint16_t*>(zero);
+    p.sz_b = sz_b;
+    p.sz_h = sz_h;
+    p.sz_s = sz_s;
+    p.quantized = quantized;
+    p.ring = ring;
+    p.sr_b = sr_b;
+    p.sr_h = sr_h;
+    p.sr_s = sr_s;
+    p.ring_slots = ring_slots;
+    p.out = out;
+    p.format = format;
+    p.so_b = so_b;
+    p.so_h = so_h;
+    p.so_s = so_s;
+    p.batch = batch;
+    p.heads = heads;
+    p.slots = slots;
+    p.head_dim = head_dim;
+    p.bits = bits;
+    p.group = group;
+    p.keys = kind == 0;
+    return kivi_packed_gather(p, static_cast<hipStream_t>(stream));
+}
+
 int eco_kivi_cells_layout(int32_t head_dim, int32_t element_size, int32_t bits, int32_t group, int32_t* offsets) {
     if (!offsets) return fail("kivi cells layout: null output");
     CellLayout L;

@@ -165,7 +165,43 @@ __global__ __launch_bounds__(256) void kivi_pack_values_kernel(KiviPackParams p)
     }
 }
 
+// A thread per output element: its code and its group's scale and zero point, or its ring entry.
+__global__ __launch_bounds__(256) void kivi_packed_gather_kernel(KiviRecordGatherParams p) {
+    const int per_byte = 8 / p.bits;
+    const int64_t total = static_cast<int64_t>(p.batch) * p.heads * p.slots * p.head_dim;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int d = static_cast<int>(i % p.head_dim);
+        const int s = static_cast<int>((i / p.head_dim) % p.slots);
+        const int h = static_cast<int>((i / (static_cast<int64_t>(p.head_dim) * p.slots)) % p.heads);
+        const int b = static_cast<int>(i / (static_cast<int64_t>(p.head_dim) * p.slots * p.heads));
+        float x;
+        if (s < p.quantized[b]) {
+            const uint32_t byte = p.codes[b * p.sc_b + h * p.sc_h + static_cast<int64_t>(s) * p.sc_s + d / per_byte];
+            const float code = static_cast<float>((byte >> ((d % per_byte) * p.bits)) & ((1u << p.bits) - 1u));
+            const int64_t so = b * p.sz_b + h * p.sz_h +
+                               (p.keys ? static_cast<int64_t>(s / p.group) * p.sz_s + d
+                                       : static_cast<int64_t>(s) * p.sz_s + d / p.group);
+            const float sc = static_cast<float>(__builtin_bit_cast(_Float16, p.scale[so]));
+            const float zr = static_cast<float>(__builtin_bit_cast(_Float16, p.zero[so]));
+            x = __fadd_rn(__fmul_rn(code, sc), zr);
+        } else {
+            const int slot = p.ring_slots > 0 ? s % p.ring_slots : s;
+            x = load_value(p.ring, b * p.sr_b + h * p.sr_h + static_cast<int64_t>(slot) * p.sr_s + d, p.format);
+        }
+        store_value(p.out, b * p.so_b + h * p.so_h + static_cast<int64_t>(s) * p.so_s + d, p.format, x);
+    }
+}
+
 }  // namespace
+
+int kivi_packed_gather(const KiviRecordGatherParams& p, hipStream_t stream) {
+    const int64_t items = static_cast<int64_t>(p.batch) * p.heads * p.slots * p.head_dim;
+    if (items == 0) return 0;
+    const int blocks = static_cast<int>((items + 255) / 256 < 65535 ? (items + 255) / 256 : 65535);
+    hipLaunchKernelGGL(kivi_packed_gather_kernel, dim3(blocks), dim3(256), 0, stream, p);
+    return check_launch("kivi_packed_gather_kernel");
+}
 
 int kivi_pack_quantize(const KiviPackParams& p, hipStream_t stream) {
     const int64_t items = static_cast<int64_t>(p.batch) * p.heads *

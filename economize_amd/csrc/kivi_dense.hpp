@@ -43,4 +43,25 @@ struct KiviPackParams {
 
 int kivi_pack_quantize(const KiviPackParams& p, hipStream_t stream);
 
+// The dense view of one kind of a packed record: out[b, h, s, d] (s < slots) is code * scale + zero rounded to the
+// output format where s < quantized[b], else the full-precision entry at slot s % ring_slots of `ring` (slot s when
+// ring_slots is 0).
+struct KiviRecordGatherParams {
+    const uint8_t* codes;
+    int64_t sc_b, sc_h, sc_s;
+    const uint16_t* scale;
+    const uint16_t* zero;
+    int64_t sz_b, sz_h, sz_s;
+    const int32_t* quantized;
+    const void* ring;
+    int64_t sr_b, sr_h, sr_s;
+    int ring_slots;
+    void* out;
+    int format;  // of the ring and the output
+    int64_t so_b, so_h, so_s;
+    int batch, heads, slots, head_dim, bits, group, keys;
+};
+
+int kivi_packed_gather(const KiviRecordGatherParams& p, hipStream_t stream);
+
 }  // namespace eco

@@ -14,10 +14,11 @@ for the techniques of this path:
 * ``KIVIConfig`` / ``FusedKIVIConfig``: new tokens in the bf16 ring, the reference's schedule run at every pass
   boundary (the tokens a pass commits are quantized when it ends, kivi.py:191-243), attention on the fused KIVI
   kernel over codes and ring (kv_kivi_fused/fused.py:152-208). Configurations the paged KIVI cache cannot hold
-  (8-bit codes, groups other than 32, other head dims or dtypes) use the simulated storage
-  (:class:`SimulatedKIVILayer`: dense buffers quantized in place, kivi.py:178-275); for ``FusedKIVIConfig`` the
-  buffers also carry the reference's packed codes, which the kernel reads (:class:`FusedKIVIDenseLayer`,
-  kv_kivi_fused/fused.py:104-250).
+  (8-bit codes, groups other than 32, other head dims or dtypes) keep the reference's packed record: codes and rings,
+  no dense buffer (:class:`PackedKIVILayer`, kv_quant/packed.py:1-370), or, for ``FusedKIVIConfig``, codes beside
+  dense buffers of the dequantized values (:class:`FusedKIVIDenseLayer`, kv_kivi_fused/fused.py:104-250); either
+  way the kernel reads the codes. ``storage="simulated"`` keeps dense buffers quantized in place
+  (:class:`SimulatedKIVILayer`, kivi.py:178-275).
 * ``QuestConfig``: on a bf16 model of head dim 64 / 128 / 256 a paged bf16 cache whose page bounds live on the
   device (:class:`~economize_amd.quest.QuestState`: the append of a pass also computes the bounds of the pages
   committed before it, one launch); on other models dense buffers of the model's dtype (:class:`DenseQuestLayer`,
@@ -51,7 +52,7 @@ from .techniques import (FP8KVConfig, FusedFP8KVConfig, FusedKIVIConfig, KIVICon
                          attn_implementation, head_dim_of, technique_for)
 
 __all__ = ["DenseFP8Layer", "DenseQuestLayer", "EconomizeCache", "EconomizedModel", "FusedKIVIDenseLayer", "KIVILayer",
-           "PagedLayer", "SimulatedKIVILayer", "apply"]
+           "PackedKIVILayer", "PagedLayer", "SimulatedKIVILayer", "apply"]
 
 
 class _PagedBase(CacheLayerMixin):
@@ -709,6 +710,149 @@ class FusedKIVIDenseLayer(SimulatedKIVILayer):
             self.store.overflow.zero_()
 
 
+class PackedKIVILayer(CacheLayerMixin):
+    """``KIVIConfig``'s packed storage where the paged KIVI cache cannot hold the layer (the reference's
+    ``PackedKIVICache``, techniques/kv_quant/packed.py:1-370; any bits, group, head dim and dtype): no dense buffer,
+    only the codes, fp16 scales and zero points of the quantized entries (:class:`~economize_amd.kivi_packed.
+    KIVIPackedStore`) and two rings of ``residual_length + headroom`` slots in the model's dtype holding the entries
+    not quantized yet (slot ``s`` at ``s % ring``).
+
+    A pass of at most ``headroom`` tokens writes them to the rings and attends through zero-memory stand-ins carrying
+    the packed record (``eco_kivi_packed_decode`` reads the codes and the rings); what it commits is quantized from
+    the rings when the next pass begins. A longer pass (a prompt) gets a dense copy (``eco_kivi_packed_gather``) with
+    its tokens written in, quantizes what its end commits from that copy and keeps only its last ``ring`` tokens in
+    the rings. Attention paths that do not read codes get the dense copy (``materialize``).
+
+    Raises:
+        ConfigError: A pass would overwrite ring entries not quantized yet (raise ``headroom``), or a scale or zero
+            point lies beyond fp16 (use ``storage="simulated"``), as the reference refuses both (packed.py:175-188).
+    """
+
+    is_sliding = False
+    is_compileable = False
+    supports_early_init = False
+
+    def __init__(self, capacity: int, config: KIVIConfig) -> None:
+        super().__init__()
+        self.capacity = int(capacity)
+        self.config = config
+        self.ring = max(1, min(config.residual_length + config.headroom, self.capacity - 1))
+        self.length = self.committed = self.kq = self.vq = 0
+        self.store = None
+        self.rings: tuple[torch.Tensor, torch.Tensor] | None = None
+
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        from .kivi_packed import KIVIPackedStore
+
+        batch, heads, _, dim = key_states.shape
+        c = self.config
+        self.store = KIVIPackedStore(batch, heads, self.capacity, dim, value_states.shape[3], c.bits, c.group_size,
+                                     key_states.device)
+        self.rings = tuple(torch.zeros(batch, heads, self.ring + 1, x.shape[3], dtype=x.dtype, device=x.device)
+                           for x in (key_states, value_states))
+        self.is_initialized = True
+
+    def get_seq_length(self) -> int:
+        return self.length
+
+    def get_mask_sizes(self, query_length: int) -> tuple[int, int]:
+        return self.length + query_length, 0
+
+    def get_max_length(self) -> int:
+        return self.capacity
+
+    def allocated_bytes(self) -> int:
+        """Bytes the layer holds on the device (codes, scales, zero points, counts and rings)."""
+        tensors = [self.store.key_codes, self.store.key_scale, self.store.key_zero, self.store.value_codes,
+                   self.store.value_scale, self.store.value_zero, *self.rings]
+        return sum(t.numel() * t.element_size() for t in tensors)
+
+    def _schedule(self, committed: int) -> tuple[int, int]:
+        r = self.config.residual_length
+        return max(self.kq, (committed // r) * r), max(self.vq, committed - r)
+
+    def _quantize(self, keys: torch.Tensor, values: torch.Tensor, k_to: int, v_to: int, ring: int) -> None:
+        """Keys ``[kq, k_to)`` and values ``[vq, v_to)`` of every row from ``keys`` / ``values`` (the rings, or a
+        dense copy with ``ring`` 0) into the record; refuses scales beyond fp16."""
+        store = self.store
+        batch = keys.shape[0]
+        device = keys.device
+
+        def rows(x: int) -> torch.Tensor:
+            return torch.full((batch,), x, dtype=torch.int32, device=device)
+
+        if k_to > self.kq:
+            store.quantize(keys, "k", rows(self.kq), rows(k_to), k_to - self.kq, ring=ring)
+            store.keys_quantized.fill_(k_to)
+        if v_to > self.vq:
+            store.quantize(values, "v", rows(self.vq), rows(v_to), v_to - self.vq, ring=ring)
+            store.values_quantized.fill_(v_to)
+        if (k_to > self.kq or v_to > self.vq) and int(store.overflow.item()):
+            store.overflow.zero_()
+            raise ConfigError("a KIVI scale or zero point exceeds the fp16 range of the packed storage; use "
+                              "storage='simulated'")
+        self.kq, self.vq = k_to, v_to
+
+    def pass_begin(self, frontier: int) -> None:
+        """Quantize what the schedule quantizes once ``frontier`` tokens are committed (kivi.py:230-243), from the
+        rings."""
+        k_to, v_to = self._schedule(frontier)
+        self._quantize(self.rings[0], self.rings[1], k_to, v_to, self.ring)
+        self.committed = frontier
+
+    def _write_rings(self, keys: torch.Tensor, values: torch.Tensor, start: int) -> None:
+        tokens = keys.shape[2]
+        if start + tokens - min(self.kq, self.vq) > self.ring:
+            raise ConfigError(f"a pass wrote more than the packed KIVI ring holds ({self.ring} slots = residual_length "
+                              "+ headroom) and would overwrite entries not quantized yet: increase headroom or use "
+                              "storage='simulated'")
+        slots = torch.arange(start, start + tokens, device=keys.device) % self.ring
+        self.rings[0].index_copy_(2, slots, keys.to(self.rings[0].dtype))
+        self.rings[1].index_copy_(2, slots, values.to(self.rings[1].dtype))
+
+    def _dense(self, length: int) -> tuple[torch.Tensor, torch.Tensor]:
+        return self.store.materialize(self.rings[0], self.rings[1], self.ring, length)
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, *args, **kwargs
+               ) -> tuple[torch.Tensor, torch.Tensor]:
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        if self.length > self.committed:
+            self.pass_begin(self.length)
+        tokens = key_states.shape[2]
+        start = self.length
+        if start + tokens > self.capacity:
+            raise ConfigError(f"the cache holds {self.capacity} tokens per row; writing {tokens} more after {start} "
+                              "exceeds it (make the cache with a larger max_length)")
+        if tokens > self.config.headroom:  # a prompt: a dense copy, what its end commits packed from it
+            old_k, old_v = self._dense(start)
+            keys = torch.cat([old_k, key_states.to(old_k.dtype)], dim=2).contiguous()
+            values = torch.cat([old_v, value_states.to(old_v.dtype)], dim=2).contiguous()
+            end = start + tokens
+            k_to, v_to = self._schedule(end)
+            self._quantize(keys, values, k_to, v_to, 0)
+            first = max(0, tokens - self.ring)
+            self._write_rings(key_states[:, :, first:], value_states[:, :, first:], start + first)
+            self.length = self.committed = end
+            return keys, values
+        self._write_rings(key_states, value_states, start)
+        self.length += tokens
+        length = self.length
+        record = self.store.record(length, key_ring=self.rings[0], value_ring=self.rings[1], ring=self.ring,
+                                   materialize=lambda: self._dense(length))
+        batch, heads, _, dim = key_states.shape
+        keys = attach_packed(stand_in((batch, heads, length, dim), key_states.dtype, key_states.device), record)
+        values = stand_in((batch, heads, length, value_states.shape[3]), value_states.dtype, value_states.device)
+        return keys, values
+
+    def reset(self) -> None:
+        self.length = self.committed = self.kq = self.vq = 0
+        if self.store is not None:
+            self.store.keys_quantized.zero_()
+            self.store.values_quantized.zero_()
+            self.store.overflow.zero_()
+
+
 class EconomizeCache(Cache):
     """transformers ``past_key_values`` whose layers are the techniques' paged caches (dense ``DynamicLayer`` for a
     layer no technique covers)."""
@@ -786,12 +930,11 @@ class EconomizedModel:
                 layers.append(PagedLayer(max_length, fp8, quest, scales=self.scales.get(index), layer=index,
                                          static=True))
                 continue
-            if isinstance(cfg, FusedKIVIConfig) and cfg.simulated(self.model):
-                layers.append(FusedKIVIDenseLayer(max_length, cfg))
-            elif isinstance(cfg, KIVIConfig) and cfg.simulated(self.model):
-                layers.append(SimulatedKIVILayer(max_length, cfg))
-            elif isinstance(cfg, KIVIConfig):
-                layers.append(KIVILayer(max_length, cfg))
+            if isinstance(cfg, KIVIConfig):
+                kind = cfg.layer_kind(self.model)
+                layer_class = {"paged": KIVILayer, "packed": PackedKIVILayer, "fused": FusedKIVIDenseLayer,
+                               "simulated": SimulatedKIVILayer}[kind]
+                layers.append(layer_class(max_length, cfg))
             elif isinstance(cfg, FP8KVConfig) and self.paged_fp8(cfg):
                 layers.append(PagedLayer(max_length, cfg.dtype, scales=self.scales.get(index)))
             elif isinstance(cfg, FP8KVConfig):

@@ -263,3 +263,30 @@ class KIVIPackedStore:
             keys_quantized=self.keys_quantized, values_quantized=self.values_quantized, key_ring=key_ring,
             value_ring=value_ring, ring=ring, materialize=materialize,
         )
+
+    def materialize(self, key_ring: torch.Tensor, value_ring: torch.Tensor, ring: int, length: int
+                    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """Fresh dense K/V ``[B, H, length, D]`` in the rings' dtype: the codes dequantized below the quantized
+        counts, the rings (slot ``s`` at ``s % ring``; the slot itself with ``ring`` 0) above them
+        (PackedKIVICache._dense, techniques/kv_quant/packed.py:300-320)."""
+        device = _lib.require_gpu(key_ring, value_ring)
+        out = []
+        for kind, src, codes, scale, zero, counts, group in (
+                (0, key_ring, self.key_codes, self.key_scale, self.key_zero, self.keys_quantized, self.key_group),
+                (1, value_ring, self.value_codes, self.value_scale, self.value_zero, self.values_quantized,
+                 self.value_group)):
+            batch, heads, _, dim = src.shape
+            dense = torch.empty(batch, heads, length, dim, dtype=src.dtype, device=device)
+            if src.stride(-1) != 1:
+                raise ConfigError("the rings need a contiguous last axis")
+            out.append(dense)
+            if length == 0:
+                continue
+            _lib.call(
+                "eco_kivi_packed_gather", kind, codes.data_ptr(), codes.stride(0), codes.stride(1), codes.stride(2),
+                scale.data_ptr(), zero.data_ptr(), scale.stride(0), scale.stride(1), scale.stride(2),
+                counts.data_ptr(), src.data_ptr(), src.stride(0), src.stride(1), src.stride(2), int(ring),
+                dense.data_ptr(), _lib.fmt(src.dtype), dense.stride(0), dense.stride(1), dense.stride(2), batch,
+                heads, int(length), dim, self.bits, group, _lib.stream_of(device),
+            )
+        return out[0], out[1]

@@ -99,8 +99,8 @@ def model_dtype(adapter) -> torch.dtype | None:
 
 def kivi_paged_refusal(config, adapter) -> str | None:
     """Why the paged KIVI cache (32-token pages of 2- or 4-bit codes read by the fused kernel) cannot hold
-    ``config``'s layers on this model, or ``None`` when it can; such layers use the simulated storage (dense buffers
-    quantized in place, any bits, group and head dim), as the reference falls back to it (kivi.py:62-66)."""
+    ``config``'s layers on this model, or ``None`` when it can; such layers keep the reference's packed record
+    (any bits, group, head dim and dtype; :meth:`KIVIConfig.layer_kind`)."""
     if config.bits not in (2, 4):
         return f"bits={config.bits}"
     if config.group_size != 32:
@@ -266,20 +266,17 @@ class KIVIConfig(TechniqueConfig):
                 raise ConfigError(f"{self.technique} supports only storage='simulated', got {self.storage!r}")
 
     def validate(self, adapter) -> None:
-        """An explicit ``storage="packed"`` the paged KIVI cache cannot hold on this model is refused (the
-        reference's explicit packed storage raises where it cannot run, kivi.py:62-66); otherwise a configuration
-        the paged cache cannot hold runs on the simulated storage, whose buffers (the model's dtype) the dense kernel
-        reads at head dims up to 512 (256 on fp32 models)."""
-        if self.storage == "packed":
-            why = kivi_paged_refusal(self, adapter)
-            if why is not None:
-                raise ConfigError(f"storage='packed' is the paged KIVI cache, which cannot hold {why}; use storage="
-                                  "None or 'simulated'")
+        """Refuses head dims the dense decode kernel does not take (up to 512, 256 on fp32 models): the packed
+        record of the configurations the paged cache cannot hold, and the simulated storage, are read by it."""
         _dense_head_dim(self.technique, adapter, kv_in_model_dtype=True)
 
-    def simulated(self, adapter) -> bool:
-        """Whether this configuration's layers use the simulated storage on ``adapter``'s model."""
-        return self.storage == "simulated" or kivi_paged_refusal(self, adapter) is not None
+    def layer_kind(self, adapter) -> str:
+        """Where this configuration's layers live on ``adapter``'s model: ``"paged"`` (the paged KIVI cache),
+        ``"packed"`` (the reference's packed record and rings, techniques/kv_quant/packed.py:1-30: any bits, group,
+        head dim and dtype) or ``"simulated"`` (dense buffers quantized in place, kivi.py:178-275)."""
+        if self.storage == "simulated":
+            return "simulated"
+        return "paged" if kivi_paged_refusal(self, adapter) is None else "packed"
 
     @property
     def kivi_storage(self) -> str:
@@ -297,10 +294,10 @@ class FusedKIVIConfig(KIVIConfig):
     technique: ClassVar[str] = "kivi_fused"
     packable: ClassVar[bool] = False
 
-    def simulated(self, adapter) -> bool:
-        """The fused kernel reads the paged codes wherever the paged cache holds them; elsewhere the simulated
-        storage holds the values that kernel would dequantize (code * scale + zero in the model's dtype)."""
-        return kivi_paged_refusal(self, adapter) is not None
+    def layer_kind(self, adapter) -> str:
+        """``"paged"`` where the paged KIVI cache holds the layers, else ``"fused"``: dense buffers of the
+        dequantized values with the reference's packed codes beside them (kv_kivi_fused/fused.py:104-250)."""
+        return "paged" if kivi_paged_refusal(self, adapter) is None else "fused"
 
     def validate(self, adapter) -> None:
         """Refuses an attention implementation that does not read KIVI codes (kv_kivi_fused/fused.py:43-51)."""

@@ -346,6 +346,19 @@ int eco_kivi_pack_quantize(int32_t kind, void* src, int32_t format, int64_t ss_b
                            const int32_t* to, int32_t batch, int32_t heads, int32_t slots, int32_t head_dim,
                            int32_t bits, int32_t group, int32_t max_tokens, uint32_t* overflow, void* stream);
 
+/* The dense view of a KIVI packed record's keys (kind 0) or values (kind 1): out [B, H, slots, D] (element strides
+ * so_*, format bf16 / fp16 / fp32) holds code * scale + zero in fp32 rounded to the format where slot s <
+ * quantized[b] (codes, scale, zero as eco_kivi_pack_quantize lays them out), and the full-precision entry of `ring`
+ * [B, H, *, D] (element strides sr_*, the output's format) at slot s % ring_slots (slot s when ring_slots is 0)
+ * elsewhere. quantized[b] must not exceed the slots the codes hold. Replaces PackedKIVICache._dense
+ * (techniques/kv_quant/packed.py:300-320), the dense copy read by attention paths that do not read codes. */
+int eco_kivi_packed_gather(int32_t kind, const uint8_t* codes, int64_t sc_b, int64_t sc_h, int64_t sc_s,
+                           const void* scale, const void* zero, int64_t sz_b, int64_t sz_h, int64_t sz_s,
+                           const int32_t* quantized, const void* ring, int64_t sr_b, int64_t sr_h, int64_t sr_s,
+                           int32_t ring_slots, void* out, int32_t format, int64_t so_b, int64_t so_h, int64_t so_s,
+                           int32_t batch, int32_t heads, int32_t slots, int32_t head_dim, int32_t bits, int32_t group,
+                           void* stream);
+
 /* KIVI's cell on vLLM's paged cache (backends/vllm/kivi/layout.py:133-213): for a head size (a power of two, 16 to
  * 256) of a cache dtype of element_size bytes, bits 2 / 4 / 8 and a power-of-two group of at most 128, writes
  * offsets[10] = {value group, key aux slots, off_v, off_vs, off_vz, off_ka, off_kc, off_vc, off_flag, cell bytes}. */

@@ -146,13 +146,15 @@ class Mirror(CacheLayerMixin):
         return -1
 
     def update(self, key_states, value_states, *args, **kwargs):
-        from economize_amd.hf import DenseFP8Layer, DenseQuestLayer, SimulatedKIVILayer
+        from economize_amd.hf import DenseFP8Layer, DenseQuestLayer, PackedKIVILayer, SimulatedKIVILayer
         from economize_amd.packed import materialized_kv
 
         if isinstance(self.source, DynamicLayer):
             return self.source.keys, self.source.values
         if isinstance(self.source, (DenseQuestLayer, SimulatedKIVILayer)):
             keys, values = (b[:, :, : self.source.length] for b in self.source.buffers)
+        elif isinstance(self.source, PackedKIVILayer):  # the codes dequantized, the rings above them
+            keys, values = self.source._dense(self.source.length)
         elif isinstance(self.source, DenseFP8Layer):  # the codes decoded to the model's dtype
             keys, values = (self.source._decoded(c[:, :, : self.source.length], i)
                             for i, c in enumerate(self.source.codes))
@@ -287,21 +289,23 @@ LOGIT_TOL = 0.5
 
 
 @pytest.mark.parametrize("technique", ["fp8", "kivi2", "kivi4", "quest", "quest_fp16", "quest_fp32", "fp8_d512",
-                                       "kivi2_d512", "quest_d512", "kivi8_fp16", "kivi4_g16"])
+                                       "kivi2_d512", "quest_d512", "kivi8_fp16", "kivi4_g16", "packed8",
+                                       "packed4_g16_fp16", "packed2_d512"])
 def test_decoding_logits_match_sdpa_over_the_cache(technique: str) -> None:
     """Heads of 512 channels (``_d512``) run on the dense kernel's two value slices: dense fp8 buffers, KIVI codes in
     the reference's dense layout and Quest over dense buffers. ``kivi8_fp16`` (8-bit codes on an fp16 model) and
     ``kivi4_g16`` (groups of 16) are configurations the paged KIVI cache does not hold: the codes beside dense
-    buffers, read by the kernel."""
+    buffers, read by the kernel. ``packed*``: ``KIVIConfig``'s packed record and rings for such configurations, no
+    dense buffer."""
     from transformers import AttentionInterface
     from transformers.masking_utils import AttentionMaskInterface
 
-    from economize_amd.techniques import FusedFP8KVConfig, FusedKIVIConfig, QuestConfig
+    from economize_amd.techniques import FusedFP8KVConfig, FusedKIVIConfig, KIVIConfig, QuestConfig
 
     attn, path, dtype = "sdpa", "kernel_fp8", torch.bfloat16
     head_dim = 512 if technique.endswith("_d512") else 64
     technique = technique.removesuffix("_d512")
-    if technique in ("quest_fp16", "kivi8_fp16"):
+    if technique in ("quest_fp16", "kivi8_fp16", "packed4_g16_fp16"):
         dtype = torch.float16
     elif technique == "quest_fp32":
         dtype = torch.float32
@@ -310,6 +314,10 @@ def test_decoding_logits_match_sdpa_over_the_cache(technique: str) -> None:
     elif technique.startswith("kivi"):
         group = 16 if technique.endswith("_g16") else 32
         configs = (FusedKIVIConfig(bits=int(technique[4]), group_size=group, residual_length=32, headroom=64),)
+        path = "kernel_kivi"
+    elif technique.startswith("packed"):
+        group = 16 if "_g16" in technique else 32
+        configs = (KIVIConfig(bits=int(technique[6]), group_size=group, residual_length=32, headroom=64),)
         path = "kernel_kivi"
     else:
         configs = (QuestConfig(page_size=16, token_budget=64, dense_layers=1),)
@@ -441,24 +449,27 @@ def test_tensor_fp8_scales_are_calibrated_and_decode_like_the_oracle() -> None:
     assert golden_greedy(model, em.make_cache(64), "cuda") == want
 
 
-def test_the_hip_path_decodes_the_reference_kivi_golden_tokens() -> None:
+@pytest.mark.parametrize("storage", [None, "simulated"])
+def test_the_hip_path_decodes_the_reference_kivi_golden_tokens(storage) -> None:
     """The reference's own golden tokens of ``KIVIConfig(bits=2, group_size=4, residual_length=8)``
-    (tests/golden/catalog.py:163-165) from its golden model on the GPU: groups of 4 are not the paged cache's, so the
-    layers use the simulated storage (buffers quantized in place by ``eco_kivi_fake_quantize`` at every pass
-    boundary) and every decoding step runs on the dense decode kernel."""
+    (tests/golden/catalog.py:163-165) from its golden model on the GPU. Groups of 4 are not the paged cache's: with
+    the default storage the layers keep the reference's packed record and rings (:class:`PackedKIVILayer`, no dense
+    buffer; every decoding step's kernel reads the codes and the rings), with ``storage="simulated"`` dense buffers
+    quantized in place by ``eco_kivi_fake_quantize`` at every pass boundary, read by the dense kernel."""
     import test_golden_reference as golden
 
     from economize_amd.attention import kernel_usage
-    from economize_amd.hf import SimulatedKIVILayer, apply
+    from economize_amd.hf import PackedKIVILayer, SimulatedKIVILayer, apply
     from economize_amd.techniques import KIVIConfig
 
     model = golden.golden_model().cuda()
-    em = apply(model, KIVIConfig(bits=2, group_size=4, residual_length=8))
+    em = apply(model, KIVIConfig(bits=2, group_size=4, residual_length=8, storage=storage))
     cache = em.make_cache(golden.PROMPT + golden.NEW_TOKENS + 1)
-    assert all(isinstance(layer, SimulatedKIVILayer) for layer in cache.layers)
+    layer_class, path = (SimulatedKIVILayer, "kernel") if storage else (PackedKIVILayer, "kernel_kivi")
+    assert all(type(layer) is layer_class for layer in cache.layers)
     kernel_usage(reset=True)
     assert golden_greedy(model, cache, "cuda") == golden.GOLDEN["kv_kivi_2bit_tokens"].tolist()
-    assert {(r["path"], r["queries"]) for r in kernel_usage(reset=True)} >= {("kernel", 1)}
+    assert {(r["path"], r["queries"]) for r in kernel_usage(reset=True)} >= {(path, 1)}
     assert (cache.layers[0].kq, cache.layers[0].vq) == (32, 31)  # 39 committed tokens before the last pass
 
 

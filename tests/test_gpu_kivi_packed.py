@@ -295,3 +295,40 @@ def test_pack_quantize_flags_scales_beyond_fp16() -> None:
     rows = lambda x: torch.tensor([x], dtype=torch.int32, device="cuda")  # noqa: E731
     store.quantize(data.cuda(), "k", rows(0), rows(32), 32)
     assert int(store.overflow.item()) == 1
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("ring", [0, 40])
+def test_dense_view_of_the_record(dtype, ring) -> None:
+    """eco_kivi_packed_gather: the codes dequantized below each row's counts (equal to what the quantizer wrote back),
+    the full-precision entries above them, from the buffer itself or from a ring at s % ring."""
+    from economize_amd.kivi_packed import KIVIPackedStore
+
+    batch, heads, slots, d, group, bits = 2, 2, 96, 48, 16, 4
+    gen = torch.Generator().manual_seed(11)
+    data = (torch.randn(batch, heads, slots, d, generator=gen) * 2).to(dtype)
+    store = KIVIPackedStore(batch, heads, slots, d, d, bits, group, "cuda")
+    written = data.clone().cuda()
+    kq, vq = [64, 32], [70, 10]
+    rows = lambda x: torch.tensor(x, dtype=torch.int32, device="cuda")  # noqa: E731
+    keys_back, values_back = written.clone(), written.clone()
+    store.quantize(keys_back, "k", rows([0, 0]), rows(kq), 64, write_back=True)
+    store.quantize(values_back, "v", rows([0, 0]), rows(vq), 70, write_back=True)
+    store.keys_quantized.copy_(rows(kq))
+    store.values_quantized.copy_(rows(vq))
+    if ring:
+        src = torch.full((batch, heads, ring + 1, d), float("nan"), dtype=dtype, device="cuda")
+        for s in range(slots - ring, slots):
+            src[:, :, s % ring] = written[:, :, s]
+        length = slots
+        lows = [slots - ring] * batch
+    else:
+        src, length, lows = written, slots, [0] * batch
+    keys, values = store.materialize(src, src, ring, length)
+    torch.cuda.synchronize()
+    for b in range(batch):
+        assert torch.equal(keys[b, :, :kq[b]], keys_back[b, :, :kq[b]])
+        assert torch.equal(values[b, :, :vq[b]], values_back[b, :, :vq[b]])
+        lo_k, lo_v = max(kq[b], lows[b]), max(vq[b], lows[b])
+        assert torch.equal(keys[b, :, lo_k:], written[b, :, lo_k:])
+        assert torch.equal(values[b, :, lo_v:], written[b, :, lo_v:])

@@ -50,12 +50,9 @@ def test_validate_refuses_what_the_path_cannot_run() -> None:
     with pytest.raises(ConfigError, match="up to 512"):
         FusedFP8KVConfig().validate(tiny_model(head_dim=640, attn="economize"))
     for config in (KIVIConfig(bits=8), KIVIConfig(group_size=64, residual_length=128), KIVIConfig(storage="simulated"),
-                   KIVIConfig(bits=4, group_size=4, residual_length=8)):
-        config.validate(model)  # the simulated storage takes what the paged cache cannot hold
-    with pytest.raises(ConfigError, match="bits=8"):
-        KIVIConfig(bits=8, storage="packed").validate(model)
-    with pytest.raises(ConfigError, match="group_size=64"):
-        KIVIConfig(group_size=64, residual_length=128, storage="packed").validate(model)
+                   KIVIConfig(bits=4, group_size=4, residual_length=8), KIVIConfig(bits=8, storage="packed"),
+                   KIVIConfig(group_size=64, residual_length=128, storage="packed")):
+        config.validate(model)  # the packed record and the simulated storage take what the paged cache cannot hold
     with pytest.raises(ConfigError, match="up to 256"):  # simulated buffers in the model's fp32
         FusedKIVIConfig().validate(tiny_model(head_dim=512, attn="economize"))
     FusedKIVIConfig().validate(tiny_model(head_dim=512, attn="economize").to(torch.bfloat16))
@@ -124,8 +121,9 @@ def test_a_cpu_call_falls_back_to_sdpa_and_is_logged() -> None:
 
 def test_kivi_layers_are_paged_where_the_paged_cache_holds_them() -> None:
     """2- and 4-bit codes in groups of 32 on a bf16 model of head dim 64 / 128 live in the paged KIVI cache; 8-bit
-    codes, other groups, head dims and dtypes, and storage='simulated' get the simulated storage (kivi.py:62-66),
-    with the reference's packed codes beside its buffers for FusedKIVIConfig (kv_kivi_fused/fused.py:104-250)."""
+    codes, other groups, head dims and dtypes keep the reference's packed record and rings (kv_quant/packed.py), or
+    its codes beside dense buffers for FusedKIVIConfig (kv_kivi_fused/fused.py:104-250); storage='simulated' gets
+    the simulated storage (kivi.py:62-66)."""
     from economize_amd.hf import apply
 
     def layer_type(model, config) -> str:
@@ -135,10 +133,11 @@ def test_kivi_layers_are_paged_where_the_paged_cache_holds_them() -> None:
     assert layer_type(bf16, FusedKIVIConfig()) == "KIVILayer"
     assert layer_type(tiny_model().to(torch.bfloat16), KIVIConfig(bits=4)) == "KIVILayer"
     assert layer_type(tiny_model().to(torch.bfloat16), KIVIConfig(storage="simulated")) == "SimulatedKIVILayer"
-    assert layer_type(tiny_model().to(torch.bfloat16), KIVIConfig(bits=8)) == "SimulatedKIVILayer"
+    assert layer_type(tiny_model().to(torch.bfloat16), KIVIConfig(bits=8)) == "PackedKIVILayer"
+    assert layer_type(tiny_model().to(torch.bfloat16), KIVIConfig(bits=8, storage="packed")) == "PackedKIVILayer"
     assert layer_type(tiny_model().to(torch.bfloat16), FusedKIVIConfig(group_size=16, residual_length=32)) == \
         "FusedKIVIDenseLayer"
-    assert layer_type(tiny_model(head_dim=16).to(torch.bfloat16), KIVIConfig()) == "SimulatedKIVILayer"
+    assert layer_type(tiny_model(head_dim=16).to(torch.bfloat16), KIVIConfig()) == "PackedKIVILayer"
     assert layer_type(tiny_model(), FusedKIVIConfig()) == "FusedKIVIDenseLayer"  # float32
 
 
