@@ -130,6 +130,20 @@ __device__ __forceinline__ float code_f32(uint2 w, int e) {
     return static_cast<float>((word >> (bit & 31)) & ((1u << BITS) - 1u));
 }
 
+// The same with the byte count and the code width known at run time only (uniform).
+__device__ __forceinline__ uint2 load_code_bytes_rt(int nb, const uint8_t* p) {
+    if (nb == 8) return *reinterpret_cast<const uint2*>(p);
+    if (nb == 4) return make_uint2(*reinterpret_cast<const uint32_t*>(p), 0u);
+    if (nb == 2) return make_uint2(*reinterpret_cast<const uint16_t*>(p), 0u);
+    return make_uint2(*p, 0u);
+}
+
+__device__ __forceinline__ float code_f32_rt(int bits, uint2 w, int e) {
+    const int bit = e * bits;
+    const uint32_t word = bit < 32 ? w.x : w.y;
+    return static_cast<float>(__builtin_amdgcn_ubfe(word, static_cast<uint32_t>(bit & 31), static_cast<uint32_t>(bits)));
+}
+
 // N fp16 values at p (16-byte aligned for 8, 8-byte for 4), as the first N halves of a word.
 template <int N>
 __device__ __forceinline__ uint4 load_halves(const uint16_t* p) {
@@ -235,6 +249,30 @@ __device__ __forceinline__ void cell_codes8(uint32_t x, float (&c)[8]) {
     c[3] = h0.y;
     c[5] = h1.x;
     c[7] = h1.y;
+}
+
+// The codes of a chunk (channel i at bit i BITS of its bytes; 8 channels, or the first 4 for fp32 chunks) as exact
+// floats: 2- and 4-bit codes through the e4m3 conversion of cell_codes8, 8-bit codes one byte each.
+template <int BITS>
+__device__ __forceinline__ void chunk_codes(uint2 w, float (&c)[8]) {
+    if constexpr (BITS == 8) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {  // (v_cvt_f32_ubyte0..3)
+            c[i] = static_cast<float>((w.x >> (8 * i)) & 0xFFu);
+            c[4 + i] = static_cast<float>((w.y >> (8 * i)) & 0xFFu);
+        }
+    } else {
+        cell_codes8<BITS>(w.x, c);
+    }
+}
+
+__device__ __forceinline__ void chunk_codes_rt(int bits, uint2 w, float (&c)[8]) {
+    if (bits == 8)
+        chunk_codes<8>(w, c);
+    else if (bits == 4)
+        chunk_codes<4>(w, c);
+    else
+        chunk_codes<2>(w, c);
 }
 
 // bf16(code * scale + zero) of eight channels, the product and the sum in fp32 (one fused multiply-add, the product
@@ -535,9 +573,140 @@ __global__ __launch_bounds__(64, DP > 256 ? 1 : 2) void dense_split_kernel(Dense
     constexpr int VCH = TK * VCR / 64;
     constexpr int KB = 4;  // key chunks per batch (each holds its entry, codes, scales and zero points)
     constexpr int VB = DP >= 256 || ES == 4 ? 4 : 8;
-    auto kp_stage = [&](auto bits_c, int t0) __attribute__((always_inline)) {
-        constexpr int BITS = decltype(bits_c)::value;
-        constexpr int NB = CE * BITS / 8;  // code bytes of a chunk
+    auto kp_stage = [&](int t0) __attribute__((always_inline)) {
+        const int BITS = p.kp_bits;
+        const int NB = CE * BITS / 8;  // code bytes of a chunk
+        // A lane's chunks share their channels (KCR and VCR divide 64): key channels kc0 .., value channels vc0 ...
+        const int kc0 = (lane % KCR) * CE, vc0 = v0 + (lane % VCR) * CE;
+        const bool k_ok = kc0 < p.head_dim, v_ok = vc0 < p.value_dim;
+        // ---- a tile of codes only (every key and value quantized, the tile's keys inside one key group, each value
+        // chunk inside one value group) or of full-precision entries only: its loads in one batch, or, where the
+        // registers would not hold them, in batches of 16 chunks (keys, then values) ----
+        constexpr bool ONE_BATCH = KCH + VCH <= 16;
+        constexpr int KF = KCH < 16 ? KCH : 16;  // chunks per batch
+        constexpr int VF = VCH < 16 ? VCH : 16;
+        const int kcc = k_ok ? kc0 : 0, vcc = v_ok ? vc0 : 0;
+        uint2 kcw[KF], vcw[VF];
+        uint4 ks = make_uint4(0, 0, 0, 0), kz = make_uint4(0, 0, 0, 0);
+        uint16_t vs[VF], vz[VF];
+        auto codes_keys = [&](int i0) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < KF; ++i) {
+                const int t = t0 + (lane + 64 * (i0 + i)) / KCR;
+                kcw[i] = load_code_bytes_rt(NB, kcb + static_cast<int64_t>(t) * p.skc_s + kcc * BITS / 8);
+            }
+            const int64_t so = static_cast<int64_t>(t0 / p.kp_kg) * p.sks_g + kcc;
+            ks = load_halves<CE>(ksb + so);
+            kz = load_halves<CE>(kzb + so);
+        };
+        auto codes_values = [&](int i0) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < VF; ++i) {
+                const int t = t0 + (lane + 64 * (i0 + i)) / VCR;
+                vcw[i] = load_code_bytes_rt(NB, vcb + static_cast<int64_t>(t) * p.svc_s + vcc * BITS / 8);
+                const int64_t so = static_cast<int64_t>(t) * p.svs_s + vcc / p.kp_vg;
+                vs[i] = vsb[so];
+                vz[i] = vzb[so];
+            }
+        };
+        auto keys_from_codes = [&](int i0) __attribute__((always_inline)) {
+            const f16x8 s8 = __builtin_bit_cast(f16x8, ks);
+            const f16x8 z8 = __builtin_bit_cast(f16x8, kz);
+#pragma unroll
+            for (int i = 0; i < KF; ++i) {
+                float c[8], x[CE];
+                chunk_codes_rt(BITS, kcw[i], c);
+#pragma unroll
+                for (int e = 0; e < CE; ++e)
+                    x[e] = __builtin_fmaf(c[e], static_cast<float>(s8[e]), static_cast<float>(z8[e]));
+                *reinterpret_cast<uint4*>(ktile + ((lane + 64 * (i0 + i)) / KCR) * KROW + kc0 * ES) =
+                    k_ok ? pack_chunk<FMT>(x) : make_uint4(0, 0, 0, 0);
+            }
+        };
+        auto values_from_codes = [&](int i0) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < VF; ++i) {
+                const float sc = half_f32(vs[i]), zr = half_f32(vz[i]);
+                float c[8], x[CE];
+                chunk_codes_rt(BITS, vcw[i], c);
+#pragma unroll
+                for (int e = 0; e < CE; ++e) x[e] = __builtin_fmaf(c[e], sc, zr);
+                *reinterpret_cast<uint4*>(vtile + ((lane + 64 * (i0 + i)) / VCR) * ROW + (vc0 - v0) * ES) =
+                    v_ok ? pack_chunk<FMT>(x) : make_uint4(0, 0, 0, 0);
+            }
+        };
+        if (t0 + TK <= kq && t0 + TK <= vq && p.kp_kg % TK == 0 && p.kp_vg % CE == 0) {
+            if constexpr (ONE_BATCH) {
+                codes_keys(0);
+                codes_values(0);
+                keys_from_codes(0);
+                values_from_codes(0);
+            } else {
+#pragma nounroll
+                for (int i0 = 0; i0 < KCH; i0 += KF) {
+                    codes_keys(i0);
+                    keys_from_codes(i0);
+                }
+#pragma nounroll
+                for (int i0 = 0; i0 < VCH; i0 += VF) {
+                    codes_values(i0);
+                    values_from_codes(i0);
+                }
+            }
+            return;
+        }
+        if (t0 >= kq && t0 >= vq) {
+            uint4 kd[KF], vd[VF];
+            auto dense_keys = [&](int i0) __attribute__((always_inline)) {
+#pragma unroll
+                for (int i = 0; i < KF; ++i) {
+                    const int t = min(t0 + (lane + 64 * (i0 + i)) / KCR, t_end - 1);
+                    kd[i] = *reinterpret_cast<const uint4*>(key_row(t) + kcc * ES);
+                }
+            };
+            auto dense_values = [&](int i0) __attribute__((always_inline)) {
+#pragma unroll
+                for (int i = 0; i < VF; ++i) {
+                    const int t = min(t0 + (lane + 64 * (i0 + i)) / VCR, t_end - 1);
+                    vd[i] = *reinterpret_cast<const uint4*>(value_row(t) + vcc * ES);
+                }
+            };
+            auto keys_to_lds = [&](int i0) __attribute__((always_inline)) {
+#pragma unroll
+                for (int i = 0; i < KF; ++i) {
+                    const int tl = (lane + 64 * (i0 + i)) / KCR;
+                    *reinterpret_cast<uint4*>(ktile + tl * KROW + kc0 * ES) =
+                        k_ok && t0 + tl < t_end ? kd[i] : make_uint4(0, 0, 0, 0);
+                }
+            };
+            auto values_to_lds = [&](int i0) __attribute__((always_inline)) {
+#pragma unroll
+                for (int i = 0; i < VF; ++i) {
+                    const int tl = (lane + 64 * (i0 + i)) / VCR;
+                    *reinterpret_cast<uint4*>(vtile + tl * ROW + (vc0 - v0) * ES) =
+                        v_ok && t0 + tl < t_end ? vd[i] : make_uint4(0, 0, 0, 0);
+                }
+            };
+            if constexpr (ONE_BATCH) {
+                dense_keys(0);
+                dense_values(0);
+                keys_to_lds(0);
+                values_to_lds(0);
+            } else {
+#pragma nounroll
+                for (int i0 = 0; i0 < KCH; i0 += KF) {
+                    dense_keys(i0);
+                    keys_to_lds(i0);
+                }
+#pragma nounroll
+                for (int i0 = 0; i0 < VCH; i0 += VF) {
+                    dense_values(i0);
+                    values_to_lds(i0);
+                }
+            }
+            return;
+        }
+        // ---- any other tile (the row's boundary tiles, value groups inside a chunk): chunk by chunk ----
 #pragma nounroll
         for (int base = 0; base < KCH; base += KB) {
             uint4 dn[KB], sc[KB], zr[KB];
@@ -550,7 +719,7 @@ __global__ __launch_bounds__(64, DP > 256 ? 1 : 2) void dense_split_kernel(Dense
                 const bool code = ok && t < kq;
                 const int tt = ok ? t : 0, cc = ok ? c : 0;
                 dn[i] = *reinterpret_cast<const uint4*>((code ? kbase : key_row(tt)) + cc * ES);
-                cw[i] = load_code_bytes<NB>(kcb + (code ? static_cast<int64_t>(tt) * p.skc_s + cc * BITS / 8 : 0));
+                cw[i] = load_code_bytes_rt(NB, kcb + (code ? static_cast<int64_t>(tt) * p.skc_s + cc * BITS / 8 : 0));
                 const int64_t so = code ? static_cast<int64_t>(tt / p.kp_kg) * p.sks_g + cc : 0;
                 sc[i] = load_halves<CE>(ksb + so);
                 zr[i] = load_halves<CE>(kzb + so);
@@ -566,7 +735,7 @@ __global__ __launch_bounds__(64, DP > 256 ? 1 : 2) void dense_split_kernel(Dense
                 float x[CE];
 #pragma unroll
                 for (int e = 0; e < CE; ++e)
-                    x[e] = __builtin_fmaf(code_f32<BITS>(cw[i], e), static_cast<float>(s8[e]),
+                    x[e] = __builtin_fmaf(code_f32_rt(BITS, cw[i], e), static_cast<float>(s8[e]),
                                           static_cast<float>(z8[e]));
                 *reinterpret_cast<uint4*>(ktile + tl * KROW + c * ES) =
                     code ? pack_chunk<FMT>(x) : (ok ? dn[i] : make_uint4(0, 0, 0, 0));
@@ -590,7 +759,7 @@ __global__ __launch_bounds__(64, DP > 256 ? 1 : 2) void dense_split_kernel(Dense
                     const bool code = ok && t < vq;
                     const int tt = ok ? t : 0, cc = ok ? c : 0;
                     dn[i] = *reinterpret_cast<const uint4*>((code ? vbase : value_row(tt)) + cc * ES);
-                    cw[i] = load_code_bytes<NB>(vcb + (code ? static_cast<int64_t>(tt) * p.svc_s + cc * BITS / 8 : 0));
+                    cw[i] = load_code_bytes_rt(NB, vcb + (code ? static_cast<int64_t>(tt) * p.svc_s + cc * BITS / 8 : 0));
                     const int64_t row = code ? static_cast<int64_t>(tt) * p.svs_s : 0;
 #pragma unroll
                     for (int e = 0; e < NS; ++e) {
@@ -608,7 +777,7 @@ __global__ __launch_bounds__(64, DP > 256 ? 1 : 2) void dense_split_kernel(Dense
                     float x[CE];
 #pragma unroll
                     for (int e = 0; e < CE; ++e)
-                        x[e] = __builtin_fmaf(code_f32<BITS>(cw[i], e), half_f32(sc[i][WHOLE ? 0 : e]),
+                        x[e] = __builtin_fmaf(code_f32_rt(BITS, cw[i], e), half_f32(sc[i][WHOLE ? 0 : e]),
                                               half_f32(zr[i][WHOLE ? 0 : e]));
                     *reinterpret_cast<uint4*>(vtile + tl * ROW + cl * ES) =
                         code ? pack_chunk<FMT>(x) : (ok ? dn[i] : make_uint4(0, 0, 0, 0));
@@ -623,11 +792,7 @@ __global__ __launch_bounds__(64, DP > 256 ? 1 : 2) void dense_split_kernel(Dense
     // ---- the tile's values into LDS (zero past the keys and past Dv); the previous tile's reads of LDS came first ----
     auto stage = [&](int t0) __attribute__((always_inline)) {
         if constexpr (KP) {
-            switch (p.kp_bits) {
-                case 2: kp_stage(std::integral_constant<int, 2>{}, t0); break;
-                case 4: kp_stage(std::integral_constant<int, 4>{}, t0); break;
-                default: kp_stage(std::integral_constant<int, 8>{}, t0); break;
-            }
+            kp_stage(t0);
             return;
         }
         if constexpr (CB != 0) {
@@ -831,8 +996,142 @@ __global__ __launch_bounds__(64, DP > 256 ? 1 : 2) void dense_split_kernel(Dense
         }
     };
 
+    // KP: the wave's leading tiles of codes only (keys and values quantized, the tile's keys inside one key group,
+    // value groups that hold whole chunks) are pipelined like the register buffers of the dense path: the next
+    // tile's codes, scales and zero points (a few registers per chunk) are loaded while a tile is dequantized into
+    // LDS and computed; every later tile is staged as it comes.
+    constexpr bool KP_PIPE = KP && DP <= 128 && !MASKED;
+    // (TWO: a tile may span two key groups, groups of 16 or 24 tokens; else every tile lies in one)
+    auto codes_run = [&](auto bits_c, auto two_c, int n) __attribute__((always_inline)) {
+        constexpr int BITS = decltype(bits_c)::value;
+        constexpr bool TWO = decltype(two_c)::value;
+        constexpr int NB = CE * BITS / 8;
+        constexpr int NW = NB > 4 ? 2 : 1;  // code words of a chunk
+        struct CodesRaw {
+            uint32_t kc[KP_PIPE ? KCH : 1][NW], vc[KP_PIPE ? VCH : 1][NW];
+            uint4 ks[TWO ? 2 : 1], kz[TWO ? 2 : 1];  // the scales and zero points of the tile's key groups
+            uint16_t vs[KP_PIPE ? VCH : 1], vz[KP_PIPE ? VCH : 1];
+            int split_at;  // the tile's first token of its last key group
+        };
+        auto words = [](uint2 w, uint32_t (&out)[NW]) __attribute__((always_inline)) {
+            out[0] = w.x;
+            if constexpr (NW == 2) out[NW - 1] = w.y;
+        };
+        auto pair = [](const uint32_t (&in)[NW]) __attribute__((always_inline)) {
+            return make_uint2(in[0], NW == 2 ? in[NW - 1] : 0u);
+        };
+        const int kc0 = (lane % KCR) * CE, vc0 = v0 + (lane % VCR) * CE;
+        const bool k_ok = kc0 < p.head_dim, v_ok = vc0 < p.value_dim;
+        const int kcc = k_ok ? kc0 : 0, vcc = v_ok ? vc0 : 0;
+        auto load = [&](CodesRaw& R, Keys& K, int k) __attribute__((always_inline)) {
+            issue(K, k);  // (the mask bytes)
+            const int t0 = tile_start(k);
+#pragma unroll
+            for (int i = 0; i < KCH; ++i) {
+                const int t = t0 + (lane + 64 * i) / KCR;
+                words(load_code_bytes<NB>(kcb + static_cast<int64_t>(t) * p.skc_s + kcc * BITS / 8), R.kc[i]);
+            }
+            const int g0 = t0 / p.kp_kg, g1 = (t0 + TK - 1) / p.kp_kg;  // g1 <= g0 + 1 on this path
+            R.split_at = g1 * p.kp_kg;
+#pragma unroll
+            for (int j = 0; j < (TWO ? 2 : 1); ++j) {
+                const int64_t so = static_cast<int64_t>(j ? g1 : g0) * p.sks_g + kcc;
+                R.ks[j] = load_halves<CE>(ksb + so);
+                R.kz[j] = load_halves<CE>(kzb + so);
+            }
+#pragma unroll
+            for (int i = 0; i < VCH; ++i) {
+                const int t = t0 + (lane + 64 * i) / VCR;
+                words(load_code_bytes<NB>(vcb + static_cast<int64_t>(t) * p.svc_s + vcc * BITS / 8), R.vc[i]);
+                const int64_t vo = static_cast<int64_t>(t) * p.svs_s + vcc / p.kp_vg;
+                R.vs[i] = vsb[vo];
+                R.vz[i] = vzb[vo];
+            }
+        };
+        auto fill = [&](const CodesRaw& R, int t0) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < KCH; ++i) {
+                const bool last = TWO && t0 + (lane + 64 * i) / KCR >= R.split_at;
+                const f16x8 s8 = __builtin_bit_cast(f16x8, last ? R.ks[TWO ? 1 : 0] : R.ks[0]);
+                const f16x8 z8 = __builtin_bit_cast(f16x8, last ? R.kz[TWO ? 1 : 0] : R.kz[0]);
+                float c[8], x[CE];
+                chunk_codes<BITS>(pair(R.kc[i]), c);
+#pragma unroll
+                for (int e = 0; e < CE; ++e)
+                    x[e] = __builtin_fmaf(c[e], static_cast<float>(s8[e]), static_cast<float>(z8[e]));
+                *reinterpret_cast<uint4*>(ktile + ((lane + 64 * i) / KCR) * KROW + kc0 * ES) =
+                    k_ok ? pack_chunk<FMT>(x) : make_uint4(0, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < VCH; ++i) {
+                const float sc = half_f32(R.vs[i]), zr = half_f32(R.vz[i]);
+                float c[8], x[CE];
+                chunk_codes<BITS>(pair(R.vc[i]), c);
+#pragma unroll
+                for (int e = 0; e < CE; ++e) x[e] = __builtin_fmaf(c[e], sc, zr);
+                *reinterpret_cast<uint4*>(vtile + ((lane + 64 * i) / VCR) * ROW + (vc0 - v0) * ES) =
+                    v_ok ? pack_chunk<FMT>(x) : make_uint4(0, 0, 0, 0);
+            }
+        };
+        // past the run's last tile every step loads that tile again (read from L2 and never used)
+        CodesRaw RA, RB;
+        Keys KA, KB;
+        int ki = 0, k = 0;
+        load(RA, KA, 0);
+        while (true) {
+            ki = min(ki + 1, n - 1);
+            load(RB, KB, ki);
+            fill(RA, tile_start(k));
+            compute(KA, tile_start(k));
+            if (++k >= n) break;
+            ki = min(ki + 1, n - 1);
+            load(RA, KA, ki);
+            fill(RB, tile_start(k));
+            compute(KB, tile_start(k));
+            if (++k >= n) break;
+        }
+    };
+
     if (my_tiles > 0) {
-        if constexpr (NBUF == 1) {
+        if constexpr (KP) {
+            int k = 0;
+            if constexpr (KP_PIPE) {
+                // tiles split + k splits lying wholly below both quantized counts, a prefix of the wave's tiles, when
+                // no tile spans more than two key groups (groups of at least 32 tokens, or of 16 or 24, whose
+                // boundaries fall at most once inside an aligned 32-token tile) and value groups hold whole chunks
+                const int below = min(kq, vq) / TK;
+                int n = split < below ? (below - 1 - split) / p.splits + 1 : 0;
+                const int kg = p.kp_kg;
+                if (!(kg >= TK || kg == 16 || kg == 24) || p.kp_vg % CE != 0) n = 0;
+                n = min(n, my_tiles);
+                const bool two = kg % TK != 0;
+                if (two && p.kp_bits == 8) n = 0;  // (two buffers of 8-bit codes and two key groups: too many registers)
+                if (n > 0) {
+                    using I2 = std::integral_constant<int, 2>;
+                    using I4 = std::integral_constant<int, 4>;
+                    using I8 = std::integral_constant<int, 8>;
+                    if (two) {
+                        if (p.kp_bits == 2)
+                            codes_run(I2{}, std::true_type{}, n);
+                        else
+                            codes_run(I4{}, std::true_type{}, n);
+                    } else if (p.kp_bits == 2) {
+                        codes_run(I2{}, std::false_type{}, n);
+                    } else if (p.kp_bits == 4) {
+                        codes_run(I4{}, std::false_type{}, n);
+                    } else {
+                        codes_run(I8{}, std::false_type{}, n);
+                    }
+                }
+                k = n;
+            }
+            for (; k < my_tiles; ++k) {
+                Keys K;
+                issue(K, k);
+                stage(tile_start(k));
+                compute(K, tile_start(k));
+            }
+        } else if constexpr (NBUF == 1) {
             for (int k = 0; k < my_tiles; ++k) {
                 Keys K;
                 issue(K, k);
