@@ -513,6 +513,43 @@ def measure_quest_graph(steps: int, warmup: int, seed: int, batch=8, q_heads=32,
             "hbm_frac_graph": round(nbytes / replay / 1e9 / HBM_PEAK_GBS, 4), "copies": 1}
 
 
+def measure_kivi_packed(steps: int, warmup: int, seed: int, bits: int = 8, group: int = 128, batch=16, q_heads=32,
+                        kv_heads=8, length=8192, residual=128) -> dict:
+    """kivi_decode_attention over the reference's KIVIPacked layout (dense buffers beside the codes, the fused
+    cache): every row quantized up to length - residual (keys in whole groups), the rest read from the buffers; bytes
+    are the codes, scales and zero points of the quantized slots plus the full-precision rest."""
+    import torch
+
+    from economize_amd.kivi_packed import KIVIPackedStore, kivi_decode_attention
+
+    d = HEAD_DIM
+    gen = torch.Generator(device="cuda:0").manual_seed(seed)
+    kq = (length - residual) // group * group
+    vq = length - residual
+    per_token = d * bits / 8
+    nbytes = int(batch * kv_heads * (kq * per_token + kq // group * d * 4 + vq * per_token + vq * 4 +
+                                     (length - kq + length - vq) * d * 2) + 2 * batch * q_heads * d * 2)
+    q = torch.randn(batch, 1, q_heads, d, generator=gen, device="cuda:0").to(torch.bfloat16).transpose(1, 2)
+    copies = copies_for(nbytes)
+    loads = []
+    for _ in range(copies):
+        k = torch.randn(batch, kv_heads, length, d, generator=gen, device="cuda:0").to(torch.bfloat16)
+        v = torch.randn(batch, kv_heads, length, d, generator=gen, device="cuda:0").to(torch.bfloat16)
+        store = KIVIPackedStore(batch, kv_heads, length, d, d, bits, group, "cuda:0")
+        rows = lambda x: torch.full((batch,), x, dtype=torch.int32, device="cuda:0")  # noqa: E731
+        store.quantize(k, "k", rows(0), rows(kq), kq, write_back=True)
+        store.quantize(v, "v", rows(0), rows(vq), vq, write_back=True)
+        store.keys_quantized.fill_(kq)
+        store.values_quantized.fill_(vq)
+        loads.append((k, v, store.record(length)))
+    out = torch.empty(batch, 1, q_heads, d, dtype=torch.bfloat16, device="cuda:0")
+    scale = 1 / math.sqrt(d)
+    seconds = time_calls(rotating([lambda k=k, v=v, r=r: kivi_decode_attention(q, k, v, None, scale, r, out=out)
+                                   for k, v, r in loads]), steps, warmup)
+    del loads
+    return _result(seconds, nbytes, copies)
+
+
 def measure_next_rows(steps: int, warmup: int, seed: int) -> dict:
     import torch
 
@@ -528,6 +565,10 @@ def measure_next_rows(steps: int, warmup: int, seed: int) -> dict:
                                  "quantized by quantize_committed), B=16 Hq=32 Hkv=8 D=128 L=8192, one query per "
                                  "request",
          lambda: measure_cells(steps, warmup, seed)),
+        ("kivi_packed_int8_g128", "kivi_decode_attention over the reference's KIVIPacked layout (8-bit codes, groups "
+                                  "of 128, beside bf16 buffers: a configuration the paged KIVI cache does not hold), "
+                                  "B=16 Hq=32 Hkv=8 D=128 L=8192, R=128",
+         lambda: measure_kivi_packed(steps, warmup, seed)),
         ("quest_graph_step", "Quest decode step with device metadata (append with the bounds refresh in one launch "
                              "+ selection + attention), B=8 Hq=32 Hkv=8 D=128 L=32768, captured graph vs eager",
          lambda: measure_quest_graph(steps, warmup, seed)),

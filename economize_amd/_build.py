@@ -20,7 +20,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 LIBRARY = HERE / "libeconomize_amd.so"
-SOURCES = ["capi.hip", "paged_attention.hip", "kv_quant.hip", "quest.hip", "kivi.hip", "dense_attention.hip", "gather.hip",
+SOURCES = ["capi.hip", "paged_attention.hip", "paged_attention_f16.hip", "kv_quant.hip", "quest.hip", "kivi.hip", "dense_attention.hip", "gather.hip",
            "kivi_dense.hip", "kivi_cells.hip", "kivi_verify.hip", "kivi_packed.hip"]
 
 FLAGS = [

@@ -32,7 +32,7 @@ _P, _I, _L, _F, _S = c_void_p, c_int32, c_int64, c_float, c_size_t
 _MASK = [_P, _L, _L, _L, _I]  # packed mask bits, word strides (batch, head, query), words per row
 _PAGED_ARGS = [_P, _L, _L, _L, _P, _P, _I, _I, _P, _P, _P, _L, _I, _P, _P, _L, _L, _I, _I, _P, _P, _P, _L, _L, _L,
                _I, _I, _I, _I, _I, _I, _I, _F, _F] + _MASK
-_PAGED_DECODE = _PAGED_ARGS + [_P, _S, _P]
+_PAGED_DECODE = _PAGED_ARGS[:1] + [_I] + _PAGED_ARGS[1:] + [_P, _S, _P]  # (the query's format after the query)
 SIGNATURES: dict[str, tuple[type | None, list]] = {
     "eco_last_error": (ctypes.c_char_p, []),
     "eco_abi_version": (c_int32, []),

@@ -127,7 +127,7 @@ class PagedKV:
     def attend(self, query: torch.Tensor, key: torch.Tensor | None, value: torch.Tensor | None,
                mask: torch.Tensor | None, scale: float | None, softcap: float | None = None,
                sinks: torch.Tensor | None = None) -> torch.Tensor:
-        """``[B, Q, Hq, D]`` bf16 attention of ``query`` ``[B, Hq, Q, D]`` over the paged cache: the ``Q`` queries
+        """``[B, Q, Hq, D]`` attention of ``query`` ``[B, Hq, Q, D]`` over the paged cache: the ``Q`` queries
         are the last ``Q`` tokens of every row (causal), and ``mask`` (boolean ``[B or 1, Hq or 1, Q or 1, >= S]``,
         key ``t`` = token ``t``) hides keys on top."""
         q = query.transpose(1, 2)
@@ -236,8 +236,8 @@ def _fallback_reason(module, query: torch.Tensor, key, attention_mask, dropout: 
     if query.dtype not in _DOT_DTYPES:
         return "dtype"
     if paged is not None:
-        if query.dtype != torch.bfloat16:
-            return "dtype"  # the paged kernels take bf16 queries
+        if query.dtype != torch.bfloat16 and not (query.dtype == torch.float16 and paged.format == "fp8"):
+            return "dtype"  # the paged kernels take bf16 queries, and fp16 ones over an fp8 cache
         kv_heads = paged.cache.kv_heads
         if q_heads % kv_heads == 0 and q_heads // kv_heads > 64:
             return "heads_per_kv"  # the paged kernels take at most 64 query heads per KV head

@@ -170,7 +170,7 @@ int check_kivi_shape(int head_dim, int bits, int group) {
     return 0;
 }
 
-int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
+int run_paged_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
                      const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
                      const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
                      const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h, int32_t n_sel,
@@ -190,6 +190,9 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
         return fail("paged decode: head dim must be 64, 128 or 256");
     if (kv_format != BF16 && kv_format != FP8_E4M3 && kv_format != FP8_E5M2)
         return fail("paged decode: KV format must be bf16, fp8 e4m3 or fp8 e5m2");
+    if (q_format != BF16 && q_format != FP16) return fail("paged decode: queries must be bf16 or fp16");
+    if (q_format == FP16 && (kv_format == BF16 || page_list))
+        return fail("paged decode: fp16 queries read an fp8 cache, without a page list");
     const int groups = q_heads / kv_heads;
     if (groups > 64) return fail("paged decode: at most 64 query heads per KV head");
     const QueryChunks qc = query_chunks(groups, queries);
@@ -223,6 +226,7 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
     PagedParams p;
     std::memset(&p, 0, sizeof(p));
     p.q = static_cast<const uint16_t*>(q);
+    p.out_f16 = q_format == FP16;
     p.sq_b = sq_b;
     p.sq_q = sq_q;
     p.sq_h = sq_h;
@@ -274,7 +278,9 @@ int run_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
         p.queries_after = queries - q0 - k;
         p.rows = groups * k;
         p.grid = grids[c + 1 < qc.count ? 0 : 1];
-        if (const int rc = paged_attention(p, static_cast<hipStream_t>(stream))) return rc;
+        const int rc = p.out_f16 ? paged_attention_f16(p, static_cast<hipStream_t>(stream))
+                                 : paged_attention(p, static_cast<hipStream_t>(stream));
+        if (rc) return rc;
     }
     return 0;
 }
@@ -591,7 +597,7 @@ extern "C" {
 
 const char* eco_last_error(void) { return g_error.c_str(); }
 
-int eco_abi_version(void) { return 7; }
+int eco_abi_version(void) { return 8; }
 
 int eco_paged_append(const void* k_new, const void* v_new, int32_t in_format, int64_t sk_t, int64_t sk_h,
                      int64_t sv_t, int64_t sv_h, const int32_t* slot_mapping, int32_t tokens, void* k_cache,
@@ -705,7 +711,7 @@ size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q
     return need;
 }
 
-int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
+int eco_paged_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
                      const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
                      const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
                      const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h, int32_t n_sel,
@@ -714,7 +720,7 @@ int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
                      int32_t head_dim, int32_t page_size, int32_t max_seq_len, float scale, float softcap,
                      const uint32_t* mask_bits, int64_t mk_b, int64_t mk_h, int64_t mk_q, int32_t mask_words,
                      void* workspace, size_t workspace_bytes, void* stream) {
-    return run_paged_decode(q, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
+    return run_paged_decode(q, q_format, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
                             block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel, list_page_size,
                             done, sinks, out, so_b, so_q, so_h, batch, queries, q_heads, kv_heads, head_dim, page_size,
                             max_seq_len, scale, softcap, mask_bits, mk_b, mk_h, mk_q, mask_words, workspace,
@@ -731,7 +737,8 @@ int eco_paged_decode_static(const void* q, int64_t sq_b, int64_t sq_q, int64_t s
                             int32_t max_seq_len, float scale, float softcap, const uint32_t* mask_bits, int64_t mk_b,
                             int64_t mk_h, int64_t mk_q, int32_t mask_words, void* stream) {
     // every argument is checked before anything is launched
-    if (const int rc = run_paged_decode(q, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
+    if (const int rc = run_paged_decode(q, BF16, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale,
+                                        v_scale,
                                         block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel,
                                         list_page_size, done, sinks, out, so_b, so_q, so_h, batch, queries, q_heads,
                                         kv_heads, head_dim, page_size, max_seq_len, scale, softcap, mask_bits, mk_b,
@@ -752,7 +759,7 @@ int eco_paged_decode_static(const void* q, int64_t sq_b, int64_t sq_q, int64_t s
     hipLaunchKernelGGL(zero_words_kernel, dim3((words + 255) / 256), dim3(256), 0, s, static_cast<uint32_t*>(ptr),
                        words);
     if (const int rc = check_launch("zero_words_kernel")) return rc;
-    return run_paged_decode(q, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
+    return run_paged_decode(q, BF16, sq_b, sq_q, sq_h, k_cache, v_cache, kv_format, num_pages, k_scale, v_scale,
                             block_table, bt_stride, bt_cols, seq_lens, page_list, pl_b, pl_h, n_sel, list_page_size,
                             done, sinks, out, so_b, so_q, so_h, batch, queries, q_heads, kv_heads, head_dim, page_size,
                             max_seq_len, scale, softcap, mask_bits, mk_b, mk_h, mk_q, mask_words, ptr, kScratchBytes,

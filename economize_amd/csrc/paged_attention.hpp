@@ -13,7 +13,7 @@ struct PagedParams {
     static constexpr int kPage = 16;   // tokens per cache page
     static constexpr int kTile = 4;    // cache pages per tile
     static constexpr bool kPageList = true;
-    const uint16_t* q;  // bf16 [B, Q, Hq, D], channel stride 1
+    const uint16_t* q;  // bf16 [B, Q, Hq, D], channel stride 1 (fp16 with an fp8 cache when out_f16 is set)
     int64_t sq_b, sq_q, sq_h;
     const uint8_t* k_cache;  // [pages, Hkv, D / X, 16, X]
     const uint8_t* v_cache;  // [pages, Hkv, D, 16]
@@ -34,7 +34,8 @@ struct PagedParams {
     int mask_words;
     int32_t* counters;  // [B * Hkv], zero between calls (the merging wave resets its row's counter)
     float* part;        // [2 * grid, rows, D + 2]: per workgroup two slots of a row segment's maxima, sums, accumulators
-    uint16_t* out;  // bf16 [B, Q, Hq, D], channel stride 1
+    uint16_t* out;  // bf16 [B, Q, Hq, D], channel stride 1 (fp16 when out_f16 is set)
+    int out_f16;    // fp16 queries and output (an fp8 cache only)
     int64_t so_b, so_q, so_h;
     int batch, queries, q_heads, kv_heads, groups, rows, head_dim, kv_format;
     int queries_after;  // queries of the call after this launch's (a call cut in query chunks): they shift the causal limit
@@ -45,5 +46,8 @@ struct PagedParams {
 // Resident workgroups per CU of the kernel instance for this shape, and its waves per workgroup.
 int paged_resident_groups(int head_dim, int format, int rows, int* per_cu, int* waves);
 int paged_attention(const PagedParams& p, hipStream_t stream);
+// The same with fp16 queries and output (fp8 caches, whole rows: no page list; paged_attention_f16.hip).
+int paged_resident_groups_f16(int head_dim, int format, int rows, int* per_cu, int* waves);
+int paged_attention_f16(const PagedParams& p, hipStream_t stream);
 
 }  // namespace eco

@@ -8,6 +8,8 @@
 // page_list, pl_b, pl_h, n_sel, span, done.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace eco {
@@ -244,6 +246,20 @@ __device__ inline int wave_of(int64_t x, int64_t total, int grid) {
     return static_cast<int>(((x + 1) * grid - 1) / total);
 }
 
+// The 16-bit output element of x: fp16 where the call's queries are fp16 (a parameter block with out_f16 set),
+// else bf16.
+template <typename P, typename = void>
+struct HasOutF16 : std::false_type {};
+template <typename P>
+struct HasOutF16<P, std::void_t<decltype(P::out_f16)>> : std::true_type {};
+
+template <typename P>
+__device__ inline uint16_t out_bits(const P& p, float x) {
+    if constexpr (HasOutF16<P>::value)
+        if (p.out_f16) return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+    return f32_to_bf16(x);
+}
+
 // out[b, qi, h, d] of query row r from its merged (acc, max, sum) in log2 units, with the sink logit of head h in
 // the denominator (attention/_decode_kernels.py:216-226): zeros for a row that sees nothing.
 template <typename P>
@@ -259,7 +275,7 @@ __device__ inline void store_output(const P& p, int b, int kvh, int r, int d, fl
         l = l * a + __builtin_amdgcn_exp2f(sink - m_new);
     }
     const float out = l > 0.0f ? o / fmaxf(l, 1e-30f) : 0.0f;
-    p.out[b * p.so_b + qi * p.so_q + h * p.so_h + d] = f32_to_bf16(out);
+    p.out[b * p.so_b + qi * p.so_q + h * p.so_h + d] = out_bits(p, out);
 }
 
 // Page ids of 64 consecutive virtual pages of one (b, kvh) row, one per lane: lane i holds the logical page and the
@@ -443,7 +459,7 @@ __device__ inline void store_output2(const P& p, int b, int kvh, int r, int d, f
     }
     const float inv = l > 0.0f ? 1.0f / fmaxf(l, 1e-30f) : 0.0f;
     uint16_t* out = p.out + b * p.so_b + qi * p.so_q + h * p.so_h + d;
-    const uint32_t pair = static_cast<uint32_t>(f32_to_bf16(o0 * inv)) | (static_cast<uint32_t>(f32_to_bf16(o1 * inv)) << 16);
+    const uint32_t pair = static_cast<uint32_t>(out_bits(p, o0 * inv)) | (static_cast<uint32_t>(out_bits(p, o1 * inv)) << 16);
     if ((reinterpret_cast<uintptr_t>(out) & 3) == 0) {
         *reinterpret_cast<uint32_t*>(out) = pair;
     } else {

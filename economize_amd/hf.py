@@ -892,10 +892,11 @@ class EconomizedModel:
         return None
 
     def paged_fp8(self, config: FP8KVConfig) -> bool:
-        """Whether ``config``'s layers live in the paged fp8 cache: the paged kernels take the model (bf16, head dim
-        64 / 128 / 256) and the scale is one they read (none, or static per head); else dense fp8 buffers."""
+        """Whether ``config``'s layers live in the paged fp8 cache: the paged kernels take the model (bf16 or fp16,
+        head dim 64 / 128 / 256) and the scale is one they read (none, or static per head); else dense fp8 buffers."""
         dtype = next(self.model.parameters()).dtype
-        return dtype == torch.bfloat16 and head_dim_of(self.model) in (64, 128, 256) and config.scale != "token"
+        return dtype in (torch.bfloat16, torch.float16) and head_dim_of(self.model) in (64, 128, 256) and \
+            config.scale != "token"
 
     def paged_quest(self) -> bool:
         """Whether Quest layers live in the paged bf16 cache (a bf16 model of head dim 64 / 128 / 256, which the paged

@@ -221,8 +221,8 @@ def paged_decode_attention(
     list_page_size: int = PAGE,
     mask: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Attention of ``query`` ``[B, Q, Hq, D]`` (bf16, channel-contiguous) over the paged cache, ``[B, Q, Hq, D]``
-    bf16 out.
+    """Attention of ``query`` ``[B, Q, Hq, D]`` (bf16, or fp16 over an fp8 cache without a page list; channel-contiguous)
+    over the paged cache, ``[B, Q, Hq, D]`` out in the query's dtype.
 
     Row ``b`` holds ``seq_lens[b]`` tokens (int32 ``[B]`` on the device; ``max_seq_len`` bounds them on the host and
     sizes the launch), its ``Q`` queries the last of them: query ``qi`` sees tokens ``< seq_lens[b] - Q + qi + 1``.
@@ -237,8 +237,10 @@ def paged_decode_attention(
     """
     cache.check()
     device = _lib.require_gpu(query, cache.keys, block_table, seq_lens)
-    if query.dim() != 4 or query.dtype != torch.bfloat16 or query.stride(-1) != 1:
-        raise ConfigError("paged decode takes a bf16 query [B, Q, Hq, D] with a contiguous channel axis")
+    if query.dim() != 4 or query.dtype not in (torch.bfloat16, torch.float16) or query.stride(-1) != 1:
+        raise ConfigError("paged decode takes a bf16 or fp16 query [B, Q, Hq, D] with a contiguous channel axis")
+    if query.dtype == torch.float16 and (cache.dtype == torch.bfloat16 or page_list is not None):
+        raise ConfigError("paged decode takes fp16 queries over an fp8 cache without a page list")
     batch, queries, q_heads, head_dim = query.shape
     if head_dim != cache.head_dim:
         raise ConfigError(f"query head dim {head_dim} != cache head dim {cache.head_dim}")
@@ -262,9 +264,9 @@ def paged_decode_attention(
             raise ConfigError(f"{sinks.numel()} sink logits for {q_heads} query heads")
         sinks = sinks.reshape(-1).float().contiguous()
     if out is None:
-        out = torch.empty(batch, queries, q_heads, head_dim, dtype=torch.bfloat16, device=device)
-    elif out.shape != query.shape or out.dtype != torch.bfloat16 or out.stride(-1) != 1:
-        raise ConfigError("out must be bf16 like the query, with a contiguous channel axis")
+        out = torch.empty(batch, queries, q_heads, head_dim, dtype=query.dtype, device=device)
+    elif out.shape != query.shape or out.dtype != query.dtype or out.stride(-1) != 1:
+        raise ConfigError("out must be like the query (shape and dtype), with a contiguous channel axis")
     if max_seq_len <= 0:
         raise ConfigError("max_seq_len must be positive")
     if list_page_size < PAGE or list_page_size % PAGE:
@@ -277,7 +279,7 @@ def paged_decode_attention(
     bits, mk, words = packed_mask(mask, batch, q_heads, queries)
     _lib.call(
         "eco_paged_decode",
-        query.data_ptr(), query.stride(0), query.stride(1), query.stride(2),
+        query.data_ptr(), _lib.fmt(query.dtype), query.stride(0), query.stride(1), query.stride(2),
         cache.keys.data_ptr(), cache.values.data_ptr(), _lib.fmt(cache.dtype), cache.num_pages,
         _lib.ptr(cache.k_scale), _lib.ptr(cache.v_scale),
         block_table.data_ptr(), block_table.stride(0), block_table.shape[1], seq_lens.data_ptr(),

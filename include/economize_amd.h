@@ -96,8 +96,9 @@ size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q
                                        int32_t head_dim, int32_t max_seq_len, int32_t n_sel, int32_t list_page_size,
                                        int32_t kv_format);
 
-/* Split-K decode attention over the paged cache: out[b, qi, h, :] (bf16, element strides so_*) for query q[b, qi,
- * h, :] (bf16, element strides sq_*, channel stride 1), query head h reading KV head h / (q_heads / kv_heads).
+/* Split-K decode attention over the paged cache: out[b, qi, h, :] (element strides so_*, the query's format) for
+ * query q[b, qi, h, :] (q_format bf16, or fp16 with an fp8 cache and no page list: a model in fp16; element strides
+ * sq_*, channel stride 1), query head h reading KV head h / (q_heads / kv_heads).
  * Row b holds seq_lens[b] tokens, its queries the last `queries` of them, query qi seeing tokens
  * < seq_lens[b] - queries + qi + 1. Scores are q . k * scale (k, v decoded times k_scale / v_scale [Hkv], NULL =
  * 1), an optional softcap > 0 applies softcap * tanh(s / softcap), optional sinks [Hq] join the softmax's
@@ -112,7 +113,7 @@ size_t eco_paged_decode_workspace_size(int32_t batch, int32_t queries, int32_t q
  * NULL = none) hides token t from query qi of head h where its bit is 0, on top of the causal limit. At most 64
  * query heads per KV head; a call of more than 64 query rows per KV head (query heads per KV head x queries) runs as
  * consecutive launches over chunks of floor(64 / (q_heads / kv_heads)) queries on the stream. */
-int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
+int eco_paged_decode(const void* q, int32_t q_format, int64_t sq_b, int64_t sq_q, int64_t sq_h, const void* k_cache,
                      const void* v_cache, int32_t kv_format, int32_t num_pages, const float* k_scale,
                      const float* v_scale, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
                      const int32_t* seq_lens, const int32_t* page_list, int64_t pl_b, int64_t pl_h, int32_t n_sel,
@@ -122,8 +123,8 @@ int eco_paged_decode(const void* q, int64_t sq_b, int64_t sq_q, int64_t sq_h, co
                      const uint32_t* mask_bits, int64_t mk_b, int64_t mk_h, int64_t mk_q, int32_t mask_words,
                      void* workspace, size_t workspace_bytes, void* stream);
 
-/* eco_paged_decode without a workspace: the scratch is the library's own, so the call allocates nothing (neither the
- * library nor the caller). No counterpart in the reference: it is for callers that cannot allocate device memory
+/* eco_paged_decode (bf16 queries) without a workspace: the scratch is the library's own, so the call allocates nothing
+ * (neither the library nor the caller). No counterpart in the reference: it is for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). The scratch is one static
  * device array of 32 MiB per GPU, held until the process ends; a call whose workspace
  * (eco_paged_decode_workspace_size) would be larger is refused before any launch. Each call clears the array's row

@@ -42,7 +42,7 @@ def test_library_exports_every_declared_function() -> None:
     from economize_amd import _lib
 
     assert sorted(_lib.SIGNATURES) == declared  # the binding declares every entry point
-    assert _lib.lib().eco_abi_version() == 7
+    assert _lib.lib().eco_abi_version() == 8
 
 
 def _parameter_counts() -> dict[str, int]:

@@ -290,7 +290,7 @@ LOGIT_TOL = 0.5
 
 @pytest.mark.parametrize("technique", ["fp8", "kivi2", "kivi4", "quest", "quest_fp16", "quest_fp32", "fp8_d512",
                                        "kivi2_d512", "quest_d512", "kivi8_fp16", "kivi4_g16", "packed8",
-                                       "packed4_g16_fp16", "packed2_d512"])
+                                       "packed4_g16_fp16", "packed2_d512", "fp8_fp16"])
 def test_decoding_logits_match_sdpa_over_the_cache(technique: str) -> None:
     """Heads of 512 channels (``_d512``) run on the dense kernel's two value slices: dense fp8 buffers, KIVI codes in
     the reference's dense layout and Quest over dense buffers. ``kivi8_fp16`` (8-bit codes on an fp16 model) and
@@ -305,11 +305,11 @@ def test_decoding_logits_match_sdpa_over_the_cache(technique: str) -> None:
     attn, path, dtype = "sdpa", "kernel_fp8", torch.bfloat16
     head_dim = 512 if technique.endswith("_d512") else 64
     technique = technique.removesuffix("_d512")
-    if technique in ("quest_fp16", "kivi8_fp16", "packed4_g16_fp16"):
-        dtype = torch.float16
+    if technique in ("quest_fp16", "kivi8_fp16", "packed4_g16_fp16", "fp8_fp16"):
+        dtype = torch.float16  # (fp8_fp16: an fp16 model over the paged fp8 cache, fp16 queries on the paged kernel)
     elif technique == "quest_fp32":
         dtype = torch.float32
-    if technique == "fp8":
+    if technique in ("fp8", "fp8_fp16"):
         configs = (FusedFP8KVConfig(),)
     elif technique.startswith("kivi"):
         group = 16 if technique.endswith("_g16") else 32

@@ -206,6 +206,49 @@ def test_append_writes_the_oracle_codes(dtype) -> None:
     assert np.array_equal(got_k, want_kc) and np.array_equal(got_v, want_vc)
 
 
+F16_CASES = [
+    # batch, queries, q heads, kv heads, head dim, lengths, dtype
+    (1, 1, 8, 2, 64, [512], torch.float8_e4m3fn),
+    (6, 1, 32, 8, 128, [1, 15, 16, 17, 100, 1000], torch.float8_e4m3fn),
+    (2, 1, 16, 4, 128, [700, 33], torch.float8_e5m2),
+    (2, 4, 16, 2, 128, [260, 71], torch.float8_e4m3fn),  # verification: 32 rows per KV head, causal
+    (2, 8, 64, 8, 128, [200, 129], torch.float8_e4m3fn),  # 64 rows per KV head
+    (2, 1, 8, 2, 256, [2000, 3333], torch.float8_e4m3fn),
+    (3, 1, 4, 4, 64, [0, 5, 40], torch.float8_e5m2),  # an empty row gives zeros
+    (2, 6, 64, 4, 128, [300, 90], torch.float8_e4m3fn),  # query chunks
+]
+
+
+@pytest.mark.parametrize("case", F16_CASES,
+                         ids=[f"b{c[0]}q{c[1]}h{c[2]}k{c[3]}d{c[4]}-{str(c[6])[6:]}" for c in F16_CASES])
+def test_fp16_queries_over_an_fp8_cache(case) -> None:
+    """A model in fp16 with its cache in fp8: fp16 queries (the keys converted to fp16 exactly for the fp16 MFMA) and
+    an fp16 output, within the same tolerance of the fp32 definition; soft cap and sinks on one case."""
+    from economize_amd.paged import paged_decode_attention
+
+    batch, queries, hq, hkv, d, lens, dtype = case
+    c = make_case(batch, queries, hq, hkv, d, lens, dtype, seed=sum(lens) + d + 1)
+    gen = torch.Generator().manual_seed(len(lens) + d)
+    c.q = (torch.randn(c.q.shape, generator=gen) * 1.5).to(torch.float16)
+    extra = {}
+    if hq == 16 and d == 128 and queries == 1:
+        extra = {"softcap": 30.0, "sinks": torch.randn(hq, generator=gen)}
+    cache = c.device_cache()
+    table = torch.from_numpy(c.table).cuda()
+    seq = torch.tensor(c.lens, dtype=torch.int32).cuda()
+    out = paged_decode_attention(c.q.cuda(), cache, table, seq, max(max(c.lens), 1), softcap=extra.get("softcap"),
+                                 sinks=None if "sinks" not in extra else extra["sinks"].cuda())
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float16
+    got = out.float().cpu().numpy()
+    want = oracle_output(c, softcap=extra.get("softcap"),
+                         sinks=None if "sinks" not in extra else extra["sinks"].numpy())
+    np.testing.assert_allclose(got, want, atol=ATOL, rtol=RTOL)
+    for b, n in enumerate(lens):
+        if n == 0:
+            assert (got[b] == 0).all()
+
+
 def test_bad_arguments_raise_before_launch() -> None:
     from economize_amd.errors import ConfigError
     from economize_amd.paged import PagedKVCache, paged_decode_attention
@@ -218,6 +261,14 @@ def test_bad_arguments_raise_before_launch() -> None:
         paged_decode_attention(q, cache, table, lens, 1)
     with pytest.raises(ConfigError):
         paged_decode_attention(torch.zeros(1, 1, 4, 128, device="cuda"), cache, table, lens, 1)  # fp32 query
+    bf16_cache = PagedKVCache.empty(2, 2, 128, torch.bfloat16, "cuda")
+    q16 = torch.zeros(1, 1, 4, 128, dtype=torch.float16, device="cuda")
+    with pytest.raises(ConfigError, match="fp16 queries"):
+        paged_decode_attention(q16, bf16_cache, table, lens, 1)  # fp16 queries read an fp8 cache only
+    with pytest.raises(ConfigError, match="fp16 queries"):
+        paged_decode_attention(q16, cache, table, lens, 1, page_list=torch.zeros(1, 2, 1, dtype=torch.int32,
+                                                                                 device="cuda"),
+                               done=torch.zeros(1, dtype=torch.int32, device="cuda"))
 
 
 @pytest.mark.parametrize("dtype,kind,queries,hq", [(torch.float8_e4m3fn, "broadcast", 1, 32),

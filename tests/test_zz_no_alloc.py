@@ -46,7 +46,7 @@ def _both(case):
     need = workspace_size(batch, queries, q_heads, cache.kv_heads, head_dim, max(case.lens), 0, cache.dtype)
     ws = new_workspace(need, "cuda")
     stream = _lib.stream_of(q.device)
-    _lib.call("eco_paged_decode", *args, ws.data_ptr(), ws.numel(), stream)
+    _lib.call("eco_paged_decode", args[0], _lib.ECO_BF16, *args[1:], ws.data_ptr(), ws.numel(), stream)
     _, args = _args(case, cache, table, lens, out_st)
     _lib.call("eco_paged_decode_static", *args, stream)
     torch.cuda.synchronize()
