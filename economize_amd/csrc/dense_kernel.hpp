@@ -8,7 +8,9 @@
 // reading KV head h / G, zeros for a query that sees no key, fp32 accumulation. Every product runs on the bf16 MFMA:
 // a bf16 or fp8 element is one bf16 operand (exact), an fp16 or fp32 element two (hi = bf16(x), lo = bf16(x - hi);
 // exact for fp16, 16 significant bits for fp32), and a product of two-term operands sums hi.hi + hi.lo + lo.hi
-// (the lo.lo term is below fp32 rounding of the sum). The softmax weights p are split the same way for P.V.
+// (the lo.lo term is below fp32 rounding of the sum). The softmax weights p are split the same way for P.V. With
+// fp16 queries over fp16 or fp8 K/V the products run on the fp16 MFMA instead: one exact product per element pair,
+// and p split into fp16 hi + lo.
 //
 // Work split (flash-decoding, as the reference): the key axis is cut into S splits; one wave takes one (row, KV
 // head, block of 16 query rows, split s) and walks the tiles of 32 keys s, s + S, s + 2 S, ... (the block's waves
@@ -187,6 +189,33 @@ __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+__device__ __forceinline__ f32x4 mfma_h(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// Eight elements of format FMT (fp16, or fp8 in w[0].x / w[0].y) as fp16, exactly.
+template <int FMT>
+__device__ __forceinline__ f16x8 to_f16x8(const uint4 (&w)[FMT == FP32 ? 2 : 1]) {
+    if constexpr (FMT == FP16) {
+        return __builtin_bit_cast(f16x8, w[0]);
+    } else {
+        static_assert(FMT == FP8_E4M3 || FMT == FP8_E5M2, "fp16 or fp8 elements");
+        uint4 r;
+        if constexpr (FMT == FP8_E4M3) {
+            r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[0].x, 1.0f, false));
+            r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[0].x, 1.0f, true));
+            r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[0].y, 1.0f, false));
+            r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w[0].y, 1.0f, true));
+        } else {
+            r.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w[0].x, 1.0f, false));
+            r.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w[0].x, 1.0f, true));
+            r.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w[0].y, 1.0f, false));
+            r.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_bf8(w[0].y, 1.0f, true));
+        }
+        return __builtin_bit_cast(f16x8, r);
+    }
+}
+
 template <int QF>
 __device__ __forceinline__ void load_query8(const DenseParams& p, int64_t offset, bf16x8& hi, bf16x8& lo) {
     uint4 w[QF == FP32 ? 2 : 1];
@@ -306,8 +335,12 @@ __global__ __launch_bounds__(64, DP > 256 ? 1 : 2) void dense_split_kernel(Dense
     constexpr int DV = DP > 256 ? 256 : DP;  // value channels of a wave
     constexpr int KS = DP / 32;  // k-steps of the S MFMA
     constexpr int ND = DV / 16;  // value blocks of 16 channels
-    constexpr bool KLO = two_terms<FMT>();
-    constexpr bool QLO = two_terms<QF>();
+    // fp16 queries over fp16 or fp8 K/V: the products take v_mfma_f32_16x16x32_f16 (every product exact, fp8 being
+    // a subset of fp16), one MFMA where bf16 operands need the hi + lo terms of the fp16 elements, and P in fp16
+    // hi + lo (22 significant bits) for P.V
+    constexpr bool H16 = QF == FP16 && (FMT == FP16 || FMT == FP8_E4M3 || FMT == FP8_E5M2) && CB == 0;
+    constexpr bool KLO = two_terms<FMT>() && !H16;
+    constexpr bool QLO = two_terms<QF>() && !H16;
     constexpr int ROW = DV * ES + 16;          // LDS bytes per staged value row
     constexpr int CHUNKS = TK * DV * ES / 16;  // 16-byte chunks of a staged value tile (a multiple of 64)
     constexpr int CPR = DV * ES / 16;          // chunks per value row
@@ -356,8 +389,13 @@ __global__ __launch_bounds__(64, DP > 256 ? 1 : 2) void dense_split_kernel(Dense
             qh[j][i] = static_cast<__bf16>(0.0f);
             ql[j][i] = static_cast<__bf16>(0.0f);
         }
-        if (r_ok && c < p.head_dim)
-            load_query8<QF>(p, b * p.sq_b + h * p.sq_h + static_cast<int64_t>(q_start + qi) * p.sq_q + c, qh[j], ql[j]);
+        if (r_ok && c < p.head_dim) {
+            const int64_t at = b * p.sq_b + h * p.sq_h + static_cast<int64_t>(q_start + qi) * p.sq_q + c;
+            if constexpr (H16)  // the fp16 bits themselves are the operand
+                qh[j] = __builtin_bit_cast(bf16x8, stream_load16(static_cast<const uint8_t*>(p.q) + at * 2));
+            else
+                load_query8<QF>(p, at, qh[j], ql[j]);
+        }
     }
     const float ks = p.k_scale ? p.k_scale[kvh] : 1.0f;
     const float vs = p.v_scale ? p.v_scale[kvh] : 1.0f;
@@ -912,6 +950,10 @@ __global__ __launch_bounds__(64, DP > 256 ? 1 : 2) void dense_split_kernel(Dense
 #pragma unroll
                     for (int x = 0; x < KW; ++x) w[x] = ok ? K.k[v][j][x] : make_uint4(0, 0, 0, 0);
                 }
+                if constexpr (H16) {
+                    s[v] = mfma_h(to_f16x8<FMT>(w), __builtin_bit_cast(f16x8, qh[j]), s[v]);
+                    continue;
+                }
                 bf16x8 kh, kl;
                 cvt8<FMT>(w, kh, kl);
                 s[v] = mfma(kh, qh[j], s[v]);
@@ -972,13 +1014,36 @@ __global__ __launch_bounds__(64, DP > 256 ? 1 : 2) void dense_split_kernel(Dense
                 l_i += pw[4 * v + i];
             }
         bf16x8 ph, pl;
-        split8(pw, ph, pl);
+        f16x8 ph16, pl16;
+        if constexpr (H16) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                ph16[i] = static_cast<_Float16>(pw[i]);
+                pl16[i] = static_cast<_Float16>(pw[i] - static_cast<float>(ph16[i]));
+            }
+        } else {
+            split8(pw, ph, pl);
+        }
         // ---- O^T += V^T P^T: lane (n, g) supplies channel 16 nd + n of keys 8 g .. 8 g + 7 ----
         __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the tile's LDS stores (one wave: in order)
 #pragma unroll
         for (int nd = 0; nd < ND; ++nd) {
             const int c = 16 * nd + n;  // (of the wave's slice)
             if (v0 + 16 * nd >= p.value_dim) break;
+            if constexpr (H16) {
+                f16x8 vh16;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    if constexpr (FMT == FP16)
+                        vh16[e] = __builtin_bit_cast(_Float16,
+                                                     *reinterpret_cast<const uint16_t*>(vtile + (8 * g + e) * ROW + c * 2));
+                    else
+                        vh16[e] = static_cast<_Float16>(elem_f32<FMT>(vtile + (8 * g + e) * ROW + c * ES));
+                }
+                acc[nd] = mfma_h(vh16, ph16, acc[nd]);
+                acc[nd] = mfma_h(vh16, pl16, acc[nd]);
+                continue;
+            }
             bf16x8 vh, vl;
             if constexpr (FMT == BF16) {  // the staged bits are the operand (no widening and rounding back)
 #pragma unroll
