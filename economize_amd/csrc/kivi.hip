@@ -445,10 +445,24 @@ kivi_attention_kernel(KiviParams p) {
         for (int v = 0; v < 2; ++v)
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) s[v][nb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        // the lane's value word of each 16-channel block from the ring (tokens 8 g .. 8 g + 7 of the tile, channel
+        // 16 nd + n): read with the ring keys when both halves of the tile hold ring tokens, so that such a tile waits
+        // out one load round trip instead of two (up to two column blocks: at four the registers would spill)
+        constexpr bool kJointRing = NB <= 2;
+        const int tok0 = t0 + 8 * g;
+        const bool key_ring = t0 >= kq, value_ring = t0 + KPAGE > vq;
+        uint4 vr[ND];
+        auto load_value_ring = [&]() __attribute__((always_inline)) {
+            const int slot = tok0 % p.ring;
+#pragma unroll
+            for (int nd = 0; nd < ND; ++nd)
+                vr[nd] = *reinterpret_cast<const uint4*>(
+                    p.v_ring + ((static_cast<int64_t>(c.b) * p.kv_heads + c.kvh) * D + 16 * nd + n) * p.ring + slot);
+        };
         // keys from codes, dequantized as the reference does (code * scale + zero in fp32, two roundings, then bf16;
         // attention/kivi.py:56-76), so that the scores see the reference's key values exactly; or, at or past kq,
         // from the ring (kq counts whole 32-token key groups, so a page is either all codes or all ring)
-        if (t0 < kq) {
+        if (!key_ring) {
 #pragma unroll
             for (int j = 0; j < KS; ++j) {
                 const f16x8 sh = *reinterpret_cast<const f16x8*>(sl + (g * (D / 4) + 8 * j) * 2);
@@ -485,6 +499,7 @@ kivi_attention_kernel(KiviParams p) {
 #pragma unroll
                 for (int j = 0; j < KS; ++j) kr[v][j] = *reinterpret_cast<const uint4*>(src + 8 * j);
             }
+            if (kJointRing && value_ring) load_value_ring();
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the ring loads of this rare branch
 #pragma unroll
             for (int v = 0; v < 2; ++v)
@@ -559,7 +574,6 @@ kivi_attention_kernel(KiviParams p) {
         }
         // values: element e of the lane's operands is token t0 + 8 g + e; p as bf16 hi + lo for both sources (p is
         // zero at every token that no query row sees)
-        const int tok0 = t0 + 8 * g;
         bf16x8 phi[NB], plo[NB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) split_bf16(pw[nb], phi[nb], plo[nb]);
@@ -590,17 +604,14 @@ kivi_attention_kernel(KiviParams p) {
                 from_codes(std::false_type{}, half_mask(code_values(tile, t0)));
             }
         }
-        if (t0 + KPAGE > vq) {  // from the ring (tokens at or past vq, below the row's end)
+        if (value_ring) {  // from the ring (tokens at or past vq, below the row's end)
             const int from = max(vq - tok0, 0), to = min(row_len - tok0, 8);
             const uint32_t keep = to > from ? ((to >= 8 ? 0xFFu : (1u << to) - 1u) & ~((1u << from) - 1u)) : 0u;
             const HalfMask mask = half_mask(keep);
-            uint4 vr[ND];
-            const int slot = tok0 % p.ring;
-#pragma unroll
-            for (int nd = 0; nd < ND; ++nd)
-                vr[nd] = *reinterpret_cast<const uint4*>(
-                    p.v_ring + ((static_cast<int64_t>(c.b) * p.kv_heads + c.kvh) * D + 16 * nd + n) * p.ring + slot);
-            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the ring loads of this rare branch
+            if (!kJointRing || !key_ring) {
+                load_value_ring();
+                __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the ring loads of this rare branch
+            }
 #pragma unroll
             for (int nd = 0; nd < ND; ++nd) product(nd, apply_mask(vr[nd], mask));
         }
