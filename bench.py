@@ -20,6 +20,10 @@ while the layers share the block table, the lengths and, here, the query: so no 
 256 MB Infinity Cache from its previous use (with a single copy the L = 4096 call reads about a sixth of its bytes
 from that cache). ``--single-copy`` measures the single-copy figures.
 
+``--length-sweep`` prints, instead of the line above, per-call times against the context length at a fixed batch
+(the fp8 shape at B = 32, the KIVI int2 / int4 decode at B = 16) and the least-squares line over L >= 4096, whose
+intercept is the per-call time that does not grow with the context.
+
 ``--gpus`` must be 1: the path runs on one GPU.
 """
 
@@ -602,6 +606,48 @@ def measure_paths(steps: int, warmup: int, seed: int) -> dict:
     return paths
 
 
+def fit_line(xs: list[float], ys: list[float]) -> tuple[float, float]:
+    """Least-squares slope and intercept of ys against xs."""
+    n = len(xs)
+    mx, my = sum(xs) / n, sum(ys) / n
+    sxx = sum((x - mx) ** 2 for x in xs)
+    slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sxx
+    return slope, my - slope * mx
+
+
+def measure_length_sweep(steps: int, warmup: int, seed: int) -> dict:
+    """Per-call time against the context length, every row of a batch at the same length: the fp8 decode at B=32
+    (lengths 2048 .. 16384) and the KIVI int2 / int4 decode at B=16 (2048 .. 16384), each timed as its bench row is
+    (rotating copies; from these lengths up a call's kernel outlasts its host-side launch). The least-squares line
+    through the lengths from 4096 up gives the microseconds per 1024 tokens of every row and the intercept: the time
+    of a call that does not grow with the context (the launch, the first dependent loads, the uneven ends of the
+    waves' ranges and the merges)."""
+    import torch
+
+    def family(name, lengths, fit_from, time_us):
+        times = []
+        for n in lengths:
+            times.append(round(time_us(n), 2))
+            print(f"length sweep: {name} L={n}: {times[-1]} us per call", file=sys.stderr, flush=True)
+            torch.cuda.empty_cache()
+        xs = [n / 1024 for n in lengths if n >= fit_from]
+        slope, intercept = fit_line(xs, [t for n, t in zip(lengths, times) if n >= fit_from])
+        return {"lengths": list(lengths), "us_per_call": times,
+                "fit": {"lengths": [n for n in lengths if n >= fit_from], "us_per_1024_tokens": round(slope, 3),
+                        "intercept_us": round(intercept, 2)}}
+
+    def paged_us(n):
+        r = measure([n] * BATCH, steps, warmup, seed)
+        return r["seconds"] * 1e6
+
+    sweep = {"paged_fp8_b32": family("paged_fp8_b32", (2048, 4096, 8192, 16384), 4096, paged_us)}
+    for bits in (2, 4):
+        sweep[f"kivi_int{bits}_b16"] = family(
+            f"kivi_int{bits}_b16", (2048, 4096, 8192, 16384), 4096,
+            lambda n, bits=bits: measure_kivi(bits, steps, warmup, seed, batch=16, lens=[n] * 16)["us_per_call"])
+    return sweep
+
+
 def traffic_per_launch() -> float | None:
     """HBM bytes per split-kernel launch from the committed rocprofv3 counter summary, if present."""
     if not TRAFFIC_FILE.exists():
@@ -623,6 +669,8 @@ def main() -> None:
     parser.add_argument("--no-paths", action="store_true", help="skip the KIVI and Quest measurements")
     parser.add_argument("--single-copy", action="store_true",
                         help="time every call on the same inputs (partly served by the 256 MB Infinity Cache)")
+    parser.add_argument("--length-sweep", action="store_true",
+                        help="only print per-call times against the context length (fp8 B=32, KIVI int2/int4 B=16)")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run a plain device copy of 256 MiB, 20 times (the reference kernel for scaling the "
                              "FETCH_SIZE / WRITE_SIZE counters of rocprofv3)")
@@ -644,6 +692,10 @@ def main() -> None:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes_per_launch": src.numel(), "launches": 20}), flush=True)
+        return
+
+    if args.length_sweep:
+        print(json.dumps({"length_sweep": measure_length_sweep(args.steps, args.warmup, args.seed)}), flush=True)
         return
 
     fixed = [4096] * BATCH
