@@ -578,29 +578,38 @@ def measure_next_rows(steps: int, warmup: int, seed: int) -> dict:
          lambda: measure_quest_graph(steps, warmup, seed)),
     ):
         rows[name] = {"workload": workload, **fn()}
+        report_path(name, rows[name])
         torch.cuda.empty_cache()
     return rows
+
+
+def report_path(name: str, row: dict) -> None:
+    """One line on stderr per measured path (the JSON line on stdout carries the figures)."""
+    us = row.get("us_per_call", row.get("us_per_step_graph"))
+    print(f"path {name}: {us} us", file=sys.stderr, flush=True)
 
 
 def measure_paths(steps: int, warmup: int, seed: int) -> dict:
     import numpy as np
     import torch
 
-    paths = {
-        "kivi_int2_decode": {"workload": "KIVI int2 decode, B=16 Hq=32 Hkv=8 D=128 L=8192, G=32 R=128",
-                             **measure_kivi(2, steps, warmup, seed)},
-        "kivi_int4_decode": {"workload": "KIVI int4 decode, B=16 Hq=32 Hkv=8 D=128 L=8192, G=32 R=128",
-                             **measure_kivi(4, steps, warmup, seed)},
-    }
+    paths = {"kivi_int2_decode": {"workload": "KIVI int2 decode, B=16 Hq=32 Hkv=8 D=128 L=8192, G=32 R=128",
+                                  **measure_kivi(2, steps, warmup, seed)}}
+    report_path("kivi_int2_decode", paths["kivi_int2_decode"])
+    paths["kivi_int4_decode"] = {"workload": "KIVI int4 decode, B=16 Hq=32 Hkv=8 D=128 L=8192, G=32 R=128",
+                                 **measure_kivi(4, steps, warmup, seed)}
+    report_path("kivi_int4_decode", paths["kivi_int4_decode"])
     torch.cuda.empty_cache()
     paths["quest_decode"] = {"workload": "Quest decode, B=8 Hq=32 Hkv=8 D=128 L=32768 bf16, 63 pages + tail",
                              **measure_quest(steps, warmup, seed)}
+    report_path("quest_decode", paths["quest_decode"])
     torch.cuda.empty_cache()
     lens = np.random.default_rng(seed + 200).integers(1024, 4097, 64).tolist()
     paths["kivi_int4_verify"] = {
         "workload": "KIVI int4 speculative verification, B=64 Q=8 Hq=64 Hkv=8 D=128 L~U[1024,4096], causal draft",
         "sum_len": int(sum(lens)),
         **measure_kivi(4, steps, warmup, seed, batch=64, queries=8, q_heads=64, kv_heads=8, lens=lens)}
+    report_path("kivi_int4_verify", paths["kivi_int4_verify"])
     torch.cuda.empty_cache()
     paths.update(measure_next_rows(steps, warmup, seed))
     return paths
@@ -700,8 +709,11 @@ def main() -> None:
 
     fixed = [4096] * BATCH
     head = measure(fixed, args.steps, args.warmup, args.seed)
+    print(f"headline: {head['seconds'] * 1e6:.2f} us", file=sys.stderr, flush=True)
     ragged_lens = np.random.default_rng(args.seed + 100).integers(1024, 8193, BATCH).tolist()
     ragged = None if args.fixed_only else measure(ragged_lens, args.steps, args.warmup, args.seed + 1)
+    if ragged is not None:
+        print(f"ragged: {ragged['seconds'] * 1e6:.2f} us", file=sys.stderr, flush=True)
     cpu = None if args.no_cpu else cpu_baseline(head["workload"], fixed)
     del head["workload"]
     torch.cuda.empty_cache()
