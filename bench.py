@@ -10,6 +10,9 @@ drawn N(0, 1) in bf16 from a seeded generator and quantize-appended into the cac
 * ``roofline``: the call is one kernel launch (``paged_attention_kernel``): algorithmic bytes per launch (KV + q +
   out + block table + lengths + scales) over its average launch time, against 8 TB/s.
 * ``ragged``: the same with lengths drawn uniformly from [1024, 8192] (mean 4608).
+* ``paths``: the other decode configurations (KIVI decode and verification, Quest, the dense, gathered, vLLM-cells
+  and KIVI packed paths, the captured Quest step), each with its algorithmic bytes, timed over at least 200 calls
+  after at least 20 warm-up calls.
 * ``cpu_baseline``: the torch-CPU fp32 restatement of the call (oracle/torch_cpu.py) over whole calls of the
   L = 4096 workload on the host's share of cores (1 warmup, median of 5), with the core count and CPU model; its
   output is also the check of the timed GPU call's output.
@@ -554,6 +557,10 @@ def measure_kivi_packed(steps: int, warmup: int, seed: int, bits: int = 8, group
     return _result(seconds, nbytes, copies)
 
 
+PATH_STEPS = 200
+PATH_WARMUP = 20
+
+
 def measure_next_rows(steps: int, warmup: int, seed: int) -> dict:
     import torch
 
@@ -590,8 +597,14 @@ def report_path(name: str, row: dict) -> None:
 
 
 def measure_paths(steps: int, warmup: int, seed: int) -> dict:
+    """The other configurations' rows, each timed over at least PATH_STEPS calls after at least PATH_WARMUP warm-up
+    calls whatever --steps / --warmup say (the headline keeps exactly those): the first few dozen calls after a
+    cache's allocation read slower (a KIVI int2 row: 53.6 us over 20 calls after 5, 50.7 us over 200 after 20), and
+    a decode step reads the same cache memory call after call."""
     import numpy as np
     import torch
+
+    steps, warmup = max(steps, PATH_STEPS), max(warmup, PATH_WARMUP)
 
     paths = {"kivi_int2_decode": {"workload": "KIVI int2 decode, B=16 Hq=32 Hkv=8 D=128 L=8192, G=32 R=128",
                                   **measure_kivi(2, steps, warmup, seed)}}
@@ -714,10 +727,12 @@ def main() -> None:
     ragged = None if args.fixed_only else measure(ragged_lens, args.steps, args.warmup, args.seed + 1)
     if ragged is not None:
         print(f"ragged: {ragged['seconds'] * 1e6:.2f} us", file=sys.stderr, flush=True)
+    # the paths before the CPU baseline: its 10-30 s leave the GPU idle, and a call timed right after an idle GPU
+    # reads slower (the first KIVI path: about 3 us)
+    paths = None if (args.no_paths or args.fixed_only) else measure_paths(args.steps, args.warmup, args.seed)
     cpu = None if args.no_cpu else cpu_baseline(head["workload"], fixed)
     del head["workload"]
     torch.cuda.empty_cache()
-    paths = None if (args.no_paths or args.fixed_only) else measure_paths(args.steps, args.warmup, args.seed)
 
     value = head["kv_bytes"] / head["seconds"] / 1e9
     achieved = head["call_bytes"] / head["seconds"] / 1e9
