@@ -15,11 +15,11 @@
 // Work split (flash-decoding, as the reference): the key axis is cut into S splits; one wave takes one (row, KV
 // head, block of 16 query rows, split s) and walks the tiles of 32 keys s, s + S, s + 2 S, ... (the block's waves
 // read adjacent runs together), the next tile's loads in flight while a tile is computed (two register buffers
-// where they fit). The splits of a block combine by
-// log-sum-exp in the last of its waves to finish (an agent-scope counter per block in the workspace, left zero by
-// every call), one launch per call; a single split writes its rows directly. Per tile, S^T = K Q^T with v_mfma_f32_16x16x32_bf16: A-row m of MFMA block v is key
-// 8 (m / 4) + 4 v + m % 4, so that lane (n, g) ends with keys 8 g .. 8 g + 7 of query row n, which is exactly the B
-// operand of O^T += V^T P^T; the keys are read token-major from HBM straight into the A operand (16-byte loads).
+// where they fit). The splits of a block combine by log-sum-exp in the last of its waves to finish (an agent-scope
+// counter per block in the workspace, left zero by every call), one launch per call; a single split writes its rows
+// directly. Per tile, S^T = K Q^T with v_mfma_f32_16x16x32_bf16: A-row m of MFMA block v is key 8 (m / 4) + 4 v +
+// m % 4, so that lane (n, g) ends with keys 8 g .. 8 g + 7 of query row n, which is exactly the B operand of
+// O^T += V^T P^T; the keys are read token-major from HBM straight into the A operand (16-byte loads).
 // V^T needs a lane to hold 8 keys of one channel: the tile's values are staged through LDS (coalesced 16-byte loads,
 // rows padded by 16 bytes so that the four lane groups' reads fall in different banks) and read back transposed.
 
@@ -324,7 +324,10 @@ __device__ __forceinline__ uint32_t word_of(uint4 x, int i) {
 // of them merges every channel.
 // KP: the KIVI packed mode (DenseParams::kp_*), one tile buffer: every tile's keys and values, read as codes below
 // the row's quantized counts and as full-precision entries past them, are dequantized into LDS (a lane turns 16-byte
-// chunks of the tile into the K/V format, their loads batched eight at a time) and the products read both from there.
+// chunks of the tile into the K/V format) and the products read both from there. A tile of codes only or of
+// full-precision entries only issues its loads in batches of up to 16 chunks; a mixed tile goes chunk by chunk; the
+// wave's leading tiles of codes only (D <= 128, no mask) hold the next tile's raw codes in registers while a tile is
+// computed (codes_run).
 template <int DP, int FMT, int QF, bool MASKED, int CB = 0, bool KP = false>
 __global__ __launch_bounds__(64, DP > 256 ? 1 : 2) void dense_split_kernel(DenseParams p) {
     static_assert(CB == 0 || (DP == 128 && FMT == BF16 && QF == BF16 && !MASKED),
