@@ -684,3 +684,60 @@ def test_a_captured_decode_step_of_a_quest_model_replays_like_eager() -> None:
     for a, b in zip(c0.layers[1:], c1.layers[1:]):
         assert torch.equal(a.state.done, b.state.done) and torch.equal(a.state.kmin, b.state.kmin)
     assert int(c1.layers[1].state.done[0]) == (PROMPT + 1 + steps) // 16
+
+
+def test_a_captured_decode_step_of_an_fp8_model_replays_like_eager() -> None:
+    """The headline path inside the drop-in: a bf16 Qwen2 whose layers live in a static paged fp8 cache (every length
+    on the device) is captured once, decoding step ``model(input_ids=token, position_ids=position,
+    past_key_values=cache)`` with the token and position in device buffers, and replayed; a twin model stepping
+    eagerly over a twin cache gives bit-identical logits at every step while the rows cross page boundaries."""
+    from economize_amd.attention import kernel_usage
+    from economize_amd.hf import PagedLayer, apply
+    from economize_amd.techniques import FusedFP8KVConfig
+
+    cap, steps = 200, 40
+
+    def build():
+        model = tiny_model("sdpa")
+        em = apply(model, FusedFP8KVConfig())
+        return model, em.make_cache(cap, static=True)
+
+    (m0, c0), (m1, c1) = build(), build()
+    assert all(isinstance(layer, PagedLayer) and layer.static for layer in c0.layers)
+    ids = prompt()
+    pos = torch.arange(PROMPT, device="cuda")[None]
+    kernel_usage(reset=True)
+    with torch.no_grad():
+        first = m0(input_ids=ids, position_ids=pos, past_key_values=c0, use_cache=True).logits
+        assert torch.equal(first, m1(input_ids=ids, position_ids=pos, past_key_values=c1, use_cache=True).logits)
+        token = torch.zeros(1, 1, dtype=torch.long, device="cuda")
+        position = torch.zeros(1, 1, dtype=torch.long, device="cuda")
+        token.copy_(first[:, -1].argmax(-1, keepdim=True))
+        position.fill_(PROMPT)
+
+        def step(model, cache):
+            return model(input_ids=token, position_ids=position, past_key_values=cache, use_cache=True).logits
+
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):  # warm-up on a side stream: workspaces exist before the capture
+            warm = step(m0, c0)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        assert torch.equal(warm, step(m1, c1))
+        token.copy_(warm[:, -1].argmax(-1, keepdim=True))
+        position += 1
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            captured = step(m0, c0)
+        for i in range(steps):
+            graph.replay()
+            torch.cuda.synchronize()
+            eager = step(m1, c1)
+            torch.cuda.synchronize()
+            assert torch.equal(captured, eager), f"step {i}, position {int(position)}"
+            token.copy_(eager[:, -1].argmax(-1, keepdim=True))
+            position += 1
+    assert int(position) == PROMPT + 1 + steps
+    paths = {(row["path"], row["queries"]) for row in kernel_usage(reset=True)}
+    assert ("kernel_fp8", 1) in paths
