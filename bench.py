@@ -612,11 +612,16 @@ def measure_paths(steps: int, warmup: int, seed: int) -> dict:
     over 200 calls after 20, 47.7 us after 1000, about 50 ms, in a fresh process; about 48 us later in the process
     on fresh inputs after 20), while a decode loop calls its kernels back to back."""
     global MIN_WARMUP_S
+    MIN_WARMUP_S = PATH_WARMUP_S
+    try:
+        return _measure_paths(max(steps, PATH_STEPS), max(warmup, PATH_WARMUP), seed)
+    finally:
+        MIN_WARMUP_S = 0.0
+
+
+def _measure_paths(steps: int, warmup: int, seed: int) -> dict:
     import numpy as np
     import torch
-
-    steps, warmup = max(steps, PATH_STEPS), max(warmup, PATH_WARMUP)
-    MIN_WARMUP_S = PATH_WARMUP_S
 
     paths = {"kivi_int2_decode": {"workload": "KIVI int2 decode, B=16 Hq=32 Hkv=8 D=128 L=8192, G=32 R=128",
                                   **measure_kivi(2, steps, warmup, seed)}}
@@ -637,7 +642,6 @@ def measure_paths(steps: int, warmup: int, seed: int) -> dict:
     report_path("kivi_int4_verify", paths["kivi_int4_verify"])
     torch.cuda.empty_cache()
     paths.update(measure_next_rows(steps, warmup, seed))
-    MIN_WARMUP_S = 0.0
     return paths
 
 
